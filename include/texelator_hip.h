@@ -1,0 +1,102 @@
+/*
+ * texelator_hip.h -- C ABI of libtexelator_hip.so, the gfx950 BC4 weight path.
+ *
+ * Each entry point replaces one function of the reference's native module
+ * (texelator/cuda/extension.cpp:27-48, implemented in texelator/cuda/texelator_cuda.cu).
+ * Plain pointers and sizes only; no framework types. Every function returns TX_OK (0) or a
+ * nonzero status; the message of the last failure on the calling thread is returned by
+ * tx_last_error(). Device pointers are HIP device memory; "stream" is a hipStream_t (NULL
+ * means the default stream). Launches are asynchronous on that stream.
+ */
+#ifndef TEXELATOR_HIP_H
+#define TEXELATOR_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TX_OK 0
+#define TX_ERR_INVALID 1     /* bad argument: the reference raises RuntimeError (TORCH_CHECK) */
+#define TX_ERR_HIP 2         /* HIP runtime failure (reference: CUDA_CHECK) */
+#define TX_ERR_UNSUPPORTED 3 /* feature of the reference with no gfx950 implementation here */
+
+#define TX_DTYPE_F16 0
+#define TX_DTYPE_BF16 1
+#define TX_DTYPE_F32 2
+
+/* Message of the last failure on this thread ("" if none). */
+const char *tx_last_error(void);
+
+/* Upload one encoded matrix and return an opaque handle.
+ * Replaces texelator_pack_encoded (texelator_cuda.cu:1260-1327; extension.cpp:28).
+ *   blocks       host bytes [M][bpr][8] (reference block format, encoder.py:105-117)
+ *   blocks_bytes total bytes; must be a positive multiple of 8*M
+ *   scales       host float32 [M]
+ *   bias         optional device pointer to [M] values of bias_dtype (F16 or BF16), copied
+ *   device       HIP device ordinal that will own the handle
+ * K = 16 * bpr. The blocks are repacked into the gfx950 tile layout on upload. */
+int tx_pack_encoded(const uint8_t *blocks, int64_t blocks_bytes, const float *scales, int64_t rows,
+                    const void *bias, int bias_dtype, int device, uint64_t *handle_out);
+
+/* y = x W^T (+ bias). Replaces texelator_linear (texelator_cuda.cu:1329-1469; extension.cpp:30).
+ *   x        device, contiguous [tokens][K] of x_dtype (BF16; F16 is reported unsupported)
+ *   x_numel  number of elements of x; tokens = x_numel / K
+ *   x_last   size of x's last dimension (must equal K)
+ *   y        device output [tokens][M] of x_dtype, allocated by the caller
+ * tokens >= prefill threshold (and tokens > 1) uses the prefill GEMM candidate set by
+ * tx_set_prefill_backend; otherwise the decode GEMV with the configured lookahead. */
+int tx_linear(uint64_t handle, const void *x, int x_dtype, int64_t x_numel, int64_t x_last,
+              int device, void *y, void *stream);
+
+/* Decode GEMV with float32 output and no bias, for parity checks (no reference counterpart:
+ * the reference only returns 16-bit outputs). x: device bf16 [tokens][K]; y: device f32. */
+int tx_linear_f32(uint64_t handle, const void *x, int64_t tokens, float *y, void *stream);
+
+/* Prefill GEMM with an explicit candidate (5..9), bf16 in/out, bias applied if present.
+ * Used by the tile autotuner (reference: set_prefill_backend + linear, autotune.py:144-187). */
+int tx_prefill(uint64_t handle, int candidate, const void *x, int64_t tokens, void *y, void *stream);
+
+/* Replaces texelator_set_lookahead (texelator_cuda.cu:1471-1478): one of 1,2,3,4,6,8. */
+int tx_set_lookahead(uint64_t handle, int lookahead);
+
+/* Replaces texelator_set_prefill (texelator_cuda.cu:1480-1488): threshold >= 1,
+ * tile_rows a positive multiple of 16 (accepted and stored; no scratch path uses it here). */
+int tx_set_prefill(uint64_t handle, int threshold, int tile_rows);
+
+/* Replaces texelator_set_prefill_backend (texelator_cuda.cu:1490-1503): 0..9. Ids 5..9 name the
+ * gfx950 tile candidates; 0..4 (the reference's CUDA-only backends) select the default tile. */
+int tx_set_prefill_backend(uint64_t handle, int backend);
+
+/* Replaces texelator_handle_info (texelator_cuda.cu:1505-1512). Writes up to n of
+ * [M, K, prefill_threshold, prefill_tile_rows, prefill_backend, pipelined(0), graphics(0),
+ *  lookahead, device]. */
+int tx_handle_info(uint64_t handle, int64_t *out, int n);
+
+/* Replaces texelator_free (texelator_cuda.cu:1538). Caller must ensure no work is pending. */
+int tx_free(uint64_t handle);
+
+/* Replaces texelator_palette_probe (texelator_cuda.cu:1551-1595): fills host_out with the
+ * 255*255*8 float32 palette measured from the device decoder, index ((e1+127)*255+(e0+127))*8+s,
+ * on the current device. Synchronous. */
+int tx_palette_probe(float *host_out);
+
+/* Decode a handle's weights to a dense device bf16 [M][K] array (test-only diagnostic; no
+ * reference counterpart -- the reference's decode tiles write scratch, texelator_cuda.cu:604-663). */
+int tx_decode_dense(uint64_t handle, uint16_t *out, void *stream);
+
+/* Kernel resource report for a candidate. Replaces the *_kernel_info functions
+ * (texelator_cuda.cu:1514-1536, cutlass_texture_mainloop.cu:251-267). candidate 5..9: prefill
+ * tiles; 100 + L: decode GEMV with lookahead L. Writes up to n of
+ * [vgprs, static_lds_bytes, private_bytes, max_threads, tile_lds_bytes, tokens_tile, rows_tile, k_tile]. */
+int tx_kernel_info(int candidate, int64_t *out, int n);
+
+/* Name of a prefill candidate (5..9) or NULL. */
+const char *tx_candidate_name(int candidate);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TEXELATOR_HIP_H */

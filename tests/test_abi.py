@@ -1,0 +1,46 @@
+"""The C ABI library loads without a GPU and exports every symbol its header declares."""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "texelator_hip.h"
+
+
+def declared_symbols() -> list[str]:
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(tx_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_header_declares_the_boundary():
+    names = declared_symbols()
+    for required in ("tx_pack_encoded", "tx_linear", "tx_set_lookahead", "tx_set_prefill",
+                     "tx_set_prefill_backend", "tx_handle_info", "tx_free", "tx_palette_probe",
+                     "tx_kernel_info", "tx_last_error"):
+        assert required in names
+
+
+def test_library_exports_every_declared_symbol():
+    from texelator_amd import _lib
+
+    if not _lib.LIBRARY_PATH.exists():
+        pytest.fail("libtexelator_hip.so is not built; run python -m texelator_amd.build")
+    lib = ctypes.CDLL(str(_lib.LIBRARY_PATH))
+    for name in declared_symbols():
+        assert hasattr(lib, name), name
+    assert set(declared_symbols()) == set(_lib.SIGNATURES), "ctypes signatures out of sync with the header"
+
+
+def test_errors_without_gpu_are_reported_not_crashing():
+    from texelator_amd import _lib
+
+    lib = _lib.load()
+    assert lib.tx_set_lookahead(0, 2) == _lib.TX_ERR_INVALID
+    assert b"null" in lib.tx_last_error()
+    assert lib.tx_free(0) == _lib.TX_ERR_INVALID
+    assert lib.tx_candidate_name(5) == b"large_256x128x128"
+    assert lib.tx_candidate_name(4) is None

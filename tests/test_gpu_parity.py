@@ -1,0 +1,193 @@
+"""GPU parity of the gfx950 BC4 path against the CPU oracle, through the C ABI.
+
+Bars: decoded weights bit-exact; GEMV fp32 output within 1e-3 relative
+error of the float64 CPU matvec on the same decoded weights; prefill bf16 output within 1e-2
+relative RMS of the float64 CPU GEMM; all prefill candidates bitwise equal (the reference's
+autotuner gate, texelator/autotune.py:160-168).
+"""
+from __future__ import annotations
+
+import hashlib
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import bc4, clib
+from tests.helpers import bf16_bits, bf16_vector, lognormal_scales, max_rel_err_floor, random_blocks, rel_err
+
+pytestmark = pytest.mark.gpu
+
+GEMV_TOL = 1e-3
+PREFILL_RRMS_TOL = 1e-2
+
+
+def _pack(ext, blocks, scales, bias=None):
+    return ext.pack_encoded(torch.from_numpy(np.ascontiguousarray(blocks).reshape(-1)),
+                            torch.from_numpy(np.ascontiguousarray(scales)), bias)
+
+
+def test_palette_probe_bitwise_equals_cpu_palette(ext):
+    probe = ext.palette_probe().numpy()
+    cpu = bc4.palette().reshape(255 * 255, 8)
+    assert probe.shape == (65025, 8)
+    assert np.array_equal(probe.view(np.uint32), cpu.view(np.uint32))
+    assert hashlib.sha256(probe.astype("<f4").tobytes()).hexdigest() == bc4.palette_sha256()
+
+
+@pytest.mark.parametrize("m,k,seed", [(16, 128, 1), (37, 272, 2), (100, 16, 3), (64, 4096, 4), (5, 2064, 5)])
+def test_decode_dense_bit_exact(ext, oracle_threads, m, k, seed):
+    blocks = random_blocks(m, k, seed)
+    scales = lognormal_scales(m, seed + 100)
+    handle = _pack(ext, blocks, scales)
+    try:
+        dense = ext.decode_dense(handle)
+        torch.cuda.synchronize()
+        got = bf16_bits(dense.cpu())
+    finally:
+        ext.free(handle)
+    want = clib.decode_bf16_bits(blocks, scales)
+    assert got.shape == want.shape
+    mismatches = int(np.count_nonzero(got != want))
+    assert mismatches == 0, f"{mismatches} of {want.size} decoded weights differ"
+
+
+@pytest.mark.parametrize("m,k,tokens,seed", [(16, 128, 1, 11), (37, 272, 1, 12), (1024, 5120, 1, 13),
+                                             (300, 1040, 3, 14), (4096, 4096, 1, 15), (8, 27648, 1, 16)])
+def test_gemv_f32_within_tolerance(ext, oracle_threads, m, k, tokens, seed):
+    blocks = random_blocks(m, k, seed)
+    scales = lognormal_scales(m, seed + 1)
+    x = bf16_vector((tokens, k), seed + 2)
+    handle = _pack(ext, blocks, scales)
+    try:
+        y = ext.linear_f32(handle, x.cuda()).cpu().numpy()
+    finally:
+        ext.free(handle)
+    w = clib.decode_bf16_bits(blocks, scales)
+    for t in range(tokens):
+        ref = clib.matvec_f64(w, bf16_bits(x[t]))
+        assert rel_err(ref, y[t]) <= GEMV_TOL
+        assert max_rel_err_floor(ref, y[t]) <= GEMV_TOL
+
+
+@pytest.mark.parametrize("lookahead", [1, 2, 3, 4, 6, 8])
+def test_gemv_lookahead_variants_bitwise_equal(ext, lookahead):
+    m, k = 512, 5120
+    blocks = random_blocks(m, k, 21)
+    scales = lognormal_scales(m, 22)
+    x = bf16_vector((1, k), 23).cuda()
+    handle = _pack(ext, blocks, scales)
+    try:
+        ext.set_lookahead(handle, 1)
+        base = ext.linear_f32(handle, x)
+        ext.set_lookahead(handle, lookahead)
+        other = ext.linear_f32(handle, x)
+        again = ext.linear_f32(handle, x)
+        torch.cuda.synchronize()
+    finally:
+        ext.free(handle)
+    assert torch.equal(base, other)
+    assert torch.equal(other, again)
+
+
+def test_gemv_bf16_output_and_bias(ext, oracle_threads):
+    m, k = 333, 2048
+    blocks = random_blocks(m, k, 31)
+    scales = lognormal_scales(m, 32)
+    x = bf16_vector((2, k), 33)
+    bias = bf16_vector((m,), 34, scale=0.5)
+    handle = _pack(ext, blocks, scales, bias.cuda())
+    try:
+        y = ext.linear(handle, x.cuda()).float().cpu().numpy()
+    finally:
+        ext.free(handle)
+    w = clib.decode_bf16_bits(blocks, scales)
+    for t in range(2):
+        ref = clib.matvec_f64(w, bf16_bits(x[t])) + bias.float().numpy()
+        # one bf16 rounding of the biased sum: 2^-8 relative per element at most
+        assert max_rel_err_floor(ref, y[t]) <= 2 ** -8 + GEMV_TOL
+
+
+@pytest.mark.parametrize("tokens", [17, 32, 100, 128])
+def test_prefill_candidates_bitwise_equal_and_within_rrms(ext, oracle_threads, tokens):
+    m, k = 200, 1280
+    blocks = random_blocks(m, k, 41)
+    scales = lognormal_scales(m, 42)
+    x = (bf16_vector((tokens, k), 43).float() * 0.125).to(torch.bfloat16)
+    handle = _pack(ext, blocks, scales)
+    outputs = {}
+    try:
+        for candidate in range(5, 10):
+            outputs[candidate] = ext.prefill(handle, candidate, x.cuda())
+        ext.set_prefill(handle, 1, 1024)
+        via_linear = ext.linear(handle, x.cuda())
+        torch.cuda.synchronize()
+    finally:
+        ext.free(handle)
+    base = outputs[5]
+    for candidate, value in outputs.items():
+        assert torch.equal(base, value), f"candidate {candidate} differs from candidate 5"
+    assert torch.equal(base, via_linear)
+    w = clib.decode_bf16_bits(blocks, scales)
+    ref = clib.gemm_f64(bf16_bits(x), w)
+    got = base.float().cpu().numpy()
+    assert bc4.relative_rms(ref, got) <= PREFILL_RRMS_TOL
+
+
+def test_prefill_bias_double_rounding(ext):
+    m, k, tokens = 64, 256, 40
+    blocks = random_blocks(m, k, 51)
+    scales = lognormal_scales(m, 52)
+    x = bf16_vector((tokens, k), 53)
+    bias = bf16_vector((m,), 54)
+    plain = _pack(ext, blocks, scales)
+    biased = _pack(ext, blocks, scales, bias.cuda())
+    try:
+        y0 = ext.prefill(plain, 6, x.cuda())
+        y1 = ext.prefill(biased, 6, x.cuda())
+        torch.cuda.synchronize()
+    finally:
+        ext.free(plain)
+        ext.free(biased)
+    expected = (y0.float() + bias.cuda().float()[None, :]).to(torch.bfloat16)
+    assert torch.equal(y1, expected)
+
+
+def test_split_k_reduction_is_deterministic(ext):
+    m, k = 64, 27648  # few row groups -> many K splits
+    blocks = random_blocks(m, k, 61)
+    scales = lognormal_scales(m, 62)
+    x = bf16_vector((1, k), 63).cuda()
+    handle = _pack(ext, blocks, scales)
+    try:
+        first = ext.linear_f32(handle, x)
+        for _ in range(20):
+            assert torch.equal(first, ext.linear_f32(handle, x))
+    finally:
+        ext.free(handle)
+
+
+def test_handle_api_errors(ext):
+    blocks = random_blocks(16, 128, 71)
+    scales = lognormal_scales(16, 72)
+    handle = _pack(ext, blocks, scales)
+    try:
+        assert ext.handle_info(handle)[:2] == [16, 128]
+        with pytest.raises(RuntimeError, match="lookahead"):
+            ext.set_lookahead(handle, 5)
+        with pytest.raises(RuntimeError, match="threshold"):
+            ext.set_prefill(handle, 0, 1024)
+        with pytest.raises(RuntimeError, match="tile rows"):
+            ext.set_prefill(handle, 16, 24)
+        with pytest.raises(RuntimeError, match="backend"):
+            ext.set_prefill_backend(handle, 10)
+        with pytest.raises(RuntimeError, match="shape"):
+            ext.linear(handle, torch.zeros((1, 64), dtype=torch.bfloat16, device="cuda"))
+        with pytest.raises(RuntimeError, match="FP16 or BF16"):
+            ext.linear(handle, torch.zeros((1, 128), dtype=torch.float32, device="cuda"))
+    finally:
+        ext.free(handle)
+    with pytest.raises(RuntimeError, match="uint8"):
+        ext.pack_encoded(torch.zeros(16, dtype=torch.int8), torch.ones(1))
+    with pytest.raises(RuntimeError, match="invalid encoded size"):
+        ext.pack_encoded(torch.zeros(12, dtype=torch.uint8), torch.ones(1))

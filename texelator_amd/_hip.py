@@ -1,0 +1,215 @@
+"""The native operator module of the gfx950 build.
+
+Same function names, argument meaning and error behaviour as the reference's pybind11
+module (``texelator/cuda/extension.cpp:27-48``); every call goes through the C ABI of
+``libtexelator_hip.so``. PyTorch provides device memory and the current stream only.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+from ._lib import TexelatorError, UnsupportedError, check
+
+_SHAPES: dict[int, tuple[int, int]] = {}
+_DTYPE_CODE = {torch.float16: _lib.TX_DTYPE_F16, torch.bfloat16: _lib.TX_DTYPE_BF16}
+
+# Reference kernel-info names -> prefill candidate ids (autotune.CANDIDATES values).
+_KERNEL_INFO_IDS = {
+    "cutlass_texture_kernel_info": 5,
+    "cutlass_t1_kernel_info": 6,
+    "cutlass_t2_kernel_info": 7,
+    "cutlass_t3_kernel_info": 8,
+    "cutlass_smalln_kernel_info": 9,
+}
+
+
+def _require(condition: bool, message: str) -> None:
+    if not condition:
+        raise TexelatorError(message)
+
+
+def _stream(device: torch.device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _aligned(x: torch.Tensor) -> torch.Tensor:
+    return x if x.data_ptr() % 16 == 0 else x.clone()
+
+
+def shape(handle: int) -> tuple[int, int]:
+    """(M, K) of a handle, cached."""
+    cached = _SHAPES.get(handle)
+    if cached is None:
+        info = handle_info(handle)
+        cached = (int(info[0]), int(info[1]))
+        _SHAPES[handle] = cached
+    return cached
+
+
+def pack_encoded(blocks: torch.Tensor, scales: torch.Tensor, bias: torch.Tensor | None = None) -> int:
+    """Upload one encoded matrix (``texelator_cuda.cu:1260-1327``); returns a handle."""
+    _require(not blocks.is_cuda and blocks.dtype == torch.uint8 and blocks.is_contiguous(),
+             "blocks must be contiguous CPU uint8")
+    _require(not scales.is_cuda and scales.dtype == torch.float32 and scales.is_contiguous(),
+             "scales must be contiguous CPU float32")
+    rows = scales.numel()
+    _require(rows > 0 and blocks.numel() % (rows * 8) == 0, "invalid encoded size")
+    bias_ptr = None
+    bias_code = -1
+    device = torch.cuda.current_device()
+    if bias is not None and bias.numel():
+        bias = bias.detach().contiguous()
+        _require(bias.is_cuda and bias.dtype in _DTYPE_CODE and bias.numel() == rows,
+                 "bias must be CUDA FP16 or BF16 [M]")
+        bias_ptr = ctypes.c_void_p(bias.data_ptr())
+        bias_code = _DTYPE_CODE[bias.dtype]
+        device = bias.device.index if bias.device.index is not None else device
+    out = ctypes.c_uint64(0)
+    lib = _lib.load()
+    check(lib.tx_pack_encoded(ctypes.c_void_p(blocks.data_ptr()), blocks.numel(),
+                              ctypes.c_void_p(scales.data_ptr()), rows, bias_ptr, bias_code, device,
+                              ctypes.byref(out)))
+    handle = int(out.value)
+    _SHAPES[handle] = (rows, blocks.numel() // rows // 8 * 16)
+    return handle
+
+
+def linear(handle: int, x: torch.Tensor) -> torch.Tensor:
+    """``y = x W^T (+ bias)`` (``texelator_cuda.cu:1329-1469``); output dtype = input dtype."""
+    _require(bool(handle), "null Texelator handle")
+    _require(x.is_cuda and x.dtype in _DTYPE_CODE and x.is_contiguous(),
+             "input must be contiguous CUDA FP16 or BF16")
+    m, k = shape(handle)
+    _require(x.dim() >= 1 and x.size(-1) == k, "input shape/device mismatch")
+    out_shape = list(x.shape)
+    out_shape[-1] = m
+    y = torch.empty(out_shape, dtype=x.dtype, device=x.device)
+    x = _aligned(x)
+    check(_lib.load().tx_linear(handle, ctypes.c_void_p(x.data_ptr()), _DTYPE_CODE[x.dtype], x.numel(),
+                                x.size(-1), x.device.index, ctypes.c_void_p(y.data_ptr()), _stream(x.device)))
+    return y
+
+
+def linear_f32(handle: int, x: torch.Tensor) -> torch.Tensor:
+    """Decode GEMV with a float32 output and no bias (parity entry point, ``tx_linear_f32``)."""
+    _require(x.is_cuda and x.dtype == torch.bfloat16 and x.is_contiguous(), "input must be contiguous CUDA BF16")
+    m, k = shape(handle)
+    _require(x.size(-1) == k, "input shape/device mismatch")
+    out_shape = list(x.shape)
+    out_shape[-1] = m
+    y = torch.empty(out_shape, dtype=torch.float32, device=x.device)
+    x = _aligned(x)
+    check(_lib.load().tx_linear_f32(handle, ctypes.c_void_p(x.data_ptr()), x.numel() // k,
+                                    ctypes.c_void_p(y.data_ptr()), _stream(x.device)))
+    return y
+
+
+def prefill(handle: int, candidate: int, x: torch.Tensor) -> torch.Tensor:
+    """Prefill GEMM with an explicit tile candidate (5..9), bf16 in and out."""
+    _require(x.is_cuda and x.dtype == torch.bfloat16 and x.is_contiguous(), "input must be contiguous CUDA BF16")
+    m, k = shape(handle)
+    _require(x.size(-1) == k, "input shape/device mismatch")
+    out_shape = list(x.shape)
+    out_shape[-1] = m
+    y = torch.empty(out_shape, dtype=torch.bfloat16, device=x.device)
+    x = _aligned(x)
+    check(_lib.load().tx_prefill(handle, int(candidate), ctypes.c_void_p(x.data_ptr()), x.numel() // k,
+                                 ctypes.c_void_p(y.data_ptr()), _stream(x.device)))
+    return y
+
+
+def set_lookahead(handle: int, lookahead: int) -> None:
+    check(_lib.load().tx_set_lookahead(handle, int(lookahead)))
+
+
+def set_prefill(handle: int, threshold: int, tile_rows: int) -> None:
+    check(_lib.load().tx_set_prefill(handle, int(threshold), int(tile_rows)))
+
+
+def set_prefill_backend(handle: int, backend: int) -> None:
+    check(_lib.load().tx_set_prefill_backend(handle, int(backend)))
+
+
+def handle_info(handle: int) -> list[int]:
+    """``[M, K, threshold, tile_rows, backend, pipelined, graphics]`` (``texelator_cuda.cu:1505-1512``)."""
+    out = (ctypes.c_int64 * 7)()
+    check(_lib.load().tx_handle_info(handle, out, 7))
+    return [int(v) for v in out]
+
+
+def lookahead(handle: int) -> int:
+    out = (ctypes.c_int64 * 8)()
+    check(_lib.load().tx_handle_info(handle, out, 8))
+    return int(out[7])
+
+
+def free(handle: int) -> None:
+    check(_lib.load().tx_free(handle))
+    _SHAPES.pop(handle, None)
+
+
+def palette_probe() -> torch.Tensor:
+    """Device-decoded palette, ``[65025, 8]`` float32 on the CPU (``texelator_cuda.cu:1551-1595``)."""
+    out = torch.empty((255 * 255, 8), dtype=torch.float32)
+    check(_lib.load().tx_palette_probe(ctypes.c_void_p(out.data_ptr())))
+    return out
+
+
+def decode_dense(handle: int) -> torch.Tensor:
+    """Decoded weights as a dense ``[M, K]`` bf16 device tensor (diagnostic)."""
+    m, k = shape(handle)
+    device = torch.device("cuda", torch.cuda.current_device())
+    out = torch.empty((m, k), dtype=torch.bfloat16, device=device)
+    check(_lib.load().tx_decode_dense(handle, ctypes.c_void_p(out.data_ptr()), _stream(device)))
+    return out
+
+
+def kernel_info(candidate: int) -> list[int]:
+    """``[vgprs, static_lds, private, max_threads, tile_lds, tokens_tile, rows_tile, k_tile]``."""
+    out = (ctypes.c_int64 * 8)()
+    check(_lib.load().tx_kernel_info(int(candidate), out, 8))
+    return [int(v) for v in out]
+
+
+def candidate_name(candidate: int) -> str | None:
+    name = _lib.load().tx_candidate_name(int(candidate))
+    return name.decode() if name else None
+
+
+def cutlass_texture_kernel_info() -> list[int]:
+    return kernel_info(_KERNEL_INFO_IDS["cutlass_texture_kernel_info"])
+
+
+def cutlass_t1_kernel_info() -> list[int]:
+    return kernel_info(_KERNEL_INFO_IDS["cutlass_t1_kernel_info"])
+
+
+def cutlass_t2_kernel_info() -> list[int]:
+    return kernel_info(_KERNEL_INFO_IDS["cutlass_t2_kernel_info"])
+
+
+def cutlass_t3_kernel_info() -> list[int]:
+    return kernel_info(_KERNEL_INFO_IDS["cutlass_t3_kernel_info"])
+
+
+def cutlass_smalln_kernel_info() -> list[int]:
+    return kernel_info(_KERNEL_INFO_IDS["cutlass_smalln_kernel_info"])
+
+
+def _no_counterpart(name: str):
+    def unsupported(*_args, **_kwargs):
+        raise UnsupportedError(f"{name} has no gfx950 counterpart in this build")
+    unsupported.__name__ = name
+    return unsupported
+
+
+# The reference's CUDA-only diagnostics and NVFP4 staging (texelator_cuda.cu:1085-1152, :1514-1536).
+pipeline_kernel_info = _no_counterpart("pipeline_kernel_info")
+graphics_kernel_info = _no_counterpart("graphics_kernel_info")
+quantize_activation_fp4 = _no_counterpart("quantize_activation_fp4")
+decode_weight_fp4 = _no_counterpart("decode_weight_fp4")
+quantize_activation_fp4_out = _no_counterpart("quantize_activation_fp4_out")
+decode_weight_fp4_out = _no_counterpart("decode_weight_fp4_out")

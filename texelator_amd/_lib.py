@@ -1,0 +1,76 @@
+"""ctypes binding of ``libtexelator_hip.so`` (the C ABI in ``include/texelator_hip.h``).
+
+There is no fallback: if the library is missing or fails to load, every call raises.
+"""
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+PACKAGE_ROOT = Path(__file__).resolve().parent
+LIBRARY_PATH = PACKAGE_ROOT / "libtexelator_hip.so"
+
+TX_OK = 0
+TX_ERR_INVALID = 1
+TX_ERR_HIP = 2
+TX_ERR_UNSUPPORTED = 3
+
+TX_DTYPE_F16 = 0
+TX_DTYPE_BF16 = 1
+TX_DTYPE_F32 = 2
+
+# name -> (restype, argtypes); every symbol declared in include/texelator_hip.h
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_I32 = ctypes.c_int
+_U64 = ctypes.c_uint64
+SIGNATURES = {
+    "tx_last_error": (ctypes.c_char_p, []),
+    "tx_pack_encoded": (_I32, [_P, _I64, _P, _I64, _P, _I32, _I32, ctypes.POINTER(_U64)]),
+    "tx_linear": (_I32, [_U64, _P, _I32, _I64, _I64, _I32, _P, _P]),
+    "tx_linear_f32": (_I32, [_U64, _P, _I64, _P, _P]),
+    "tx_prefill": (_I32, [_U64, _I32, _P, _I64, _P, _P]),
+    "tx_set_lookahead": (_I32, [_U64, _I32]),
+    "tx_set_prefill": (_I32, [_U64, _I32, _I32]),
+    "tx_set_prefill_backend": (_I32, [_U64, _I32]),
+    "tx_handle_info": (_I32, [_U64, ctypes.POINTER(_I64), _I32]),
+    "tx_free": (_I32, [_U64]),
+    "tx_palette_probe": (_I32, [_P]),
+    "tx_decode_dense": (_I32, [_U64, _P, _P]),
+    "tx_kernel_info": (_I32, [_I32, ctypes.POINTER(_I64), _I32]),
+    "tx_candidate_name": (ctypes.c_char_p, [_I32]),
+}
+
+_LIB = None
+
+
+class TexelatorError(RuntimeError):
+    """A failed C-ABI call (the reference raises RuntimeError from TORCH_CHECK)."""
+
+
+class UnsupportedError(TexelatorError):
+    pass
+
+
+def load() -> ctypes.CDLL:
+    global _LIB
+    if _LIB is None:
+        if not LIBRARY_PATH.exists():
+            raise TexelatorError(
+                f"the gfx950 BC4 library is not built ({LIBRARY_PATH}); run `python -m texelator_amd.build`")
+        lib = ctypes.CDLL(str(LIBRARY_PATH))
+        for name, (restype, argtypes) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = restype
+            fn.argtypes = argtypes
+        _LIB = lib
+    return _LIB
+
+
+def check(status: int) -> None:
+    if status == TX_OK:
+        return
+    message = load().tx_last_error().decode(errors="replace") or f"texelator status {status}"
+    if status == TX_ERR_UNSUPPORTED:
+        raise UnsupportedError(message)
+    raise TexelatorError(message)

@@ -1,0 +1,390 @@
+// C ABI of libtexelator_hip.so: handle ownership, upload/repack, dispatch, diagnostics.
+//
+// Reference counterparts (texelator/cuda/texelator_cuda.cu): Handle :47-73, pack :1260-1327,
+// dispatch :1329-1469, setters :1471-1503, handle_info :1505-1512, free :1538, probe :1551-1595.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstring>
+#include <new>
+#include <string>
+#include <thread>
+#include <vector>
+
+#include "../../include/texelator_hip.h"
+#include "bc4_device.h"
+#include "kernels.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const std::string &message) {
+  g_last_error = message;
+  return code;
+}
+
+#define TX_HIP(call)                                                                   \
+  do {                                                                                 \
+    hipError_t _e = (call);                                                            \
+    if (_e != hipSuccess) return fail(TX_ERR_HIP, std::string("HIP: ") + hipGetErrorString(_e) + " (" #call ")"); \
+  } while (0)
+
+struct DeviceGuard {
+  int previous = -1;
+  bool changed = false;
+  explicit DeviceGuard(int device) {
+    if (hipGetDevice(&previous) == hipSuccess && previous != device) changed = hipSetDevice(device) == hipSuccess;
+  }
+  ~DeviceGuard() {
+    if (changed) (void)hipSetDevice(previous);
+  }
+};
+
+constexpr uint32_t kHandleMagic = 0x54584834u;  // "TXH4"
+
+struct Handle {
+  uint32_t magic = kHandleMagic;
+  int M = 0, K = 0, bpr = 0, Mp = 0, bp = 0, RG = 0, CG = 0, device = 0;
+  int lookahead = 2;
+  int prefill_threshold = 16, prefill_tile_rows = 1024, prefill_backend = 0;
+  int gemv_splits = 1;
+  uint4 *tiles = nullptr;
+  float *scales = nullptr;
+  void *bias = nullptr;
+  int bias_dtype = -1;
+  float *partials = nullptr;
+  uint32_t *counters = nullptr;
+
+  ~Handle() {
+    DeviceGuard guard(device);
+    if (tiles) (void)hipFree(tiles);
+    if (scales) (void)hipFree(scales);
+    if (bias) (void)hipFree(bias);
+    if (partials) (void)hipFree(partials);
+    if (counters) (void)hipFree(counters);
+    magic = 0;
+  }
+};
+
+Handle *as_handle(uint64_t value) {
+  auto *h = reinterpret_cast<Handle *>(value);
+  if (!h || h->magic != kHandleMagic) return nullptr;
+  return h;
+}
+
+// One reference block (8 bytes) -> device words A, B (layout in bc4_device.h).
+inline void encode_block(const uint8_t *blk, uint32_t &a, uint32_t &b) {
+  int e0 = (int)(int8_t)blk[0];
+  int e1 = (int)(int8_t)blk[1];
+  e0 = e0 < -127 ? -127 : e0;
+  e1 = e1 < -127 ? -127 : e1;
+  const uint32_t eb0 = (uint32_t)(e0 + 127);
+  const uint32_t eb1 = (uint32_t)(e1 + 127);
+  uint64_t bits = 0;
+  for (int i = 0; i < 6; ++i) bits |= (uint64_t)blk[2 + i] << (8 * i);
+  uint32_t s[16];
+  for (int p = 0; p < 16; ++p) s[p] = (uint32_t)((bits >> (3 * p)) & 7u);
+  a = 0;
+  b = 0;
+  for (int c = 0; c < 4; ++c) {
+    a |= (s[c] | (s[4 + c] << 3) | (((eb0 >> (2 * c)) & 3u) << 6)) << (8 * c);
+    b |= (s[8 + c] | (s[12 + c] << 3) | (((eb1 >> (2 * c)) & 3u) << 6)) << (8 * c);
+  }
+}
+
+void repack_rows(const uint8_t *blocks, const Handle &h, uint32_t *out, int g_begin, int g_end) {
+  for (int g = g_begin; g < g_end; ++g) {
+    for (int c = 0; c < h.CG; ++c) {
+      uint32_t *tile = out + ((size_t)g * h.CG + c) * 256;
+      for (int lane = 0; lane < 64; ++lane) {
+        const int m = g * tx::kTileRows + (lane & 15);
+        for (int half = 0; half < 2; ++half) {
+          const int blk = c * tx::kTileBlocks + 2 * (lane >> 4) + half;
+          uint32_t a = tx::kZeroBlockWord, b = tx::kZeroBlockWord;
+          if (m < h.M && blk < h.bpr) encode_block(blocks + ((size_t)m * h.bpr + blk) * 8, a, b);
+          tile[lane * 4 + half * 2] = a;
+          tile[lane * 4 + half * 2 + 1] = b;
+        }
+      }
+    }
+  }
+}
+
+int choose_splits(int RG, int CG, int device) {
+  int cus = 256;
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, device) == hipSuccess && prop.multiProcessorCount > 0) cus = prop.multiProcessorCount;
+  const int target = 8 * cus;
+  int ks = (target + RG - 1) / RG;
+  ks = std::min(ks, std::max(1, CG / 4));
+  return std::max(ks, 1);
+}
+
+int default_candidate(int tokens) {
+  if (tokens <= 32) return 9;
+  if (tokens <= 128) return 6;
+  return 5;
+}
+
+int run_prefill(Handle *h, int candidate, const void *x, int64_t tokens, void *y, hipStream_t stream) {
+  tx::PrefillParams p{};
+  p.tiles = h->tiles;
+  p.scales = h->scales;
+  p.x = x;
+  p.bias = h->bias;
+  p.y = y;
+  p.M = h->M;
+  p.K = h->K;
+  p.Mp = h->Mp;
+  p.RG = h->RG;
+  p.CG = h->CG;
+  p.tokens = (int)tokens;
+  const int bt_limit = 65535;
+  int bt = 0, bn = 0, bk = 0;
+  tx::prefill_candidate_shape(candidate, &bt, &bn, &bk);
+  if (bt <= 0 || (tokens + bt - 1) / bt > bt_limit) return fail(TX_ERR_INVALID, "token count exceeds the prefill grid limit");
+  TX_HIP(tx::launch_prefill(p, candidate, stream));
+  return TX_OK;
+}
+
+int run_gemv(Handle *h, const void *x, int64_t tokens, void *y, bool f32_out, hipStream_t stream) {
+  if (tokens > 65535) return fail(TX_ERR_INVALID, "token grid exceeds the HIP grid.z limit");
+  tx::GemvParams p{};
+  p.tiles = h->tiles;
+  p.scales = h->scales;
+  p.x = x;
+  p.bias = f32_out ? nullptr : h->bias;
+  p.y = y;
+  p.M = h->M;
+  p.K = h->K;
+  p.Mp = h->Mp;
+  p.RG = h->RG;
+  p.CG = h->CG;
+  p.tokens = (int)tokens;
+  p.ks = tokens == 1 ? h->gemv_splits : 1;
+  p.partials = h->partials;
+  p.counters = h->counters;
+  TX_HIP(tx::launch_gemv(p, h->lookahead, f32_out, stream));
+  return TX_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *tx_last_error(void) { return g_last_error.c_str(); }
+
+int tx_pack_encoded(const uint8_t *blocks, int64_t blocks_bytes, const float *scales, int64_t rows, const void *bias,
+                    int bias_dtype, int device, uint64_t *handle_out) {
+  g_last_error.clear();
+  if (!blocks || !scales || !handle_out) return fail(TX_ERR_INVALID, "blocks, scales and handle_out must be non-null");
+  if (rows <= 0 || blocks_bytes <= 0 || blocks_bytes % (rows * 8) != 0) return fail(TX_ERR_INVALID, "invalid encoded size");
+  const int64_t bpr = blocks_bytes / (rows * 8);
+  if (rows > (1 << 30) || bpr * 16 > (1 << 30)) return fail(TX_ERR_INVALID, "matrix too large");
+  if (bias && bias_dtype != TX_DTYPE_F16 && bias_dtype != TX_DTYPE_BF16)
+    return fail(TX_ERR_INVALID, "bias must be CUDA FP16 or BF16 [M]");
+  DeviceGuard guard(device);
+  Handle *h = new (std::nothrow) Handle;
+  if (!h) return fail(TX_ERR_HIP, "host allocation failed");
+  h->M = (int)rows;
+  h->bpr = (int)bpr;
+  h->K = (int)bpr * 16;
+  h->device = device;
+  h->RG = (h->M + tx::kTileRows - 1) / tx::kTileRows;
+  h->Mp = h->RG * tx::kTileRows;
+  h->CG = (h->bpr + tx::kTileBlocks - 1) / tx::kTileBlocks;
+  h->bp = h->CG * tx::kTileBlocks;
+  h->gemv_splits = choose_splits(h->RG, h->CG, device);
+
+  const size_t tile_bytes = (size_t)h->RG * h->CG * tx::kTileBytes;
+  std::vector<uint32_t> host(tile_bytes / 4);
+  const int workers = (int)std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
+  const int per = (h->RG + workers - 1) / workers;
+  std::vector<std::thread> threads;
+  for (int w = 0; w < workers; ++w) {
+    const int gb = w * per, ge = std::min(h->RG, gb + per);
+    if (gb >= ge) break;
+    threads.emplace_back(repack_rows, blocks, std::cref(*h), host.data(), gb, ge);
+  }
+  for (auto &t : threads) t.join();
+
+  std::vector<float> padded_scales(h->Mp, 0.0f);
+  std::memcpy(padded_scales.data(), scales, (size_t)h->M * sizeof(float));
+
+  auto cleanup = [&](int code) {
+    delete h;
+    return code;
+  };
+  hipError_t e;
+  if ((e = hipMalloc(&h->tiles, tile_bytes)) != hipSuccess) return cleanup(fail(TX_ERR_HIP, std::string("HIP: ") + hipGetErrorString(e)));
+  if ((e = hipMemcpy(h->tiles, host.data(), tile_bytes, hipMemcpyHostToDevice)) != hipSuccess)
+    return cleanup(fail(TX_ERR_HIP, std::string("HIP: ") + hipGetErrorString(e)));
+  if ((e = hipMalloc(&h->scales, (size_t)h->Mp * sizeof(float))) != hipSuccess)
+    return cleanup(fail(TX_ERR_HIP, std::string("HIP: ") + hipGetErrorString(e)));
+  if ((e = hipMemcpy(h->scales, padded_scales.data(), (size_t)h->Mp * sizeof(float), hipMemcpyHostToDevice)) != hipSuccess)
+    return cleanup(fail(TX_ERR_HIP, std::string("HIP: ") + hipGetErrorString(e)));
+  if (bias) {
+    if ((e = hipMalloc(&h->bias, (size_t)h->M * 2)) != hipSuccess) return cleanup(fail(TX_ERR_HIP, std::string("HIP: ") + hipGetErrorString(e)));
+    if ((e = hipMemcpy(h->bias, bias, (size_t)h->M * 2, hipMemcpyDeviceToDevice)) != hipSuccess)
+      return cleanup(fail(TX_ERR_HIP, std::string("HIP: ") + hipGetErrorString(e)));
+    h->bias_dtype = bias_dtype;
+  }
+  if (h->gemv_splits > 1) {
+    if ((e = hipMalloc(&h->partials, (size_t)h->gemv_splits * h->Mp * sizeof(float))) != hipSuccess)
+      return cleanup(fail(TX_ERR_HIP, std::string("HIP: ") + hipGetErrorString(e)));
+    if ((e = hipMalloc(&h->counters, (size_t)h->RG * sizeof(uint32_t))) != hipSuccess)
+      return cleanup(fail(TX_ERR_HIP, std::string("HIP: ") + hipGetErrorString(e)));
+    if ((e = hipMemset(h->counters, 0, (size_t)h->RG * sizeof(uint32_t))) != hipSuccess)
+      return cleanup(fail(TX_ERR_HIP, std::string("HIP: ") + hipGetErrorString(e)));
+  }
+  if ((e = hipDeviceSynchronize()) != hipSuccess) return cleanup(fail(TX_ERR_HIP, std::string("HIP: ") + hipGetErrorString(e)));
+  *handle_out = reinterpret_cast<uint64_t>(h);
+  return TX_OK;
+}
+
+int tx_linear(uint64_t value, const void *x, int x_dtype, int64_t x_numel, int64_t x_last, int device, void *y,
+              void *stream) {
+  g_last_error.clear();
+  Handle *h = as_handle(value);
+  if (!h) return fail(TX_ERR_INVALID, "null Texelator handle");
+  if (x_dtype != TX_DTYPE_BF16 && x_dtype != TX_DTYPE_F16) return fail(TX_ERR_INVALID, "input must be contiguous CUDA FP16 or BF16");
+  if (x_last != h->K || device != h->device) return fail(TX_ERR_INVALID, "input shape/device mismatch");
+  if (!x || !y) return fail(TX_ERR_INVALID, "null input or output pointer");
+  if (reinterpret_cast<uintptr_t>(x) % 16 != 0) return fail(TX_ERR_INVALID, "input must be 16-byte aligned");
+  if (x_dtype == TX_DTYPE_F16) return fail(TX_ERR_UNSUPPORTED, "FP16 activations are not supported by the gfx950 BC4 path");
+  const int64_t tokens = x_numel / h->K;
+  if (tokens <= 0) return TX_OK;
+  DeviceGuard guard(h->device);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (tokens >= h->prefill_threshold && tokens > 1) {
+    if (h->bias && h->bias_dtype != TX_DTYPE_BF16) return fail(TX_ERR_INVALID, "BF16 prefill requires a BF16 bias");
+    const int candidate = h->prefill_backend >= tx::kPrefillFirst ? h->prefill_backend : default_candidate((int)tokens);
+    return run_prefill(h, candidate, x, tokens, y, s);
+  }
+  if (h->bias && h->bias_dtype != x_dtype) return fail(TX_ERR_INVALID, "input and bias dtypes must match");
+  return run_gemv(h, x, tokens, y, false, s);
+}
+
+int tx_linear_f32(uint64_t value, const void *x, int64_t tokens, float *y, void *stream) {
+  g_last_error.clear();
+  Handle *h = as_handle(value);
+  if (!h) return fail(TX_ERR_INVALID, "null Texelator handle");
+  if (!x || !y) return fail(TX_ERR_INVALID, "null input or output pointer");
+  if (reinterpret_cast<uintptr_t>(x) % 16 != 0) return fail(TX_ERR_INVALID, "input must be 16-byte aligned");
+  if (tokens <= 0) return TX_OK;
+  DeviceGuard guard(h->device);
+  return run_gemv(h, x, tokens, y, true, reinterpret_cast<hipStream_t>(stream));
+}
+
+int tx_prefill(uint64_t value, int candidate, const void *x, int64_t tokens, void *y, void *stream) {
+  g_last_error.clear();
+  Handle *h = as_handle(value);
+  if (!h) return fail(TX_ERR_INVALID, "null Texelator handle");
+  if (!x || !y) return fail(TX_ERR_INVALID, "null input or output pointer");
+  if (reinterpret_cast<uintptr_t>(x) % 16 != 0) return fail(TX_ERR_INVALID, "input must be 16-byte aligned");
+  if (!tx::prefill_candidate_eligible(candidate, h->M, h->K)) return fail(TX_ERR_INVALID, "unknown or ineligible prefill candidate");
+  if (h->bias && h->bias_dtype != TX_DTYPE_BF16) return fail(TX_ERR_INVALID, "BF16 prefill requires a BF16 bias");
+  if (tokens <= 0) return TX_OK;
+  DeviceGuard guard(h->device);
+  return run_prefill(h, candidate, x, tokens, y, reinterpret_cast<hipStream_t>(stream));
+}
+
+int tx_set_lookahead(uint64_t value, int lookahead) {
+  g_last_error.clear();
+  Handle *h = as_handle(value);
+  if (!h) return fail(TX_ERR_INVALID, "null Texelator handle");
+  if (!tx::gemv_lookahead_supported(lookahead)) return fail(TX_ERR_INVALID, "lookahead must be one of 1,2,3,4,6,8");
+  h->lookahead = lookahead;
+  return TX_OK;
+}
+
+int tx_set_prefill(uint64_t value, int threshold, int tile_rows) {
+  g_last_error.clear();
+  Handle *h = as_handle(value);
+  if (!h) return fail(TX_ERR_INVALID, "null Texelator handle");
+  if (threshold < 1) return fail(TX_ERR_INVALID, "prefill threshold must be positive");
+  if (tile_rows < 16 || tile_rows % 16 != 0) return fail(TX_ERR_INVALID, "prefill tile rows must be a positive multiple of 16");
+  h->prefill_threshold = threshold;
+  h->prefill_tile_rows = tile_rows;
+  return TX_OK;
+}
+
+int tx_set_prefill_backend(uint64_t value, int backend) {
+  g_last_error.clear();
+  Handle *h = as_handle(value);
+  if (!h) return fail(TX_ERR_INVALID, "null Texelator handle");
+  if (backend < 0 || backend > 9)
+    return fail(TX_ERR_INVALID,
+                "prefill backend must be 0-4 (default tile) or 5 (large_256x128x128), 6 (medium_128x128x128), "
+                "7 (medium_128x64x128), 8 (medium_64x128x128), or 9 (small_32x64x128)");
+  h->prefill_backend = backend;
+  return TX_OK;
+}
+
+int tx_handle_info(uint64_t value, int64_t *out, int n) {
+  g_last_error.clear();
+  Handle *h = as_handle(value);
+  if (!h) return fail(TX_ERR_INVALID, "null Texelator handle");
+  if (!out || n < 0) return fail(TX_ERR_INVALID, "invalid output buffer");
+  const int64_t info[9] = {h->M, h->K, h->prefill_threshold, h->prefill_tile_rows, h->prefill_backend, 0, 0,
+                           h->lookahead, h->device};
+  for (int i = 0; i < n && i < 9; ++i) out[i] = info[i];
+  return TX_OK;
+}
+
+int tx_free(uint64_t value) {
+  g_last_error.clear();
+  Handle *h = as_handle(value);
+  if (!h) return fail(TX_ERR_INVALID, "null Texelator handle");
+  delete h;
+  return TX_OK;
+}
+
+int tx_palette_probe(float *host_out) {
+  g_last_error.clear();
+  if (!host_out) return fail(TX_ERR_INVALID, "null output");
+  float *device_out = nullptr;
+  const size_t bytes = (size_t)255 * 255 * 8 * sizeof(float);
+  TX_HIP(hipMalloc(&device_out, bytes));
+  hipError_t e = tx::launch_palette_probe(device_out, nullptr);
+  if (e == hipSuccess) e = hipMemcpy(host_out, device_out, bytes, hipMemcpyDeviceToHost);
+  (void)hipFree(device_out);
+  if (e != hipSuccess) return fail(TX_ERR_HIP, std::string("HIP: ") + hipGetErrorString(e));
+  return TX_OK;
+}
+
+int tx_decode_dense(uint64_t value, uint16_t *out, void *stream) {
+  g_last_error.clear();
+  Handle *h = as_handle(value);
+  if (!h) return fail(TX_ERR_INVALID, "null Texelator handle");
+  if (!out) return fail(TX_ERR_INVALID, "null output");
+  DeviceGuard guard(h->device);
+  TX_HIP(tx::launch_decode_dense(h->tiles, h->scales, h->M, h->K, h->RG, h->CG, out, reinterpret_cast<hipStream_t>(stream)));
+  return TX_OK;
+}
+
+int tx_kernel_info(int candidate, int64_t *out, int n) {
+  g_last_error.clear();
+  if (!out || n < 0) return fail(TX_ERR_INVALID, "invalid output buffer");
+  hipFuncAttributes attr{};
+  int lds = 0, bt = 0, bn = 0, bk = 0;
+  if (candidate >= 100) {
+    TX_HIP(tx::gemv_kernel_attributes(candidate - 100, &attr));
+    bt = 1;
+    bn = tx::kTileRows;
+    bk = tx::kTileK;
+  } else {
+    if (!tx::prefill_candidate_name(candidate)) return fail(TX_ERR_INVALID, "unknown kernel candidate");
+    TX_HIP(tx::prefill_kernel_attributes(candidate, &attr, &lds));
+    tx::prefill_candidate_shape(candidate, &bt, &bn, &bk);
+  }
+  const int64_t info[8] = {attr.numRegs, (int64_t)attr.sharedSizeBytes, (int64_t)attr.localSizeBytes,
+                           attr.maxThreadsPerBlock, lds, bt, bn, bk};
+  for (int i = 0; i < n && i < 8; ++i) out[i] = info[i];
+  return TX_OK;
+}
+
+const char *tx_candidate_name(int candidate) { return tx::prefill_candidate_name(candidate); }
+
+}  // extern "C"

@@ -1,0 +1,146 @@
+// BC4 device layout and ALU decoder for gfx950.
+//
+// Reference semantics (paths in the reference checkout):
+//   block format  texelator/encoder.py:105-117 -- [e0:i8][e1:i8][48-bit selectors, 3 bits each,
+//                 position p at bits 3p..3p+2]; position p of block b is input column 16b+p
+//                 (texelator/cuda/texelator_cuda.cu:127-131).
+//   decoded value texelator/cuda/texelator_cuda.cu:141-152 -- bf16_rne(palette * scale[row]),
+//                 fp32 product.
+//
+// The palette is computed in registers instead of sampled from texture hardware:
+//   endpoints clamped to [-127,127]; base = RN(e0/127), end = RN(e1/127);
+//   e0 > e1 : step = RN((e1-e0)/889); P[s] = fma(s-1, step, base), s = 2..7
+//   e0 <= e1: step = RN((e1-e0)/635); P[s] = fma(s-1, step, base), s = 2..5; P[6] = -1, P[7] = +1.
+// Correctly rounded quotients use q = fma(n, RHI, n*RLO) with RHI = RN(1/d), RLO = RN(1/d - RHI);
+// this is exact-rounded for every |n| <= 889 and d in {127, 635, 889} (checked exhaustively).
+//
+// Device block (8 bytes, two little-endian dwords A, B), written by the host repack:
+//   A byte c (c = 0..3): bits 0-2 = sel[c],     bits 3-5 = sel[4+c],  bits 6-7 = bits 2c..2c+1 of eb0
+//   B byte c:            bits 0-2 = sel[8+c],   bits 3-5 = sel[12+c], bits 6-7 = bits 2c..2c+1 of eb1
+// with eb = clamp(e, -127, 127) + 127. Selector groups (A & 0x07070707, (A>>3) & 0x07070707, ...)
+// are then ready-made v_perm_b32 byte selectors for four positions each.
+//
+// Tile layout: rows padded to a multiple of 16, blocks per row padded to a multiple of 8. A tile
+// is 16 rows x 8 blocks = 1 KiB; tile (g, c) sits at ((g * CG) + c) * 1 KiB. Inside a tile, lane
+// l (0..63) owns 16 contiguous bytes: row 16g + (l & 15), blocks 8c + 2(l >> 4) and +1. One
+// wave-wide 128-bit load therefore reads one whole contiguous tile.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace tx {
+
+constexpr int kTileRows = 16;
+constexpr int kTileBlocks = 8;
+constexpr int kTileBytes = 1024;
+constexpr int kTileK = kTileBlocks * 16;  // 128 input columns per tile
+
+// Reciprocal pairs (hi = RN(1/d), lo = RN(1/d - hi)), pre-divided by 64 because the endpoint
+// extraction yields 64*e (the scaling by 2^6 is exact, so results are unchanged).
+constexpr float kR127Hi = 0x1.020408p-7f / 64.0f;
+constexpr float kR127Lo = 0x1.020408p-35f / 64.0f;
+constexpr float kR889Hi = 0x1.26e00ap-10f / 64.0f;
+constexpr float kR889Lo = -0x1.91ff6cp-35f / 64.0f;
+constexpr float kR635Hi = 0x1.9cd34p-10f / 64.0f;
+constexpr float kR635Lo = 0x1.9cd34p-38f / 64.0f;
+
+// Device block whose endpoints are 0/0 and selectors 0: decodes to zero weights (padding).
+constexpr uint32_t kZeroBlockWord = 0x40C0C0C0u;
+
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Streaming 128-bit load of one lane's tile slot (weights are read once per call).
+__device__ __forceinline__ uint4 load_stream(const uint4 *ptr) {
+  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(ptr));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+__device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) {
+  return __builtin_amdgcn_perm(hi, lo, sel);
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  bf16x2 v = {(__bf16)a, (__bf16)b};  // v_cvt_pk_bf16_f32, round-to-nearest-even
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// 64*e from the 2-bit fields in bits 6-7 of each byte (dot4 with weights 1,4,16,64 and a
+// wrapping bias of -127*64).
+__device__ __forceinline__ float endpoint_x64(uint32_t word) {
+  return (float)(int)__builtin_amdgcn_udot4(word & 0xC0C0C0C0u, 0x40100401u, 0xFFFFE040u, false);
+}
+
+struct Palette {
+  float p[8];
+  bool eight;
+};
+
+// The fp32 palette of one block (the values a LUT row holds).
+__device__ __forceinline__ Palette palette8(uint32_t a, uint32_t b) {
+  Palette out;
+  float f0 = endpoint_x64(a);
+  float f1 = endpoint_x64(b);
+  float d = f1 - f0;
+  out.eight = f0 > f1;
+  float rhi = out.eight ? kR889Hi : kR635Hi;
+  float rlo = out.eight ? kR889Lo : kR635Lo;
+  float step = __builtin_fmaf(d, rhi, d * rlo);
+  float base = __builtin_fmaf(f0, kR127Hi, f0 * kR127Lo);
+  float end = __builtin_fmaf(f1, kR127Hi, f1 * kR127Lo);
+  out.p[0] = base;
+  out.p[1] = end;
+  out.p[2] = base + step;
+  out.p[3] = __builtin_fmaf(2.0f, step, base);
+  out.p[4] = __builtin_fmaf(3.0f, step, base);
+  out.p[5] = __builtin_fmaf(4.0f, step, base);
+  out.p[6] = out.eight ? __builtin_fmaf(5.0f, step, base) : -1.0f;
+  out.p[7] = out.eight ? __builtin_fmaf(6.0f, step, base) : 1.0f;
+  return out;
+}
+
+// Packed bf16 pair (bf16(-scale), bf16(+scale)): slots 6 and 7 of a 6-value block.
+__device__ __forceinline__ uint32_t pm_scale_pair(float scale) { return pack_bf16x2(-scale, scale); }
+
+// Decode one device block to 16 bf16 weights (8 dwords, positions 0..15 in order).
+// w[j] holds positions 2j (low half) and 2j+1 (high half).
+__device__ __forceinline__ void decode_block(uint32_t a, uint32_t b, float scale, uint32_t pm,
+                                             uint32_t w[8]) {
+  float f0 = endpoint_x64(a);
+  float f1 = endpoint_x64(b);
+  float d = f1 - f0;
+  bool eight = f0 > f1;
+  float rhi = eight ? kR889Hi : kR635Hi;
+  float rlo = eight ? kR889Lo : kR635Lo;
+  float step = __builtin_fmaf(d, rhi, d * rlo);
+  float base = __builtin_fmaf(f0, kR127Hi, f0 * kR127Lo);
+  float end = __builtin_fmaf(f1, kR127Hi, f1 * kR127Lo);
+  float p2 = base + step;
+  float p3 = __builtin_fmaf(2.0f, step, base);
+  float p4 = __builtin_fmaf(3.0f, step, base);
+  float p5 = __builtin_fmaf(4.0f, step, base);
+  float p6 = __builtin_fmaf(5.0f, step, base);
+  float p7 = __builtin_fmaf(6.0f, step, base);
+  uint32_t pk01 = pack_bf16x2(base * scale, end * scale);
+  uint32_t pk23 = pack_bf16x2(p2 * scale, p3 * scale);
+  uint32_t pk45 = pack_bf16x2(p4 * scale, p5 * scale);
+  uint32_t pk67 = pack_bf16x2(p6 * scale, p7 * scale);
+  pk67 = eight ? pk67 : pm;
+  // Byte tables: low and high bytes of the eight bf16 values.
+  uint32_t lo0 = perm(pk23, pk01, 0x06040200u);
+  uint32_t hi0 = perm(pk23, pk01, 0x07050301u);
+  uint32_t lo1 = perm(pk67, pk45, 0x06040200u);
+  uint32_t hi1 = perm(pk67, pk45, 0x07050301u);
+  uint32_t sel[4] = {a & 0x07070707u, (a >> 3) & 0x07070707u, b & 0x07070707u,
+                     (b >> 3) & 0x07070707u};
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    uint32_t l = perm(lo1, lo0, sel[g]);
+    uint32_t h = perm(hi1, hi0, sel[g]);
+    w[2 * g] = perm(h, l, 0x05010400u);
+    w[2 * g + 1] = perm(h, l, 0x07030602u);
+  }
+}
+
+}  // namespace tx

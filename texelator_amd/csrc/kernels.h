@@ -1,0 +1,49 @@
+// Host-side launchers of the gfx950 kernels (internal to libtexelator_hip.so).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace tx {
+
+enum DType : int { kF16 = 0, kBF16 = 1, kF32 = 2 };
+
+struct GemvParams {
+  const uint4 *tiles;      // RG * CG tiles of 64 x 16 bytes
+  const float *scales;     // [Mp], zero beyond M
+  const void *x;           // [tokens][K] bf16
+  const void *bias;        // [M] bf16 or nullptr
+  void *y;                 // [tokens][M] bf16 or f32
+  float *partials;         // [ks][Mp] when ks > 1
+  uint32_t *counters;      // [RG] when ks > 1, all zero between launches
+  int M, K, Mp, RG, CG, ks, tokens;
+};
+
+struct PrefillParams {
+  const uint4 *tiles;
+  const float *scales;
+  const void *x;           // [tokens][K] bf16
+  const void *bias;        // [M] bf16 or nullptr
+  void *y;                 // [tokens][M] bf16
+  int M, K, Mp, RG, CG, tokens;
+};
+
+// GEMV variants selected by the lookahead knob (number of 1 KiB tiles in flight per wave).
+bool gemv_lookahead_supported(int lookahead);
+hipError_t launch_gemv(const GemvParams &p, int lookahead, bool f32_out, hipStream_t stream);
+hipError_t gemv_kernel_attributes(int lookahead, hipFuncAttributes *attr);
+
+// Prefill tile candidates: ids 5..9 (kept from the reference's backend numbering).
+constexpr int kPrefillFirst = 5;
+constexpr int kPrefillLast = 9;
+bool prefill_candidate_eligible(int candidate, int M, int K);
+hipError_t launch_prefill(const PrefillParams &p, int candidate, hipStream_t stream);
+hipError_t prefill_kernel_attributes(int candidate, hipFuncAttributes *attr, int *lds_bytes);
+const char *prefill_candidate_name(int candidate);
+void prefill_candidate_shape(int candidate, int *tokens, int *rows, int *k);
+
+hipError_t launch_palette_probe(float *out, hipStream_t stream);
+hipError_t launch_decode_dense(const uint4 *tiles, const float *scales, int M, int K, int RG, int CG,
+                               uint16_t *out, hipStream_t stream);
+
+}  // namespace tx

@@ -1,0 +1,79 @@
+// Exhaustive palette probe and dense decode (diagnostics).
+//
+// Reference: texelator_palette_probe / texelator_dump_palette
+// (texelator/cuda/texelator_cuda.cu:1542-1595) sample every endpoint pair (e0, e1) in
+// [-127,127]^2 and write out[(y*255 + x)*8 + s] with x = e0+127, y = e1+127. Here the same
+// table is produced by the register decoder (palette8 in bc4_device.h) run on probe blocks built
+// in the device layout, so its SHA-256 can be compared with the CPU palette.
+#include "bc4_device.h"
+#include "kernels.h"
+
+namespace tx {
+
+namespace {
+
+// Device-layout word for endpoint byte eb (biased, 0..254) with selector bits zero.
+__device__ __forceinline__ uint32_t endpoint_word(uint32_t eb) {
+  uint32_t w = 0;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) w |= ((eb >> (2 * c)) & 3u) << (8 * c + 6);
+  return w;
+}
+
+__global__ void palette_probe_kernel(float *out) {
+  const int index = blockIdx.x * blockDim.x + threadIdx.x;
+  if (index >= 255 * 255) return;
+  const uint32_t x = index % 255;
+  const uint32_t y = index / 255;
+  Palette pal = palette8(endpoint_word(x), endpoint_word(y));
+  float4 *dst = reinterpret_cast<float4 *>(out + (size_t)index * 8);
+  dst[0] = make_float4(pal.p[0], pal.p[1], pal.p[2], pal.p[3]);
+  dst[1] = make_float4(pal.p[4], pal.p[5], pal.p[6], pal.p[7]);
+}
+
+// One thread per lane-slot of a tile: decodes two blocks into out[M][K] (bf16 bits).
+__global__ void decode_dense_kernel(const uint4 *tiles, const float *scales, int M, int K, int RG,
+                                    int CG, uint16_t *out) {
+  const size_t slot = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (slot >= (size_t)RG * CG * 64) return;
+  const int lane = slot & 63;
+  const size_t tile = slot >> 6;
+  const int g = (int)(tile / CG);
+  const int c = (int)(tile % CG);
+  const int row = g * kTileRows + (lane & 15);
+  if (row >= M) return;
+  const uint4 cur = tiles[slot];
+  const float scale = scales[row];
+  const uint32_t pm = pm_scale_pair(scale);
+  uint32_t w[2][8];
+  decode_block(cur.x, cur.y, scale, pm, w[0]);
+  decode_block(cur.z, cur.w, scale, pm, w[1]);
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int k0 = (c * kTileBlocks + 2 * (lane >> 4) + h) * 16;
+    if (k0 >= K) continue;
+    uint16_t *dst = out + (size_t)row * K + k0;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      dst[2 * q] = (uint16_t)(w[h][q] & 0xFFFFu);
+      dst[2 * q + 1] = (uint16_t)(w[h][q] >> 16);
+    }
+  }
+}
+
+}  // namespace
+
+hipError_t launch_palette_probe(float *out, hipStream_t stream) {
+  hipLaunchKernelGGL(palette_probe_kernel, dim3((255 * 255 + 255) / 256), dim3(256), 0, stream, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_decode_dense(const uint4 *tiles, const float *scales, int M, int K, int RG, int CG,
+                               uint16_t *out, hipStream_t stream) {
+  const size_t slots = (size_t)RG * CG * 64;
+  hipLaunchKernelGGL(decode_dense_kernel, dim3((unsigned)((slots + 255) / 256)), dim3(256), 0, stream, tiles, scales,
+                     M, K, RG, CG, out);
+  return hipGetLastError();
+}
+
+}  // namespace tx
