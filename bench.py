@@ -1,0 +1,268 @@
+"""Throughput of the gfx950 BC4 decode GEMV on the 27B-class linear shapes (batch 1).
+
+One "step" is one decode sweep: every q, k, v, o, gate, up and down linear of ``--layers``
+distinct layer copies, each a batch-1 GEMV with a float32 output. The
+copies are distinct device buffers, together far larger than the 256 MB Infinity Cache, so the
+weights stream from HBM. A step is captured once as a HIP graph and replayed.
+
+Prints one JSON line. ``value`` is the algorithmic HBM bytes of a step (BC4 payload + row
+scales + bf16 x + fp32 y per linear) times the step count, divided by the timed wall time.
+``roofline`` is the 5120->27648 (gate/up) GEMV alone: its algorithmic bytes divided by its
+average launch time over back-to-back launches timed with HIP events on the launch stream.
+``cpu_baseline`` is the C restatement of the decode + matvec on the host cores.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+SEED = 20260827
+HIDDEN, INTER, KV = 5120, 27648, 1024
+# (name, M = output features, K = input features)
+LAYER = [("q", HIDDEN, HIDDEN), ("k", KV, HIDDEN), ("v", KV, HIDDEN), ("o", HIDDEN, HIDDEN),
+         ("gate", INTER, HIDDEN), ("up", INTER, HIDDEN), ("down", HIDDEN, INTER)]
+DOMINANT = ("gate", "up")
+TRAFFIC_FILE = ROOT / "profiles" / "gemv_gate_up_traffic.txt"
+
+
+def gemv_bytes(m: int, k: int) -> int:
+    """Algorithmic HBM bytes of one batch-1 GEMV: payload + scales + bf16 x + fp32 y."""
+    return m * k // 2 + 4 * m + 2 * k + 4 * m
+
+
+def log(message: str) -> None:
+    print(f"[bench] {message}", file=sys.stderr, flush=True)
+
+
+def encoded_weights(torch, shapes, lut):
+    """BC4-encode one W ~ N(0, 0.02^2) * LogNormal(0, 0.3) per input channel for each shape."""
+    from texelator_amd.encoder import encode_matrix
+
+    out = {}
+    generator = torch.Generator(device="cuda").manual_seed(SEED)
+    for m, k in shapes:
+        w = torch.randn((m, k), device="cuda", generator=generator) * 0.02
+        s = torch.exp(0.3 * torch.randn(k, device="cuda", generator=generator))
+        w *= s[None, :]
+        hdiag = torch.ones(k, device="cuda")
+        out[(m, k)] = encode_matrix(w, hdiag, lut, rows_per_chunk=2048)
+        del w
+    torch.cuda.synchronize()
+    return out
+
+
+def read_traffic():
+    """HBM bytes per gate/up launch measured with rocprofv3 counters, if recorded."""
+    if not TRAFFIC_FILE.exists():
+        return None
+    for line in TRAFFIC_FILE.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return float(line.split(":", 1)[1])
+    return None
+
+
+def cpu_baseline(weights, seconds: float) -> dict:
+    """Fused BC4 decode + fp32 matvec of the C restatement, over one layer's seven linears."""
+    import numpy as np
+
+    from oracle import clib
+
+    cores = min(16, len(os.sched_getaffinity(0)))
+    clib.set_threads(cores)
+    rng = np.random.default_rng(SEED)
+    xs = {k: rng.standard_normal(k).astype(np.float32) for k in (HIDDEN, INTER)}
+    xbits = {k: (v.view(np.uint32) >> 16).astype(np.uint16) for k, v in xs.items()}
+    layer_bytes = sum(gemv_bytes(m, k) for _, m, k in LAYER)
+    sweeps = 0
+    start = time.perf_counter()
+    while True:
+        for _, m, k in LAYER:
+            blocks, scales = weights[(m, k)]
+            clib.decode_matvec_f32(blocks, scales, xbits[k])
+        sweeps += 1
+        elapsed = time.perf_counter() - start
+        if elapsed >= seconds:
+            break
+    return {
+        "value": round(layer_bytes * sweeps / elapsed / 1e9, 3),
+        "unit": "GB/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": (f"{sweeps} sweeps of one layer's 7 linears ({layer_bytes / 1e6:.1f} MB of BC4 + scales) "
+                   f"through oracle_decode_matvec_f32 (C, OpenMP, {cores} threads) on "
+                   f"{platform.processor() or platform.machine()}; {elapsed:.1f} s"),
+    }
+
+
+def main() -> int:
+    parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=200)
+    parser.add_argument("--warmup", type=int, default=20)
+    parser.add_argument("--layers", type=int, default=8, help="distinct layer copies swept per step")
+    parser.add_argument("--lookahead", type=int, default=0, help="GEMV lookahead (0 = library default)")
+    parser.add_argument("--cpu-seconds", type=float, default=10.0)
+    parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    parser.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a graph")
+    args = parser.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: the BC4 GEMV path has no multi-GPU mode in this build "
+              "(run with --gpus 1)", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from texelator_amd import hardware, runtime
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a visible GPU", file=sys.stderr)
+        return 1
+    ext = runtime.extension()
+    device = torch.device("cuda", 0)
+    torch.cuda.set_device(device)
+
+    log("probing palette and encoding weights")
+    lut = hardware.device_palette(device)
+    unique = sorted({(m, k) for _, m, k in LAYER})
+    weights = encoded_weights(torch, unique, lut)
+    del lut
+
+    log(f"packing {args.layers} layer copies")
+    handles = []  # (name, m, k, handle)
+    for _ in range(args.layers):
+        for name, m, k in LAYER:
+            blocks, scales = weights[(m, k)]
+            (handle,) = runtime.pack_arrays(blocks, scales, lookahead=args.lookahead or 1)
+            if args.lookahead:
+                ext.set_lookahead(handle, args.lookahead)
+            handles.append((name, m, k, handle))
+    lookahead = ext.lookahead(handles[0][3])
+    generator = torch.Generator(device="cuda").manual_seed(SEED + 1)
+    xs = {k: torch.randn((1, k), device=device, generator=generator).to(torch.bfloat16) for k in (HIDDEN, INTER)}
+    ys = [torch.empty((1, m), device=device, dtype=torch.float32) for _, m, _, _ in handles]
+    step_bytes = sum(gemv_bytes(m, k) for _, m, k, _ in handles)
+
+    def step():
+        for (_, _, k, handle), y in zip(handles, ys):
+            ext.linear_f32_into(handle, xs[k], y)
+
+    stream = torch.cuda.Stream(device)
+    graph = None
+    with torch.cuda.stream(stream):
+        step()
+        torch.cuda.synchronize()
+        if not args.no_graph:
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=stream):
+                step()
+            torch.cuda.synchronize()
+        run = graph.replay if graph is not None else step
+
+        log(f"warmup {args.warmup} steps")
+        for _ in range(args.warmup):
+            run()
+        torch.cuda.synchronize()
+
+        log(f"timing {args.steps} steps")
+        start = time.perf_counter()
+        for _ in range(args.steps):
+            run()
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - start
+
+        # Dominant kernel: back-to-back gate/up launches between two events on this stream,
+        # queued behind a spin kernel so that host launch cost is hidden.
+        dominant = [(h, y, k, m) for (name, m, k, h), y in zip(handles, ys) if name in DOMINANT]
+        repeats = 8
+        torch.cuda.synchronize()
+        torch.cuda._sleep(20_000_000)
+        begin = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        begin.record(stream)
+        for _ in range(repeats):
+            for h, y, k, _ in dominant:
+                ext.linear_f32_into(h, xs[k], y)
+        end.record(stream)
+        torch.cuda.synchronize()
+        launches = repeats * len(dominant)
+        dominant_s = begin.elapsed_time(end) / 1e3 / launches
+
+        # Per-shape averages, same method (reported for context).
+        per_shape = {}
+        for name, m, k in LAYER:
+            group = [(h, y) for (n, _, _, h), y in zip(handles, ys) if n == name]
+            torch.cuda._sleep(20_000_000)
+            b = torch.cuda.Event(enable_timing=True)
+            e = torch.cuda.Event(enable_timing=True)
+            b.record(stream)
+            for _ in range(repeats):
+                for h, y in group:
+                    ext.linear_f32_into(h, xs[k], y)
+            e.record(stream)
+            torch.cuda.synchronize()
+            t = b.elapsed_time(e) / 1e3 / (repeats * len(group))
+            per_shape[f"{name}_{k}x{m}"] = {"us": round(t * 1e6, 3), "GB/s": round(gemv_bytes(m, k) / t / 1e9, 1)}
+
+    gate_m, gate_k = INTER, HIDDEN
+    achieved = gemv_bytes(gate_m, gate_k) / dominant_s / 1e9
+    value = step_bytes * args.steps / elapsed / 1e9
+    result = {
+        "metric": "BC4 GEMV GB/s (% HBM peak); decode tok/s; prefill tok/s @512 tokens",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(elapsed / args.steps * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: W~N(0,0.02^2)*LogNormal(0,0.3) per input channel, BC4-encoded on device; x~N(0,1) bf16",
+        "config": {
+            "workload": "decode GEMV sweep, batch 1, 27B-class shapes q,k,v,o 5120->5120/1024, "
+                        "gate/up 5120->27648, down 27648->5120, fp32 outputs",
+            "layers": args.layers,
+            "linears_per_step": len(handles),
+            "bytes_per_step": step_bytes,
+            "graph": graph is not None,
+            "lookahead": lookahead,
+            "parallelism": "single GPU",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": read_traffic(),
+            "kernel": "gemv 5120->27648 (gate/up)",
+            "bytes_per_launch": gemv_bytes(gate_m, gate_k),
+            "avg_launch_us": round(dominant_s * 1e6, 3),
+        },
+        "per_shape": per_shape,
+    }
+    if not args.no_cpu:
+        log("cpu baseline")
+        result["cpu_baseline"] = cpu_baseline(weights, args.cpu_seconds)
+    else:
+        result["cpu_baseline"] = None
+
+    runtime.free([h for _, _, _, h in handles])
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

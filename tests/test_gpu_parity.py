@@ -70,6 +70,32 @@ def test_gemv_f32_within_tolerance(ext, oracle_threads, m, k, tokens, seed):
         assert max_rel_err_floor(ref, y[t]) <= GEMV_TOL
 
 
+@pytest.mark.parametrize("tokens", [2, 15, 16, 17, 40])
+def test_gemv_multi_token_within_tolerance(ext, oracle_threads, tokens):
+    """Below the prefill threshold several tokens share one pass of the GEMV (16 per MFMA column
+    block); every token must match its own float64 matvec."""
+    m, k = 272, 3072
+    blocks = random_blocks(m, k, 81)
+    scales = lognormal_scales(m, 82)
+    x = bf16_vector((tokens, k), 83)
+    handle = _pack(ext, blocks, scales)
+    try:
+        ext.set_prefill(handle, 1 << 20, 1024)
+        y32 = ext.linear_f32(handle, x.cuda()).cpu().numpy()
+        y16 = ext.linear(handle, x.cuda()).float().cpu().numpy()
+        single = np.stack([ext.linear_f32(handle, x[t:t + 1].cuda()).cpu().numpy()[0] for t in range(tokens)])
+    finally:
+        ext.free(handle)
+    w = clib.decode_bf16_bits(blocks, scales)
+    ref = clib.gemm_f64(bf16_bits(x), w)
+    for t in range(tokens):
+        assert rel_err(ref[t], y32[t]) <= GEMV_TOL
+        assert max_rel_err_floor(ref[t], y32[t]) <= GEMV_TOL
+        assert max_rel_err_floor(ref[t], single[t]) <= GEMV_TOL
+    # the bf16 output is the fp32 sum rounded once
+    assert max_rel_err_floor(ref, y16) <= 2 ** -8 + GEMV_TOL
+
+
 @pytest.mark.parametrize("lookahead", [1, 2, 3, 4, 6, 8])
 def test_gemv_lookahead_variants_bitwise_equal(ext, lookahead):
     m, k = 512, 5120

@@ -107,6 +107,19 @@ def linear_f32(handle: int, x: torch.Tensor) -> torch.Tensor:
     return y
 
 
+def linear_f32_into(handle: int, x: torch.Tensor, y: torch.Tensor) -> None:
+    """``linear_f32`` writing into a caller-provided float32 ``y`` (no allocation; graph-capturable).
+
+    ``x`` must be a contiguous, 16-byte aligned CUDA bf16 tensor of ``[..., K]`` and ``y`` a
+    contiguous CUDA float32 tensor of ``[..., M]`` with the same leading shape."""
+    m, k = shape(handle)
+    if (x.dtype != torch.bfloat16 or y.dtype != torch.float32 or not x.is_contiguous() or not y.is_contiguous()
+            or x.size(-1) != k or y.size(-1) != m or x.numel() // k != y.numel() // m or x.data_ptr() % 16):
+        raise TexelatorError("linear_f32_into: expected aligned contiguous bf16 x [..., K] and f32 y [..., M]")
+    check(_lib.load().tx_linear_f32(handle, ctypes.c_void_p(x.data_ptr()), x.numel() // k,
+                                    ctypes.c_void_p(y.data_ptr()), _stream(x.device)))
+
+
 def prefill(handle: int, candidate: int, x: torch.Tensor) -> torch.Tensor:
     """Prefill GEMM with an explicit tile candidate (5..9), bf16 in and out."""
     _require(x.is_cuda and x.dtype == torch.bfloat16 and x.is_contiguous(), "input must be contiguous CUDA BF16")

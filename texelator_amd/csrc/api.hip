@@ -54,7 +54,6 @@ struct Handle {
   void *bias = nullptr;
   int bias_dtype = -1;
   float *partials = nullptr;
-  uint32_t *counters = nullptr;
 
   ~Handle() {
     DeviceGuard guard(device);
@@ -62,7 +61,6 @@ struct Handle {
     if (scales) (void)hipFree(scales);
     if (bias) (void)hipFree(bias);
     if (partials) (void)hipFree(partials);
-    if (counters) (void)hipFree(counters);
     magic = 0;
   }
 };
@@ -111,14 +109,20 @@ void repack_rows(const uint8_t *blocks, const Handle &h, uint32_t *out, int g_be
   }
 }
 
+// K splits of the single-token GEMV. Tall matrices (>= 1024 row groups) fill the chip without
+// splitting; shorter ones split K so that there are about six workgroups per CU, each covering at
+// least 4 tile columns. A split never covers more tile columns than the LDS x slice holds.
 int choose_splits(int RG, int CG, int device) {
   int cus = 256;
   hipDeviceProp_t prop;
   if (hipGetDeviceProperties(&prop, device) == hipSuccess && prop.multiProcessorCount > 0) cus = prop.multiProcessorCount;
-  const int target = 8 * cus;
-  int ks = (target + RG - 1) / RG;
-  ks = std::min(ks, std::max(1, CG / 4));
-  return std::max(ks, 1);
+  int ks = 1;
+  if (RG < 1024) {
+    ks = (6 * cus + RG - 1) / RG;
+    ks = std::min(ks, std::max(1, CG / 4));
+  }
+  ks = std::max(ks, (CG + tx::kGemvMaxLdsColumns - 1) / tx::kGemvMaxLdsColumns);
+  return std::max(1, std::min(ks, CG));
 }
 
 int default_candidate(int tokens) {
@@ -162,9 +166,9 @@ int run_gemv(Handle *h, const void *x, int64_t tokens, void *y, bool f32_out, hi
   p.RG = h->RG;
   p.CG = h->CG;
   p.tokens = (int)tokens;
+  // One token: K splits reduced by a second kernel. Several tokens: one pass per 16 tokens.
   p.ks = tokens == 1 ? h->gemv_splits : 1;
   p.partials = h->partials;
-  p.counters = h->counters;
   TX_HIP(tx::launch_gemv(p, h->lookahead, f32_out, stream));
   return TX_OK;
 }
@@ -232,10 +236,6 @@ int tx_pack_encoded(const uint8_t *blocks, int64_t blocks_bytes, const float *sc
   }
   if (h->gemv_splits > 1) {
     if ((e = hipMalloc(&h->partials, (size_t)h->gemv_splits * h->Mp * sizeof(float))) != hipSuccess)
-      return cleanup(fail(TX_ERR_HIP, std::string("HIP: ") + hipGetErrorString(e)));
-    if ((e = hipMalloc(&h->counters, (size_t)h->RG * sizeof(uint32_t))) != hipSuccess)
-      return cleanup(fail(TX_ERR_HIP, std::string("HIP: ") + hipGetErrorString(e)));
-    if ((e = hipMemset(h->counters, 0, (size_t)h->RG * sizeof(uint32_t))) != hipSuccess)
       return cleanup(fail(TX_ERR_HIP, std::string("HIP: ") + hipGetErrorString(e)));
   }
   if ((e = hipDeviceSynchronize()) != hipSuccess) return cleanup(fail(TX_ERR_HIP, std::string("HIP: ") + hipGetErrorString(e)));

@@ -36,14 +36,21 @@ constexpr int kTileBlocks = 8;
 constexpr int kTileBytes = 1024;
 constexpr int kTileK = kTileBlocks * 16;  // 128 input columns per tile
 
-// Reciprocal pairs (hi = RN(1/d), lo = RN(1/d - hi)), pre-divided by 64 because the endpoint
-// extraction yields 64*e (the scaling by 2^6 is exact, so results are unchanged).
-constexpr float kR127Hi = 0x1.020408p-7f / 64.0f;
-constexpr float kR127Lo = 0x1.020408p-35f / 64.0f;
-constexpr float kR889Hi = 0x1.26e00ap-10f / 64.0f;
-constexpr float kR889Lo = -0x1.91ff6cp-35f / 64.0f;
-constexpr float kR635Hi = 0x1.9cd34p-10f / 64.0f;
-constexpr float kR635Lo = 0x1.9cd34p-38f / 64.0f;
+// Reciprocal pairs (hi = RN(1/d), lo = RN(1/d - hi)) for the correctly rounded quotients.
+constexpr float kInv127Hi = 0x1.020408p-7f;
+constexpr float kInv127Lo = 0x1.020408p-35f;
+constexpr float kInv889Hi = 0x1.26e00ap-10f;
+constexpr float kInv889Lo = -0x1.91ff6cp-35f;
+constexpr float kInv635Hi = 0x1.9cd34p-10f;
+constexpr float kInv635Lo = 0x1.9cd34p-38f;
+// The same pairs pre-divided by 64, because the register endpoint extraction yields 64*e (the
+// scaling by 2^6 is exact, so results are unchanged).
+constexpr float kR127Hi = kInv127Hi / 64.0f;
+constexpr float kR127Lo = kInv127Lo / 64.0f;
+constexpr float kR889Hi = kInv889Hi / 64.0f;
+constexpr float kR889Lo = kInv889Lo / 64.0f;
+constexpr float kR635Hi = kInv635Hi / 64.0f;
+constexpr float kR635Lo = kInv635Lo / 64.0f;
 
 // Device block whose endpoints are 0/0 and selectors 0: decodes to zero weights (padding).
 constexpr uint32_t kZeroBlockWord = 0x40C0C0C0u;
@@ -103,19 +110,10 @@ __device__ __forceinline__ Palette palette8(uint32_t a, uint32_t b) {
 // Packed bf16 pair (bf16(-scale), bf16(+scale)): slots 6 and 7 of a 6-value block.
 __device__ __forceinline__ uint32_t pm_scale_pair(float scale) { return pack_bf16x2(-scale, scale); }
 
-// Decode one device block to 16 bf16 weights (8 dwords, positions 0..15 in order).
-// w[j] holds positions 2j (low half) and 2j+1 (high half).
-__device__ __forceinline__ void decode_block(uint32_t a, uint32_t b, float scale, uint32_t pm,
-                                             uint32_t w[8]) {
-  float f0 = endpoint_x64(a);
-  float f1 = endpoint_x64(b);
-  float d = f1 - f0;
-  bool eight = f0 > f1;
-  float rhi = eight ? kR889Hi : kR635Hi;
-  float rlo = eight ? kR889Lo : kR635Lo;
-  float step = __builtin_fmaf(d, rhi, d * rlo);
-  float base = __builtin_fmaf(f0, kR127Hi, f0 * kR127Lo);
-  float end = __builtin_fmaf(f1, kR127Hi, f1 * kR127Lo);
+// Packed bf16 weights of one block from its fp32 palette seeds. w[j] holds positions 2j (low half)
+// and 2j+1 (high half). eight: 8-value mode (e0 > e1); pm: the 6-value mode's slots 6 and 7.
+__device__ __forceinline__ void decode_from_seeds(float base, float end, float step, bool eight, uint32_t a,
+                                                  uint32_t b, float scale, uint32_t pm, uint32_t w[8]) {
   float p2 = base + step;
   float p3 = __builtin_fmaf(2.0f, step, base);
   float p4 = __builtin_fmaf(3.0f, step, base);
@@ -141,6 +139,64 @@ __device__ __forceinline__ void decode_block(uint32_t a, uint32_t b, float scale
     w[2 * g] = perm(h, l, 0x05010400u);
     w[2 * g + 1] = perm(h, l, 0x07030602u);
   }
+}
+
+// Decode one device block to 16 bf16 weights, palette seeds computed in registers.
+__device__ __forceinline__ void decode_block(uint32_t a, uint32_t b, float scale, uint32_t pm,
+                                             uint32_t w[8]) {
+  float f0 = endpoint_x64(a);
+  float f1 = endpoint_x64(b);
+  float d = f1 - f0;
+  bool eight = f0 > f1;
+  float rhi = eight ? kR889Hi : kR635Hi;
+  float rlo = eight ? kR889Lo : kR635Lo;
+  float step = __builtin_fmaf(d, rhi, d * rlo);
+  float base = __builtin_fmaf(f0, kR127Hi, f0 * kR127Lo);
+  float end = __builtin_fmaf(f1, kR127Hi, f1 * kR127Lo);
+  decode_from_seeds(base, end, step, eight, a, b, scale, pm, w);
+}
+
+// LDS tables of the palette seeds, shared by a workgroup:
+//   base[eb]      = RN((eb - 127) / 127),                       eb = 0..254
+//   step[d + 254] = RN(d / 889) if d < 0 else RN(d / 635),      d = e1 - e0 = -254..254
+// (d < 0 is exactly the 8-value mode e0 > e1). Same arithmetic as decode_block.
+struct PaletteTableStorage {
+  float base[256];
+  float step[512];
+};
+
+__device__ __forceinline__ void build_palette_tables(PaletteTableStorage &t, int tid, int nthreads) {
+  for (int idx = tid; idx < 256 + 512; idx += nthreads) {
+    if (idx < 256) {
+      const float e = (float)(idx - 127);
+      t.base[idx] = __builtin_fmaf(e, kInv127Hi, e * kInv127Lo);
+    } else {
+      const int d = idx - 256 - 254;
+      const float f = (float)d;
+      const float rhi = d < 0 ? kInv889Hi : kInv635Hi;
+      const float rlo = d < 0 ? kInv889Lo : kInv635Lo;
+      t.step[idx - 256] = __builtin_fmaf(f, rhi, f * rlo);
+    }
+  }
+}
+
+// 4 * eb from the 2-bit endpoint fields in bits 6-7 of each byte: a byte offset into base[].
+__device__ __forceinline__ uint32_t endpoint_offset(uint32_t word) {
+  return __builtin_amdgcn_udot4(word & 0xC0C0C0C0u, 0x40100401u, 0u, false) >> 4;
+}
+
+// Decode one device block with the palette seeds read from LDS tables.
+__device__ __forceinline__ void decode_block_lds(uint32_t a, uint32_t b, float scale, uint32_t pm,
+                                                 const PaletteTableStorage &t, uint32_t w[8]) {
+  const uint32_t o0 = endpoint_offset(a);
+  const uint32_t o1 = endpoint_offset(b);
+  const int od = (int)o1 - (int)o0;  // 4 * (e1 - e0)
+  const char *base_bytes = reinterpret_cast<const char *>(t.base);
+  const char *step_bytes = reinterpret_cast<const char *>(t.step + 254);
+  const float base = *reinterpret_cast<const float *>(base_bytes + o0);
+  const float end = *reinterpret_cast<const float *>(base_bytes + o1);
+  const float step = *reinterpret_cast<const float *>(step_bytes + od);
+  decode_from_seeds(base, end, step, od < 0, a, b, scale, pm, w);
 }
 
 }  // namespace tx

@@ -1,16 +1,18 @@
-// Batch-1 decode GEMV over BC4 tiles (gfx950, wave64).
+// Decode GEMV over BC4 tiles (gfx950, wave64, MFMA accumulation).
 //
 // Reference: texelator_bc4_bf16_kernel<L> (texelator/cuda/texelator_cuda.cu:154-199) computes
 // y[t,m] = bf16( sum_k bf16(P*scale[m]) * x[t,k] + bias[m] ) with fp32 accumulation; L is the
-// number of texture requests in flight. Here the same sum is formed from streamed BC4 tiles:
-//   * one workgroup = 4 waves = one 16-row group x one K-slice; the x slice is staged in LDS;
-//   * each wave streams every 4th 1 KiB tile of the slice with one 128-bit load per lane
-//     (LOOKAHEAD tiles in flight), decodes its two blocks in VGPRs (bc4_device.h) and
-//     accumulates with v_dot2_f32_bf16;
-//   * lanes of one row are combined with cross-lane shuffles, waves through LDS (fixed order);
-//   * when the K range is split over workgroups, each writes an fp32 partial and the last one
-//     to arrive (agent-scope counter) sums the partials in split order, so the result does not
-//     depend on scheduling. The counter is reset by that last workgroup.
+// number of texture requests in flight per warp. Here:
+//   * a workgroup (4 waves) owns one 16-row group and one K range (a "split"); each wave streams
+//     every 4th 1 KiB tile of that range with one 128-bit load per lane, LOOKAHEAD tiles in
+//     flight, and decodes its two blocks per tile in VGPRs (decode_block_lds);
+//   * the decoded bf16 weights are the A operand of v_mfma_f32_16x16x32_bf16 (lane = row x K
+//     chunk of 8), the activations the B operand with one token per column, so one pass over the
+//     weights serves up to 16 tokens and the K reduction across lanes happens inside the MFMA;
+//   * the four waves' accumulators are summed through LDS in wave order;
+//   * with several splits each workgroup writes an fp32 partial row and a second kernel sums
+//     the partials in split order, so results never depend on scheduling.
+// Single-token calls stage x in LDS; multi-token calls read x through the cache hierarchy.
 #include "bc4_device.h"
 #include "kernels.h"
 
@@ -19,63 +21,89 @@ namespace tx {
 namespace {
 
 constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
 
-__device__ __forceinline__ float dot2(uint32_t w, uint32_t x, float acc) {
-  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w), __builtin_bit_cast(bf16x2, x),
-                                        acc, false);
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ bf16x8 as_bf16x8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+  u32x4 v = {a, b, c, d};
+  return __builtin_bit_cast(bf16x8, v);
 }
+
+__device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return as_bf16x8(v.x, v.y, v.z, v.w); }
 
 __device__ __forceinline__ float bf16_bits_to_float(uint16_t v) {
   return __builtin_bit_cast(float, (uint32_t)v << 16);
 }
 
-template <int LA, bool F32OUT>
+__device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// x of one token, 16 k-values per block: x0/x1 = block 2kg positions 0-7 / 8-15, x2/x3 = block 2kg+1.
+struct XFrag {
+  uint4 x0, x1, x2, x3;
+};
+
+__device__ __forceinline__ uint4 load_x8(const uint16_t *x, int k, int K) {
+  return k < K ? *reinterpret_cast<const uint4 *>(x + k) : make_uint4(0, 0, 0, 0);
+}
+
+// One tile for one lane: decode both blocks and accumulate 4 MFMAs (block 0 into acc0, block 1
+// into acc1; the two are added at the end in a fixed order).
+__device__ __forceinline__ void tile_mfma(uint4 cur, const XFrag &xf, float scale, uint32_t pm,
+                                          const PaletteTableStorage &t, f32x4 &acc0, f32x4 &acc1) {
+  uint32_t w[8];
+  decode_block_lds(cur.x, cur.y, scale, pm, t, w);
+  acc0 = mfma(as_bf16x8(w[0], w[1], w[2], w[3]), as_bf16x8(xf.x0), acc0);
+  acc0 = mfma(as_bf16x8(w[4], w[5], w[6], w[7]), as_bf16x8(xf.x1), acc0);
+  decode_block_lds(cur.z, cur.w, scale, pm, t, w);
+  acc1 = mfma(as_bf16x8(w[0], w[1], w[2], w[3]), as_bf16x8(xf.x2), acc1);
+  acc1 = mfma(as_bf16x8(w[4], w[5], w[6], w[7]), as_bf16x8(xf.x3), acc1);
+}
+
+template <int LA, bool MULTI, bool F32OUT>
 __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvParams p) {
-  extern __shared__ uint4 xs[];  // x slice, 16 uint4 (128 bf16) per tile column
-  __shared__ float red[4][16];
-  __shared__ int last_flag;
+  extern __shared__ uint4 xs[];  // single token: x slice, 16 uint4 (128 bf16) per tile column
+  __shared__ PaletteTableStorage tables;
+  __shared__ float red[kWaves][16][16];  // [wave][token][row]
 
   const int g = blockIdx.x;
   const int split = blockIdx.y;
-  const int token = blockIdx.z;
+  const int t0 = blockIdx.z * 16;
+  const int tc = min(16, p.tokens - t0);
   const int c_begin = (int)((int64_t)split * p.CG / p.ks);
   const int c_end = (int)((int64_t)(split + 1) * p.CG / p.ks);
   const int nc = c_end - c_begin;
+  const uint16_t *x = static_cast<const uint16_t *>(p.x);
 
-  const uint16_t *x = static_cast<const uint16_t *>(p.x) + (size_t)token * p.K;
-  for (int idx = threadIdx.x; idx < nc * 16; idx += kThreads) {
-    const int k0 = (c_begin * 16 + idx) * 8;
-    uint4 v;
-    if (k0 + 8 <= p.K) {
-      v = *reinterpret_cast<const uint4 *>(x + k0);
-    } else {
-      uint16_t e[8];
-#pragma unroll
-      for (int q = 0; q < 8; ++q) e[q] = (k0 + q < p.K) ? x[k0 + q] : (uint16_t)0;
-      v.x = e[0] | ((uint32_t)e[1] << 16);
-      v.y = e[2] | ((uint32_t)e[3] << 16);
-      v.z = e[4] | ((uint32_t)e[5] << 16);
-      v.w = e[6] | ((uint32_t)e[7] << 16);
+  build_palette_tables(tables, threadIdx.x, kThreads);
+  if constexpr (!MULTI) {
+    for (int idx = threadIdx.x; idx < nc * 16; idx += kThreads) {
+      const int k0 = (c_begin * 16 + idx) * 8;
+      xs[idx] = load_x8(x, k0, p.K);  // K is a multiple of 16: a chunk of 8 is wholly in or out
     }
-    xs[idx] = v;
   }
   __syncthreads();
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int i = lane & 15;
-  const int kg = lane >> 4;
+  const int i = lane & 15;   // weight row within the group; token column of the B operand
+  const int kg = lane >> 4;  // K chunk: blocks 2kg and 2kg+1 of each tile
   const int row = g * kTileRows + i;
   const float scale = p.scales[row];
   const uint32_t pm = pm_scale_pair(scale);
   const uint4 *tile_ptr = p.tiles + ((size_t)g * p.CG + c_begin) * 64 + lane;
-  const int nt = nc > wave ? (nc - wave + 3) / 4 : 0;
+  const int nt = nc > wave ? (nc - wave + kWaves - 1) / kWaves : 0;
+  // Multi-token: this lane's token column (duplicates the last token past the end).
+  const uint16_t *xrow = x + (size_t)(t0 + min(i, tc - 1)) * p.K;
 
-  float acc0 = 0.f, acc1 = 0.f, acc2 = 0.f, acc3 = 0.f;
+  f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
   uint4 buf[LA];
 #pragma unroll
   for (int u = 0; u < LA; ++u)
-    if (u < nt) buf[u] = load_stream(tile_ptr + (size_t)(u * 4 + wave) * 64);
+    if (u < nt) buf[u] = load_stream(tile_ptr + (size_t)(u * kWaves + wave) * 64);
 
   for (int j0 = 0; j0 < nt; j0 += LA) {
 #pragma unroll
@@ -83,88 +111,89 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvParams p) {
       const int j = j0 + u;
       if (j < nt) {
         const uint4 cur = buf[u];
-        if (j + LA < nt) buf[u] = load_stream(tile_ptr + (size_t)((j + LA) * 4 + wave) * 64);
-        const uint4 *xv = xs + (j * 4 + wave) * 16 + kg * 4;
-        const uint4 x0 = xv[0], x1 = xv[1], x2 = xv[2], x3 = xv[3];
-        uint32_t w[8];
-        decode_block(cur.x, cur.y, scale, pm, w);
-        acc0 = dot2(w[0], x0.x, acc0);
-        acc1 = dot2(w[1], x0.y, acc1);
-        acc0 = dot2(w[2], x0.z, acc0);
-        acc1 = dot2(w[3], x0.w, acc1);
-        acc0 = dot2(w[4], x1.x, acc0);
-        acc1 = dot2(w[5], x1.y, acc1);
-        acc0 = dot2(w[6], x1.z, acc0);
-        acc1 = dot2(w[7], x1.w, acc1);
-        decode_block(cur.z, cur.w, scale, pm, w);
-        acc2 = dot2(w[0], x2.x, acc2);
-        acc3 = dot2(w[1], x2.y, acc3);
-        acc2 = dot2(w[2], x2.z, acc2);
-        acc3 = dot2(w[3], x2.w, acc3);
-        acc2 = dot2(w[4], x3.x, acc2);
-        acc3 = dot2(w[5], x3.y, acc3);
-        acc2 = dot2(w[6], x3.z, acc2);
-        acc3 = dot2(w[7], x3.w, acc3);
+        if (j + LA < nt) buf[u] = load_stream(tile_ptr + (size_t)((j + LA) * kWaves + wave) * 64);
+        const int col = j * kWaves + wave;  // tile column within this split
+        XFrag xf;
+        if constexpr (MULTI) {
+          const int k = (c_begin + col) * kTileK + kg * 32;
+          xf.x0 = load_x8(xrow, k, p.K);
+          xf.x1 = load_x8(xrow, k + 8, p.K);
+          xf.x2 = load_x8(xrow, k + 16, p.K);
+          xf.x3 = load_x8(xrow, k + 24, p.K);
+        } else {
+          const uint4 *xv = xs + col * 16 + kg * 4;
+          xf.x0 = xv[0];
+          xf.x1 = xv[1];
+          xf.x2 = xv[2];
+          xf.x3 = xv[3];
+        }
+        tile_mfma(cur, xf, scale, pm, tables, acc0, acc1);
       }
     }
   }
 
-  float acc = (acc0 + acc1) + (acc2 + acc3);
-  acc += __shfl_xor(acc, 16);
-  acc += __shfl_xor(acc, 32);
-  if (lane < 16) red[wave][lane] = acc;
+  // acc[r] = partial y[token i][row 4kg + r] of this wave.
+  const f32x4 acc = acc0 + acc1;
+  if (i < tc) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) red[wave][i][kg * 4 + r] = acc[r];
+  }
   __syncthreads();
 
-  float total = 0.f;
-  if (threadIdx.x < 16) total = ((red[0][threadIdx.x] + red[1][threadIdx.x]) + red[2][threadIdx.x]) + red[3][threadIdx.x];
-
-  if (p.ks > 1) {
-    if (threadIdx.x < 16) {
-      p.partials[(size_t)split * p.Mp + g * kTileRows + threadIdx.x] = total;
-      __threadfence();
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      const uint32_t prior = __hip_atomic_fetch_add(p.counters + g, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-      last_flag = (prior == (uint32_t)(p.ks - 1));
-    }
-    __syncthreads();
-    if (!last_flag) return;
-    __threadfence();
-    if (threadIdx.x < 16) {
-      total = 0.f;
-      for (int s = 0; s < p.ks; ++s)
-        total += __hip_atomic_load(p.partials + (size_t)s * p.Mp + g * kTileRows + threadIdx.x, __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
-    }
-    if (threadIdx.x == 0)
-      __hip_atomic_store(p.counters + g, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-
-  if (threadIdx.x < 16) {
-    const int out_row = g * kTileRows + threadIdx.x;
-    if (out_row < p.M) {
+  if (threadIdx.x < tc * 16) {
+    const int n = threadIdx.x >> 4;
+    const int rr = threadIdx.x & 15;
+    float total = red[0][n][rr];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) total += red[w][n][rr];
+    const int out_row = g * kTileRows + rr;
+    const int token = t0 + n;
+    if (p.ks > 1) {
+      p.partials[((size_t)split * p.tokens + token) * p.Mp + out_row] = total;
+    } else if (out_row < p.M) {
       if constexpr (F32OUT) {
         static_cast<float *>(p.y)[(size_t)token * p.M + out_row] = total;
       } else {
-        float value = total;
-        if (p.bias) value += bf16_bits_to_float(static_cast<const uint16_t *>(p.bias)[out_row]);
-        static_cast<__bf16 *>(p.y)[(size_t)token * p.M + out_row] = (__bf16)value;
+        if (p.bias) total += bf16_bits_to_float(static_cast<const uint16_t *>(p.bias)[out_row]);
+        static_cast<__bf16 *>(p.y)[(size_t)token * p.M + out_row] = (__bf16)total;
       }
     }
   }
 }
 
+// y[t][m] = sum over splits s (in order) of partials[s][t][m], then bias and output cast.
+template <bool F32OUT>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(GemvParams p) {
+  const int m = blockIdx.x * 256 + threadIdx.x;
+  const int token = blockIdx.y;
+  if (m >= p.M) return;
+  float total = 0.f;
+  for (int s = 0; s < p.ks; ++s) total += p.partials[((size_t)s * p.tokens + token) * p.Mp + m];
+  if constexpr (F32OUT) {
+    static_cast<float *>(p.y)[(size_t)token * p.M + m] = total;
+  } else {
+    if (p.bias) total += bf16_bits_to_float(static_cast<const uint16_t *>(p.bias)[m]);
+    static_cast<__bf16 *>(p.y)[(size_t)token * p.M + m] = (__bf16)total;
+  }
+}
+
+template <int LA, bool MULTI, bool F32OUT>
+hipError_t launch_variant(const GemvParams &p, hipStream_t stream) {
+  const int max_cols = (p.CG + p.ks - 1) / p.ks;
+  const size_t lds = MULTI ? 0 : (size_t)max_cols * 16 * sizeof(uint4);
+  dim3 grid(p.RG, p.ks, (p.tokens + 15) / 16);
+  hipLaunchKernelGGL((gemv_kernel<LA, MULTI, F32OUT>), grid, dim3(kThreads), lds, stream, p);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || p.ks == 1) return e;
+  hipLaunchKernelGGL((splitk_reduce_kernel<F32OUT>), dim3((p.M + 255) / 256, p.tokens), dim3(256), 0, stream, p);
+  return hipGetLastError();
+}
+
 template <int LA>
 hipError_t launch_la(const GemvParams &p, bool f32_out, hipStream_t stream) {
-  const int max_cols = (p.CG + p.ks - 1) / p.ks;
-  const size_t lds = (size_t)max_cols * 16 * sizeof(uint4);
-  dim3 grid(p.RG, p.ks, p.tokens);
-  if (f32_out)
-    hipLaunchKernelGGL((gemv_kernel<LA, true>), grid, dim3(kThreads), lds, stream, p);
-  else
-    hipLaunchKernelGGL((gemv_kernel<LA, false>), grid, dim3(kThreads), lds, stream, p);
-  return hipGetLastError();
+  const bool multi = p.tokens > 1;
+  if (multi) return f32_out ? launch_variant<LA, true, true>(p, stream) : launch_variant<LA, true, false>(p, stream);
+  return f32_out ? launch_variant<LA, false, true>(p, stream) : launch_variant<LA, false, false>(p, stream);
 }
 
 }  // namespace
@@ -185,12 +214,12 @@ hipError_t launch_gemv(const GemvParams &p, int lookahead, bool f32_out, hipStre
 
 hipError_t gemv_kernel_attributes(int lookahead, hipFuncAttributes *attr) {
   switch (lookahead) {
-    case 1: return hipFuncGetAttributes(attr, reinterpret_cast<const void *>(&gemv_kernel<1, false>));
-    case 2: return hipFuncGetAttributes(attr, reinterpret_cast<const void *>(&gemv_kernel<2, false>));
-    case 3: return hipFuncGetAttributes(attr, reinterpret_cast<const void *>(&gemv_kernel<3, false>));
-    case 4: return hipFuncGetAttributes(attr, reinterpret_cast<const void *>(&gemv_kernel<4, false>));
-    case 6: return hipFuncGetAttributes(attr, reinterpret_cast<const void *>(&gemv_kernel<6, false>));
-    case 8: return hipFuncGetAttributes(attr, reinterpret_cast<const void *>(&gemv_kernel<8, false>));
+    case 1: return hipFuncGetAttributes(attr, reinterpret_cast<const void *>(&gemv_kernel<1, false, false>));
+    case 2: return hipFuncGetAttributes(attr, reinterpret_cast<const void *>(&gemv_kernel<2, false, false>));
+    case 3: return hipFuncGetAttributes(attr, reinterpret_cast<const void *>(&gemv_kernel<3, false, false>));
+    case 4: return hipFuncGetAttributes(attr, reinterpret_cast<const void *>(&gemv_kernel<4, false, false>));
+    case 6: return hipFuncGetAttributes(attr, reinterpret_cast<const void *>(&gemv_kernel<6, false, false>));
+    case 8: return hipFuncGetAttributes(attr, reinterpret_cast<const void *>(&gemv_kernel<8, false, false>));
     default: return hipErrorInvalidValue;
   }
 }

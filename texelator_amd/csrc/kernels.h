@@ -14,10 +14,13 @@ struct GemvParams {
   const void *x;           // [tokens][K] bf16
   const void *bias;        // [M] bf16 or nullptr
   void *y;                 // [tokens][M] bf16 or f32
-  float *partials;         // [ks][Mp] when ks > 1
-  uint32_t *counters;      // [RG] when ks > 1, all zero between launches
+  float *partials;         // [ks][tokens][Mp] when ks > 1
   int M, K, Mp, RG, CG, ks, tokens;
 };
+
+// Single-token GEMV stages the x slice of a split in LDS: at most this many tile columns
+// (128 input features each) per split.
+constexpr int kGemvMaxLdsColumns = 128;
 
 struct PrefillParams {
   const uint4 *tiles;
