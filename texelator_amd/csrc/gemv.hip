@@ -78,6 +78,22 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvParams p) {
   const int nc = c_end - c_begin;
   const uint16_t *x = static_cast<const uint16_t *>(p.x);
 
+  const int lane = threadIdx.x & 63;
+  // The wave index is uniform across the wave: keep it (and everything derived from it, the
+  // tile loop included) in scalar registers.
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nt = nc > wave ? (nc - wave + kWaves - 1) / kWaves : 0;
+  // Tile j of this wave is tile column c_begin + j*kWaves + wave of row group g.
+  const uint4 *wave_tiles = p.tiles + ((size_t)g * p.CG + c_begin + wave) * 64;
+
+  // Ring of LA+1 tile slots: while tile j is decoded, tiles j+1..j+LA are in flight. The first
+  // loads are issued before the LDS set-up so that they overlap it.
+  constexpr int R = LA + 1;
+  uint4 ring[R];
+#pragma unroll
+  for (int u = 0; u < LA; ++u)
+    ring[u] = load_stream(wave_tiles + (size_t)min(u, max(nt - 1, 0)) * kWaves * 64 + lane);
+
   build_palette_tables(tables, threadIdx.x, kThreads);
   if constexpr (!MULTI) {
     for (int idx = threadIdx.x; idx < nc * 16; idx += kThreads) {
@@ -87,50 +103,49 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvParams p) {
   }
   __syncthreads();
 
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
   const int i = lane & 15;   // weight row within the group; token column of the B operand
   const int kg = lane >> 4;  // K chunk: blocks 2kg and 2kg+1 of each tile
   const int row = g * kTileRows + i;
   const float scale = p.scales[row];
   const uint32_t pm = pm_scale_pair(scale);
-  const uint4 *tile_ptr = p.tiles + ((size_t)g * p.CG + c_begin) * 64 + lane;
-  const int nt = nc > wave ? (nc - wave + kWaves - 1) / kWaves : 0;
   // Multi-token: this lane's token column (duplicates the last token past the end).
   const uint16_t *xrow = x + (size_t)(t0 + min(i, tc - 1)) * p.K;
 
   f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-  uint4 buf[LA];
-#pragma unroll
-  for (int u = 0; u < LA; ++u)
-    if (u < nt) buf[u] = load_stream(tile_ptr + (size_t)(u * kWaves + wave) * 64);
+  auto consume = [&](const uint4 &tile, int j) {
+    const int col = j * kWaves + wave;  // tile column within this split
+    XFrag xf;
+    if constexpr (MULTI) {
+      const int k = (c_begin + col) * kTileK + kg * 32;
+      xf.x0 = load_x8(xrow, k, p.K);
+      xf.x1 = load_x8(xrow, k + 8, p.K);
+      xf.x2 = load_x8(xrow, k + 16, p.K);
+      xf.x3 = load_x8(xrow, k + 24, p.K);
+    } else {
+      const uint4 *xv = xs + col * 16 + kg * 4;
+      xf.x0 = xv[0];
+      xf.x1 = xv[1];
+      xf.x2 = xv[2];
+      xf.x3 = xv[3];
+    }
+    tile_mfma(tile, xf, scale, pm, tables, acc0, acc1);
+  };
 
-  for (int j0 = 0; j0 < nt; j0 += LA) {
+  // Main loop over whole ring turns, branch-free: every step issues exactly one load (clamped to
+  // the wave's last tile near the end), so each decode waits only for its own tile.
+  int j0 = 0;
+  for (; j0 + R <= nt; j0 += R) {
 #pragma unroll
-    for (int u = 0; u < LA; ++u) {
-      const int j = j0 + u;
-      if (j < nt) {
-        const uint4 cur = buf[u];
-        if (j + LA < nt) buf[u] = load_stream(tile_ptr + (size_t)((j + LA) * kWaves + wave) * 64);
-        const int col = j * kWaves + wave;  // tile column within this split
-        XFrag xf;
-        if constexpr (MULTI) {
-          const int k = (c_begin + col) * kTileK + kg * 32;
-          xf.x0 = load_x8(xrow, k, p.K);
-          xf.x1 = load_x8(xrow, k + 8, p.K);
-          xf.x2 = load_x8(xrow, k + 16, p.K);
-          xf.x3 = load_x8(xrow, k + 24, p.K);
-        } else {
-          const uint4 *xv = xs + col * 16 + kg * 4;
-          xf.x0 = xv[0];
-          xf.x1 = xv[1];
-          xf.x2 = xv[2];
-          xf.x3 = xv[3];
-        }
-        tile_mfma(cur, xf, scale, pm, tables, acc0, acc1);
-      }
+    for (int u = 0; u < R; ++u) {
+      const int jn = min(j0 + u + LA, nt - 1);
+      ring[(u + LA) % R] = load_stream(wave_tiles + (size_t)jn * kWaves * 64 + lane);
+      consume(ring[u], j0 + u);
     }
   }
+  // Tail: at most LA tiles, already in slots 0..LA-1.
+#pragma unroll
+  for (int u = 0; u < LA; ++u)
+    if (j0 + u < nt) consume(ring[u], j0 + u);
 
   // acc[r] = partial y[token i][row 4kg + r] of this wave.
   const f32x4 acc = acc0 + acc1;
