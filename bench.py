@@ -32,7 +32,7 @@ HIDDEN, INTER, KV = 5120, 27648, 1024
 LAYER = [("q", HIDDEN, HIDDEN), ("k", KV, HIDDEN), ("v", KV, HIDDEN), ("o", HIDDEN, HIDDEN),
          ("gate", INTER, HIDDEN), ("up", INTER, HIDDEN), ("down", HIDDEN, INTER)]
 DOMINANT = ("gate", "up")
-TRAFFIC_FILE = ROOT / "profiles" / "gemv_gate_up_traffic.txt"
+TRAFFIC_FILE = ROOT / "profiles" / "gemv_gate_up_5120x27648.md"
 
 
 def gemv_bytes(m: int, k: int) -> int:
@@ -104,6 +104,79 @@ def cpu_baseline(weights, seconds: float) -> dict:
     }
 
 
+COPY_BYTES = 1 << 30
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+PREFILL_TOKENS = (32, 128, 512)
+PREFILL_SHAPES = ("q", "gate", "down")
+
+
+def timed_launches(torch, stream, launch, count: int) -> float:
+    """Seconds per launch of ``count`` back-to-back launches, queued behind a spin kernel so that
+    the host cost of issuing them is hidden, timed with events on ``stream``."""
+    torch.cuda.synchronize()
+    torch.cuda._sleep(20_000_000)
+    begin = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    begin.record(stream)
+    for i in range(count):
+        launch(i)
+    end.record(stream)
+    torch.cuda.synchronize()
+    return begin.elapsed_time(end) / 1e3 / count
+
+
+def prefill_section(torch, ext, stream, handles, candidates=range(5, 10), repeats: int = 2) -> dict:
+    """bf16 prefill GEMM per shape and token count: every tile candidate timed over the layer
+    copies; reports the fastest, its TFLOP/s and MFMA utilisation against the dense bf16 peak."""
+    out = {}
+    generator = torch.Generator(device="cuda").manual_seed(SEED + 2)
+    for name in PREFILL_SHAPES:
+        group = [(m, k, h) for (n, m, k, h) in handles if n == name]
+        m, k, _ = group[0]
+        for tokens in PREFILL_TOKENS:
+            x = torch.randn((tokens, k), device="cuda", generator=generator).to(torch.bfloat16)
+            y = torch.empty((tokens, m), device="cuda", dtype=torch.bfloat16)
+            times = {}
+            for cand in candidates:
+                launch = lambda i, c=cand: ext.prefill_into(group[i % len(group)][2], c, x, y)  # noqa: E731
+                launch(0)
+                times[cand] = timed_launches(torch, stream, launch, repeats * len(group))
+            best = min(times, key=times.get)
+            flops = 2.0 * tokens * m * k
+            tflops = flops / times[best] / 1e12
+            out[f"{name}_{k}x{m}_T{tokens}"] = {
+                "best": ext.candidate_name(best), "us": round(times[best] * 1e6, 2),
+                "TFLOP/s": round(tflops, 1), "mfma_util": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+                "tokens_per_s": round(tokens / times[best], 1),
+                "all_us": {ext.candidate_name(c): round(t * 1e6, 2) for c, t in times.items()},
+            }
+    return out
+
+
+def kernel_only(torch, ext, runtime, hardware, device, args) -> int:
+    """Launches for counter runs: the 5120->27648 GEMV on ``--layers`` distinct copies, three
+    times each, then one device-to-device copy of COPY_BYTES (read COPY_BYTES, write COPY_BYTES)
+    whose FETCH_SIZE/WRITE_SIZE readings give the counters' scale."""
+    lut = hardware.device_palette(device)
+    blocks, scales = encoded_weights(torch, [(INTER, HIDDEN)], lut)[(INTER, HIDDEN)]
+    handles = [runtime.pack_arrays(blocks, scales, lookahead=args.lookahead or 1)[0] for _ in range(args.layers)]
+    x = torch.randn((1, HIDDEN), device=device).to(torch.bfloat16)
+    y = torch.empty((1, INTER), device=device, dtype=torch.float32)
+    for _ in range(3):
+        for handle in handles:
+            ext.linear_f32_into(handle, x, y)
+    torch.cuda.synchronize()
+    src = torch.empty(COPY_BYTES, dtype=torch.uint8, device=device).fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    runtime.free(handles)
+    print(json.dumps({"kernel_only": True, "launches": 3 * len(handles), "bytes_per_launch": gemv_bytes(INTER, HIDDEN),
+                      "copy_bytes": COPY_BYTES}), flush=True)
+    return 0
+
+
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     parser.add_argument("--gpus", type=int, default=1)
@@ -114,6 +187,10 @@ def main() -> int:
     parser.add_argument("--cpu-seconds", type=float, default=10.0)
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     parser.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a graph")
+    parser.add_argument("--no-prefill", action="store_true", help="skip the prefill GEMM measurements")
+    parser.add_argument("--kernel-only", action="store_true",
+                        help="profiling mode: only the gate/up GEMV over the layer copies, then a plain copy of "
+                             "COPY_BYTES bytes that calibrates the HBM byte counters")
     args = parser.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -131,6 +208,9 @@ def main() -> int:
     ext = runtime.extension()
     device = torch.device("cuda", 0)
     torch.cuda.set_device(device)
+
+    if args.kernel_only:
+        return kernel_only(torch, ext, runtime, hardware, device, args)
 
     log("probing palette and encoding weights")
     lut = hardware.device_palette(device)
@@ -253,6 +333,10 @@ def main() -> int:
         },
         "per_shape": per_shape,
     }
+    if not args.no_prefill:
+        log("prefill GEMM")
+        with torch.cuda.stream(stream):
+            result["prefill"] = prefill_section(torch, ext, stream, handles)
     if not args.no_cpu:
         log("cpu baseline")
         result["cpu_baseline"] = cpu_baseline(weights, args.cpu_seconds)

@@ -134,6 +134,16 @@ def prefill(handle: int, candidate: int, x: torch.Tensor) -> torch.Tensor:
     return y
 
 
+def prefill_into(handle: int, candidate: int, x: torch.Tensor, y: torch.Tensor) -> None:
+    """``prefill`` writing into a caller-provided bf16 ``y`` of ``[..., M]`` (no allocation)."""
+    m, k = shape(handle)
+    if (x.dtype != torch.bfloat16 or y.dtype != torch.bfloat16 or not x.is_contiguous() or not y.is_contiguous()
+            or x.size(-1) != k or y.size(-1) != m or x.numel() // k != y.numel() // m or x.data_ptr() % 16):
+        raise TexelatorError("prefill_into: expected aligned contiguous bf16 x [..., K] and bf16 y [..., M]")
+    check(_lib.load().tx_prefill(handle, int(candidate), ctypes.c_void_p(x.data_ptr()), x.numel() // k,
+                                 ctypes.c_void_p(y.data_ptr()), _stream(x.device)))
+
+
 def set_lookahead(handle: int, lookahead: int) -> None:
     check(_lib.load().tx_set_lookahead(handle, int(lookahead)))
 
