@@ -136,9 +136,11 @@ def prefill_section(torch, ext, stream, handles, candidates=range(5, 10), repeat
         for tokens in PREFILL_TOKENS:
             x = torch.randn((tokens, k), device="cuda", generator=generator).to(torch.bfloat16)
             y = torch.empty((tokens, m), device="cuda", dtype=torch.bfloat16)
+            nbytes = ext.workspace_bytes(group[0][2], tokens)
+            ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device="cuda")
             times = {}
             for cand in candidates:
-                launch = lambda i, c=cand: ext.prefill_into(group[i % len(group)][2], c, x, y)  # noqa: E731
+                launch = lambda i, c=cand: ext.prefill_into(group[i % len(group)][2], c, x, y, ws)  # noqa: E731
                 launch(0)
                 times[cand] = timed_launches(torch, stream, launch, repeats * len(group))
             best = min(times, key=times.get)
@@ -148,6 +150,7 @@ def prefill_section(torch, ext, stream, handles, candidates=range(5, 10), repeat
                 "best": ext.candidate_name(best), "us": round(times[best] * 1e6, 2),
                 "TFLOP/s": round(tflops, 1), "mfma_util": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
                 "tokens_per_s": round(tokens / times[best], 1),
+                "workspace_bytes": nbytes,
                 "all_us": {ext.candidate_name(c): round(t * 1e6, 2) for c, t in times.items()},
             }
     return out

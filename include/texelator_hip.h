@@ -41,22 +41,33 @@ int tx_pack_encoded(const uint8_t *blocks, int64_t blocks_bytes, const float *sc
                     const void *bias, int bias_dtype, int device, uint64_t *handle_out);
 
 /* y = x W^T (+ bias). Replaces texelator_linear (texelator_cuda.cu:1329-1469; extension.cpp:30).
- *   x        device, contiguous [tokens][K] of x_dtype (BF16; F16 is reported unsupported)
- *   x_numel  number of elements of x; tokens = x_numel / K
- *   x_last   size of x's last dimension (must equal K)
- *   y        device output [tokens][M] of x_dtype, allocated by the caller
+ *   x         device, contiguous, 16-byte aligned [tokens][K] of x_dtype (BF16; F16 is reported
+ *             unsupported)
+ *   x_numel   number of elements of x; tokens = x_numel / K
+ *   x_last    size of x's last dimension (must equal K)
+ *   y         device output [tokens][M] of x_dtype, allocated by the caller
+ *   workspace device scratch of at least tx_workspace_bytes(handle, tokens) bytes, 16-byte
+ *             aligned (may be NULL when that is 0); used only by the prefill path, stream-ordered
  * tokens >= prefill threshold (and tokens > 1) uses the prefill GEMM candidate set by
- * tx_set_prefill_backend; otherwise the decode GEMV with the configured lookahead. */
+ * tx_set_prefill_backend; otherwise the decode GEMV with the configured lookahead.
+ * The reference allocates its prefill scratch inside the call (texelator_cuda.cu:942-957); here
+ * the caller supplies it, so the library never allocates on this path. */
 int tx_linear(uint64_t handle, const void *x, int x_dtype, int64_t x_numel, int64_t x_last,
-              int device, void *y, void *stream);
+              int device, void *y, void *workspace, int64_t workspace_bytes, void *stream);
+
+/* Workspace bytes tx_linear's prefill path and tx_prefill need for `tokens` tokens (split-K
+ * partial sums; 0 when the shape is not split). No reference counterpart (see tx_linear). */
+int tx_workspace_bytes(uint64_t handle, int64_t tokens, int64_t *bytes);
 
 /* Decode GEMV with float32 output and no bias, for parity checks (no reference counterpart:
  * the reference only returns 16-bit outputs). x: device bf16 [tokens][K]; y: device f32. */
 int tx_linear_f32(uint64_t handle, const void *x, int64_t tokens, float *y, void *stream);
 
-/* Prefill GEMM with an explicit candidate (5..9), bf16 in/out, bias applied if present.
- * Used by the tile autotuner (reference: set_prefill_backend + linear, autotune.py:144-187). */
-int tx_prefill(uint64_t handle, int candidate, const void *x, int64_t tokens, void *y, void *stream);
+/* Prefill GEMM with an explicit candidate (5..9), bf16 in/out, bias applied if present; same
+ * workspace rule as tx_linear. Used by the tile autotuner (reference: set_prefill_backend +
+ * linear, autotune.py:144-187). */
+int tx_prefill(uint64_t handle, int candidate, const void *x, int64_t tokens, void *y,
+               void *workspace, int64_t workspace_bytes, void *stream);
 
 /* Replaces texelator_set_lookahead (texelator_cuda.cu:1471-1478): one of 1,2,3,4,6,8. */
 int tx_set_lookahead(uint64_t handle, int lookahead);

@@ -39,6 +39,22 @@ def _aligned(x: torch.Tensor) -> torch.Tensor:
     return x if x.data_ptr() % 16 == 0 else x.clone()
 
 
+def workspace_bytes(handle: int, tokens: int) -> int:
+    """Device scratch the prefill path needs for ``tokens`` tokens (``tx_workspace_bytes``)."""
+    out = ctypes.c_int64(0)
+    check(_lib.load().tx_workspace_bytes(handle, int(tokens), ctypes.byref(out)))
+    return int(out.value)
+
+
+def _workspace(handle: int, tokens: int, device: torch.device):
+    """Stream-ordered scratch from the caching allocator (None when the shape needs none)."""
+    nbytes = workspace_bytes(handle, tokens) if tokens > 1 else 0
+    if nbytes == 0:
+        return None, ctypes.c_void_p(None), 0
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
+    return ws, ctypes.c_void_p(ws.data_ptr()), nbytes
+
+
 def shape(handle: int) -> tuple[int, int]:
     """(M, K) of a handle, cached."""
     cached = _SHAPES.get(handle)
@@ -88,8 +104,12 @@ def linear(handle: int, x: torch.Tensor) -> torch.Tensor:
     out_shape[-1] = m
     y = torch.empty(out_shape, dtype=x.dtype, device=x.device)
     x = _aligned(x)
+    tokens = x.numel() // k
+    ws, ws_ptr, ws_bytes = _workspace(handle, tokens, x.device)
     check(_lib.load().tx_linear(handle, ctypes.c_void_p(x.data_ptr()), _DTYPE_CODE[x.dtype], x.numel(),
-                                x.size(-1), x.device.index, ctypes.c_void_p(y.data_ptr()), _stream(x.device)))
+                                x.size(-1), x.device.index, ctypes.c_void_p(y.data_ptr()), ws_ptr, ws_bytes,
+                                _stream(x.device)))
+    del ws
     return y
 
 
@@ -129,19 +149,27 @@ def prefill(handle: int, candidate: int, x: torch.Tensor) -> torch.Tensor:
     out_shape[-1] = m
     y = torch.empty(out_shape, dtype=torch.bfloat16, device=x.device)
     x = _aligned(x)
-    check(_lib.load().tx_prefill(handle, int(candidate), ctypes.c_void_p(x.data_ptr()), x.numel() // k,
-                                 ctypes.c_void_p(y.data_ptr()), _stream(x.device)))
+    tokens = x.numel() // k
+    ws, ws_ptr, ws_bytes = _workspace(handle, tokens, x.device)
+    check(_lib.load().tx_prefill(handle, int(candidate), ctypes.c_void_p(x.data_ptr()), tokens,
+                                 ctypes.c_void_p(y.data_ptr()), ws_ptr, ws_bytes, _stream(x.device)))
+    del ws
     return y
 
 
-def prefill_into(handle: int, candidate: int, x: torch.Tensor, y: torch.Tensor) -> None:
-    """``prefill`` writing into a caller-provided bf16 ``y`` of ``[..., M]`` (no allocation)."""
+def prefill_into(handle: int, candidate: int, x: torch.Tensor, y: torch.Tensor,
+                 workspace: torch.Tensor | None = None) -> None:
+    """``prefill`` writing into a caller-provided bf16 ``y`` of ``[..., M]``; ``workspace`` (a
+    CUDA tensor of at least ``workspace_bytes(handle, tokens)`` bytes) is required when that is
+    nonzero."""
     m, k = shape(handle)
     if (x.dtype != torch.bfloat16 or y.dtype != torch.bfloat16 or not x.is_contiguous() or not y.is_contiguous()
             or x.size(-1) != k or y.size(-1) != m or x.numel() // k != y.numel() // m or x.data_ptr() % 16):
         raise TexelatorError("prefill_into: expected aligned contiguous bf16 x [..., K] and bf16 y [..., M]")
+    ws_ptr = ctypes.c_void_p(workspace.data_ptr()) if workspace is not None else ctypes.c_void_p(None)
+    ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
     check(_lib.load().tx_prefill(handle, int(candidate), ctypes.c_void_p(x.data_ptr()), x.numel() // k,
-                                 ctypes.c_void_p(y.data_ptr()), _stream(x.device)))
+                                 ctypes.c_void_p(y.data_ptr()), ws_ptr, ws_bytes, _stream(x.device)))
 
 
 def set_lookahead(handle: int, lookahead: int) -> None:

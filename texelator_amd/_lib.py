@@ -7,8 +7,12 @@ from __future__ import annotations
 import ctypes
 from pathlib import Path
 
+import os
+
 PACKAGE_ROOT = Path(__file__).resolve().parent
-LIBRARY_PATH = PACKAGE_ROOT / "libtexelator_hip.so"
+# TEXELATOR_HIP_LIBRARY selects another build of the same library (e.g. one compiled with
+# different tile constants by texelator_amd.build); the default is the in-tree build.
+LIBRARY_PATH = Path(os.environ.get("TEXELATOR_HIP_LIBRARY", PACKAGE_ROOT / "libtexelator_hip.so"))
 
 TX_OK = 0
 TX_ERR_INVALID = 1
@@ -27,9 +31,10 @@ _U64 = ctypes.c_uint64
 SIGNATURES = {
     "tx_last_error": (ctypes.c_char_p, []),
     "tx_pack_encoded": (_I32, [_P, _I64, _P, _I64, _P, _I32, _I32, ctypes.POINTER(_U64)]),
-    "tx_linear": (_I32, [_U64, _P, _I32, _I64, _I64, _I32, _P, _P]),
+    "tx_linear": (_I32, [_U64, _P, _I32, _I64, _I64, _I32, _P, _P, _I64, _P]),
+    "tx_workspace_bytes": (_I32, [_U64, _I64, ctypes.POINTER(_I64)]),
     "tx_linear_f32": (_I32, [_U64, _P, _I64, _P, _P]),
-    "tx_prefill": (_I32, [_U64, _I32, _P, _I64, _P, _P]),
+    "tx_prefill": (_I32, [_U64, _I32, _P, _I64, _P, _P, _I64, _P]),
     "tx_set_lookahead": (_I32, [_U64, _I32]),
     "tx_set_prefill": (_I32, [_U64, _I32, _I32]),
     "tx_set_prefill_backend": (_I32, [_U64, _I32]),

@@ -41,31 +41,34 @@ def sources() -> list[Path]:
     return sorted(CSRC.glob("*.hip"))
 
 
-def _compile(source: Path) -> Path:
-    obj = BUILD_DIR / (source.stem + ".o")
-    cmd = [hipcc(), *HIPCC_FLAGS, "-c", str(source), "-o", str(obj)]
+def _compile(source: Path, build_dir: Path, defines: tuple[str, ...]) -> Path:
+    obj = build_dir / (source.stem + ".o")
+    cmd = [hipcc(), *HIPCC_FLAGS, *(f"-D{d}" for d in defines), "-c", str(source), "-o", str(obj)]
     result = subprocess.run(cmd, capture_output=True, text=True)
     if result.returncode != 0:
         raise RuntimeError(f"hipcc failed for {source.name}:\n{result.stderr}")
     return obj
 
 
-def build(verbose: bool = False) -> Path:
-    """Compile every HIP source for gfx950 and link ``libtexelator_hip.so``."""
-    BUILD_DIR.mkdir(exist_ok=True)
+def build(verbose: bool = False, output: Path | None = None, defines: tuple[str, ...] = ()) -> Path:
+    """Compile every HIP source for gfx950 and link ``libtexelator_hip.so`` (or ``output``, with
+    extra preprocessor ``defines`` such as ``TX_PREFILL_LA=2``)."""
+    library = Path(output) if output is not None else LIBRARY
+    build_dir = BUILD_DIR if output is None else library.parent / (library.stem + "_build")
+    build_dir.mkdir(parents=True, exist_ok=True)
     srcs = sources()
     workers = min(len(srcs), max(1, (os.cpu_count() or 4)))
     with concurrent.futures.ThreadPoolExecutor(max_workers=workers) as pool:
-        objects = list(pool.map(_compile, srcs))
-    tmp = LIBRARY.with_suffix(".so.tmp")
+        objects = list(pool.map(lambda src: _compile(src, build_dir, tuple(defines)), srcs))
+    tmp = library.with_suffix(".so.tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objects), "-o", str(tmp)]
     result = subprocess.run(cmd, capture_output=True, text=True)
     if result.returncode != 0:
         raise RuntimeError(f"link failed:\n{result.stderr}")
-    tmp.replace(LIBRARY)
+    tmp.replace(library)
     if verbose:
-        print(f"[texelator_amd] built {LIBRARY}", flush=True)
-    return LIBRARY
+        print(f"[texelator_amd] built {library}", flush=True)
+    return library
 
 
 if __name__ == "__main__":

@@ -49,6 +49,7 @@ struct Handle {
   int lookahead = 2;
   int prefill_threshold = 16, prefill_tile_rows = 1024, prefill_backend = 0;
   int gemv_splits = 1;
+  int cus = 256;
   uint4 *tiles = nullptr;
   float *scales = nullptr;
   void *bias = nullptr;
@@ -112,10 +113,13 @@ void repack_rows(const uint8_t *blocks, const Handle &h, uint32_t *out, int g_be
 // K splits of the single-token GEMV. Tall matrices (>= 1024 row groups) fill the chip without
 // splitting; shorter ones split K so that there are about six workgroups per CU, each covering at
 // least 4 tile columns. A split never covers more tile columns than the LDS x slice holds.
-int choose_splits(int RG, int CG, int device) {
-  int cus = 256;
+int device_cus(int device) {
   hipDeviceProp_t prop;
-  if (hipGetDeviceProperties(&prop, device) == hipSuccess && prop.multiProcessorCount > 0) cus = prop.multiProcessorCount;
+  if (hipGetDeviceProperties(&prop, device) == hipSuccess && prop.multiProcessorCount > 0) return prop.multiProcessorCount;
+  return 256;
+}
+
+int choose_splits(int RG, int CG, int cus) {
   int ks = 1;
   if (RG < 1024) {
     ks = (6 * cus + RG - 1) / RG;
@@ -125,13 +129,20 @@ int choose_splits(int RG, int CG, int device) {
   return std::max(1, std::min(ks, CG));
 }
 
-int default_candidate(int tokens) {
+int default_candidate(int64_t tokens) {
   if (tokens <= 32) return 9;
-  if (tokens <= 128) return 6;
-  return 5;
+  if (tokens <= 64) return 8;
+  return 6;
 }
 
-int run_prefill(Handle *h, int candidate, const void *x, int64_t tokens, void *y, hipStream_t stream) {
+// Workspace bytes of a prefill call (split-K partials), 0 if none.
+int64_t prefill_workspace_bytes(const Handle *h, int64_t tokens) {
+  const int ks = tx::prefill_splits(h->M, h->CG, tokens, h->cus);
+  return ks > 1 ? (int64_t)ks * tokens * h->Mp * (int64_t)sizeof(float) : 0;
+}
+
+int run_prefill(Handle *h, int candidate, const void *x, int64_t tokens, void *y, void *workspace,
+                int64_t workspace_bytes, hipStream_t stream) {
   tx::PrefillParams p{};
   p.tiles = h->tiles;
   p.scales = h->scales;
@@ -144,10 +155,14 @@ int run_prefill(Handle *h, int candidate, const void *x, int64_t tokens, void *y
   p.RG = h->RG;
   p.CG = h->CG;
   p.tokens = (int)tokens;
-  const int bt_limit = 65535;
-  int bt = 0, bn = 0, bk = 0;
-  tx::prefill_candidate_shape(candidate, &bt, &bn, &bk);
-  if (bt <= 0 || (tokens + bt - 1) / bt > bt_limit) return fail(TX_ERR_INVALID, "token count exceeds the prefill grid limit");
+  p.ks = tx::prefill_splits(h->M, h->CG, tokens, h->cus);
+  if (tokens > (1 << 20)) return fail(TX_ERR_INVALID, "token count exceeds the prefill limit (1048576)");
+  const int64_t need = prefill_workspace_bytes(h, tokens);
+  if (need > 0) {
+    if (!workspace || workspace_bytes < need || reinterpret_cast<uintptr_t>(workspace) % 16 != 0)
+      return fail(TX_ERR_INVALID, "prefill workspace missing or too small (see tx_workspace_bytes)");
+    p.partials = static_cast<float *>(workspace);
+  }
   TX_HIP(tx::launch_prefill(p, candidate, stream));
   return TX_OK;
 }
@@ -199,7 +214,8 @@ int tx_pack_encoded(const uint8_t *blocks, int64_t blocks_bytes, const float *sc
   h->Mp = h->RG * tx::kTileRows;
   h->CG = (h->bpr + tx::kTileBlocks - 1) / tx::kTileBlocks;
   h->bp = h->CG * tx::kTileBlocks;
-  h->gemv_splits = choose_splits(h->RG, h->CG, device);
+  h->cus = device_cus(device);
+  h->gemv_splits = choose_splits(h->RG, h->CG, h->cus);
 
   const size_t tile_bytes = (size_t)h->RG * h->CG * tx::kTileBytes;
   std::vector<uint32_t> host(tile_bytes / 4);
@@ -244,7 +260,7 @@ int tx_pack_encoded(const uint8_t *blocks, int64_t blocks_bytes, const float *sc
 }
 
 int tx_linear(uint64_t value, const void *x, int x_dtype, int64_t x_numel, int64_t x_last, int device, void *y,
-              void *stream) {
+              void *workspace, int64_t workspace_bytes, void *stream) {
   g_last_error.clear();
   Handle *h = as_handle(value);
   if (!h) return fail(TX_ERR_INVALID, "null Texelator handle");
@@ -259,8 +275,8 @@ int tx_linear(uint64_t value, const void *x, int x_dtype, int64_t x_numel, int64
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (tokens >= h->prefill_threshold && tokens > 1) {
     if (h->bias && h->bias_dtype != TX_DTYPE_BF16) return fail(TX_ERR_INVALID, "BF16 prefill requires a BF16 bias");
-    const int candidate = h->prefill_backend >= tx::kPrefillFirst ? h->prefill_backend : default_candidate((int)tokens);
-    return run_prefill(h, candidate, x, tokens, y, s);
+    const int candidate = h->prefill_backend >= tx::kPrefillFirst ? h->prefill_backend : default_candidate(tokens);
+    return run_prefill(h, candidate, x, tokens, y, workspace, workspace_bytes, s);
   }
   if (h->bias && h->bias_dtype != x_dtype) return fail(TX_ERR_INVALID, "input and bias dtypes must match");
   return run_gemv(h, x, tokens, y, false, s);
@@ -277,7 +293,8 @@ int tx_linear_f32(uint64_t value, const void *x, int64_t tokens, float *y, void 
   return run_gemv(h, x, tokens, y, true, reinterpret_cast<hipStream_t>(stream));
 }
 
-int tx_prefill(uint64_t value, int candidate, const void *x, int64_t tokens, void *y, void *stream) {
+int tx_prefill(uint64_t value, int candidate, const void *x, int64_t tokens, void *y, void *workspace,
+               int64_t workspace_bytes, void *stream) {
   g_last_error.clear();
   Handle *h = as_handle(value);
   if (!h) return fail(TX_ERR_INVALID, "null Texelator handle");
@@ -287,7 +304,16 @@ int tx_prefill(uint64_t value, int candidate, const void *x, int64_t tokens, voi
   if (h->bias && h->bias_dtype != TX_DTYPE_BF16) return fail(TX_ERR_INVALID, "BF16 prefill requires a BF16 bias");
   if (tokens <= 0) return TX_OK;
   DeviceGuard guard(h->device);
-  return run_prefill(h, candidate, x, tokens, y, reinterpret_cast<hipStream_t>(stream));
+  return run_prefill(h, candidate, x, tokens, y, workspace, workspace_bytes, reinterpret_cast<hipStream_t>(stream));
+}
+
+int tx_workspace_bytes(uint64_t value, int64_t tokens, int64_t *bytes) {
+  g_last_error.clear();
+  Handle *h = as_handle(value);
+  if (!h) return fail(TX_ERR_INVALID, "null Texelator handle");
+  if (!bytes) return fail(TX_ERR_INVALID, "null output");
+  *bytes = tokens > 1 ? prefill_workspace_bytes(h, tokens) : 0;
+  return TX_OK;
 }
 
 int tx_set_lookahead(uint64_t value, int lookahead) {

@@ -28,7 +28,8 @@ struct PrefillParams {
   const void *x;           // [tokens][K] bf16
   const void *bias;        // [M] bf16 or nullptr
   void *y;                 // [tokens][M] bf16
-  int M, K, Mp, RG, CG, tokens;
+  float *partials;         // [ks][tokens][Mp] when ks > 1 (caller's workspace)
+  int M, K, Mp, RG, CG, tokens, ks;
 };
 
 // GEMV variants selected by the lookahead knob (number of 1 KiB tiles in flight per wave).
@@ -40,6 +41,8 @@ hipError_t gemv_kernel_attributes(int lookahead, hipFuncAttributes *attr);
 constexpr int kPrefillFirst = 5;
 constexpr int kPrefillLast = 9;
 bool prefill_candidate_eligible(int candidate, int M, int K);
+// K splits of the prefill GEMM for a shape (the same for every candidate).
+int prefill_splits(int M, int CG, int64_t tokens, int cus);
 hipError_t launch_prefill(const PrefillParams &p, int candidate, hipStream_t stream);
 hipError_t prefill_kernel_attributes(int candidate, hipFuncAttributes *attr, int *lds_bytes);
 const char *prefill_candidate_name(int candidate);

@@ -1,19 +1,26 @@
-// BF16 prefill GEMM over BC4 tiles (gfx950 MFMA).
+// BF16 prefill GEMM over BC4 tiles (gfx950 MFMA, weight-stationary).
 //
 // Reference: the CUTLASS MmaPipelined prefill whose operand-B iterator rebuilds BC4 weights
 // (texelator/cuda/cutlass_texture_mainloop.cu:58-188, launcher :203-249) computes
 // D[T x M] = X[T x K] * W^T with W = bf16(P*scale[row]), fp32 accumulation and a bf16 output;
-// the bias is added afterwards with a second bf16 rounding (:190-199). Its five tile shapes
-// (tokens x rows x K) 256x128x32, 128x128x32, 128x64x32, 64x128x32, 32x32x64 are backends 5..9.
+// the bias is added afterwards with a second bf16 rounding (:190-199). Its five tile shapes are
+// backends 5..9; here ids 5..9 name this build's own tile candidates.
 //
-// Here a workgroup (4 waves) owns a BT x BN output tile and walks K in steps of 128 columns
-// (one column of BC4 tiles):
-//   * the BT x 128 activation tile is copied to LDS;
-//   * the BN x 128 weight tile is decoded from BC4 straight into LDS as bf16 (no dense copy in
-//     global memory ever exists), each lane decoding two blocks with the register decoder;
-//   * each wave multiplies its (BT/WT) x (BN/WN) sub-tile with v_mfma_f32_16x16x32_bf16.
-// Every candidate accumulates each output in the same order (32-column MFMA steps from k = 0
-// upward into one fp32 accumulator), so all candidates give bitwise-identical results.
+// A workgroup (4 waves) owns BT = 16*MT tokens x BN = 64*NT output rows x one K range (split):
+//   * each wave owns NT 16-row groups; it streams their BC4 tiles (one 1 KiB tile per group and
+//     128-wide K step, LA steps ahead) and decodes them (palette seeds from LDS tables) straight
+//     into MFMA A operands in registers -- weights never pass through LDS, and no dense 16-bit
+//     copy exists anywhere;
+//   * the activations of a K step (BT x 128 bf16) are double-buffered in LDS and shared by the
+//     four waves; lane (token, kg) reads the 8 values matching the decoded weights' K chunk;
+//   * v_mfma_f32_16x16x32_bf16 with rows as M and tokens as N: acc[u][v] = D[rows][tokens].
+// Every candidate uses the same MFMA K grouping and order, and the K splits depend only on the
+// shape, so all candidates give bitwise-identical results. With several splits the partial sums
+// are written to the caller's workspace and reduced in split order by a second kernel.
+// Workgroups are mapped so that each XCD (workgroups arrive round-robin) works on few
+// (token tile, split) pairs: their activations stay in that XCD's L2.
+#include <algorithm>
+
 #include "bc4_device.h"
 #include "kernels.h"
 
@@ -22,7 +29,8 @@ namespace tx {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kStride = 136;  // LDS row stride in bf16 elements (128 + 8 padding)
+constexpr int kStride = 136;  // LDS row stride of the activation tile in bf16 (128 + 8 padding)
+constexpr int kXcds = 8;
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -31,24 +39,94 @@ __device__ __forceinline__ float bf16_bits_to_float(uint16_t v) {
   return __builtin_bit_cast(float, (uint32_t)v << 16);
 }
 
-template <int BT, int BN, int WT, int WN>
-__global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillParams p) {
-  static_assert(WT * WN == 4, "four waves per workgroup");
-  constexpr int TW = BT / WT;  // tokens per wave
-  constexpr int NW = BN / WN;  // rows per wave
-  constexpr int MT = TW / 16;
-  constexpr int NT = NW / 16;
-  static_assert(MT >= 1 && NT >= 1, "wave tile must cover at least one 16x16 MFMA tile");
-  __shared__ __attribute__((aligned(16))) uint16_t xs[BT * kStride];
-  __shared__ __attribute__((aligned(16))) uint16_t ws[BN * kStride];
+__device__ __forceinline__ bf16x8 as_bf16x8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+  u32x4 v = {a, b, c, d};
+  return __builtin_bit_cast(bf16x8, v);
+}
 
-  const int n0 = blockIdx.x * BN;
-  const int t0 = blockIdx.y * BT;
+struct WorkItem {
+  int t0, n0, c_begin, nc, split;
+};
+
+// Token-tile-major, then split, then row tile; contiguous ranges go to one XCD.
+__device__ __forceinline__ bool work_item(const PrefillParams &p, int BT, int BN, WorkItem &w) {
+  const int n_rows = (p.M + BN - 1) / BN;
+  const int n_tok = (p.tokens + BT - 1) / BT;
+  const int items = n_rows * n_tok * p.ks;
+  const int per_xcd = (items + kXcds - 1) / kXcds;
+  const int q = (int)(blockIdx.x % kXcds) * per_xcd + (int)(blockIdx.x / kXcds);
+  if (q >= items) return false;
+  const int row_tile = q % n_rows;
+  const int rest = q / n_rows;
+  w.split = rest % p.ks;
+  w.t0 = (rest / p.ks) * BT;
+  w.n0 = row_tile * BN;
+  w.c_begin = (int)((int64_t)w.split * p.CG / p.ks);
+  w.nc = (int)((int64_t)(w.split + 1) * p.CG / p.ks) - w.c_begin;
+  return true;
+}
+
+template <int MT, int NT, int LA>
+__global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillParams p) {
+  constexpr int BT = 16 * MT;
+  constexpr int BN = 64 * NT;
+  constexpr int R = LA + 1;
+  __shared__ __attribute__((aligned(16))) uint16_t xs[2][BT * kStride];
+  __shared__ PaletteTableStorage tables;
+
+  WorkItem w;
+  if (!work_item(p, BT, BN, w)) return;
+
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int wt = wave / WN;
-  const int wn = wave % WN;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int i = lane & 15;
+  const int kg = lane >> 4;
   const uint16_t *x = static_cast<const uint16_t *>(p.x);
+
+  // Row groups of this wave (clamped into the matrix; rows past M are computed, never stored).
+  const uint4 *gtiles[NT];
+  float scale[NT];
+  uint32_t pm[NT];
+#pragma unroll
+  for (int v = 0; v < NT; ++v) {
+    const int g = min(w.n0 / kTileRows + wave * NT + v, p.RG - 1);
+    gtiles[v] = p.tiles + ((size_t)g * p.CG + w.c_begin) * 64 + lane;
+    scale[v] = p.scales[g * kTileRows + i];
+    pm[v] = pm_scale_pair(scale[v]);
+  }
+
+  // Weight ring: slot s holds the NT tiles of one K step.
+  uint4 ring[R][NT];
+#pragma unroll
+  for (int u = 0; u < LA; ++u)
+#pragma unroll
+    for (int v = 0; v < NT; ++v) ring[u][v] = load_stream(gtiles[v] + (size_t)min(u, w.nc - 1) * 64);
+
+  // Activation staging: MT uint4 per thread per K step (16 uint4 per token row).
+  uint4 xr[MT];
+  auto load_x = [&](int j) {
+    const int c = w.c_begin + min(j, w.nc - 1);
+#pragma unroll
+    for (int v = 0; v < MT; ++v) {
+      const int idx = v * kThreads + threadIdx.x;
+      const int t = w.t0 + (idx >> 4);
+      const int k = c * kTileK + (idx & 15) * 8;
+      xr[v] = (t < p.tokens && k < p.K) ? *reinterpret_cast<const uint4 *>(x + (size_t)t * p.K + k)
+                                        : make_uint4(0, 0, 0, 0);
+    }
+  };
+  auto store_x = [&](int buf) {
+#pragma unroll
+    for (int v = 0; v < MT; ++v) {
+      const int idx = v * kThreads + threadIdx.x;
+      *reinterpret_cast<uint4 *>(&xs[buf][(idx >> 4) * kStride + (idx & 15) * 8]) = xr[v];
+    }
+  };
+  load_x(0);
+  store_x(0);
+  load_x(1);
+  build_palette_tables(tables, threadIdx.x, kThreads);
+  __syncthreads();
 
   f32x4 acc[MT][NT];
 #pragma unroll
@@ -56,93 +134,88 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillParams p) {
 #pragma unroll
     for (int b = 0; b < NT; ++b) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  const int i = lane & 15;
-  const int kg = lane >> 4;
-
-  for (int c = 0; c < p.CG; ++c) {
-    // Activation tile: BT rows x 128 columns, 16 bytes per thread per pass.
-    for (int idx = threadIdx.x; idx < BT * 16; idx += kThreads) {
-      const int r = idx >> 4;
-      const int q = idx & 15;
-      const int t = t0 + r;
-      const int k = c * kTileK + q * 8;
-      uint4 v = make_uint4(0, 0, 0, 0);
-      if (t < p.tokens) {
-        const uint16_t *src = x + (size_t)t * p.K + k;
-        if (k + 8 <= p.K) {
-          v = *reinterpret_cast<const uint4 *>(src);
-        } else {
-          uint16_t e[8];
+  auto step = [&](int j, int u) {
+    // Prefetch the weights LA steps ahead (clamped, so every step issues the same loads).
+    const int jn = min(j + LA, w.nc - 1);
 #pragma unroll
-          for (int u = 0; u < 8; ++u) e[u] = (k + u < p.K) ? src[u] : (uint16_t)0;
-          v.x = e[0] | ((uint32_t)e[1] << 16);
-          v.y = e[2] | ((uint32_t)e[3] << 16);
-          v.z = e[4] | ((uint32_t)e[5] << 16);
-          v.w = e[6] | ((uint32_t)e[7] << 16);
-        }
+    for (int v = 0; v < NT; ++v) ring[(u + LA) % R][v] = load_stream(gtiles[v] + (size_t)jn * 64);
+    // Decode this step's tiles into A operands: a[v][q] covers block 2kg + (q >> 1),
+    // positions 8*(q & 1) .. +7, i.e. K offset 32kg + 8q within the step.
+    bf16x8 a[NT][4];
+#pragma unroll
+    for (int v = 0; v < NT; ++v) {
+      uint32_t d[8];
+      decode_block_lds(ring[u][v].x, ring[u][v].y, scale[v], pm[v], tables, d);
+      a[v][0] = as_bf16x8(d[0], d[1], d[2], d[3]);
+      a[v][1] = as_bf16x8(d[4], d[5], d[6], d[7]);
+      decode_block_lds(ring[u][v].z, ring[u][v].w, scale[v], pm[v], tables, d);
+      a[v][2] = as_bf16x8(d[0], d[1], d[2], d[3]);
+      a[v][3] = as_bf16x8(d[4], d[5], d[6], d[7]);
+    }
+    const uint16_t *xb = xs[j & 1];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+#pragma unroll
+      for (int mu = 0; mu < MT; ++mu) {
+        const bf16x8 b = *reinterpret_cast<const bf16x8 *>(xb + (mu * 16 + i) * kStride + kg * 32 + q * 8);
+#pragma unroll
+        for (int v = 0; v < NT; ++v) acc[mu][v] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[v][q], b, acc[mu][v], 0, 0, 0);
       }
-      *reinterpret_cast<uint4 *>(xs + r * kStride + q * 8) = v;
     }
-    // Weight tile: BN/16 BC4 tiles, decoded by lanes of the four waves.
-    for (int d = wave; d < BN / kTileRows; d += 4) {
-      const int g = n0 / kTileRows + d;
-      uint32_t w0[8], w1[8];
-      if (g < p.RG) {
-        const uint4 cur = load_stream(p.tiles + ((size_t)g * p.CG + c) * 64 + lane);
-        const float scale = p.scales[g * kTileRows + i];
-        const uint32_t pm = pm_scale_pair(scale);
-        decode_block(cur.x, cur.y, scale, pm, w0);
-        decode_block(cur.z, cur.w, scale, pm, w1);
-      } else {
-#pragma unroll
-        for (int u = 0; u < 8; ++u) w0[u] = w1[u] = 0u;
-      }
-      uint4 *dst = reinterpret_cast<uint4 *>(ws + (d * kTileRows + i) * kStride + kg * 32);
-      dst[0] = make_uint4(w0[0], w0[1], w0[2], w0[3]);
-      dst[1] = make_uint4(w0[4], w0[5], w0[6], w0[7]);
-      dst[2] = make_uint4(w1[0], w1[1], w1[2], w1[3]);
-      dst[3] = make_uint4(w1[4], w1[5], w1[6], w1[7]);
-    }
+    // Stage the next step's activations into the other buffer (read two steps ago).
+    store_x((j + 1) & 1);
+    load_x(j + 2);
     __syncthreads();
+  };
 
+  int j0 = 0;
+  for (; j0 + R <= w.nc; j0 += R) {
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      bf16x8 a[MT], b[NT];
-#pragma unroll
-      for (int u = 0; u < MT; ++u)
-        a[u] = *reinterpret_cast<const bf16x8 *>(xs + (wt * TW + u * 16 + i) * kStride + kk * 32 + kg * 8);
-#pragma unroll
-      for (int u = 0; u < NT; ++u)
-        b[u] = *reinterpret_cast<const bf16x8 *>(ws + (wn * NW + u * 16 + i) * kStride + kk * 32 + kg * 8);
-#pragma unroll
-      for (int u = 0; u < MT; ++u)
-#pragma unroll
-        for (int v = 0; v < NT; ++v) acc[u][v] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[u], b[v], acc[u][v], 0, 0, 0);
-    }
-    __syncthreads();
+    for (int u = 0; u < R; ++u) step(j0 + u, u);
   }
+#pragma unroll
+  for (int u = 0; u < LA; ++u)
+    if (j0 + u < w.nc) step(j0 + u, u);
 
-  // acc[u][v][r] = D[token 4*kg + r][row i] of the 16x16 sub-tile (u, v).
-  __bf16 *y = static_cast<__bf16 *>(p.y);
+  // acc[mu][v][r] = D[row 4kg + r of group v][token mu*16 + i].
   const uint16_t *bias = static_cast<const uint16_t *>(p.bias);
 #pragma unroll
-  for (int v = 0; v < NT; ++v) {
-    const int n = n0 + wn * NW + v * 16 + i;
-    if (n >= p.M) continue;
-    const float bv = bias ? bf16_bits_to_float(bias[n]) : 0.f;
+  for (int mu = 0; mu < MT; ++mu) {
+    const int t = w.t0 + mu * 16 + i;
+    if (t >= p.tokens) continue;
 #pragma unroll
-    for (int u = 0; u < MT; ++u) {
+    for (int v = 0; v < NT; ++v) {
+      const int row0 = w.n0 + (wave * NT + v) * kTileRows + kg * 4;
+      if (p.ks > 1) {
+        float *dst = p.partials + ((size_t)w.split * p.tokens + t) * p.Mp + row0;
+        if (row0 < p.Mp) *reinterpret_cast<float4 *>(dst) = make_float4(acc[mu][v][0], acc[mu][v][1], acc[mu][v][2], acc[mu][v][3]);
+      } else {
+        __bf16 *y = static_cast<__bf16 *>(p.y) + (size_t)t * p.M;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int t = t0 + wt * TW + u * 16 + kg * 4 + r;
-        if (t < p.tokens) {
-          __bf16 out = (__bf16)acc[u][v][r];
-          if (bias) out = (__bf16)((float)out + bv);
-          y[(size_t)t * p.M + n] = out;
+        for (int r = 0; r < 4; ++r) {
+          const int n = row0 + r;
+          if (n < p.M) {
+            __bf16 out = (__bf16)acc[mu][v][r];
+            if (bias) out = (__bf16)((float)out + bf16_bits_to_float(bias[n]));
+            y[n] = out;
+          }
         }
       }
     }
   }
+}
+
+// y[t][m] = bf16(sum over splits in order of partials[s][t][m]), then the bias with a second
+// rounding (the reference's epilogue order).
+__global__ __launch_bounds__(256) void prefill_reduce_kernel(PrefillParams p) {
+  const int m = blockIdx.x * 256 + threadIdx.x;
+  const int t = blockIdx.y;
+  if (m >= p.M) return;
+  float total = 0.f;
+  for (int s = 0; s < p.ks; ++s) total += p.partials[((size_t)s * p.tokens + t) * p.Mp + m];
+  __bf16 out = (__bf16)total;
+  if (p.bias) out = (__bf16)((float)out + bf16_bits_to_float(static_cast<const uint16_t *>(p.bias)[m]));
+  static_cast<__bf16 *>(p.y)[(size_t)t * p.M + m] = out;
 }
 
 struct Candidate {
@@ -153,25 +226,35 @@ struct Candidate {
   int lds;
 };
 
-template <int BT, int BN, int WT, int WN>
+template <int MT, int NT, int LA>
 hipError_t launch_tile(const PrefillParams &p, hipStream_t stream) {
-  dim3 grid((p.M + BN - 1) / BN, (p.tokens + BT - 1) / BT);
-  hipLaunchKernelGGL((prefill_kernel<BT, BN, WT, WN>), grid, dim3(kThreads), 0, stream, p);
+  constexpr int BT = 16 * MT, BN = 64 * NT;
+  const int items = ((p.M + BN - 1) / BN) * ((p.tokens + BT - 1) / BT) * p.ks;
+  const int grid = ((items + kXcds - 1) / kXcds) * kXcds;
+  hipLaunchKernelGGL((prefill_kernel<MT, NT, LA>), dim3(grid), dim3(kThreads), 0, stream, p);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || p.ks == 1) return e;
+  hipLaunchKernelGGL(prefill_reduce_kernel, dim3((p.M + 255) / 256, p.tokens), dim3(256), 0, stream, p);
   return hipGetLastError();
 }
 
-#define TX_CANDIDATE(NAME, BT, BN, WT, WN)                                                              \
+#define TX_CANDIDATE(NAME, MT, NT, LA)                                                                  \
   Candidate {                                                                                          \
-    NAME, BT, BN, reinterpret_cast<const void *>(&prefill_kernel<BT, BN, WT, WN>),                     \
-        &launch_tile<BT, BN, WT, WN>, (BT + BN) * kStride * 2                                          \
+    NAME, 16 * (MT), 64 * (NT), reinterpret_cast<const void *>(&prefill_kernel<MT, NT, LA>),           \
+        &launch_tile<MT, NT, LA>, 2 * 16 * (MT) * kStride * 2                                          \
   }
 
+// Weight tiles in flight per wave, in K steps.
+#ifndef TX_PREFILL_LA
+#define TX_PREFILL_LA 2
+#endif
+
 const Candidate kCandidates[] = {
-    TX_CANDIDATE("large_256x128x128", 256, 128, 2, 2),
-    TX_CANDIDATE("medium_128x128x128", 128, 128, 2, 2),
-    TX_CANDIDATE("medium_128x64x128", 128, 64, 2, 2),
-    TX_CANDIDATE("medium_64x128x128", 64, 128, 2, 2),
-    TX_CANDIDATE("small_32x64x128", 32, 64, 2, 2),
+    TX_CANDIDATE("large_128x256x128", 8, 4, TX_PREFILL_LA),
+    TX_CANDIDATE("medium_128x128x128", 8, 2, TX_PREFILL_LA),
+    TX_CANDIDATE("medium_64x256x128", 4, 4, TX_PREFILL_LA),
+    TX_CANDIDATE("medium_64x128x128", 4, 2, TX_PREFILL_LA),
+    TX_CANDIDATE("small_32x128x128", 2, 2, TX_PREFILL_LA),
 };
 
 const Candidate *find(int candidate) {
@@ -180,6 +263,19 @@ const Candidate *find(int candidate) {
 }
 
 }  // namespace
+
+int prefill_splits(int M, int CG, int64_t tokens, int cus) {
+  // Candidate-independent so that every tile gives the same sums: about two workgroups of the
+  // largest tile per CU, each split at least 8 tile columns long, partials at most 32 MiB.
+  const int64_t items = ((M + 255) / 256) * ((tokens + 127) / 128);
+  const int64_t target = 2 * (int64_t)cus;
+  if (items >= target) return 1;
+  int64_t ks = (target + items - 1) / items;
+  ks = std::min<int64_t>(ks, std::max(1, CG / 8));
+  const int64_t cap = std::max<int64_t>(1, (int64_t(32) << 20) / (tokens * (int64_t)((M + 15) / 16 * 16) * 4));
+  ks = std::min(ks, cap);
+  return (int)std::max<int64_t>(1, ks);
+}
 
 bool prefill_candidate_eligible(int candidate, int M, int K) {
   return find(candidate) != nullptr && M > 0 && K > 0 && K % 16 == 0;
