@@ -1,0 +1,226 @@
+"""CPU tests of the host-side modules: artifact layout, naming, profile keys and gates, metrics.
+
+Modelled on the reference's CPU contract tests (tests/test_adapters.py, tests/test_runtime_layout.py,
+tests/test_store.py) and on the numeric gates its commands apply (autotune.py:63-85,
+tuning.py:66-81). Device queries are replaced by monkeypatched fakes; no GPU is used.
+"""
+from __future__ import annotations
+
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+from torch import nn
+
+from oracle import bc4
+from tests.helpers import lognormal_scales, random_blocks
+from texelator_amd import adapters, artifacts, autotune, hardware, runtime, tuning
+
+
+def _write_small_artifact(path: Path, shapes=((32, 64), (48, 128)), palette=None) -> Path:
+    matrices = []
+    for index, (m, k) in enumerate(shapes):
+        matrices.append((f"model.layers.{index}.mlp.up_proj", random_blocks(m, k, 100 + index),
+                         lognormal_scales(m, 200 + index)))
+    return artifacts.write_artifact(path, matrices, palette or hardware.PALETTE_SHA256)
+
+
+def test_palette_constant_matches_oracle():
+    assert hardware.PALETTE_SHA256 == bc4.palette_sha256()
+
+
+def test_artifact_layout_and_validation(tmp_path):
+    art = _write_small_artifact(tmp_path / "art")
+    manifest = artifacts.read_manifest(art)
+    assert manifest["format"] == "texelator-bc4-v1" and manifest["runtime_dtype"] == "bfloat16"
+    metadata = json.loads((art / "weights" / "metadata.json").read_text())
+    assert [e["M"] for e in metadata["entries"]] == [32, 48]
+    assert [e["K"] for e in metadata["entries"]] == [64, 128]
+    first = metadata["entries"][0]
+    assert (art / "weights" / first["blocks_file"]).stat().st_size == 32 * 64 // 2
+    assert (art / "weights" / first["scales_file"]).stat().st_size == 32 * 4
+    assert artifacts.validate_encoded(art / "weights")["ok"]
+    # a flipped byte is caught by the checksum gate (artifacts.py:76-87)
+    blob = bytearray((art / "weights" / first["blocks_file"]).read_bytes())
+    blob[3] ^= 1
+    (art / "weights" / first["blocks_file"]).write_bytes(bytes(blob))
+    report = artifacts.validate_encoded(art / "weights")
+    assert not report["ok"] and report["failures"][0]["module_name"] == first["module_name"]
+
+
+def test_missing_manifest_is_rejected(tmp_path):
+    with pytest.raises(RuntimeError, match="not a Texelator artifact"):
+        artifacts.read_manifest(tmp_path)
+
+
+def test_artifact_key_is_stable_safe_and_unique():
+    names = ["model.layers.0.self_attn.q_proj", "model.layers.0.self_attn.k_proj",
+             "model.layers.10.mlp.down_proj", "model.layers.1.mlp.down_proj", "weird name/with:chars"]
+    keys = [adapters.artifact_key(n) for n in names]
+    assert len(set(keys)) == len(keys)
+    assert keys == [adapters.artifact_key(n) for n in names]
+    for key in keys:
+        assert all(c.isalnum() or c in "_.-" for c in key)
+    assert keys[0].startswith("model__layers__0__self_attn__q_proj--") and len(keys[0].split("--")[-1]) == 10
+
+
+@pytest.mark.parametrize("name,layer", [("model.layers.7.mlp.up_proj", 7), ("transformer.h.3.attn", 3),
+                                        ("decoder.layers.12.fc1", 12), ("lm_head", None)])
+def test_layer_index(name, layer):
+    assert adapters.layer_index(name) == layer
+
+
+def test_resolve_top_level_module():
+    model = nn.Module()
+    model.lm_head = nn.Linear(4, 8, bias=False)
+    parent, child = adapters.resolve_parent(model, "lm_head")
+    assert parent is model and child == "lm_head"
+    with pytest.raises(RuntimeError, match="does not exist"):
+        adapters.resolve_parent(model, "missing")
+
+
+def test_texelator_linear_requires_handles():
+    with pytest.raises(ValueError, match="at least one"):
+        runtime.TexelatorLinear([])
+
+
+def test_decode_only_linear_routes_single_tokens():
+    calls = []
+
+    class Tag(nn.Module):
+        def __init__(self, tag):
+            super().__init__()
+            self.tag = tag
+
+        def forward(self, x):
+            calls.append(self.tag)
+            return x
+
+    module = runtime.DecodeOnlyLinear(Tag("dense"), Tag("bc4"))
+    module(torch.zeros(1, 1, 8))
+    module(torch.zeros(1, 3, 8))
+    assert calls == ["bc4", "dense"]
+
+
+def test_fp4_hybrid_cannot_be_enabled():
+    runtime.set_fp4_hybrid(False)
+    with pytest.raises(RuntimeError, match="no gfx950 counterpart"):
+        runtime.set_fp4_hybrid(True)
+
+
+@pytest.mark.parametrize("tokens,bucket", [(1, 32), (32, 32), (33, 128), (512, 512), (513, 2048), (65535, 65535)])
+def test_token_buckets(tokens, bucket):
+    assert autotune.token_bucket(tokens) == bucket
+    assert autotune.dispatch_key(tokens, 5120, 27648) == f"tokens<={bucket}:M=5120:K=27648"
+
+
+@pytest.mark.parametrize("tokens", [0, 65536])
+def test_token_bucket_limits(tokens):
+    with pytest.raises(ValueError):
+        autotune.token_bucket(tokens)
+
+
+def test_candidates_match_library_names():
+    from texelator_amd import _lib
+
+    lib = _lib.load()
+    assert list(autotune.CANDIDATES) == [lib.tx_candidate_name(i).decode() for i in range(5, 10)]
+    assert autotune.BASELINE in autotune.CANDIDATES
+
+
+def test_kernel_source_hash_tracks_sources(tmp_path, monkeypatch):
+    first = autotune.kernel_source_sha256()
+    assert first == autotune.kernel_source_sha256()
+    fake = tmp_path / "pkg"
+    (fake / "csrc").mkdir(parents=True)
+    for path in (runtime.PACKAGE_ROOT / "csrc").iterdir():
+        (fake / "csrc" / path.name).write_bytes(path.read_bytes())
+    monkeypatch.setattr(autotune, "PACKAGE_ROOT", fake)
+    assert autotune.kernel_source_sha256() == first
+    (fake / "csrc" / "gemv.hip").write_bytes((fake / "csrc" / "gemv.hip").read_bytes() + b"\n")
+    assert autotune.kernel_source_sha256() != first
+
+
+def test_error_metrics_match_oracle():
+    rng = np.random.default_rng(5)
+    ref = rng.standard_normal((7, 33)).astype(np.float32)
+    val = ref + 0.01 * rng.standard_normal(ref.shape).astype(np.float32)
+    got = autotune._error(torch.from_numpy(ref), torch.from_numpy(val))
+    want = bc4.error_metrics(ref, val)
+    for key in ("max_abs", "mean_abs", "relative_rms", "cosine"):
+        assert got[key] == pytest.approx(want[key], rel=1e-5)
+    assert got["bitwise_equal"] is False
+    assert autotune._error(torch.from_numpy(ref), torch.from_numpy(ref.copy()))["bitwise_equal"] is True
+    # closed form: a uniform relative scaling by (1+e) has rrms = e and cosine = 1
+    scaled = autotune._error(torch.ones(10), torch.full((10,), 1.25))
+    assert scaled["relative_rms"] == pytest.approx(0.25) and scaled["cosine"] == pytest.approx(1.0)
+
+
+def test_eligibility():
+    assert autotune._eligible("small_32x128x128", 17, 48) == (True, None)
+    assert autotune._eligible("small_32x128x128", 16, 40)[0] is False
+
+
+@pytest.fixture()
+def fake_device(monkeypatch):
+    class Props:
+        multi_processor_count = 256
+        total_memory = 288 << 30
+        name = "AMD Instinct MI355X"
+
+    monkeypatch.setattr(torch.cuda, "get_device_name", lambda *a, **k: "AMD Instinct MI355X")
+    monkeypatch.setattr(torch.cuda, "current_device", lambda: 0)
+    monkeypatch.setattr(torch.cuda, "get_device_properties", lambda *a, **k: Props())
+    monkeypatch.setattr(autotune, "device_key", lambda: "gfx950")
+    monkeypatch.setattr(tuning, "device_key", lambda: "gfx950")
+    return Props
+
+
+def test_profile_gate_rejects_foreign_profiles(fake_device):
+    good = {"kernel_source_sha256": autotune.kernel_source_sha256(),
+            "device": {"arch": "gfx950", "multiprocessor_count": 256}}
+    autotune.check_profile_device(good)
+    with pytest.raises(RuntimeError, match="kernel hash"):
+        autotune.check_profile_device({**good, "kernel_source_sha256": "0" * 64})
+    with pytest.raises(RuntimeError, match="architecture"):
+        autotune.check_profile_device({**good, "device": {"arch": "gfx942", "multiprocessor_count": 256}})
+    with pytest.raises(RuntimeError, match="CU count"):
+        autotune.check_profile_device({**good, "device": {"arch": "gfx950", "multiprocessor_count": 304}})
+
+
+def test_profile_paths_and_selected_profile_gates(tmp_path, fake_device, monkeypatch):
+    monkeypatch.setattr(autotune, "STATE_HOME", tmp_path / "state")
+    monkeypatch.setattr(tuning, "STATE_HOME", tmp_path / "state")
+    art = _write_small_artifact(tmp_path / "art")
+    assert autotune.selected_profile(art)[0] is None
+    assert tuning.selected_lookahead(art) == (1, None)
+    target = autotune.profile_path(art)
+    assert target.name == "gfx950-amd-instinct-mi355x-prefill.json"
+    metadata_sha = artifacts.sha256_file(art / "weights" / "metadata.json")
+    assert target.parent.name == metadata_sha[:20]
+    profile = {"metadata_sha256": metadata_sha, "kernel_source_sha256": autotune.kernel_source_sha256()}
+    target.parent.mkdir(parents=True)
+    target.write_text(json.dumps(profile))
+    assert autotune.selected_profile(art)[0] == profile
+    target.write_text(json.dumps({**profile, "metadata_sha256": "x"}))
+    with pytest.raises(RuntimeError, match="encoded weights"):
+        autotune.selected_profile(art)
+    # decode profile: the palette hash of the artifact must match
+    decode = tuning._profile_path(art)
+    decode.write_text(json.dumps({"weights_metadata_sha256": metadata_sha, "palette_sha256": "other",
+                                  "selected_lookahead": 4}))
+    with pytest.raises(RuntimeError, match="palette"):
+        tuning.selected_lookahead(art)
+    decode.write_text(json.dumps({"weights_metadata_sha256": metadata_sha,
+                                  "palette_sha256": hardware.PALETTE_SHA256, "selected_lookahead": 4}))
+    assert tuning.selected_lookahead(art) == (4, decode)
+
+
+def test_runtime_dtype_gate():
+    assert tuning._runtime_dtype({"runtime_dtype": "bfloat16"}) is torch.bfloat16
+    with pytest.raises(RuntimeError, match="FP16"):
+        tuning._runtime_dtype({})
+    with pytest.raises(RuntimeError, match="unsupported"):
+        tuning._runtime_dtype({"runtime_dtype": "float32"})

@@ -80,3 +80,82 @@ def validate_encoded(encoded: Path) -> dict:
                 failures.append({"module_name": entry["module_name"], "file": str(path),
                                  "expected": expected, "actual": actual})
     return {"ok": not failures, "entries": len(metadata["entries"]), "failures": failures}
+
+
+MANIFEST = "texelator.json"
+ARTIFACT_FORMAT = "texelator-bc4-v1"
+WEIGHTS_FORMAT = "BC4_SNORM + one FP32 scale per output row"
+
+
+def read_manifest(artifact: Path) -> dict:
+    """The artifact's ``texelator.json`` (``converter.py:216-230``)."""
+    path = Path(artifact) / MANIFEST
+    if not path.is_file():
+        raise RuntimeError(f"not a Texelator artifact (missing {MANIFEST}): {artifact}")
+    return json.loads(path.read_text())
+
+
+def weights_dir(artifact: Path) -> Path:
+    return Path(artifact) / read_manifest(artifact).get("weights", "weights")
+
+
+def write_artifact(destination: Path, matrices, palette_sha256: str, runtime_dtype: str = "bfloat16",
+                   name: str | None = None, extra: dict | None = None) -> Path:
+    """Write an encoded artifact in the reference's on-disk layout.
+
+    ``matrices`` yields ``(module_name, blocks, scales)`` with ``blocks`` uint8 ``[M, K/16*8]``
+    and ``scales`` float32 ``[M]``. Files: ``weights/<key>.bc4``, ``weights/<key>.scales.f32``,
+    ``weights/metadata.json`` with per-entry sha256 (``converter.py:172-215``),
+    ``validation.json`` and ``texelator.json`` (``converter.py:216-230``).
+    """
+    import numpy as np
+
+    from .adapters import artifact_key, layer_index
+
+    destination = Path(destination)
+    weights = destination / "weights"
+    weights.mkdir(parents=True, exist_ok=True)
+    entries = []
+    for module_name, blocks, scales in matrices:
+        blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+        scales = np.ascontiguousarray(scales, dtype="<f4")
+        m = int(scales.shape[0])
+        blocks = blocks.reshape(m, -1)
+        k = blocks.shape[1] // 8 * 16
+        key = artifact_key(module_name)
+        blocks_path = weights / f"{key}.bc4"
+        scales_path = weights / f"{key}.scales.f32"
+        blocks_path.write_bytes(blocks.tobytes())
+        scales_path.write_bytes(scales.tobytes())
+        entries.append({
+            "module_name": module_name, "artifact_key": key, "layer": layer_index(module_name),
+            "op": module_name.rsplit(".", 1)[-1], "M": m, "K": k, "bias": False, "supported": True,
+            "reason": "ok",
+            "blocks_file": blocks_path.name, "blocks_bytes": blocks_path.stat().st_size,
+            "blocks_sha256": sha256_file(blocks_path),
+            "scales_file": scales_path.name, "scales_bytes": scales_path.stat().st_size,
+            "scales_sha256": sha256_file(scales_path),
+        })
+    write_json(weights / "metadata.json", {
+        "schema_version": 1,
+        "format": WEIGHTS_FORMAT,
+        "palette_sha256": palette_sha256,
+        "entries": entries,
+        "bc4_bytes": sum(entry["blocks_bytes"] for entry in entries),
+        "scale_bytes": sum(entry["scales_bytes"] for entry in entries),
+    })
+    validation = validate_encoded(weights)
+    write_json(destination / "validation.json", validation)
+    manifest = {
+        "schema_version": 1,
+        "format": ARTIFACT_FORMAT,
+        "name": name or destination.name,
+        "runtime_dtype": runtime_dtype,
+        "hardware": {"palette_sha256": palette_sha256},
+        "weights": "weights",
+        "validation": "validation.json",
+        "linked_source": False,
+    }
+    manifest.update(extra or {})
+    write_json(destination / MANIFEST, manifest)
+    return destination

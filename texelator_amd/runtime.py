@@ -97,6 +97,12 @@ def pack_entry(weights: Path, entry: dict, bias: torch.Tensor | None = None, loo
     return handle
 
 
+def _host_copy(array: np.ndarray) -> np.ndarray:
+    """A contiguous, writable host array (read-only memory maps are copied)."""
+    array = np.ascontiguousarray(array)
+    return array if array.flags.writeable else array.copy()
+
+
 def pack_arrays(blocks: np.ndarray, scales: np.ndarray, bias: torch.Tensor | None = None,
                 lookahead: int = 1, max_rows: int = 32768) -> list[int]:
     """Pack an in-memory matrix (``[M, K/16*8]`` uint8 blocks, ``[M]`` float32 scales),
@@ -112,8 +118,8 @@ def pack_arrays(blocks: np.ndarray, scales: np.ndarray, bias: torch.Tensor | Non
         for start in range(0, m, max_rows):
             stop = min(start + max_rows, m)
             handle = extension().pack_encoded(
-                torch.from_numpy(np.ascontiguousarray(blocks[start:stop]).reshape(-1)),
-                torch.from_numpy(np.ascontiguousarray(scales[start:stop])),
+                torch.from_numpy(_host_copy(blocks[start:stop]).reshape(-1)),
+                torch.from_numpy(_host_copy(scales[start:stop])),
                 bias[start:stop] if bias is not None else None)
             extension().set_lookahead(handle, lookahead)
             extension().set_prefill(handle, PREFILL_THRESHOLD, PREFILL_TILE_ROWS)
