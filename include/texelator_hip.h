@@ -40,6 +40,12 @@ const char *tx_last_error(void);
 int tx_pack_encoded(const uint8_t *blocks, int64_t blocks_bytes, const float *scales, int64_t rows,
                     const void *bias, int bias_dtype, int device, uint64_t *handle_out);
 
+/* Same as tx_pack_encoded, but blocks (8-byte aligned) and scales are device pointers on
+ * `device`; the tile repack runs on the GPU. The reference only accepts CPU inputs
+ * (texelator_cuda.cu:1262-1268); this variant serves weights encoded on the GPU. Synchronous. */
+int tx_pack_encoded_device(const uint8_t *blocks, int64_t blocks_bytes, const float *scales, int64_t rows,
+                           const void *bias, int bias_dtype, int device, uint64_t *handle_out);
+
 /* y = x W^T (+ bias). Replaces texelator_linear (texelator_cuda.cu:1329-1469; extension.cpp:30).
  *   x         device, contiguous, 16-byte aligned [tokens][K] of x_dtype (BF16; F16 is reported
  *             unsupported)

@@ -52,6 +52,26 @@ def test_decode_dense_bit_exact(ext, oracle_threads, m, k, seed):
     assert mismatches == 0, f"{mismatches} of {want.size} decoded weights differ"
 
 
+@pytest.mark.parametrize("m,k,seed", [(16, 128, 91), (37, 272, 92), (300, 2064, 93)])
+def test_device_pack_equals_host_pack(ext, oracle_threads, m, k, seed):
+    """tx_pack_encoded_device (repack kernel) builds the same tiles as the host repack."""
+    blocks = random_blocks(m, k, seed)
+    scales = lognormal_scales(m, seed + 1)
+    host = _pack(ext, blocks, scales)
+    dev = ext.pack_encoded_device(torch.from_numpy(blocks.reshape(-1)).cuda(), torch.from_numpy(scales).cuda())
+    x = bf16_vector((3, k), seed + 2).cuda()
+    try:
+        assert ext.handle_info(dev)[:2] == [m, k]
+        assert torch.equal(ext.decode_dense(host), ext.decode_dense(dev))
+        assert torch.equal(ext.linear_f32(host, x[:1]), ext.linear_f32(dev, x[:1]))
+        assert torch.equal(ext.linear(host, x), ext.linear(dev, x))
+        got = bf16_bits(ext.decode_dense(dev).cpu())
+    finally:
+        ext.free(host)
+        ext.free(dev)
+    assert np.array_equal(got, clib.decode_bf16_bits(blocks, scales))
+
+
 @pytest.mark.parametrize("m,k,tokens,seed", [(16, 128, 1, 11), (37, 272, 1, 12), (1024, 5120, 1, 13),
                                              (300, 1040, 3, 14), (4096, 4096, 1, 15), (8, 27648, 1, 16)])
 def test_gemv_f32_within_tolerance(ext, oracle_threads, m, k, tokens, seed):

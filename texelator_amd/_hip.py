@@ -93,6 +93,31 @@ def pack_encoded(blocks: torch.Tensor, scales: torch.Tensor, bias: torch.Tensor 
     return handle
 
 
+def pack_encoded_device(blocks: torch.Tensor, scales: torch.Tensor, bias: torch.Tensor | None = None) -> int:
+    """``pack_encoded`` from device tensors (``tx_pack_encoded_device``): blocks CUDA uint8
+    ``[M * K/16 * 8]``, scales CUDA float32 ``[M]``, on the same device."""
+    _require(blocks.is_cuda and blocks.dtype == torch.uint8 and blocks.is_contiguous(),
+             "blocks must be contiguous CUDA uint8")
+    _require(scales.is_cuda and scales.dtype == torch.float32 and scales.is_contiguous(),
+             "scales must be contiguous CUDA float32")
+    _require(blocks.device == scales.device, "blocks and scales must be on one device")
+    rows = scales.numel()
+    _require(rows > 0 and blocks.numel() % (rows * 8) == 0, "invalid encoded size")
+    bias_ptr, bias_code = None, -1
+    if bias is not None and bias.numel():
+        bias = bias.detach().contiguous()
+        _require(bias.is_cuda and bias.dtype in _DTYPE_CODE and bias.numel() == rows and bias.device == blocks.device,
+                 "bias must be CUDA FP16 or BF16 [M]")
+        bias_ptr, bias_code = ctypes.c_void_p(bias.data_ptr()), _DTYPE_CODE[bias.dtype]
+    out = ctypes.c_uint64(0)
+    check(_lib.load().tx_pack_encoded_device(ctypes.c_void_p(blocks.data_ptr()), blocks.numel(),
+                                             ctypes.c_void_p(scales.data_ptr()), rows, bias_ptr, bias_code,
+                                             blocks.device.index, ctypes.byref(out)))
+    handle = int(out.value)
+    _SHAPES[handle] = (rows, blocks.numel() // rows // 8 * 16)
+    return handle
+
+
 def linear(handle: int, x: torch.Tensor) -> torch.Tensor:
     """``y = x W^T (+ bias)`` (``texelator_cuda.cu:1329-1469``); output dtype = input dtype."""
     _require(bool(handle), "null Texelator handle")

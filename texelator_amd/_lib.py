@@ -31,6 +31,7 @@ _U64 = ctypes.c_uint64
 SIGNATURES = {
     "tx_last_error": (ctypes.c_char_p, []),
     "tx_pack_encoded": (_I32, [_P, _I64, _P, _I64, _P, _I32, _I32, ctypes.POINTER(_U64)]),
+    "tx_pack_encoded_device": (_I32, [_P, _I64, _P, _I64, _P, _I32, _I32, ctypes.POINTER(_U64)]),
     "tx_linear": (_I32, [_U64, _P, _I32, _I64, _I64, _I32, _P, _P, _I64, _P]),
     "tx_workspace_bytes": (_I32, [_U64, _I64, ctypes.POINTER(_I64)]),
     "tx_linear_f32": (_I32, [_U64, _P, _I64, _P, _P]),

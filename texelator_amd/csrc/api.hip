@@ -72,26 +72,6 @@ Handle *as_handle(uint64_t value) {
   return h;
 }
 
-// One reference block (8 bytes) -> device words A, B (layout in bc4_device.h).
-inline void encode_block(const uint8_t *blk, uint32_t &a, uint32_t &b) {
-  int e0 = (int)(int8_t)blk[0];
-  int e1 = (int)(int8_t)blk[1];
-  e0 = e0 < -127 ? -127 : e0;
-  e1 = e1 < -127 ? -127 : e1;
-  const uint32_t eb0 = (uint32_t)(e0 + 127);
-  const uint32_t eb1 = (uint32_t)(e1 + 127);
-  uint64_t bits = 0;
-  for (int i = 0; i < 6; ++i) bits |= (uint64_t)blk[2 + i] << (8 * i);
-  uint32_t s[16];
-  for (int p = 0; p < 16; ++p) s[p] = (uint32_t)((bits >> (3 * p)) & 7u);
-  a = 0;
-  b = 0;
-  for (int c = 0; c < 4; ++c) {
-    a |= (s[c] | (s[4 + c] << 3) | (((eb0 >> (2 * c)) & 3u) << 6)) << (8 * c);
-    b |= (s[8 + c] | (s[12 + c] << 3) | (((eb1 >> (2 * c)) & 3u) << 6)) << (8 * c);
-  }
-}
-
 void repack_rows(const uint8_t *blocks, const Handle &h, uint32_t *out, int g_begin, int g_end) {
   for (int g = g_begin; g < g_end; ++g) {
     for (int c = 0; c < h.CG; ++c) {
@@ -101,7 +81,7 @@ void repack_rows(const uint8_t *blocks, const Handle &h, uint32_t *out, int g_be
         for (int half = 0; half < 2; ++half) {
           const int blk = c * tx::kTileBlocks + 2 * (lane >> 4) + half;
           uint32_t a = tx::kZeroBlockWord, b = tx::kZeroBlockWord;
-          if (m < h.M && blk < h.bpr) encode_block(blocks + ((size_t)m * h.bpr + blk) * 8, a, b);
+          if (m < h.M && blk < h.bpr) tx::encode_device_block(blocks + ((size_t)m * h.bpr + blk) * 8, a, b);
           tile[lane * 4 + half * 2] = a;
           tile[lane * 4 + half * 2 + 1] = b;
         }
@@ -188,14 +168,9 @@ int run_gemv(Handle *h, const void *x, int64_t tokens, void *y, bool f32_out, hi
   return TX_OK;
 }
 
-}  // namespace
-
-extern "C" {
-
-const char *tx_last_error(void) { return g_last_error.c_str(); }
-
-int tx_pack_encoded(const uint8_t *blocks, int64_t blocks_bytes, const float *scales, int64_t rows, const void *bias,
-                    int bias_dtype, int device, uint64_t *handle_out) {
+// Shared by tx_pack_encoded (host blocks and scales) and tx_pack_encoded_device (device ones).
+int pack_common(const uint8_t *blocks, int64_t blocks_bytes, const float *scales, int64_t rows, const void *bias,
+                int bias_dtype, int device, bool on_device, uint64_t *handle_out) {
   g_last_error.clear();
   if (!blocks || !scales || !handle_out) return fail(TX_ERR_INVALID, "blocks, scales and handle_out must be non-null");
   if (rows <= 0 || blocks_bytes <= 0 || blocks_bytes % (rows * 8) != 0) return fail(TX_ERR_INVALID, "invalid encoded size");
@@ -203,6 +178,7 @@ int tx_pack_encoded(const uint8_t *blocks, int64_t blocks_bytes, const float *sc
   if (rows > (1 << 30) || bpr * 16 > (1 << 30)) return fail(TX_ERR_INVALID, "matrix too large");
   if (bias && bias_dtype != TX_DTYPE_F16 && bias_dtype != TX_DTYPE_BF16)
     return fail(TX_ERR_INVALID, "bias must be CUDA FP16 or BF16 [M]");
+  if (on_device && reinterpret_cast<uintptr_t>(blocks) % 8 != 0) return fail(TX_ERR_INVALID, "device blocks must be 8-byte aligned");
   DeviceGuard guard(device);
   Handle *h = new (std::nothrow) Handle;
   if (!h) return fail(TX_ERR_HIP, "host allocation failed");
@@ -216,47 +192,64 @@ int tx_pack_encoded(const uint8_t *blocks, int64_t blocks_bytes, const float *sc
   h->bp = h->CG * tx::kTileBlocks;
   h->cus = device_cus(device);
   h->gemv_splits = choose_splits(h->RG, h->CG, h->cus);
-
   const size_t tile_bytes = (size_t)h->RG * h->CG * tx::kTileBytes;
-  std::vector<uint32_t> host(tile_bytes / 4);
-  const int workers = (int)std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
-  const int per = (h->RG + workers - 1) / workers;
-  std::vector<std::thread> threads;
-  for (int w = 0; w < workers; ++w) {
-    const int gb = w * per, ge = std::min(h->RG, gb + per);
-    if (gb >= ge) break;
-    threads.emplace_back(repack_rows, blocks, std::cref(*h), host.data(), gb, ge);
-  }
-  for (auto &t : threads) t.join();
 
-  std::vector<float> padded_scales(h->Mp, 0.0f);
-  std::memcpy(padded_scales.data(), scales, (size_t)h->M * sizeof(float));
-
-  auto cleanup = [&](int code) {
+  auto cleanup = [&](hipError_t e) {
     delete h;
-    return code;
+    return fail(TX_ERR_HIP, std::string("HIP: ") + hipGetErrorString(e));
   };
   hipError_t e;
-  if ((e = hipMalloc(&h->tiles, tile_bytes)) != hipSuccess) return cleanup(fail(TX_ERR_HIP, std::string("HIP: ") + hipGetErrorString(e)));
-  if ((e = hipMemcpy(h->tiles, host.data(), tile_bytes, hipMemcpyHostToDevice)) != hipSuccess)
-    return cleanup(fail(TX_ERR_HIP, std::string("HIP: ") + hipGetErrorString(e)));
-  if ((e = hipMalloc(&h->scales, (size_t)h->Mp * sizeof(float))) != hipSuccess)
-    return cleanup(fail(TX_ERR_HIP, std::string("HIP: ") + hipGetErrorString(e)));
-  if ((e = hipMemcpy(h->scales, padded_scales.data(), (size_t)h->Mp * sizeof(float), hipMemcpyHostToDevice)) != hipSuccess)
-    return cleanup(fail(TX_ERR_HIP, std::string("HIP: ") + hipGetErrorString(e)));
+  if ((e = hipMalloc(&h->tiles, tile_bytes)) != hipSuccess) return cleanup(e);
+  if ((e = hipMalloc(&h->scales, (size_t)h->Mp * sizeof(float))) != hipSuccess) return cleanup(e);
+  if (on_device) {
+    if ((e = tx::launch_repack(blocks, h->M, h->bpr, h->RG, h->CG, h->tiles, nullptr)) != hipSuccess) return cleanup(e);
+    if ((e = hipMemset(h->scales, 0, (size_t)h->Mp * sizeof(float))) != hipSuccess) return cleanup(e);
+    if ((e = hipMemcpy(h->scales, scales, (size_t)h->M * sizeof(float), hipMemcpyDeviceToDevice)) != hipSuccess)
+      return cleanup(e);
+  } else {
+    std::vector<uint32_t> host(tile_bytes / 4);
+    const int workers = (int)std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
+    const int per = (h->RG + workers - 1) / workers;
+    std::vector<std::thread> threads;
+    for (int w = 0; w < workers; ++w) {
+      const int gb = w * per, ge = std::min(h->RG, gb + per);
+      if (gb >= ge) break;
+      threads.emplace_back(repack_rows, blocks, std::cref(*h), host.data(), gb, ge);
+    }
+    for (auto &t : threads) t.join();
+    std::vector<float> padded_scales(h->Mp, 0.0f);
+    std::memcpy(padded_scales.data(), scales, (size_t)h->M * sizeof(float));
+    if ((e = hipMemcpy(h->tiles, host.data(), tile_bytes, hipMemcpyHostToDevice)) != hipSuccess) return cleanup(e);
+    if ((e = hipMemcpy(h->scales, padded_scales.data(), (size_t)h->Mp * sizeof(float), hipMemcpyHostToDevice)) != hipSuccess)
+      return cleanup(e);
+  }
   if (bias) {
-    if ((e = hipMalloc(&h->bias, (size_t)h->M * 2)) != hipSuccess) return cleanup(fail(TX_ERR_HIP, std::string("HIP: ") + hipGetErrorString(e)));
-    if ((e = hipMemcpy(h->bias, bias, (size_t)h->M * 2, hipMemcpyDeviceToDevice)) != hipSuccess)
-      return cleanup(fail(TX_ERR_HIP, std::string("HIP: ") + hipGetErrorString(e)));
+    if ((e = hipMalloc(&h->bias, (size_t)h->M * 2)) != hipSuccess) return cleanup(e);
+    if ((e = hipMemcpy(h->bias, bias, (size_t)h->M * 2, hipMemcpyDeviceToDevice)) != hipSuccess) return cleanup(e);
     h->bias_dtype = bias_dtype;
   }
   if (h->gemv_splits > 1) {
-    if ((e = hipMalloc(&h->partials, (size_t)h->gemv_splits * h->Mp * sizeof(float))) != hipSuccess)
-      return cleanup(fail(TX_ERR_HIP, std::string("HIP: ") + hipGetErrorString(e)));
+    if ((e = hipMalloc(&h->partials, (size_t)h->gemv_splits * h->Mp * sizeof(float))) != hipSuccess) return cleanup(e);
   }
-  if ((e = hipDeviceSynchronize()) != hipSuccess) return cleanup(fail(TX_ERR_HIP, std::string("HIP: ") + hipGetErrorString(e)));
+  if ((e = hipDeviceSynchronize()) != hipSuccess) return cleanup(e);
   *handle_out = reinterpret_cast<uint64_t>(h);
   return TX_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *tx_last_error(void) { return g_last_error.c_str(); }
+
+int tx_pack_encoded(const uint8_t *blocks, int64_t blocks_bytes, const float *scales, int64_t rows, const void *bias,
+                    int bias_dtype, int device, uint64_t *handle_out) {
+  return pack_common(blocks, blocks_bytes, scales, rows, bias, bias_dtype, device, false, handle_out);
+}
+
+int tx_pack_encoded_device(const uint8_t *blocks, int64_t blocks_bytes, const float *scales, int64_t rows,
+                           const void *bias, int bias_dtype, int device, uint64_t *handle_out) {
+  return pack_common(blocks, blocks_bytes, scales, rows, bias, bias_dtype, device, true, handle_out);
 }
 
 int tx_linear(uint64_t value, const void *x, int x_dtype, int64_t x_numel, int64_t x_last, int device, void *y,

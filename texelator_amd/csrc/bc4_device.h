@@ -55,6 +55,30 @@ constexpr float kR635Lo = kInv635Lo / 64.0f;
 // Device block whose endpoints are 0/0 and selectors 0: decodes to zero weights (padding).
 constexpr uint32_t kZeroBlockWord = 0x40C0C0C0u;
 
+// One reference block (8 bytes: e0, e1, 48-bit little-endian selector field) -> device words
+// A, B (layout above). Endpoint byte -128 is clamped to -127 as the decoder does. Used by the
+// host repack and by the device repack kernel, so both produce identical tiles.
+__host__ __device__ inline void encode_device_block(const uint8_t *blk, uint32_t &a, uint32_t &b) {
+  int e0 = (int)(int8_t)blk[0];
+  int e1 = (int)(int8_t)blk[1];
+  e0 = e0 < -127 ? -127 : e0;
+  e1 = e1 < -127 ? -127 : e1;
+  const uint32_t eb0 = (uint32_t)(e0 + 127);
+  const uint32_t eb1 = (uint32_t)(e1 + 127);
+  uint64_t bits = 0;
+  for (int i = 0; i < 6; ++i) bits |= (uint64_t)blk[2 + i] << (8 * i);
+  a = 0;
+  b = 0;
+  for (int c = 0; c < 4; ++c) {
+    const uint32_t s0 = (uint32_t)(bits >> (3 * c)) & 7u;
+    const uint32_t s1 = (uint32_t)(bits >> (3 * (4 + c))) & 7u;
+    const uint32_t s2 = (uint32_t)(bits >> (3 * (8 + c))) & 7u;
+    const uint32_t s3 = (uint32_t)(bits >> (3 * (12 + c))) & 7u;
+    a |= (s0 | (s1 << 3) | (((eb0 >> (2 * c)) & 3u) << 6)) << (8 * c);
+    b |= (s2 | (s3 << 3) | (((eb1 >> (2 * c)) & 3u) << 6)) << (8 * c);
+  }
+}
+
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 

@@ -49,6 +49,8 @@ const char *prefill_candidate_name(int candidate);
 void prefill_candidate_shape(int candidate, int *tokens, int *rows, int *k);
 
 hipError_t launch_palette_probe(float *out, hipStream_t stream);
+// Reference-layout device blocks [M][bpr][8] -> device tiles (RG x CG tiles of 1 KiB).
+hipError_t launch_repack(const uint8_t *blocks, int M, int bpr, int RG, int CG, uint4 *tiles, hipStream_t stream);
 hipError_t launch_decode_dense(const uint4 *tiles, const float *scales, int M, int K, int RG, int CG,
                                uint16_t *out, hipStream_t stream);
 
