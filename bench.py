@@ -180,6 +180,43 @@ def kernel_only(torch, ext, runtime, hardware, device, args) -> int:
     return 0
 
 
+def model_section(torch, args) -> dict:
+    """Prefill tok/s at ``--prompt`` tokens (reference protocol, texelator/prefill.py:63-131) and
+    graph-replayed greedy decode tok/s from the prompt up to ``--context``, on a random-init BC4
+    decoder of BASELINE config 5 (or 4)."""
+    from texelator_amd import modeling, prefill
+
+    config = modeling.DecoderConfig.class_27b() if args.model == "27b" else modeling.DecoderConfig.qwen25_3b_style()
+    model = modeling.BC4Decoder(config, max_context=args.context, seed=SEED)
+    try:
+        try:
+            pre = prefill.benchmark_prefill(model, tokens=args.prompt, warmup=2, runs=5)
+        except RuntimeError as error:        # gate failed: still time it, and say so
+            log(str(error))
+            pre = prefill.benchmark_prefill(model, tokens=args.prompt, warmup=2, runs=5, rrms_limit=None)
+            pre["correctness"]["gate_failed"] = True
+        dec = prefill.benchmark_decode(model, prompt_tokens=args.prompt, context=args.context,
+                                       sample_steps=args.decode_sample or None)
+    finally:
+        model.close()
+    bytes_per_token = config.bc4_bytes() + 2 * config.vocab * config.hidden
+    return {
+        "config": args.model, "layers": config.layers, "hidden": config.hidden, "bc4_bytes": config.bc4_bytes(),
+        "prefill_tokens": args.prompt,
+        "prefill_tok_s": round(pre["fused_bc4_mfma"]["gpu_tokens_per_second"], 1),
+        "prefill_ms": round(pre["fused_bc4_mfma"]["gpu_seconds_median"] * 1e3, 2),
+        "prefill_gemv_only_tok_s": round(pre["scalar_gemv"]["gpu_tokens_per_second"], 1),
+        "prefill_correctness": pre["correctness"],
+        "decode_context": [args.prompt, args.context],
+        "decode_tok_s": round(dec["gpu_tokens_per_second"], 2),
+        "decode_ms_per_token": round(dec["ms_per_token"], 3),
+        "decode_projected_from_samples": dec["projected"],
+        "decode_per_bucket_tok_s": {k: round(v["tokens_per_second"], 2) for k, v in dec["per_bucket"].items()},
+        "decode_weight_bytes_per_token": bytes_per_token,
+        "data": "random-init weights (BC4 blocks uniform, GPT-2 depth-scaled init), random prompt",
+    }
+
+
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     parser.add_argument("--gpus", type=int, default=1)
@@ -191,6 +228,12 @@ def main() -> int:
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     parser.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a graph")
     parser.add_argument("--no-prefill", action="store_true", help="skip the prefill GEMM measurements")
+    parser.add_argument("--model", choices=("27b", "3b", "none"), default="27b",
+                        help="model-level decode/prefill tok/s on a random-init BASELINE config 5 (27b) or 4 (3b)")
+    parser.add_argument("--context", type=int, default=4096, help="decode up to this context")
+    parser.add_argument("--prompt", type=int, default=512, help="prefill tokens")
+    parser.add_argument("--decode-sample", type=int, default=64,
+                        help="decode steps timed per 512-position bucket (0 = every step)")
     parser.add_argument("--kernel-only", action="store_true",
                         help="profiling mode: only the gate/up GEMV over the layer copies, then a plain copy of "
                              "COPY_BYTES bytes that calibrates the HBM byte counters")
@@ -340,13 +383,18 @@ def main() -> int:
         log("prefill GEMM")
         with torch.cuda.stream(stream):
             result["prefill"] = prefill_section(torch, ext, stream, handles)
+    del graph
+    runtime.free([h for _, _, _, h in handles])
+    handles = []
+    if args.model != "none":
+        log(f"model-level tok/s ({args.model})")
+        result["model"] = model_section(torch, args)
     if not args.no_cpu:
         log("cpu baseline")
         result["cpu_baseline"] = cpu_baseline(weights, args.cpu_seconds)
     else:
         result["cpu_baseline"] = None
 
-    runtime.free([h for _, _, _, h in handles])
     print(json.dumps(result), flush=True)
     return 0
 

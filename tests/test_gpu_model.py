@@ -44,7 +44,7 @@ def reference_hidden(model: modeling.BC4Decoder, ids: torch.Tensor, ext) -> torc
         y = x @ w.t().contiguous()
         return y + layer.biases[name].float() if name in layer.biases else y
 
-    h = model.embed.float()[ids]
+    h = model.embed.float()[ids]  # fp32 residual stream, as the decoder keeps it
     group = c.heads // c.kv_heads
     mask = torch.triu(torch.ones(t, t, dtype=torch.bool, device=ids.device), 1)
     for layer in model.layers:

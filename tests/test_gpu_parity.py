@@ -180,6 +180,28 @@ def test_prefill_candidates_bitwise_equal_and_within_rrms(ext, oracle_threads, t
     assert bc4.relative_rms(ref, got) <= PREFILL_RRMS_TOL
 
 
+@pytest.mark.parametrize("m,k,tokens", [(96, 4096, 20), (300, 27648, 32), (1024, 5120, 130)])
+def test_prefill_split_k_matches_oracle(ext, oracle_threads, m, k, tokens):
+    """Shapes whose prefill is split along K (partials in the workspace, ordered reduction):
+    still bitwise equal across tiles and within the rrms bar of the float64 GEMM."""
+    blocks = random_blocks(m, k, 44)
+    scales = lognormal_scales(m, 45)
+    x = (bf16_vector((tokens, k), 46).float() * 0.125).to(torch.bfloat16)
+    bias = bf16_vector((m,), 47, scale=0.1)
+    handle = _pack(ext, blocks, scales, bias.cuda())
+    try:
+        assert ext.workspace_bytes(handle, tokens) > 0, "shape expected to split"
+        outputs = [ext.prefill(handle, c, x.cuda()) for c in range(5, 10)]
+        torch.cuda.synchronize()
+    finally:
+        ext.free(handle)
+    for c, value in zip(range(6, 10), outputs[1:]):
+        assert torch.equal(outputs[0], value), f"candidate {c} differs"
+    w = clib.decode_bf16_bits(blocks, scales)
+    ref = clib.gemm_f64(bf16_bits(x), w) + bias.float().numpy()[None, :]
+    assert bc4.relative_rms(ref, outputs[0].float().cpu().numpy()) <= PREFILL_RRMS_TOL
+
+
 def test_prefill_bias_double_rounding(ext):
     m, k, tokens = 64, 256, 40
     blocks = random_blocks(m, k, 51)

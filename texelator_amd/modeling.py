@@ -11,8 +11,9 @@ Layer math follows Qwen2, the architecture of BASELINE configs 4 and 5:
 - RMSNorm in fp32 with ``weight * x``;
 - rotate-half RoPE with ``theta``;
 - grouped-query attention with q/k/v biases;
-- SwiGLU MLP;
-- residuals in bf16.
+- SwiGLU MLP.
+
+The residual stream and the SwiGLU product are kept in fp32; every linear reads and writes bf16.
 
 Attention uses plain batched products whose right operands are contiguous (no transposed
 views), with the softmax in fp32.
@@ -69,12 +70,23 @@ class DecoderConfig:
         return self.layers * sum(m * k // 2 + 4 * m for _, m, k in self.linear_shapes())
 
 
-def random_bc4(m: int, k: int, generator: torch.Generator, device: torch.device) -> tuple[torch.Tensor, torch.Tensor]:
+def random_bc4(m: int, k: int, generator: torch.Generator, device: torch.device,
+               std: float = 0.02) -> tuple[torch.Tensor, torch.Tensor]:
     """Random BC4 matrix on the device: uniform block bytes (every endpoint and selector value
-    occurs) and row scales 0.035 * LogNormal(0, 0.1), so decoded weights have std ~0.02."""
+    occurs) and row scales 1.75 * std * LogNormal(0, 0.1). Uniform blocks decode to palette
+    values with standard deviation ~0.57, so the weights have standard deviation ~std."""
     blocks = torch.randint(0, 256, (m * (k // 16) * 8,), dtype=torch.uint8, device=device, generator=generator)
-    scales = 0.035 * torch.exp(0.1 * torch.randn(m, device=device, generator=generator))
+    scales = 1.75 * std * torch.exp(0.1 * torch.randn(m, device=device, generator=generator))
     return blocks, scales
+
+
+def init_std(config: "DecoderConfig", name: str, depth_scaled: bool) -> float:
+    """Random-init standard deviation of a linear: Hugging Face's ``initializer_range`` 0.02.
+    With ``depth_scaled``, the two projections that write into the residual stream (o_proj,
+    down_proj) also get GPT-2's 1/sqrt(2 * layers)."""
+    if depth_scaled and name in ("self_attn.o_proj", "mlp.down_proj"):
+        return 0.02 / math.sqrt(2 * config.layers)
+    return 0.02
 
 
 class _Layer:
@@ -89,9 +101,19 @@ class BC4Decoder:
     """Decoder with BC4 linears, a static KV cache and graph-captured decode steps."""
 
     def __init__(self, config: DecoderConfig, max_context: int, device: torch.device | str = "cuda", seed: int = 0,
-                 lookahead: int = 1, linear_source=None):
+                 lookahead: int = 1, linear_source=None, depth_scaled: bool = True, embed_std: float = 1.0):
         """``linear_source(layer, name, m, k)`` may return ``(blocks, scales)`` device tensors for a
-        linear (reference block layout); by default every linear is a seeded random BC4 matrix."""
+        linear (reference block layout). By default every linear is a seeded random BC4 matrix.
+
+        The random init follows Hugging Face's for Qwen2: weights N(0, 0.02) (here as BC4), norms
+        1, and q/k/v biases 0. The biases are still passed to the handles, so the kernels' bias
+        epilogues run.
+
+        Two defaults condition the deep random network, so that rounding differences between
+        the decode and prefill kernels are not amplified chaotically through 64 layers:
+        - ``depth_scaled``: GPT-2's 1/sqrt(2 * layers) on o_proj and down_proj;
+        - a unit-scale embedding (``embed_std``).
+        ``depth_scaled=False, embed_std=0.02`` gives Hugging Face's plain init."""
         self.config = config
         self.device = torch.device(device)
         self.max_context = int(max_context)
@@ -103,7 +125,7 @@ class BC4Decoder:
         def normal(*shape, std=0.02):
             return (torch.randn(shape, device=self.device, generator=g) * std).to(bf16)
 
-        self.embed = normal(c.vocab, c.hidden)
+        self.embed = normal(c.vocab, c.hidden, std=embed_std)
         self.lm_head = normal(c.vocab, c.hidden)
         self.final_norm = torch.ones(c.hidden, device=self.device, dtype=bf16)
         self.handles: list[int] = []
@@ -115,9 +137,11 @@ class BC4Decoder:
                 layer.post_norm = torch.ones(c.hidden, device=self.device, dtype=bf16)
                 for name, m, k in c.linear_shapes():
                     source = linear_source(index, name, m, k) if linear_source else None
-                    blocks, scales = source if source is not None else random_bc4(m, k, g, self.device)
-                    bias = normal(m) if (c.qkv_bias and name in ("self_attn.q_proj", "self_attn.k_proj",
-                                                                   "self_attn.v_proj")) else None
+                    blocks, scales = source if source is not None else random_bc4(
+                        m, k, g, self.device, init_std(c, name, depth_scaled))
+                    bias = (torch.zeros(m, device=self.device, dtype=bf16)
+                            if c.qkv_bias and name in ("self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj")
+                            else None)
                     handle = ext.pack_encoded_device(blocks, scales, bias)
                     if bias is not None:
                         layer.biases[name] = bias
@@ -156,6 +180,7 @@ class BC4Decoder:
             ext.set_prefill_backend(handle, backend)
 
     def _rms_norm(self, x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+        """RMSNorm of the fp32 residual stream, returned as the bf16 input of the next linears."""
         xf = x.float()
         xf = xf * torch.rsqrt(xf.square().mean(-1, keepdim=True) + self.config.rms_eps)
         return weight * xf.to(torch.bfloat16)
@@ -186,7 +211,8 @@ class BC4Decoder:
         # queries as [kv, d, group * T] (column = g * T + t), contiguous
         qt = q.view(tokens, c.kv_heads, group, c.head_dim).permute(1, 3, 2, 0).reshape(
             c.kv_heads, c.head_dim, group * tokens).contiguous()
-        scores = torch.bmm(keys, qt).float() * (1.0 / math.sqrt(c.head_dim))   # [kv, L, G*T]
+        # scores accumulate and stay in fp32 (as flash attention keeps them), never rounded to bf16
+        scores = torch.bmm(keys, qt, out_dtype=torch.float32) * (1.0 / math.sqrt(c.head_dim))   # [kv, L, G*T]
         future = self.key_positions[:length, None] > positions.repeat(group)[None, :]
         scores = scores.masked_fill(future, float("-inf"))
         probs = torch.softmax(scores, dim=1).to(torch.bfloat16)     # [kv, L, G*T], contiguous
@@ -195,9 +221,12 @@ class BC4Decoder:
             tokens, c.heads * c.head_dim)
 
     def hidden_states(self, ids: torch.Tensor, positions: torch.Tensor, length: int) -> torch.Tensor:
-        """Final-norm hidden states [T, hidden] for tokens ``ids`` at ``positions``."""
+        """Final-norm hidden states [T, hidden] (bf16) for tokens ``ids`` at ``positions``.
+
+        The residual stream is kept in fp32 and the SwiGLU product is formed in fp32; every
+        linear reads bf16 activations and writes bf16 outputs."""
         c = self.config
-        h = self.embed.index_select(0, ids)
+        h = self.embed.index_select(0, ids).float()
         for index, layer in enumerate(self.layers):
             x = self._rms_norm(h, layer.input_norm)
             lin = layer.linears
@@ -205,9 +234,10 @@ class BC4Decoder:
             k = lin["self_attn.k_proj"](x).view(-1, c.kv_heads, c.head_dim)
             v = lin["self_attn.v_proj"](x).view(-1, c.kv_heads, c.head_dim)
             q, k = self._rope(q, positions), self._rope(k, positions)
-            h = h + lin["self_attn.o_proj"](self._attention(index, q, k, v, positions, length))
+            h = h + lin["self_attn.o_proj"](self._attention(index, q, k, v, positions, length)).float()
             x = self._rms_norm(h, layer.post_norm)
-            h = h + lin["mlp.down_proj"](functional.silu(lin["mlp.gate_proj"](x)) * lin["mlp.up_proj"](x))
+            act = functional.silu(lin["mlp.gate_proj"](x).float()) * lin["mlp.up_proj"](x).float()
+            h = h + lin["mlp.down_proj"](act.to(torch.bfloat16)).float()
         return self._rms_norm(h, self.final_norm)
 
     def logits(self, hidden: torch.Tensor) -> torch.Tensor:
