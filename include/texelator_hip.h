@@ -112,6 +112,38 @@ int tx_kernel_info(int candidate, int64_t *out, int n);
 /* Name of a prefill candidate (5..9) or NULL. */
 const char *tx_candidate_name(int candidate);
 
+/* ---- Decoder-layer helpers ------------------------------------------------------------------
+ * No reference counterpart: the reference runs these layers as stock Hugging Face modules
+ * (docs/supported-models.md:3-5) and replaces only the linears. They let a whole BC4 decode step
+ * be a short, graph-capturable kernel sequence. All device pointers; bf16 data as uint16 bits.
+ * The KV caches are bf16 [kv_heads][max_context][head_dim]. */
+
+/* residual[r] += delta[r] (delta may be NULL); out[r] = bf16(weight * bf16(residual[r] *
+ * rsqrt(mean(residual[r]^2) + eps))). residual f32 [rows][hidden]; delta, out bf16; weight bf16 [hidden];
+ * hidden a multiple of 4; all pointers 16-byte aligned. */
+int tx_add_rmsnorm(float *residual, const void *delta, const void *weight, float eps, void *out, int64_t rows,
+                   int64_t hidden, void *stream);
+
+/* Rotate-half RoPE of the q and k heads of a packed [q | k | v] bf16 row (stride row_stride
+ * elements) at positions[t]: q heads to q_out [tokens][heads][head_dim], k heads into k_cache, and
+ * v heads copied into v_cache, at row positions[t]. cos/sin tables f32 [max_context][head_dim]. */
+int tx_rope_kv_cache(const void *qkv, int64_t row_stride, int64_t tokens, const int64_t *positions,
+                     const float *cos_table, const float *sin_table, int heads, int kv_heads, int head_dim,
+                     void *q_out, void *k_cache, void *v_cache, int64_t max_context, void *stream);
+
+/* Workspace bytes of tx_decode_attention for `length` cached positions. */
+int tx_decode_attention_workspace(int heads, int64_t length, int64_t *bytes);
+
+/* Attention of one query token q [heads][head_dim] over cached keys 0..*position (device int64;
+ * keys up to `length`, a static bound) with fp32 scores and softmax; grouped-query (heads /
+ * kv_heads query heads per KV head, at most 8); head_dim must be 128. out bf16 [heads][head_dim]. */
+int tx_decode_attention(const void *q, const void *k_cache, const void *v_cache, const int64_t *position,
+                        int64_t length, int heads, int kv_heads, int head_dim, int64_t max_context, float scale,
+                        void *workspace, int64_t workspace_bytes, void *out, void *stream);
+
+/* out[r][c] = bf16(silu(g) * u) for gate_up rows [g (intermediate) | u (intermediate)], fp32 math. */
+int tx_swiglu(const void *gate_up, int64_t rows, int64_t intermediate, void *out, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -10,7 +10,7 @@ import pytest
 import torch
 from torch.nn import functional
 
-from texelator_amd import modeling, prefill
+from texelator_amd import layers, modeling, prefill
 
 pytestmark = pytest.mark.gpu
 
@@ -22,8 +22,15 @@ def tiny(ext):
     model.close()
 
 
+@pytest.fixture(scope="module")
+def tiny_torch(ext):
+    model = modeling.BC4Decoder(modeling.DecoderConfig.tiny(), max_context=1024, seed=3, fused=False)
+    yield model
+    model.close()
+
+
 def reference_hidden(model: modeling.BC4Decoder, ids: torch.Tensor, ext) -> torch.Tensor:
-    """Float32 forward of the same architecture on the dense decoded weights."""
+    """Float32 forward of the same architecture on the dense decoded weights (attention in fp32)."""
     c = model.config
     t = ids.numel()
     pos = torch.arange(t, device=ids.device)
@@ -39,27 +46,26 @@ def reference_hidden(model: modeling.BC4Decoder, ids: torch.Tensor, ext) -> torc
         h = x.shape[-1] // 2
         return x * cos + torch.cat([-x[..., h:], x[..., :h]], -1) * sin
 
-    def lin(layer, name, x):
-        w = ext.decode_dense(layer.linears[name].handles[0]).float()
-        y = x @ w.t().contiguous()
-        return y + layer.biases[name].float() if name in layer.biases else y
+    def lin(index, name, x):
+        return x @ model.dense_weight(index, name).float().t().contiguous()
 
     h = model.embed.float()[ids]  # fp32 residual stream, as the decoder keeps it
     group = c.heads // c.kv_heads
     mask = torch.triu(torch.ones(t, t, dtype=torch.bool, device=ids.device), 1)
-    for layer in model.layers:
+    for index, layer in enumerate(model.layers):
         x = norm(h, layer.input_norm)
-        q = rope(lin(layer, "self_attn.q_proj", x).view(t, c.heads, c.head_dim))
-        k = rope(lin(layer, "self_attn.k_proj", x).view(t, c.kv_heads, c.head_dim))
-        v = lin(layer, "self_attn.v_proj", x).view(t, c.kv_heads, c.head_dim)
+        q = rope(lin(index, "self_attn.q_proj", x).view(t, c.heads, c.head_dim))
+        k = rope(lin(index, "self_attn.k_proj", x).view(t, c.kv_heads, c.head_dim))
+        v = lin(index, "self_attn.v_proj", x).view(t, c.kv_heads, c.head_dim)
         k = k.repeat_interleave(group, 1)
         v = v.repeat_interleave(group, 1)
         scores = torch.einsum("thd,shd->hts", q, k) / math.sqrt(c.head_dim)
         probs = torch.softmax(scores.masked_fill(mask, float("-inf")), -1)
         attn = torch.einsum("hts,shd->thd", probs, v).reshape(t, -1)
-        h = h + lin(layer, "self_attn.o_proj", attn)
+        h = h + lin(index, "self_attn.o_proj", attn)
         x = norm(h, layer.post_norm)
-        h = h + lin(layer, "mlp.down_proj", functional.silu(lin(layer, "mlp.gate_proj", x)) * lin(layer, "mlp.up_proj", x))
+        h = h + lin(index, "mlp.down_proj",
+                    functional.silu(lin(index, "mlp.gate_proj", x)) * lin(index, "mlp.up_proj", x))
     return norm(h, model.final_norm)
 
 
@@ -114,3 +120,77 @@ def test_benchmark_decode_reports_buckets(ext, tiny):
     result = prefill.benchmark_decode(tiny, prompt_tokens=100, context=600)
     assert result["steps"] == 500 and set(result["per_bucket"]) == {"512", "1024"}
     assert result["gpu_tokens_per_second"] > 0
+
+
+def test_fused_path_matches_torch_path(ext, tiny, tiny_torch):
+    """Same seed, same BC4 weights: the fused kernels agree with the plain PyTorch layer glue."""
+    ids = prefill.prompt_ids(tiny, 40, seed=5)
+    with torch.inference_mode():
+        a = tiny.hidden_states(ids, tiny.key_positions[:40], 40)
+        b = tiny_torch.hidden_states(ids, tiny_torch.key_positions[:40], 40)
+    assert rrms(b, a) < 1e-2
+    # decode: the split-length attention against the torch attention over the cache
+    ga = tiny.generate(ids, 8, eager=True)
+    gb = tiny_torch.generate(ids, 8, eager=True)
+    with torch.inference_mode():
+        ha = tiny.hidden_states(ga[-1:], tiny.key_positions[47:48], 48)
+        hb = tiny_torch.hidden_states(ga[-1:], tiny_torch.key_positions[47:48], 48)
+    assert rrms(hb, ha) < 2e-2
+    assert (ga == gb).float().mean() >= 0.75
+
+
+def test_add_rmsnorm_kernel(ext):
+    g = torch.Generator(device="cuda").manual_seed(7)
+    h = torch.randn(5, 5120, device="cuda", generator=g)
+    d = torch.randn(5, 5120, device="cuda", generator=g).to(torch.bfloat16)
+    w = (1 + 0.1 * torch.randn(5120, device="cuda", generator=g)).to(torch.bfloat16)
+    want_h = h + d.float()
+    want = w.float() * (want_h * torch.rsqrt(want_h.square().mean(-1, keepdim=True) + 1e-6)).to(torch.bfloat16).float()
+    got = layers.add_rmsnorm(h, d, w, 1e-6)
+    assert torch.equal(h, want_h)
+    assert rrms(want, got) < 4e-3
+
+
+def test_rope_kv_cache_kernel(ext, tiny):
+    c = tiny.config
+    g = torch.Generator(device="cuda").manual_seed(8)
+    t = 6
+    width = (c.heads + 2 * c.kv_heads) * c.head_dim
+    qkv = torch.randn(t, width, device="cuda", generator=g).to(torch.bfloat16)
+    positions = torch.tensor([0, 3, 7, 100, 511, 1023], device="cuda")
+    kc = torch.zeros(c.kv_heads, 1024, c.head_dim, device="cuda", dtype=torch.bfloat16)
+    vc = torch.zeros_like(kc)
+    q = layers.rope_kv_cache(qkv, positions, tiny.rope_cos, tiny.rope_sin, c.heads, c.kv_heads, c.head_dim, kc, vc)
+    qs = c.heads * c.head_dim
+    ks = c.kv_heads * c.head_dim
+    want_q = tiny._rope(qkv[:, :qs].reshape(t, c.heads, c.head_dim), positions).reshape(t, -1)
+    want_k = tiny._rope(qkv[:, qs:qs + ks].reshape(t, c.kv_heads, c.head_dim), positions)
+    assert torch.equal(q, want_q)
+    assert torch.equal(kc[:, positions].transpose(0, 1), want_k)
+    assert torch.equal(vc[:, positions].transpose(0, 1), qkv[:, qs + ks:].reshape(t, c.kv_heads, c.head_dim))
+
+
+@pytest.mark.parametrize("position,length", [(0, 512), (100, 512), (511, 512), (700, 1024), (1023, 1024)])
+def test_decode_attention_kernel(ext, position, length):
+    heads, kv, d, ctx = 40, 8, 128, 1024
+    g = torch.Generator(device="cuda").manual_seed(position)
+    kc = torch.randn(kv, ctx, d, device="cuda", generator=g).to(torch.bfloat16)
+    vc = torch.randn(kv, ctx, d, device="cuda", generator=g).to(torch.bfloat16)
+    q = (torch.randn(heads * d, device="cuda", generator=g) * 0.3).to(torch.bfloat16)
+    pos = torch.tensor([position], device="cuda")
+    ws = torch.empty(layers.decode_attention_workspace_bytes(heads, length), dtype=torch.uint8, device="cuda")
+    got = layers.decode_attention(q, kc, vc, pos, length, heads, kv, 1 / math.sqrt(d), ws).float()
+    qf = q.float().view(kv, heads // kv, d)
+    keys, values = kc[:, :position + 1].float(), vc[:, :position + 1].float()
+    scores = torch.einsum("kgd,ksd->kgs", qf, keys) / math.sqrt(d)
+    want = torch.einsum("kgs,ksd->kgd", torch.softmax(scores, -1), values).reshape(1, -1)
+    assert rrms(want, got) < 5e-3
+
+
+def test_swiglu_kernel(ext):
+    g = torch.Generator(device="cuda").manual_seed(9)
+    gu = (torch.randn(3, 2 * 1024, device="cuda", generator=g) * 3).to(torch.bfloat16)
+    got = layers.swiglu(gu).float()
+    f = gu.float()
+    want = (functional.silu(f[:, :1024]) * f[:, 1024:]).to(torch.bfloat16).float()
+    assert rrms(want, got) < 4e-3

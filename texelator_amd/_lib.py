@@ -45,6 +45,11 @@ SIGNATURES = {
     "tx_decode_dense": (_I32, [_U64, _P, _P]),
     "tx_kernel_info": (_I32, [_I32, ctypes.POINTER(_I64), _I32]),
     "tx_candidate_name": (ctypes.c_char_p, [_I32]),
+    "tx_add_rmsnorm": (_I32, [_P, _P, _P, ctypes.c_float, _P, _I64, _I64, _P]),
+    "tx_rope_kv_cache": (_I32, [_P, _I64, _I64, _P, _P, _P, _I32, _I32, _I32, _P, _P, _P, _I64, _P]),
+    "tx_decode_attention_workspace": (_I32, [_I32, _I64, ctypes.POINTER(_I64)]),
+    "tx_decode_attention": (_I32, [_P, _P, _P, _P, _I64, _I32, _I32, _I32, _I64, ctypes.c_float, _P, _I64, _P, _P]),
+    "tx_swiglu": (_I32, [_P, _I64, _I64, _P, _P]),
 }
 
 _LIB = None

@@ -406,4 +406,68 @@ int tx_kernel_info(int candidate, int64_t *out, int n) {
 
 const char *tx_candidate_name(int candidate) { return tx::prefill_candidate_name(candidate); }
 
+int tx_add_rmsnorm(float *residual, const void *delta, const void *weight, float eps, void *out, int64_t rows,
+                   int64_t hidden, void *stream) {
+  g_last_error.clear();
+  if (!residual || !weight || !out || rows < 0 || hidden <= 0 || hidden > (1 << 24) || hidden % 4)
+    return fail(TX_ERR_INVALID, "add_rmsnorm: invalid arguments (hidden must be a positive multiple of 4)");
+  if (rows == 0) return TX_OK;
+  TX_HIP(tx::launch_add_rmsnorm(residual, static_cast<const uint16_t *>(delta), static_cast<const uint16_t *>(weight),
+                                eps, static_cast<uint16_t *>(out), rows, (int)hidden, reinterpret_cast<hipStream_t>(stream)));
+  return TX_OK;
+}
+
+int tx_rope_kv_cache(const void *qkv, int64_t row_stride, int64_t tokens, const int64_t *positions, const float *cos_table,
+                     const float *sin_table, int heads, int kv_heads, int head_dim, void *q_out, void *k_cache,
+                     void *v_cache, int64_t max_context, void *stream) {
+  g_last_error.clear();
+  if (!qkv || !positions || !cos_table || !sin_table || !q_out || !k_cache || !v_cache)
+    return fail(TX_ERR_INVALID, "rope_kv_cache: null pointer");
+  if (heads <= 0 || kv_heads <= 0 || head_dim <= 0 || head_dim % 2 || head_dim > 1024 || tokens < 0 ||
+      row_stride < (int64_t)(heads + 2 * kv_heads) * head_dim || max_context <= 0)
+    return fail(TX_ERR_INVALID, "rope_kv_cache: invalid shape");
+  if (tokens == 0) return TX_OK;
+  TX_HIP(tx::launch_rope_cache(static_cast<const uint16_t *>(qkv), row_stride, tokens, positions, cos_table, sin_table,
+                               heads, kv_heads, head_dim, static_cast<uint16_t *>(q_out), static_cast<uint16_t *>(k_cache),
+                               static_cast<uint16_t *>(v_cache), max_context, reinterpret_cast<hipStream_t>(stream)));
+  return TX_OK;
+}
+
+int tx_decode_attention_workspace(int heads, int64_t length, int64_t *bytes) {
+  g_last_error.clear();
+  if (!bytes || heads <= 0 || length <= 0) return fail(TX_ERR_INVALID, "decode_attention_workspace: invalid arguments");
+  *bytes = (int64_t)tx::decode_attention_chunks(length) * heads * (128 + 2) * (int64_t)sizeof(float);
+  return TX_OK;
+}
+
+int tx_decode_attention(const void *q, const void *k_cache, const void *v_cache, const int64_t *position, int64_t length,
+                        int heads, int kv_heads, int head_dim, int64_t max_context, float scale, void *workspace,
+                        int64_t workspace_bytes, void *out, void *stream) {
+  g_last_error.clear();
+  if (!q || !k_cache || !v_cache || !position || !out || !workspace)
+    return fail(TX_ERR_INVALID, "decode_attention: null pointer");
+  if (!tx::decode_attention_supported(heads, kv_heads, head_dim))
+    return fail(TX_ERR_UNSUPPORTED, "decode_attention: needs head_dim 128 and at most 8 query heads per KV head");
+  if (length <= 0 || length > max_context || length > tx::decode_attention_max_length())
+    return fail(TX_ERR_INVALID, "decode_attention: length outside the cache or above 65536");
+  int64_t need = 0;
+  tx_decode_attention_workspace(heads, length, &need);
+  if (workspace_bytes < need) return fail(TX_ERR_INVALID, "decode_attention: workspace too small");
+  TX_HIP(tx::launch_decode_attention(static_cast<const uint16_t *>(q), static_cast<const uint16_t *>(k_cache),
+                                     static_cast<const uint16_t *>(v_cache), position, length, heads, kv_heads,
+                                     max_context, scale, static_cast<float *>(workspace), static_cast<uint16_t *>(out),
+                                     reinterpret_cast<hipStream_t>(stream)));
+  return TX_OK;
+}
+
+int tx_swiglu(const void *gate_up, int64_t rows, int64_t intermediate, void *out, void *stream) {
+  g_last_error.clear();
+  if (!gate_up || !out || rows < 0 || intermediate <= 0 || intermediate % 8)
+    return fail(TX_ERR_INVALID, "swiglu: intermediate size must be a positive multiple of 8");
+  if (rows == 0) return TX_OK;
+  TX_HIP(tx::launch_swiglu(static_cast<const uint16_t *>(gate_up), rows, intermediate, static_cast<uint16_t *>(out),
+                           reinterpret_cast<hipStream_t>(stream)));
+  return TX_OK;
+}
+
 }  // extern "C"

@@ -1,0 +1,354 @@
+// Decoder-layer helpers around the BC4 linears (gfx950): fused residual add + RMSNorm, RoPE +
+// KV-cache write, split-length decode attention and SwiGLU.
+//
+// No reference counterpart: the reference runs these layers as stock Hugging Face modules
+// (docs/supported-models.md:3-5) and only replaces the linears. Here they exist so that a whole
+// decode step is a short, graph-capturable sequence of kernels.
+//
+// Layouts: activations row-major bf16 [rows][width]; the residual stream fp32; the KV caches
+// bf16 [kv_head][position][head_dim].
+#include <math.h>
+
+#include "kernels.h"
+
+namespace tx {
+
+namespace {
+
+__device__ __forceinline__ float bf(uint16_t v) { return __builtin_bit_cast(float, (uint32_t)v << 16); }
+
+__device__ __forceinline__ uint16_t to_bf(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
+
+// h[row] += delta[row] (if given); out[row] = bf16(weight * bf16(h * rsqrt(mean(h^2) + eps))).
+// One block per row; each thread owns groups of 4 columns (4 * t + 1024 * i), all of whose loads
+// are issued before the reduction. hidden must be a multiple of 4.
+__global__ __launch_bounds__(256) void add_rmsnorm_kernel(float *h, const uint16_t *delta, const uint16_t *weight,
+                                                          float eps, uint16_t *out, int hidden) {
+  constexpr int kUnroll = 8;  // register-resident groups per thread (covers hidden <= 8192)
+  __shared__ float partial[4];
+  float4 *hr = reinterpret_cast<float4 *>(h + (size_t)blockIdx.x * hidden);
+  const uint2 *dr = delta ? reinterpret_cast<const uint2 *>(delta + (size_t)blockIdx.x * hidden) : nullptr;
+  uint2 *orow = reinterpret_cast<uint2 *>(out + (size_t)blockIdx.x * hidden);
+  const uint2 *wr = reinterpret_cast<const uint2 *>(weight);
+  const int groups = hidden / 4;
+  float ss = 0.f;
+  for (int base = 0; base < groups; base += 256 * kUnroll) {
+    // load phase: every load of this pass in flight at once (indices clamped, then masked)
+    float4 v[kUnroll];
+    uint2 d[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int i = min(base + u * 256 + (int)threadIdx.x, groups - 1);
+      v[u] = hr[i];
+      if (dr) d[u] = dr[i];
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int i = base + u * 256 + (int)threadIdx.x;
+      if (i >= groups) continue;
+      if (dr) {
+        v[u].x += bf((uint16_t)(d[u].x & 0xFFFFu));
+        v[u].y += bf((uint16_t)(d[u].x >> 16));
+        v[u].z += bf((uint16_t)(d[u].y & 0xFFFFu));
+        v[u].w += bf((uint16_t)(d[u].y >> 16));
+        hr[i] = v[u];
+      }
+      ss += (v[u].x * v[u].x + v[u].y * v[u].y) + (v[u].z * v[u].z + v[u].w * v[u].w);
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+  if ((threadIdx.x & 63) == 0) partial[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  ss = (partial[0] + partial[1]) + (partial[2] + partial[3]);
+  const float inv = rsqrtf(ss / (float)hidden + eps);
+  for (int i = threadIdx.x; i < groups; i += 256) {
+    const float4 v = hr[i];
+    const uint2 w = wr[i];
+    const float n0 = bf(to_bf(v.x * inv)), n1 = bf(to_bf(v.y * inv)), n2 = bf(to_bf(v.z * inv)), n3 = bf(to_bf(v.w * inv));
+    const uint32_t lo = (uint32_t)to_bf(bf((uint16_t)(w.x & 0xFFFFu)) * n0) | ((uint32_t)to_bf(bf((uint16_t)(w.x >> 16)) * n1) << 16);
+    const uint32_t hi = (uint32_t)to_bf(bf((uint16_t)(w.y & 0xFFFFu)) * n2) | ((uint32_t)to_bf(bf((uint16_t)(w.y >> 16)) * n3) << 16);
+    orow[i] = make_uint2(lo, hi);
+  }
+}
+
+// One block per (token, head); thread j rotates the pair (j, j + d/2) of rotate-half RoPE.
+// q heads are written to q_out; k heads are rotated into the K cache; v heads are copied.
+__global__ void rope_cache_kernel(const uint16_t *qkv, int64_t stride, const int64_t *positions, const float *cos_t,
+                                  const float *sin_t, int heads, int kv_heads, int d, uint16_t *q_out, uint16_t *k_cache,
+                                  uint16_t *v_cache, int64_t max_ctx) {
+  const int t = blockIdx.x;
+  const int head = blockIdx.y;
+  const int j = threadIdx.x;
+  const int half = d / 2;
+  const int64_t pos = positions[t];
+  const uint16_t *row = qkv + (size_t)t * stride;
+  if (head < heads + kv_heads) {
+    const uint16_t *src = row + (size_t)head * d;
+    const float x1 = bf(src[j]), x2 = bf(src[j + half]);
+    const float c1 = cos_t[pos * d + j], c2 = cos_t[pos * d + j + half];
+    const float s1 = sin_t[pos * d + j], s2 = sin_t[pos * d + j + half];
+    const uint16_t o1 = to_bf(x1 * c1 - x2 * s1);
+    const uint16_t o2 = to_bf(x2 * c2 + x1 * s2);
+    uint16_t *dst = head < heads ? q_out + ((size_t)t * heads + head) * d
+                                 : k_cache + ((size_t)(head - heads) * max_ctx + pos) * d;
+    dst[j] = o1;
+    dst[j + half] = o2;
+  } else {
+    const int kv = head - heads - kv_heads;
+    const uint16_t *src = row + (size_t)(heads + kv_heads + kv) * d;
+    uint16_t *dst = v_cache + ((size_t)kv * max_ctx + pos) * d;
+    dst[j] = src[j];
+    dst[j + half] = src[j + half];
+  }
+}
+
+constexpr int kChunk = 64;      // keys per attention block
+constexpr int kHeadDim = 128;   // head_dim handled by the decode attention kernels
+constexpr int kMaxGroup = 8;    // query heads per KV head
+constexpr int kRowU4 = kHeadDim * 2 / 16;  // uint4 per cached key or value row (16)
+
+// Split-length decode attention for one query token. Block (kv, chunk) loads the chunk's keys and
+// values (those <= position) into LDS in one burst, scores the group's query heads against them
+// in fp32, and writes the chunk's max m, sum of exp l and unnormalised output o to
+// partials[kv][chunk][g][130].
+__global__ __launch_bounds__(256) void decode_attention_kernel(const uint16_t *q, const uint16_t *k_cache,
+                                                               const uint16_t *v_cache, const int64_t *position,
+                                                               int group, int64_t max_ctx, float scale,
+                                                               int chunks, float *partials) {
+  __shared__ uint4 ks[kChunk * kRowU4];
+  __shared__ uint4 vs[kChunk * kRowU4];
+  __shared__ float qs[kMaxGroup][kHeadDim];
+  __shared__ float probs[kMaxGroup][kChunk];
+  __shared__ float stats[kMaxGroup][2];
+  const int kv = blockIdx.x;
+  const int chunk = blockIdx.y;
+  const int tid = threadIdx.x;
+  const int j0 = chunk * kChunk;
+  float *out = partials + ((size_t)kv * chunks + chunk) * group * (kHeadDim + 2);
+  // Issue the chunk's K/V rows (clamped into the cache) and q before the position arrives:
+  // nothing waits for a load whose result only masks.
+  const uint4 *kg = reinterpret_cast<const uint4 *>(k_cache + (size_t)kv * max_ctx * kHeadDim);
+  const uint4 *vg = reinterpret_cast<const uint4 *>(v_cache + (size_t)kv * max_ctx * kHeadDim);
+  uint4 kr[4], vr[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int idx = u * 256 + tid;
+    const int64_t row = min((int64_t)(j0 + idx / kRowU4), max_ctx - 1);
+    kr[u] = kg[row * kRowU4 + idx % kRowU4];
+    vr[u] = vg[row * kRowU4 + idx % kRowU4];
+  }
+  float qv[kMaxGroup * kHeadDim / 256];
+#pragma unroll
+  for (int u = 0; u < kMaxGroup * kHeadDim / 256; ++u) {
+    const int i = u * 256 + tid;
+    qv[u] = i < group * kHeadDim ? bf(q[(size_t)kv * group * kHeadDim + i]) : 0.f;
+  }
+  const int64_t pos = *position;
+  if (j0 > pos) {
+    for (int i = tid; i < group * (kHeadDim + 2); i += 256) out[i] = (i % (kHeadDim + 2)) == kHeadDim ? -INFINITY : 0.f;
+    return;
+  }
+  const int count = (int)min((int64_t)kChunk, pos - j0 + 1);  // valid keys in this chunk
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    ks[u * 256 + tid] = kr[u];
+    vs[u * 256 + tid] = vr[u];
+  }
+#pragma unroll
+  for (int u = 0; u < kMaxGroup * kHeadDim / 256; ++u) {
+    const int i = u * 256 + tid;
+    if (i < group * kHeadDim) qs[i / kHeadDim][i % kHeadDim] = qv[u];
+  }
+  __syncthreads();
+
+  // scores: four threads per key, 32 dimensions each
+  {
+    const int jl = tid >> 2;
+    const int part = tid & 3;
+    float kf[32];
+    const uint4 *row = ks + jl * kRowU4 + part * 4;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const uint4 w = row[v];
+      const uint32_t words[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        kf[v * 8 + 2 * e] = bf((uint16_t)(words[e] & 0xFFFFu));
+        kf[v * 8 + 2 * e + 1] = bf((uint16_t)(words[e] >> 16));
+      }
+    }
+    for (int g = 0; g < group; ++g) {
+      float s = 0.f;
+#pragma unroll
+      for (int e = 0; e < 32; ++e) s = __builtin_fmaf(qs[g][part * 32 + e], kf[e], s);
+      s += __shfl_xor(s, 1);
+      s += __shfl_xor(s, 2);
+      if (part == 0) probs[g][jl] = jl < count ? s * scale : -INFINITY;
+    }
+  }
+  __syncthreads();
+
+  // per query head: max, exp, sum (one wave per head, one lane per key)
+  {
+    const int wave = tid >> 6, lane = tid & 63;
+    for (int g = wave; g < group; g += 4) {
+      const float a = probs[g][lane];
+      float m = a;
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+      const float pa = expf(a - m);
+      probs[g][lane] = pa;
+      float l = pa;
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o);
+      if (lane == 0) {
+        stats[g][0] = m;
+        stats[g][1] = l;
+      }
+    }
+  }
+  __syncthreads();
+
+  // o[g][dd] = sum_j p[g][j] v[j][dd]; thread (dd, half of the heads), values from LDS
+  {
+    const int dd = tid & (kHeadDim - 1);
+    const int gg = tid >> 7;
+    float acc[kMaxGroup / 2];
+#pragma unroll
+    for (int u = 0; u < kMaxGroup / 2; ++u) acc[u] = 0.f;
+    const uint16_t *vcol = reinterpret_cast<const uint16_t *>(vs) + dd;
+    for (int j = 0; j < count; ++j) {
+      const float v = bf(vcol[j * kHeadDim]);
+#pragma unroll
+      for (int u = 0; u < kMaxGroup / 2; ++u) {
+        const int g = gg + 2 * u;
+        if (g < group) acc[u] = __builtin_fmaf(probs[g][j], v, acc[u]);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kMaxGroup / 2; ++u) {
+      const int g = gg + 2 * u;
+      if (g < group) {
+        float *o = out + (size_t)g * (kHeadDim + 2);
+        o[dd] = acc[u];
+        if (dd == 0) {
+          o[kHeadDim] = stats[g][0];
+          o[kHeadDim + 1] = stats[g][1];
+        }
+      }
+    }
+  }
+}
+
+// Merge the chunks of one query head (block = head, thread = dimension) into bf16 output:
+// all chunk statistics are loaded in parallel, then every thread sums its dimension over chunks.
+constexpr int kMaxChunks = 1024;
+__global__ __launch_bounds__(128) void decode_attention_combine_kernel(const float *partials, int group, int chunks,
+                                                                       uint16_t *out) {
+  __shared__ float weight[kMaxChunks];
+  __shared__ float red[2];
+  const int head = blockIdx.x;
+  const int kv = head / group, g = head % group;
+  const int dd = threadIdx.x;
+  const float *base = partials + ((size_t)kv * chunks * group + g) * (kHeadDim + 2);
+  const size_t step = (size_t)group * (kHeadDim + 2);
+  float m = -INFINITY;
+  for (int c = dd; c < chunks; c += 128) {
+    weight[c] = base[c * step + kHeadDim];
+    m = fmaxf(m, weight[c]);
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+  if ((dd & 63) == 0) red[dd >> 6] = m;
+  __syncthreads();
+  m = fmaxf(red[0], red[1]);
+  __syncthreads();
+  float total = 0.f;
+  for (int c = dd; c < chunks; c += 128) {
+    const float w = weight[c] == -INFINITY ? 0.f : expf(weight[c] - m);
+    weight[c] = w;
+    total = __builtin_fmaf(base[c * step + kHeadDim + 1], w, total);
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) total += __shfl_xor(total, o);
+  if ((dd & 63) == 0) red[dd >> 6] = total;
+  __syncthreads();
+  total = red[0] + red[1];
+  float acc0 = 0.f, acc1 = 0.f, acc2 = 0.f, acc3 = 0.f;
+  int c = 0;
+  for (; c + 4 <= chunks; c += 4) {
+    acc0 = __builtin_fmaf(base[c * step + dd], weight[c], acc0);
+    acc1 = __builtin_fmaf(base[(c + 1) * step + dd], weight[c + 1], acc1);
+    acc2 = __builtin_fmaf(base[(c + 2) * step + dd], weight[c + 2], acc2);
+    acc3 = __builtin_fmaf(base[(c + 3) * step + dd], weight[c + 3], acc3);
+  }
+  for (; c < chunks; ++c) acc0 = __builtin_fmaf(base[c * step + dd], weight[c], acc0);
+  out[(size_t)head * kHeadDim + dd] = to_bf(((acc0 + acc1) + (acc2 + acc3)) / total);
+}
+
+// out[r][c] = bf16(silu(g) * u) with g = gu[r][c], u = gu[r][inter + c], in fp32.
+__global__ __launch_bounds__(256) void swiglu_kernel(const uint16_t *gu, int64_t rows, int64_t inter, uint16_t *out) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;   // one group of 8 columns
+  const int64_t groups = inter / 8;
+  if (idx >= rows * groups) return;
+  const int64_t r = idx / groups, c = (idx % groups) * 8;
+  const uint4 gv = *reinterpret_cast<const uint4 *>(gu + r * 2 * inter + c);
+  const uint4 uv = *reinterpret_cast<const uint4 *>(gu + r * 2 * inter + inter + c);
+  const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w}, uw[4] = {uv.x, uv.y, uv.z, uv.w};
+  uint32_t ow[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float g0 = bf((uint16_t)(gw[e] & 0xFFFFu)), g1 = bf((uint16_t)(gw[e] >> 16));
+    const float u0 = bf((uint16_t)(uw[e] & 0xFFFFu)), u1 = bf((uint16_t)(uw[e] >> 16));
+    const float a0 = g0 / (1.0f + expf(-g0)) * u0;
+    const float a1 = g1 / (1.0f + expf(-g1)) * u1;
+    ow[e] = (uint32_t)to_bf(a0) | ((uint32_t)to_bf(a1) << 16);
+  }
+  *reinterpret_cast<uint4 *>(out + r * inter + c) = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+}
+
+}  // namespace
+
+hipError_t launch_add_rmsnorm(float *h, const uint16_t *delta, const uint16_t *weight, float eps, uint16_t *out,
+                              int64_t rows, int hidden, hipStream_t stream) {
+  hipLaunchKernelGGL(add_rmsnorm_kernel, dim3((unsigned)rows), dim3(256), 0, stream, h, delta, weight, eps, out, hidden);
+  return hipGetLastError();
+}
+
+hipError_t launch_rope_cache(const uint16_t *qkv, int64_t stride, int64_t tokens, const int64_t *positions,
+                             const float *cos_t, const float *sin_t, int heads, int kv_heads, int d, uint16_t *q_out,
+                             uint16_t *k_cache, uint16_t *v_cache, int64_t max_ctx, hipStream_t stream) {
+  hipLaunchKernelGGL(rope_cache_kernel, dim3((unsigned)tokens, heads + 2 * kv_heads), dim3(d / 2), 0, stream, qkv, stride,
+                     positions, cos_t, sin_t, heads, kv_heads, d, q_out, k_cache, v_cache, max_ctx);
+  return hipGetLastError();
+}
+
+int decode_attention_chunks(int64_t length) { return (int)((length + kChunk - 1) / kChunk); }
+
+bool decode_attention_supported(int heads, int kv_heads, int head_dim) {
+  return head_dim == kHeadDim && kv_heads > 0 && heads % kv_heads == 0 && heads / kv_heads <= kMaxGroup;
+}
+
+int64_t decode_attention_max_length() { return (int64_t)kMaxChunks * kChunk; }
+
+hipError_t launch_decode_attention(const uint16_t *q, const uint16_t *k_cache, const uint16_t *v_cache,
+                                   const int64_t *position, int64_t length, int heads, int kv_heads, int64_t max_ctx,
+                                   float scale, float *partials, uint16_t *out, hipStream_t stream) {
+  const int chunks = decode_attention_chunks(length);
+  const int group = heads / kv_heads;
+  hipLaunchKernelGGL(decode_attention_kernel, dim3(kv_heads, chunks), dim3(256), 0, stream, q, k_cache, v_cache,
+                     position, group, max_ctx, scale, chunks, partials);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(decode_attention_combine_kernel, dim3(heads), dim3(kHeadDim), 0, stream, partials, group, chunks, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_swiglu(const uint16_t *gu, int64_t rows, int64_t inter, uint16_t *out, hipStream_t stream) {
+  const int64_t threads = rows * (inter / 8);
+  hipLaunchKernelGGL(swiglu_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream, gu, rows, inter, out);
+  return hipGetLastError();
+}
+
+}  // namespace tx

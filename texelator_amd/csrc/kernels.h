@@ -54,4 +54,18 @@ hipError_t launch_repack(const uint8_t *blocks, int M, int bpr, int RG, int CG, 
 hipError_t launch_decode_dense(const uint4 *tiles, const float *scales, int M, int K, int RG, int CG,
                                uint16_t *out, hipStream_t stream);
 
+// Decoder-layer helpers (decoder.hip).
+hipError_t launch_add_rmsnorm(float *h, const uint16_t *delta, const uint16_t *weight, float eps, uint16_t *out,
+                              int64_t rows, int hidden, hipStream_t stream);
+hipError_t launch_rope_cache(const uint16_t *qkv, int64_t stride, int64_t tokens, const int64_t *positions,
+                             const float *cos_t, const float *sin_t, int heads, int kv_heads, int d, uint16_t *q_out,
+                             uint16_t *k_cache, uint16_t *v_cache, int64_t max_ctx, hipStream_t stream);
+int decode_attention_chunks(int64_t length);
+bool decode_attention_supported(int heads, int kv_heads, int head_dim);
+int64_t decode_attention_max_length();
+hipError_t launch_decode_attention(const uint16_t *q, const uint16_t *k_cache, const uint16_t *v_cache,
+                                   const int64_t *position, int64_t length, int heads, int kv_heads, int64_t max_ctx,
+                                   float scale, float *partials, uint16_t *out, hipStream_t stream);
+hipError_t launch_swiglu(const uint16_t *gu, int64_t rows, int64_t inter, uint16_t *out, hipStream_t stream);
+
 }  // namespace tx

@@ -1,0 +1,112 @@
+"""Decoder-layer helpers of ``libtexelator_hip.so`` on torch tensors (no reference counterpart:
+the reference leaves these layers to Hugging Face modules; see ``include/texelator_hip.h``).
+
+Every function checks shapes, dtypes and devices on the host before the launch, and launches on
+the current stream. Nothing here allocates unless an output is not supplied.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+from ._lib import TexelatorError, check
+
+
+def _ptr(t: torch.Tensor | None) -> ctypes.c_void_p:
+    return ctypes.c_void_p(t.data_ptr() if t is not None else None)
+
+
+def _stream(t: torch.Tensor) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _expect(condition: bool, message: str) -> None:
+    if not condition:
+        raise TexelatorError(message)
+
+
+def add_rmsnorm(residual: torch.Tensor, delta: torch.Tensor | None, weight: torch.Tensor, eps: float,
+                out: torch.Tensor | None = None) -> torch.Tensor:
+    """``residual += delta`` (in place, fp32) then ``out = bf16(weight * bf16(rmsnorm(residual)))``."""
+    _expect(residual.is_cuda and residual.dtype == torch.float32 and residual.is_contiguous() and residual.dim() == 2,
+            "residual must be a contiguous CUDA float32 [rows, hidden]")
+    rows, hidden = residual.shape
+    _expect(weight.dtype == torch.bfloat16 and weight.is_contiguous() and weight.numel() == hidden, "weight must be bf16 [hidden]")
+    if delta is not None:
+        _expect(delta.dtype == torch.bfloat16 and delta.is_contiguous() and delta.shape == residual.shape,
+                "delta must be a contiguous bf16 tensor shaped like the residual")
+    if out is None:
+        out = torch.empty((rows, hidden), dtype=torch.bfloat16, device=residual.device)
+    _expect(out.dtype == torch.bfloat16 and out.is_contiguous() and out.shape == residual.shape, "bad output")
+    check(_lib.load().tx_add_rmsnorm(_ptr(residual), _ptr(delta), _ptr(weight), float(eps), _ptr(out), rows, hidden,
+                                     _stream(residual)))
+    return out
+
+
+def rope_kv_cache(qkv: torch.Tensor, positions: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, heads: int,
+                  kv_heads: int, head_dim: int, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                  q_out: torch.Tensor | None = None) -> torch.Tensor:
+    """RoPE on the q and k heads of packed ``[q | k | v]`` rows; k and v go into the caches at
+    ``positions``; returns the rotated q ``[tokens, heads * head_dim]``."""
+    _expect(qkv.dtype == torch.bfloat16 and qkv.dim() == 2 and qkv.stride(1) == 1, "qkv must be bf16 [tokens, width]")
+    tokens = qkv.shape[0]
+    _expect(qkv.shape[1] >= (heads + 2 * kv_heads) * head_dim, "qkv row too short for the heads")
+    _expect(positions.dtype == torch.int64 and positions.is_contiguous() and positions.numel() == tokens,
+            "positions must be int64 [tokens]")
+    max_ctx = k_cache.shape[1]
+    for cache in (k_cache, v_cache):
+        _expect(cache.dtype == torch.bfloat16 and cache.is_contiguous() and tuple(cache.shape) == (kv_heads, max_ctx, head_dim),
+                "caches must be contiguous bf16 [kv_heads, max_context, head_dim]")
+    for table in (cos, sin):
+        _expect(table.dtype == torch.float32 and table.is_contiguous() and tuple(table.shape) == (max_ctx, head_dim),
+                "rope tables must be float32 [max_context, head_dim]")
+    if q_out is None:
+        q_out = torch.empty((tokens, heads * head_dim), dtype=torch.bfloat16, device=qkv.device)
+    _expect(q_out.dtype == torch.bfloat16 and q_out.is_contiguous() and q_out.numel() == tokens * heads * head_dim, "bad q_out")
+    check(_lib.load().tx_rope_kv_cache(_ptr(qkv), qkv.stride(0), tokens, _ptr(positions), _ptr(cos), _ptr(sin), heads,
+                                       kv_heads, head_dim, _ptr(q_out), _ptr(k_cache), _ptr(v_cache), max_ctx,
+                                       _stream(qkv)))
+    return q_out
+
+
+def decode_attention_supported(config) -> bool:
+    """The fused decode attention handles head_dim 128 and at most 8 query heads per KV head."""
+    return config.head_dim == 128 and config.heads % config.kv_heads == 0 and config.heads // config.kv_heads <= 8
+
+
+def decode_attention_workspace_bytes(heads: int, length: int) -> int:
+    out = ctypes.c_int64(0)
+    check(_lib.load().tx_decode_attention_workspace(int(heads), int(length), ctypes.byref(out)))
+    return int(out.value)
+
+
+def decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, position: torch.Tensor, length: int,
+                     heads: int, kv_heads: int, scale: float, workspace: torch.Tensor,
+                     out: torch.Tensor | None = None) -> torch.Tensor:
+    """One-token grouped-query attention over cache positions 0..position (device int64 [1])."""
+    head_dim = k_cache.shape[2]
+    _expect(q.dtype == torch.bfloat16 and q.is_contiguous() and q.numel() == heads * head_dim, "q must be bf16 [heads*head_dim]")
+    _expect(position.dtype == torch.int64 and position.numel() == 1, "position must be int64 [1]")
+    for cache in (k_cache, v_cache):
+        _expect(cache.dtype == torch.bfloat16 and cache.is_contiguous() and cache.shape[0] == kv_heads, "bad cache")
+    need = decode_attention_workspace_bytes(heads, length)
+    _expect(workspace.is_cuda and workspace.numel() * workspace.element_size() >= need, "decode attention workspace too small")
+    if out is None:
+        out = torch.empty((1, heads * head_dim), dtype=torch.bfloat16, device=q.device)
+    check(_lib.load().tx_decode_attention(_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(position), int(length), heads,
+                                          kv_heads, head_dim, k_cache.shape[1], float(scale), _ptr(workspace),
+                                          workspace.numel() * workspace.element_size(), _ptr(out), _stream(q)))
+    return out
+
+
+def swiglu(gate_up: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """``bf16(silu(g) * u)`` for rows ``[g | u]``."""
+    _expect(gate_up.dtype == torch.bfloat16 and gate_up.is_contiguous() and gate_up.dim() == 2 and gate_up.shape[1] % 2 == 0,
+            "gate_up must be contiguous bf16 [rows, 2 * intermediate]")
+    rows, width = gate_up.shape
+    if out is None:
+        out = torch.empty((rows, width // 2), dtype=torch.bfloat16, device=gate_up.device)
+    check(_lib.load().tx_swiglu(_ptr(gate_up), rows, width // 2, _ptr(out), _stream(gate_up)))
+    return out

@@ -26,6 +26,7 @@ from dataclasses import dataclass
 import torch
 from torch.nn import functional
 
+from . import layers
 from .runtime import TexelatorLinear, extension, free
 
 
@@ -56,7 +57,7 @@ class DecoderConfig:
 
     @staticmethod
     def tiny() -> "DecoderConfig":
-        return DecoderConfig(layers=2, hidden=256, heads=4, kv_heads=2, head_dim=64, intermediate=512, vocab=512)
+        return DecoderConfig(layers=2, hidden=256, heads=4, kv_heads=2, head_dim=128, intermediate=512, vocab=512)
 
     def linear_shapes(self) -> list[tuple[str, int, int]]:
         """(name, M = out features, K = in features) of one layer's seven linears."""
@@ -89,19 +90,36 @@ def init_std(config: "DecoderConfig", name: str, depth_scaled: bool) -> float:
     return 0.02
 
 
+# Merged handles of a layer: rows of q, k, v (one launch) and of gate, up (one launch).
+MERGED = {
+    "qkv": ("self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj"),
+    "o": ("self_attn.o_proj",),
+    "gate_up": ("mlp.gate_proj", "mlp.up_proj"),
+    "down": ("mlp.down_proj",),
+}
+
+
 class _Layer:
     def __init__(self):
-        self.linears: dict[str, TexelatorLinear] = {}
-        self.biases: dict[str, torch.Tensor] = {}
+        self.linears: dict[str, TexelatorLinear] = {}     # keys of MERGED
+        self.rows: dict[str, tuple[int, int]] = {}         # reference linear name -> (first row, rows)
+        self.biases: dict[str, torch.Tensor] = {}          # merged key -> bias
         self.input_norm: torch.Tensor | None = None
         self.post_norm: torch.Tensor | None = None
 
 
 class BC4Decoder:
-    """Decoder with BC4 linears, a static KV cache and graph-captured decode steps."""
+    """Decoder with BC4 linears, a static KV cache and graph-captured decode steps.
+
+    The seven linears of a layer are packed as four handles: q|k|v and gate|up are merged along
+    the output rows (one launch each), o and down stay single. With ``fused`` (the default) the
+    layer glue runs as this library's kernels (``texelator_amd.layers``): add+RMSNorm, RoPE+KV
+    write, split-length decode attention and SwiGLU. Without it, the same math runs as plain
+    PyTorch ops (the cross-check path)."""
 
     def __init__(self, config: DecoderConfig, max_context: int, device: torch.device | str = "cuda", seed: int = 0,
-                 lookahead: int = 1, linear_source=None, depth_scaled: bool = True, embed_std: float = 1.0):
+                 lookahead: int = 1, linear_source=None, depth_scaled: bool = True, embed_std: float = 1.0,
+                 fused: bool = True):
         """``linear_source(layer, name, m, k)`` may return ``(blocks, scales)`` device tensors for a
         linear (reference block layout). By default every linear is a seeded random BC4 matrix.
 
@@ -117,8 +135,11 @@ class BC4Decoder:
         self.config = config
         self.device = torch.device(device)
         self.max_context = int(max_context)
+        self.fused = fused
         ext = extension()
         c = config
+        if fused and not layers.decode_attention_supported(c):
+            raise ValueError("the fused decode attention needs head_dim 128 and at most 8 query heads per KV head")
         g = torch.Generator(device=self.device).manual_seed(seed)
         bf16 = torch.bfloat16
 
@@ -130,38 +151,50 @@ class BC4Decoder:
         self.final_norm = torch.ones(c.hidden, device=self.device, dtype=bf16)
         self.handles: list[int] = []
         self.layers: list[_Layer] = []
+        shapes = {name: (m, k) for name, m, k in c.linear_shapes()}
         try:
             for index in range(c.layers):
                 layer = _Layer()
                 layer.input_norm = torch.ones(c.hidden, device=self.device, dtype=bf16)
                 layer.post_norm = torch.ones(c.hidden, device=self.device, dtype=bf16)
-                for name, m, k in c.linear_shapes():
-                    source = linear_source(index, name, m, k) if linear_source else None
-                    blocks, scales = source if source is not None else random_bc4(
-                        m, k, g, self.device, init_std(c, name, depth_scaled))
-                    bias = (torch.zeros(m, device=self.device, dtype=bf16)
-                            if c.qkv_bias and name in ("self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj")
-                            else None)
-                    handle = ext.pack_encoded_device(blocks, scales, bias)
-                    if bias is not None:
-                        layer.biases[name] = bias
+                for key, names in MERGED.items():
+                    parts_blocks, parts_scales, row = [], [], 0
+                    for name in names:
+                        m, k = shapes[name]
+                        source = linear_source(index, name, m, k) if linear_source else None
+                        blocks, scales = source if source is not None else random_bc4(
+                            m, k, g, self.device, init_std(c, name, depth_scaled))
+                        parts_blocks.append(blocks.reshape(-1))
+                        parts_scales.append(scales.reshape(-1).float())
+                        layer.rows[name] = (row, m)
+                        row += m
+                    blocks = torch.cat(parts_blocks) if len(parts_blocks) > 1 else parts_blocks[0]
+                    scales = torch.cat(parts_scales) if len(parts_scales) > 1 else parts_scales[0]
+                    bias = torch.zeros(row, device=self.device, dtype=bf16) if (c.qkv_bias and key == "qkv") else None
+                    handle = ext.pack_encoded_device(blocks.contiguous(), scales.contiguous(), bias)
                     self.handles.append(handle)
                     ext.set_lookahead(handle, lookahead)
-                    layer.linears[name] = TexelatorLinear([handle])
-                    del blocks, scales
+                    layer.linears[key] = TexelatorLinear([handle])
+                    if bias is not None:
+                        layer.biases[key] = bias
+                    del blocks, scales, parts_blocks, parts_scales
                 self.layers.append(layer)
         except Exception:
             free(self.handles)
             raise
-        # K cache [layer, kv_head, position, head_dim]; V cache transposed [layer, kv_head, head_dim, position]
-        self.k_cache = torch.zeros((c.layers, c.kv_heads, self.max_context, c.head_dim), device=self.device, dtype=bf16)
-        self.v_cache = torch.zeros((c.layers, c.kv_heads, c.head_dim, self.max_context), device=self.device, dtype=bf16)
+        # K and V caches [layer, kv_head, position, head_dim]
+        shape = (c.layers, c.kv_heads, self.max_context, c.head_dim)
+        self.k_cache = torch.zeros(shape, device=self.device, dtype=bf16)
+        self.v_cache = torch.zeros(shape, device=self.device, dtype=bf16)
         inv_freq = 1.0 / (c.rope_theta ** (torch.arange(0, c.head_dim, 2, device=self.device, dtype=torch.float32)
                                            / c.head_dim))
         angles = torch.arange(self.max_context, device=self.device, dtype=torch.float32)[:, None] * inv_freq[None, :]
         angles = torch.cat([angles, angles], dim=-1)
-        self.rope_cos, self.rope_sin = angles.cos(), angles.sin()
+        self.rope_cos, self.rope_sin = angles.cos().contiguous(), angles.sin().contiguous()
         self.key_positions = torch.arange(self.max_context, device=self.device)
+        self.attention_workspace = torch.empty(
+            layers.decode_attention_workspace_bytes(c.heads, self.max_context) if fused else 16,
+            dtype=torch.uint8, device=self.device)
         # decode-step state (static buffers read and advanced by the captured graphs)
         self.token = torch.zeros(1, dtype=torch.long, device=self.device)
         self.position = torch.zeros(1, dtype=torch.long, device=self.device)
@@ -179,6 +212,13 @@ class BC4Decoder:
         for handle in self.handles:
             ext.set_prefill_backend(handle, backend)
 
+    def dense_weight(self, index: int, name: str) -> torch.Tensor:
+        """Decoded bf16 weight ``[M, K]`` of one reference linear (for checks)."""
+        layer = self.layers[index]
+        key = next(k for k, names in MERGED.items() if name in names)
+        first, rows = layer.rows[name]
+        return extension().decode_dense(layer.linears[key].handles[0])[first:first + rows]
+
     def _rms_norm(self, x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
         """RMSNorm of the fp32 residual stream, returned as the bf16 input of the next linears."""
         xf = x.float()
@@ -194,51 +234,69 @@ class BC4Decoder:
         rotated = torch.cat([-xf[..., half:], xf[..., :half]], dim=-1)
         return (xf * cos + rotated * sin).to(torch.bfloat16)
 
-    def _attention(self, index: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, positions: torch.Tensor,
-                   length: int) -> torch.Tensor:
-        """q [T, heads, d], k/v [T, kv, d] at ``positions``; attends keys 0..length-1 causally.
+    def _cached_attention(self, index: int, q: torch.Tensor, positions: torch.Tensor, length: int) -> torch.Tensor:
+        """q [T, heads, d] at ``positions`` over cache positions 0..length-1, causally.
 
-        Keys are cached as rows ([kv, position, d]) and values transposed ([kv, d, position]), so
-        scores^T = K q^T and out^T = V^T P^T are batched products whose right operands are
-        contiguous and whose left operands are row-strided cache slices."""
+        scores^T = K q^T and out = P V are batched products whose right operands are
+        contiguous or row-strided cache slices (never transposed views); scores and softmax in fp32."""
         c = self.config
         tokens = q.shape[0]
         group = c.heads // c.kv_heads
-        self.k_cache[index].index_copy_(1, positions, k.transpose(0, 1))
-        self.v_cache[index].index_copy_(2, positions, v.permute(1, 2, 0))
         keys = self.k_cache[index, :, :length]                      # [kv, L, d]
-        values_t = self.v_cache[index, :, :, :length]               # [kv, d, L]
-        # queries as [kv, d, group * T] (column = g * T + t), contiguous
-        qt = q.view(tokens, c.kv_heads, group, c.head_dim).permute(1, 3, 2, 0).reshape(
-            c.kv_heads, c.head_dim, group * tokens).contiguous()
-        # scores accumulate and stay in fp32 (as flash attention keeps them), never rounded to bf16
+        values = self.v_cache[index, :, :length]                    # [kv, L, d]
+        qt = q.reshape(tokens, c.kv_heads, group, c.head_dim).permute(1, 3, 2, 0).reshape(
+            c.kv_heads, c.head_dim, group * tokens).contiguous()   # column = g * T + t
         scores = torch.bmm(keys, qt, out_dtype=torch.float32) * (1.0 / math.sqrt(c.head_dim))   # [kv, L, G*T]
         future = self.key_positions[:length, None] > positions.repeat(group)[None, :]
-        scores = scores.masked_fill(future, float("-inf"))
-        probs = torch.softmax(scores, dim=1).to(torch.bfloat16)     # [kv, L, G*T], contiguous
-        out_t = torch.bmm(values_t, probs)                          # [kv, d, G*T]
-        return out_t.view(c.kv_heads, c.head_dim, group, tokens).permute(3, 0, 2, 1).reshape(
-            tokens, c.heads * c.head_dim)
+        probs = torch.softmax(scores.masked_fill(future, float("-inf")), dim=1)
+        probs = probs.to(torch.bfloat16).transpose(1, 2).contiguous()              # [kv, G*T, L]
+        out = torch.bmm(probs, values)                                             # [kv, G*T, d]
+        return out.view(c.kv_heads, group, tokens, c.head_dim).permute(2, 0, 1, 3).reshape(tokens, c.heads * c.head_dim)
+
+    def _layer_torch(self, index: int, layer: _Layer, h: torch.Tensor, positions: torch.Tensor, length: int) -> torch.Tensor:
+        c = self.config
+        q_rows, kv_rows = c.heads * c.head_dim, c.kv_heads * c.head_dim
+        x = self._rms_norm(h, layer.input_norm)
+        qkv = layer.linears["qkv"](x)
+        q = self._rope(qkv[:, :q_rows].reshape(-1, c.heads, c.head_dim), positions)
+        k = self._rope(qkv[:, q_rows:q_rows + kv_rows].reshape(-1, c.kv_heads, c.head_dim), positions)
+        v = qkv[:, q_rows + kv_rows:].reshape(-1, c.kv_heads, c.head_dim)
+        self.k_cache[index].index_copy_(1, positions, k.transpose(0, 1))
+        self.v_cache[index].index_copy_(1, positions, v.transpose(0, 1))
+        h = h + layer.linears["o"](self._cached_attention(index, q, positions, length)).float()
+        x = self._rms_norm(h, layer.post_norm)
+        gu = layer.linears["gate_up"](x).float()
+        act = functional.silu(gu[:, :c.intermediate]) * gu[:, c.intermediate:]
+        return h + layer.linears["down"](act.to(torch.bfloat16)).float()
 
     def hidden_states(self, ids: torch.Tensor, positions: torch.Tensor, length: int) -> torch.Tensor:
         """Final-norm hidden states [T, hidden] (bf16) for tokens ``ids`` at ``positions``.
 
-        The residual stream is kept in fp32 and the SwiGLU product is formed in fp32; every
-        linear reads bf16 activations and writes bf16 outputs."""
+        The residual stream is kept in fp32; every linear reads bf16 activations and writes bf16
+        outputs. A single token uses the split-length decode attention (fused path)."""
         c = self.config
         h = self.embed.index_select(0, ids).float()
+        if not self.fused:
+            for index, layer in enumerate(self.layers):
+                h = self._layer_torch(index, layer, h, positions, length)
+            return self._rms_norm(h, self.final_norm)
+        tokens = ids.numel()
+        scale = 1.0 / math.sqrt(c.head_dim)
+        x = layers.add_rmsnorm(h, None, self.layers[0].input_norm, c.rms_eps)
         for index, layer in enumerate(self.layers):
-            x = self._rms_norm(h, layer.input_norm)
-            lin = layer.linears
-            q = lin["self_attn.q_proj"](x).view(-1, c.heads, c.head_dim)
-            k = lin["self_attn.k_proj"](x).view(-1, c.kv_heads, c.head_dim)
-            v = lin["self_attn.v_proj"](x).view(-1, c.kv_heads, c.head_dim)
-            q, k = self._rope(q, positions), self._rope(k, positions)
-            h = h + lin["self_attn.o_proj"](self._attention(index, q, k, v, positions, length)).float()
-            x = self._rms_norm(h, layer.post_norm)
-            act = functional.silu(lin["mlp.gate_proj"](x).float()) * lin["mlp.up_proj"](x).float()
-            h = h + lin["mlp.down_proj"](act.to(torch.bfloat16)).float()
-        return self._rms_norm(h, self.final_norm)
+            qkv = layer.linears["qkv"](x)
+            q = layers.rope_kv_cache(qkv, positions, self.rope_cos, self.rope_sin, c.heads, c.kv_heads, c.head_dim,
+                                     self.k_cache[index], self.v_cache[index])
+            if tokens == 1:
+                attn = layers.decode_attention(q, self.k_cache[index], self.v_cache[index], positions, length, c.heads,
+                                               c.kv_heads, scale, self.attention_workspace)
+            else:
+                attn = self._cached_attention(index, q.view(tokens, c.heads, c.head_dim), positions, length)
+            layers.add_rmsnorm(h, layer.linears["o"](attn), layer.post_norm, c.rms_eps, out=x)
+            act = layers.swiglu(layer.linears["gate_up"](x))
+            following = self.layers[index + 1].input_norm if index + 1 < len(self.layers) else self.final_norm
+            layers.add_rmsnorm(h, layer.linears["down"](act), following, c.rms_eps, out=x)
+        return x
 
     def logits(self, hidden: torch.Tensor) -> torch.Tensor:
         return functional.linear(hidden, self.lm_head)
