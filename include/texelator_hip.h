@@ -144,6 +144,24 @@ int tx_decode_attention(const void *q, const void *k_cache, const void *v_cache,
 /* out[r][c] = bf16(silu(g) * u) for gate_up rows [g (intermediate) | u (intermediate)], fp32 math. */
 int tx_swiglu(const void *gate_up, int64_t rows, int64_t intermediate, void *out, void *stream);
 
+/* ---- Fused single-token decode (no reference counterpart; same role as the helpers above) ----
+ * tx_linear_split runs a handle's one-token decode GEMV (x bf16 [K]) but leaves its output as
+ * the fp32 split-K partials in the handle's own buffer; the *_split consumers below read them,
+ * sum them in split order, add the (BF16) bias and round to bf16 exactly as tx_linear would, and
+ * then do their own work. A split consumer must run on the same stream after the
+ * tx_linear_split of its handle and before the next one. Outputs are bit-identical to
+ * tx_linear followed by the plain helper. */
+int tx_linear_split(uint64_t handle, const void *x, void *stream);
+
+/* tx_add_rmsnorm for one row whose delta is the output of delta_handle (M == hidden). */
+int tx_add_rmsnorm_split(float *residual, uint64_t delta_handle, const void *weight, float eps, void *out,
+                         int64_t hidden, void *stream);
+
+/* tx_rope_kv_cache for one token whose [q | k | v] row is the output of qkv_handle. */
+int tx_rope_kv_cache_split(uint64_t qkv_handle, const int64_t *positions, const float *cos_table,
+                           const float *sin_table, int heads, int kv_heads, int head_dim, void *q_out,
+                           void *k_cache, void *v_cache, int64_t max_context, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

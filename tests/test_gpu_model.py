@@ -194,3 +194,67 @@ def test_swiglu_kernel(ext):
     f = gu.float()
     want = (functional.silu(f[:, :1024]) * f[:, 1024:]).to(torch.bfloat16).float()
     assert rrms(want, got) < 4e-3
+
+
+def _random_handle(ext, m, k, seed, bias=False):
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    blocks = torch.randint(0, 256, (m * k // 2,), device="cuda", dtype=torch.uint8, generator=g)
+    scales = 0.02 * torch.exp(0.3 * torch.randn(m, device="cuda", generator=g))
+    b = (0.1 * torch.randn(m, device="cuda", generator=g)).to(torch.bfloat16) if bias else None
+    return ext.pack_encoded_device(blocks, scales.float(), b)
+
+
+@pytest.mark.parametrize("m,k,bias", [(5120, 5120, False), (5120, 5120, True), (16384, 256, True), (256, 512, False)])
+def test_add_rmsnorm_split_is_bit_identical(ext, m, k, bias):
+    """linear_split + add_rmsnorm_split == linear + add_rmsnorm, bit for bit (k splits 5, 1, 1)."""
+    handle = _random_handle(ext, m, k, seed=m + k, bias=bias)
+    try:
+        g = torch.Generator(device="cuda").manual_seed(11)
+        x = torch.randn(1, k, device="cuda", generator=g).to(torch.bfloat16)
+        w = (1 + 0.1 * torch.randn(m, device="cuda", generator=g)).to(torch.bfloat16)
+        h0 = torch.randn(1, m, device="cuda", generator=g)
+        h1, h2 = h0.clone(), h0.clone()
+        want = layers.add_rmsnorm(h1, ext.linear(handle, x), w, 1e-6)
+        layers.linear_split(handle, x)
+        got = layers.add_rmsnorm_split(h2, handle, w, 1e-6, out=torch.empty_like(want))
+        assert torch.equal(h1, h2)
+        assert torch.equal(want, got)
+    finally:
+        ext.free(handle)
+
+
+@pytest.mark.parametrize("heads,kv,k,bias", [(40, 8, 5120, True), (4, 2, 256, False)])
+def test_rope_kv_cache_split_is_bit_identical(ext, heads, kv, k, bias):
+    d, ctx = 128, 1024
+    handle = _random_handle(ext, (heads + 2 * kv) * d, k, seed=heads, bias=bias)
+    try:
+        g = torch.Generator(device="cuda").manual_seed(13)
+        x = torch.randn(1, k, device="cuda", generator=g).to(torch.bfloat16)
+        angles = torch.rand(ctx, d, device="cuda", generator=g) * 6
+        cos, sin = angles.cos().contiguous(), angles.sin().contiguous()
+        pos = torch.tensor([517], device="cuda")
+        caches = [torch.zeros(kv, ctx, d, device="cuda", dtype=torch.bfloat16) for _ in range(4)]
+        want = layers.rope_kv_cache(ext.linear(handle, x), pos, cos, sin, heads, kv, d, caches[0], caches[1])
+        layers.linear_split(handle, x)
+        got = layers.rope_kv_cache_split(handle, pos, cos, sin, heads, kv, d, caches[2], caches[3],
+                                         torch.empty(heads * d, device="cuda", dtype=torch.bfloat16))
+        assert torch.equal(want.view(-1), got)
+        assert torch.equal(caches[0], caches[2]) and torch.equal(caches[1], caches[3])
+    finally:
+        ext.free(handle)
+
+
+def test_split_decode_step_is_bit_identical(ext, tiny):
+    """A decode step through the split-K consumers equals the unsplit fused step, bit for bit."""
+    ids = prefill.prompt_ids(tiny, 30, seed=6)
+    with torch.inference_mode():
+        tiny.prefill(ids)
+        token = ids[-1:]
+        tiny.split_decode = False
+        a = tiny.hidden_states(token, tiny.key_positions[30:31], 512).clone()
+        ka = tiny.k_cache[:, :, 30].clone()
+        tiny.split_decode = True
+        b = tiny.hidden_states(token, tiny.key_positions[30:31], 512)
+        kb = tiny.k_cache[:, :, 30].clone()
+    assert torch.equal(a, b)
+    assert torch.equal(ka, kb)

@@ -13,6 +13,7 @@
 
 #include "../../include/texelator_hip.h"
 #include "bc4_device.h"
+#include "elementwise.h"
 #include "kernels.h"
 
 namespace {
@@ -46,7 +47,7 @@ constexpr uint32_t kHandleMagic = 0x54584834u;  // "TXH4"
 struct Handle {
   uint32_t magic = kHandleMagic;
   int M = 0, K = 0, bpr = 0, Mp = 0, bp = 0, RG = 0, CG = 0, device = 0;
-  int lookahead = 2;
+  int lookahead = 1;
   int prefill_threshold = 16, prefill_tile_rows = 1024, prefill_backend = 0;
   int gemv_splits = 1;
   int cus = 256;
@@ -147,6 +148,11 @@ int run_prefill(Handle *h, int candidate, const void *x, int64_t tokens, void *y
   return TX_OK;
 }
 
+// The single-token split-K partials a handle's last tx_linear_split wrote.
+tx::SplitSource split_source(const Handle *h) {
+  return tx::SplitSource{h->partials, static_cast<const uint16_t *>(h->bias), h->gemv_splits, h->Mp, 1};
+}
+
 int run_gemv(Handle *h, const void *x, int64_t tokens, void *y, bool f32_out, hipStream_t stream) {
   if (tokens > 65535) return fail(TX_ERR_INVALID, "token grid exceeds the HIP grid.z limit");
   tx::GemvParams p{};
@@ -165,6 +171,24 @@ int run_gemv(Handle *h, const void *x, int64_t tokens, void *y, bool f32_out, hi
   p.ks = tokens == 1 ? h->gemv_splits : 1;
   p.partials = h->partials;
   TX_HIP(tx::launch_gemv(p, h->lookahead, f32_out, stream));
+  return TX_OK;
+}
+
+int run_gemv_split(Handle *h, const void *x, hipStream_t stream) {
+  tx::GemvParams p{};
+  p.tiles = h->tiles;
+  p.scales = h->scales;
+  p.x = x;
+  p.M = h->M;
+  p.K = h->K;
+  p.Mp = h->Mp;
+  p.RG = h->RG;
+  p.CG = h->CG;
+  p.tokens = 1;
+  p.ks = h->gemv_splits;
+  p.partials = h->partials;
+  p.force_partials = 1;
+  TX_HIP(tx::launch_gemv(p, h->lookahead, true, stream));
   return TX_OK;
 }
 
@@ -228,9 +252,8 @@ int pack_common(const uint8_t *blocks, int64_t blocks_bytes, const float *scales
     if ((e = hipMemcpy(h->bias, bias, (size_t)h->M * 2, hipMemcpyDeviceToDevice)) != hipSuccess) return cleanup(e);
     h->bias_dtype = bias_dtype;
   }
-  if (h->gemv_splits > 1) {
-    if ((e = hipMalloc(&h->partials, (size_t)h->gemv_splits * h->Mp * sizeof(float))) != hipSuccess) return cleanup(e);
-  }
+  // Split-K partials of single-token calls; also the output of tx_linear_split when ks == 1.
+  if ((e = hipMalloc(&h->partials, (size_t)h->gemv_splits * h->Mp * sizeof(float))) != hipSuccess) return cleanup(e);
   if ((e = hipDeviceSynchronize()) != hipSuccess) return cleanup(e);
   *handle_out = reinterpret_cast<uint64_t>(h);
   return TX_OK;
@@ -414,6 +437,51 @@ int tx_add_rmsnorm(float *residual, const void *delta, const void *weight, float
   if (rows == 0) return TX_OK;
   TX_HIP(tx::launch_add_rmsnorm(residual, static_cast<const uint16_t *>(delta), static_cast<const uint16_t *>(weight),
                                 eps, static_cast<uint16_t *>(out), rows, (int)hidden, reinterpret_cast<hipStream_t>(stream)));
+  return TX_OK;
+}
+
+int tx_linear_split(uint64_t value, const void *x, void *stream) {
+  g_last_error.clear();
+  Handle *h = as_handle(value);
+  if (!h) return fail(TX_ERR_INVALID, "null Texelator handle");
+  if (!x) return fail(TX_ERR_INVALID, "null input pointer");
+  if (reinterpret_cast<uintptr_t>(x) % 16 != 0) return fail(TX_ERR_INVALID, "input must be 16-byte aligned");
+  if (h->bias && h->bias_dtype != TX_DTYPE_BF16) return fail(TX_ERR_INVALID, "linear_split: the bias must be BF16");
+  DeviceGuard guard(h->device);
+  return run_gemv_split(h, x, reinterpret_cast<hipStream_t>(stream));
+}
+
+int tx_add_rmsnorm_split(float *residual, uint64_t delta_handle, const void *weight, float eps, void *out, int64_t hidden,
+                         void *stream) {
+  g_last_error.clear();
+  Handle *h = as_handle(delta_handle);
+  if (!h) return fail(TX_ERR_INVALID, "null Texelator handle");
+  if (!residual || !weight || !out || hidden <= 0 || hidden > (1 << 24) || hidden % 4)
+    return fail(TX_ERR_INVALID, "add_rmsnorm_split: invalid arguments (hidden must be a positive multiple of 4)");
+  if (h->M != hidden) return fail(TX_ERR_INVALID, "add_rmsnorm_split: the handle's output size must equal hidden");
+  if (h->bias && h->bias_dtype != TX_DTYPE_BF16) return fail(TX_ERR_INVALID, "add_rmsnorm_split: the bias must be BF16");
+  DeviceGuard guard(h->device);
+  TX_HIP(tx::launch_add_rmsnorm_split(residual, split_source(h), static_cast<const uint16_t *>(weight), eps,
+                                      static_cast<uint16_t *>(out), 1, (int)hidden, reinterpret_cast<hipStream_t>(stream)));
+  return TX_OK;
+}
+
+int tx_rope_kv_cache_split(uint64_t qkv_handle, const int64_t *positions, const float *cos_table, const float *sin_table,
+                           int heads, int kv_heads, int head_dim, void *q_out, void *k_cache, void *v_cache,
+                           int64_t max_context, void *stream) {
+  g_last_error.clear();
+  Handle *h = as_handle(qkv_handle);
+  if (!h) return fail(TX_ERR_INVALID, "null Texelator handle");
+  if (!positions || !cos_table || !sin_table || !q_out || !k_cache || !v_cache)
+    return fail(TX_ERR_INVALID, "rope_kv_cache_split: null pointer");
+  if (heads <= 0 || kv_heads <= 0 || head_dim <= 0 || head_dim % 2 || head_dim > 1024 || max_context <= 0 ||
+      (int64_t)h->M < (int64_t)(heads + 2 * kv_heads) * head_dim)
+    return fail(TX_ERR_INVALID, "rope_kv_cache_split: invalid shape");
+  if (h->bias && h->bias_dtype != TX_DTYPE_BF16) return fail(TX_ERR_INVALID, "rope_kv_cache_split: the bias must be BF16");
+  DeviceGuard guard(h->device);
+  TX_HIP(tx::launch_rope_cache_split(split_source(h), 1, positions, cos_table, sin_table, heads, kv_heads, head_dim,
+                                     static_cast<uint16_t *>(q_out), static_cast<uint16_t *>(k_cache),
+                                     static_cast<uint16_t *>(v_cache), max_context, reinterpret_cast<hipStream_t>(stream)));
   return TX_OK;
 }
 

@@ -9,44 +9,79 @@
 // bf16 [kv_head][position][head_dim].
 #include <math.h>
 
+#include "elementwise.h"
 #include "kernels.h"
 
 namespace tx {
 
 namespace {
 
-__device__ __forceinline__ float bf(uint16_t v) { return __builtin_bit_cast(float, (uint32_t)v << 16); }
-
-__device__ __forceinline__ uint16_t to_bf(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
-
 // h[row] += delta[row] (if given); out[row] = bf16(weight * bf16(h * rsqrt(mean(h^2) + eps))).
-// One block per row; each thread owns groups of 4 columns (4 * t + 1024 * i), all of whose loads
-// are issued before the reduction. hidden must be a multiple of 4.
-__global__ __launch_bounds__(256) void add_rmsnorm_kernel(float *h, const uint16_t *delta, const uint16_t *weight,
-                                                          float eps, uint16_t *out, int hidden) {
-  constexpr int kUnroll = 8;  // register-resident groups per thread (covers hidden <= 8192)
-  __shared__ float partial[4];
+// One block per row; each thread owns groups of 4 columns (4 * t + 4096 * i), all of whose
+// loads are issued before the reduction. hidden must be a multiple of 4.
+// With SPLIT, delta is the fp32 split-K partials of a decode GEMV: each group's partials are read
+// as float4 per split (all groups of a split in flight together) and summed in split order plus
+// the bias, exactly as split_sum does. Both variants reduce in the same order, so their outputs
+// are bit-identical; a row gets 1024 threads (a decode step has a single row).
+constexpr int kNormThreads = 1024;
+
+template <bool SPLIT>
+__global__ __launch_bounds__(kNormThreads) void add_rmsnorm_kernel(float *h, const uint16_t *delta, SplitSource split,
+                                                                   const uint16_t *weight, float eps, uint16_t *out,
+                                                                   int hidden) {
+  constexpr int kThreads = kNormThreads;
+  constexpr int kUnroll = 2;  // register-resident groups per thread per pass (covers 8192 columns)
+  __shared__ float partial[kThreads / 64];
   float4 *hr = reinterpret_cast<float4 *>(h + (size_t)blockIdx.x * hidden);
-  const uint2 *dr = delta ? reinterpret_cast<const uint2 *>(delta + (size_t)blockIdx.x * hidden) : nullptr;
+  const uint2 *dr = !SPLIT && delta ? reinterpret_cast<const uint2 *>(delta + (size_t)blockIdx.x * hidden) : nullptr;
   uint2 *orow = reinterpret_cast<uint2 *>(out + (size_t)blockIdx.x * hidden);
   const uint2 *wr = reinterpret_cast<const uint2 *>(weight);
   const int groups = hidden / 4;
   float ss = 0.f;
-  for (int base = 0; base < groups; base += 256 * kUnroll) {
+  for (int base = 0; base < groups; base += kThreads * kUnroll) {
     // load phase: every load of this pass in flight at once (indices clamped, then masked)
     float4 v[kUnroll];
     uint2 d[kUnroll];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
-      const int i = min(base + u * 256 + (int)threadIdx.x, groups - 1);
+      const int i = min(base + u * kThreads + (int)threadIdx.x, groups - 1);
       v[u] = hr[i];
-      if (dr) d[u] = dr[i];
+      if (!SPLIT && dr) d[u] = dr[i];
+    }
+    if constexpr (SPLIT) {
+      const float4 *pp = reinterpret_cast<const float4 *>(split.partials + (size_t)blockIdx.x * split.Mp);
+      const size_t step = (size_t)split.tokens * split.Mp / 4;
+      float4 acc[kUnroll];
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) acc[u] = pp[min(base + u * kThreads + (int)threadIdx.x, groups - 1)];
+      for (int k = 1; k < split.ks; ++k) {
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+          const float4 q = pp[k * step + min(base + u * kThreads + (int)threadIdx.x, groups - 1)];
+          acc[u].x += q.x;
+          acc[u].y += q.y;
+          acc[u].z += q.z;
+          acc[u].w += q.w;
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        if (split.bias) {
+          const uint2 b = reinterpret_cast<const uint2 *>(split.bias)[min(base + u * kThreads + (int)threadIdx.x, groups - 1)];
+          acc[u].x += bf((uint16_t)(b.x & 0xFFFFu));
+          acc[u].y += bf((uint16_t)(b.x >> 16));
+          acc[u].z += bf((uint16_t)(b.y & 0xFFFFu));
+          acc[u].w += bf((uint16_t)(b.y >> 16));
+        }
+        d[u].x = (uint32_t)to_bf(acc[u].x) | ((uint32_t)to_bf(acc[u].y) << 16);
+        d[u].y = (uint32_t)to_bf(acc[u].z) | ((uint32_t)to_bf(acc[u].w) << 16);
+      }
     }
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
-      const int i = base + u * 256 + (int)threadIdx.x;
+      const int i = base + u * kThreads + (int)threadIdx.x;
       if (i >= groups) continue;
-      if (dr) {
+      if (SPLIT || dr) {
         v[u].x += bf((uint16_t)(d[u].x & 0xFFFFu));
         v[u].y += bf((uint16_t)(d[u].x >> 16));
         v[u].z += bf((uint16_t)(d[u].y & 0xFFFFu));
@@ -60,9 +95,11 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(float *h, const uint16
   for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
   if ((threadIdx.x & 63) == 0) partial[threadIdx.x >> 6] = ss;
   __syncthreads();
-  ss = (partial[0] + partial[1]) + (partial[2] + partial[3]);
-  const float inv = rsqrtf(ss / (float)hidden + eps);
-  for (int i = threadIdx.x; i < groups; i += 256) {
+  float total = 0.f;
+#pragma unroll
+  for (int w = 0; w < kThreads / 64; ++w) total += partial[w];
+  const float inv = rsqrtf(total / (float)hidden + eps);
+  for (int i = threadIdx.x; i < groups; i += kThreads) {
     const float4 v = hr[i];
     const uint2 w = wr[i];
     const float n0 = bf(to_bf(v.x * inv)), n1 = bf(to_bf(v.y * inv)), n2 = bf(to_bf(v.z * inv)), n3 = bf(to_bf(v.w * inv));
@@ -74,18 +111,20 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(float *h, const uint16
 
 // One block per (token, head); thread j rotates the pair (j, j + d/2) of rotate-half RoPE.
 // q heads are written to q_out; k heads are rotated into the K cache; v heads are copied.
-__global__ void rope_cache_kernel(const uint16_t *qkv, int64_t stride, const int64_t *positions, const float *cos_t,
-                                  const float *sin_t, int heads, int kv_heads, int d, uint16_t *q_out, uint16_t *k_cache,
-                                  uint16_t *v_cache, int64_t max_ctx) {
+// With SPLIT, the [q | k | v] row is the fp32 split-K partials of the qkv decode GEMV.
+template <bool SPLIT>
+__global__ void rope_cache_kernel(const uint16_t *qkv, SplitSource split, int64_t stride, const int64_t *positions,
+                                  const float *cos_t, const float *sin_t, int heads, int kv_heads, int d, uint16_t *q_out,
+                                  uint16_t *k_cache, uint16_t *v_cache, int64_t max_ctx) {
   const int t = blockIdx.x;
   const int head = blockIdx.y;
   const int j = threadIdx.x;
   const int half = d / 2;
   const int64_t pos = positions[t];
   const uint16_t *row = qkv + (size_t)t * stride;
+  auto value = [&](int64_t col) { return SPLIT ? split_value(split, t, col) : bf(row[col]); };
   if (head < heads + kv_heads) {
-    const uint16_t *src = row + (size_t)head * d;
-    const float x1 = bf(src[j]), x2 = bf(src[j + half]);
+    const float x1 = value((int64_t)head * d + j), x2 = value((int64_t)head * d + j + half);
     const float c1 = cos_t[pos * d + j], c2 = cos_t[pos * d + j + half];
     const float s1 = sin_t[pos * d + j], s2 = sin_t[pos * d + j + half];
     const uint16_t o1 = to_bf(x1 * c1 - x2 * s1);
@@ -96,10 +135,10 @@ __global__ void rope_cache_kernel(const uint16_t *qkv, int64_t stride, const int
     dst[j + half] = o2;
   } else {
     const int kv = head - heads - kv_heads;
-    const uint16_t *src = row + (size_t)(heads + kv_heads + kv) * d;
+    const int64_t col = (int64_t)(heads + kv_heads + kv) * d;
     uint16_t *dst = v_cache + ((size_t)kv * max_ctx + pos) * d;
-    dst[j] = src[j];
-    dst[j + half] = src[j + half];
+    dst[j] = to_bf(value(col + j));
+    dst[j + half] = to_bf(value(col + j + half));
   }
 }
 
@@ -295,32 +334,38 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const uint16_t *gu, int64_t
   const int64_t r = idx / groups, c = (idx % groups) * 8;
   const uint4 gv = *reinterpret_cast<const uint4 *>(gu + r * 2 * inter + c);
   const uint4 uv = *reinterpret_cast<const uint4 *>(gu + r * 2 * inter + inter + c);
-  const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w}, uw[4] = {uv.x, uv.y, uv.z, uv.w};
-  uint32_t ow[4];
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const float g0 = bf((uint16_t)(gw[e] & 0xFFFFu)), g1 = bf((uint16_t)(gw[e] >> 16));
-    const float u0 = bf((uint16_t)(uw[e] & 0xFFFFu)), u1 = bf((uint16_t)(uw[e] >> 16));
-    const float a0 = g0 / (1.0f + expf(-g0)) * u0;
-    const float a1 = g1 / (1.0f + expf(-g1)) * u1;
-    ow[e] = (uint32_t)to_bf(a0) | ((uint32_t)to_bf(a1) << 16);
-  }
-  *reinterpret_cast<uint4 *>(out + r * inter + c) = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+  *reinterpret_cast<uint4 *>(out + r * inter + c) = swiglu8(gv, uv);
 }
 
 }  // namespace
 
 hipError_t launch_add_rmsnorm(float *h, const uint16_t *delta, const uint16_t *weight, float eps, uint16_t *out,
                               int64_t rows, int hidden, hipStream_t stream) {
-  hipLaunchKernelGGL(add_rmsnorm_kernel, dim3((unsigned)rows), dim3(256), 0, stream, h, delta, weight, eps, out, hidden);
+  hipLaunchKernelGGL(add_rmsnorm_kernel<false>, dim3((unsigned)rows), dim3(kNormThreads), 0, stream, h, delta, SplitSource{},
+                     weight, eps, out, hidden);
+  return hipGetLastError();
+}
+
+hipError_t launch_add_rmsnorm_split(float *h, const SplitSource &delta, const uint16_t *weight, float eps, uint16_t *out,
+                                    int64_t rows, int hidden, hipStream_t stream) {
+  hipLaunchKernelGGL(add_rmsnorm_kernel<true>, dim3((unsigned)rows), dim3(kNormThreads), 0, stream, h, nullptr, delta, weight,
+                     eps, out, hidden);
   return hipGetLastError();
 }
 
 hipError_t launch_rope_cache(const uint16_t *qkv, int64_t stride, int64_t tokens, const int64_t *positions,
                              const float *cos_t, const float *sin_t, int heads, int kv_heads, int d, uint16_t *q_out,
                              uint16_t *k_cache, uint16_t *v_cache, int64_t max_ctx, hipStream_t stream) {
-  hipLaunchKernelGGL(rope_cache_kernel, dim3((unsigned)tokens, heads + 2 * kv_heads), dim3(d / 2), 0, stream, qkv, stride,
-                     positions, cos_t, sin_t, heads, kv_heads, d, q_out, k_cache, v_cache, max_ctx);
+  hipLaunchKernelGGL(rope_cache_kernel<false>, dim3((unsigned)tokens, heads + 2 * kv_heads), dim3(d / 2), 0, stream, qkv,
+                     SplitSource{}, stride, positions, cos_t, sin_t, heads, kv_heads, d, q_out, k_cache, v_cache, max_ctx);
+  return hipGetLastError();
+}
+
+hipError_t launch_rope_cache_split(const SplitSource &qkv, int64_t tokens, const int64_t *positions, const float *cos_t,
+                                   const float *sin_t, int heads, int kv_heads, int d, uint16_t *q_out,
+                                   uint16_t *k_cache, uint16_t *v_cache, int64_t max_ctx, hipStream_t stream) {
+  hipLaunchKernelGGL(rope_cache_kernel<true>, dim3((unsigned)tokens, heads + 2 * kv_heads), dim3(d / 2), 0, stream,
+                     nullptr, qkv, 0, positions, cos_t, sin_t, heads, kv_heads, d, q_out, k_cache, v_cache, max_ctx);
   return hipGetLastError();
 }
 

@@ -14,6 +14,7 @@
 //     the partials in split order, so results never depend on scheduling.
 // Single-token calls stage x in LDS; multi-token calls read x through the cache hierarchy.
 #include "bc4_device.h"
+#include "elementwise.h"
 #include "kernels.h"
 
 namespace tx {
@@ -32,10 +33,6 @@ __device__ __forceinline__ bf16x8 as_bf16x8(uint32_t a, uint32_t b, uint32_t c, 
 }
 
 __device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return as_bf16x8(v.x, v.y, v.z, v.w); }
-
-__device__ __forceinline__ float bf16_bits_to_float(uint16_t v) {
-  return __builtin_bit_cast(float, (uint32_t)v << 16);
-}
 
 __device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
@@ -63,8 +60,14 @@ __device__ __forceinline__ void tile_mfma(uint4 cur, const XFrag &xf, float scal
   acc1 = mfma(as_bf16x8(w[4], w[5], w[6], w[7]), as_bf16x8(xf.x3), acc1);
 }
 
+// Minimum waves per SIMD the register allocation must allow (7 keeps the kernel at <= 72 VGPRs
+// without spills, so seven 4-wave workgroups fit on a CU).
+#ifndef TX_GEMV_WAVES_PER_EU
+#define TX_GEMV_WAVES_PER_EU 7
+#endif
+
 template <int LA, bool MULTI, bool F32OUT>
-__global__ __launch_bounds__(kThreads) void gemv_kernel(GemvParams p) {
+__global__ __launch_bounds__(kThreads, TX_GEMV_WAVES_PER_EU) void gemv_kernel(GemvParams p) {
   extern __shared__ uint4 xs[];  // single token: x slice, 16 uint4 (128 bf16) per tile column
   __shared__ PaletteTableStorage tables;
   __shared__ float red[kWaves][16][16];  // [wave][token][row]
@@ -83,8 +86,9 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvParams p) {
   // tile loop included) in scalar registers.
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int nt = nc > wave ? (nc - wave + kWaves - 1) / kWaves : 0;
-  // Tile j of this wave is tile column c_begin + j*kWaves + wave of row group g.
-  const uint4 *wave_tiles = p.tiles + ((size_t)g * p.CG + c_begin + wave) * 64;
+  // Tile j of this wave is tile column c_begin + j*kWaves + wave of row group g. A wave with no
+  // tile (nc < kWaves) still issues its prefetch loads: they read the split's last column.
+  const uint4 *wave_tiles = p.tiles + ((size_t)g * p.CG + c_begin + min(wave, nc - 1)) * 64;
 
   // Ring of LA+1 tile slots: while tile j is decoded, tiles j+1..j+LA are in flight. The first
   // loads are issued before the LDS set-up so that they overlap it.
@@ -112,16 +116,19 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvParams p) {
   const uint16_t *xrow = x + (size_t)(t0 + min(i, tc - 1)) * p.K;
 
   f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+  // Single token: only B-operand column 0 (lanes with i == 0) carries x; the other columns
+  // produce output columns that are never read, so their lanes skip the LDS reads and keep
+  // whatever their registers hold.
+  XFrag xf = {};
   auto consume = [&](const uint4 &tile, int j) {
     const int col = j * kWaves + wave;  // tile column within this split
-    XFrag xf;
     if constexpr (MULTI) {
       const int k = (c_begin + col) * kTileK + kg * 32;
       xf.x0 = load_x8(xrow, k, p.K);
       xf.x1 = load_x8(xrow, k + 8, p.K);
       xf.x2 = load_x8(xrow, k + 16, p.K);
       xf.x3 = load_x8(xrow, k + 24, p.K);
-    } else {
+    } else if (i == 0) {
       const uint4 *xv = xs + col * 16 + kg * 4;
       xf.x0 = xv[0];
       xf.x1 = xv[1];
@@ -163,31 +170,31 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvParams p) {
     for (int w = 1; w < kWaves; ++w) total += red[w][n][rr];
     const int out_row = g * kTileRows + rr;
     const int token = t0 + n;
-    if (p.ks > 1) {
+    if (p.ks > 1 || p.force_partials) {
       p.partials[((size_t)split * p.tokens + token) * p.Mp + out_row] = total;
     } else if (out_row < p.M) {
       if constexpr (F32OUT) {
         static_cast<float *>(p.y)[(size_t)token * p.M + out_row] = total;
       } else {
-        if (p.bias) total += bf16_bits_to_float(static_cast<const uint16_t *>(p.bias)[out_row]);
+        if (p.bias) total += bf(static_cast<const uint16_t *>(p.bias)[out_row]);
         static_cast<__bf16 *>(p.y)[(size_t)token * p.M + out_row] = (__bf16)total;
       }
     }
   }
 }
 
-// y[t][m] = sum over splits s (in order) of partials[s][t][m], then bias and output cast.
+// y[t][m] = sum over splits s (in order) of partials[s][t][m], then bias and output cast
+// (split_sum, which fused consumers of the partials use as well).
 template <bool F32OUT>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemvParams p) {
   const int m = blockIdx.x * 256 + threadIdx.x;
   const int token = blockIdx.y;
   if (m >= p.M) return;
-  float total = 0.f;
-  for (int s = 0; s < p.ks; ++s) total += p.partials[((size_t)s * p.tokens + token) * p.Mp + m];
+  const SplitSource src{p.partials, F32OUT ? nullptr : static_cast<const uint16_t *>(p.bias), p.ks, p.Mp, p.tokens};
+  const float total = split_sum(src, token, m);
   if constexpr (F32OUT) {
     static_cast<float *>(p.y)[(size_t)token * p.M + m] = total;
   } else {
-    if (p.bias) total += bf16_bits_to_float(static_cast<const uint16_t *>(p.bias)[m]);
     static_cast<__bf16 *>(p.y)[(size_t)token * p.M + m] = (__bf16)total;
   }
 }
@@ -199,7 +206,7 @@ hipError_t launch_variant(const GemvParams &p, hipStream_t stream) {
   dim3 grid(p.RG, p.ks, (p.tokens + 15) / 16);
   hipLaunchKernelGGL((gemv_kernel<LA, MULTI, F32OUT>), grid, dim3(kThreads), lds, stream, p);
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess || p.ks == 1) return e;
+  if (e != hipSuccess || p.ks == 1 || p.force_partials) return e;
   hipLaunchKernelGGL((splitk_reduce_kernel<F32OUT>), dim3((p.M + 255) / 256, p.tokens), dim3(256), 0, stream, p);
   return hipGetLastError();
 }

@@ -14,8 +14,9 @@ struct GemvParams {
   const void *x;           // [tokens][K] bf16
   const void *bias;        // [M] bf16 or nullptr
   void *y;                 // [tokens][M] bf16 or f32
-  float *partials;         // [ks][tokens][Mp] when ks > 1
+  float *partials;         // [ks][tokens][Mp] when ks > 1 or force_partials
   int M, K, Mp, RG, CG, ks, tokens;
+  int force_partials;      // write fp32 partials (no bias, no reduction) even when ks == 1
 };
 
 // Single-token GEMV stages the x slice of a split in LDS: at most this many tile columns
@@ -55,11 +56,19 @@ hipError_t launch_decode_dense(const uint4 *tiles, const float *scales, int M, i
                                uint16_t *out, hipStream_t stream);
 
 // Decoder-layer helpers (decoder.hip).
+struct SplitSource;
 hipError_t launch_add_rmsnorm(float *h, const uint16_t *delta, const uint16_t *weight, float eps, uint16_t *out,
                               int64_t rows, int hidden, hipStream_t stream);
+// The same with delta = the split-K partials of a decode GEMV (summed and rounded as the GEMV's
+// own reduction does).
+hipError_t launch_add_rmsnorm_split(float *h, const SplitSource &delta, const uint16_t *weight, float eps, uint16_t *out,
+                                    int64_t rows, int hidden, hipStream_t stream);
 hipError_t launch_rope_cache(const uint16_t *qkv, int64_t stride, int64_t tokens, const int64_t *positions,
                              const float *cos_t, const float *sin_t, int heads, int kv_heads, int d, uint16_t *q_out,
                              uint16_t *k_cache, uint16_t *v_cache, int64_t max_ctx, hipStream_t stream);
+hipError_t launch_rope_cache_split(const SplitSource &qkv, int64_t tokens, const int64_t *positions, const float *cos_t,
+                                   const float *sin_t, int heads, int kv_heads, int d, uint16_t *q_out,
+                                   uint16_t *k_cache, uint16_t *v_cache, int64_t max_ctx, hipStream_t stream);
 int decode_attention_chunks(int64_t length);
 bool decode_attention_supported(int heads, int kv_heads, int head_dim);
 int64_t decode_attention_max_length();

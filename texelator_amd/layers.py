@@ -11,6 +11,7 @@ import ctypes
 import torch
 
 from . import _lib
+from ._hip import shape as _hip_shape
 from ._lib import TexelatorError, check
 
 
@@ -99,6 +100,51 @@ def decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
                                           kv_heads, head_dim, k_cache.shape[1], float(scale), _ptr(workspace),
                                           workspace.numel() * workspace.element_size(), _ptr(out), _stream(q)))
     return out
+
+
+def linear_split(handle: int, x: torch.Tensor) -> None:
+    """One-token decode GEMV of ``handle`` (``x`` bf16 ``[K]``) whose output stays as split-K
+    partials inside the handle, for :func:`add_rmsnorm_split` or :func:`rope_kv_cache_split`."""
+    _expect(x.is_cuda and x.dtype == torch.bfloat16 and x.is_contiguous() and x.data_ptr() % 16 == 0,
+            "x must be a contiguous, 16-byte aligned CUDA bf16 tensor")
+    _expect(x.numel() == _hip_shape(handle)[1], "x has the wrong length for this handle")
+    check(_lib.load().tx_linear_split(handle, _ptr(x), _stream(x)))
+
+
+def add_rmsnorm_split(residual: torch.Tensor, delta_handle: int, weight: torch.Tensor, eps: float,
+                      out: torch.Tensor) -> torch.Tensor:
+    """:func:`add_rmsnorm` of one row whose delta is the last :func:`linear_split` of ``delta_handle``."""
+    _expect(residual.is_cuda and residual.dtype == torch.float32 and residual.is_contiguous() and residual.numel() ==
+            weight.numel(), "residual must be a contiguous CUDA float32 row of hidden values")
+    hidden = residual.numel()
+    _expect(_hip_shape(delta_handle)[0] == hidden, "the delta handle's output size must equal hidden")
+    _expect(weight.dtype == torch.bfloat16 and weight.is_contiguous(), "weight must be bf16 [hidden]")
+    _expect(out.dtype == torch.bfloat16 and out.is_contiguous() and out.numel() == hidden, "bad output")
+    check(_lib.load().tx_add_rmsnorm_split(_ptr(residual), delta_handle, _ptr(weight), float(eps), _ptr(out), hidden,
+                                           _stream(residual)))
+    return out
+
+
+def rope_kv_cache_split(qkv_handle: int, positions: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, heads: int,
+                        kv_heads: int, head_dim: int, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                        q_out: torch.Tensor) -> torch.Tensor:
+    """:func:`rope_kv_cache` of one token whose ``[q | k | v]`` row is the last :func:`linear_split`
+    of ``qkv_handle``."""
+    _expect(_hip_shape(qkv_handle)[0] >= (heads + 2 * kv_heads) * head_dim, "qkv handle too narrow for the heads")
+    _expect(positions.dtype == torch.int64 and positions.is_contiguous() and positions.numel() == 1,
+            "positions must be int64 [1]")
+    max_ctx = k_cache.shape[1]
+    for cache in (k_cache, v_cache):
+        _expect(cache.dtype == torch.bfloat16 and cache.is_contiguous() and tuple(cache.shape) == (kv_heads, max_ctx, head_dim),
+                "caches must be contiguous bf16 [kv_heads, max_context, head_dim]")
+    for table in (cos, sin):
+        _expect(table.dtype == torch.float32 and table.is_contiguous() and tuple(table.shape) == (max_ctx, head_dim),
+                "rope tables must be float32 [max_context, head_dim]")
+    _expect(q_out.dtype == torch.bfloat16 and q_out.is_contiguous() and q_out.numel() == heads * head_dim, "bad q_out")
+    check(_lib.load().tx_rope_kv_cache_split(qkv_handle, _ptr(positions), _ptr(cos), _ptr(sin), heads, kv_heads,
+                                             head_dim, _ptr(q_out), _ptr(k_cache), _ptr(v_cache), max_ctx,
+                                             _stream(positions)))
+    return q_out
 
 
 def swiglu(gate_up: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:

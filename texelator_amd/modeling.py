@@ -102,6 +102,7 @@ MERGED = {
 class _Layer:
     def __init__(self):
         self.linears: dict[str, TexelatorLinear] = {}     # keys of MERGED
+        self.handles: dict[str, int] = {}                  # keys of MERGED -> library handle
         self.rows: dict[str, tuple[int, int]] = {}         # reference linear name -> (first row, rows)
         self.biases: dict[str, torch.Tensor] = {}          # merged key -> bias
         self.input_norm: torch.Tensor | None = None
@@ -115,11 +116,16 @@ class BC4Decoder:
     the output rows (one launch each), o and down stay single. With ``fused`` (the default) the
     layer glue runs as this library's kernels (``texelator_amd.layers``): add+RMSNorm, RoPE+KV
     write, split-length decode attention and SwiGLU. Without it, the same math runs as plain
-    PyTorch ops (the cross-check path)."""
+    PyTorch ops (the cross-check path).
+
+    With ``split_decode`` (the default; needs ``fused``) a one-token step hands the split-K
+    partials of qkv, o and down straight to their consumer kernels (RoPE, add+RMSNorm), so a
+    layer is ten kernels instead of thirteen; the results are bit-identical to the unsplit fused
+    path."""
 
     def __init__(self, config: DecoderConfig, max_context: int, device: torch.device | str = "cuda", seed: int = 0,
                  lookahead: int = 1, linear_source=None, depth_scaled: bool = True, embed_std: float = 1.0,
-                 fused: bool = True):
+                 fused: bool = True, split_decode: bool = True):
         """``linear_source(layer, name, m, k)`` may return ``(blocks, scales)`` device tensors for a
         linear (reference block layout). By default every linear is a seeded random BC4 matrix.
 
@@ -136,6 +142,7 @@ class BC4Decoder:
         self.device = torch.device(device)
         self.max_context = int(max_context)
         self.fused = fused
+        self.split_decode = fused and split_decode
         ext = extension()
         c = config
         if fused and not layers.decode_attention_supported(c):
@@ -175,6 +182,7 @@ class BC4Decoder:
                     self.handles.append(handle)
                     ext.set_lookahead(handle, lookahead)
                     layer.linears[key] = TexelatorLinear([handle])
+                    layer.handles[key] = handle
                     if bias is not None:
                         layer.biases[key] = bias
                     del blocks, scales, parts_blocks, parts_scales
@@ -196,6 +204,7 @@ class BC4Decoder:
             layers.decode_attention_workspace_bytes(c.heads, self.max_context) if fused else 16,
             dtype=torch.uint8, device=self.device)
         # decode-step state (static buffers read and advanced by the captured graphs)
+        self.q_buffer = torch.empty(c.heads * c.head_dim, dtype=bf16, device=self.device)
         self.token = torch.zeros(1, dtype=torch.long, device=self.device)
         self.position = torch.zeros(1, dtype=torch.long, device=self.device)
         self.graphs: dict[int, torch.cuda.CUDAGraph] = {}
@@ -283,6 +292,8 @@ class BC4Decoder:
         tokens = ids.numel()
         scale = 1.0 / math.sqrt(c.head_dim)
         x = layers.add_rmsnorm(h, None, self.layers[0].input_norm, c.rms_eps)
+        if tokens == 1 and self.split_decode:
+            return self._decode_split(h, x, positions, length, scale)
         for index, layer in enumerate(self.layers):
             qkv = layer.linears["qkv"](x)
             q = layers.rope_kv_cache(qkv, positions, self.rope_cos, self.rope_sin, c.heads, c.kv_heads, c.head_dim,
@@ -296,6 +307,24 @@ class BC4Decoder:
             act = layers.swiglu(layer.linears["gate_up"](x))
             following = self.layers[index + 1].input_norm if index + 1 < len(self.layers) else self.final_norm
             layers.add_rmsnorm(h, layer.linears["down"](act), following, c.rms_eps, out=x)
+        return x
+
+    def _decode_split(self, h: torch.Tensor, x: torch.Tensor, positions: torch.Tensor, length: int,
+                      scale: float) -> torch.Tensor:
+        """One token through every layer with the split-K consumers (ten kernels a layer)."""
+        c = self.config
+        for index, layer in enumerate(self.layers):
+            layers.linear_split(layer.handles["qkv"], x)
+            q = layers.rope_kv_cache_split(layer.handles["qkv"], positions, self.rope_cos, self.rope_sin, c.heads,
+                                           c.kv_heads, c.head_dim, self.k_cache[index], self.v_cache[index],
+                                           self.q_buffer)
+            attn = layers.decode_attention(q, self.k_cache[index], self.v_cache[index], positions, length, c.heads,
+                                           c.kv_heads, scale, self.attention_workspace)
+            layers.linear_split(layer.handles["o"], attn)
+            layers.add_rmsnorm_split(h, layer.handles["o"], layer.post_norm, c.rms_eps, out=x)
+            layers.linear_split(layer.handles["down"], layers.swiglu(layer.linears["gate_up"](x)))
+            following = self.layers[index + 1].input_norm if index + 1 < len(self.layers) else self.final_norm
+            layers.add_rmsnorm_split(h, layer.handles["down"], following, c.rms_eps, out=x)
         return x
 
     def logits(self, hidden: torch.Tensor) -> torch.Tensor:
