@@ -47,8 +47,12 @@ int tx_pack_encoded_device(const uint8_t *blocks, int64_t blocks_bytes, const fl
                            const void *bias, int bias_dtype, int device, uint64_t *handle_out);
 
 /* y = x W^T (+ bias). Replaces texelator_linear (texelator_cuda.cu:1329-1469; extension.cpp:30).
- *   x         device, contiguous, 16-byte aligned [tokens][K] of x_dtype (BF16; F16 is reported
- *             unsupported)
+ *   x         device, contiguous, 16-byte aligned [tokens][K] of x_dtype (BF16 or F16). With F16
+ *             the weights are rounded to fp16 before the fp32-accumulating MFMA; the reference's
+ *             FP16 GEMV (texelator_cuda.cu:94-139) multiplies them unrounded (at most 2^-11
+ *             relative per weight), its FP16 prefill rounds them the same way (:604-628). The
+ *             bias must have x's dtype; y = round(acc + bias) on the GEMV, and
+ *             round(round(acc) + bias) on the prefill path, as in the reference.
  *   x_numel   number of elements of x; tokens = x_numel / K
  *   x_last    size of x's last dimension (must equal K)
  *   y         device output [tokens][M] of x_dtype, allocated by the caller
@@ -69,10 +73,10 @@ int tx_workspace_bytes(uint64_t handle, int64_t tokens, int64_t *bytes);
  * the reference only returns 16-bit outputs). x: device bf16 [tokens][K]; y: device f32. */
 int tx_linear_f32(uint64_t handle, const void *x, int64_t tokens, float *y, void *stream);
 
-/* Prefill GEMM with an explicit candidate (5..9), bf16 in/out, bias applied if present; same
- * workspace rule as tx_linear. Used by the tile autotuner (reference: set_prefill_backend +
- * linear, autotune.py:144-187). */
-int tx_prefill(uint64_t handle, int candidate, const void *x, int64_t tokens, void *y,
+/* Prefill GEMM with an explicit candidate (5..9), x_dtype (BF16 or F16) in and out, bias
+ * applied if present; same workspace rule as tx_linear. Used by the tile autotuner (reference:
+ * set_prefill_backend + linear, autotune.py:144-187). */
+int tx_prefill(uint64_t handle, int candidate, const void *x, int x_dtype, int64_t tokens, void *y,
                void *workspace, int64_t workspace_bytes, void *stream);
 
 /* Replaces texelator_set_lookahead (texelator_cuda.cu:1471-1478): one of 1,2,3,4,6,8. */
@@ -99,9 +103,10 @@ int tx_free(uint64_t handle);
  * on the current device. Synchronous. */
 int tx_palette_probe(float *host_out);
 
-/* Decode a handle's weights to a dense device bf16 [M][K] array (test-only diagnostic; no
- * reference counterpart -- the reference's decode tiles write scratch, texelator_cuda.cu:604-663). */
-int tx_decode_dense(uint64_t handle, uint16_t *out, void *stream);
+/* Decode a handle's weights to a dense device [M][K] array of dtype (BF16: bf16_rne(P*scale);
+ * F16: fp16_rne(P*scale), the FP16 path's weights) -- a test-only diagnostic; no reference
+ * counterpart (the reference's decode tiles write scratch, texelator_cuda.cu:604-663). */
+int tx_decode_dense(uint64_t handle, int dtype, uint16_t *out, void *stream);
 
 /* Kernel resource report for a candidate. Replaces the *_kernel_info functions
  * (texelator_cuda.cu:1514-1536, cutlass_texture_mainloop.cu:251-267). candidate 5..9: prefill

@@ -11,6 +11,9 @@ Reference anchors (paths relative to the reference checkout):
   (``texelator/cuda/texelator_cuda.cu:1542-1595``: ``out[(y*255 + x)*8 + s]``, x = e0+127).
 * decoded weight -- ``texelator/cuda/texelator_cuda.cu:141-152``:
   ``bf16_rne(palette_value * scale[row])`` with an fp32 product.
+* FP16 path -- the FP16 GEMV multiplies the unrounded fp32 product ``palette_value * scale``
+  by the fp16 activation (``texelator_cuda.cu:75-83``, ``:94-139``); the FP16 prefill decodes
+  ``fp16_rne(palette_value * scale)`` into its scratch matrix (``texelator_cuda.cu:604-628``).
 * error metrics -- ``texelator/autotune.py:63-76`` and ``texelator/prefill.py:94-105``.
 
 Palette definition (this build's; the reference's palette is measured from NVIDIA texture
@@ -174,6 +177,19 @@ def decode_bf16_bits(blocks: np.ndarray, scales: np.ndarray, lut: np.ndarray | N
     pal = decode_f32_palette(blocks, m, lut)
     prod = (pal * scales[:, None]).astype(np.float32)  # float32 * float32 -> correctly rounded
     return f32_to_bf16_bits(prod)
+
+
+def decode_f32_weights(blocks: np.ndarray, scales: np.ndarray, lut: np.ndarray | None = None) -> np.ndarray:
+    """Unrounded FP16-path weights ``fp32(P * scale[m])`` ``[M, K]`` (``texelator_cuda.cu:75-83``)."""
+    scales = np.asarray(scales, dtype=np.float32)
+    pal = decode_f32_palette(blocks, scales.shape[0], lut)
+    return (pal * scales[:, None]).astype(np.float32)
+
+
+def decode_f16_bits(blocks: np.ndarray, scales: np.ndarray, lut: np.ndarray | None = None) -> np.ndarray:
+    """FP16 prefill weights as fp16 bit patterns ``[M, K]``: ``fp16_rne(fp32(P * scale[m]))``
+    (``texelator_cuda.cu:624``, ``__float2half``)."""
+    return decode_f32_weights(blocks, scales, lut).astype(np.float16).view(np.uint16)
 
 
 def matvec_f64(w_bits: np.ndarray, x: np.ndarray) -> np.ndarray:

@@ -26,6 +26,11 @@ def bf16_vector(shape, seed: int, scale: float = 1.0) -> torch.Tensor:
     return (torch.randn(shape, generator=generator) * scale).to(torch.bfloat16)
 
 
+def f16_vector(shape, seed: int, scale: float = 1.0) -> torch.Tensor:
+    generator = torch.Generator().manual_seed(seed)
+    return (torch.randn(shape, generator=generator) * scale).to(torch.float16)
+
+
 def bf16_bits(t: torch.Tensor) -> np.ndarray:
     return t.contiguous().view(torch.int16).numpy().view(np.uint16)
 

@@ -14,7 +14,8 @@ import pytest
 import torch
 
 from oracle import bc4, clib
-from tests.helpers import bf16_bits, bf16_vector, lognormal_scales, max_rel_err_floor, random_blocks, rel_err
+from tests.helpers import (bf16_bits, bf16_vector, f16_vector, lognormal_scales, max_rel_err_floor, random_blocks,
+                           rel_err)
 
 pytestmark = pytest.mark.gpu
 
@@ -259,3 +260,99 @@ def test_handle_api_errors(ext):
         ext.pack_encoded(torch.zeros(16, dtype=torch.int8), torch.ones(1))
     with pytest.raises(RuntimeError, match="invalid encoded size"):
         ext.pack_encoded(torch.zeros(12, dtype=torch.uint8), torch.ones(1))
+
+
+# ---- FP16 activations (the reference's FP16 GEMV and FP16 prefill, texelator_cuda.cu:94-139,
+# :1004-1045): fp16 x, bias and y; the weights are fp16_rne(P * scale).
+
+def f16_bits(t: torch.Tensor) -> np.ndarray:
+    return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+@pytest.mark.parametrize("m,k,seed", [(16, 128, 401), (37, 272, 402), (64, 4096, 403)])
+def test_decode_dense_f16_bit_exact(ext, m, k, seed):
+    blocks = random_blocks(m, k, seed)
+    scales = lognormal_scales(m, seed + 100)
+    handle = _pack(ext, blocks, scales)
+    try:
+        got = f16_bits(ext.decode_dense(handle, torch.float16))
+    finally:
+        ext.free(handle)
+    want = bc4.decode_f16_bits(blocks, scales)
+    mismatches = int(np.count_nonzero(got != want))
+    assert mismatches == 0, f"{mismatches} of {want.size} fp16 weights differ"
+
+
+@pytest.mark.parametrize("m,k,tokens,bias", [(1024, 5120, 1, False), (333, 2048, 1, True), (272, 3072, 5, True),
+                                             (5120, 27648, 1, False), (64, 27648, 1, True)])
+def test_gemv_f16_within_tolerance(ext, m, k, tokens, bias):
+    """FP16 GEMV against the reference's arithmetic in float64: unrounded fp32 weights times the
+    fp16 input, plus the bias. Our weights are rounded to fp16 (2^-11 relative each), the output
+    is rounded to fp16 once (2^-11 relative per element)."""
+    blocks = random_blocks(m, k, 411 + m)
+    scales = lognormal_scales(m, 412 + m)
+    x = f16_vector((tokens, k), 413 + m)
+    b = f16_vector((m,), 414 + m, scale=0.5) if bias else None
+    handle = _pack(ext, blocks, scales, b.cuda() if bias else None)
+    try:
+        ext.set_prefill(handle, 1 << 20, 1024)
+        y = ext.linear(handle, x.cuda())
+        torch.cuda.synchronize()
+    finally:
+        ext.free(handle)
+    assert y.dtype == torch.float16
+    w = bc4.decode_f32_weights(blocks, scales).astype(np.float64)
+    ref = x.double().numpy() @ w.T
+    if bias:
+        ref = ref + b.double().numpy()[None, :]
+    got = y.double().cpu().numpy()
+    for t in range(tokens):
+        assert rel_err(ref[t], got[t]) <= GEMV_TOL
+        assert max_rel_err_floor(ref[t], got[t]) <= 2 ** -11 + GEMV_TOL
+
+
+@pytest.mark.parametrize("tokens", [17, 64, 130])
+def test_prefill_f16_candidates_bitwise_equal_and_within_rrms(ext, tokens):
+    m, k = 200, 1280
+    blocks = random_blocks(m, k, 421)
+    scales = lognormal_scales(m, 422)
+    x = f16_vector((tokens, k), 423, scale=0.125)
+    bias = f16_vector((m,), 424, scale=0.1)
+    plain = _pack(ext, blocks, scales)
+    biased = _pack(ext, blocks, scales, bias.cuda())
+    try:
+        outputs = [ext.prefill(plain, c, x.cuda()) for c in range(5, 10)]
+        with_bias = ext.prefill(biased, 6, x.cuda())
+        ext.set_prefill(biased, 1, 1024)
+        via_linear = ext.linear(biased, x.cuda())
+        torch.cuda.synchronize()
+    finally:
+        ext.free(plain)
+        ext.free(biased)
+    for c, value in zip(range(6, 10), outputs[1:]):
+        assert torch.equal(outputs[0], value), f"candidate {c} differs"
+    assert outputs[0].dtype == torch.float16
+    # the bias is added to the fp16 product with a second fp16 rounding (texelator_cuda.cu:630-635)
+    assert torch.equal(with_bias, (outputs[0].float() + bias.cuda().float()[None, :]).to(torch.float16))
+    assert torch.equal(with_bias, via_linear)
+    w = bc4.decode_f16_bits(blocks, scales).view(np.float16).astype(np.float64)
+    ref = x.double().numpy() @ w.T
+    assert bc4.relative_rms(ref, outputs[0].double().cpu().numpy()) <= PREFILL_RRMS_TOL
+
+
+def test_prefill_f16_split_k_matches_oracle(ext):
+    m, k, tokens = 300, 27648, 32
+    blocks = random_blocks(m, k, 431)
+    scales = lognormal_scales(m, 432)
+    x = f16_vector((tokens, k), 433, scale=0.125)
+    handle = _pack(ext, blocks, scales)
+    try:
+        assert ext.workspace_bytes(handle, tokens) > 0, "shape expected to split"
+        outputs = [ext.prefill(handle, c, x.cuda()) for c in (5, 9)]
+        torch.cuda.synchronize()
+    finally:
+        ext.free(handle)
+    assert torch.equal(outputs[0], outputs[1])
+    w = bc4.decode_f16_bits(blocks, scales).view(np.float16).astype(np.float64)
+    ref = x.double().numpy() @ w.T
+    assert bc4.relative_rms(ref, outputs[0].double().cpu().numpy()) <= PREFILL_RRMS_TOL

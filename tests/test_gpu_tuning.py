@@ -25,10 +25,11 @@ def state(tmp_path, monkeypatch):
     return tmp_path / "state"
 
 
-def _artifact(path, palette=None):
+def _artifact(path, palette=None, runtime_dtype="bfloat16"):
     matrices = [(f"model.layers.{i}.mlp.down_proj", random_blocks(m, k, 300 + i), lognormal_scales(m, 400 + i))
                 for i, (m, k) in enumerate(SHAPES)]
-    return artifacts.write_artifact(path, matrices, palette or hardware.PALETTE_SHA256), matrices
+    return artifacts.write_artifact(path, matrices, palette or hardware.PALETTE_SHA256,
+                                    runtime_dtype=runtime_dtype), matrices
 
 
 def test_ensure_hardware_caches_the_defined_palette(ext, state):
@@ -38,8 +39,9 @@ def test_ensure_hardware_caches_the_defined_palette(ext, state):
     assert payload["palette_sha256"] == hardware.PALETTE_SHA256 and payload["endpoint_pairs"] == 65025
 
 
-def test_lookahead_tuner_selects_and_persists(ext, state, tmp_path):
-    art, _ = _artifact(tmp_path / "art")
+@pytest.mark.parametrize("runtime_dtype", ["bfloat16", "float16"])
+def test_lookahead_tuner_selects_and_persists(ext, state, tmp_path, runtime_dtype):
+    art, _ = _artifact(tmp_path / "art", runtime_dtype=runtime_dtype)
     profile = tuning.tune_artifact(art, warmup=1, measured=3, runs=2)
     assert profile["selected_lookahead"] in tuning.CANDIDATES
     assert all(row["max_abs_vs_k1"] == 0.0 for row in profile["candidates"])

@@ -219,8 +219,9 @@ def test_profile_paths_and_selected_profile_gates(tmp_path, fake_device, monkeyp
 
 
 def test_runtime_dtype_gate():
+    """bfloat16 and float16 artifacts are accepted; float16 is the default (``tuning.py``)."""
     assert tuning._runtime_dtype({"runtime_dtype": "bfloat16"}) is torch.bfloat16
-    with pytest.raises(RuntimeError, match="FP16"):
-        tuning._runtime_dtype({})
+    assert tuning._runtime_dtype({"runtime_dtype": "float16"}) is torch.float16
+    assert tuning._runtime_dtype({}) is torch.float16
     with pytest.raises(RuntimeError, match="unsupported"):
         tuning._runtime_dtype({"runtime_dtype": "float32"})

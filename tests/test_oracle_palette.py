@@ -109,3 +109,42 @@ def test_palette_sha_is_stable():
 def test_bf16_round_to_nearest_even(bits, expected):
     v = np.array([bits], dtype=np.uint32).view(np.float32)
     assert int(bc4.f32_to_bf16_bits(v)[0]) == expected
+
+
+def _blocks(m, k, seed):
+    from tests.helpers import random_blocks
+    return random_blocks(m, k, seed)
+
+
+def test_fp16_path_weights_are_the_fp32_products():
+    """decode_f32_weights is the fp32 product P * scale: with a power-of-two scale it is the
+    palette value scaled exactly, and its bf16 rounding is the BF16 path's decoded weight."""
+    m, k = 24, 256
+    blocks = _blocks(m, k, 301)
+    pal = bc4.decode_f32_palette(blocks, m)
+    exact = bc4.decode_f32_weights(blocks, np.full(m, 0.125, np.float32))
+    assert np.array_equal(exact, pal / np.float32(8))
+    scales = (0.02 * np.exp(0.3 * np.random.default_rng(302).standard_normal(m))).astype(np.float32)
+    w = bc4.decode_f32_weights(blocks, scales)
+    assert np.array_equal(bc4.f32_to_bf16_bits(w), bc4.decode_bf16_bits(blocks, scales))
+
+
+def test_fp16_weights_round_to_nearest_even():
+    """Each fp16 weight is a nearest fp16 value of the fp32 product, and an exact tie picks the
+    even significand -- checked from the fp16 neighbours, not by converting again."""
+    m, k = 32, 512
+    blocks = _blocks(m, k, 303)
+    scales = (0.5 * np.exp(np.random.default_rng(304).standard_normal(m))).astype(np.float32)
+    w = bc4.decode_f32_weights(blocks, scales).astype(np.float64).ravel()
+    bits = bc4.decode_f16_bits(blocks, scales).ravel()
+    h = bits.view(np.float16)
+    up = np.nextafter(h, np.float16(np.inf)).astype(np.float64)
+    down = np.nextafter(h, np.float16(-np.inf)).astype(np.float64)
+    hv = h.astype(np.float64)
+    err = np.abs(w - hv)
+    assert np.all(err <= np.abs(w - up)) and np.all(err <= np.abs(w - down))
+    ties = (err == np.abs(w - up)) | (err == np.abs(w - down))
+    ties &= err > 0
+    assert np.all((bits[ties] & 1) == 0)
+    # a hand-made tie: 1 + 2^-11 lies halfway between 1 and 1 + 2^-10 and rounds to 1
+    assert np.float32(1 + 2 ** -11).astype(np.float16) == np.float16(1.0)

@@ -166,17 +166,17 @@ def linear_f32_into(handle: int, x: torch.Tensor, y: torch.Tensor) -> None:
 
 
 def prefill(handle: int, candidate: int, x: torch.Tensor) -> torch.Tensor:
-    """Prefill GEMM with an explicit tile candidate (5..9), bf16 in and out."""
-    _require(x.is_cuda and x.dtype == torch.bfloat16 and x.is_contiguous(), "input must be contiguous CUDA BF16")
+    """Prefill GEMM with an explicit tile candidate (5..9); fp16 or bf16 in, the same type out."""
+    _require(x.is_cuda and x.dtype in _DTYPE_CODE and x.is_contiguous(), "input must be contiguous CUDA FP16 or BF16")
     m, k = shape(handle)
     _require(x.size(-1) == k, "input shape/device mismatch")
     out_shape = list(x.shape)
     out_shape[-1] = m
-    y = torch.empty(out_shape, dtype=torch.bfloat16, device=x.device)
+    y = torch.empty(out_shape, dtype=x.dtype, device=x.device)
     x = _aligned(x)
     tokens = x.numel() // k
     ws, ws_ptr, ws_bytes = _workspace(handle, tokens, x.device)
-    check(_lib.load().tx_prefill(handle, int(candidate), ctypes.c_void_p(x.data_ptr()), tokens,
+    check(_lib.load().tx_prefill(handle, int(candidate), ctypes.c_void_p(x.data_ptr()), _DTYPE_CODE[x.dtype], tokens,
                                  ctypes.c_void_p(y.data_ptr()), ws_ptr, ws_bytes, _stream(x.device)))
     del ws
     return y
@@ -184,17 +184,17 @@ def prefill(handle: int, candidate: int, x: torch.Tensor) -> torch.Tensor:
 
 def prefill_into(handle: int, candidate: int, x: torch.Tensor, y: torch.Tensor,
                  workspace: torch.Tensor | None = None) -> None:
-    """``prefill`` writing into a caller-provided bf16 ``y`` of ``[..., M]``; ``workspace`` (a
-    CUDA tensor of at least ``workspace_bytes(handle, tokens)`` bytes) is required when that is
+    """``prefill`` writing into a caller-provided ``y`` of ``[..., M]`` (x's dtype); ``workspace``
+    (a CUDA tensor of at least ``workspace_bytes(handle, tokens)`` bytes) is required when that is
     nonzero."""
     m, k = shape(handle)
-    if (x.dtype != torch.bfloat16 or y.dtype != torch.bfloat16 or not x.is_contiguous() or not y.is_contiguous()
+    if (x.dtype not in _DTYPE_CODE or y.dtype != x.dtype or not x.is_contiguous() or not y.is_contiguous()
             or x.size(-1) != k or y.size(-1) != m or x.numel() // k != y.numel() // m or x.data_ptr() % 16):
-        raise TexelatorError("prefill_into: expected aligned contiguous bf16 x [..., K] and bf16 y [..., M]")
+        raise TexelatorError("prefill_into: expected aligned contiguous fp16/bf16 x [..., K] and y [..., M] of x's dtype")
     ws_ptr = ctypes.c_void_p(workspace.data_ptr()) if workspace is not None else ctypes.c_void_p(None)
     ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
-    check(_lib.load().tx_prefill(handle, int(candidate), ctypes.c_void_p(x.data_ptr()), x.numel() // k,
-                                 ctypes.c_void_p(y.data_ptr()), ws_ptr, ws_bytes, _stream(x.device)))
+    check(_lib.load().tx_prefill(handle, int(candidate), ctypes.c_void_p(x.data_ptr()), _DTYPE_CODE[x.dtype],
+                                 x.numel() // k, ctypes.c_void_p(y.data_ptr()), ws_ptr, ws_bytes, _stream(x.device)))
 
 
 def set_lookahead(handle: int, lookahead: int) -> None:
@@ -234,12 +234,14 @@ def palette_probe() -> torch.Tensor:
     return out
 
 
-def decode_dense(handle: int) -> torch.Tensor:
-    """Decoded weights as a dense ``[M, K]`` bf16 device tensor (diagnostic)."""
+def decode_dense(handle: int, dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+    """Decoded weights as a dense ``[M, K]`` device tensor (diagnostic): bf16 (the BF16 path's
+    weights) or fp16 (the FP16 path's)."""
+    _require(dtype in _DTYPE_CODE, "dtype must be torch.float16 or torch.bfloat16")
     m, k = shape(handle)
     device = torch.device("cuda", torch.cuda.current_device())
-    out = torch.empty((m, k), dtype=torch.bfloat16, device=device)
-    check(_lib.load().tx_decode_dense(handle, ctypes.c_void_p(out.data_ptr()), _stream(device)))
+    out = torch.empty((m, k), dtype=dtype, device=device)
+    check(_lib.load().tx_decode_dense(handle, _DTYPE_CODE[dtype], ctypes.c_void_p(out.data_ptr()), _stream(device)))
     return out
 
 

@@ -35,14 +35,14 @@ SIGNATURES = {
     "tx_linear": (_I32, [_U64, _P, _I32, _I64, _I64, _I32, _P, _P, _I64, _P]),
     "tx_workspace_bytes": (_I32, [_U64, _I64, ctypes.POINTER(_I64)]),
     "tx_linear_f32": (_I32, [_U64, _P, _I64, _P, _P]),
-    "tx_prefill": (_I32, [_U64, _I32, _P, _I64, _P, _P, _I64, _P]),
+    "tx_prefill": (_I32, [_U64, _I32, _P, _I32, _I64, _P, _P, _I64, _P]),
     "tx_set_lookahead": (_I32, [_U64, _I32]),
     "tx_set_prefill": (_I32, [_U64, _I32, _I32]),
     "tx_set_prefill_backend": (_I32, [_U64, _I32]),
     "tx_handle_info": (_I32, [_U64, ctypes.POINTER(_I64), _I32]),
     "tx_free": (_I32, [_U64]),
     "tx_palette_probe": (_I32, [_P]),
-    "tx_decode_dense": (_I32, [_U64, _P, _P]),
+    "tx_decode_dense": (_I32, [_U64, _I32, _P, _P]),
     "tx_kernel_info": (_I32, [_I32, ctypes.POINTER(_I64), _I32]),
     "tx_candidate_name": (ctypes.c_char_p, [_I32]),
     "tx_add_rmsnorm": (_I32, [_P, _P, _P, ctypes.c_float, _P, _I64, _I64, _P]),

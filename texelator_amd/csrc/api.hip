@@ -122,9 +122,10 @@ int64_t prefill_workspace_bytes(const Handle *h, int64_t tokens) {
   return ks > 1 ? (int64_t)ks * tokens * h->Mp * (int64_t)sizeof(float) : 0;
 }
 
-int run_prefill(Handle *h, int candidate, const void *x, int64_t tokens, void *y, void *workspace,
+int run_prefill(Handle *h, int candidate, const void *x, bool f16, int64_t tokens, void *y, void *workspace,
                 int64_t workspace_bytes, hipStream_t stream) {
   tx::PrefillParams p{};
+  p.f16 = f16 ? 1 : 0;
   p.tiles = h->tiles;
   p.scales = h->scales;
   p.x = x;
@@ -153,9 +154,10 @@ tx::SplitSource split_source(const Handle *h) {
   return tx::SplitSource{h->partials, static_cast<const uint16_t *>(h->bias), h->gemv_splits, h->Mp, 1};
 }
 
-int run_gemv(Handle *h, const void *x, int64_t tokens, void *y, bool f32_out, hipStream_t stream) {
+int run_gemv(Handle *h, const void *x, bool f16, int64_t tokens, void *y, bool f32_out, hipStream_t stream) {
   if (tokens > 65535) return fail(TX_ERR_INVALID, "token grid exceeds the HIP grid.z limit");
   tx::GemvParams p{};
+  p.f16 = f16 ? 1 : 0;
   p.tiles = h->tiles;
   p.scales = h->scales;
   p.x = x;
@@ -284,18 +286,19 @@ int tx_linear(uint64_t value, const void *x, int x_dtype, int64_t x_numel, int64
   if (x_last != h->K || device != h->device) return fail(TX_ERR_INVALID, "input shape/device mismatch");
   if (!x || !y) return fail(TX_ERR_INVALID, "null input or output pointer");
   if (reinterpret_cast<uintptr_t>(x) % 16 != 0) return fail(TX_ERR_INVALID, "input must be 16-byte aligned");
-  if (x_dtype == TX_DTYPE_F16) return fail(TX_ERR_UNSUPPORTED, "FP16 activations are not supported by the gfx950 BC4 path");
+  const bool f16 = x_dtype == TX_DTYPE_F16;
   const int64_t tokens = x_numel / h->K;
   if (tokens <= 0) return TX_OK;
   DeviceGuard guard(h->device);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (tokens >= h->prefill_threshold && tokens > 1) {
-    if (h->bias && h->bias_dtype != TX_DTYPE_BF16) return fail(TX_ERR_INVALID, "BF16 prefill requires a BF16 bias");
+    if (h->bias && h->bias_dtype != x_dtype)
+      return fail(TX_ERR_INVALID, f16 ? "FP16 prefill requires an FP16 bias" : "BF16 prefill requires a BF16 bias");
     const int candidate = h->prefill_backend >= tx::kPrefillFirst ? h->prefill_backend : default_candidate(tokens);
-    return run_prefill(h, candidate, x, tokens, y, workspace, workspace_bytes, s);
+    return run_prefill(h, candidate, x, f16, tokens, y, workspace, workspace_bytes, s);
   }
   if (h->bias && h->bias_dtype != x_dtype) return fail(TX_ERR_INVALID, "input and bias dtypes must match");
-  return run_gemv(h, x, tokens, y, false, s);
+  return run_gemv(h, x, f16, tokens, y, false, s);
 }
 
 int tx_linear_f32(uint64_t value, const void *x, int64_t tokens, float *y, void *stream) {
@@ -306,21 +309,24 @@ int tx_linear_f32(uint64_t value, const void *x, int64_t tokens, float *y, void 
   if (reinterpret_cast<uintptr_t>(x) % 16 != 0) return fail(TX_ERR_INVALID, "input must be 16-byte aligned");
   if (tokens <= 0) return TX_OK;
   DeviceGuard guard(h->device);
-  return run_gemv(h, x, tokens, y, true, reinterpret_cast<hipStream_t>(stream));
+  return run_gemv(h, x, false, tokens, y, true, reinterpret_cast<hipStream_t>(stream));
 }
 
-int tx_prefill(uint64_t value, int candidate, const void *x, int64_t tokens, void *y, void *workspace,
+int tx_prefill(uint64_t value, int candidate, const void *x, int x_dtype, int64_t tokens, void *y, void *workspace,
                int64_t workspace_bytes, void *stream) {
   g_last_error.clear();
   Handle *h = as_handle(value);
   if (!h) return fail(TX_ERR_INVALID, "null Texelator handle");
   if (!x || !y) return fail(TX_ERR_INVALID, "null input or output pointer");
+  if (x_dtype != TX_DTYPE_BF16 && x_dtype != TX_DTYPE_F16) return fail(TX_ERR_INVALID, "input must be FP16 or BF16");
   if (reinterpret_cast<uintptr_t>(x) % 16 != 0) return fail(TX_ERR_INVALID, "input must be 16-byte aligned");
   if (!tx::prefill_candidate_eligible(candidate, h->M, h->K)) return fail(TX_ERR_INVALID, "unknown or ineligible prefill candidate");
-  if (h->bias && h->bias_dtype != TX_DTYPE_BF16) return fail(TX_ERR_INVALID, "BF16 prefill requires a BF16 bias");
+  const bool f16 = x_dtype == TX_DTYPE_F16;
+  if (h->bias && h->bias_dtype != x_dtype)
+    return fail(TX_ERR_INVALID, f16 ? "FP16 prefill requires an FP16 bias" : "BF16 prefill requires a BF16 bias");
   if (tokens <= 0) return TX_OK;
   DeviceGuard guard(h->device);
-  return run_prefill(h, candidate, x, tokens, y, workspace, workspace_bytes, reinterpret_cast<hipStream_t>(stream));
+  return run_prefill(h, candidate, x, f16, tokens, y, workspace, workspace_bytes, reinterpret_cast<hipStream_t>(stream));
 }
 
 int tx_workspace_bytes(uint64_t value, int64_t tokens, int64_t *bytes) {
@@ -396,13 +402,15 @@ int tx_palette_probe(float *host_out) {
   return TX_OK;
 }
 
-int tx_decode_dense(uint64_t value, uint16_t *out, void *stream) {
+int tx_decode_dense(uint64_t value, int dtype, uint16_t *out, void *stream) {
   g_last_error.clear();
   Handle *h = as_handle(value);
   if (!h) return fail(TX_ERR_INVALID, "null Texelator handle");
   if (!out) return fail(TX_ERR_INVALID, "null output");
+  if (dtype != TX_DTYPE_BF16 && dtype != TX_DTYPE_F16) return fail(TX_ERR_INVALID, "decode_dense: dtype must be FP16 or BF16");
   DeviceGuard guard(h->device);
-  TX_HIP(tx::launch_decode_dense(h->tiles, h->scales, h->M, h->K, h->RG, h->CG, out, reinterpret_cast<hipStream_t>(stream)));
+  TX_HIP(tx::launch_decode_dense(h->tiles, h->scales, h->M, h->K, h->RG, h->CG, dtype == TX_DTYPE_F16, out,
+                                 reinterpret_cast<hipStream_t>(stream)));
   return TX_OK;
 }
 

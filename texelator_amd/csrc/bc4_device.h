@@ -97,6 +97,21 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
+  f16x2 v = {(_Float16)a, (_Float16)b};  // v_cvt_pk_f16_f32, round-to-nearest-even
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// Two fp32 weights rounded to the 16-bit weight type: bf16 (the BF16 path) or fp16 (the FP16
+// path, texelator_cuda.cu:624).
+template <bool F16>
+__device__ __forceinline__ uint32_t pack_weights(float a, float b) {
+  if constexpr (F16) return pack_f16x2(a, b);
+  else return pack_bf16x2(a, b);
+}
+
 // 64*e from the 2-bit fields in bits 6-7 of each byte (dot4 with weights 1,4,16,64 and a
 // wrapping bias of -127*64).
 __device__ __forceinline__ float endpoint_x64(uint32_t word) {
@@ -131,11 +146,14 @@ __device__ __forceinline__ Palette palette8(uint32_t a, uint32_t b) {
   return out;
 }
 
-// Packed bf16 pair (bf16(-scale), bf16(+scale)): slots 6 and 7 of a 6-value block.
-__device__ __forceinline__ uint32_t pm_scale_pair(float scale) { return pack_bf16x2(-scale, scale); }
+// Packed 16-bit pair (-scale, +scale): slots 6 and 7 of a 6-value block.
+template <bool F16 = false>
+__device__ __forceinline__ uint32_t pm_scale_pair(float scale) { return pack_weights<F16>(-scale, scale); }
 
-// Packed bf16 weights of one block from its fp32 palette seeds. w[j] holds positions 2j (low half)
-// and 2j+1 (high half). eight: 8-value mode (e0 > e1); pm: the 6-value mode's slots 6 and 7.
+// Packed 16-bit weights (bf16, or fp16 with F16) of one block from its fp32 palette seeds. w[j]
+// holds positions 2j (low half) and 2j+1 (high half). eight: 8-value mode (e0 > e1); pm: the
+// 6-value mode's slots 6 and 7 (pm_scale_pair of the same type).
+template <bool F16 = false>
 __device__ __forceinline__ void decode_from_seeds(float base, float end, float step, bool eight, uint32_t a,
                                                   uint32_t b, float scale, uint32_t pm, uint32_t w[8]) {
   float p2 = base + step;
@@ -144,12 +162,12 @@ __device__ __forceinline__ void decode_from_seeds(float base, float end, float s
   float p5 = __builtin_fmaf(4.0f, step, base);
   float p6 = __builtin_fmaf(5.0f, step, base);
   float p7 = __builtin_fmaf(6.0f, step, base);
-  uint32_t pk01 = pack_bf16x2(base * scale, end * scale);
-  uint32_t pk23 = pack_bf16x2(p2 * scale, p3 * scale);
-  uint32_t pk45 = pack_bf16x2(p4 * scale, p5 * scale);
-  uint32_t pk67 = pack_bf16x2(p6 * scale, p7 * scale);
+  uint32_t pk01 = pack_weights<F16>(base * scale, end * scale);
+  uint32_t pk23 = pack_weights<F16>(p2 * scale, p3 * scale);
+  uint32_t pk45 = pack_weights<F16>(p4 * scale, p5 * scale);
+  uint32_t pk67 = pack_weights<F16>(p6 * scale, p7 * scale);
   pk67 = eight ? pk67 : pm;
-  // Byte tables: low and high bytes of the eight bf16 values.
+  // Byte tables: low and high bytes of the eight 16-bit values.
   uint32_t lo0 = perm(pk23, pk01, 0x06040200u);
   uint32_t hi0 = perm(pk23, pk01, 0x07050301u);
   uint32_t lo1 = perm(pk67, pk45, 0x06040200u);
@@ -165,7 +183,9 @@ __device__ __forceinline__ void decode_from_seeds(float base, float end, float s
   }
 }
 
-// Decode one device block to 16 bf16 weights, palette seeds computed in registers.
+// Decode one device block to 16 weights (bf16, or fp16 with F16), palette seeds computed in
+// registers.
+template <bool F16 = false>
 __device__ __forceinline__ void decode_block(uint32_t a, uint32_t b, float scale, uint32_t pm,
                                              uint32_t w[8]) {
   float f0 = endpoint_x64(a);
@@ -177,7 +197,7 @@ __device__ __forceinline__ void decode_block(uint32_t a, uint32_t b, float scale
   float step = __builtin_fmaf(d, rhi, d * rlo);
   float base = __builtin_fmaf(f0, kR127Hi, f0 * kR127Lo);
   float end = __builtin_fmaf(f1, kR127Hi, f1 * kR127Lo);
-  decode_from_seeds(base, end, step, eight, a, b, scale, pm, w);
+  decode_from_seeds<F16>(base, end, step, eight, a, b, scale, pm, w);
 }
 
 // LDS tables of the palette seeds, shared by a workgroup:
@@ -210,6 +230,7 @@ __device__ __forceinline__ uint32_t endpoint_offset(uint32_t word) {
 }
 
 // Decode one device block with the palette seeds read from LDS tables.
+template <bool F16 = false>
 __device__ __forceinline__ void decode_block_lds(uint32_t a, uint32_t b, float scale, uint32_t pm,
                                                  const PaletteTableStorage &t, uint32_t w[8]) {
   const uint32_t o0 = endpoint_offset(a);
@@ -220,7 +241,7 @@ __device__ __forceinline__ void decode_block_lds(uint32_t a, uint32_t b, float s
   const float base = *reinterpret_cast<const float *>(base_bytes + o0);
   const float end = *reinterpret_cast<const float *>(base_bytes + o1);
   const float step = *reinterpret_cast<const float *>(step_bytes + od);
-  decode_from_seeds(base, end, step, od < 0, a, b, scale, pm, w);
+  decode_from_seeds<F16>(base, end, step, od < 0, a, b, scale, pm, w);
 }
 
 }  // namespace tx

@@ -10,6 +10,15 @@ namespace tx {
 
 __device__ __forceinline__ float bf(uint16_t v) { return __builtin_bit_cast(float, (uint32_t)v << 16); }
 
+__device__ __forceinline__ float hf(uint16_t v) { return (float)__builtin_bit_cast(_Float16, v); }
+
+// A 16-bit value (fp16 with F16, else bf16) widened to fp32.
+template <bool F16>
+__device__ __forceinline__ float half_bits_to_float(uint16_t v) {
+  if constexpr (F16) return hf(v);
+  else return bf(v);
+}
+
 // Round to bf16, nearest-even.
 __device__ __forceinline__ uint16_t to_bf(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
 
@@ -34,16 +43,17 @@ __device__ __forceinline__ uint4 swiglu8(uint4 gv, uint4 uv) {
 // The decode GEMV's own reduction uses this, so fused consumers reproduce its output bits.
 struct SplitSource {
   const float *partials;
-  const uint16_t *bias;  // bf16 [M] or nullptr
+  const uint16_t *bias;  // [M] of the activation type (bf16, or fp16 with F16), or nullptr
   int ks, Mp, tokens;
 };
 
+template <bool F16 = false>
 __device__ __forceinline__ float split_sum(const SplitSource &s, int64_t token, int64_t m) {
   const float *p = s.partials + (size_t)token * s.Mp + m;
   const size_t stride = (size_t)s.tokens * s.Mp;
   float total = p[0];
   for (int k = 1; k < s.ks; ++k) total += p[k * stride];
-  if (s.bias) total += bf(s.bias[m]);
+  if (s.bias) total += half_bits_to_float<F16>(s.bias[m]);
   return total;
 }
 

@@ -25,17 +25,19 @@ constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ bf16x8 as_bf16x8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
-  u32x4 v = {a, b, c, d};
-  return __builtin_bit_cast(bf16x8, v);
-}
-
-__device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return as_bf16x8(v.x, v.y, v.z, v.w); }
-
-__device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+// D += A * B for 16x16x32 tiles whose operands are 8 packed 16-bit values per lane (bf16, or fp16
+// with F16).
+template <bool F16>
+__device__ __forceinline__ f32x4 mfma(uint32_t a0, uint32_t a1, uint32_t a2, uint32_t a3, uint4 b, f32x4 c) {
+  const u32x4 av = {a0, a1, a2, a3};
+  const u32x4 bv = {b.x, b.y, b.z, b.w};
+  if constexpr (F16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, av), __builtin_bit_cast(f16x8, bv), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, av), __builtin_bit_cast(bf16x8, bv), c, 0, 0, 0);
 }
 
 // x of one token, 16 k-values per block: x0/x1 = block 2kg positions 0-7 / 8-15, x2/x3 = block 2kg+1.
@@ -49,15 +51,16 @@ __device__ __forceinline__ uint4 load_x8(const uint16_t *x, int k, int K) {
 
 // One tile for one lane: decode both blocks and accumulate 4 MFMAs (block 0 into acc0, block 1
 // into acc1; the two are added at the end in a fixed order).
+template <bool F16>
 __device__ __forceinline__ void tile_mfma(uint4 cur, const XFrag &xf, float scale, uint32_t pm,
                                           const PaletteTableStorage &t, f32x4 &acc0, f32x4 &acc1) {
   uint32_t w[8];
-  decode_block_lds(cur.x, cur.y, scale, pm, t, w);
-  acc0 = mfma(as_bf16x8(w[0], w[1], w[2], w[3]), as_bf16x8(xf.x0), acc0);
-  acc0 = mfma(as_bf16x8(w[4], w[5], w[6], w[7]), as_bf16x8(xf.x1), acc0);
-  decode_block_lds(cur.z, cur.w, scale, pm, t, w);
-  acc1 = mfma(as_bf16x8(w[0], w[1], w[2], w[3]), as_bf16x8(xf.x2), acc1);
-  acc1 = mfma(as_bf16x8(w[4], w[5], w[6], w[7]), as_bf16x8(xf.x3), acc1);
+  decode_block_lds<F16>(cur.x, cur.y, scale, pm, t, w);
+  acc0 = mfma<F16>(w[0], w[1], w[2], w[3], xf.x0, acc0);
+  acc0 = mfma<F16>(w[4], w[5], w[6], w[7], xf.x1, acc0);
+  decode_block_lds<F16>(cur.z, cur.w, scale, pm, t, w);
+  acc1 = mfma<F16>(w[0], w[1], w[2], w[3], xf.x2, acc1);
+  acc1 = mfma<F16>(w[4], w[5], w[6], w[7], xf.x3, acc1);
 }
 
 // Minimum waves per SIMD the register allocation must allow (7 keeps the kernel at <= 72 VGPRs
@@ -66,7 +69,10 @@ __device__ __forceinline__ void tile_mfma(uint4 cur, const XFrag &xf, float scal
 #define TX_GEMV_WAVES_PER_EU 7
 #endif
 
-template <int LA, bool MULTI, bool F32OUT>
+// F16: fp16 activations, bias and output with fp16-rounded weights (the reference's FP16 GEMV,
+// texelator_cuda.cu:94-139, multiplies unrounded fp32 weights; the rounding costs at most 2^-11
+// relative per weight).
+template <bool F16, int LA, bool MULTI, bool F32OUT>
 __global__ __launch_bounds__(kThreads, TX_GEMV_WAVES_PER_EU) void gemv_kernel(GemvParams p) {
   extern __shared__ uint4 xs[];  // single token: x slice, 16 uint4 (128 bf16) per tile column
   __shared__ PaletteTableStorage tables;
@@ -111,7 +117,7 @@ __global__ __launch_bounds__(kThreads, TX_GEMV_WAVES_PER_EU) void gemv_kernel(Ge
   const int kg = lane >> 4;  // K chunk: blocks 2kg and 2kg+1 of each tile
   const int row = g * kTileRows + i;
   const float scale = p.scales[row];
-  const uint32_t pm = pm_scale_pair(scale);
+  const uint32_t pm = pm_scale_pair<F16>(scale);
   // Multi-token: this lane's token column (duplicates the last token past the end).
   const uint16_t *xrow = x + (size_t)(t0 + min(i, tc - 1)) * p.K;
 
@@ -135,7 +141,7 @@ __global__ __launch_bounds__(kThreads, TX_GEMV_WAVES_PER_EU) void gemv_kernel(Ge
       xf.x2 = xv[2];
       xf.x3 = xv[3];
     }
-    tile_mfma(tile, xf, scale, pm, tables, acc0, acc1);
+    tile_mfma<F16>(tile, xf, scale, pm, tables, acc0, acc1);
   };
 
   // Main loop over whole ring turns, branch-free: every step issues exactly one load (clamped to
@@ -176,8 +182,9 @@ __global__ __launch_bounds__(kThreads, TX_GEMV_WAVES_PER_EU) void gemv_kernel(Ge
       if constexpr (F32OUT) {
         static_cast<float *>(p.y)[(size_t)token * p.M + out_row] = total;
       } else {
-        if (p.bias) total += bf(static_cast<const uint16_t *>(p.bias)[out_row]);
-        static_cast<__bf16 *>(p.y)[(size_t)token * p.M + out_row] = (__bf16)total;
+        if (p.bias) total += half_bits_to_float<F16>(static_cast<const uint16_t *>(p.bias)[out_row]);
+        if constexpr (F16) static_cast<_Float16 *>(p.y)[(size_t)token * p.M + out_row] = (_Float16)total;
+        else static_cast<__bf16 *>(p.y)[(size_t)token * p.M + out_row] = (__bf16)total;
       }
     }
   }
@@ -185,37 +192,44 @@ __global__ __launch_bounds__(kThreads, TX_GEMV_WAVES_PER_EU) void gemv_kernel(Ge
 
 // y[t][m] = sum over splits s (in order) of partials[s][t][m], then bias and output cast
 // (split_sum, which fused consumers of the partials use as well).
-template <bool F32OUT>
+template <bool F16, bool F32OUT>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemvParams p) {
   const int m = blockIdx.x * 256 + threadIdx.x;
   const int token = blockIdx.y;
   if (m >= p.M) return;
   const SplitSource src{p.partials, F32OUT ? nullptr : static_cast<const uint16_t *>(p.bias), p.ks, p.Mp, p.tokens};
-  const float total = split_sum(src, token, m);
+  const float total = split_sum<F16>(src, token, m);
   if constexpr (F32OUT) {
     static_cast<float *>(p.y)[(size_t)token * p.M + m] = total;
+  } else if constexpr (F16) {
+    static_cast<_Float16 *>(p.y)[(size_t)token * p.M + m] = (_Float16)total;
   } else {
     static_cast<__bf16 *>(p.y)[(size_t)token * p.M + m] = (__bf16)total;
   }
 }
 
-template <int LA, bool MULTI, bool F32OUT>
+template <bool F16, int LA, bool MULTI, bool F32OUT>
 hipError_t launch_variant(const GemvParams &p, hipStream_t stream) {
   const int max_cols = (p.CG + p.ks - 1) / p.ks;
   const size_t lds = MULTI ? 0 : (size_t)max_cols * 16 * sizeof(uint4);
   dim3 grid(p.RG, p.ks, (p.tokens + 15) / 16);
-  hipLaunchKernelGGL((gemv_kernel<LA, MULTI, F32OUT>), grid, dim3(kThreads), lds, stream, p);
+  hipLaunchKernelGGL((gemv_kernel<F16, LA, MULTI, F32OUT>), grid, dim3(kThreads), lds, stream, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || p.ks == 1 || p.force_partials) return e;
-  hipLaunchKernelGGL((splitk_reduce_kernel<F32OUT>), dim3((p.M + 255) / 256, p.tokens), dim3(256), 0, stream, p);
+  hipLaunchKernelGGL((splitk_reduce_kernel<F16, F32OUT>), dim3((p.M + 255) / 256, p.tokens), dim3(256), 0, stream, p);
   return hipGetLastError();
 }
 
+// The fp32-output variants (parity and split consumers) exist for bf16 activations only.
 template <int LA>
 hipError_t launch_la(const GemvParams &p, bool f32_out, hipStream_t stream) {
   const bool multi = p.tokens > 1;
-  if (multi) return f32_out ? launch_variant<LA, true, true>(p, stream) : launch_variant<LA, true, false>(p, stream);
-  return f32_out ? launch_variant<LA, false, true>(p, stream) : launch_variant<LA, false, false>(p, stream);
+  if (p.f16) {
+    if (f32_out) return hipErrorInvalidValue;
+    return multi ? launch_variant<true, LA, true, false>(p, stream) : launch_variant<true, LA, false, false>(p, stream);
+  }
+  if (multi) return f32_out ? launch_variant<false, LA, true, true>(p, stream) : launch_variant<false, LA, true, false>(p, stream);
+  return f32_out ? launch_variant<false, LA, false, true>(p, stream) : launch_variant<false, LA, false, false>(p, stream);
 }
 
 }  // namespace
@@ -236,12 +250,12 @@ hipError_t launch_gemv(const GemvParams &p, int lookahead, bool f32_out, hipStre
 
 hipError_t gemv_kernel_attributes(int lookahead, hipFuncAttributes *attr) {
   switch (lookahead) {
-    case 1: return hipFuncGetAttributes(attr, reinterpret_cast<const void *>(&gemv_kernel<1, false, false>));
-    case 2: return hipFuncGetAttributes(attr, reinterpret_cast<const void *>(&gemv_kernel<2, false, false>));
-    case 3: return hipFuncGetAttributes(attr, reinterpret_cast<const void *>(&gemv_kernel<3, false, false>));
-    case 4: return hipFuncGetAttributes(attr, reinterpret_cast<const void *>(&gemv_kernel<4, false, false>));
-    case 6: return hipFuncGetAttributes(attr, reinterpret_cast<const void *>(&gemv_kernel<6, false, false>));
-    case 8: return hipFuncGetAttributes(attr, reinterpret_cast<const void *>(&gemv_kernel<8, false, false>));
+    case 1: return hipFuncGetAttributes(attr, reinterpret_cast<const void *>(&gemv_kernel<false, 1, false, false>));
+    case 2: return hipFuncGetAttributes(attr, reinterpret_cast<const void *>(&gemv_kernel<false, 2, false, false>));
+    case 3: return hipFuncGetAttributes(attr, reinterpret_cast<const void *>(&gemv_kernel<false, 3, false, false>));
+    case 4: return hipFuncGetAttributes(attr, reinterpret_cast<const void *>(&gemv_kernel<false, 4, false, false>));
+    case 6: return hipFuncGetAttributes(attr, reinterpret_cast<const void *>(&gemv_kernel<false, 6, false, false>));
+    case 8: return hipFuncGetAttributes(attr, reinterpret_cast<const void *>(&gemv_kernel<false, 8, false, false>));
     default: return hipErrorInvalidValue;
   }
 }

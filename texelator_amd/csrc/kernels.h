@@ -17,6 +17,7 @@ struct GemvParams {
   float *partials;         // [ks][tokens][Mp] when ks > 1 or force_partials
   int M, K, Mp, RG, CG, ks, tokens;
   int force_partials;      // write fp32 partials (no bias, no reduction) even when ks == 1
+  int f16;                 // x, bias and y are fp16 (weights rounded to fp16) instead of bf16
 };
 
 // Single-token GEMV stages the x slice of a split in LDS: at most this many tile columns
@@ -31,6 +32,7 @@ struct PrefillParams {
   void *y;                 // [tokens][M] bf16
   float *partials;         // [ks][tokens][Mp] when ks > 1 (caller's workspace)
   int M, K, Mp, RG, CG, tokens, ks;
+  int f16;                 // x, bias and y are fp16 (weights rounded to fp16) instead of bf16
 };
 
 // GEMV variants selected by the lookahead knob (number of 1 KiB tiles in flight per wave).
@@ -53,7 +55,7 @@ hipError_t launch_palette_probe(float *out, hipStream_t stream);
 // Reference-layout device blocks [M][bpr][8] -> device tiles (RG x CG tiles of 1 KiB).
 hipError_t launch_repack(const uint8_t *blocks, int M, int bpr, int RG, int CG, uint4 *tiles, hipStream_t stream);
 hipError_t launch_decode_dense(const uint4 *tiles, const float *scales, int M, int K, int RG, int CG,
-                               uint16_t *out, hipStream_t stream);
+                               bool f16, uint16_t *out, hipStream_t stream);
 
 // Decoder-layer helpers (decoder.hip).
 struct SplitSource;

@@ -22,6 +22,7 @@
 #include <algorithm>
 
 #include "bc4_device.h"
+#include "elementwise.h"
 #include "kernels.h"
 
 namespace tx {
@@ -33,15 +34,29 @@ constexpr int kStride = 136;  // LDS row stride of the activation tile in bf16 (
 constexpr int kXcds = 8;
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ float bf16_bits_to_float(uint16_t v) {
-  return __builtin_bit_cast(float, (uint32_t)v << 16);
+// D += A * B on 16x16x32 tiles of packed 16-bit operands (bf16, or fp16 with F16).
+template <bool F16>
+__device__ __forceinline__ f32x4 mfma(u32x4 a, u32x4 b, f32x4 c) {
+  if constexpr (F16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
 
-__device__ __forceinline__ bf16x8 as_bf16x8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
-  u32x4 v = {a, b, c, d};
-  return __builtin_bit_cast(bf16x8, v);
+// Round to the output type and widen back (bf16, or fp16 with F16).
+template <bool F16>
+__device__ __forceinline__ float round_out(float v) {
+  if constexpr (F16) return (float)(_Float16)v;
+  else return (float)(__bf16)v;
+}
+
+template <bool F16>
+__device__ __forceinline__ void store_out(void *y, size_t index, float v) {
+  if constexpr (F16) static_cast<_Float16 *>(y)[index] = (_Float16)v;
+  else static_cast<__bf16 *>(y)[index] = (__bf16)v;
 }
 
 struct WorkItem {
@@ -66,7 +81,10 @@ __device__ __forceinline__ bool work_item(const PrefillParams &p, int BT, int BN
   return true;
 }
 
-template <int MT, int NT, int LA>
+// F16: fp16 activations, bias and output, weights rounded to fp16 (the reference's FP16 prefill
+// decodes __float2half(P*scale) into its scratch matrix, texelator_cuda.cu:604-628, and adds
+// the bias with a second fp16 rounding, :630-635).
+template <bool F16, int MT, int NT, int LA>
 __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillParams p) {
   constexpr int BT = 16 * MT;
   constexpr int BN = 64 * NT;
@@ -92,7 +110,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillParams p) {
     const int g = min(w.n0 / kTileRows + wave * NT + v, p.RG - 1);
     gtiles[v] = p.tiles + ((size_t)g * p.CG + w.c_begin) * 64 + lane;
     scale[v] = p.scales[g * kTileRows + i];
-    pm[v] = pm_scale_pair(scale[v]);
+    pm[v] = pm_scale_pair<F16>(scale[v]);
   }
 
   // Weight ring: slot s holds the NT tiles of one K step.
@@ -141,25 +159,25 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillParams p) {
     for (int v = 0; v < NT; ++v) ring[(u + LA) % R][v] = load_stream(gtiles[v] + (size_t)jn * 64);
     // Decode this step's tiles into A operands: a[v][q] covers block 2kg + (q >> 1),
     // positions 8*(q & 1) .. +7, i.e. K offset 32kg + 8q within the step.
-    bf16x8 a[NT][4];
+    u32x4 a[NT][4];
 #pragma unroll
     for (int v = 0; v < NT; ++v) {
       uint32_t d[8];
-      decode_block_lds(ring[u][v].x, ring[u][v].y, scale[v], pm[v], tables, d);
-      a[v][0] = as_bf16x8(d[0], d[1], d[2], d[3]);
-      a[v][1] = as_bf16x8(d[4], d[5], d[6], d[7]);
-      decode_block_lds(ring[u][v].z, ring[u][v].w, scale[v], pm[v], tables, d);
-      a[v][2] = as_bf16x8(d[0], d[1], d[2], d[3]);
-      a[v][3] = as_bf16x8(d[4], d[5], d[6], d[7]);
+      decode_block_lds<F16>(ring[u][v].x, ring[u][v].y, scale[v], pm[v], tables, d);
+      a[v][0] = u32x4{d[0], d[1], d[2], d[3]};
+      a[v][1] = u32x4{d[4], d[5], d[6], d[7]};
+      decode_block_lds<F16>(ring[u][v].z, ring[u][v].w, scale[v], pm[v], tables, d);
+      a[v][2] = u32x4{d[0], d[1], d[2], d[3]};
+      a[v][3] = u32x4{d[4], d[5], d[6], d[7]};
     }
     const uint16_t *xb = xs[j & 1];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
 #pragma unroll
       for (int mu = 0; mu < MT; ++mu) {
-        const bf16x8 b = *reinterpret_cast<const bf16x8 *>(xb + (mu * 16 + i) * kStride + kg * 32 + q * 8);
+        const u32x4 b = *reinterpret_cast<const u32x4 *>(xb + (mu * 16 + i) * kStride + kg * 32 + q * 8);
 #pragma unroll
-        for (int v = 0; v < NT; ++v) acc[mu][v] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[v][q], b, acc[mu][v], 0, 0, 0);
+        for (int v = 0; v < NT; ++v) acc[mu][v] = mfma<F16>(a[v][q], b, acc[mu][v]);
       }
     }
     // Stage the next step's activations into the other buffer (read two steps ago).
@@ -190,14 +208,13 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillParams p) {
         float *dst = p.partials + ((size_t)w.split * p.tokens + t) * p.Mp + row0;
         if (row0 < p.Mp) *reinterpret_cast<float4 *>(dst) = make_float4(acc[mu][v][0], acc[mu][v][1], acc[mu][v][2], acc[mu][v][3]);
       } else {
-        __bf16 *y = static_cast<__bf16 *>(p.y) + (size_t)t * p.M;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int n = row0 + r;
           if (n < p.M) {
-            __bf16 out = (__bf16)acc[mu][v][r];
-            if (bias) out = (__bf16)((float)out + bf16_bits_to_float(bias[n]));
-            y[n] = out;
+            float out = round_out<F16>(acc[mu][v][r]);
+            if (bias) out += half_bits_to_float<F16>(bias[n]);
+            store_out<F16>(p.y, (size_t)t * p.M + n, out);
           }
         }
       }
@@ -205,17 +222,18 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillParams p) {
   }
 }
 
-// y[t][m] = bf16(sum over splits in order of partials[s][t][m]), then the bias with a second
-// rounding (the reference's epilogue order).
+// y[t][m] = round(sum over splits in order of partials[s][t][m]), then the bias with a second
+// rounding (the reference's epilogue order); bf16, or fp16 with F16.
+template <bool F16>
 __global__ __launch_bounds__(256) void prefill_reduce_kernel(PrefillParams p) {
   const int m = blockIdx.x * 256 + threadIdx.x;
   const int t = blockIdx.y;
   if (m >= p.M) return;
   float total = 0.f;
   for (int s = 0; s < p.ks; ++s) total += p.partials[((size_t)s * p.tokens + t) * p.Mp + m];
-  __bf16 out = (__bf16)total;
-  if (p.bias) out = (__bf16)((float)out + bf16_bits_to_float(static_cast<const uint16_t *>(p.bias)[m]));
-  static_cast<__bf16 *>(p.y)[(size_t)t * p.M + m] = out;
+  float out = round_out<F16>(total);
+  if (p.bias) out += half_bits_to_float<F16>(static_cast<const uint16_t *>(p.bias)[m]);
+  store_out<F16>(p.y, (size_t)t * p.M + m, out);
 }
 
 struct Candidate {
@@ -231,16 +249,22 @@ hipError_t launch_tile(const PrefillParams &p, hipStream_t stream) {
   constexpr int BT = 16 * MT, BN = 64 * NT;
   const int items = ((p.M + BN - 1) / BN) * ((p.tokens + BT - 1) / BT) * p.ks;
   const int grid = ((items + kXcds - 1) / kXcds) * kXcds;
-  hipLaunchKernelGGL((prefill_kernel<MT, NT, LA>), dim3(grid), dim3(kThreads), 0, stream, p);
+  if (p.f16)
+    hipLaunchKernelGGL((prefill_kernel<true, MT, NT, LA>), dim3(grid), dim3(kThreads), 0, stream, p);
+  else
+    hipLaunchKernelGGL((prefill_kernel<false, MT, NT, LA>), dim3(grid), dim3(kThreads), 0, stream, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || p.ks == 1) return e;
-  hipLaunchKernelGGL(prefill_reduce_kernel, dim3((p.M + 255) / 256, p.tokens), dim3(256), 0, stream, p);
+  if (p.f16)
+    hipLaunchKernelGGL(prefill_reduce_kernel<true>, dim3((p.M + 255) / 256, p.tokens), dim3(256), 0, stream, p);
+  else
+    hipLaunchKernelGGL(prefill_reduce_kernel<false>, dim3((p.M + 255) / 256, p.tokens), dim3(256), 0, stream, p);
   return hipGetLastError();
 }
 
 #define TX_CANDIDATE(NAME, MT, NT, LA)                                                                  \
   Candidate {                                                                                          \
-    NAME, 16 * (MT), 64 * (NT), reinterpret_cast<const void *>(&prefill_kernel<MT, NT, LA>),           \
+    NAME, 16 * (MT), 64 * (NT), reinterpret_cast<const void *>(&prefill_kernel<false, MT, NT, LA>),    \
         &launch_tile<MT, NT, LA>, 2 * 16 * (MT) * kStride * 2                                          \
   }
 

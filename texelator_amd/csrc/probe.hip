@@ -31,7 +31,9 @@ __global__ void palette_probe_kernel(float *out) {
   dst[1] = make_float4(pal.p[4], pal.p[5], pal.p[6], pal.p[7]);
 }
 
-// One thread per lane-slot of a tile: decodes two blocks into out[M][K] (bf16 bits).
+// One thread per lane-slot of a tile: decodes two blocks into out[M][K] (bf16 bits, or fp16
+// bits with F16).
+template <bool F16>
 __global__ void decode_dense_kernel(const uint4 *tiles, const float *scales, int M, int K, int RG,
                                     int CG, uint16_t *out) {
   const size_t slot = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -44,10 +46,10 @@ __global__ void decode_dense_kernel(const uint4 *tiles, const float *scales, int
   if (row >= M) return;
   const uint4 cur = tiles[slot];
   const float scale = scales[row];
-  const uint32_t pm = pm_scale_pair(scale);
+  const uint32_t pm = pm_scale_pair<F16>(scale);
   uint32_t w[2][8];
-  decode_block(cur.x, cur.y, scale, pm, w[0]);
-  decode_block(cur.z, cur.w, scale, pm, w[1]);
+  decode_block<F16>(cur.x, cur.y, scale, pm, w[0]);
+  decode_block<F16>(cur.z, cur.w, scale, pm, w[1]);
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     const int k0 = (c * kTileBlocks + 2 * (lane >> 4) + h) * 16;
@@ -69,10 +71,13 @@ hipError_t launch_palette_probe(float *out, hipStream_t stream) {
 }
 
 hipError_t launch_decode_dense(const uint4 *tiles, const float *scales, int M, int K, int RG, int CG,
-                               uint16_t *out, hipStream_t stream) {
+                               bool f16, uint16_t *out, hipStream_t stream) {
   const size_t slots = (size_t)RG * CG * 64;
-  hipLaunchKernelGGL(decode_dense_kernel, dim3((unsigned)((slots + 255) / 256)), dim3(256), 0, stream, tiles, scales,
-                     M, K, RG, CG, out);
+  const dim3 grid((unsigned)((slots + 255) / 256));
+  if (f16)
+    hipLaunchKernelGGL(decode_dense_kernel<true>, grid, dim3(256), 0, stream, tiles, scales, M, K, RG, CG, out);
+  else
+    hipLaunchKernelGGL(decode_dense_kernel<false>, grid, dim3(256), 0, stream, tiles, scales, M, K, RG, CG, out);
   return hipGetLastError();
 }
 

@@ -35,7 +35,7 @@ def _runtime_dtype(manifest: dict) -> torch.dtype:
     if name == "bfloat16":
         return torch.bfloat16
     if name == "float16":
-        raise RuntimeError("FP16 Texelator artifacts are not supported by the gfx950 BC4 path (bf16 only)")
+        return torch.float16
     raise RuntimeError(f"unsupported Texelator runtime dtype: {name!r}")
 
 
