@@ -234,6 +234,8 @@ def main() -> int:
     parser.add_argument("--prompt", type=int, default=512, help="prefill tokens")
     parser.add_argument("--decode-sample", type=int, default=64,
                         help="decode steps timed per 512-position bucket (0 = every step)")
+    parser.add_argument("--model-only", action="store_true",
+                        help="profiling mode: only the model-level prefill and decode measurement (its JSON)")
     parser.add_argument("--kernel-only", action="store_true",
                         help="profiling mode: only the gate/up GEMV over the layer copies, then a plain copy of "
                              "COPY_BYTES bytes that calibrates the HBM byte counters")
@@ -257,6 +259,9 @@ def main() -> int:
 
     if args.kernel_only:
         return kernel_only(torch, ext, runtime, hardware, device, args)
+    if args.model_only:
+        print(json.dumps({"model_only": True, "model": model_section(torch, args)}), flush=True)
+        return 0
 
     log("probing palette and encoding weights")
     lut = hardware.device_palette(device)
