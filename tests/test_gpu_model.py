@@ -258,3 +258,17 @@ def test_split_decode_step_is_bit_identical(ext, tiny):
         kb = tiny.k_cache[:, :, 30].clone()
     assert torch.equal(a, b)
     assert torch.equal(ka, kb)
+
+
+def test_prompt_flash_attention_matches_cached_attention(ext, tiny):
+    """The prompt path (causal flash attention over the prompt's own cache rows) agrees with the
+    cached fp32 attention that any other multi-token call uses."""
+    ids = prefill.prompt_ids(tiny, 48, seed=9)
+    with torch.inference_mode():
+        a = tiny.hidden_states(ids, tiny.key_positions[:48], 48).clone()
+        tiny.flash_prompt_attention = False
+        try:
+            b = tiny.hidden_states(ids, tiny.key_positions[:48], 48)
+        finally:
+            tiny.flash_prompt_attention = True
+    assert rrms(b, a) < 1e-2

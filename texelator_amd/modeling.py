@@ -26,6 +26,8 @@ from dataclasses import dataclass
 import torch
 from torch.nn import functional
 
+from torch.nn.attention import SDPBackend, sdpa_kernel
+
 from . import layers
 from .runtime import TexelatorLinear, extension, free
 
@@ -143,6 +145,7 @@ class BC4Decoder:
         self.max_context = int(max_context)
         self.fused = fused
         self.split_decode = fused and split_decode
+        self.flash_prompt_attention = fused
         ext = extension()
         c = config
         if fused and not layers.decode_attention_supported(c):
@@ -243,6 +246,20 @@ class BC4Decoder:
         rotated = torch.cat([-xf[..., half:], xf[..., :half]], dim=-1)
         return (xf * cos + rotated * sin).to(torch.bfloat16)
 
+    def _prompt_attention(self, index: int, q: torch.Tensor) -> torch.Tensor:
+        """Causal attention of a prompt (positions 0..T-1) over its own keys, q [T, heads, d], with
+        torch's flash-attention kernel (bf16 in, fp32 softmax); the prompt's keys and values are
+        the cache rows 0..T-1 that ``rope_kv_cache`` just wrote. Only the flash backend is allowed,
+        so an unsupported shape raises instead of running the unfused math path."""
+        c = self.config
+        tokens = q.shape[0]
+        keys = self.k_cache[index, :, :tokens].unsqueeze(0)        # [1, kv, T, d]
+        values = self.v_cache[index, :, :tokens].unsqueeze(0)
+        with sdpa_kernel([SDPBackend.FLASH_ATTENTION]):
+            out = functional.scaled_dot_product_attention(q.permute(1, 0, 2).unsqueeze(0), keys, values,
+                                                          is_causal=True, enable_gqa=c.heads != c.kv_heads)
+        return out[0].permute(1, 0, 2).reshape(tokens, c.heads * c.head_dim)
+
     def _cached_attention(self, index: int, q: torch.Tensor, positions: torch.Tensor, length: int) -> torch.Tensor:
         """q [T, heads, d] at ``positions`` over cache positions 0..length-1, causally.
 
@@ -282,7 +299,9 @@ class BC4Decoder:
         """Final-norm hidden states [T, hidden] (bf16) for tokens ``ids`` at ``positions``.
 
         The residual stream is kept in fp32; every linear reads bf16 activations and writes bf16
-        outputs. A single token uses the split-length decode attention (fused path)."""
+        outputs. On the fused path a single token uses the split-length decode attention, a prompt
+        (positions ``key_positions[:T]``, ``length == T``) torch's causal flash attention, and any
+        other multi-token call the cached fp32 attention."""
         c = self.config
         h = self.embed.index_select(0, ids).float()
         if not self.fused:
@@ -294,6 +313,9 @@ class BC4Decoder:
         x = layers.add_rmsnorm(h, None, self.layers[0].input_norm, c.rms_eps)
         if tokens == 1 and self.split_decode:
             return self._decode_split(h, x, positions, length, scale)
+        # a prompt at positions 0..T-1 attending to itself only: causal flash attention
+        prompt = (tokens > 1 and length == tokens and positions.data_ptr() == self.key_positions.data_ptr()
+                  and self.flash_prompt_attention)
         for index, layer in enumerate(self.layers):
             qkv = layer.linears["qkv"](x)
             q = layers.rope_kv_cache(qkv, positions, self.rope_cos, self.rope_sin, c.heads, c.kv_heads, c.head_dim,
@@ -301,6 +323,8 @@ class BC4Decoder:
             if tokens == 1:
                 attn = layers.decode_attention(q, self.k_cache[index], self.v_cache[index], positions, length, c.heads,
                                                c.kv_heads, scale, self.attention_workspace)
+            elif prompt:
+                attn = self._prompt_attention(index, q.view(tokens, c.heads, c.head_dim))
             else:
                 attn = self._cached_attention(index, q.view(tokens, c.heads, c.head_dim), positions, length)
             layers.add_rmsnorm(h, layer.linears["o"](attn), layer.post_norm, c.rms_eps, out=x)
