@@ -84,8 +84,10 @@ __device__ __forceinline__ bool work_item(const PrefillParams &p, int BT, int BN
 // F16: fp16 activations, bias and output, weights rounded to fp16 (the reference's FP16 prefill
 // decodes __float2half(P*scale) into its scratch matrix, texelator_cuda.cu:604-628, and adds
 // the bias with a second fp16 rounding, :630-635).
-template <bool F16, int MT, int NT, int LA>
+// PIPE: software-pipelined K loop (see the step below).
+template <bool F16, int MT, int NT, int LA, bool PIPE>
 __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillParams p) {
+  static_assert(!PIPE || LA >= 2, "the pipelined K loop needs two weight tiles in flight");
   constexpr int BT = 16 * MT;
   constexpr int BN = 64 * NT;
   constexpr int R = LA + 1;
@@ -152,24 +154,21 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillParams p) {
 #pragma unroll
     for (int b = 0; b < NT; ++b) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  auto step = [&](int j, int u) {
-    // Prefetch the weights LA steps ahead (clamped, so every step issues the same loads).
-    const int jn = min(j + LA, w.nc - 1);
-#pragma unroll
-    for (int v = 0; v < NT; ++v) ring[(u + LA) % R][v] = load_stream(gtiles[v] + (size_t)jn * 64);
-    // Decode this step's tiles into A operands: a[v][q] covers block 2kg + (q >> 1),
-    // positions 8*(q & 1) .. +7, i.e. K offset 32kg + 8q within the step.
-    u32x4 a[NT][4];
+  // Decode one K step's NT tiles into A operands: a[v][q] covers block 2kg + (q >> 1), positions
+  // 8*(q & 1) .. +7, i.e. K offset 32kg + 8q within the step.
+  auto decode_step = [&](const uint4 (&tiles)[NT], u32x4 (&a)[NT][4]) {
 #pragma unroll
     for (int v = 0; v < NT; ++v) {
       uint32_t d[8];
-      decode_block_lds<F16>(ring[u][v].x, ring[u][v].y, scale[v], pm[v], tables, d);
+      decode_block_lds<F16>(tiles[v].x, tiles[v].y, scale[v], pm[v], tables, d);
       a[v][0] = u32x4{d[0], d[1], d[2], d[3]};
       a[v][1] = u32x4{d[4], d[5], d[6], d[7]};
-      decode_block_lds<F16>(ring[u][v].z, ring[u][v].w, scale[v], pm[v], tables, d);
+      decode_block_lds<F16>(tiles[v].z, tiles[v].w, scale[v], pm[v], tables, d);
       a[v][2] = u32x4{d[0], d[1], d[2], d[3]};
       a[v][3] = u32x4{d[4], d[5], d[6], d[7]};
     }
+  };
+  auto mfma_step = [&](int j, const u32x4 (&a)[NT][4]) {
     const uint16_t *xb = xs[j & 1];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -180,20 +179,54 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillParams p) {
         for (int v = 0; v < NT; ++v) acc[mu][v] = mfma<F16>(a[v][q], b, acc[mu][v]);
       }
     }
-    // Stage the next step's activations into the other buffer (read two steps ago).
-    store_x((j + 1) & 1);
-    load_x(j + 2);
-    __syncthreads();
   };
 
-  int j0 = 0;
-  for (; j0 + R <= w.nc; j0 += R) {
+  // Whole ring turns, then at most LA tail steps (each step issues the same loads, clamped).
+  auto run_steps = [&](auto &&step) {
+    int j0 = 0;
+    for (; j0 + R <= w.nc; j0 += R) {
 #pragma unroll
-    for (int u = 0; u < R; ++u) step(j0 + u, u);
+      for (int u = 0; u < R; ++u) step(j0 + u, u);
+    }
+#pragma unroll
+    for (int u = 0; u < LA; ++u)
+      if (j0 + u < w.nc) step(j0 + u, u);
+  };
+
+  if constexpr (PIPE) {
+    // Software-pipelined: step j multiplies the tiles decoded during step j-1 while decoding tile
+    // j+1 (already in the ring), so the decode's VALU work and the MFMAs interleave in one
+    // instruction stream. Tile j+1 was requested a step earlier (LA >= 2).
+    u32x4 acur[NT][4];
+    decode_step(ring[0], acur);
+    run_steps([&](int j, int u) {
+      const int jn = min(j + LA, w.nc - 1);
+#pragma unroll
+      for (int v = 0; v < NT; ++v) ring[(u + LA) % R][v] = load_stream(gtiles[v] + (size_t)jn * 64);
+      u32x4 anext[NT][4];
+      decode_step(ring[(u + 1) % R], anext);  // tile j+1 (past the end: the clamped last tile, unused)
+      mfma_step(j, acur);
+      store_x((j + 1) & 1);  // the next step's activations, into the buffer read two steps ago
+      load_x(j + 2);
+      __syncthreads();
+#pragma unroll
+      for (int v = 0; v < NT; ++v)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) acur[v][q] = anext[v][q];
+    });
+  } else {
+    run_steps([&](int j, int u) {
+      const int jn = min(j + LA, w.nc - 1);
+#pragma unroll
+      for (int v = 0; v < NT; ++v) ring[(u + LA) % R][v] = load_stream(gtiles[v] + (size_t)jn * 64);
+      u32x4 a[NT][4];
+      decode_step(ring[u], a);
+      mfma_step(j, a);
+      store_x((j + 1) & 1);  // the next step's activations, into the buffer read two steps ago
+      load_x(j + 2);
+      __syncthreads();
+    });
   }
-#pragma unroll
-  for (int u = 0; u < LA; ++u)
-    if (j0 + u < w.nc) step(j0 + u, u);
 
   // acc[mu][v][r] = D[row 4kg + r of group v][token mu*16 + i].
   const uint16_t *bias = static_cast<const uint16_t *>(p.bias);
@@ -244,15 +277,15 @@ struct Candidate {
   int lds;
 };
 
-template <int MT, int NT, int LA>
+template <int MT, int NT, int LA, bool PIPE>
 hipError_t launch_tile(const PrefillParams &p, hipStream_t stream) {
   constexpr int BT = 16 * MT, BN = 64 * NT;
   const int items = ((p.M + BN - 1) / BN) * ((p.tokens + BT - 1) / BT) * p.ks;
   const int grid = ((items + kXcds - 1) / kXcds) * kXcds;
   if (p.f16)
-    hipLaunchKernelGGL((prefill_kernel<true, MT, NT, LA>), dim3(grid), dim3(kThreads), 0, stream, p);
+    hipLaunchKernelGGL((prefill_kernel<true, MT, NT, LA, PIPE>), dim3(grid), dim3(kThreads), 0, stream, p);
   else
-    hipLaunchKernelGGL((prefill_kernel<false, MT, NT, LA>), dim3(grid), dim3(kThreads), 0, stream, p);
+    hipLaunchKernelGGL((prefill_kernel<false, MT, NT, LA, PIPE>), dim3(grid), dim3(kThreads), 0, stream, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || p.ks == 1) return e;
   if (p.f16)
@@ -262,10 +295,10 @@ hipError_t launch_tile(const PrefillParams &p, hipStream_t stream) {
   return hipGetLastError();
 }
 
-#define TX_CANDIDATE(NAME, MT, NT, LA)                                                                  \
+#define TX_CANDIDATE(NAME, MT, NT, LA, PIPE)                                                            \
   Candidate {                                                                                          \
-    NAME, 16 * (MT), 64 * (NT), reinterpret_cast<const void *>(&prefill_kernel<false, MT, NT, LA>),    \
-        &launch_tile<MT, NT, LA>, 2 * 16 * (MT) * kStride * 2                                          \
+    NAME, 16 * (MT), 64 * (NT), reinterpret_cast<const void *>(&prefill_kernel<false, MT, NT, LA, PIPE>), \
+        &launch_tile<MT, NT, LA, PIPE>, 2 * 16 * (MT) * kStride * 2                                    \
   }
 
 // Weight tiles in flight per wave, in K steps.
@@ -273,12 +306,14 @@ hipError_t launch_tile(const PrefillParams &p, hipStream_t stream) {
 #define TX_PREFILL_LA 2
 #endif
 
+// The two 128-token tiles pipeline their K loop (4-5% faster at T >= 128 on the 27B shapes); the
+// smaller tiles run it plainly (pipelining cost them up to 12% at T = 32).
 const Candidate kCandidates[] = {
-    TX_CANDIDATE("large_128x256x128", 8, 4, TX_PREFILL_LA),
-    TX_CANDIDATE("medium_128x128x128", 8, 2, TX_PREFILL_LA),
-    TX_CANDIDATE("medium_64x256x128", 4, 4, TX_PREFILL_LA),
-    TX_CANDIDATE("medium_64x128x128", 4, 2, TX_PREFILL_LA),
-    TX_CANDIDATE("small_32x128x128", 2, 2, TX_PREFILL_LA),
+    TX_CANDIDATE("large_128x256x128", 8, 4, TX_PREFILL_LA, true),
+    TX_CANDIDATE("medium_128x128x128", 8, 2, TX_PREFILL_LA, true),
+    TX_CANDIDATE("medium_64x256x128", 4, 4, TX_PREFILL_LA, false),
+    TX_CANDIDATE("medium_64x128x128", 4, 2, TX_PREFILL_LA, false),
+    TX_CANDIDATE("small_32x128x128", 2, 2, TX_PREFILL_LA, false),
 };
 
 const Candidate *find(int candidate) {
