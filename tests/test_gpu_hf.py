@@ -1,0 +1,103 @@
+"""Hugging Face integration on the GPU (reference: ``runtime.install`` :210-239 driving a stock
+``transformers`` Qwen2 model, and ``cli._generate`` / ``standalone.py`` generation).
+
+A tiny random Qwen2 model is encoded with this build's PTQ encoder running on the GPU (the
+reference's ``endpoint_opt`` with the LUT on a CUDA device), written as an artifact, installed
+with ``runtime.install`` and compared with the same architecture whose linears hold the decoded
+BC4 weights as dense bf16 matrices. Attention runs through torch's flash kernel only, so no
+bf16 batched product of the math path is issued.
+"""
+from __future__ import annotations
+
+import copy
+
+import numpy as np
+import pytest
+import torch
+from torch.nn.attention import SDPBackend, sdpa_kernel
+
+from texelator_amd import artifacts, encoder, hardware, runtime
+
+pytestmark = pytest.mark.gpu
+
+transformers = pytest.importorskip("transformers")
+
+LINEARS = ("self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj", "self_attn.o_proj",
+           "mlp.gate_proj", "mlp.up_proj", "mlp.down_proj")
+
+
+def rrms(ref: torch.Tensor, got: torch.Tensor) -> float:
+    ref, got = ref.float(), got.float()
+    return float(torch.sqrt(torch.mean((got - ref) ** 2)) / torch.sqrt(torch.mean(ref ** 2)))
+
+
+@pytest.fixture(scope="module")
+def qwen_pair(ext, tmp_path_factory):
+    """(BC4-installed model, dense model on the decoded weights, handles)."""
+    torch.manual_seed(0)
+    config = transformers.Qwen2Config(vocab_size=512, hidden_size=256, intermediate_size=512, num_hidden_layers=2,
+                                      num_attention_heads=4, num_key_value_heads=2, max_position_embeddings=1024,
+                                      rope_theta=1e6, tie_word_embeddings=False, attn_implementation="sdpa")
+    dense = transformers.Qwen2ForCausalLM(config).to(device="cuda", dtype=torch.bfloat16).eval()
+    lut = hardware.device_palette("cuda")
+    matrices = []
+    for layer in range(config.num_hidden_layers):
+        for name in LINEARS:
+            module = dense.get_submodule(f"model.layers.{layer}.{name}")
+            blocks, scales = encoder.encode_matrix(module.weight.float(), torch.ones(module.in_features), lut)
+            matrices.append((f"model.layers.{layer}.{name}", blocks, scales))
+    path = artifacts.write_artifact(tmp_path_factory.mktemp("qwen") / "art", matrices, hardware.PALETTE_SHA256)
+    quantized = copy.deepcopy(dense)
+    handles = runtime.install(quantized, artifacts.weights_dir(path))
+    # the reference model: the same BC4 weights, decoded, as plain dense linears
+    for module_name, handle_module in [(n, quantized.get_submodule(n)) for n, _, _ in matrices]:
+        target = dense.get_submodule(module_name)
+        decoded = torch.cat([ext.decode_dense(h) for h in handle_module.handles], dim=0)
+        with torch.no_grad():
+            target.weight.copy_(decoded)
+    yield quantized, dense, handles
+    runtime.free(handles)
+
+
+def test_gpu_encoder_matches_cpu_encoder(ext):
+    """The PTQ encoder on the GPU chooses the CPU's endpoints and selectors for almost every block
+    (fp32 reductions may round differently on rare near-ties), with the same reconstruction error."""
+    g = torch.Generator().manual_seed(5)
+    w = torch.randn(192, 512, generator=g) * 0.02 * torch.exp(0.3 * torch.randn(512, generator=g))[None, :]
+    hdiag = torch.exp(torch.randn(512, generator=g))
+    lut_gpu = hardware.device_palette("cuda")
+    gpu_blocks, gpu_scales = encoder.encode_matrix(w.cuda(), hdiag, lut_gpu)
+    cpu_blocks, cpu_scales = encoder.encode_matrix(w, hdiag, lut_gpu.cpu())
+    assert np.array_equal(gpu_scales, cpu_scales)
+    same = np.all(gpu_blocks.reshape(-1, 8) == cpu_blocks.reshape(-1, 8), axis=1)
+    assert same.mean() >= 0.999
+
+
+def test_installed_linears_are_texelator(qwen_pair):
+    quantized, _, handles = qwen_pair
+    assert len(handles) == 14
+    assert type(quantized.get_submodule("model.layers.1.mlp.down_proj")).__name__ == "TexelatorLinear"
+
+
+@pytest.mark.parametrize("tokens", [1, 7, 40])
+def test_logits_match_dense_decoded_model(qwen_pair, tokens):
+    """Decode GEMV (1 and 7 tokens) and prefill GEMM (40 tokens) inside the HF forward."""
+    quantized, dense, _ = qwen_pair
+    ids = torch.randint(0, 512, (1, tokens), generator=torch.Generator().manual_seed(tokens)).cuda()
+    with torch.inference_mode(), sdpa_kernel([SDPBackend.FLASH_ATTENTION]):
+        got = quantized(ids).logits
+        want = dense(ids).logits
+    assert torch.isfinite(got).all()
+    assert rrms(want, got) < 2e-2
+
+
+def test_hf_generate_greedy(qwen_pair):
+    """HF ``generate`` (prefill, then cached one-token steps) through the BC4 linears."""
+    quantized, dense, _ = qwen_pair
+    ids = torch.randint(0, 512, (1, 24), generator=torch.Generator().manual_seed(3)).cuda()
+    with torch.inference_mode(), sdpa_kernel([SDPBackend.FLASH_ATTENTION]):
+        got = quantized.generate(ids, max_new_tokens=12, do_sample=False, pad_token_id=0)
+        want = dense.generate(ids, max_new_tokens=12, do_sample=False, pad_token_id=0)
+    assert got.shape == want.shape == (1, 36)
+    assert torch.equal(got[:, :24], ids)
+    assert (got[:, 24:] == want[:, 24:]).float().mean() >= 0.75
