@@ -180,14 +180,16 @@ def kernel_only(torch, ext, runtime, hardware, device, args) -> int:
     return 0
 
 
-def model_section(torch, args) -> dict:
+def model_section(torch, args, model_name: str | None = None, context: int | None = None) -> dict:
     """Prefill tok/s at ``--prompt`` tokens (reference protocol, texelator/prefill.py:63-131) and
-    graph-replayed greedy decode tok/s from the prompt up to ``--context``, on a random-init BC4
-    decoder of BASELINE config 5 (or 4)."""
+    graph-replayed greedy decode tok/s from the prompt up to ``context``, on a random-init BC4
+    decoder of BASELINE config 5 (27b) or 4 (3b)."""
     from texelator_amd import modeling, prefill
 
-    config = modeling.DecoderConfig.class_27b() if args.model == "27b" else modeling.DecoderConfig.qwen25_3b_style()
-    model = modeling.BC4Decoder(config, max_context=args.context, seed=SEED)
+    model_name = model_name or args.model
+    context = context or args.context
+    config = modeling.DecoderConfig.class_27b() if model_name == "27b" else modeling.DecoderConfig.qwen25_3b_style()
+    model = modeling.BC4Decoder(config, max_context=context, seed=SEED)
     try:
         try:
             pre = prefill.benchmark_prefill(model, tokens=args.prompt, warmup=2, runs=5)
@@ -195,19 +197,19 @@ def model_section(torch, args) -> dict:
             log(str(error))
             pre = prefill.benchmark_prefill(model, tokens=args.prompt, warmup=2, runs=5, rrms_limit=None)
             pre["correctness"]["gate_failed"] = True
-        dec = prefill.benchmark_decode(model, prompt_tokens=args.prompt, context=args.context,
+        dec = prefill.benchmark_decode(model, prompt_tokens=args.prompt, context=context,
                                        sample_steps=args.decode_sample or None)
     finally:
         model.close()
     bytes_per_token = config.bc4_bytes() + 2 * config.vocab * config.hidden
     return {
-        "config": args.model, "layers": config.layers, "hidden": config.hidden, "bc4_bytes": config.bc4_bytes(),
+        "config": model_name, "layers": config.layers, "hidden": config.hidden, "bc4_bytes": config.bc4_bytes(),
         "prefill_tokens": args.prompt,
         "prefill_tok_s": round(pre["fused_bc4_mfma"]["gpu_tokens_per_second"], 1),
         "prefill_ms": round(pre["fused_bc4_mfma"]["gpu_seconds_median"] * 1e3, 2),
         "prefill_gemv_only_tok_s": round(pre["scalar_gemv"]["gpu_tokens_per_second"], 1),
         "prefill_correctness": pre["correctness"],
-        "decode_context": [args.prompt, args.context],
+        "decode_context": [args.prompt, context],
         "decode_tok_s": round(dec["gpu_tokens_per_second"], 2),
         "decode_ms_per_token": round(dec["ms_per_token"], 3),
         "decode_projected_from_samples": dec["projected"],
@@ -231,6 +233,8 @@ def main() -> int:
     parser.add_argument("--model", choices=("27b", "3b", "none"), default="27b",
                         help="model-level decode/prefill tok/s on a random-init BASELINE config 5 (27b) or 4 (3b)")
     parser.add_argument("--context", type=int, default=4096, help="decode up to this context")
+    parser.add_argument("--no-small-model", action="store_true",
+                        help="skip the Qwen2.5-3B-style decoder (BASELINE config 4) after the 27B-class one")
     parser.add_argument("--prompt", type=int, default=512, help="prefill tokens")
     parser.add_argument("--decode-sample", type=int, default=64,
                         help="decode steps timed per 512-position bucket (0 = every step)")
@@ -394,6 +398,10 @@ def main() -> int:
     if args.model != "none":
         log(f"model-level tok/s ({args.model})")
         result["model"] = model_section(torch, args)
+    if args.model == "27b" and not args.no_small_model:
+        # BASELINE config 4 as stated there: 512-token prompt, then 256 greedy decode steps
+        log("model-level tok/s (3b)")
+        result["model_3b"] = model_section(torch, args, "3b", args.prompt + 256)
     if not args.no_cpu:
         log("cpu baseline")
         result["cpu_baseline"] = cpu_baseline(weights, args.cpu_seconds)

@@ -159,9 +159,8 @@ def benchmark_decode(model: BC4Decoder, prompt_tokens: int, context: int, warmup
     if context > model.max_context or prompt_tokens >= context:
         raise ValueError("need prompt_tokens < context <= max_context")
     ids = prompt_ids(model, prompt_tokens)
-    for length in range(512, model.max_context + 1, 512):
-        if length > prompt_tokens:
-            model.capture(length)
+    for length in sorted({model._bucket(p) for p in range(prompt_tokens, context)}):
+        model.capture(length)                     # every bucket the timed steps use, before timing
     model.prefill(ids)
     torch.cuda.synchronize()
     warm = min(warmup_steps, context - prompt_tokens - 1)
