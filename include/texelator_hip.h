@@ -90,6 +90,15 @@ int tx_set_prefill(uint64_t handle, int threshold, int tile_rows);
  * gfx950 tile candidates; 0..4 (the reference's CUDA-only backends) select the default tile. */
 int tx_set_prefill_backend(uint64_t handle, int backend);
 
+/* LUT-mode decode (no reference counterpart: on NVIDIA the texture unit is the palette). With a
+ * non-NULL device_table -- 255*255*8 float32 in the probe layout, index ((e1+127)*255+(e0+127))*8+s,
+ * 16-byte aligned, owned by the caller and kept alive while the handle uses it -- every kernel of
+ * this handle reads each block's 8 palette values from the table instead of computing this
+ * build's defined palette; weights are round(P[s] * scale[row]) as before. This decodes artifacts
+ * encoded against another palette (e.g. the NVIDIA palette an artifact bundles as
+ * hardware/common/palette.bin, packager.py:185-191) bit-exactly. NULL restores the defined palette. */
+int tx_set_palette_table(uint64_t handle, const float *device_table);
+
 /* Replaces texelator_handle_info (texelator_cuda.cu:1505-1512). Writes up to n of
  * [M, K, prefill_threshold, prefill_tile_rows, prefill_backend, pipelined(0), graphics(0),
  *  lookahead, device]. */

@@ -14,6 +14,8 @@ from . import _lib
 from ._lib import TexelatorError, UnsupportedError, check
 
 _SHAPES: dict[int, tuple[int, int]] = {}
+# LUT-mode palette tables, kept alive for as long as a handle uses them.
+_PALETTES: dict[int, torch.Tensor] = {}
 _DTYPE_CODE = {torch.float16: _lib.TX_DTYPE_F16, torch.bfloat16: _lib.TX_DTYPE_BF16}
 
 # Reference kernel-info names -> prefill candidate ids (autotune.CANDIDATES values).
@@ -225,6 +227,22 @@ def lookahead(handle: int) -> int:
 def free(handle: int) -> None:
     check(_lib.load().tx_free(handle))
     _SHAPES.pop(handle, None)
+    _PALETTES.pop(handle, None)
+
+
+def set_palette_table(handle: int, table: torch.Tensor | None) -> None:
+    """LUT-mode decode: read every block's palette from ``table`` (255 x 255 x 8 float32 on the
+    handle's device, probe layout ``[e1 + 127][e0 + 127][s]``) instead of this build's defined
+    palette; ``None`` restores the defined palette. The table is kept alive with the handle."""
+    if table is None:
+        check(_lib.load().tx_set_palette_table(handle, ctypes.c_void_p(None)))
+        _PALETTES.pop(handle, None)
+        return
+    _require(table.is_cuda and table.dtype == torch.float32 and table.numel() == 255 * 255 * 8,
+             "palette table must be a CUDA float32 tensor of 255*255*8 values")
+    table = table.contiguous()
+    check(_lib.load().tx_set_palette_table(handle, ctypes.c_void_p(table.data_ptr())))
+    _PALETTES[handle] = table
 
 
 def palette_probe() -> torch.Tensor:

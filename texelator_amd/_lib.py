@@ -39,6 +39,7 @@ SIGNATURES = {
     "tx_set_lookahead": (_I32, [_U64, _I32]),
     "tx_set_prefill": (_I32, [_U64, _I32, _I32]),
     "tx_set_prefill_backend": (_I32, [_U64, _I32]),
+    "tx_set_palette_table": (_I32, [_U64, _P]),
     "tx_handle_info": (_I32, [_U64, ctypes.POINTER(_I64), _I32]),
     "tx_free": (_I32, [_U64]),
     "tx_palette_probe": (_I32, [_P]),

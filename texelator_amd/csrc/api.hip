@@ -56,6 +56,7 @@ struct Handle {
   void *bias = nullptr;
   int bias_dtype = -1;
   float *partials = nullptr;
+  const float4 *lut = nullptr;  // LUT mode: caller-owned 255 x 255 x 8 fp32 device palette table
 
   ~Handle() {
     DeviceGuard guard(device);
@@ -128,6 +129,7 @@ int run_prefill(Handle *h, int candidate, const void *x, bool f16, int64_t token
                 int64_t workspace_bytes, hipStream_t stream) {
   tx::PrefillParams p{};
   p.f16 = f16 ? 1 : 0;
+  p.lut = h->lut;
   p.tiles = h->tiles;
   p.scales = h->scales;
   p.x = x;
@@ -160,6 +162,7 @@ int run_gemv(Handle *h, const void *x, bool f16, int64_t tokens, void *y, bool f
   if (tokens > 65535) return fail(TX_ERR_INVALID, "token grid exceeds the HIP grid.z limit");
   tx::GemvParams p{};
   p.f16 = f16 ? 1 : 0;
+  p.lut = h->lut;
   p.tiles = h->tiles;
   p.scales = h->scales;
   p.x = x;
@@ -192,6 +195,7 @@ int run_gemv_split(Handle *h, const void *x, hipStream_t stream) {
   p.ks = h->gemv_splits;
   p.partials = h->partials;
   p.force_partials = 1;
+  p.lut = h->lut;
   TX_HIP(tx::launch_gemv(p, h->lookahead, true, stream));
   return TX_OK;
 }
@@ -360,6 +364,16 @@ int tx_set_prefill(uint64_t value, int threshold, int tile_rows) {
   return TX_OK;
 }
 
+int tx_set_palette_table(uint64_t value, const float *device_table) {
+  g_last_error.clear();
+  Handle *h = as_handle(value);
+  if (!h) return fail(TX_ERR_INVALID, "null Texelator handle");
+  if (device_table && reinterpret_cast<uintptr_t>(device_table) % 16 != 0)
+    return fail(TX_ERR_INVALID, "palette table must be 16-byte aligned");
+  h->lut = reinterpret_cast<const float4 *>(device_table);
+  return TX_OK;
+}
+
 int tx_set_prefill_backend(uint64_t value, int backend) {
   g_last_error.clear();
   Handle *h = as_handle(value);
@@ -411,7 +425,7 @@ int tx_decode_dense(uint64_t value, int dtype, uint16_t *out, void *stream) {
   if (!out) return fail(TX_ERR_INVALID, "null output");
   if (dtype != TX_DTYPE_BF16 && dtype != TX_DTYPE_F16) return fail(TX_ERR_INVALID, "decode_dense: dtype must be FP16 or BF16");
   DeviceGuard guard(h->device);
-  TX_HIP(tx::launch_decode_dense(h->tiles, h->scales, h->M, h->K, h->RG, h->CG, dtype == TX_DTYPE_F16, out,
+  TX_HIP(tx::launch_decode_dense(h->tiles, h->scales, h->lut, h->M, h->K, h->RG, h->CG, dtype == TX_DTYPE_F16, out,
                                  reinterpret_cast<hipStream_t>(stream)));
   return TX_OK;
 }

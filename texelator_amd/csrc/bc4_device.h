@@ -150,23 +150,10 @@ __device__ __forceinline__ Palette palette8(uint32_t a, uint32_t b) {
 template <bool F16 = false>
 __device__ __forceinline__ uint32_t pm_scale_pair(float scale) { return pack_weights<F16>(-scale, scale); }
 
-// Packed 16-bit weights (bf16, or fp16 with F16) of one block from its fp32 palette seeds. w[j]
-// holds positions 2j (low half) and 2j+1 (high half). eight: 8-value mode (e0 > e1); pm: the
-// 6-value mode's slots 6 and 7 (pm_scale_pair of the same type).
-template <bool F16 = false>
-__device__ __forceinline__ void decode_from_seeds(float base, float end, float step, bool eight, uint32_t a,
-                                                  uint32_t b, float scale, uint32_t pm, uint32_t w[8]) {
-  float p2 = base + step;
-  float p3 = __builtin_fmaf(2.0f, step, base);
-  float p4 = __builtin_fmaf(3.0f, step, base);
-  float p5 = __builtin_fmaf(4.0f, step, base);
-  float p6 = __builtin_fmaf(5.0f, step, base);
-  float p7 = __builtin_fmaf(6.0f, step, base);
-  uint32_t pk01 = pack_weights<F16>(base * scale, end * scale);
-  uint32_t pk23 = pack_weights<F16>(p2 * scale, p3 * scale);
-  uint32_t pk45 = pack_weights<F16>(p4 * scale, p5 * scale);
-  uint32_t pk67 = pack_weights<F16>(p6 * scale, p7 * scale);
-  pk67 = eight ? pk67 : pm;
+// The 16 packed weights of one block from its 8 scaled palette values packed in pairs (pk01 =
+// values 0 and 1, ...). w[j] holds positions 2j (low half) and 2j+1 (high half).
+__device__ __forceinline__ void select_weights(uint32_t pk01, uint32_t pk23, uint32_t pk45, uint32_t pk67, uint32_t a,
+                                               uint32_t b, uint32_t w[8]) {
   // Byte tables: low and high bytes of the eight 16-bit values.
   uint32_t lo0 = perm(pk23, pk01, 0x06040200u);
   uint32_t hi0 = perm(pk23, pk01, 0x07050301u);
@@ -181,6 +168,43 @@ __device__ __forceinline__ void decode_from_seeds(float base, float end, float s
     w[2 * g] = perm(h, l, 0x05010400u);
     w[2 * g + 1] = perm(h, l, 0x07030602u);
   }
+}
+
+// Packed 16-bit weights (bf16, or fp16 with F16) of one block from its fp32 palette seeds.
+// eight: 8-value mode (e0 > e1); pm: the 6-value mode's slots 6 and 7 (pm_scale_pair of the same
+// type).
+template <bool F16 = false>
+__device__ __forceinline__ void decode_from_seeds(float base, float end, float step, bool eight, uint32_t a,
+                                                  uint32_t b, float scale, uint32_t pm, uint32_t w[8]) {
+  float p2 = base + step;
+  float p3 = __builtin_fmaf(2.0f, step, base);
+  float p4 = __builtin_fmaf(3.0f, step, base);
+  float p5 = __builtin_fmaf(4.0f, step, base);
+  float p6 = __builtin_fmaf(5.0f, step, base);
+  float p7 = __builtin_fmaf(6.0f, step, base);
+  uint32_t pk01 = pack_weights<F16>(base * scale, end * scale);
+  uint32_t pk23 = pack_weights<F16>(p2 * scale, p3 * scale);
+  uint32_t pk45 = pack_weights<F16>(p4 * scale, p5 * scale);
+  uint32_t pk67 = pack_weights<F16>(p6 * scale, p7 * scale);
+  pk67 = eight ? pk67 : pm;
+  select_weights(pk01, pk23, pk45, pk67, a, b, w);
+}
+
+// Packed 16-bit weights of one block whose 8 palette values come from a table row (LUT mode:
+// any palette, e.g. one measured from another GPU's texture unit): round(P[s] * scale).
+template <bool F16 = false>
+__device__ __forceinline__ void decode_from_palette(float4 p03, float4 p47, uint32_t a, uint32_t b, float scale,
+                                                    uint32_t w[8]) {
+  select_weights(pack_weights<F16>(p03.x * scale, p03.y * scale), pack_weights<F16>(p03.z * scale, p03.w * scale),
+                 pack_weights<F16>(p47.x * scale, p47.y * scale), pack_weights<F16>(p47.z * scale, p47.w * scale), a, b, w);
+}
+
+// Row of a block's endpoint pair in a 255 x 255 x 8 palette table, (e1 + 127) * 255 + (e0 + 127)
+// (the probe layout), from the device words' 2-bit endpoint fields.
+__device__ __forceinline__ uint32_t palette_row(uint32_t a, uint32_t b) {
+  const uint32_t eb0 = __builtin_amdgcn_udot4(a & 0xC0C0C0C0u, 0x40100401u, 0u, false) >> 6;
+  const uint32_t eb1 = __builtin_amdgcn_udot4(b & 0xC0C0C0C0u, 0x40100401u, 0u, false) >> 6;
+  return eb1 * 255u + eb0;
 }
 
 // Decode one device block to 16 weights (bf16, or fp16 with F16), palette seeds computed in

@@ -63,6 +63,30 @@ __device__ __forceinline__ void tile_mfma(uint4 cur, const XFrag &xf, float scal
   acc1 = mfma<F16>(w[4], w[5], w[6], w[7], xf.x3, acc1);
 }
 
+// Palette rows (8 fp32 values each) of a tile's two blocks, for LUT mode.
+struct TileRows {
+  float4 a03, a47, b03, b47;
+};
+
+__device__ __forceinline__ TileRows tile_rows(const float4 *lut, uint4 tile) {
+  const float4 *ra = lut + 2 * (size_t)palette_row(tile.x, tile.y);
+  const float4 *rb = lut + 2 * (size_t)palette_row(tile.z, tile.w);
+  return TileRows{ra[0], ra[1], rb[0], rb[1]};
+}
+
+// LUT mode: the tile's weights from its palette rows.
+template <bool F16>
+__device__ __forceinline__ void tile_mfma_lut(uint4 cur, const TileRows &rows, const XFrag &xf, float scale,
+                                              f32x4 &acc0, f32x4 &acc1) {
+  uint32_t w[8];
+  decode_from_palette<F16>(rows.a03, rows.a47, cur.x, cur.y, scale, w);
+  acc0 = mfma<F16>(w[0], w[1], w[2], w[3], xf.x0, acc0);
+  acc0 = mfma<F16>(w[4], w[5], w[6], w[7], xf.x1, acc0);
+  decode_from_palette<F16>(rows.b03, rows.b47, cur.z, cur.w, scale, w);
+  acc1 = mfma<F16>(w[0], w[1], w[2], w[3], xf.x2, acc1);
+  acc1 = mfma<F16>(w[4], w[5], w[6], w[7], xf.x3, acc1);
+}
+
 // Minimum waves per SIMD the register allocation must allow (7 keeps the kernel at <= 72 VGPRs
 // without spills, so seven 4-wave workgroups fit on a CU).
 #ifndef TX_GEMV_WAVES_PER_EU
@@ -72,8 +96,11 @@ __device__ __forceinline__ void tile_mfma(uint4 cur, const XFrag &xf, float scal
 // F16: fp16 activations, bias and output with fp16-rounded weights (the reference's FP16 GEMV,
 // texelator_cuda.cu:94-139, multiplies unrounded fp32 weights; the rounding costs at most 2^-11
 // relative per weight).
-template <bool F16, int LA, bool MULTI, bool F32OUT>
-__global__ __launch_bounds__(kThreads, TX_GEMV_WAVES_PER_EU) void gemv_kernel(GemvParams p) {
+// LUT: the palette of every block is read from a 255 x 255 x 8 table (p.lut) instead of being
+// computed; the rows of tile j+1 are fetched while tile j is decoded (needs LA >= 2).
+template <bool F16, int LA, bool MULTI, bool F32OUT, bool LUT>
+__global__ __launch_bounds__(kThreads, LUT ? 4 : TX_GEMV_WAVES_PER_EU) void gemv_kernel(GemvParams p) {
+  static_assert(!LUT || LA >= 2, "LUT mode prefetches the palette rows of the next tile");
   extern __shared__ uint4 xs[];  // single token: x slice, 16 uint4 (128 bf16) per tile column
   __shared__ PaletteTableStorage tables;
   __shared__ float red[kWaves][16][16];  // [wave][token][row]
@@ -104,7 +131,7 @@ __global__ __launch_bounds__(kThreads, TX_GEMV_WAVES_PER_EU) void gemv_kernel(Ge
   for (int u = 0; u < LA; ++u)
     ring[u] = load_stream(wave_tiles + (size_t)min(u, max(nt - 1, 0)) * kWaves * 64 + lane);
 
-  build_palette_tables(tables, threadIdx.x, kThreads);
+  if constexpr (!LUT) build_palette_tables(tables, threadIdx.x, kThreads);
   if constexpr (!MULTI) {
     for (int idx = threadIdx.x; idx < nc * 16; idx += kThreads) {
       const int k0 = (c_begin * 16 + idx) * 8;
@@ -126,7 +153,7 @@ __global__ __launch_bounds__(kThreads, TX_GEMV_WAVES_PER_EU) void gemv_kernel(Ge
   // produce output columns that are never read, so their lanes skip the LDS reads and keep
   // whatever their registers hold.
   XFrag xf = {};
-  auto consume = [&](const uint4 &tile, int j) {
+  auto load_xf = [&](int j) {
     const int col = j * kWaves + wave;  // tile column within this split
     if constexpr (MULTI) {
       const int k = (c_begin + col) * kTileK + kg * 32;
@@ -141,24 +168,52 @@ __global__ __launch_bounds__(kThreads, TX_GEMV_WAVES_PER_EU) void gemv_kernel(Ge
       xf.x2 = xv[2];
       xf.x3 = xv[3];
     }
-    tile_mfma<F16>(tile, xf, scale, pm, tables, acc0, acc1);
   };
 
   // Main loop over whole ring turns, branch-free: every step issues exactly one load (clamped to
   // the wave's last tile near the end), so each decode waits only for its own tile.
   int j0 = 0;
-  for (; j0 + R <= nt; j0 += R) {
+  if constexpr (LUT) {
+    const float4 *lut = p.lut;
+    TileRows cur = tile_rows(lut, ring[0]);
+    for (; j0 + R <= nt; j0 += R) {
 #pragma unroll
-    for (int u = 0; u < R; ++u) {
-      const int jn = min(j0 + u + LA, nt - 1);
-      ring[(u + LA) % R] = load_stream(wave_tiles + (size_t)jn * kWaves * 64 + lane);
-      consume(ring[u], j0 + u);
+      for (int u = 0; u < R; ++u) {
+        const int jn = min(j0 + u + LA, nt - 1);
+        ring[(u + LA) % R] = load_stream(wave_tiles + (size_t)jn * kWaves * 64 + lane);
+        const TileRows next = tile_rows(lut, ring[(u + 1) % R]);  // tile j+1 (clamped near the end)
+        load_xf(j0 + u);
+        tile_mfma_lut<F16>(ring[u], cur, xf, scale, acc0, acc1);
+        cur = next;
+      }
     }
-  }
-  // Tail: at most LA tiles, already in slots 0..LA-1.
 #pragma unroll
-  for (int u = 0; u < LA; ++u)
-    if (j0 + u < nt) consume(ring[u], j0 + u);
+    for (int u = 0; u < LA; ++u) {
+      const TileRows next = tile_rows(lut, ring[(u + 1) % R]);
+      if (j0 + u < nt) {
+        load_xf(j0 + u);
+        tile_mfma_lut<F16>(ring[u], cur, xf, scale, acc0, acc1);
+      }
+      cur = next;
+    }
+  } else {
+    for (; j0 + R <= nt; j0 += R) {
+#pragma unroll
+      for (int u = 0; u < R; ++u) {
+        const int jn = min(j0 + u + LA, nt - 1);
+        ring[(u + LA) % R] = load_stream(wave_tiles + (size_t)jn * kWaves * 64 + lane);
+        load_xf(j0 + u);
+        tile_mfma<F16>(ring[u], xf, scale, pm, tables, acc0, acc1);
+      }
+    }
+    // Tail: at most LA tiles, already in slots 0..LA-1.
+#pragma unroll
+    for (int u = 0; u < LA; ++u)
+      if (j0 + u < nt) {
+        load_xf(j0 + u);
+        tile_mfma<F16>(ring[u], xf, scale, pm, tables, acc0, acc1);
+      }
+  }
 
   // acc[r] = partial y[token i][row 4kg + r] of this wave.
   const f32x4 acc = acc0 + acc1;
@@ -213,7 +268,12 @@ hipError_t launch_variant(const GemvParams &p, hipStream_t stream) {
   const int max_cols = (p.CG + p.ks - 1) / p.ks;
   const size_t lds = MULTI ? 0 : (size_t)max_cols * 16 * sizeof(uint4);
   dim3 grid(p.RG, p.ks, (p.tokens + 15) / 16);
-  hipLaunchKernelGGL((gemv_kernel<F16, LA, MULTI, F32OUT>), grid, dim3(kThreads), lds, stream, p);
+  if (p.lut) {
+    constexpr int kLutLA = LA < 2 ? 2 : LA;  // the palette-row prefetch needs a second tile in flight
+    hipLaunchKernelGGL((gemv_kernel<F16, kLutLA, MULTI, F32OUT, true>), grid, dim3(kThreads), lds, stream, p);
+  } else {
+    hipLaunchKernelGGL((gemv_kernel<F16, LA, MULTI, F32OUT, false>), grid, dim3(kThreads), lds, stream, p);
+  }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || p.ks == 1 || p.force_partials) return e;
   hipLaunchKernelGGL((splitk_reduce_kernel<F16, F32OUT>), dim3((p.M + 255) / 256, p.tokens), dim3(256), 0, stream, p);
@@ -250,12 +310,12 @@ hipError_t launch_gemv(const GemvParams &p, int lookahead, bool f32_out, hipStre
 
 hipError_t gemv_kernel_attributes(int lookahead, hipFuncAttributes *attr) {
   switch (lookahead) {
-    case 1: return hipFuncGetAttributes(attr, reinterpret_cast<const void *>(&gemv_kernel<false, 1, false, false>));
-    case 2: return hipFuncGetAttributes(attr, reinterpret_cast<const void *>(&gemv_kernel<false, 2, false, false>));
-    case 3: return hipFuncGetAttributes(attr, reinterpret_cast<const void *>(&gemv_kernel<false, 3, false, false>));
-    case 4: return hipFuncGetAttributes(attr, reinterpret_cast<const void *>(&gemv_kernel<false, 4, false, false>));
-    case 6: return hipFuncGetAttributes(attr, reinterpret_cast<const void *>(&gemv_kernel<false, 6, false, false>));
-    case 8: return hipFuncGetAttributes(attr, reinterpret_cast<const void *>(&gemv_kernel<false, 8, false, false>));
+    case 1: return hipFuncGetAttributes(attr, reinterpret_cast<const void *>(&gemv_kernel<false, 1, false, false, false>));
+    case 2: return hipFuncGetAttributes(attr, reinterpret_cast<const void *>(&gemv_kernel<false, 2, false, false, false>));
+    case 3: return hipFuncGetAttributes(attr, reinterpret_cast<const void *>(&gemv_kernel<false, 3, false, false, false>));
+    case 4: return hipFuncGetAttributes(attr, reinterpret_cast<const void *>(&gemv_kernel<false, 4, false, false, false>));
+    case 6: return hipFuncGetAttributes(attr, reinterpret_cast<const void *>(&gemv_kernel<false, 6, false, false, false>));
+    case 8: return hipFuncGetAttributes(attr, reinterpret_cast<const void *>(&gemv_kernel<false, 8, false, false, false>));
     default: return hipErrorInvalidValue;
   }
 }

@@ -18,6 +18,7 @@ struct GemvParams {
   int M, K, Mp, RG, CG, ks, tokens;
   int force_partials;      // write fp32 partials (no bias, no reduction) even when ks == 1
   int f16;                 // x, bias and y are fp16 (weights rounded to fp16) instead of bf16
+  const float4 *lut;       // LUT mode: 255 x 255 x 8 fp32 palette table, or nullptr (defined palette)
 };
 
 // Single-token GEMV stages the x slice of a split in LDS: at most this many tile columns
@@ -33,6 +34,7 @@ struct PrefillParams {
   float *partials;         // [ks][tokens][Mp] when ks > 1 (caller's workspace)
   int M, K, Mp, RG, CG, tokens, ks;
   int f16;                 // x, bias and y are fp16 (weights rounded to fp16) instead of bf16
+  const float4 *lut;       // LUT mode: 255 x 255 x 8 fp32 palette table, or nullptr (defined palette)
 };
 
 // GEMV variants selected by the lookahead knob (number of 1 KiB tiles in flight per wave).
@@ -54,7 +56,7 @@ void prefill_candidate_shape(int candidate, int *tokens, int *rows, int *k);
 hipError_t launch_palette_probe(float *out, hipStream_t stream);
 // Reference-layout device blocks [M][bpr][8] -> device tiles (RG x CG tiles of 1 KiB).
 hipError_t launch_repack(const uint8_t *blocks, int M, int bpr, int RG, int CG, uint4 *tiles, hipStream_t stream);
-hipError_t launch_decode_dense(const uint4 *tiles, const float *scales, int M, int K, int RG, int CG,
+hipError_t launch_decode_dense(const uint4 *tiles, const float *scales, const float4 *lut, int M, int K, int RG, int CG,
                                bool f16, uint16_t *out, hipStream_t stream);
 
 // Decoder-layer helpers (decoder.hip).

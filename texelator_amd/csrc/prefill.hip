@@ -84,8 +84,9 @@ __device__ __forceinline__ bool work_item(const PrefillParams &p, int BT, int BN
 // F16: fp16 activations, bias and output, weights rounded to fp16 (the reference's FP16 prefill
 // decodes __float2half(P*scale) into its scratch matrix, texelator_cuda.cu:604-628, and adds
 // the bias with a second fp16 rounding, :630-635).
-// PIPE: software-pipelined K loop (see the step below).
-template <bool F16, int MT, int NT, int LA, bool PIPE>
+// PIPE: software-pipelined K loop (see the step below). LUT: palettes read from p.lut (a
+// 255 x 255 x 8 fp32 table) instead of computed.
+template <bool F16, int MT, int NT, int LA, bool PIPE, bool LUT>
 __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillParams p) {
   static_assert(!PIPE || LA >= 2, "the pipelined K loop needs two weight tiles in flight");
   constexpr int BT = 16 * MT;
@@ -145,7 +146,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillParams p) {
   load_x(0);
   store_x(0);
   load_x(1);
-  build_palette_tables(tables, threadIdx.x, kThreads);
+  if constexpr (!LUT) build_palette_tables(tables, threadIdx.x, kThreads);
   __syncthreads();
 
   f32x4 acc[MT][NT];
@@ -157,15 +158,38 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillParams p) {
   // Decode one K step's NT tiles into A operands: a[v][q] covers block 2kg + (q >> 1), positions
   // 8*(q & 1) .. +7, i.e. K offset 32kg + 8q within the step.
   auto decode_step = [&](const uint4 (&tiles)[NT], u32x4 (&a)[NT][4]) {
+    if constexpr (LUT) {
+      float4 rows[NT][4];  // all palette rows of the step in flight together
 #pragma unroll
-    for (int v = 0; v < NT; ++v) {
-      uint32_t d[8];
-      decode_block_lds<F16>(tiles[v].x, tiles[v].y, scale[v], pm[v], tables, d);
-      a[v][0] = u32x4{d[0], d[1], d[2], d[3]};
-      a[v][1] = u32x4{d[4], d[5], d[6], d[7]};
-      decode_block_lds<F16>(tiles[v].z, tiles[v].w, scale[v], pm[v], tables, d);
-      a[v][2] = u32x4{d[0], d[1], d[2], d[3]};
-      a[v][3] = u32x4{d[4], d[5], d[6], d[7]};
+      for (int v = 0; v < NT; ++v) {
+        const float4 *ra = p.lut + 2 * (size_t)palette_row(tiles[v].x, tiles[v].y);
+        const float4 *rb = p.lut + 2 * (size_t)palette_row(tiles[v].z, tiles[v].w);
+        rows[v][0] = ra[0];
+        rows[v][1] = ra[1];
+        rows[v][2] = rb[0];
+        rows[v][3] = rb[1];
+      }
+#pragma unroll
+      for (int v = 0; v < NT; ++v) {
+        uint32_t d[8];
+        decode_from_palette<F16>(rows[v][0], rows[v][1], tiles[v].x, tiles[v].y, scale[v], d);
+        a[v][0] = u32x4{d[0], d[1], d[2], d[3]};
+        a[v][1] = u32x4{d[4], d[5], d[6], d[7]};
+        decode_from_palette<F16>(rows[v][2], rows[v][3], tiles[v].z, tiles[v].w, scale[v], d);
+        a[v][2] = u32x4{d[0], d[1], d[2], d[3]};
+        a[v][3] = u32x4{d[4], d[5], d[6], d[7]};
+      }
+    } else {
+#pragma unroll
+      for (int v = 0; v < NT; ++v) {
+        uint32_t d[8];
+        decode_block_lds<F16>(tiles[v].x, tiles[v].y, scale[v], pm[v], tables, d);
+        a[v][0] = u32x4{d[0], d[1], d[2], d[3]};
+        a[v][1] = u32x4{d[4], d[5], d[6], d[7]};
+        decode_block_lds<F16>(tiles[v].z, tiles[v].w, scale[v], pm[v], tables, d);
+        a[v][2] = u32x4{d[0], d[1], d[2], d[3]};
+        a[v][3] = u32x4{d[4], d[5], d[6], d[7]};
+      }
     }
   };
   auto mfma_step = [&](int j, const u32x4 (&a)[NT][4]) {
@@ -282,10 +306,16 @@ hipError_t launch_tile(const PrefillParams &p, hipStream_t stream) {
   constexpr int BT = 16 * MT, BN = 64 * NT;
   const int items = ((p.M + BN - 1) / BN) * ((p.tokens + BT - 1) / BT) * p.ks;
   const int grid = ((items + kXcds - 1) / kXcds) * kXcds;
-  if (p.f16)
-    hipLaunchKernelGGL((prefill_kernel<true, MT, NT, LA, PIPE>), dim3(grid), dim3(kThreads), 0, stream, p);
-  else
-    hipLaunchKernelGGL((prefill_kernel<false, MT, NT, LA, PIPE>), dim3(grid), dim3(kThreads), 0, stream, p);
+  if (p.lut) {
+    if (p.f16)
+      hipLaunchKernelGGL((prefill_kernel<true, MT, NT, LA, PIPE, true>), dim3(grid), dim3(kThreads), 0, stream, p);
+    else
+      hipLaunchKernelGGL((prefill_kernel<false, MT, NT, LA, PIPE, true>), dim3(grid), dim3(kThreads), 0, stream, p);
+  } else if (p.f16) {
+    hipLaunchKernelGGL((prefill_kernel<true, MT, NT, LA, PIPE, false>), dim3(grid), dim3(kThreads), 0, stream, p);
+  } else {
+    hipLaunchKernelGGL((prefill_kernel<false, MT, NT, LA, PIPE, false>), dim3(grid), dim3(kThreads), 0, stream, p);
+  }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || p.ks == 1) return e;
   if (p.f16)
@@ -297,7 +327,7 @@ hipError_t launch_tile(const PrefillParams &p, hipStream_t stream) {
 
 #define TX_CANDIDATE(NAME, MT, NT, LA, PIPE)                                                            \
   Candidate {                                                                                          \
-    NAME, 16 * (MT), 64 * (NT), reinterpret_cast<const void *>(&prefill_kernel<false, MT, NT, LA, PIPE>), \
+    NAME, 16 * (MT), 64 * (NT), reinterpret_cast<const void *>(&prefill_kernel<false, MT, NT, LA, PIPE, false>), \
         &launch_tile<MT, NT, LA, PIPE>, 2 * 16 * (MT) * kStride * 2                                    \
   }
 

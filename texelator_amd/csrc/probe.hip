@@ -34,7 +34,7 @@ __global__ void palette_probe_kernel(float *out) {
 // One thread per lane-slot of a tile: decodes two blocks into out[M][K] (bf16 bits, or fp16
 // bits with F16).
 template <bool F16>
-__global__ void decode_dense_kernel(const uint4 *tiles, const float *scales, int M, int K, int RG,
+__global__ void decode_dense_kernel(const uint4 *tiles, const float *scales, const float4 *lut, int M, int K, int RG,
                                     int CG, uint16_t *out) {
   const size_t slot = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (slot >= (size_t)RG * CG * 64) return;
@@ -48,8 +48,15 @@ __global__ void decode_dense_kernel(const uint4 *tiles, const float *scales, int
   const float scale = scales[row];
   const uint32_t pm = pm_scale_pair<F16>(scale);
   uint32_t w[2][8];
-  decode_block<F16>(cur.x, cur.y, scale, pm, w[0]);
-  decode_block<F16>(cur.z, cur.w, scale, pm, w[1]);
+  if (lut) {  // LUT mode: the palette rows come from the table
+    const float4 *ra = lut + 2 * (size_t)palette_row(cur.x, cur.y);
+    const float4 *rb = lut + 2 * (size_t)palette_row(cur.z, cur.w);
+    decode_from_palette<F16>(ra[0], ra[1], cur.x, cur.y, scale, w[0]);
+    decode_from_palette<F16>(rb[0], rb[1], cur.z, cur.w, scale, w[1]);
+  } else {
+    decode_block<F16>(cur.x, cur.y, scale, pm, w[0]);
+    decode_block<F16>(cur.z, cur.w, scale, pm, w[1]);
+  }
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     const int k0 = (c * kTileBlocks + 2 * (lane >> 4) + h) * 16;
@@ -70,14 +77,14 @@ hipError_t launch_palette_probe(float *out, hipStream_t stream) {
   return hipGetLastError();
 }
 
-hipError_t launch_decode_dense(const uint4 *tiles, const float *scales, int M, int K, int RG, int CG,
+hipError_t launch_decode_dense(const uint4 *tiles, const float *scales, const float4 *lut, int M, int K, int RG, int CG,
                                bool f16, uint16_t *out, hipStream_t stream) {
   const size_t slots = (size_t)RG * CG * 64;
   const dim3 grid((unsigned)((slots + 255) / 256));
   if (f16)
-    hipLaunchKernelGGL(decode_dense_kernel<true>, grid, dim3(256), 0, stream, tiles, scales, M, K, RG, CG, out);
+    hipLaunchKernelGGL(decode_dense_kernel<true>, grid, dim3(256), 0, stream, tiles, scales, lut, M, K, RG, CG, out);
   else
-    hipLaunchKernelGGL(decode_dense_kernel<false>, grid, dim3(256), 0, stream, tiles, scales, M, K, RG, CG, out);
+    hipLaunchKernelGGL(decode_dense_kernel<false>, grid, dim3(256), 0, stream, tiles, scales, lut, M, K, RG, CG, out);
   return hipGetLastError();
 }
 

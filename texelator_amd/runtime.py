@@ -131,18 +131,49 @@ def pack_arrays(blocks: np.ndarray, scales: np.ndarray, bias: torch.Tensor | Non
 
 
 def pack_entry_handles(weights: Path, entry: dict, bias: torch.Tensor | None = None, lookahead: int = 1,
-                       max_texture_rows: int = 32768) -> list[int]:
-    """Pack one matrix, splitting very tall outputs into independent handles (``runtime.py:179-207``)."""
+                       max_texture_rows: int = 32768, palette: torch.Tensor | None = None) -> list[int]:
+    """Pack one matrix, splitting very tall outputs into independent handles (``runtime.py:179-207``).
+    ``palette`` (a device table from :func:`artifact_palette`) switches the handles to LUT mode."""
     m, k = int(entry["M"]), int(entry["K"])
     if max_texture_rows <= 0:
         raise ValueError("max_texture_rows must be positive")
     raw_blocks = np.memmap(weights / entry["blocks_file"], dtype=np.uint8, mode="r", shape=(m, (k // 16) * 8))
     raw_scales = np.memmap(weights / entry["scales_file"], dtype="<f4", mode="r", shape=(m,))
-    return pack_arrays(raw_blocks, raw_scales, bias=bias, lookahead=lookahead, max_rows=max_texture_rows)
+    handles = pack_arrays(raw_blocks, raw_scales, bias=bias, lookahead=lookahead, max_rows=max_texture_rows)
+    if palette is not None:
+        for handle in handles:
+            extension().set_palette_table(handle, palette)
+    return handles
 
 
-def install(model: nn.Module, weights: Path, lookahead: int = 1, fp16_prefill: bool = False) -> list[int]:
-    """Replace the linears listed in ``weights/metadata.json`` (``runtime.py:210-239``)."""
+def artifact_palette(artifact: Path, device: torch.device | str = "cuda") -> torch.Tensor | None:
+    """The palette table an artifact's blocks must be decoded with, or ``None`` when that is this
+    build's defined palette (decoded arithmetically).
+
+    An artifact encoded on another GPU (the reference's NVIDIA texture palette) names its palette
+    by hash and bundles the table (``manifest["hardware"]["palette"]``, by default
+    ``hardware/common/palette.bin``; ``packager.py:185-191``, ``standalone.py:68-70``). The
+    reference refuses such an artifact unless this GPU reproduces the palette; here it runs in
+    LUT mode instead, bit-exact to that palette."""
+    from .artifacts import read_manifest, sha256_file
+    from .hardware import PALETTE_SHA256
+    from .encoder import load_palette
+
+    artifact = Path(artifact)
+    hardware = read_manifest(artifact).get("hardware", {})
+    expected = hardware.get("palette_sha256")
+    if expected is None or expected == PALETTE_SHA256:
+        return None
+    bundled = artifact / hardware.get("palette", "hardware/common/palette.bin")
+    if not bundled.is_file() or sha256_file(bundled) != expected:
+        raise RuntimeError("bundled model palette is missing or corrupt")
+    return load_palette(bundled, device).reshape(-1).contiguous()
+
+
+def install(model: nn.Module, weights: Path, lookahead: int = 1, fp16_prefill: bool = False,
+            palette: torch.Tensor | None = None) -> list[int]:
+    """Replace the linears listed in ``weights/metadata.json`` (``runtime.py:210-239``); with
+    ``palette`` the handles decode in LUT mode (see :func:`artifact_palette`)."""
     metadata = json.loads((weights / "metadata.json").read_text())
     handles: list[int] = []
     for entry in metadata["entries"]:
@@ -153,7 +184,7 @@ def install(model: nn.Module, weights: Path, lookahead: int = 1, fp16_prefill: b
             raise RuntimeError(f"{entry['module_name']} is on {device}; selected linears must be CUDA resident")
         bias = original.bias if getattr(original, "bias", None) is not None else None
         with torch.cuda.device(device):
-            entry_handles = pack_entry_handles(weights, entry, bias=bias, lookahead=lookahead)
+            entry_handles = pack_entry_handles(weights, entry, bias=bias, lookahead=lookahead, palette=palette)
         quantized = TexelatorLinear(entry_handles)
         replacement = DecodeOnlyLinear(original, quantized) if fp16_prefill else quantized
         setattr(parent, child, replacement)
