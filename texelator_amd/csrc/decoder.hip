@@ -146,6 +146,9 @@ constexpr int kChunk = 64;      // keys per attention block
 constexpr int kHeadDim = 128;   // head_dim handled by the decode attention kernels
 constexpr int kMaxGroup = 8;    // query heads per KV head
 constexpr int kRowU4 = kHeadDim * 2 / 16;  // uint4 per cached key or value row (16)
+// LDS row stride of the key tile in uint4: one uint4 of padding, so the 16 keys a wave scores at
+// once (256 bytes apart unpadded) fall into different LDS banks.
+constexpr int kKeyStrideU4 = kRowU4 + 1;
 
 // Split-length decode attention for one query token. Block (kv, chunk) loads the chunk's keys and
 // values (those <= position) into LDS in one burst, scores the group's query heads against them
@@ -155,7 +158,7 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(const uint16_t *q
                                                                const uint16_t *v_cache, const int64_t *position,
                                                                int group, int64_t max_ctx, float scale,
                                                                int chunks, float *partials) {
-  __shared__ uint4 ks[kChunk * kRowU4];
+  __shared__ uint4 ks[kChunk * kKeyStrideU4];
   __shared__ uint4 vs[kChunk * kRowU4];
   __shared__ float qs[kMaxGroup][kHeadDim];
   __shared__ float probs[kMaxGroup][kChunk];
@@ -191,8 +194,9 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(const uint16_t *q
   const int count = (int)min((int64_t)kChunk, pos - j0 + 1);  // valid keys in this chunk
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
-    ks[u * 256 + tid] = kr[u];
-    vs[u * 256 + tid] = vr[u];
+    const int idx = u * 256 + tid;
+    ks[(idx / kRowU4) * kKeyStrideU4 + idx % kRowU4] = kr[u];
+    vs[idx] = idx / kRowU4 < count ? vr[u] : make_uint4(0, 0, 0, 0);  // rows past the position: zero
   }
 #pragma unroll
   for (int u = 0; u < kMaxGroup * kHeadDim / 256; ++u) {
@@ -206,7 +210,7 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(const uint16_t *q
     const int jl = tid >> 2;
     const int part = tid & 3;
     float kf[32];
-    const uint4 *row = ks + jl * kRowU4 + part * 4;
+    const uint4 *row = ks + jl * kKeyStrideU4 + part * 4;
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const uint4 w = row[v];
@@ -218,9 +222,16 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(const uint16_t *q
       }
     }
     for (int g = 0; g < group; ++g) {
+      const float4 *q4 = reinterpret_cast<const float4 *>(&qs[g][part * 32]);
       float s = 0.f;
 #pragma unroll
-      for (int e = 0; e < 32; ++e) s = __builtin_fmaf(qs[g][part * 32 + e], kf[e], s);
+      for (int e4 = 0; e4 < 8; ++e4) {
+        const float4 qq = q4[e4];
+        s = __builtin_fmaf(qq.x, kf[4 * e4], s);
+        s = __builtin_fmaf(qq.y, kf[4 * e4 + 1], s);
+        s = __builtin_fmaf(qq.z, kf[4 * e4 + 2], s);
+        s = __builtin_fmaf(qq.w, kf[4 * e4 + 3], s);
+      }
       s += __shfl_xor(s, 1);
       s += __shfl_xor(s, 2);
       if (part == 0) probs[g][jl] = jl < count ? s * scale : -INFINITY;
@@ -257,12 +268,21 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(const uint16_t *q
 #pragma unroll
     for (int u = 0; u < kMaxGroup / 2; ++u) acc[u] = 0.f;
     const uint16_t *vcol = reinterpret_cast<const uint16_t *>(vs) + dd;
-    for (int j = 0; j < count; ++j) {
-      const float v = bf(vcol[j * kHeadDim]);
+    // four keys per pass (probabilities read as float4); keys past the position have p = 0 and
+    // zeroed values, so the padded tail adds exact zeros
+    for (int j = 0; j < count; j += 4) {
+      const float v0 = bf(vcol[j * kHeadDim]), v1 = bf(vcol[(j + 1) * kHeadDim]);
+      const float v2 = bf(vcol[(j + 2) * kHeadDim]), v3 = bf(vcol[(j + 3) * kHeadDim]);
 #pragma unroll
       for (int u = 0; u < kMaxGroup / 2; ++u) {
         const int g = gg + 2 * u;
-        if (g < group) acc[u] = __builtin_fmaf(probs[g][j], v, acc[u]);
+        if (g < group) {
+          const float4 p4 = *reinterpret_cast<const float4 *>(&probs[g][j]);
+          acc[u] = __builtin_fmaf(p4.x, v0, acc[u]);
+          acc[u] = __builtin_fmaf(p4.y, v1, acc[u]);
+          acc[u] = __builtin_fmaf(p4.z, v2, acc[u]);
+          acc[u] = __builtin_fmaf(p4.w, v3, acc[u]);
+        }
       }
     }
 #pragma unroll
