@@ -101,7 +101,7 @@ int tx_set_palette_table(uint64_t handle, const float *device_table);
 
 /* Replaces texelator_handle_info (texelator_cuda.cu:1505-1512). Writes up to n of
  * [M, K, prefill_threshold, prefill_tile_rows, prefill_backend, pipelined(0), graphics(0),
- *  lookahead, device]. */
+ *  lookahead, device, decode GEMV K splits, LUT mode (0/1)]; the last four are this library's. */
 int tx_handle_info(uint64_t handle, int64_t *out, int n);
 
 /* Replaces texelator_free (texelator_cuda.cu:1538). Caller must ensure no work is pending. */
@@ -166,6 +166,12 @@ int tx_swiglu(const void *gate_up, int64_t rows, int64_t intermediate, void *out
  * tx_linear_split of its handle and before the next one. Outputs are bit-identical to
  * tx_linear followed by the plain helper. */
 int tx_linear_split(uint64_t handle, const void *x, void *stream);
+
+/* One-token GEMV of a merged [gate (inter) | up (inter)] handle with SwiGLU applied in its
+ * epilogue: out bf16 [inter] = tx_swiglu(tx_linear(handle, x)), bit for bit, in one kernel.
+ * x bf16 [K]. Needs inter % 16 == 0, a BF16 bias or none, and a handle that runs its one-token
+ * GEMV unsplit without LUT mode (TX_ERR_UNSUPPORTED otherwise: use tx_linear + tx_swiglu). */
+int tx_linear_swiglu(uint64_t handle, const void *x, void *out, void *stream);
 
 /* tx_add_rmsnorm for one row whose delta is the output of delta_handle (M == hidden). */
 int tx_add_rmsnorm_split(float *residual, uint64_t delta_handle, const void *weight, float eps, void *out,

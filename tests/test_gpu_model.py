@@ -10,7 +10,7 @@ import pytest
 import torch
 from torch.nn import functional
 
-from texelator_amd import layers, modeling, prefill
+from texelator_amd import _lib, layers, modeling, prefill
 
 pytestmark = pytest.mark.gpu
 
@@ -242,6 +242,61 @@ def test_rope_kv_cache_split_is_bit_identical(ext, heads, kv, k, bias):
         assert torch.equal(caches[0], caches[2]) and torch.equal(caches[1], caches[3])
     finally:
         ext.free(handle)
+
+
+@pytest.mark.parametrize("inter,k,bias,lookahead", [(8192, 1024, False, 1), (11008, 2048, True, 2),
+                                                    (27648, 5120, False, 4), (16384, 4096, True, 8)])
+def test_linear_swiglu_is_bit_identical(ext, inter, k, bias, lookahead):
+    """The gate|up GEMV with the SwiGLU epilogue == linear + swiglu, bit for bit."""
+    handle = _random_handle(ext, 2 * inter, k, seed=inter + k, bias=bias)
+    try:
+        ext.set_lookahead(handle, lookahead)
+        assert ext.gemv_plan(handle) == (1, False)
+        g = torch.Generator(device="cuda").manual_seed(17)
+        for scale in (1.0, 30.0):  # large inputs drive silu into both saturated ends
+            x = (scale * torch.randn(1, k, device="cuda", generator=g)).to(torch.bfloat16)
+            want = layers.swiglu(ext.linear(handle, x))
+            got = layers.linear_swiglu(handle, x)
+            assert got.shape == (1, inter)
+            assert torch.equal(want, got)
+    finally:
+        ext.free(handle)
+
+
+def test_linear_swiglu_refuses_unsupported_handles(ext):
+    split = _random_handle(ext, 512, 4096, seed=1)       # 32 row groups x 32 tile columns: K splits 8 ways
+    odd = _random_handle(ext, 48, 256, seed=2)           # halves of 24 rows
+    x = torch.zeros(1, 4096, device="cuda", dtype=torch.bfloat16)
+    try:
+        assert ext.gemv_plan(split)[0] > 1
+        with pytest.raises(_lib.UnsupportedError):
+            layers.linear_swiglu(split, x)
+        with pytest.raises(_lib.TexelatorError, match="16-row aligned"):
+            layers.linear_swiglu(odd, x[:, :256])
+    finally:
+        ext.free(split)
+        ext.free(odd)
+
+
+def test_split_decode_with_fused_swiglu_is_bit_identical(ext):
+    """A model whose gate|up GEMV runs unsplit takes the fused SwiGLU epilogue in its split decode
+    step; the step still equals the unsplit fused step bit for bit."""
+    config = modeling.DecoderConfig(layers=2, hidden=512, heads=4, kv_heads=2, head_dim=128, intermediate=8192,
+                                    vocab=512)
+    model = modeling.BC4Decoder(config, max_context=256, seed=5)
+    try:
+        assert ext.gemv_plan(model.layers[0].handles["gate_up"]) == (1, False)
+        ids = prefill.prompt_ids(model, 20, seed=8)
+        with torch.inference_mode():
+            model.prefill(ids)
+            token = ids[-1:]
+            model.split_decode = False
+            a = model.hidden_states(token, model.key_positions[20:21], 128).clone()
+            model.split_decode = True
+            b = model.hidden_states(token, model.key_positions[20:21], 128)
+        assert torch.equal(a, b)
+    finally:
+        model.close()
 
 
 def test_split_decode_step_is_bit_identical(ext, tiny):

@@ -218,6 +218,13 @@ def handle_info(handle: int) -> list[int]:
     return [int(v) for v in out]
 
 
+def gemv_plan(handle: int) -> tuple[int, bool]:
+    """(K splits of the one-token GEMV, LUT mode) of a handle."""
+    out = (ctypes.c_int64 * 11)()
+    check(_lib.load().tx_handle_info(handle, out, 11))
+    return int(out[9]), bool(out[10])
+
+
 def lookahead(handle: int) -> int:
     out = (ctypes.c_int64 * 8)()
     check(_lib.load().tx_handle_info(handle, out, 8))

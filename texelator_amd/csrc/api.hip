@@ -391,9 +391,9 @@ int tx_handle_info(uint64_t value, int64_t *out, int n) {
   Handle *h = as_handle(value);
   if (!h) return fail(TX_ERR_INVALID, "null Texelator handle");
   if (!out || n < 0) return fail(TX_ERR_INVALID, "invalid output buffer");
-  const int64_t info[9] = {h->M, h->K, h->prefill_threshold, h->prefill_tile_rows, h->prefill_backend, 0, 0,
-                           h->lookahead, h->device};
-  for (int i = 0; i < n && i < 9; ++i) out[i] = info[i];
+  const int64_t info[11] = {h->M, h->K, h->prefill_threshold, h->prefill_tile_rows, h->prefill_backend, 0, 0,
+                            h->lookahead, h->device, h->gemv_splits, h->lut != nullptr};
+  for (int i = 0; i < n && i < 11; ++i) out[i] = info[i];
   return TX_OK;
 }
 
@@ -473,6 +473,34 @@ int tx_linear_split(uint64_t value, const void *x, void *stream) {
   if (h->bias && h->bias_dtype != TX_DTYPE_BF16) return fail(TX_ERR_INVALID, "linear_split: the bias must be BF16");
   DeviceGuard guard(h->device);
   return run_gemv_split(h, x, reinterpret_cast<hipStream_t>(stream));
+}
+
+int tx_linear_swiglu(uint64_t value, const void *x, void *out, void *stream) {
+  g_last_error.clear();
+  Handle *h = as_handle(value);
+  if (!h) return fail(TX_ERR_INVALID, "null Texelator handle");
+  if (!x || !out) return fail(TX_ERR_INVALID, "null input or output pointer");
+  if (reinterpret_cast<uintptr_t>(x) % 16 != 0) return fail(TX_ERR_INVALID, "input must be 16-byte aligned");
+  if (h->M % 32 != 0) return fail(TX_ERR_INVALID, "linear_swiglu: the handle must hold [gate | up] with 16-row aligned halves");
+  if (h->gemv_splits != 1 || h->CG > tx::kGemvMaxLdsColumns || h->lut)
+    return fail(TX_ERR_UNSUPPORTED, "linear_swiglu: needs a one-split, non-LUT handle with K <= 16384");
+  if (h->bias && h->bias_dtype != TX_DTYPE_BF16) return fail(TX_ERR_INVALID, "linear_swiglu: the bias must be BF16");
+  DeviceGuard guard(h->device);
+  tx::GemvParams p{};
+  p.tiles = h->tiles;
+  p.scales = h->scales;
+  p.x = x;
+  p.bias = h->bias;
+  p.y = out;
+  p.M = h->M;
+  p.K = h->K;
+  p.Mp = h->Mp;
+  p.RG = h->RG;
+  p.CG = h->CG;
+  p.ks = 1;
+  p.tokens = 1;
+  TX_HIP(tx::launch_gemv_swiglu(p, h->lookahead, reinterpret_cast<hipStream_t>(stream)));
+  return TX_OK;
 }
 
 int tx_add_rmsnorm_split(float *residual, uint64_t delta_handle, const void *weight, float eps, void *out, int64_t hidden,

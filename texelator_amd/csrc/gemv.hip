@@ -245,6 +245,105 @@ __global__ __launch_bounds__(kThreads, LUT ? 4 : TX_GEMV_WAVES_PER_EU) void gemv
   }
 }
 
+// One-token GEMV of a merged [gate | up] handle (M = 2 * inter, inter a multiple of 16, one K
+// split) whose epilogue applies SwiGLU: out[r] = bf16(silu(bf16(gate_r)) * bf16(up_r)), exactly the
+// values tx_linear followed by tx_swiglu produce. Workgroup g computes gate row group g and up row
+// group g + RG/2 with the same four-wave K split, tile order and MFMA chains as gemv_kernel, so
+// each of the two row groups' sums is bit-identical to the plain GEMV's. Two rings of LA + 1 tiles
+// are in flight, so the occupancy bound falls with LA (no spills).
+template <int LA>
+__global__ __launch_bounds__(kThreads, LA == 1 ? 6 : (LA == 2 ? 5 : 4)) void gemv_swiglu_kernel(GemvParams p) {
+  extern __shared__ uint4 xs[];
+  __shared__ PaletteTableStorage tables;
+  __shared__ float red[2][kWaves][16];  // [gate|up][wave][row]
+
+  const int g = blockIdx.x;
+  const int half = p.RG / 2;
+  const int nc = p.CG;
+  const uint16_t *x = static_cast<const uint16_t *>(p.x);
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nt = nc > wave ? (nc - wave + kWaves - 1) / kWaves : 0;
+  const int first = min(wave, nc - 1);
+  const uint4 *gate_tiles = p.tiles + ((size_t)g * p.CG + first) * 64;
+  const uint4 *up_tiles = p.tiles + ((size_t)(g + half) * p.CG + first) * 64;
+
+  constexpr int R = LA + 1;
+  uint4 ring_g[R], ring_u[R];
+#pragma unroll
+  for (int u = 0; u < LA; ++u) {
+    const size_t off = (size_t)min(u, max(nt - 1, 0)) * kWaves * 64 + lane;
+    ring_g[u] = load_stream(gate_tiles + off);
+    ring_u[u] = load_stream(up_tiles + off);
+  }
+  build_palette_tables(tables, threadIdx.x, kThreads);
+  for (int idx = threadIdx.x; idx < nc * 16; idx += kThreads) xs[idx] = load_x8(x, idx * 8, p.K);
+  __syncthreads();
+
+  const int i = lane & 15;
+  const int kg = lane >> 4;
+  const float scale_g = p.scales[g * kTileRows + i];
+  const float scale_u = p.scales[(g + half) * kTileRows + i];
+  const uint32_t pm_g = pm_scale_pair<false>(scale_g);
+  const uint32_t pm_u = pm_scale_pair<false>(scale_u);
+  f32x4 ga0 = {0.f, 0.f, 0.f, 0.f}, ga1 = ga0, ua0 = ga0, ua1 = ga0;
+  XFrag xf = {};
+  auto consume = [&](int u, int j) {
+    if (i == 0) {
+      const uint4 *xv = xs + (j * kWaves + wave) * 16 + kg * 4;
+      xf.x0 = xv[0];
+      xf.x1 = xv[1];
+      xf.x2 = xv[2];
+      xf.x3 = xv[3];
+    }
+    tile_mfma<false>(ring_g[u], xf, scale_g, pm_g, tables, ga0, ga1);
+    tile_mfma<false>(ring_u[u], xf, scale_u, pm_u, tables, ua0, ua1);
+  };
+  int j0 = 0;
+  for (; j0 + R <= nt; j0 += R) {
+#pragma unroll
+    for (int u = 0; u < R; ++u) {
+      const size_t off = (size_t)min(j0 + u + LA, nt - 1) * kWaves * 64 + lane;
+      ring_g[(u + LA) % R] = load_stream(gate_tiles + off);
+      ring_u[(u + LA) % R] = load_stream(up_tiles + off);
+      consume(u, j0 + u);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < LA; ++u)
+    if (j0 + u < nt) consume(u, j0 + u);
+
+  const f32x4 gacc = ga0 + ga1, uacc = ua0 + ua1;
+  if (i == 0) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      red[0][wave][kg * 4 + r] = gacc[r];
+      red[1][wave][kg * 4 + r] = uacc[r];
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x < 16) {
+    const int rr = threadIdx.x;
+    float gate = red[0][0][rr], up = red[1][0][rr];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) {
+      gate += red[0][w][rr];
+      up += red[1][w][rr];
+    }
+    const int row = g * kTileRows + rr;  // output index = gate row
+    const int inter = p.M / 2;
+    if (row < inter) {
+      const uint16_t *bias = static_cast<const uint16_t *>(p.bias);
+      if (bias) {
+        gate += bf(bias[row]);
+        up += bf(bias[inter + row]);
+      }
+      const float act = swiglu_value(bf(to_bf(gate)), bf(to_bf(up)));
+      static_cast<uint16_t *>(p.y)[row] = to_bf(act);
+    }
+  }
+}
+
 // y[t][m] = sum over splits s (in order) of partials[s][t][m], then bias and output cast
 // (split_sum, which fused consumers of the partials use as well).
 template <bool F16, bool F32OUT>
@@ -293,6 +392,17 @@ hipError_t launch_la(const GemvParams &p, bool f32_out, hipStream_t stream) {
 }
 
 }  // namespace
+
+hipError_t launch_gemv_swiglu(const GemvParams &p, int lookahead, hipStream_t stream) {
+  const size_t lds = (size_t)p.CG * 16 * sizeof(uint4);
+  const dim3 grid(p.RG / 2);
+  switch (lookahead) {
+    case 1: hipLaunchKernelGGL(gemv_swiglu_kernel<1>, grid, dim3(kThreads), lds, stream, p); break;
+    case 2: hipLaunchKernelGGL(gemv_swiglu_kernel<2>, grid, dim3(kThreads), lds, stream, p); break;
+    default: hipLaunchKernelGGL(gemv_swiglu_kernel<4>, grid, dim3(kThreads), lds, stream, p); break;
+  }
+  return hipGetLastError();
+}
 
 bool gemv_lookahead_supported(int la) { return la == 1 || la == 2 || la == 3 || la == 4 || la == 6 || la == 8; }
 

@@ -41,6 +41,9 @@ struct PrefillParams {
 bool gemv_lookahead_supported(int lookahead);
 hipError_t launch_gemv(const GemvParams &p, int lookahead, bool f32_out, hipStream_t stream);
 hipError_t gemv_kernel_attributes(int lookahead, hipFuncAttributes *attr);
+// One-token GEMV of a merged [gate | up] handle with a SwiGLU epilogue (p.M = 2 * inter, one
+// split, bf16); p.y receives bf16 [inter].
+hipError_t launch_gemv_swiglu(const GemvParams &p, int lookahead, hipStream_t stream);
 
 // Prefill tile candidates: ids 5..9 (kept from the reference's backend numbering).
 constexpr int kPrefillFirst = 5;

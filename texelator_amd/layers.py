@@ -111,6 +111,21 @@ def linear_split(handle: int, x: torch.Tensor) -> None:
     check(_lib.load().tx_linear_split(handle, _ptr(x), _stream(x)))
 
 
+def linear_swiglu(handle: int, x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """``swiglu(linear(handle, x))`` for one token of a merged ``[gate | up]`` handle, in one kernel
+    (bit-identical to the two calls). Raises ``UnsupportedError`` for a handle whose GEMV is split
+    or in LUT mode."""
+    _expect(x.is_cuda and x.dtype == torch.bfloat16 and x.is_contiguous() and x.data_ptr() % 16 == 0,
+            "x must be a contiguous, 16-byte aligned CUDA bf16 tensor")
+    m, k = _hip_shape(handle)
+    _expect(x.numel() == k, "x has the wrong length for this handle")
+    if out is None:
+        out = torch.empty((1, m // 2), dtype=torch.bfloat16, device=x.device)
+    _expect(out.dtype == torch.bfloat16 and out.is_contiguous() and out.numel() == m // 2, "bad output")
+    check(_lib.load().tx_linear_swiglu(handle, _ptr(x), _ptr(out), _stream(x)))
+    return out
+
+
 def add_rmsnorm_split(residual: torch.Tensor, delta_handle: int, weight: torch.Tensor, eps: float,
                       out: torch.Tensor) -> torch.Tensor:
     """:func:`add_rmsnorm` of one row whose delta is the last :func:`linear_split` of ``delta_handle``."""

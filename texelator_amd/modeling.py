@@ -121,9 +121,9 @@ class BC4Decoder:
     PyTorch ops (the cross-check path).
 
     With ``split_decode`` (the default; needs ``fused``) a one-token step hands the split-K
-    partials of qkv, o and down straight to their consumer kernels (RoPE, add+RMSNorm), so a
-    layer is ten kernels instead of thirteen; the results are bit-identical to the unsplit fused
-    path."""
+    partials of qkv, o and down straight to their consumer kernels (RoPE, add+RMSNorm), and the
+    gate|up GEMV applies SwiGLU in its epilogue, so a layer is nine kernels instead of thirteen;
+    the results are bit-identical to the unsplit fused path."""
 
     def __init__(self, config: DecoderConfig, max_context: int, device: torch.device | str = "cuda", seed: int = 0,
                  lookahead: int = 1, linear_source=None, depth_scaled: bool = True, embed_std: float = 1.0,
@@ -208,6 +208,7 @@ class BC4Decoder:
             dtype=torch.uint8, device=self.device)
         # decode-step state (static buffers read and advanced by the captured graphs)
         self.q_buffer = torch.empty(c.heads * c.head_dim, dtype=bf16, device=self.device)
+        self.act_buffer = torch.empty((1, c.intermediate), dtype=bf16, device=self.device)
         self.token = torch.zeros(1, dtype=torch.long, device=self.device)
         self.position = torch.zeros(1, dtype=torch.long, device=self.device)
         self.graphs: dict[int, torch.cuda.CUDAGraph] = {}
@@ -335,7 +336,7 @@ class BC4Decoder:
 
     def _decode_split(self, h: torch.Tensor, x: torch.Tensor, positions: torch.Tensor, length: int,
                       scale: float) -> torch.Tensor:
-        """One token through every layer with the split-K consumers (ten kernels a layer)."""
+        """One token through every layer with the split-K consumers (nine kernels a layer)."""
         c = self.config
         for index, layer in enumerate(self.layers):
             layers.linear_split(layer.handles["qkv"], x)
@@ -346,10 +347,20 @@ class BC4Decoder:
                                            c.kv_heads, scale, self.attention_workspace)
             layers.linear_split(layer.handles["o"], attn)
             layers.add_rmsnorm_split(h, layer.handles["o"], layer.post_norm, c.rms_eps, out=x)
-            layers.linear_split(layer.handles["down"], layers.swiglu(layer.linears["gate_up"](x)))
+            layers.linear_split(layer.handles["down"], self._gate_up_swiglu(layer, x))
             following = self.layers[index + 1].input_norm if index + 1 < len(self.layers) else self.final_norm
             layers.add_rmsnorm_split(h, layer.handles["down"], following, c.rms_eps, out=x)
         return x
+
+    def _gate_up_swiglu(self, layer: _Layer, x: torch.Tensor) -> torch.Tensor:
+        """SwiGLU of the merged gate|up projection of one token: one GEMV with the SwiGLU epilogue
+        when the handle's GEMV runs unsplit (bit-identical to the GEMV + SwiGLU kernels it
+        replaces), else those two kernels."""
+        handle = layer.handles["gate_up"]
+        splits, lut = extension().gemv_plan(handle)
+        if splits == 1 and not lut and self.config.intermediate % 16 == 0:
+            return layers.linear_swiglu(handle, x, out=self.act_buffer)
+        return layers.swiglu(layer.linears["gate_up"](x))
 
     def logits(self, hidden: torch.Tensor) -> torch.Tensor:
         return functional.linear(hidden, self.lm_head)
