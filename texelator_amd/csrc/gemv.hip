@@ -87,6 +87,22 @@ __device__ __forceinline__ void tile_mfma_lut(uint4 cur, const TileRows &rows, c
   acc1 = mfma<F16>(w[4], w[5], w[6], w[7], xf.x3, acc1);
 }
 
+// Wave priority from the share of a wave's tiles still to do (3 while more than three quarters
+// remain, down to 0 in the last quarter). The sequencer issues the oldest ready wave first, so
+// with equal priorities the first workgroups on a CU race ahead and the last ones finish alone,
+// with the CU mostly idle; ranking waves by remaining work keeps them level and the CU full
+// until the end of the launch.
+#ifndef TX_GEMV_PRIORITY
+#define TX_GEMV_PRIORITY 1
+#endif
+__device__ __forceinline__ void progress_priority(int remaining, int total) {
+  if constexpr (!TX_GEMV_PRIORITY) return;
+  if (remaining * 4 > total * 3) __builtin_amdgcn_s_setprio(3);
+  else if (remaining * 2 > total) __builtin_amdgcn_s_setprio(2);
+  else if (remaining * 4 > total) __builtin_amdgcn_s_setprio(1);
+  else __builtin_amdgcn_s_setprio(0);
+}
+
 // Minimum waves per SIMD the register allocation must allow (7 keeps the kernel at <= 72 VGPRs
 // without spills, so seven 4-wave workgroups fit on a CU).
 #ifndef TX_GEMV_WAVES_PER_EU
@@ -177,6 +193,7 @@ __global__ __launch_bounds__(kThreads, LUT ? 4 : TX_GEMV_WAVES_PER_EU) void gemv
     const float4 *lut = p.lut;
     TileRows cur = tile_rows(lut, ring[0]);
     for (; j0 + R <= nt; j0 += R) {
+      progress_priority(nt - j0, nt);
 #pragma unroll
       for (int u = 0; u < R; ++u) {
         const int jn = min(j0 + u + LA, nt - 1);
@@ -198,6 +215,7 @@ __global__ __launch_bounds__(kThreads, LUT ? 4 : TX_GEMV_WAVES_PER_EU) void gemv
     }
   } else {
     for (; j0 + R <= nt; j0 += R) {
+      progress_priority(nt - j0, nt);
 #pragma unroll
       for (int u = 0; u < R; ++u) {
         const int jn = min(j0 + u + LA, nt - 1);
@@ -301,6 +319,7 @@ __global__ __launch_bounds__(kThreads, LA == 1 ? 6 : (LA == 2 ? 5 : 4)) void gem
   };
   int j0 = 0;
   for (; j0 + R <= nt; j0 += R) {
+    progress_priority(nt - j0, nt);
 #pragma unroll
     for (int u = 0; u < R; ++u) {
       const size_t off = (size_t)min(j0 + u + LA, nt - 1) * kWaves * 64 + lane;
