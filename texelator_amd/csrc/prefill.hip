@@ -6,14 +6,18 @@
 // the bias is added afterwards with a second bf16 rounding (:190-199). Its five tile shapes are
 // backends 5..9; here ids 5..9 name this build's own tile candidates.
 //
-// A workgroup (4 waves) owns BT = 16*MT tokens x BN = 64*NT output rows x one K range (split):
-//   * each wave owns NT 16-row groups; it streams their BC4 tiles (one 1 KiB tile per group and
-//     128-wide K step, LA steps ahead) and decodes them (palette seeds from LDS tables) straight
-//     into MFMA A operands in registers -- weights never pass through LDS, and no dense 16-bit
-//     copy exists anywhere;
-//   * the activations of a K step (BT x 128 bf16) are double-buffered in LDS and shared by the
-//     four waves; lane (token, kg) reads the 8 values matching the decoded weights' K chunk;
-//   * v_mfma_f32_16x16x32_bf16 with rows as M and tokens as N: acc[u][v] = D[rows][tokens].
+// A workgroup (4 waves) owns BT = 32*TB tokens x BN = 128*RB output rows x one K range (split):
+//   * each wave owns RB blocks of 32 rows (two 16-row tile groups each). Per 128-wide K step it
+//     streams the two groups' 1 KiB tiles (LA steps ahead): lane l gathers the 32 bytes holding
+//     blocks 4h..4h+3 (h = l / 32) of row l % 32, and decodes them (palette seeds from LDS
+//     tables) straight into MFMA A operands -- weights never pass through LDS, and no dense
+//     16-bit copy exists anywhere;
+//   * v_mfma_f32_32x32x16_bf16 (twice the rate of the 16x16x32 form on gfx950): MFMA s = 2j + e
+//     of a step takes positions 8e..8e+7 of block j from lanes 0-31 and of block 4+j from lanes
+//     32-63, i.e. K = {16j + 8e ..+7} u {64 + 16j + 8e ..+7}. The activations of the step
+//     (BT x 128 bf16) are double-buffered in LDS, shared by the four waves, and read with the
+//     same K sets;
+//   * acc[tb][rb] = D[32 rows of block rb][32 tokens of block tb].
 // Every candidate uses the same MFMA K grouping and order, and the K splits depend only on the
 // shape, so all candidates give bitwise-identical results. With several splits the partial sums
 // are written to the caller's workspace and reduced in split order by a second kernel.
@@ -33,17 +37,22 @@ constexpr int kThreads = 256;
 constexpr int kStride = 136;  // LDS row stride of the activation tile in bf16 (128 + 8 padding)
 constexpr int kXcds = 8;
 
+// Weight tiles in flight per wave, in K steps.
+#ifndef TX_PREFILL_LA
+#define TX_PREFILL_LA 2
+#endif
+
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-// D += A * B on 16x16x32 tiles of packed 16-bit operands (bf16, or fp16 with F16).
+// D += A * B on 32x32x16 tiles of packed 16-bit operands (bf16, or fp16 with F16).
 template <bool F16>
-__device__ __forceinline__ f32x4 mfma(u32x4 a, u32x4 b, f32x4 c) {
+__device__ __forceinline__ f32x16 mfma(u32x4 a, u32x4 b, f32x16 c) {
   if constexpr (F16)
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
   else
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
 
 // Round to the output type and widen back (bf16, or fp16 with F16).
@@ -84,13 +93,14 @@ __device__ __forceinline__ bool work_item(const PrefillParams &p, int BT, int BN
 // F16: fp16 activations, bias and output, weights rounded to fp16 (the reference's FP16 prefill
 // decodes __float2half(P*scale) into its scratch matrix, texelator_cuda.cu:604-628, and adds
 // the bias with a second fp16 rounding, :630-635).
-// PIPE: software-pipelined K loop (see the step below). LUT: palettes read from p.lut (a
-// 255 x 255 x 8 fp32 table) instead of computed.
-template <bool F16, int MT, int NT, int LA, bool PIPE, bool LUT>
+// PIPE: software-pipelined K loop (tile j+1 decoded while tile j is multiplied). LUT: palettes
+// read from p.lut (a 255 x 255 x 8 fp32 table) instead of computed.
+template <bool F16, int TB, int RB, int LA, bool PIPE, bool LUT>
 __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillParams p) {
   static_assert(!PIPE || LA >= 2, "the pipelined K loop needs two weight tiles in flight");
-  constexpr int BT = 16 * MT;
-  constexpr int BN = 64 * NT;
+  constexpr int BT = 32 * TB;
+  constexpr int BN = 128 * RB;
+  constexpr int XC = BT * 16 / kThreads;  // activation chunks (8 bf16) staged per thread per step
   constexpr int R = LA + 1;
   __shared__ __attribute__((aligned(16))) uint16_t xs[2][BT * kStride];
   __shared__ PaletteTableStorage tables;
@@ -100,45 +110,56 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillParams p) {
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int i = lane & 15;
-  const int kg = lane >> 4;
+  const int r32 = lane & 31;  // row of the 32-row block (A), token of the 32-token block (B)
+  const int h = lane >> 5;    // which four blocks of the step this lane holds
   const uint16_t *x = static_cast<const uint16_t *>(p.x);
 
-  // Row groups of this wave (clamped into the matrix; rows past M are computed, never stored).
-  const uint4 *gtiles[NT];
-  float scale[NT];
-  uint32_t pm[NT];
+  // Row blocks of this wave: 32 rows = tile groups 2b and 2b+1 (clamped into the matrix; rows
+  // past M are computed, never stored). Lane slot (row & 15) + 32h of a tile holds blocks
+  // 4h, 4h+1 of that row; slot + 16 holds blocks 4h+2, 4h+3.
+  const uint4 *gtiles[RB];
+  float scale[RB];
+  uint32_t pm[RB];
 #pragma unroll
-  for (int v = 0; v < NT; ++v) {
-    const int g = min(w.n0 / kTileRows + wave * NT + v, p.RG - 1);
-    gtiles[v] = p.tiles + ((size_t)g * p.CG + w.c_begin) * 64 + lane;
-    scale[v] = p.scales[g * kTileRows + i];
-    pm[v] = pm_scale_pair<F16>(scale[v]);
+  for (int b = 0; b < RB; ++b) {
+    const int g = min(w.n0 / kTileRows + (wave * RB + b) * 2 + (r32 >> 4), p.RG - 1);
+    gtiles[b] = p.tiles + ((size_t)g * p.CG + w.c_begin) * 64 + (lane & 15) + 32 * h;
+    scale[b] = p.scales[g * kTileRows + (lane & 15)];
+    pm[b] = pm_scale_pair<F16>(scale[b]);
   }
 
-  // Weight ring: slot s holds the NT tiles of one K step.
-  uint4 ring[R][NT];
+  // Weight ring: slot s holds the two 16-byte pieces of each row block for one K step.
+  uint4 ring[R][RB][2];
+  auto load_tiles = [&](uint4 (&slot)[RB][2], int j) {
+    const size_t off = (size_t)min(j, w.nc - 1) * 64;
 #pragma unroll
-  for (int u = 0; u < LA; ++u)
+    for (int b = 0; b < RB; ++b) {
+      slot[b][0] = load_stream(gtiles[b] + off);
+      slot[b][1] = load_stream(gtiles[b] + off + 16);
+    }
+  };
 #pragma unroll
-    for (int v = 0; v < NT; ++v) ring[u][v] = load_stream(gtiles[v] + (size_t)min(u, w.nc - 1) * 64);
+  for (int u = 0; u < LA; ++u) load_tiles(ring[u], u);
 
-  // Activation staging: MT uint4 per thread per K step (16 uint4 per token row).
-  uint4 xr[MT];
+  // Activation staging: XC uint4 per thread per K step (16 uint4 per token row). Rows and
+  // columns out of range load a clamped, valid address and are masked to zero.
+  uint4 xr[XC];
   auto load_x = [&](int j) {
     const int c = w.c_begin + min(j, w.nc - 1);
 #pragma unroll
-    for (int v = 0; v < MT; ++v) {
+    for (int v = 0; v < XC; ++v) {
       const int idx = v * kThreads + threadIdx.x;
       const int t = w.t0 + (idx >> 4);
       const int k = c * kTileK + (idx & 15) * 8;
-      xr[v] = (t < p.tokens && k < p.K) ? *reinterpret_cast<const uint4 *>(x + (size_t)t * p.K + k)
-                                        : make_uint4(0, 0, 0, 0);
+      const uint32_t keep = (t < p.tokens && k < p.K) ? 0xFFFFFFFFu : 0u;
+      const uint4 value =
+          *reinterpret_cast<const uint4 *>(x + (size_t)min(t, p.tokens - 1) * p.K + min(k, p.K - 8));
+      xr[v] = make_uint4(value.x & keep, value.y & keep, value.z & keep, value.w & keep);
     }
   };
   auto store_x = [&](int buf) {
 #pragma unroll
-    for (int v = 0; v < MT; ++v) {
+    for (int v = 0; v < XC; ++v) {
       const int idx = v * kThreads + threadIdx.x;
       *reinterpret_cast<uint4 *>(&xs[buf][(idx >> 4) * kStride + (idx & 15) * 8]) = xr[v];
     }
@@ -149,58 +170,45 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillParams p) {
   if constexpr (!LUT) build_palette_tables(tables, threadIdx.x, kThreads);
   __syncthreads();
 
-  f32x4 acc[MT][NT];
+  f32x16 acc[TB][RB];
 #pragma unroll
-  for (int a = 0; a < MT; ++a)
+  for (int a = 0; a < TB; ++a)
 #pragma unroll
-    for (int b = 0; b < NT; ++b) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int b = 0; b < RB; ++b)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.f;
 
-  // Decode one K step's NT tiles into A operands: a[v][q] covers block 2kg + (q >> 1), positions
-  // 8*(q & 1) .. +7, i.e. K offset 32kg + 8q within the step.
-  auto decode_step = [&](const uint4 (&tiles)[NT], u32x4 (&a)[NT][4]) {
-    if constexpr (LUT) {
-      float4 rows[NT][4];  // all palette rows of the step in flight together
+  // Decode one K step into A operands: a[b][2j + e] = positions 8e..8e+7 of this lane's block j.
+  auto decode_step = [&](const uint4 (&slot)[RB][2], u32x4 (&a)[RB][8]) {
 #pragma unroll
-      for (int v = 0; v < NT; ++v) {
-        const float4 *ra = p.lut + 2 * (size_t)palette_row(tiles[v].x, tiles[v].y);
-        const float4 *rb = p.lut + 2 * (size_t)palette_row(tiles[v].z, tiles[v].w);
-        rows[v][0] = ra[0];
-        rows[v][1] = ra[1];
-        rows[v][2] = rb[0];
-        rows[v][3] = rb[1];
-      }
+    for (int b = 0; b < RB; ++b) {
 #pragma unroll
-      for (int v = 0; v < NT; ++v) {
+      for (int j = 0; j < 4; ++j) {
+        const uint4 &piece = slot[b][j >> 1];
+        const uint32_t wa = (j & 1) ? piece.z : piece.x;
+        const uint32_t wb = (j & 1) ? piece.w : piece.y;
         uint32_t d[8];
-        decode_from_palette<F16>(rows[v][0], rows[v][1], tiles[v].x, tiles[v].y, scale[v], d);
-        a[v][0] = u32x4{d[0], d[1], d[2], d[3]};
-        a[v][1] = u32x4{d[4], d[5], d[6], d[7]};
-        decode_from_palette<F16>(rows[v][2], rows[v][3], tiles[v].z, tiles[v].w, scale[v], d);
-        a[v][2] = u32x4{d[0], d[1], d[2], d[3]};
-        a[v][3] = u32x4{d[4], d[5], d[6], d[7]};
-      }
-    } else {
-#pragma unroll
-      for (int v = 0; v < NT; ++v) {
-        uint32_t d[8];
-        decode_block_lds<F16>(tiles[v].x, tiles[v].y, scale[v], pm[v], tables, d);
-        a[v][0] = u32x4{d[0], d[1], d[2], d[3]};
-        a[v][1] = u32x4{d[4], d[5], d[6], d[7]};
-        decode_block_lds<F16>(tiles[v].z, tiles[v].w, scale[v], pm[v], tables, d);
-        a[v][2] = u32x4{d[0], d[1], d[2], d[3]};
-        a[v][3] = u32x4{d[4], d[5], d[6], d[7]};
+        if constexpr (LUT) {
+          const float4 *row = p.lut + 2 * (size_t)palette_row(wa, wb);
+          decode_from_palette<F16>(row[0], row[1], wa, wb, scale[b], d);
+        } else {
+          decode_block_lds<F16>(wa, wb, scale[b], pm[b], tables, d);
+        }
+        a[b][2 * j] = u32x4{d[0], d[1], d[2], d[3]};
+        a[b][2 * j + 1] = u32x4{d[4], d[5], d[6], d[7]};
       }
     }
   };
-  auto mfma_step = [&](int j, const u32x4 (&a)[NT][4]) {
+  auto mfma_step = [&](int j, const u32x4 (&a)[RB][8]) {
     const uint16_t *xb = xs[j & 1];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+    for (int s = 0; s < 8; ++s) {
+      const int k_off = 16 * (4 * h + (s >> 1)) + 8 * (s & 1);
 #pragma unroll
-      for (int mu = 0; mu < MT; ++mu) {
-        const u32x4 b = *reinterpret_cast<const u32x4 *>(xb + (mu * 16 + i) * kStride + kg * 32 + q * 8);
+      for (int tb = 0; tb < TB; ++tb) {
+        const u32x4 bv = *reinterpret_cast<const u32x4 *>(xb + (tb * 32 + r32) * kStride + k_off);
 #pragma unroll
-        for (int v = 0; v < NT; ++v) acc[mu][v] = mfma<F16>(a[v][q], b, acc[mu][v]);
+        for (int b = 0; b < RB; ++b) acc[tb][b] = mfma<F16>(a[b][s], bv, acc[tb][b]);
       }
     }
   };
@@ -219,31 +227,69 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillParams p) {
 
   if constexpr (PIPE) {
     // Software-pipelined: step j multiplies the tiles decoded during step j-1 while decoding tile
-    // j+1 (already in the ring), so the decode's VALU work and the MFMAs interleave in one
-    // instruction stream. Tile j+1 was requested a step earlier (LA >= 2).
-    u32x4 acur[NT][4];
+    // j+1 (already in the ring; requested a step earlier, LA >= 2). The step is woven: each of
+    // its eight MFMA groups (one per K set s) carries the decode of one block of tile j+1 and the
+    // activation reads of the next group, in a scheduling region of its own (the decoded block is
+    // pinned to it), so the matrix core and the VALU work side by side instead of in turn.
+    u32x4 acur[RB][8];
     decode_step(ring[0], acur);
     run_steps([&](int j, int u) {
-      const int jn = min(j + LA, w.nc - 1);
+      load_tiles(ring[(u + LA) % R], j + LA);
+      const uint4(&next)[RB][2] = ring[(u + 1) % R];  // tile j+1 (past the end: the clamped last tile)
+      u32x4 anext[RB][8];
+      if constexpr (LUT) {
+        decode_step(next, anext);  // the palette-row gathers of a step stay together
+        mfma_step(j, acur);
+      } else {
+        const uint16_t *xb = xs[j & 1];
+        auto read_b = [&](int tb, int sg) {
+          return *reinterpret_cast<const u32x4 *>(xb + (tb * 32 + r32) * kStride + 16 * (4 * h + (sg >> 1)) +
+                                                  8 * (sg & 1));
+        };
+        constexpr int kBlocks = 4 * RB;  // blocks per lane and step, spread over the 8 groups
+        u32x4 bcur[TB];
 #pragma unroll
-      for (int v = 0; v < NT; ++v) ring[(u + LA) % R][v] = load_stream(gtiles[v] + (size_t)jn * 64);
-      u32x4 anext[NT][4];
-      decode_step(ring[(u + 1) % R], anext);  // tile j+1 (past the end: the clamped last tile, unused)
-      mfma_step(j, acur);
+        for (int tb = 0; tb < TB; ++tb) bcur[tb] = read_b(tb, 0);
+#pragma unroll
+        for (int sg = 0; sg < 8; ++sg) {
+          u32x4 bnext[TB];
+          if (sg + 1 < 8) {
+#pragma unroll
+            for (int tb = 0; tb < TB; ++tb) bnext[tb] = read_b(tb, sg + 1);
+          }
+          const bool decodes = (sg * kBlocks) % 8 < kBlocks;
+          const int q = sg * kBlocks / 8, b = q >> 2, jj = q & 3;
+          if (decodes) {
+            const uint4 &piece = next[b][jj >> 1];
+            uint32_t d[8];
+            decode_block_lds<F16>((jj & 1) ? piece.z : piece.x, (jj & 1) ? piece.w : piece.y, scale[b], pm[b], tables, d);
+            anext[b][2 * jj] = u32x4{d[0], d[1], d[2], d[3]};
+            anext[b][2 * jj + 1] = u32x4{d[4], d[5], d[6], d[7]};
+          }
+#pragma unroll
+          for (int tb = 0; tb < TB; ++tb)
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb) acc[tb][rb] = mfma<F16>(acur[rb][sg], bcur[tb], acc[tb][rb]);
+          if (decodes) asm volatile("" : "+v"(anext[b][2 * jj]), "+v"(anext[b][2 * jj + 1]));
+          __builtin_amdgcn_sched_barrier(0);
+          if (sg + 1 < 8) {
+#pragma unroll
+            for (int tb = 0; tb < TB; ++tb) bcur[tb] = bnext[tb];
+          }
+        }
+      }
       store_x((j + 1) & 1);  // the next step's activations, into the buffer read two steps ago
       load_x(j + 2);
       __syncthreads();
 #pragma unroll
-      for (int v = 0; v < NT; ++v)
+      for (int b = 0; b < RB; ++b)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) acur[v][q] = anext[v][q];
+        for (int s = 0; s < 8; ++s) acur[b][s] = anext[b][s];
     });
   } else {
     run_steps([&](int j, int u) {
-      const int jn = min(j + LA, w.nc - 1);
-#pragma unroll
-      for (int v = 0; v < NT; ++v) ring[(u + LA) % R][v] = load_stream(gtiles[v] + (size_t)jn * 64);
-      u32x4 a[NT][4];
+      load_tiles(ring[(u + LA) % R], j + LA);
+      u32x4 a[RB][8];
       decode_step(ring[u], a);
       mfma_step(j, a);
       store_x((j + 1) & 1);  // the next step's activations, into the buffer read two steps ago
@@ -252,26 +298,30 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillParams p) {
     });
   }
 
-  // acc[mu][v][r] = D[row 4kg + r of group v][token mu*16 + i].
+  // acc[tb][b][r] = D[row 8(r/4) + 4h + r%4 of row block b][token tb*32 + r32].
   const uint16_t *bias = static_cast<const uint16_t *>(p.bias);
 #pragma unroll
-  for (int mu = 0; mu < MT; ++mu) {
-    const int t = w.t0 + mu * 16 + i;
+  for (int tb = 0; tb < TB; ++tb) {
+    const int t = w.t0 + tb * 32 + r32;
     if (t >= p.tokens) continue;
 #pragma unroll
-    for (int v = 0; v < NT; ++v) {
-      const int row0 = w.n0 + (wave * NT + v) * kTileRows + kg * 4;
-      if (p.ks > 1) {
-        float *dst = p.partials + ((size_t)w.split * p.tokens + t) * p.Mp + row0;
-        if (row0 < p.Mp) *reinterpret_cast<float4 *>(dst) = make_float4(acc[mu][v][0], acc[mu][v][1], acc[mu][v][2], acc[mu][v][3]);
-      } else {
+    for (int b = 0; b < RB; ++b) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int n = row0 + r;
-          if (n < p.M) {
-            float out = round_out<F16>(acc[mu][v][r]);
-            if (bias) out += half_bits_to_float<F16>(bias[n]);
-            store_out<F16>(p.y, (size_t)t * p.M + n, out);
+      for (int rq = 0; rq < 4; ++rq) {
+        const int row0 = w.n0 + (wave * RB + b) * 32 + 8 * rq + 4 * h;
+        const f32x16 &v = acc[tb][b];
+        if (p.ks > 1) {
+          float *dst = p.partials + ((size_t)w.split * p.tokens + t) * p.Mp + row0;
+          if (row0 < p.Mp) *reinterpret_cast<float4 *>(dst) = make_float4(v[4 * rq], v[4 * rq + 1], v[4 * rq + 2], v[4 * rq + 3]);
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int n = row0 + r;
+            if (n < p.M) {
+              float out = round_out<F16>(v[4 * rq + r]);
+              if (bias) out += half_bits_to_float<F16>(bias[n]);
+              store_out<F16>(p.y, (size_t)t * p.M + n, out);
+            }
           }
         }
       }
@@ -301,20 +351,20 @@ struct Candidate {
   int lds;
 };
 
-template <int MT, int NT, int LA, bool PIPE>
+template <int TB, int RB, int LA, bool PIPE>
 hipError_t launch_tile(const PrefillParams &p, hipStream_t stream) {
-  constexpr int BT = 16 * MT, BN = 64 * NT;
+  constexpr int BT = 32 * TB, BN = 128 * RB;
   const int items = ((p.M + BN - 1) / BN) * ((p.tokens + BT - 1) / BT) * p.ks;
   const int grid = ((items + kXcds - 1) / kXcds) * kXcds;
   if (p.lut) {
     if (p.f16)
-      hipLaunchKernelGGL((prefill_kernel<true, MT, NT, LA, PIPE, true>), dim3(grid), dim3(kThreads), 0, stream, p);
+      hipLaunchKernelGGL((prefill_kernel<true, TB, RB, LA, PIPE, true>), dim3(grid), dim3(kThreads), 0, stream, p);
     else
-      hipLaunchKernelGGL((prefill_kernel<false, MT, NT, LA, PIPE, true>), dim3(grid), dim3(kThreads), 0, stream, p);
+      hipLaunchKernelGGL((prefill_kernel<false, TB, RB, LA, PIPE, true>), dim3(grid), dim3(kThreads), 0, stream, p);
   } else if (p.f16) {
-    hipLaunchKernelGGL((prefill_kernel<true, MT, NT, LA, PIPE, false>), dim3(grid), dim3(kThreads), 0, stream, p);
+    hipLaunchKernelGGL((prefill_kernel<true, TB, RB, LA, PIPE, false>), dim3(grid), dim3(kThreads), 0, stream, p);
   } else {
-    hipLaunchKernelGGL((prefill_kernel<false, MT, NT, LA, PIPE, false>), dim3(grid), dim3(kThreads), 0, stream, p);
+    hipLaunchKernelGGL((prefill_kernel<false, TB, RB, LA, PIPE, false>), dim3(grid), dim3(kThreads), 0, stream, p);
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || p.ks == 1) return e;
@@ -325,25 +375,19 @@ hipError_t launch_tile(const PrefillParams &p, hipStream_t stream) {
   return hipGetLastError();
 }
 
-#define TX_CANDIDATE(NAME, MT, NT, LA, PIPE)                                                            \
+#define TX_CANDIDATE(NAME, TB, RB, LA, PIPE)                                                            \
   Candidate {                                                                                          \
-    NAME, 16 * (MT), 64 * (NT), reinterpret_cast<const void *>(&prefill_kernel<false, MT, NT, LA, PIPE, false>), \
-        &launch_tile<MT, NT, LA, PIPE>, 2 * 16 * (MT) * kStride * 2                                    \
+    NAME, 32 * (TB), 128 * (RB), reinterpret_cast<const void *>(&prefill_kernel<false, TB, RB, LA, PIPE, false>), \
+        &launch_tile<TB, RB, LA, PIPE>, 2 * 32 * (TB) * kStride * 2                                    \
   }
 
-// Weight tiles in flight per wave, in K steps.
-#ifndef TX_PREFILL_LA
-#define TX_PREFILL_LA 2
-#endif
-
-// The two 128-token tiles pipeline their K loop (4-5% faster at T >= 128 on the 27B shapes); the
-// smaller tiles run it plainly (pipelining cost them up to 12% at T = 32).
+// The two 128-token tiles pipeline their K loop; the smaller tiles run it plainly.
 const Candidate kCandidates[] = {
-    TX_CANDIDATE("large_128x256x128", 8, 4, TX_PREFILL_LA, true),
-    TX_CANDIDATE("medium_128x128x128", 8, 2, TX_PREFILL_LA, true),
-    TX_CANDIDATE("medium_64x256x128", 4, 4, TX_PREFILL_LA, false),
-    TX_CANDIDATE("medium_64x128x128", 4, 2, TX_PREFILL_LA, false),
-    TX_CANDIDATE("small_32x128x128", 2, 2, TX_PREFILL_LA, false),
+    TX_CANDIDATE("large_128x256x128", 4, 2, TX_PREFILL_LA, true),
+    TX_CANDIDATE("medium_128x128x128", 4, 1, TX_PREFILL_LA, true),
+    TX_CANDIDATE("medium_64x256x128", 2, 2, TX_PREFILL_LA, false),
+    TX_CANDIDATE("medium_64x128x128", 2, 1, TX_PREFILL_LA, false),
+    TX_CANDIDATE("small_32x128x128", 1, 1, TX_PREFILL_LA, false),
 };
 
 const Candidate *find(int candidate) {
