@@ -180,6 +180,23 @@ def kernel_only(torch, ext, runtime, hardware, device, args) -> int:
     return 0
 
 
+def prefill_only(torch, ext, runtime, hardware, device, args) -> int:
+    """Launches for counter runs: the 5120->27648 prefill GEMM at ``--prompt`` tokens (the library's
+    default tile for that token count) on ``--layers`` distinct copies, twice each."""
+    lut = hardware.device_palette(device)
+    blocks, scales = encoded_weights(torch, [(INTER, HIDDEN)], lut)[(INTER, HIDDEN)]
+    handles = [runtime.pack_arrays(blocks, scales)[0] for _ in range(args.layers)]
+    x = torch.randn((args.prompt, HIDDEN), device=device).to(torch.bfloat16)
+    for _ in range(2):
+        for handle in handles:
+            ext.linear(handle, x)
+    torch.cuda.synchronize()
+    runtime.free(handles)
+    print(json.dumps({"prefill_only": True, "launches": 2 * len(handles), "tokens": args.prompt,
+                      "flops_per_launch": 2 * args.prompt * INTER * HIDDEN}), flush=True)
+    return 0
+
+
 def model_section(torch, args, model_name: str | None = None, context: int | None = None) -> dict:
     """Prefill tok/s at ``--prompt`` tokens (reference protocol, texelator/prefill.py:63-131) and
     graph-replayed greedy decode tok/s from the prompt up to ``context``, on a random-init BC4
@@ -240,6 +257,8 @@ def main() -> int:
                         help="decode steps timed per 512-position bucket (0 = every step)")
     parser.add_argument("--model-only", action="store_true",
                         help="profiling mode: only the model-level prefill and decode measurement (its JSON)")
+    parser.add_argument("--prefill-only", action="store_true",
+                        help="profiling mode: only the gate/up prefill GEMM at --prompt tokens over the layer copies")
     parser.add_argument("--kernel-only", action="store_true",
                         help="profiling mode: only the gate/up GEMV over the layer copies, then a plain copy of "
                              "COPY_BYTES bytes that calibrates the HBM byte counters")
@@ -263,6 +282,8 @@ def main() -> int:
 
     if args.kernel_only:
         return kernel_only(torch, ext, runtime, hardware, device, args)
+    if args.prefill_only:
+        return prefill_only(torch, ext, runtime, hardware, device, args)
     if args.model_only:
         print(json.dumps({"model_only": True, "model": model_section(torch, args)}), flush=True)
         return 0
