@@ -10,6 +10,8 @@ scales + bf16 x + fp32 y per linear) times the step count, divided by the timed 
 ``roofline`` is the 5120->27648 (gate/up) GEMV alone: its algorithmic bytes divided by its
 average launch time over back-to-back launches timed with HIP events on the launch stream.
 ``cpu_baseline`` is the C restatement of the decode + matvec on the host cores.
+``hbm_stream_read`` is a plain streaming read of the same launch size (the achievable HBM rate);
+``roofline.frac_of_stream_read`` is the GEMV's rate against it.
 """
 from __future__ import annotations
 
@@ -154,6 +156,33 @@ def prefill_section(torch, ext, stream, handles, candidates=range(5, 10), repeat
                 "all_us": {ext.candidate_name(c): round(t * 1e6, 2) for c, t in times.items()},
             }
     return out
+
+
+def stream_read(torch, stream, copies: int, repeats: int = 2) -> dict:
+    """Achievable HBM read rate for the gate/up launch size: a plain streaming-read kernel over
+    ``copies`` distinct buffers of the gate/up payload size, back-to-back launches between events
+    (the GEMV's timing method)."""
+    import ctypes
+
+    from texelator_amd import _lib
+    from texelator_amd._lib import check
+
+    nbytes = INTER * HIDDEN // 2
+    generator = torch.Generator(device="cuda").manual_seed(SEED + 3)
+    bufs = [torch.randint(0, 256, (nbytes,), dtype=torch.uint8, device="cuda", generator=generator)
+            for _ in range(copies)]
+    sink = torch.empty(4096, dtype=torch.int32, device="cuda")
+    lib = _lib.load()
+
+    def launch(i):
+        check(lib.tx_stream_read(ctypes.c_void_p(bufs[i % copies].data_ptr()), nbytes,
+                                 ctypes.c_void_p(sink.data_ptr()), ctypes.c_void_p(stream.cuda_stream)))
+
+    launch(0)
+    seconds = timed_launches(torch, stream, launch, repeats * copies)
+    del bufs
+    return {"GB/s": round(nbytes / seconds / 1e9, 1), "bytes_per_launch": nbytes, "avg_launch_us": round(seconds * 1e6, 3),
+            "launches": repeats * copies}
 
 
 def kernel_only(torch, ext, runtime, hardware, device, args) -> int:
@@ -409,6 +438,9 @@ def main() -> int:
         },
         "per_shape": per_shape,
     }
+    log("streaming-read reference")
+    result["hbm_stream_read"] = stream_read(torch, stream, args.layers)
+    result["roofline"]["frac_of_stream_read"] = round(achieved / result["hbm_stream_read"]["GB/s"], 4)
     if not args.no_prefill:
         log("prefill GEMM")
         with torch.cuda.stream(stream):

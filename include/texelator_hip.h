@@ -104,6 +104,11 @@ int tx_set_palette_table(uint64_t handle, const float *device_table);
  *  lookahead, device, decode GEMV K splits, LUT mode (0/1)]; the last four are this library's. */
 int tx_handle_info(uint64_t handle, int64_t *out, int n);
 
+/* No reference counterpart: a plain streaming read of `bytes` (multiple of 16, 16-byte aligned
+ * device memory), the achievable-bandwidth reference point next to which bench.py reports the
+ * GEMV. `sink` must hold 4096 uint32 (written only for a sentinel input). */
+int tx_stream_read(const void *data, int64_t bytes, uint32_t *sink, void *stream);
+
 /* Replaces texelator_free (texelator_cuda.cu:1538). Caller must ensure no work is pending. */
 int tx_free(uint64_t handle);
 

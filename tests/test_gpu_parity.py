@@ -356,3 +356,20 @@ def test_prefill_f16_split_k_matches_oracle(ext):
     w = bc4.decode_f16_bits(blocks, scales).view(np.float16).astype(np.float64)
     ref = x.double().numpy() @ w.T
     assert bc4.relative_rms(ref, outputs[0].double().cpu().numpy()) <= PREFILL_RRMS_TOL
+
+
+def test_stream_read_probe(ext):
+    """The streaming-read reference kernel runs over any 16-byte multiple and rejects the rest."""
+    import ctypes
+
+    from texelator_amd import _lib
+
+    data = torch.randint(0, 256, (1 << 20,), dtype=torch.uint8, device="cuda")
+    sink = torch.zeros(4096, dtype=torch.int32, device="cuda")
+    lib = _lib.load()
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    for nbytes in (16, 4096 + 16, data.numel()):
+        _lib.check(lib.tx_stream_read(ctypes.c_void_p(data.data_ptr()), nbytes, ctypes.c_void_p(sink.data_ptr()), stream))
+    torch.cuda.synchronize()
+    with pytest.raises(_lib.TexelatorError, match="multiple of 16"):
+        _lib.check(lib.tx_stream_read(ctypes.c_void_p(data.data_ptr()), 24, ctypes.c_void_p(sink.data_ptr()), stream))

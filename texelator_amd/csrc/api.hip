@@ -430,6 +430,15 @@ int tx_decode_dense(uint64_t value, int dtype, uint16_t *out, void *stream) {
   return TX_OK;
 }
 
+int tx_stream_read(const void *data, int64_t bytes, uint32_t *sink, void *stream) {
+  g_last_error.clear();
+  if (!data || !sink) return fail(TX_ERR_INVALID, "null data or sink");
+  if (bytes <= 0 || bytes % 16 != 0 || reinterpret_cast<uintptr_t>(data) % 16 != 0)
+    return fail(TX_ERR_INVALID, "stream_read: bytes must be a positive multiple of 16 and data 16-byte aligned");
+  TX_HIP(tx::launch_stream_read(data, (size_t)bytes, sink, reinterpret_cast<hipStream_t>(stream)));
+  return TX_OK;
+}
+
 int tx_kernel_info(int candidate, int64_t *out, int n) {
   g_last_error.clear();
   if (!out || n < 0) return fail(TX_ERR_INVALID, "invalid output buffer");

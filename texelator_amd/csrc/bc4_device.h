@@ -253,19 +253,28 @@ __device__ __forceinline__ uint32_t endpoint_offset(uint32_t word) {
   return __builtin_amdgcn_udot4(word & 0xC0C0C0C0u, 0x40100401u, 0u, false) >> 4;
 }
 
-// Decode one device block with the palette seeds read from LDS tables.
-template <bool F16 = false>
-__device__ __forceinline__ void decode_block_lds(uint32_t a, uint32_t b, float scale, uint32_t pm,
-                                                 const PaletteTableStorage &t, uint32_t w[8]) {
+// The palette seeds of one device block, read from the LDS tables.
+struct Seeds {
+  float base, end, step;
+  bool eight;
+};
+
+__device__ __forceinline__ Seeds read_seeds(uint32_t a, uint32_t b, const PaletteTableStorage &t) {
   const uint32_t o0 = endpoint_offset(a);
   const uint32_t o1 = endpoint_offset(b);
   const int od = (int)o1 - (int)o0;  // 4 * (e1 - e0)
   const char *base_bytes = reinterpret_cast<const char *>(t.base);
   const char *step_bytes = reinterpret_cast<const char *>(t.step + 254);
-  const float base = *reinterpret_cast<const float *>(base_bytes + o0);
-  const float end = *reinterpret_cast<const float *>(base_bytes + o1);
-  const float step = *reinterpret_cast<const float *>(step_bytes + od);
-  decode_from_seeds<F16>(base, end, step, od < 0, a, b, scale, pm, w);
+  return Seeds{*reinterpret_cast<const float *>(base_bytes + o0), *reinterpret_cast<const float *>(base_bytes + o1),
+               *reinterpret_cast<const float *>(step_bytes + od), od < 0};
+}
+
+// Decode one device block with the palette seeds read from LDS tables.
+template <bool F16 = false>
+__device__ __forceinline__ void decode_block_lds(uint32_t a, uint32_t b, float scale, uint32_t pm,
+                                                 const PaletteTableStorage &t, uint32_t w[8]) {
+  const Seeds s = read_seeds(a, b, t);
+  decode_from_seeds<F16>(s.base, s.end, s.step, s.eight, a, b, scale, pm, w);
 }
 
 }  // namespace tx

@@ -57,6 +57,10 @@ const char *prefill_candidate_name(int candidate);
 void prefill_candidate_shape(int candidate, int *tokens, int *rows, int *k);
 
 hipError_t launch_palette_probe(float *out, hipStream_t stream);
+// Streaming read of bytes (a multiple of 16) with kStreamReadBlocks workgroups; sink receives at
+// most one word per workgroup (only for an input that XORs to a sentinel value).
+constexpr int kStreamReadBlocks = 4096;
+hipError_t launch_stream_read(const void *data, size_t bytes, uint32_t *sink, hipStream_t stream);
 // Reference-layout device blocks [M][bpr][8] -> device tiles (RG x CG tiles of 1 KiB).
 hipError_t launch_repack(const uint8_t *blocks, int M, int bpr, int RG, int CG, uint4 *tiles, hipStream_t stream);
 hipError_t launch_decode_dense(const uint4 *tiles, const float *scales, const float4 *lut, int M, int K, int RG, int CG,

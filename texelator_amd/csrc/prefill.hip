@@ -41,6 +41,12 @@ constexpr int kXcds = 8;
 #ifndef TX_PREFILL_LA
 #define TX_PREFILL_LA 2
 #endif
+// Scheduling regions per K step of the woven loop (each holds 8/NR MFMA groups and its share of
+// the next tile's block decodes).
+#ifndef TX_PREFILL_REGIONS
+#define TX_PREFILL_REGIONS 8
+#endif
+constexpr int NR = TX_PREFILL_REGIONS;
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
@@ -144,8 +150,16 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillParams p) {
   // Activation staging: XC uint4 per thread per K step (16 uint4 per token row). Rows and
   // columns out of range load a clamped, valid address and are masked to zero.
   uint4 xr[XC];
+  // Chunk v of this thread is token row 16v + tid/16 of the tile, columns (tid%16)*8..+7 of the step.
+  const bool tile_full = w.t0 + BT <= p.tokens;  // uniform: no row to mask
+  const uint16_t *xt = x + (size_t)(w.t0 + (threadIdx.x >> 4)) * p.K + (threadIdx.x & 15) * 8;
   auto load_x = [&](int j) {
     const int c = w.c_begin + min(j, w.nc - 1);
+    if (tile_full && (c + 1) * kTileK <= p.K) {
+#pragma unroll
+      for (int v = 0; v < XC; ++v) xr[v] = *reinterpret_cast<const uint4 *>(xt + (size_t)v * 16 * p.K + c * kTileK);
+      return;
+    }
 #pragma unroll
     for (int v = 0; v < XC; ++v) {
       const int idx = v * kThreads + threadIdx.x;
@@ -246,35 +260,78 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillParams p) {
           return *reinterpret_cast<const u32x4 *>(xb + (tb * 32 + r32) * kStride + 16 * (4 * h + (sg >> 1)) +
                                                   8 * (sg & 1));
         };
-        constexpr int kBlocks = 4 * RB;  // blocks per lane and step, spread over the 8 groups
-        u32x4 bcur[TB];
+        constexpr int kBlocks = 4 * RB;                  // blocks per lane and step
+        constexpr int kRegions = kBlocks < NR ? kBlocks : NR;  // regions per step
+        constexpr int kGroups = 8 / kRegions;             // MFMA groups (K sets) per region
+        constexpr int kPer = kBlocks / kRegions;          // block decodes per region
+        static_assert(8 % kRegions == 0 && kBlocks % kRegions == 0, "regions must split the step evenly");
+        auto block_words = [&](int q, uint32_t &wa, uint32_t &wb) {
+          const uint4 &piece = next[q >> 2][(q & 3) >> 1];
+          wa = (q & 1) ? piece.z : piece.x;
+          wb = (q & 1) ? piece.w : piece.y;
+        };
+        u32x4 bcur[kGroups][TB];
 #pragma unroll
-        for (int tb = 0; tb < TB; ++tb) bcur[tb] = read_b(tb, 0);
+        for (int g = 0; g < kGroups; ++g)
 #pragma unroll
-        for (int sg = 0; sg < 8; ++sg) {
-          u32x4 bnext[TB];
-          if (sg + 1 < 8) {
+          for (int tb = 0; tb < TB; ++tb) bcur[g][tb] = read_b(tb, g);
+        // The palette seeds of each region's blocks are read one region ahead, so their LDS
+        // latency is not on the decode's critical path.
+        Seeds seeds[kPer];
 #pragma unroll
-            for (int tb = 0; tb < TB; ++tb) bnext[tb] = read_b(tb, sg + 1);
+        for (int e = 0; e < kPer; ++e) {
+          uint32_t wa, wb;
+          block_words(e, wa, wb);
+          seeds[e] = read_seeds(wa, wb, tables);
+        }
+#pragma unroll
+        for (int rg = 0; rg < kRegions; ++rg) {
+          u32x4 bnext[kGroups][TB];
+          if (rg + 1 < kRegions) {
+#pragma unroll
+            for (int g = 0; g < kGroups; ++g)
+#pragma unroll
+              for (int tb = 0; tb < TB; ++tb) bnext[g][tb] = read_b(tb, (rg + 1) * kGroups + g);
           }
-          const bool decodes = (sg * kBlocks) % 8 < kBlocks;
-          const int q = sg * kBlocks / 8, b = q >> 2, jj = q & 3;
-          if (decodes) {
-            const uint4 &piece = next[b][jj >> 1];
+          Seeds cur[kPer];
+#pragma unroll
+          for (int e = 0; e < kPer; ++e) cur[e] = seeds[e];
+          if (rg + 1 < kRegions) {
+#pragma unroll
+            for (int e = 0; e < kPer; ++e) {
+              uint32_t na, nb;
+              block_words((rg + 1) * kPer + e, na, nb);
+              seeds[e] = read_seeds(na, nb, tables);
+            }
+          }
+#pragma unroll
+          for (int e = 0; e < kPer; ++e) {
+            const int q = rg * kPer + e, b = q >> 2, jj = q & 3;
+            uint32_t wa, wb;
+            block_words(q, wa, wb);
             uint32_t d[8];
-            decode_block_lds<F16>((jj & 1) ? piece.z : piece.x, (jj & 1) ? piece.w : piece.y, scale[b], pm[b], tables, d);
+            decode_from_seeds<F16>(cur[e].base, cur[e].end, cur[e].step, cur[e].eight, wa, wb, scale[b], pm[b], d);
             anext[b][2 * jj] = u32x4{d[0], d[1], d[2], d[3]};
             anext[b][2 * jj + 1] = u32x4{d[4], d[5], d[6], d[7]};
           }
 #pragma unroll
-          for (int tb = 0; tb < TB; ++tb)
+          for (int g = 0; g < kGroups; ++g)
 #pragma unroll
-            for (int rb = 0; rb < RB; ++rb) acc[tb][rb] = mfma<F16>(acur[rb][sg], bcur[tb], acc[tb][rb]);
-          if (decodes) asm volatile("" : "+v"(anext[b][2 * jj]), "+v"(anext[b][2 * jj + 1]));
+            for (int tb = 0; tb < TB; ++tb)
+#pragma unroll
+              for (int rb = 0; rb < RB; ++rb)
+                acc[tb][rb] = mfma<F16>(acur[rb][rg * kGroups + g], bcur[g][tb], acc[tb][rb]);
+#pragma unroll
+          for (int e = 0; e < kPer; ++e) {
+            const int q = rg * kPer + e, b = q >> 2, jj = q & 3;
+            asm volatile("" : "+v"(anext[b][2 * jj]), "+v"(anext[b][2 * jj + 1]));
+          }
           __builtin_amdgcn_sched_barrier(0);
-          if (sg + 1 < 8) {
+          if (rg + 1 < kRegions) {
 #pragma unroll
-            for (int tb = 0; tb < TB; ++tb) bcur[tb] = bnext[tb];
+            for (int g = 0; g < kGroups; ++g)
+#pragma unroll
+              for (int tb = 0; tb < TB; ++tb) bcur[g][tb] = bnext[g][tb];
           }
         }
       }
