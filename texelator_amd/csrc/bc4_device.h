@@ -15,10 +15,11 @@
 // this is exact-rounded for every |n| <= 889 and d in {127, 635, 889} (checked exhaustively).
 //
 // Device block (8 bytes, two little-endian dwords A, B), written by the host repack:
-//   A byte c (c = 0..3): bits 0-2 = sel[c],     bits 3-5 = sel[4+c],  bits 6-7 = bits 2c..2c+1 of eb0
-//   B byte c:            bits 0-2 = sel[8+c],   bits 3-5 = sel[12+c], bits 6-7 = bits 2c..2c+1 of eb1
-// with eb = clamp(e, -127, 127) + 127. Selector groups (A & 0x07070707, (A>>3) & 0x07070707, ...)
-// are then ready-made v_perm_b32 byte selectors for four positions each.
+//   A byte c (c = 0..3): bits 0-2 = sel[4+c],  bits 3-4 = bits 2c..2c+1 of eb0,  bits 5-7 = sel[c]
+//   B byte c:            bits 0-2 = sel[12+c], bits 3-4 = bits 2c..2c+1 of eb1,  bits 5-7 = sel[8+c]
+// with eb = clamp(e, -127, 127) + 127. Selector groups ((A>>5) & 0x07070707, A & 0x07070707, ...)
+// are then ready-made v_perm_b32 byte selectors for four positions each, and one v_dot4 of
+// A & 0x18181818 with weights 1,4,16,64 gives 8*eb0: a byte offset into a table of 8-byte entries.
 //
 // Tile layout: rows padded to a multiple of 16, blocks per row padded to a multiple of 8. A tile
 // is 16 rows x 8 blocks = 1 KiB; tile (g, c) sits at ((g * CG) + c) * 1 KiB. Inside a tile, lane
@@ -43,17 +44,17 @@ constexpr float kInv889Hi = 0x1.26e00ap-10f;
 constexpr float kInv889Lo = -0x1.91ff6cp-35f;
 constexpr float kInv635Hi = 0x1.9cd34p-10f;
 constexpr float kInv635Lo = 0x1.9cd34p-38f;
-// The same pairs pre-divided by 64, because the register endpoint extraction yields 64*e (the
-// scaling by 2^6 is exact, so results are unchanged).
-constexpr float kR127Hi = kInv127Hi / 64.0f;
-constexpr float kR127Lo = kInv127Lo / 64.0f;
-constexpr float kR889Hi = kInv889Hi / 64.0f;
-constexpr float kR889Lo = kInv889Lo / 64.0f;
-constexpr float kR635Hi = kInv635Hi / 64.0f;
-constexpr float kR635Lo = kInv635Lo / 64.0f;
+// The same pairs pre-divided by 8, because the register endpoint extraction yields 8*e (the
+// scaling by 2^3 is exact, so results are unchanged).
+constexpr float kR127Hi = kInv127Hi / 8.0f;
+constexpr float kR127Lo = kInv127Lo / 8.0f;
+constexpr float kR889Hi = kInv889Hi / 8.0f;
+constexpr float kR889Lo = kInv889Lo / 8.0f;
+constexpr float kR635Hi = kInv635Hi / 8.0f;
+constexpr float kR635Lo = kInv635Lo / 8.0f;
 
 // Device block whose endpoints are 0/0 and selectors 0: decodes to zero weights (padding).
-constexpr uint32_t kZeroBlockWord = 0x40C0C0C0u;
+constexpr uint32_t kZeroBlockWord = 0x08181818u;
 
 // One reference block (8 bytes: e0, e1, 48-bit little-endian selector field) -> device words
 // A, B (layout above). Endpoint byte -128 is clamped to -127 as the decoder does. Used by the
@@ -74,8 +75,8 @@ __host__ __device__ inline void encode_device_block(const uint8_t *blk, uint32_t
     const uint32_t s1 = (uint32_t)(bits >> (3 * (4 + c))) & 7u;
     const uint32_t s2 = (uint32_t)(bits >> (3 * (8 + c))) & 7u;
     const uint32_t s3 = (uint32_t)(bits >> (3 * (12 + c))) & 7u;
-    a |= (s0 | (s1 << 3) | (((eb0 >> (2 * c)) & 3u) << 6)) << (8 * c);
-    b |= (s2 | (s3 << 3) | (((eb1 >> (2 * c)) & 3u) << 6)) << (8 * c);
+    a |= (s1 | (((eb0 >> (2 * c)) & 3u) << 3) | (s0 << 5)) << (8 * c);
+    b |= (s3 | (((eb1 >> (2 * c)) & 3u) << 3) | (s2 << 5)) << (8 * c);
   }
 }
 
@@ -112,10 +113,10 @@ __device__ __forceinline__ uint32_t pack_weights(float a, float b) {
   else return pack_bf16x2(a, b);
 }
 
-// 64*e from the 2-bit fields in bits 6-7 of each byte (dot4 with weights 1,4,16,64 and a
-// wrapping bias of -127*64).
-__device__ __forceinline__ float endpoint_x64(uint32_t word) {
-  return (float)(int)__builtin_amdgcn_udot4(word & 0xC0C0C0C0u, 0x40100401u, 0xFFFFE040u, false);
+// 8*e from the 2-bit fields in bits 3-4 of each byte (dot4 with weights 1,4,16,64 and a
+// wrapping bias of -127*8).
+__device__ __forceinline__ float endpoint_x8(uint32_t word) {
+  return (float)(int)__builtin_amdgcn_udot4(word & 0x18181818u, 0x40100401u, 0xFFFFFC08u, false);
 }
 
 struct Palette {
@@ -126,8 +127,8 @@ struct Palette {
 // The fp32 palette of one block (the values a LUT row holds).
 __device__ __forceinline__ Palette palette8(uint32_t a, uint32_t b) {
   Palette out;
-  float f0 = endpoint_x64(a);
-  float f1 = endpoint_x64(b);
+  float f0 = endpoint_x8(a);
+  float f1 = endpoint_x8(b);
   float d = f1 - f0;
   out.eight = f0 > f1;
   float rhi = out.eight ? kR889Hi : kR635Hi;
@@ -159,8 +160,8 @@ __device__ __forceinline__ void select_weights(uint32_t pk01, uint32_t pk23, uin
   uint32_t hi0 = perm(pk23, pk01, 0x07050301u);
   uint32_t lo1 = perm(pk67, pk45, 0x06040200u);
   uint32_t hi1 = perm(pk67, pk45, 0x07050301u);
-  uint32_t sel[4] = {a & 0x07070707u, (a >> 3) & 0x07070707u, b & 0x07070707u,
-                     (b >> 3) & 0x07070707u};
+  uint32_t sel[4] = {(a >> 5) & 0x07070707u, a & 0x07070707u, (b >> 5) & 0x07070707u,
+                     b & 0x07070707u};
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
     uint32_t l = perm(lo1, lo0, sel[g]);
@@ -202,8 +203,8 @@ __device__ __forceinline__ void decode_from_palette(float4 p03, float4 p47, uint
 // Row of a block's endpoint pair in a 255 x 255 x 8 palette table, (e1 + 127) * 255 + (e0 + 127)
 // (the probe layout), from the device words' 2-bit endpoint fields.
 __device__ __forceinline__ uint32_t palette_row(uint32_t a, uint32_t b) {
-  const uint32_t eb0 = __builtin_amdgcn_udot4(a & 0xC0C0C0C0u, 0x40100401u, 0u, false) >> 6;
-  const uint32_t eb1 = __builtin_amdgcn_udot4(b & 0xC0C0C0C0u, 0x40100401u, 0u, false) >> 6;
+  const uint32_t eb0 = __builtin_amdgcn_udot4(a & 0x18181818u, 0x40100401u, 0u, false) >> 3;
+  const uint32_t eb1 = __builtin_amdgcn_udot4(b & 0x18181818u, 0x40100401u, 0u, false) >> 3;
   return eb1 * 255u + eb0;
 }
 
@@ -212,8 +213,8 @@ __device__ __forceinline__ uint32_t palette_row(uint32_t a, uint32_t b) {
 template <bool F16 = false>
 __device__ __forceinline__ void decode_block(uint32_t a, uint32_t b, float scale, uint32_t pm,
                                              uint32_t w[8]) {
-  float f0 = endpoint_x64(a);
-  float f1 = endpoint_x64(b);
+  float f0 = endpoint_x8(a);
+  float f1 = endpoint_x8(b);
   float d = f1 - f0;
   bool eight = f0 > f1;
   float rhi = eight ? kR889Hi : kR635Hi;
@@ -224,33 +225,33 @@ __device__ __forceinline__ void decode_block(uint32_t a, uint32_t b, float scale
   decode_from_seeds<F16>(base, end, step, eight, a, b, scale, pm, w);
 }
 
-// LDS tables of the palette seeds, shared by a workgroup:
-//   base[eb]      = RN((eb - 127) / 127),                       eb = 0..254
-//   step[d + 254] = RN(d / 889) if d < 0 else RN(d / 635),      d = e1 - e0 = -254..254
-// (d < 0 is exactly the 8-value mode e0 > e1). Same arithmetic as decode_block.
+// LDS table of the palette seeds, shared by a workgroup, as 509 entries of 8 bytes:
+//   entry[i].base = RN((i - 127) / 127)                                       i = 0..254
+//   entry[i].step = RN(d / 889) if d < 0 else RN(d / 635), d = i - 254,      i = 0..508
+// (d = e1 - e0 < 0 is exactly the 8-value mode e0 > e1). Same arithmetic as decode_block. Both
+// fields are addressed by 8 * index, which is what the endpoint extraction yields.
+struct SeedEntry {
+  float base, step;
+};
 struct PaletteTableStorage {
-  float base[256];
-  float step[512];
+  SeedEntry entry[509];
 };
 
 __device__ __forceinline__ void build_palette_tables(PaletteTableStorage &t, int tid, int nthreads) {
-  for (int idx = tid; idx < 256 + 512; idx += nthreads) {
-    if (idx < 256) {
-      const float e = (float)(idx - 127);
-      t.base[idx] = __builtin_fmaf(e, kInv127Hi, e * kInv127Lo);
-    } else {
-      const int d = idx - 256 - 254;
-      const float f = (float)d;
-      const float rhi = d < 0 ? kInv889Hi : kInv635Hi;
-      const float rlo = d < 0 ? kInv889Lo : kInv635Lo;
-      t.step[idx - 256] = __builtin_fmaf(f, rhi, f * rlo);
-    }
+  for (int idx = tid; idx < 509; idx += nthreads) {
+    const float e = (float)(idx - 127);
+    const int d = idx - 254;
+    const float f = (float)d;
+    const float rhi = d < 0 ? kInv889Hi : kInv635Hi;
+    const float rlo = d < 0 ? kInv889Lo : kInv635Lo;
+    t.entry[idx].base = idx < 255 ? __builtin_fmaf(e, kInv127Hi, e * kInv127Lo) : 0.0f;
+    t.entry[idx].step = __builtin_fmaf(f, rhi, f * rlo);
   }
 }
 
-// 4 * eb from the 2-bit endpoint fields in bits 6-7 of each byte: a byte offset into base[].
+// 8 * eb from the 2-bit endpoint fields in bits 3-4 of each byte: a byte offset into entry[].
 __device__ __forceinline__ uint32_t endpoint_offset(uint32_t word) {
-  return __builtin_amdgcn_udot4(word & 0xC0C0C0C0u, 0x40100401u, 0u, false) >> 4;
+  return __builtin_amdgcn_udot4(word & 0x18181818u, 0x40100401u, 0u, false);
 }
 
 // The palette seeds of one device block, read from the LDS tables.
@@ -262,10 +263,10 @@ struct Seeds {
 __device__ __forceinline__ Seeds read_seeds(uint32_t a, uint32_t b, const PaletteTableStorage &t) {
   const uint32_t o0 = endpoint_offset(a);
   const uint32_t o1 = endpoint_offset(b);
-  const int od = (int)o1 - (int)o0;  // 4 * (e1 - e0)
-  const char *base_bytes = reinterpret_cast<const char *>(t.base);
-  const char *step_bytes = reinterpret_cast<const char *>(t.step + 254);
-  return Seeds{*reinterpret_cast<const float *>(base_bytes + o0), *reinterpret_cast<const float *>(base_bytes + o1),
+  const int od = (int)o1 - (int)o0;  // 8 * (e1 - e0)
+  const char *bytes = reinterpret_cast<const char *>(t.entry);
+  const char *step_bytes = reinterpret_cast<const char *>(&t.entry[254].step);
+  return Seeds{*reinterpret_cast<const float *>(bytes + o0), *reinterpret_cast<const float *>(bytes + o1),
                *reinterpret_cast<const float *>(step_bytes + od), od < 0};
 }
 

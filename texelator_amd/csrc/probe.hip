@@ -16,7 +16,7 @@ namespace {
 __device__ __forceinline__ uint32_t endpoint_word(uint32_t eb) {
   uint32_t w = 0;
 #pragma unroll
-  for (int c = 0; c < 4; ++c) w |= ((eb >> (2 * c)) & 3u) << (8 * c + 6);
+  for (int c = 0; c < 4; ++c) w |= ((eb >> (2 * c)) & 3u) << (8 * c + 3);
   return w;
 }
 
