@@ -206,7 +206,7 @@ def _random_handle(ext, m, k, seed, bias=False):
 
 @pytest.mark.parametrize("m,k,bias", [(5120, 5120, False), (5120, 5120, True), (16384, 256, True), (256, 512, False)])
 def test_add_rmsnorm_split_is_bit_identical(ext, m, k, bias):
-    """linear_split + add_rmsnorm_split == linear + add_rmsnorm, bit for bit (k splits 5, 1, 1)."""
+    """linear_split + add_rmsnorm_split == linear + add_rmsnorm, bit for bit (k splits 4, 1, 1)."""
     handle = _random_handle(ext, m, k, seed=m + k, bias=bias)
     try:
         g = torch.Generator(device="cuda").manual_seed(11)

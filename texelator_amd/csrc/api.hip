@@ -101,10 +101,15 @@ int device_cus(int device) {
   return 256;
 }
 
+// Target workgroups per CU for short matrices (their one-token GEMV is latency-bound).
+#ifndef TX_GEMV_SPLIT_TARGET
+#define TX_GEMV_SPLIT_TARGET 4
+#endif
+
 int choose_splits(int RG, int CG, int cus) {
   int ks = 1;
   if (RG < 1024) {
-    ks = (6 * cus + RG - 1) / RG;
+    ks = (TX_GEMV_SPLIT_TARGET * cus + RG - 1) / RG;
     ks = std::min(ks, std::max(1, CG / 4));
   }
   ks = std::max(ks, (CG + tx::kGemvMaxLdsColumns - 1) / tx::kGemvMaxLdsColumns);
