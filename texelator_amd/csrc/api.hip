@@ -117,11 +117,12 @@ int choose_splits(int RG, int CG, int cus) {
 }
 
 // Default tile by token count (the autotuner's profile overrides it): measured best on the 27B-class
-// shapes -- small_32x128 up to 32 tokens, medium_64x128 up to 64, large_128x256 beyond.
+// shapes -- small_32x128 up to 32 tokens, medium_64x128 up to 64, medium_128x128 beyond (two
+// workgroups per CU, which hide each other's LDS and decode latency).
 int default_candidate(int64_t tokens) {
   if (tokens <= 32) return 9;
   if (tokens <= 64) return 8;
-  return 5;
+  return 6;
 }
 
 // Workspace bytes of a prefill call (split-K partials), 0 if none.

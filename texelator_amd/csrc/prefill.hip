@@ -9,14 +9,17 @@
 // A workgroup (4 waves) owns BT = 32*TB tokens x BN = 128*RB output rows x one K range (split):
 //   * each wave owns RB blocks of 32 rows (two 16-row tile groups each). Per 128-wide K step it
 //     streams the two groups' 1 KiB tiles (LA steps ahead): lane l gathers the 32 bytes holding
-//     blocks 4h..4h+3 (h = l / 32) of row l % 32, and decodes them (palette seeds from LDS
-//     tables) straight into MFMA A operands -- weights never pass through LDS, and no dense
+//     blocks 2h, 2h+1, 4+2h, 5+2h (h = l / 32) of row l % 32, and decodes them (palette seeds from
+//     LDS tables) straight into MFMA A operands -- weights never pass through LDS, and no dense
 //     16-bit copy exists anywhere;
-//   * v_mfma_f32_32x32x16_bf16 (twice the rate of the 16x16x32 form on gfx950): MFMA s = 2j + e
-//     of a step takes positions 8e..8e+7 of block j from lanes 0-31 and of block 4+j from lanes
-//     32-63, i.e. K = {16j + 8e ..+7} u {64 + 16j + 8e ..+7}. The activations of the step
-//     (BT x 128 bf16) are double-buffered in LDS, shared by the four waves, and read with the
-//     same K sets;
+//   * v_mfma_f32_32x32x16_bf16 (twice the rate of the 16x16x32 form on gfx950): MFMA
+//     s = 4*h2 + 2j + e of a step (h2 = which 64-wide half of the step) takes positions 8e..8e+7 of
+//     block 4*h2 + j from lanes 0-31 and of block 4*h2 + 2 + j from lanes 32-63, i.e.
+//     K = {64*h2 + 16j + 8e ..+7} u {64*h2 + 32 + 16j + 8e ..+7}: every MFMA's K set lies in one
+//     64-wide half. The activations of the step (BT x 128 bf16) are double-buffered in LDS, shared
+//     by the four waves, and read with the same K sets; they are staged by direct global-to-LDS
+//     loads (no registers) one step ahead, in rows of 256 bytes whose 16-byte slots are
+//     XOR-swizzled by row;
 //   * acc[tb][rb] = D[32 rows of block rb][32 tokens of block tb].
 // Every candidate uses the same MFMA K grouping and order, and the K splits depend only on the
 // shape, so all candidates give bitwise-identical results. With several splits the partial sums
@@ -34,7 +37,6 @@ namespace tx {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kStride = 136;  // LDS row stride of the activation tile in bf16 (128 + 8 padding)
 constexpr int kXcds = 8;
 
 // Weight tiles in flight per wave, in K steps.
@@ -43,6 +45,12 @@ constexpr int kXcds = 8;
 #endif
 // Scheduling regions per K step of the woven loop (each holds 8/NR MFMA groups and its share of
 // the next tile's block decodes).
+// When a step issues the direct loads of the next step's activations: 0 before its weight
+// loads, 1 after them, 2 spread over the woven regions (pipelined tiles; the others as 1).
+#ifndef TX_PREFILL_STAGE
+#define TX_PREFILL_STAGE 2
+#endif
+constexpr int kStage = TX_PREFILL_STAGE;
 #ifndef TX_PREFILL_REGIONS
 #define TX_PREFILL_REGIONS 8
 #endif
@@ -106,9 +114,13 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillParams p) {
   static_assert(!PIPE || LA >= 2, "the pipelined K loop needs two weight tiles in flight");
   constexpr int BT = 32 * TB;
   constexpr int BN = 128 * RB;
-  constexpr int XC = BT * 16 / kThreads;  // activation chunks (8 bf16) staged per thread per step
-  constexpr int R = LA + 1;
-  __shared__ __attribute__((aligned(16))) uint16_t xs[2][BT * kStride];
+  constexpr int XC = BT * 16 / kThreads;  // 16-byte activation chunks staged per thread per step
+  constexpr int D = PIPE ? 1 : 0;         // step j decodes weight tile j + D
+  constexpr int NS = LA - D;              // weight tiles held between steps
+  // The two activation buffers are separate LDS objects, so the compiler can tell the reads of
+  // one from the direct-to-LDS loads that fill the other and does not make them wait.
+  __shared__ __attribute__((aligned(16))) uint16_t xs0[BT * kTileK];
+  __shared__ __attribute__((aligned(16))) uint16_t xs1[BT * kTileK];
   __shared__ PaletteTableStorage tables;
 
   WorkItem w;
@@ -119,69 +131,91 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillParams p) {
   const int r32 = lane & 31;  // row of the 32-row block (A), token of the 32-token block (B)
   const int h = lane >> 5;    // which four blocks of the step this lane holds
   const uint16_t *x = static_cast<const uint16_t *>(p.x);
+  // K offset within the step of this lane's 8 activations for MFMA s (s = 4*h2 + 2*j + e).
+  auto k_offset = [&](int s) { return 64 * (s >> 2) + 32 * h + 16 * ((s >> 1) & 1) + 8 * (s & 1); };
 
   // Row blocks of this wave: 32 rows = tile groups 2b and 2b+1 (clamped into the matrix; rows
-  // past M are computed, never stored). Lane slot (row & 15) + 32h of a tile holds blocks
-  // 4h, 4h+1 of that row; slot + 16 holds blocks 4h+2, 4h+3.
+  // past M are computed, never stored). Lane slot (row & 15) + 16h of a tile holds blocks
+  // 2h, 2h+1 of that row; slot + 32 holds blocks 4+2h, 5+2h.
   const uint4 *gtiles[RB];
   float scale[RB];
   uint32_t pm[RB];
 #pragma unroll
   for (int b = 0; b < RB; ++b) {
     const int g = min(w.n0 / kTileRows + (wave * RB + b) * 2 + (r32 >> 4), p.RG - 1);
-    gtiles[b] = p.tiles + ((size_t)g * p.CG + w.c_begin) * 64 + (lane & 15) + 32 * h;
+    gtiles[b] = p.tiles + ((size_t)g * p.CG + w.c_begin) * 64 + (lane & 15) + 16 * h;
     scale[b] = p.scales[g * kTileRows + (lane & 15)];
     pm[b] = pm_scale_pair<F16>(scale[b]);
   }
-
-  // Weight ring: slot s holds the two 16-byte pieces of each row block for one K step.
-  uint4 ring[R][RB][2];
+  // The two 16-byte pieces of each row block for one K step (past the end: the last step's).
   auto load_tiles = [&](uint4 (&slot)[RB][2], int j) {
     const size_t off = (size_t)min(j, w.nc - 1) * 64;
 #pragma unroll
     for (int b = 0; b < RB; ++b) {
       slot[b][0] = load_stream(gtiles[b] + off);
-      slot[b][1] = load_stream(gtiles[b] + off + 16);
+      slot[b][1] = load_stream(gtiles[b] + off + 32);
     }
   };
-#pragma unroll
-  for (int u = 0; u < LA; ++u) load_tiles(ring[u], u);
 
-  // Activation staging: XC uint4 per thread per K step (16 uint4 per token row). Rows and
-  // columns out of range load a clamped, valid address and are masked to zero.
-  uint4 xr[XC];
-  // Chunk v of this thread is token row 16v + tid/16 of the tile, columns (tid%16)*8..+7 of the step.
-  const bool tile_full = w.t0 + BT <= p.tokens;  // uniform: no row to mask
-  const uint16_t *xt = x + (size_t)(w.t0 + (threadIdx.x >> 4)) * p.K + (threadIdx.x & 15) * 8;
-  auto load_x = [&](int j) {
-    const int c = w.c_begin + min(j, w.nc - 1);
-    if (tile_full && (c + 1) * kTileK <= p.K) {
+  // Activation tile of a step in LDS: token row r takes 256 bytes, and its 16-byte slot q holds
+  // columns 8*(q ^ (r % 16))..+7 of the step (XOR swizzle: the 16 rows one MFMA operand read
+  // serves per LDS pass fall on distinct banks). Thread i stages row 16v + i/16 (v < XC) into
+  // slot i % 16; with a direct load, lane l of a wave lands in slot l of the wave's 1 KiB.
+  const int srow = threadIdx.x >> 4;                 // = row % 16 for every v
+  const int scol = ((threadIdx.x & 15) ^ srow) * 8;  // step column of the chunk this thread stages
+  const bool tile_full = w.t0 + BT <= p.tokens;      // uniform: no row past the tokens
+  const uint32_t lane_off = (uint32_t)(srow * p.K + scol) * 2;  // bytes from row 16v, column 0
+  auto stage_part = [&](uint16_t *buf, int j, int v0, int v1) {
+    const int c = w.c_begin + j;
+    if ((c + 1) * kTileK <= p.K) {
+      // Direct loads: a uniform base (row 16v of the tile, the step's first column) plus a 32-bit
+      // lane offset. Rows past the tokens repeat the last token; their outputs are never stored.
+      // The base row is clamped too, so the offset is never negative.
 #pragma unroll
-      for (int v = 0; v < XC; ++v) xr[v] = *reinterpret_cast<const uint4 *>(xt + (size_t)v * 16 * p.K + c * kTileK);
-      return;
-    }
-#pragma unroll
-    for (int v = 0; v < XC; ++v) {
-      const int idx = v * kThreads + threadIdx.x;
-      const int t = w.t0 + (idx >> 4);
-      const int k = c * kTileK + (idx & 15) * 8;
-      const uint32_t keep = (t < p.tokens && k < p.K) ? 0xFFFFFFFFu : 0u;
-      const uint4 value =
-          *reinterpret_cast<const uint4 *>(x + (size_t)min(t, p.tokens - 1) * p.K + min(k, p.K - 8));
-      xr[v] = make_uint4(value.x & keep, value.y & keep, value.z & keep, value.w & keep);
+      for (int v = v0; v < v1; ++v) {
+        const int row0 = tile_full ? w.t0 + 16 * v : min(w.t0 + 16 * v, p.tokens - 1);
+        const char *base = reinterpret_cast<const char *>(x + ((size_t)row0 * p.K + c * kTileK));
+        uint32_t off = lane_off;
+        if (!tile_full) off = (uint32_t)((min(w.t0 + 16 * v + srow, p.tokens - 1) - row0) * p.K + scol) * 2;
+        __builtin_amdgcn_global_load_lds((const void *)(base + off),
+                                         (__attribute__((address_space(3))) void *)(buf + (16 * v + 4 * wave) * kTileK),
+                                         16, 0, 0);
+      }
+    } else if (v0 == 0) {
+      // The matrix's last, partial K tile: columns past K are staged as zeros.
+      const int k = c * kTileK + scol;
+#pragma unroll 2
+      for (int v = 0; v < XC; ++v) {
+        const int t = min(w.t0 + 16 * v + srow, p.tokens - 1);
+        uint4 value = make_uint4(0u, 0u, 0u, 0u);
+        if (k < p.K) value = *reinterpret_cast<const uint4 *>(x + (size_t)t * p.K + k);
+        *reinterpret_cast<uint4 *>(buf + (16 * v + srow) * kTileK + (threadIdx.x & 15) * 8) = value;
+      }
     }
   };
-  auto store_x = [&](int buf) {
-#pragma unroll
-    for (int v = 0; v < XC; ++v) {
-      const int idx = v * kThreads + threadIdx.x;
-      *reinterpret_cast<uint4 *>(&xs[buf][(idx >> 4) * kStride + (idx & 15) * 8]) = xr[v];
-    }
+  auto stage_x = [&](uint16_t *buf, int j) { stage_part(buf, j, 0, XC); };
+  // Element offset of this lane's B operand of MFMA s in token block 0 of a staged tile.
+  const int sw = r32 & 15;
+  auto b_off = [&](int s) { return r32 * kTileK + 8 * ((k_offset(s) >> 3) ^ sw); };
+  // End of a step: this wave's staged chunks have landed (at most the 2*RB weight loads issued
+  // after them are outstanding, and loads complete in order), its LDS stores are done, then the
+  // workgroup barrier. A fence would also wait for the weight loads, which are meant to stay in
+  // flight across the barrier; the memory clobber keeps the compiler from moving LDS accesses
+  // across it.
+  auto step_barrier = [&]() {
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::"n"(kStage == 0 ? 2 * RB : 0) : "memory");
   };
-  load_x(0);
-  store_x(0);
-  load_x(1);
+
+  // Prologue: step 0's activations, the palette tables, the first weight tiles.
+  stage_x(xs0, 0);
+  __builtin_amdgcn_sched_barrier(0);
+  uint4 ring[NS > 0 ? NS : 1][RB][2];
+  uint4 first[RB][2];
+  if constexpr (PIPE) load_tiles(first, 0);
+#pragma unroll
+  for (int u = 0; u < NS; ++u) load_tiles(ring[u], u + D);
   if constexpr (!LUT) build_palette_tables(tables, threadIdx.x, kThreads);
+  __builtin_amdgcn_s_waitcnt(0x0F70);
   __syncthreads();
 
   f32x16 acc[TB][RB];
@@ -213,52 +247,68 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillParams p) {
       }
     }
   };
-  auto mfma_step = [&](int j, const u32x4 (&a)[RB][8]) {
-    const uint16_t *xb = xs[j & 1];
+  auto mfma_step = [&](const uint16_t *xb, const u32x4 (&a)[RB][8]) {
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
-      const int k_off = 16 * (4 * h + (s >> 1)) + 8 * (s & 1);
 #pragma unroll
       for (int tb = 0; tb < TB; ++tb) {
-        const u32x4 bv = *reinterpret_cast<const u32x4 *>(xb + (tb * 32 + r32) * kStride + k_off);
+        const u32x4 bv = *reinterpret_cast<const u32x4 *>(xb + tb * 32 * kTileK + b_off(s));
 #pragma unroll
         for (int b = 0; b < RB; ++b) acc[tb][b] = mfma<F16>(a[b][s], bv, acc[tb][b]);
       }
     }
   };
-
-  // Whole ring turns, then at most LA tail steps (each step issues the same loads, clamped).
+  // Step j reads buffer j & 1 while the direct loads fill the other one (last read in step j-1,
+  // which ended with a barrier) with step j+1's activations. The K loop runs two steps per turn,
+  // so that which buffer a step reads is known at compile time.
   auto run_steps = [&](auto &&step) {
     int j0 = 0;
-    for (; j0 + R <= w.nc; j0 += R) {
-#pragma unroll
-      for (int u = 0; u < R; ++u) step(j0 + u, u);
+    for (; j0 + 2 <= w.nc; j0 += 2) {
+      step(j0, xs0, xs1);
+      step(j0 + 1, xs1, xs0);
     }
+    if (j0 < w.nc) step(j0, xs0, xs1);
+  };
+  // Shift the held weight tiles by one step; `fresh` is the tile loaded this step.
+  auto shift_ring = [&](const uint4 (&fresh)[RB][2]) {
 #pragma unroll
-    for (int u = 0; u < LA; ++u)
-      if (j0 + u < w.nc) step(j0 + u, u);
+    for (int u = 0; u + 1 < NS; ++u)
+#pragma unroll
+      for (int b = 0; b < RB; ++b) {
+        ring[u][b][0] = ring[u + 1][b][0];
+        ring[u][b][1] = ring[u + 1][b][1];
+      }
+#pragma unroll
+    for (int b = 0; b < RB; ++b) {
+      ring[NS - 1][b][0] = fresh[b][0];
+      ring[NS - 1][b][1] = fresh[b][1];
+    }
   };
 
   if constexpr (PIPE) {
     // Software-pipelined: step j multiplies the tiles decoded during step j-1 while decoding tile
-    // j+1 (already in the ring; requested a step earlier, LA >= 2). The step is woven: each of
-    // its eight MFMA groups (one per K set s) carries the decode of one block of tile j+1 and the
-    // activation reads of the next group, in a scheduling region of its own (the decoded block is
-    // pinned to it), so the matrix core and the VALU work side by side instead of in turn.
+    // j+1 (held since step j-1, LA >= 2). The step is woven: each of its eight MFMA groups (one
+    // per K set s) carries the decode of one block of tile j+1 and the activation reads of the
+    // next group, in a scheduling region of its own (the decoded block is pinned to it), so the
+    // matrix core and the VALU work side by side instead of in turn.
     u32x4 acur[RB][8];
-    decode_step(ring[0], acur);
-    run_steps([&](int j, int u) {
-      load_tiles(ring[(u + LA) % R], j + LA);
-      const uint4(&next)[RB][2] = ring[(u + 1) % R];  // tile j+1 (past the end: the clamped last tile)
+    decode_step(first, acur);
+    run_steps([&](int j, const uint16_t *xb, uint16_t *xn) {
+      const bool more = j + 1 < w.nc;
+      if (kStage == 0 && more) stage_x(xn, j + 1);
+      __builtin_amdgcn_sched_barrier(0);
+      uint4 fresh[RB][2];
+      load_tiles(fresh, j + LA);
+      __builtin_amdgcn_sched_barrier(0);
+      if ((kStage == 1 || (kStage == 2 && LUT)) && more) stage_x(xn, j + 1);
+      const uint4(&next)[RB][2] = ring[0];  // tile j+1 (past the end: the clamped last tile)
       u32x4 anext[RB][8];
       if constexpr (LUT) {
         decode_step(next, anext);  // the palette-row gathers of a step stay together
-        mfma_step(j, acur);
+        mfma_step(xb, acur);
       } else {
-        const uint16_t *xb = xs[j & 1];
         auto read_b = [&](int tb, int sg) {
-          return *reinterpret_cast<const u32x4 *>(xb + (tb * 32 + r32) * kStride + 16 * (4 * h + (sg >> 1)) +
-                                                  8 * (sg & 1));
+          return *reinterpret_cast<const u32x4 *>(xb + tb * 32 * kTileK + b_off(sg));
         };
         constexpr int kBlocks = 4 * RB;                  // blocks per lane and step
         constexpr int kRegions = kBlocks < NR ? kBlocks : NR;  // regions per step
@@ -286,6 +336,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillParams p) {
         }
 #pragma unroll
         for (int rg = 0; rg < kRegions; ++rg) {
+          if (kStage == 2 && more) stage_part(xn, j + 1, rg * XC / kRegions, (rg + 1) * XC / kRegions);
           u32x4 bnext[kGroups][TB];
           if (rg + 1 < kRegions) {
 #pragma unroll
@@ -335,23 +386,27 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillParams p) {
           }
         }
       }
-      store_x((j + 1) & 1);  // the next step's activations, into the buffer read two steps ago
-      load_x(j + 2);
-      __syncthreads();
+      step_barrier();
 #pragma unroll
       for (int b = 0; b < RB; ++b)
 #pragma unroll
         for (int s = 0; s < 8; ++s) acur[b][s] = anext[b][s];
+      shift_ring(fresh);
     });
   } else {
-    run_steps([&](int j, int u) {
-      load_tiles(ring[(u + LA) % R], j + LA);
+    run_steps([&](int j, const uint16_t *xb, uint16_t *xn) {
+      const bool more = j + 1 < w.nc;
+      if (kStage == 0 && more) stage_x(xn, j + 1);
+      __builtin_amdgcn_sched_barrier(0);
+      uint4 fresh[RB][2];
+      load_tiles(fresh, j + LA);
+      __builtin_amdgcn_sched_barrier(0);
+      if (kStage != 0 && more) stage_x(xn, j + 1);
       u32x4 a[RB][8];
-      decode_step(ring[u], a);
-      mfma_step(j, a);
-      store_x((j + 1) & 1);  // the next step's activations, into the buffer read two steps ago
-      load_x(j + 2);
-      __syncthreads();
+      decode_step(ring[0], a);
+      mfma_step(xb, a);
+      step_barrier();
+      shift_ring(fresh);
     });
   }
 
@@ -435,7 +490,7 @@ hipError_t launch_tile(const PrefillParams &p, hipStream_t stream) {
 #define TX_CANDIDATE(NAME, TB, RB, LA, PIPE)                                                            \
   Candidate {                                                                                          \
     NAME, 32 * (TB), 128 * (RB), reinterpret_cast<const void *>(&prefill_kernel<false, TB, RB, LA, PIPE, false>), \
-        &launch_tile<TB, RB, LA, PIPE>, 2 * 32 * (TB) * kStride * 2                                    \
+        &launch_tile<TB, RB, LA, PIPE>, 2 * 32 * (TB) * kTileK * 2                                    \
   }
 
 // The two 128-token tiles pipeline their K loop; the smaller tiles run it plainly.
