@@ -39,18 +39,22 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kXcds = 8;
 
-// Weight tiles in flight per wave, in K steps.
+// Weight tiles in flight per wave, in K steps: the pipelined 128-token tiles, the plain tiles.
 #ifndef TX_PREFILL_LA
-#define TX_PREFILL_LA 2
+#define TX_PREFILL_LA 3
 #endif
-// Scheduling regions per K step of the woven loop (each holds 8/NR MFMA groups and its share of
-// the next tile's block decodes).
-// When a step issues the direct loads of the next step's activations: 0 before its weight
-// loads, 1 after them, 2 spread over the woven regions (pipelined tiles; the others as 1).
+#ifndef TX_PREFILL_LA_PLAIN
+#define TX_PREFILL_LA_PLAIN 2
+#endif
+// When a pipelined step issues the direct loads of the next step's activations: 0 before its
+// weight loads, 1 after them, 2 spread over the woven regions. Plain steps issue them after
+// their weight loads.
 #ifndef TX_PREFILL_STAGE
 #define TX_PREFILL_STAGE 2
 #endif
 constexpr int kStage = TX_PREFILL_STAGE;
+// Scheduling regions per K step of the woven loop (each holds 8/NR MFMA groups and its share of
+// the next tile's block decodes).
 #ifndef TX_PREFILL_REGIONS
 #define TX_PREFILL_REGIONS 8
 #endif
@@ -197,13 +201,13 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillParams p) {
   // Element offset of this lane's B operand of MFMA s in token block 0 of a staged tile.
   const int sw = r32 & 15;
   auto b_off = [&](int s) { return r32 * kTileK + 8 * ((k_offset(s) >> 3) ^ sw); };
-  // End of a step: this wave's staged chunks have landed (at most the 2*RB weight loads issued
-  // after them are outstanding, and loads complete in order), its LDS stores are done, then the
-  // workgroup barrier. A fence would also wait for the weight loads, which are meant to stay in
-  // flight across the barrier; the memory clobber keeps the compiler from moving LDS accesses
-  // across it.
+  // End of a step: this wave's direct loads have landed (with kStage 0 on a pipelined tile at most
+  // the 2*RB weight loads issued after them are outstanding, and loads complete in order), its
+  // LDS stores are done, then the workgroup barrier. A fence would also wait for weight loads
+  // that may stay in flight across the barrier; the memory clobber keeps the compiler from moving
+  // LDS accesses across it.
   auto step_barrier = [&]() {
-    asm volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::"n"(kStage == 0 ? 2 * RB : 0) : "memory");
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::"n"(PIPE && kStage == 0 ? 2 * RB : 0) : "memory");
   };
 
   // Prologue: step 0's activations, the palette tables, the first weight tiles.
@@ -395,13 +399,10 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillParams p) {
     });
   } else {
     run_steps([&](int j, const uint16_t *xb, uint16_t *xn) {
-      const bool more = j + 1 < w.nc;
-      if (kStage == 0 && more) stage_x(xn, j + 1);
-      __builtin_amdgcn_sched_barrier(0);
       uint4 fresh[RB][2];
       load_tiles(fresh, j + LA);
       __builtin_amdgcn_sched_barrier(0);
-      if (kStage != 0 && more) stage_x(xn, j + 1);
+      if (j + 1 < w.nc) stage_x(xn, j + 1);
       u32x4 a[RB][8];
       decode_step(ring[0], a);
       mfma_step(xb, a);
@@ -497,9 +498,9 @@ hipError_t launch_tile(const PrefillParams &p, hipStream_t stream) {
 const Candidate kCandidates[] = {
     TX_CANDIDATE("large_128x256x128", 4, 2, TX_PREFILL_LA, true),
     TX_CANDIDATE("medium_128x128x128", 4, 1, TX_PREFILL_LA, true),
-    TX_CANDIDATE("medium_64x256x128", 2, 2, TX_PREFILL_LA, false),
-    TX_CANDIDATE("medium_64x128x128", 2, 1, TX_PREFILL_LA, false),
-    TX_CANDIDATE("small_32x128x128", 1, 1, TX_PREFILL_LA, false),
+    TX_CANDIDATE("medium_64x256x128", 2, 2, TX_PREFILL_LA_PLAIN, false),
+    TX_CANDIDATE("medium_64x128x128", 2, 1, TX_PREFILL_LA_PLAIN, false),
+    TX_CANDIDATE("small_32x128x128", 1, 1, TX_PREFILL_LA_PLAIN, false),
 };
 
 const Candidate *find(int candidate) {
