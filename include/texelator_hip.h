@@ -150,7 +150,8 @@ int tx_rope_kv_cache(const void *qkv, int64_t row_stride, int64_t tokens, const 
                      const float *cos_table, const float *sin_table, int heads, int kv_heads, int head_dim,
                      void *q_out, void *k_cache, void *v_cache, int64_t max_context, void *stream);
 
-/* Workspace bytes of tx_decode_attention for `length` cached positions. */
+/* Workspace bytes of tx_decode_attention and tx_decode_attention_split for `length` cached
+ * positions (the chunk partials). */
 int tx_decode_attention_workspace(int heads, int64_t length, int64_t *bytes);
 
 /* Attention of one query token q [heads][head_dim] over cached keys 0..*position (device int64;
@@ -159,6 +160,16 @@ int tx_decode_attention_workspace(int heads, int64_t length, int64_t *bytes);
 int tx_decode_attention(const void *q, const void *k_cache, const void *v_cache, const int64_t *position,
                         int64_t length, int heads, int kv_heads, int head_dim, int64_t max_context, float scale,
                         void *workspace, int64_t workspace_bytes, void *out, void *stream);
+
+/* tx_rope_kv_cache_split followed by tx_decode_attention, one kernel launch fewer: q and the new
+ * token's key and value are the last tx_linear_split of qkv_handle ([q | k | v] rows), rotated
+ * with the RoPE tables inside the attention kernel; the key and value are written to the caches
+ * at *position. Bit-identical to the two calls. No counterpart in the reference (its decoder layers are Hugging Face modules,
+ * docs/supported-models.md:3-5). */
+int tx_decode_attention_split(uint64_t qkv_handle, const int64_t *position, const float *cos_table,
+                              const float *sin_table, int64_t length, int heads, int kv_heads, int head_dim,
+                              void *k_cache, void *v_cache, int64_t max_context, float scale, void *workspace,
+                              int64_t workspace_bytes, void *out, void *stream);
 
 /* out[r][c] = bf16(silu(g) * u) for gate_up rows [g (intermediate) | u (intermediate)], fp32 math. */
 int tx_swiglu(const void *gate_up, int64_t rows, int64_t intermediate, void *out, void *stream);

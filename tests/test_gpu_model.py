@@ -170,16 +170,22 @@ def test_rope_kv_cache_kernel(ext, tiny):
     assert torch.equal(vc[:, positions].transpose(0, 1), qkv[:, qs + ks:].reshape(t, c.kv_heads, c.head_dim))
 
 
-@pytest.mark.parametrize("position,length", [(0, 512), (100, 512), (511, 512), (700, 1024), (1023, 1024)])
-def test_decode_attention_kernel(ext, position, length):
-    heads, kv, d, ctx = 40, 8, 128, 1024
+@pytest.mark.parametrize("position,length,ctx", [(0, 512, 1024), (100, 512, 1024), (511, 512, 1024), (700, 1024, 1024),
+                                                 (1023, 1024, 1024), (33000, 33024, 33024)])
+def test_decode_attention_kernel(ext, position, length, ctx):
+    """Against an fp32 reference, up to 516 chunks; a second call on the same workspace repeats
+    the output."""
+    heads, kv, d = 40, 8, 128
     g = torch.Generator(device="cuda").manual_seed(position)
     kc = torch.randn(kv, ctx, d, device="cuda", generator=g).to(torch.bfloat16)
     vc = torch.randn(kv, ctx, d, device="cuda", generator=g).to(torch.bfloat16)
     q = (torch.randn(heads * d, device="cuda", generator=g) * 0.3).to(torch.bfloat16)
     pos = torch.tensor([position], device="cuda")
     ws = torch.empty(layers.decode_attention_workspace_bytes(heads, length), dtype=torch.uint8, device="cuda")
-    got = layers.decode_attention(q, kc, vc, pos, length, heads, kv, 1 / math.sqrt(d), ws).float()
+    first = layers.decode_attention(q, kc, vc, pos, length, heads, kv, 1 / math.sqrt(d), ws).clone()
+    got = layers.decode_attention(q, kc, vc, pos, length, heads, kv, 1 / math.sqrt(d), ws)
+    assert torch.equal(first, got)
+    got = got.float()
     qf = q.float().view(kv, heads // kv, d)
     keys, values = kc[:, :position + 1].float(), vc[:, :position + 1].float()
     scores = torch.einsum("kgd,ksd->kgs", qf, keys) / math.sqrt(d)
@@ -240,6 +246,37 @@ def test_rope_kv_cache_split_is_bit_identical(ext, heads, kv, k, bias):
                                          torch.empty(heads * d, device="cuda", dtype=torch.bfloat16))
         assert torch.equal(want.view(-1), got)
         assert torch.equal(caches[0], caches[2]) and torch.equal(caches[1], caches[3])
+    finally:
+        ext.free(handle)
+
+
+@pytest.mark.parametrize("heads,kv,k,bias,position,length", [(40, 8, 5120, True, 517, 1024), (40, 8, 5120, False, 0, 512),
+                                                             (4, 2, 256, False, 63, 512), (4, 2, 256, True, 64, 1024)])
+def test_decode_attention_split_is_bit_identical(ext, heads, kv, k, bias, position, length):
+    """RoPE + KV write inside the attention kernel == rope_kv_cache_split + decode_attention, bit
+    for bit: output and both caches; repeated on the same workspace."""
+    d, ctx = 128, 1024
+    handle = _random_handle(ext, (heads + 2 * kv) * d, k, seed=heads + position, bias=bias)
+    try:
+        g = torch.Generator(device="cuda").manual_seed(position + 5)
+        x = torch.randn(1, k, device="cuda", generator=g).to(torch.bfloat16)
+        angles = torch.rand(ctx, d, device="cuda", generator=g) * 6
+        cos, sin = angles.cos().contiguous(), angles.sin().contiguous()
+        pos = torch.tensor([position], device="cuda")
+        kc = torch.randn(kv, ctx, d, device="cuda", generator=g).to(torch.bfloat16)
+        vc = torch.randn(kv, ctx, d, device="cuda", generator=g).to(torch.bfloat16)
+        caches = [kc.clone(), vc.clone(), kc.clone(), vc.clone()]
+        ws = torch.empty(layers.decode_attention_workspace_bytes(heads, length), dtype=torch.uint8, device="cuda")
+        scale = 1 / math.sqrt(d)
+        layers.linear_split(handle, x)
+        q = layers.rope_kv_cache_split(handle, pos, cos, sin, heads, kv, d, caches[0], caches[1],
+                                       torch.empty(heads * d, device="cuda", dtype=torch.bfloat16))
+        want = layers.decode_attention(q, caches[0], caches[1], pos, length, heads, kv, scale, ws).clone()
+        for _ in range(2):
+            got = layers.decode_attention_split(handle, pos, cos, sin, heads, kv, d, caches[2], caches[3], length,
+                                                scale, ws)
+            assert torch.equal(want, got)
+            assert torch.equal(caches[0], caches[2]) and torch.equal(caches[1], caches[3])
     finally:
         ext.free(handle)
 

@@ -571,7 +571,7 @@ int tx_rope_kv_cache(const void *qkv, int64_t row_stride, int64_t tokens, const 
 int tx_decode_attention_workspace(int heads, int64_t length, int64_t *bytes) {
   g_last_error.clear();
   if (!bytes || heads <= 0 || length <= 0) return fail(TX_ERR_INVALID, "decode_attention_workspace: invalid arguments");
-  *bytes = (int64_t)tx::decode_attention_chunks(length) * heads * (128 + 2) * (int64_t)sizeof(float);
+  *bytes = tx::decode_attention_workspace(heads, length);
   return TX_OK;
 }
 
@@ -592,6 +592,33 @@ int tx_decode_attention(const void *q, const void *k_cache, const void *v_cache,
                                      static_cast<const uint16_t *>(v_cache), position, length, heads, kv_heads,
                                      max_context, scale, static_cast<float *>(workspace), static_cast<uint16_t *>(out),
                                      reinterpret_cast<hipStream_t>(stream)));
+  return TX_OK;
+}
+
+int tx_decode_attention_split(uint64_t qkv_handle, const int64_t *position, const float *cos_table,
+                              const float *sin_table, int64_t length, int heads, int kv_heads, int head_dim,
+                              void *k_cache, void *v_cache, int64_t max_context, float scale, void *workspace,
+                              int64_t workspace_bytes, void *out, void *stream) {
+  g_last_error.clear();
+  Handle *h = as_handle(qkv_handle);
+  if (!h) return fail(TX_ERR_INVALID, "null Texelator handle");
+  if (!position || !cos_table || !sin_table || !k_cache || !v_cache || !out || !workspace)
+    return fail(TX_ERR_INVALID, "decode_attention_split: null pointer");
+  if (!tx::decode_attention_supported(heads, kv_heads, head_dim))
+    return fail(TX_ERR_UNSUPPORTED, "decode_attention_split: needs head_dim 128 and at most 8 query heads per KV head");
+  if ((int64_t)h->M < (int64_t)(heads + 2 * kv_heads) * head_dim)
+    return fail(TX_ERR_INVALID, "decode_attention_split: qkv handle too narrow for the heads");
+  if (h->bias && h->bias_dtype != TX_DTYPE_BF16) return fail(TX_ERR_INVALID, "decode_attention_split: the bias must be BF16");
+  if (length <= 0 || length > max_context || length > tx::decode_attention_max_length())
+    return fail(TX_ERR_INVALID, "decode_attention_split: length outside the cache or above 65536");
+  int64_t need = 0;
+  tx_decode_attention_workspace(heads, length, &need);
+  if (workspace_bytes < need) return fail(TX_ERR_INVALID, "decode_attention_split: workspace too small");
+  DeviceGuard guard(h->device);
+  TX_HIP(tx::launch_decode_attention_split(split_source(h), position, cos_table, sin_table, length, heads, kv_heads,
+                                           static_cast<uint16_t *>(k_cache), static_cast<uint16_t *>(v_cache),
+                                           max_context, scale, static_cast<float *>(workspace),
+                                           static_cast<uint16_t *>(out), reinterpret_cast<hipStream_t>(stream)));
   return TX_OK;
 }
 

@@ -37,16 +37,21 @@ __global__ __launch_bounds__(kNormThreads) void add_rmsnorm_kernel(float *h, con
   uint2 *orow = reinterpret_cast<uint2 *>(out + (size_t)blockIdx.x * hidden);
   const uint2 *wr = reinterpret_cast<const uint2 *>(weight);
   const int groups = hidden / 4;
+  // One pass covers every group (hidden <= 8192): the values stay in registers for the output,
+  // and the norm weight is loaded with them.
+  const bool one_pass = groups <= kThreads * kUnroll;
+  float4 v[kUnroll];
+  uint2 wv[kUnroll];
   float ss = 0.f;
   for (int base = 0; base < groups; base += kThreads * kUnroll) {
     // load phase: every load of this pass in flight at once (indices clamped, then masked)
-    float4 v[kUnroll];
     uint2 d[kUnroll];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       const int i = min(base + u * kThreads + (int)threadIdx.x, groups - 1);
       v[u] = hr[i];
       if (!SPLIT && dr) d[u] = dr[i];
+      if (one_pass) wv[u] = wr[i];
     }
     if constexpr (SPLIT) {
       const float4 *pp = reinterpret_cast<const float4 *>(split.partials + (size_t)blockIdx.x * split.Mp);
@@ -99,14 +104,21 @@ __global__ __launch_bounds__(kNormThreads) void add_rmsnorm_kernel(float *h, con
 #pragma unroll
   for (int w = 0; w < kThreads / 64; ++w) total += partial[w];
   const float inv = rsqrtf(total / (float)hidden + eps);
-  for (int i = threadIdx.x; i < groups; i += kThreads) {
-    const float4 v = hr[i];
-    const uint2 w = wr[i];
-    const float n0 = bf(to_bf(v.x * inv)), n1 = bf(to_bf(v.y * inv)), n2 = bf(to_bf(v.z * inv)), n3 = bf(to_bf(v.w * inv));
+  auto normalize = [&](const float4 &h4, const uint2 &w) {
+    const float n0 = bf(to_bf(h4.x * inv)), n1 = bf(to_bf(h4.y * inv)), n2 = bf(to_bf(h4.z * inv)), n3 = bf(to_bf(h4.w * inv));
     const uint32_t lo = (uint32_t)to_bf(bf((uint16_t)(w.x & 0xFFFFu)) * n0) | ((uint32_t)to_bf(bf((uint16_t)(w.x >> 16)) * n1) << 16);
     const uint32_t hi = (uint32_t)to_bf(bf((uint16_t)(w.y & 0xFFFFu)) * n2) | ((uint32_t)to_bf(bf((uint16_t)(w.y >> 16)) * n3) << 16);
-    orow[i] = make_uint2(lo, hi);
+    return make_uint2(lo, hi);
+  };
+  if (one_pass) {
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int i = u * kThreads + (int)threadIdx.x;
+      if (i < groups) orow[i] = normalize(v[u], wv[u]);
+    }
+    return;
   }
+  for (int i = threadIdx.x; i < groups; i += kThreads) orow[i] = normalize(hr[i], wr[i]);
 }
 
 // One block per (token, head); thread j rotates the pair (j, j + d/2) of rotate-half RoPE.
@@ -154,10 +166,24 @@ constexpr int kKeyStrideU4 = kRowU4 + 1;
 // values (those <= position) into LDS in one burst, scores the group's query heads against them
 // in fp32, and writes the chunk's max m, sum of exp l and unnormalised output o to
 // partials[kv][chunk][g][130].
-__global__ __launch_bounds__(256) void decode_attention_kernel(const uint16_t *q, const uint16_t *k_cache,
-                                                               const uint16_t *v_cache, const int64_t *position,
-                                                               int group, int64_t max_ctx, float scale,
-                                                               int chunks, float *partials) {
+// ROPE: q and the new token's key and value come from the qkv decode GEMV's split-K partials
+// (summed, rounded and rotated exactly as rope_cache_kernel<true> does); the block whose chunk
+// holds the position writes the key and value into the caches and into its own tiles.
+// (Merging the chunks in the same launch -- each block publishing its partials behind a device
+// fence and the last one to take a ticket merging -- measured slower on MI355X: every such fence
+// writes back the XCD's L2, 64 times per XCD and layer at 4096 positions.)
+
+struct AttnInput {
+  const uint16_t *q;  // bf16 [heads][128] (without ROPE)
+  SplitSource split;  // [q | k | v] split-K partials (with ROPE)
+  const float *cos_t, *sin_t;
+  int heads, kv_heads;
+};
+
+template <bool ROPE>
+__global__ __launch_bounds__(256) void decode_attention_kernel(AttnInput in, uint16_t *k_cache, uint16_t *v_cache,
+                                                               const int64_t *position, int group, int64_t max_ctx,
+                                                               float scale, int chunks, float *partials) {
   __shared__ uint4 ks[kChunk * kKeyStrideU4];
   __shared__ uint4 vs[kChunk * kRowU4];
   __shared__ float qs[kMaxGroup][kHeadDim];
@@ -180,123 +206,171 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(const uint16_t *q
     kr[u] = kg[row * kRowU4 + idx % kRowU4];
     vr[u] = vg[row * kRowU4 + idx % kRowU4];
   }
-  float qv[kMaxGroup * kHeadDim / 256];
+  constexpr int kHalf = kHeadDim / 2;
+  // Without ROPE: q element u * 256 + tid of the group. With ROPE: the rotate-half pair
+  // (j, j + 64) of head g for p = u * 256 + tid = 64 g + j, as the unrotated sums x1, x2.
+  float qv[kMaxGroup * kHeadDim / 256], qw[kMaxGroup * kHeadDim / 256];
 #pragma unroll
   for (int u = 0; u < kMaxGroup * kHeadDim / 256; ++u) {
     const int i = u * 256 + tid;
-    qv[u] = i < group * kHeadDim ? bf(q[(size_t)kv * group * kHeadDim + i]) : 0.f;
+    if constexpr (ROPE) {
+      const int g = i / kHalf, j = i % kHalf;
+      const int64_t col = (int64_t)(kv * group + g) * kHeadDim + j;
+      qv[u] = i < group * kHalf ? split_value(in.split, 0, col) : 0.f;
+      qw[u] = i < group * kHalf ? split_value(in.split, 0, col + kHalf) : 0.f;
+    } else {
+      qv[u] = i < group * kHeadDim ? bf(in.q[(size_t)kv * group * kHeadDim + i]) : 0.f;
+    }
   }
   const int64_t pos = *position;
-  if (j0 > pos) {
-    for (int i = tid; i < group * (kHeadDim + 2); i += 256) out[i] = (i % (kHeadDim + 2)) == kHeadDim ? -INFINITY : 0.f;
-    return;
-  }
-  const int count = (int)min((int64_t)kChunk, pos - j0 + 1);  // valid keys in this chunk
+  const bool active = j0 <= pos;
+  if (active) {
+    const int count = (int)min((int64_t)kChunk, pos - j0 + 1);  // valid keys in this chunk
 #pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const int idx = u * 256 + tid;
-    ks[(idx / kRowU4) * kKeyStrideU4 + idx % kRowU4] = kr[u];
-    vs[idx] = idx / kRowU4 < count ? vr[u] : make_uint4(0, 0, 0, 0);  // rows past the position: zero
-  }
+    for (int u = 0; u < 4; ++u) {
+      const int idx = u * 256 + tid;
+      ks[(idx / kRowU4) * kKeyStrideU4 + idx % kRowU4] = kr[u];
+      vs[idx] = idx / kRowU4 < count ? vr[u] : make_uint4(0, 0, 0, 0);  // rows past the position: zero
+    }
 #pragma unroll
-  for (int u = 0; u < kMaxGroup * kHeadDim / 256; ++u) {
-    const int i = u * 256 + tid;
-    if (i < group * kHeadDim) qs[i / kHeadDim][i % kHeadDim] = qv[u];
-  }
-  __syncthreads();
-
-  // scores: four threads per key, 32 dimensions each
-  {
-    const int jl = tid >> 2;
-    const int part = tid & 3;
-    float kf[32];
-    const uint4 *row = ks + jl * kKeyStrideU4 + part * 4;
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const uint4 w = row[v];
-      const uint32_t words[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        kf[v * 8 + 2 * e] = bf((uint16_t)(words[e] & 0xFFFFu));
-        kf[v * 8 + 2 * e + 1] = bf((uint16_t)(words[e] >> 16));
+    for (int u = 0; u < kMaxGroup * kHeadDim / 256; ++u) {
+      const int i = u * 256 + tid;
+      if constexpr (ROPE) {
+        if (i < group * kHalf) {
+          const int g = i / kHalf, j = i % kHalf;
+          const float x1 = qv[u], x2 = qw[u];
+          const float c1 = in.cos_t[pos * kHeadDim + j], c2 = in.cos_t[pos * kHeadDim + j + kHalf];
+          const float s1 = in.sin_t[pos * kHeadDim + j], s2 = in.sin_t[pos * kHeadDim + j + kHalf];
+          qs[g][j] = bf(to_bf(x1 * c1 - x2 * s1));
+          qs[g][j + kHalf] = bf(to_bf(x2 * c2 + x1 * s2));
+        }
+      } else {
+        if (i < group * kHeadDim) qs[i / kHeadDim][i % kHeadDim] = qv[u];
       }
     }
-    for (int g = 0; g < group; ++g) {
-      const float4 *q4 = reinterpret_cast<const float4 *>(&qs[g][part * 32]);
-      float s = 0.f;
-#pragma unroll
-      for (int e4 = 0; e4 < 8; ++e4) {
-        const float4 qq = q4[e4];
-        s = __builtin_fmaf(qq.x, kf[4 * e4], s);
-        s = __builtin_fmaf(qq.y, kf[4 * e4 + 1], s);
-        s = __builtin_fmaf(qq.z, kf[4 * e4 + 2], s);
-        s = __builtin_fmaf(qq.w, kf[4 * e4 + 3], s);
+    __syncthreads();
+    if (ROPE && pos - j0 < kChunk) {
+      // This chunk holds the new token: rotate its key, take its value, write both to the caches
+      // and over the (not yet written) row of the tiles.
+      const int r = (int)(pos - j0);
+      uint16_t *krow = reinterpret_cast<uint16_t *>(ks + r * kKeyStrideU4);
+      uint16_t *vrow = reinterpret_cast<uint16_t *>(vs + r * kRowU4);
+      if (tid < kHalf) {
+        const int64_t col = (int64_t)(in.heads + kv) * kHeadDim + tid;
+        const float x1 = split_value(in.split, 0, col), x2 = split_value(in.split, 0, col + kHalf);
+        const float c1 = in.cos_t[pos * kHeadDim + tid], c2 = in.cos_t[pos * kHeadDim + tid + kHalf];
+        const float s1 = in.sin_t[pos * kHeadDim + tid], s2 = in.sin_t[pos * kHeadDim + tid + kHalf];
+        const uint16_t o1 = to_bf(x1 * c1 - x2 * s1), o2 = to_bf(x2 * c2 + x1 * s2);
+        uint16_t *dst = k_cache + ((size_t)kv * max_ctx + pos) * kHeadDim;
+        dst[tid] = o1;
+        dst[tid + kHalf] = o2;
+        krow[tid] = o1;
+        krow[tid + kHalf] = o2;
+      } else if (tid < kHalf + kHeadDim) {
+        const int e = tid - kHalf;
+        const uint16_t v = to_bf(split_value(in.split, 0, (int64_t)(in.heads + in.kv_heads + kv) * kHeadDim + e));
+        v_cache[((size_t)kv * max_ctx + pos) * kHeadDim + e] = v;
+        vrow[e] = v;
       }
-      s += __shfl_xor(s, 1);
-      s += __shfl_xor(s, 2);
-      if (part == 0) probs[g][jl] = jl < count ? s * scale : -INFINITY;
+      __syncthreads();
     }
-  }
-  __syncthreads();
 
-  // per query head: max, exp, sum (one wave per head, one lane per key)
-  {
-    const int wave = tid >> 6, lane = tid & 63;
-    for (int g = wave; g < group; g += 4) {
-      const float a = probs[g][lane];
-      float m = a;
+    // scores: four threads per key, 32 dimensions each
+    {
+      const int jl = tid >> 2;
+      const int part = tid & 3;
+      float kf[32];
+      const uint4 *row = ks + jl * kKeyStrideU4 + part * 4;
 #pragma unroll
-      for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
-      const float pa = expf(a - m);
-      probs[g][lane] = pa;
-      float l = pa;
+      for (int v = 0; v < 4; ++v) {
+        const uint4 w = row[v];
+        const uint32_t words[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
-      for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o);
-      if (lane == 0) {
-        stats[g][0] = m;
-        stats[g][1] = l;
+        for (int e = 0; e < 4; ++e) {
+          kf[v * 8 + 2 * e] = bf((uint16_t)(words[e] & 0xFFFFu));
+          kf[v * 8 + 2 * e + 1] = bf((uint16_t)(words[e] >> 16));
+        }
+      }
+      for (int g = 0; g < group; ++g) {
+        const float4 *q4 = reinterpret_cast<const float4 *>(&qs[g][part * 32]);
+        float s = 0.f;
+#pragma unroll
+        for (int e4 = 0; e4 < 8; ++e4) {
+          const float4 qq = q4[e4];
+          s = __builtin_fmaf(qq.x, kf[4 * e4], s);
+          s = __builtin_fmaf(qq.y, kf[4 * e4 + 1], s);
+          s = __builtin_fmaf(qq.z, kf[4 * e4 + 2], s);
+          s = __builtin_fmaf(qq.w, kf[4 * e4 + 3], s);
+        }
+        s += __shfl_xor(s, 1);
+        s += __shfl_xor(s, 2);
+        if (part == 0) probs[g][jl] = jl < count ? s * scale : -INFINITY;
       }
     }
-  }
-  __syncthreads();
+    __syncthreads();
 
-  // o[g][dd] = sum_j p[g][j] v[j][dd]; thread (dd, half of the heads), values from LDS
-  {
-    const int dd = tid & (kHeadDim - 1);
-    const int gg = tid >> 7;
-    float acc[kMaxGroup / 2];
+    // per query head: max, exp, sum (one wave per head, one lane per key)
+    {
+      const int wave = tid >> 6, lane = tid & 63;
+      for (int g = wave; g < group; g += 4) {
+        const float a = probs[g][lane];
+        float m = a;
 #pragma unroll
-    for (int u = 0; u < kMaxGroup / 2; ++u) acc[u] = 0.f;
-    const uint16_t *vcol = reinterpret_cast<const uint16_t *>(vs) + dd;
-    // four keys per pass (probabilities read as float4); keys past the position have p = 0 and
-    // zeroed values, so the padded tail adds exact zeros
-    for (int j = 0; j < count; j += 4) {
-      const float v0 = bf(vcol[j * kHeadDim]), v1 = bf(vcol[(j + 1) * kHeadDim]);
-      const float v2 = bf(vcol[(j + 2) * kHeadDim]), v3 = bf(vcol[(j + 3) * kHeadDim]);
+        for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+        const float pa = expf(a - m);
+        probs[g][lane] = pa;
+        float l = pa;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o);
+        if (lane == 0) {
+          stats[g][0] = m;
+          stats[g][1] = l;
+        }
+      }
+    }
+    __syncthreads();
+
+    // o[g][dd] = sum_j p[g][j] v[j][dd]; thread (dd, half of the heads), values from LDS
+    {
+      const int dd = tid & (kHeadDim - 1);
+      const int gg = tid >> 7;
+      float acc[kMaxGroup / 2];
+#pragma unroll
+      for (int u = 0; u < kMaxGroup / 2; ++u) acc[u] = 0.f;
+      const uint16_t *vcol = reinterpret_cast<const uint16_t *>(vs) + dd;
+      // four keys per pass (probabilities read as float4); keys past the position have p = 0 and
+      // zeroed values, so the padded tail adds exact zeros
+      for (int j = 0; j < count; j += 4) {
+        const float v0 = bf(vcol[j * kHeadDim]), v1 = bf(vcol[(j + 1) * kHeadDim]);
+        const float v2 = bf(vcol[(j + 2) * kHeadDim]), v3 = bf(vcol[(j + 3) * kHeadDim]);
+#pragma unroll
+        for (int u = 0; u < kMaxGroup / 2; ++u) {
+          const int g = gg + 2 * u;
+          if (g < group) {
+            const float4 p4 = *reinterpret_cast<const float4 *>(&probs[g][j]);
+            acc[u] = __builtin_fmaf(p4.x, v0, acc[u]);
+            acc[u] = __builtin_fmaf(p4.y, v1, acc[u]);
+            acc[u] = __builtin_fmaf(p4.z, v2, acc[u]);
+            acc[u] = __builtin_fmaf(p4.w, v3, acc[u]);
+          }
+        }
+      }
 #pragma unroll
       for (int u = 0; u < kMaxGroup / 2; ++u) {
         const int g = gg + 2 * u;
         if (g < group) {
-          const float4 p4 = *reinterpret_cast<const float4 *>(&probs[g][j]);
-          acc[u] = __builtin_fmaf(p4.x, v0, acc[u]);
-          acc[u] = __builtin_fmaf(p4.y, v1, acc[u]);
-          acc[u] = __builtin_fmaf(p4.z, v2, acc[u]);
-          acc[u] = __builtin_fmaf(p4.w, v3, acc[u]);
+          float *o = out + (size_t)g * (kHeadDim + 2);
+          o[dd] = acc[u];
+          if (dd == 0) {
+            o[kHeadDim] = stats[g][0];
+            o[kHeadDim + 1] = stats[g][1];
+          }
         }
       }
     }
-#pragma unroll
-    for (int u = 0; u < kMaxGroup / 2; ++u) {
-      const int g = gg + 2 * u;
-      if (g < group) {
-        float *o = out + (size_t)g * (kHeadDim + 2);
-        o[dd] = acc[u];
-        if (dd == 0) {
-          o[kHeadDim] = stats[g][0];
-          o[kHeadDim + 1] = stats[g][1];
-        }
-      }
-    }
+  } else {
+    // chunk past the position: an empty partial for the merge kernel
+    for (int i = tid; i < group * (kHeadDim + 2); i += 256) out[i] = (i % (kHeadDim + 2)) == kHeadDim ? -INFINITY : 0.f;
   }
 }
 
@@ -397,17 +471,48 @@ bool decode_attention_supported(int heads, int kv_heads, int head_dim) {
 
 int64_t decode_attention_max_length() { return (int64_t)kMaxChunks * kChunk; }
 
+int64_t decode_attention_workspace(int heads, int64_t length) {
+  return (int64_t)decode_attention_chunks(length) * heads * (kHeadDim + 2) * (int64_t)sizeof(float);
+}
+
+namespace {
+template <bool ROPE>
+hipError_t launch_attention(const AttnInput &in, uint16_t *k_cache, uint16_t *v_cache, const int64_t *position,
+                            int64_t length, int64_t max_ctx, float scale, float *partials, uint16_t *out,
+                            hipStream_t stream) {
+  const int chunks = decode_attention_chunks(length);
+  const int group = in.heads / in.kv_heads;
+  hipLaunchKernelGGL((decode_attention_kernel<ROPE>), dim3(in.kv_heads, chunks), dim3(256), 0, stream, in, k_cache,
+                     v_cache, position, group, max_ctx, scale, chunks, partials);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(decode_attention_combine_kernel, dim3(in.heads), dim3(kHeadDim), 0, stream, partials, group, chunks, out);
+  return hipGetLastError();
+}
+}  // namespace
+
 hipError_t launch_decode_attention(const uint16_t *q, const uint16_t *k_cache, const uint16_t *v_cache,
                                    const int64_t *position, int64_t length, int heads, int kv_heads, int64_t max_ctx,
                                    float scale, float *partials, uint16_t *out, hipStream_t stream) {
-  const int chunks = decode_attention_chunks(length);
-  const int group = heads / kv_heads;
-  hipLaunchKernelGGL(decode_attention_kernel, dim3(kv_heads, chunks), dim3(256), 0, stream, q, k_cache, v_cache,
-                     position, group, max_ctx, scale, chunks, partials);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(decode_attention_combine_kernel, dim3(heads), dim3(kHeadDim), 0, stream, partials, group, chunks, out);
-  return hipGetLastError();
+  AttnInput in{};
+  in.q = q;
+  in.heads = heads;
+  in.kv_heads = kv_heads;
+  return launch_attention<false>(in, const_cast<uint16_t *>(k_cache), const_cast<uint16_t *>(v_cache), position, length,
+                                 max_ctx, scale, partials, out, stream);
+}
+
+hipError_t launch_decode_attention_split(const SplitSource &qkv, const int64_t *position, const float *cos_t,
+                                         const float *sin_t, int64_t length, int heads, int kv_heads,
+                                         uint16_t *k_cache, uint16_t *v_cache, int64_t max_ctx, float scale,
+                                         float *partials, uint16_t *out, hipStream_t stream) {
+  AttnInput in{};
+  in.split = qkv;
+  in.cos_t = cos_t;
+  in.sin_t = sin_t;
+  in.heads = heads;
+  in.kv_heads = kv_heads;
+  return launch_attention<true>(in, k_cache, v_cache, position, length, max_ctx, scale, partials, out, stream);
 }
 
 hipError_t launch_swiglu(const uint16_t *gu, int64_t rows, int64_t inter, uint16_t *out, hipStream_t stream) {

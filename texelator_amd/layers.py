@@ -102,6 +102,35 @@ def decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
     return out
 
 
+def decode_attention_split(qkv_handle: int, positions: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+                           heads: int, kv_heads: int, head_dim: int, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                           length: int, scale: float, workspace: torch.Tensor,
+                           out: torch.Tensor | None = None) -> torch.Tensor:
+    """:func:`rope_kv_cache_split` then :func:`decode_attention` with one kernel launch fewer
+    (bit-identical to the two calls): one token whose ``[q | k | v]`` row is the last
+    :func:`linear_split` of ``qkv_handle``; its key and value are written to the caches at
+    ``positions[0]``."""
+    _expect(positions.dtype == torch.int64 and positions.is_contiguous() and positions.numel() == 1,
+            "positions must be int64 [1]")
+    max_ctx = k_cache.shape[1]
+    for cache in (k_cache, v_cache):
+        _expect(cache.dtype == torch.bfloat16 and cache.is_contiguous() and tuple(cache.shape) == (kv_heads, max_ctx, head_dim),
+                "caches must be contiguous bf16 [kv_heads, max_context, head_dim]")
+    for table in (cos, sin):
+        _expect(table.dtype == torch.float32 and table.is_contiguous() and tuple(table.shape) == (max_ctx, head_dim),
+                "rope tables must be float32 [max_context, head_dim]")
+    need = decode_attention_workspace_bytes(heads, length)
+    _expect(workspace.is_cuda and workspace.numel() * workspace.element_size() >= need, "decode attention workspace too small")
+    if out is None:
+        out = torch.empty((1, heads * head_dim), dtype=torch.bfloat16, device=k_cache.device)
+    _expect(out.dtype == torch.bfloat16 and out.is_contiguous() and out.numel() == heads * head_dim, "bad out")
+    check(_lib.load().tx_decode_attention_split(qkv_handle, _ptr(positions), _ptr(cos), _ptr(sin), int(length), heads,
+                                                kv_heads, head_dim, _ptr(k_cache), _ptr(v_cache), max_ctx, float(scale),
+                                                _ptr(workspace), workspace.numel() * workspace.element_size(),
+                                                _ptr(out), _stream(positions)))
+    return out
+
+
 def linear_split(handle: int, x: torch.Tensor) -> None:
     """One-token decode GEMV of ``handle`` (``x`` bf16 ``[K]``) whose output stays as split-K
     partials inside the handle, for :func:`add_rmsnorm_split` or :func:`rope_kv_cache_split`."""

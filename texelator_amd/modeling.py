@@ -121,9 +121,10 @@ class BC4Decoder:
     PyTorch ops (the cross-check path).
 
     With ``split_decode`` (the default; needs ``fused``) a one-token step hands the split-K
-    partials of qkv, o and down straight to their consumer kernels (RoPE, add+RMSNorm), and the
-    gate|up GEMV applies SwiGLU in its epilogue, so a layer is nine kernels instead of thirteen;
-    the results are bit-identical to the unsplit fused path."""
+    partials of qkv, o and down straight to their consumer kernels (the decode attention, which
+    applies RoPE and writes the KV caches itself, and add+RMSNorm), and the gate|up GEMV applies
+    SwiGLU in its epilogue, so a layer is eight kernels instead of thirteen; the results are
+    bit-identical to the unsplit fused path."""
 
     def __init__(self, config: DecoderConfig, max_context: int, device: torch.device | str = "cuda", seed: int = 0,
                  lookahead: int = 1, linear_source=None, depth_scaled: bool = True, embed_std: float = 1.0,
@@ -207,7 +208,7 @@ class BC4Decoder:
             layers.decode_attention_workspace_bytes(c.heads, self.max_context) if fused else 16,
             dtype=torch.uint8, device=self.device)
         # decode-step state (static buffers read and advanced by the captured graphs)
-        self.q_buffer = torch.empty(c.heads * c.head_dim, dtype=bf16, device=self.device)
+        self.attn_buffer = torch.empty(1, c.heads * c.head_dim, dtype=bf16, device=self.device)
         self.act_buffer = torch.empty((1, c.intermediate), dtype=bf16, device=self.device)
         self.token = torch.zeros(1, dtype=torch.long, device=self.device)
         self.position = torch.zeros(1, dtype=torch.long, device=self.device)
@@ -336,15 +337,13 @@ class BC4Decoder:
 
     def _decode_split(self, h: torch.Tensor, x: torch.Tensor, positions: torch.Tensor, length: int,
                       scale: float) -> torch.Tensor:
-        """One token through every layer with the split-K consumers (nine kernels a layer)."""
+        """One token through every layer with the split-K consumers (eight kernels a layer)."""
         c = self.config
         for index, layer in enumerate(self.layers):
             layers.linear_split(layer.handles["qkv"], x)
-            q = layers.rope_kv_cache_split(layer.handles["qkv"], positions, self.rope_cos, self.rope_sin, c.heads,
-                                           c.kv_heads, c.head_dim, self.k_cache[index], self.v_cache[index],
-                                           self.q_buffer)
-            attn = layers.decode_attention(q, self.k_cache[index], self.v_cache[index], positions, length, c.heads,
-                                           c.kv_heads, scale, self.attention_workspace)
+            attn = layers.decode_attention_split(layer.handles["qkv"], positions, self.rope_cos, self.rope_sin, c.heads,
+                                                 c.kv_heads, c.head_dim, self.k_cache[index], self.v_cache[index],
+                                                 length, scale, self.attention_workspace, out=self.attn_buffer)
             layers.linear_split(layer.handles["o"], attn)
             layers.add_rmsnorm_split(h, layer.handles["o"], layer.post_norm, c.rms_eps, out=x)
             layers.linear_split(layer.handles["down"], self._gate_up_swiglu(layer, x))
