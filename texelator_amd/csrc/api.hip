@@ -116,15 +116,6 @@ int choose_splits(int RG, int CG, int cus) {
   return std::max(1, std::min(ks, CG));
 }
 
-// Default tile by token count (the autotuner's profile overrides it): measured best on the 27B-class
-// shapes -- small_32x128 up to 32 tokens, medium_64x128 up to 64, medium_128x128 beyond (two
-// workgroups per CU, which hide each other's LDS and decode latency).
-int default_candidate(int64_t tokens) {
-  if (tokens <= 32) return 9;
-  if (tokens <= 64) return 8;
-  return 6;
-}
-
 // Workspace bytes of a prefill call (split-K partials), 0 if none.
 int64_t prefill_workspace_bytes(const Handle *h, int64_t tokens) {
   const int ks = tx::prefill_splits(h->M, h->CG, tokens, h->cus);
@@ -306,7 +297,7 @@ int tx_linear(uint64_t value, const void *x, int x_dtype, int64_t x_numel, int64
   if (tokens >= h->prefill_threshold && tokens > 1) {
     if (h->bias && h->bias_dtype != x_dtype)
       return fail(TX_ERR_INVALID, f16 ? "FP16 prefill requires an FP16 bias" : "BF16 prefill requires a BF16 bias");
-    const int candidate = h->prefill_backend >= tx::kPrefillFirst ? h->prefill_backend : default_candidate(tokens);
+    const int candidate = h->prefill_backend >= tx::kPrefillFirst ? h->prefill_backend : tx::prefill_default_candidate(tokens);
     return run_prefill(h, candidate, x, f16, tokens, y, workspace, workspace_bytes, s);
   }
   if (h->bias && h->bias_dtype != x_dtype) return fail(TX_ERR_INVALID, "input and bias dtypes must match");

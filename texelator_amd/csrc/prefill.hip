@@ -27,6 +27,7 @@
 // Workgroups are mapped so that each XCD (workgroups arrive round-robin) works on few
 // (token tile, split) pairs: their activations stay in that XCD's L2.
 #include <algorithm>
+#include <array>
 
 #include "bc4_device.h"
 #include "elementwise.h"
@@ -508,15 +509,41 @@ const Candidate *find(int candidate) {
   return &kCandidates[candidate - kPrefillFirst];
 }
 
+// Workgroups of each candidate that one CU holds at once (its compiled registers and LDS), queried
+// once; 1 if the runtime cannot say.
+const std::array<int, kPrefillLast - kPrefillFirst + 1> &resident_per_cu() {
+  static const std::array<int, kPrefillLast - kPrefillFirst + 1> table = [] {
+    std::array<int, kPrefillLast - kPrefillFirst + 1> out{};
+    for (size_t i = 0; i < out.size(); ++i) {
+      int n = 0;
+      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kCandidates[i].fn, kThreads, 0) != hipSuccess || n < 1) {
+        (void)hipGetLastError();
+        n = 1;
+      }
+      out[i] = n;
+    }
+    return out;
+  }();
+  return table;
+}
+
 }  // namespace
 
+int prefill_default_candidate(int64_t tokens) {
+  if (tokens <= 32) return 9;  // small_32x128x128
+  if (tokens <= 64) return 8;  // medium_64x128x128
+  return 6;                    // medium_128x128x128
+}
+
 int prefill_splits(int M, int CG, int64_t tokens, int cus) {
-  // Candidate-independent so that every tile gives the same sums: about two workgroups of the
-  // largest tile per CU, each split at least 8 tile columns long, partials at most 32 MiB.
-  const int64_t items = ((M + 255) / 256) * ((tokens + 127) / 128);
-  const int64_t target = 2 * (int64_t)cus;
-  if (items >= target) return 1;
-  int64_t ks = (target + items - 1) / items;
+  // Candidate-independent, so that every tile gives the same sums, and sized for the default tile
+  // of this token count: as many splits as keep all of its workgroups resident at once, each
+  // split at least 8 tile columns long, partials at most 32 MiB.
+  const int dc = prefill_default_candidate(tokens);
+  const Candidate *c = find(dc);
+  const int64_t items = ((M + c->bn - 1) / c->bn) * ((tokens + c->bt - 1) / c->bt);
+  const int64_t slots = (int64_t)resident_per_cu()[dc - kPrefillFirst] * cus;
+  int64_t ks = std::max<int64_t>(1, slots / items);
   ks = std::min<int64_t>(ks, std::max(1, CG / 8));
   const int64_t cap = std::max<int64_t>(1, (int64_t(32) << 20) / (tokens * (int64_t)((M + 15) / 16 * 16) * 4));
   ks = std::min(ks, cap);
