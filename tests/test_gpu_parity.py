@@ -203,6 +203,29 @@ def test_prefill_split_k_matches_oracle(ext, oracle_threads, m, k, tokens):
     assert bc4.relative_rms(ref, outputs[0].float().cpu().numpy()) <= PREFILL_RRMS_TOL
 
 
+@pytest.mark.parametrize("m,k,tokens", [(200, 1040, 17), (200, 1040, 100), (37, 272, 40), (96, 4112, 20),
+                                         (64, 16, 70), (300, 2064, 129)])
+def test_prefill_ragged_k_matches_oracle(ext, oracle_threads, m, k, tokens):
+    """K not a multiple of the 128-wide step (the last step's activations are staged with the
+    columns past K zeroed), ragged rows and token counts, with and without K splits: every tile
+    bitwise equal and within the rrms bar of the float64 GEMM."""
+    blocks = random_blocks(m, k, 48)
+    scales = lognormal_scales(m, 49)
+    x = (bf16_vector((tokens, k), 50).float() * 0.125).to(torch.bfloat16)
+    bias = bf16_vector((m,), 51, scale=0.1)
+    handle = _pack(ext, blocks, scales, bias.cuda())
+    try:
+        outputs = [ext.prefill(handle, c, x.cuda()) for c in range(5, 10)]
+        torch.cuda.synchronize()
+    finally:
+        ext.free(handle)
+    for c, value in zip(range(6, 10), outputs[1:]):
+        assert torch.equal(outputs[0], value), f"candidate {c} differs"
+    w = clib.decode_bf16_bits(blocks, scales)
+    ref = clib.gemm_f64(bf16_bits(x), w) + bias.float().numpy()[None, :]
+    assert bc4.relative_rms(ref, outputs[0].float().cpu().numpy()) <= PREFILL_RRMS_TOL
+
+
 def test_prefill_bias_double_rounding(ext):
     m, k, tokens = 64, 256, 40
     blocks = random_blocks(m, k, 51)
