@@ -163,13 +163,14 @@ int tx_decode_attention(const void *q, const void *k_cache, const void *v_cache,
 
 /* tx_rope_kv_cache_split followed by tx_decode_attention, one kernel launch fewer: q and the new
  * token's key and value are the last tx_linear_split of qkv_handle ([q | k | v] rows), rotated
- * with the RoPE tables inside the attention kernel; the key and value are written to the caches
- * at *position. Bit-identical to the two calls. No counterpart in the reference (its decoder layers are Hugging Face modules,
- * docs/supported-models.md:3-5). */
-int tx_decode_attention_split(uint64_t qkv_handle, const int64_t *position, const float *cos_table,
-                              const float *sin_table, int64_t length, int heads, int kv_heads, int head_dim,
-                              void *k_cache, void *v_cache, int64_t max_context, float scale, void *workspace,
-                              int64_t workspace_bytes, void *out, void *stream);
+ * inside the attention kernel with rope_row = the RoPE tables' rows at *position (cos[head_dim]
+ * then sin[head_dim], fp32, gathered by the caller once per token); the key and value are
+ * written to the caches at *position. Bit-identical to the two calls. No counterpart in the
+ * reference (its decoder layers are Hugging Face modules, docs/supported-models.md:3-5). */
+int tx_decode_attention_split(uint64_t qkv_handle, const int64_t *position, const float *rope_row, int64_t length,
+                              int heads, int kv_heads, int head_dim, void *k_cache, void *v_cache,
+                              int64_t max_context, float scale, void *workspace, int64_t workspace_bytes, void *out,
+                              void *stream);
 
 /* out[r][c] = bf16(silu(g) * u) for gate_up rows [g (intermediate) | u (intermediate)], fp32 math. */
 int tx_swiglu(const void *gate_up, int64_t rows, int64_t intermediate, void *out, void *stream);

@@ -273,7 +273,8 @@ def test_decode_attention_split_is_bit_identical(ext, heads, kv, k, bias, positi
                                        torch.empty(heads * d, device="cuda", dtype=torch.bfloat16))
         want = layers.decode_attention(q, caches[0], caches[1], pos, length, heads, kv, scale, ws).clone()
         for _ in range(2):
-            got = layers.decode_attention_split(handle, pos, cos, sin, heads, kv, d, caches[2], caches[3], length,
+            rope_row = torch.cat([cos[position], sin[position]])
+            got = layers.decode_attention_split(handle, pos, rope_row, heads, kv, d, caches[2], caches[3], length,
                                                 scale, ws)
             assert torch.equal(want, got)
             assert torch.equal(caches[0], caches[2]) and torch.equal(caches[1], caches[3])

@@ -50,8 +50,8 @@ SIGNATURES = {
     "tx_rope_kv_cache": (_I32, [_P, _I64, _I64, _P, _P, _P, _I32, _I32, _I32, _P, _P, _P, _I64, _P]),
     "tx_decode_attention_workspace": (_I32, [_I32, _I64, ctypes.POINTER(_I64)]),
     "tx_decode_attention": (_I32, [_P, _P, _P, _P, _I64, _I32, _I32, _I32, _I64, ctypes.c_float, _P, _I64, _P, _P]),
-    "tx_decode_attention_split": (_I32, [_U64, _P, _P, _P, _I64, _I32, _I32, _I32, _P, _P, _I64, ctypes.c_float, _P,
-                                         _I64, _P, _P]),
+    "tx_decode_attention_split": (_I32, [_U64, _P, _P, _I64, _I32, _I32, _I32, _P, _P, _I64, ctypes.c_float, _P, _I64,
+                                         _P, _P]),
     "tx_swiglu": (_I32, [_P, _I64, _I64, _P, _P]),
     "tx_linear_split": (_I32, [_U64, _P, _P]),
     "tx_linear_swiglu": (_I32, [_U64, _P, _P, _P]),

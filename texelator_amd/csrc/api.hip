@@ -586,14 +586,14 @@ int tx_decode_attention(const void *q, const void *k_cache, const void *v_cache,
   return TX_OK;
 }
 
-int tx_decode_attention_split(uint64_t qkv_handle, const int64_t *position, const float *cos_table,
-                              const float *sin_table, int64_t length, int heads, int kv_heads, int head_dim,
-                              void *k_cache, void *v_cache, int64_t max_context, float scale, void *workspace,
-                              int64_t workspace_bytes, void *out, void *stream) {
+int tx_decode_attention_split(uint64_t qkv_handle, const int64_t *position, const float *rope_row, int64_t length,
+                              int heads, int kv_heads, int head_dim, void *k_cache, void *v_cache,
+                              int64_t max_context, float scale, void *workspace, int64_t workspace_bytes, void *out,
+                              void *stream) {
   g_last_error.clear();
   Handle *h = as_handle(qkv_handle);
   if (!h) return fail(TX_ERR_INVALID, "null Texelator handle");
-  if (!position || !cos_table || !sin_table || !k_cache || !v_cache || !out || !workspace)
+  if (!position || !rope_row || !k_cache || !v_cache || !out || !workspace)
     return fail(TX_ERR_INVALID, "decode_attention_split: null pointer");
   if (!tx::decode_attention_supported(heads, kv_heads, head_dim))
     return fail(TX_ERR_UNSUPPORTED, "decode_attention_split: needs head_dim 128 and at most 8 query heads per KV head");
@@ -606,7 +606,7 @@ int tx_decode_attention_split(uint64_t qkv_handle, const int64_t *position, cons
   tx_decode_attention_workspace(heads, length, &need);
   if (workspace_bytes < need) return fail(TX_ERR_INVALID, "decode_attention_split: workspace too small");
   DeviceGuard guard(h->device);
-  TX_HIP(tx::launch_decode_attention_split(split_source(h), position, cos_table, sin_table, length, heads, kv_heads,
+  TX_HIP(tx::launch_decode_attention_split(split_source(h), position, rope_row, length, heads, kv_heads,
                                            static_cast<uint16_t *>(k_cache), static_cast<uint16_t *>(v_cache),
                                            max_context, scale, static_cast<float *>(workspace),
                                            static_cast<uint16_t *>(out), reinterpret_cast<hipStream_t>(stream)));

@@ -167,8 +167,9 @@ constexpr int kKeyStrideU4 = kRowU4 + 1;
 // in fp32, and writes the chunk's max m, sum of exp l and unnormalised output o to
 // partials[kv][chunk][g][130].
 // ROPE: q and the new token's key and value come from the qkv decode GEMV's split-K partials
-// (summed, rounded and rotated exactly as rope_cache_kernel<true> does); the block whose chunk
-// holds the position writes the key and value into the caches and into its own tiles.
+// (summed, rounded and rotated exactly as rope_cache_kernel<true> does, with the RoPE table rows
+// of the position gathered by the caller, so no load waits for the position); the block whose
+// chunk holds the position writes the key and value into the caches and into its own tiles.
 // (Merging the chunks in the same launch -- each block publishing its partials behind a device
 // fence and the last one to take a ticket merging -- measured slower on MI355X: every such fence
 // writes back the XCD's L2, 64 times per XCD and layer at 4096 positions.)
@@ -176,7 +177,7 @@ constexpr int kKeyStrideU4 = kRowU4 + 1;
 struct AttnInput {
   const uint16_t *q;  // bf16 [heads][128] (without ROPE)
   SplitSource split;  // [q | k | v] split-K partials (with ROPE)
-  const float *cos_t, *sin_t;
+  const float *rope_row;  // cos[128] then sin[128] at the token's position (with ROPE)
   int heads, kv_heads;
 };
 
@@ -239,8 +240,8 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(AttnInput in, uin
         if (i < group * kHalf) {
           const int g = i / kHalf, j = i % kHalf;
           const float x1 = qv[u], x2 = qw[u];
-          const float c1 = in.cos_t[pos * kHeadDim + j], c2 = in.cos_t[pos * kHeadDim + j + kHalf];
-          const float s1 = in.sin_t[pos * kHeadDim + j], s2 = in.sin_t[pos * kHeadDim + j + kHalf];
+          const float c1 = in.rope_row[j], c2 = in.rope_row[j + kHalf];
+          const float s1 = in.rope_row[kHeadDim + j], s2 = in.rope_row[kHeadDim + j + kHalf];
           qs[g][j] = bf(to_bf(x1 * c1 - x2 * s1));
           qs[g][j + kHalf] = bf(to_bf(x2 * c2 + x1 * s2));
         }
@@ -258,8 +259,8 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(AttnInput in, uin
       if (tid < kHalf) {
         const int64_t col = (int64_t)(in.heads + kv) * kHeadDim + tid;
         const float x1 = split_value(in.split, 0, col), x2 = split_value(in.split, 0, col + kHalf);
-        const float c1 = in.cos_t[pos * kHeadDim + tid], c2 = in.cos_t[pos * kHeadDim + tid + kHalf];
-        const float s1 = in.sin_t[pos * kHeadDim + tid], s2 = in.sin_t[pos * kHeadDim + tid + kHalf];
+        const float c1 = in.rope_row[tid], c2 = in.rope_row[tid + kHalf];
+        const float s1 = in.rope_row[kHeadDim + tid], s2 = in.rope_row[kHeadDim + tid + kHalf];
         const uint16_t o1 = to_bf(x1 * c1 - x2 * s1), o2 = to_bf(x2 * c2 + x1 * s2);
         uint16_t *dst = k_cache + ((size_t)kv * max_ctx + pos) * kHeadDim;
         dst[tid] = o1;
@@ -502,14 +503,13 @@ hipError_t launch_decode_attention(const uint16_t *q, const uint16_t *k_cache, c
                                  max_ctx, scale, partials, out, stream);
 }
 
-hipError_t launch_decode_attention_split(const SplitSource &qkv, const int64_t *position, const float *cos_t,
-                                         const float *sin_t, int64_t length, int heads, int kv_heads,
+hipError_t launch_decode_attention_split(const SplitSource &qkv, const int64_t *position, const float *rope_row,
+                                         int64_t length, int heads, int kv_heads,
                                          uint16_t *k_cache, uint16_t *v_cache, int64_t max_ctx, float scale,
                                          float *partials, uint16_t *out, hipStream_t stream) {
   AttnInput in{};
   in.split = qkv;
-  in.cos_t = cos_t;
-  in.sin_t = sin_t;
+  in.rope_row = rope_row;
   in.heads = heads;
   in.kv_heads = kv_heads;
   return launch_attention<true>(in, k_cache, v_cache, position, length, max_ctx, scale, partials, out, stream);

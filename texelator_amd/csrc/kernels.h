@@ -92,10 +92,11 @@ int64_t decode_attention_workspace(int heads, int64_t length);
 hipError_t launch_decode_attention(const uint16_t *q, const uint16_t *k_cache, const uint16_t *v_cache,
                                    const int64_t *position, int64_t length, int heads, int kv_heads, int64_t max_ctx,
                                    float scale, float *partials, uint16_t *out, hipStream_t stream);
-// The same with RoPE: q and the new token's key and value from the qkv GEMV's split-K partials;
-// the key and value are also written to the caches at the position.
-hipError_t launch_decode_attention_split(const SplitSource &qkv, const int64_t *position, const float *cos_t,
-                                         const float *sin_t, int64_t length, int heads, int kv_heads,
+// The same with RoPE: q and the new token's key and value from the qkv GEMV's split-K partials,
+// rotated with rope_row (cos[128] then sin[128] at the position); the key and value are also
+// written to the caches at the position.
+hipError_t launch_decode_attention_split(const SplitSource &qkv, const int64_t *position, const float *rope_row,
+                                         int64_t length, int heads, int kv_heads,
                                          uint16_t *k_cache, uint16_t *v_cache, int64_t max_ctx, float scale,
                                          float *partials, uint16_t *out, hipStream_t stream);
 hipError_t launch_swiglu(const uint16_t *gu, int64_t rows, int64_t inter, uint16_t *out, hipStream_t stream);

@@ -102,29 +102,28 @@ def decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
     return out
 
 
-def decode_attention_split(qkv_handle: int, positions: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
-                           heads: int, kv_heads: int, head_dim: int, k_cache: torch.Tensor, v_cache: torch.Tensor,
-                           length: int, scale: float, workspace: torch.Tensor,
-                           out: torch.Tensor | None = None) -> torch.Tensor:
+def decode_attention_split(qkv_handle: int, positions: torch.Tensor, rope_row: torch.Tensor, heads: int,
+                           kv_heads: int, head_dim: int, k_cache: torch.Tensor, v_cache: torch.Tensor, length: int,
+                           scale: float, workspace: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
     """:func:`rope_kv_cache_split` then :func:`decode_attention` with one kernel launch fewer
     (bit-identical to the two calls): one token whose ``[q | k | v]`` row is the last
-    :func:`linear_split` of ``qkv_handle``; its key and value are written to the caches at
-    ``positions[0]``."""
+    :func:`linear_split` of ``qkv_handle``; ``rope_row`` holds the RoPE tables' rows at
+    ``positions[0]`` (fp32 ``[cos (head_dim) | sin (head_dim)]``). The key and value are written to
+    the caches at ``positions[0]``."""
     _expect(positions.dtype == torch.int64 and positions.is_contiguous() and positions.numel() == 1,
             "positions must be int64 [1]")
+    _expect(rope_row.dtype == torch.float32 and rope_row.is_contiguous() and rope_row.numel() == 2 * head_dim,
+            "rope_row must be float32 [2 * head_dim]")
     max_ctx = k_cache.shape[1]
     for cache in (k_cache, v_cache):
         _expect(cache.dtype == torch.bfloat16 and cache.is_contiguous() and tuple(cache.shape) == (kv_heads, max_ctx, head_dim),
                 "caches must be contiguous bf16 [kv_heads, max_context, head_dim]")
-    for table in (cos, sin):
-        _expect(table.dtype == torch.float32 and table.is_contiguous() and tuple(table.shape) == (max_ctx, head_dim),
-                "rope tables must be float32 [max_context, head_dim]")
     need = decode_attention_workspace_bytes(heads, length)
     _expect(workspace.is_cuda and workspace.numel() * workspace.element_size() >= need, "decode attention workspace too small")
     if out is None:
         out = torch.empty((1, heads * head_dim), dtype=torch.bfloat16, device=k_cache.device)
     _expect(out.dtype == torch.bfloat16 and out.is_contiguous() and out.numel() == heads * head_dim, "bad out")
-    check(_lib.load().tx_decode_attention_split(qkv_handle, _ptr(positions), _ptr(cos), _ptr(sin), int(length), heads,
+    check(_lib.load().tx_decode_attention_split(qkv_handle, _ptr(positions), _ptr(rope_row), int(length), heads,
                                                 kv_heads, head_dim, _ptr(k_cache), _ptr(v_cache), max_ctx, float(scale),
                                                 _ptr(workspace), workspace.numel() * workspace.element_size(),
                                                 _ptr(out), _stream(positions)))

@@ -203,6 +203,9 @@ class BC4Decoder:
         angles = torch.arange(self.max_context, device=self.device, dtype=torch.float32)[:, None] * inv_freq[None, :]
         angles = torch.cat([angles, angles], dim=-1)
         self.rope_cos, self.rope_sin = angles.cos().contiguous(), angles.sin().contiguous()
+        # [cos | sin] per position, and the row of the current decode step (gathered once per token)
+        self.rope_cs = torch.cat([self.rope_cos, self.rope_sin], dim=1).contiguous()
+        self.rope_row = torch.empty(1, 2 * c.head_dim, dtype=torch.float32, device=self.device)
         self.key_positions = torch.arange(self.max_context, device=self.device)
         self.attention_workspace = torch.empty(
             layers.decode_attention_workspace_bytes(c.heads, self.max_context) if fused else 16,
@@ -339,11 +342,12 @@ class BC4Decoder:
                       scale: float) -> torch.Tensor:
         """One token through every layer with the split-K consumers (eight kernels a layer)."""
         c = self.config
+        torch.index_select(self.rope_cs, 0, positions, out=self.rope_row)
         for index, layer in enumerate(self.layers):
             layers.linear_split(layer.handles["qkv"], x)
-            attn = layers.decode_attention_split(layer.handles["qkv"], positions, self.rope_cos, self.rope_sin, c.heads,
-                                                 c.kv_heads, c.head_dim, self.k_cache[index], self.v_cache[index],
-                                                 length, scale, self.attention_workspace, out=self.attn_buffer)
+            attn = layers.decode_attention_split(layer.handles["qkv"], positions, self.rope_row, c.heads, c.kv_heads,
+                                                 c.head_dim, self.k_cache[index], self.v_cache[index], length, scale,
+                                                 self.attention_workspace, out=self.attn_buffer)
             layers.linear_split(layer.handles["o"], attn)
             layers.add_rmsnorm_split(h, layer.handles["o"], layer.post_norm, c.rms_eps, out=x)
             layers.linear_split(layer.handles["down"], self._gate_up_swiglu(layer, x))
