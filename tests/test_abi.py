@@ -42,5 +42,5 @@ def test_errors_without_gpu_are_reported_not_crashing():
     assert lib.tx_set_lookahead(0, 2) == _lib.TX_ERR_INVALID
     assert b"null" in lib.tx_last_error()
     assert lib.tx_free(0) == _lib.TX_ERR_INVALID
-    assert lib.tx_candidate_name(5) == b"large_128x256x128"
+    assert lib.tx_candidate_name(5) == b"large_256x128x128"
     assert lib.tx_candidate_name(4) is None

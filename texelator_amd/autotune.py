@@ -26,13 +26,13 @@ from .runtime import PACKAGE_ROOT, extension, free, pack_entry_handles
 from .store import STATE_HOME, safe_name
 
 CANDIDATES = {
-    "large_128x256x128": 5,
+    "large_256x128x128": 5,
     "medium_128x128x128": 6,
     "medium_64x256x128": 7,
     "medium_64x128x128": 8,
     "small_32x128x128": 9,
 }
-BASELINE = "large_128x256x128"
+BASELINE = "large_256x128x128"
 TOKEN_BUCKETS = (32, 128, 512, 2048, 8192, 16384, 32768, 65535)
 
 

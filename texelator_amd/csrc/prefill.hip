@@ -28,6 +28,7 @@
 // (token tile, split) pairs: their activations stay in that XCD's L2.
 #include <algorithm>
 #include <array>
+#include <type_traits>
 
 #include "bc4_device.h"
 #include "elementwise.h"
@@ -443,6 +444,213 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillParams p) {
   }
 }
 
+// Pair-shared tile: 8 waves, 256 tokens x 128 rows. Waves w and w + 4 own the same 32-row block
+// (rb = w % 4) for token halves 0 and 1. Per K step each of the two decodes only the blocks of
+// one 64-wide half of the step (h2 = its token half, MFMAs s = 4*h2 .. 4*h2 + 3) and hands the
+// operands to its partner through LDS, so a weight is decoded once per 256 tokens while every
+// SIMD keeps two waves. MFMA order per accumulator is the other tiles' (s = 0..7 per step), so
+// the results are bitwise equal to theirs. Palette seeds are computed in registers: the two
+// activation buffers (64 KiB each) and the operand exchange (32 KiB) fill the 160 KiB of LDS.
+constexpr int kPairThreads = 512;
+
+template <bool F16, int LA, bool LUT>
+__global__ __launch_bounds__(kPairThreads) void prefill_pair_kernel(PrefillParams p) {
+  static_assert(LA >= 2, "the pipelined K loop needs two weight tiles in flight");
+  constexpr int BT = 256, BN = 128, TBH = 4;  // tokens, rows, 32-token blocks per wave
+  constexpr int XC = BT * 16 / kPairThreads;  // 16-byte activation chunks staged per thread per step
+  constexpr int NS = LA - 1;                  // weight pieces held between steps
+  __shared__ __attribute__((aligned(16))) uint16_t xs0[BT * kTileK];
+  __shared__ __attribute__((aligned(16))) uint16_t xs1[BT * kTileK];
+  __shared__ u32x4 xch[4][2][4][64];  // [row block][K half][MFMA of the half][lane]
+
+  WorkItem w;
+  if (!work_item(p, BT, BN, w)) return;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int rb = wave & 3;
+  const int half = wave >> 2;
+  const int r32 = lane & 31;
+  const int h = lane >> 5;
+  const uint16_t *x = static_cast<const uint16_t *>(p.x);
+  auto k_offset = [&](int s) { return 64 * (s >> 2) + 32 * h + 16 * ((s >> 1) & 1) + 8 * (s & 1); };
+
+  // This wave's piece of each step: lane slot (row & 15) + 16h + 32*half of the row block's tiles,
+  // i.e. blocks 4*half + 2h (words x, y) and 4*half + 2h + 1 (words z, w) of row l % 32.
+  const int g = min(w.n0 / kTileRows + rb * 2 + (r32 >> 4), p.RG - 1);
+  const uint4 *gt = p.tiles + ((size_t)g * p.CG + w.c_begin) * 64 + (lane & 15) + 16 * h + 32 * half;
+  const float scale = p.scales[g * kTileRows + (lane & 15)];
+  const uint32_t pm = pm_scale_pair<F16>(scale);
+  auto load_piece = [&](int j) { return load_stream(gt + (size_t)min(j, w.nc - 1) * 64); };
+  // Operands a[2jj + e] = positions 8e..8e+7 of local block jj (MFMA s = 4*half + 2jj + e).
+  auto decode_one = [&](const uint4 &piece, int jj, u32x4 (&a)[4]) {
+    const uint32_t wa = jj ? piece.z : piece.x;
+    const uint32_t wb = jj ? piece.w : piece.y;
+    uint32_t d[8];
+    if constexpr (LUT) {
+      const float4 *row = p.lut + 2 * (size_t)palette_row(wa, wb);
+      decode_from_palette<F16>(row[0], row[1], wa, wb, scale, d);
+    } else {
+      decode_block<F16>(wa, wb, scale, pm, d);
+    }
+    a[2 * jj] = u32x4{d[0], d[1], d[2], d[3]};
+    a[2 * jj + 1] = u32x4{d[4], d[5], d[6], d[7]};
+  };
+
+  // Activation staging as in prefill_kernel, 512 threads: thread i stages row 32v + i/16 into
+  // slot i % 16 (row % 16 = (i/16) % 16).
+  const int srow = threadIdx.x >> 4;
+  const int scol = ((threadIdx.x & 15) ^ (srow & 15)) * 8;
+  const bool tile_full = w.t0 + BT <= p.tokens;
+  const uint32_t lane_off = (uint32_t)(srow * p.K + scol) * 2;
+  auto stage_part = [&](uint16_t *buf, int j, int v0, int v1) {
+    const int c = w.c_begin + j;
+    if ((c + 1) * kTileK <= p.K) {
+#pragma unroll
+      for (int v = v0; v < v1; ++v) {
+        const int row0 = tile_full ? w.t0 + 32 * v : min(w.t0 + 32 * v, p.tokens - 1);
+        const char *base = reinterpret_cast<const char *>(x + ((size_t)row0 * p.K + c * kTileK));
+        uint32_t off = lane_off;
+        if (!tile_full) off = (uint32_t)((min(w.t0 + 32 * v + srow, p.tokens - 1) - row0) * p.K + scol) * 2;
+        __builtin_amdgcn_global_load_lds((const void *)(base + off),
+                                         (__attribute__((address_space(3))) void *)(buf + (32 * v + 4 * wave) * kTileK),
+                                         16, 0, 0);
+      }
+    } else if (v0 == 0) {
+      const int k = c * kTileK + scol;
+#pragma unroll 2
+      for (int v = 0; v < XC; ++v) {
+        const int t = min(w.t0 + 32 * v + srow, p.tokens - 1);
+        uint4 value = make_uint4(0u, 0u, 0u, 0u);
+        if (k < p.K) value = *reinterpret_cast<const uint4 *>(x + (size_t)t * p.K + k);
+        *reinterpret_cast<uint4 *>(buf + (32 * v + srow) * kTileK + (threadIdx.x & 15) * 8) = value;
+      }
+    }
+  };
+  auto full_barrier = [&]() { asm volatile("s_waitcnt vmcnt(0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
+  auto lds_barrier = [&]() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
+
+  // Prologue: step 0's activations and the first weight pieces.
+  stage_part(xs0, 0, 0, XC);
+  __builtin_amdgcn_sched_barrier(0);
+  const uint4 first = load_piece(0);
+  uint4 ring[NS];
+#pragma unroll
+  for (int u = 0; u < NS; ++u) ring[u] = load_piece(u + 1);
+  __builtin_amdgcn_s_waitcnt(0x0F70);
+  __syncthreads();
+
+  auto run = [&](auto half_c) {
+    constexpr int HALF = decltype(half_c)::value;
+    f32x16 acc[TBH];
+#pragma unroll
+    for (int tb = 0; tb < TBH; ++tb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[tb][r] = 0.f;
+    // Operands of the step being multiplied: this wave's half and its partner's.
+    u32x4 aown[4], apar[4];
+    decode_one(first, 0, aown);
+    decode_one(first, 1, aown);
+#pragma unroll
+    for (int sl = 0; sl < 4; ++sl) xch[rb][HALF][sl][lane] = aown[sl];
+    full_barrier();
+#pragma unroll
+    for (int sl = 0; sl < 4; ++sl) apar[sl] = xch[rb][1 - HALF][sl][lane];
+    lds_barrier();
+    auto operand = [&](int s) -> const u32x4 & { return (s >> 2) == HALF ? aown[s & 3] : apar[s & 3]; };
+
+    auto step = [&](int j, const uint16_t *xb, uint16_t *xn) {
+      const bool more = j + 1 < w.nc;
+      const uint4 fresh = load_piece(j + LA);
+      __builtin_amdgcn_sched_barrier(0);
+      const uint4 next = ring[0];  // piece of step j+1 (past the end: the clamped last piece)
+      auto read_b = [&](int tb, int s) {
+        return *reinterpret_cast<const u32x4 *>(xb + (128 * HALF + 32 * tb + r32) * kTileK +
+                                                8 * ((k_offset(s) >> 3) ^ (r32 & 15)));
+      };
+      u32x4 anext[4];
+      u32x4 bcur[2][TBH];
+#pragma unroll
+      for (int e = 0; e < 2; ++e)
+#pragma unroll
+        for (int tb = 0; tb < TBH; ++tb) bcur[e][tb] = read_b(tb, e);
+#pragma unroll
+      for (int rg = 0; rg < 4; ++rg) {
+        if (more) stage_part(xn, j + 1, rg * XC / 4, (rg + 1) * XC / 4);
+        u32x4 bnext[2][TBH];
+        if (rg + 1 < 4) {
+#pragma unroll
+          for (int e = 0; e < 2; ++e)
+#pragma unroll
+            for (int tb = 0; tb < TBH; ++tb) bnext[e][tb] = read_b(tb, 2 * rg + 2 + e);
+        }
+        if (rg % 2 == 0) decode_one(next, rg / 2, anext);
+#pragma unroll
+        for (int e = 0; e < 2; ++e)
+#pragma unroll
+          for (int tb = 0; tb < TBH; ++tb) acc[tb] = mfma<F16>(operand(2 * rg + e), bcur[e][tb], acc[tb]);
+        if (rg % 2 == 0) asm volatile("" : "+v"(anext[rg]), "+v"(anext[rg + 1]));
+        __builtin_amdgcn_sched_barrier(0);
+        if (rg + 1 < 4) {
+#pragma unroll
+          for (int e = 0; e < 2; ++e)
+#pragma unroll
+            for (int tb = 0; tb < TBH; ++tb) bcur[e][tb] = bnext[e][tb];
+        }
+      }
+      // Hand over the next step's operands: written before the step's barrier, read after it, and
+      // a second barrier before they are overwritten a step later.
+#pragma unroll
+      for (int sl = 0; sl < 4; ++sl) xch[rb][HALF][sl][lane] = anext[sl];
+      full_barrier();
+#pragma unroll
+      for (int sl = 0; sl < 4; ++sl) {
+        aown[sl] = anext[sl];
+        apar[sl] = xch[rb][1 - HALF][sl][lane];
+      }
+      lds_barrier();
+#pragma unroll
+      for (int u = 0; u + 1 < NS; ++u) ring[u] = ring[u + 1];
+      ring[NS - 1] = fresh;
+    };
+    int j0 = 0;
+    for (; j0 + 2 <= w.nc; j0 += 2) {
+      step(j0, xs0, xs1);
+      step(j0 + 1, xs1, xs0);
+    }
+    if (j0 < w.nc) step(j0, xs0, xs1);
+
+    // acc[tb][r] = D[row 8(r/4) + 4h + r%4 of row block rb][token 128*HALF + 32*tb + r32].
+    const uint16_t *bias = static_cast<const uint16_t *>(p.bias);
+#pragma unroll
+    for (int tb = 0; tb < TBH; ++tb) {
+      const int t = w.t0 + 128 * HALF + tb * 32 + r32;
+      if (t >= p.tokens) continue;
+#pragma unroll
+      for (int rq = 0; rq < 4; ++rq) {
+        const int row0 = w.n0 + rb * 32 + 8 * rq + 4 * h;
+        const f32x16 &v = acc[tb];
+        if (p.ks > 1) {
+          float *dst = p.partials + ((size_t)w.split * p.tokens + t) * p.Mp + row0;
+          if (row0 < p.Mp) *reinterpret_cast<float4 *>(dst) = make_float4(v[4 * rq], v[4 * rq + 1], v[4 * rq + 2], v[4 * rq + 3]);
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int n = row0 + r;
+            if (n < p.M) {
+              float out = round_out<F16>(v[4 * rq + r]);
+              if (bias) out += half_bits_to_float<F16>(bias[n]);
+              store_out<F16>(p.y, (size_t)t * p.M + n, out);
+            }
+          }
+        }
+      }
+    }
+  };
+  if (half == 0) run(std::integral_constant<int, 0>{});
+  else run(std::integral_constant<int, 1>{});
+}
+
 // y[t][m] = round(sum over splits in order of partials[s][t][m]), then the bias with a second
 // rounding (the reference's epilogue order); bf16, or fp16 with F16.
 template <bool F16>
@@ -463,7 +671,36 @@ struct Candidate {
   const void *fn;
   hipError_t (*launch)(const PrefillParams &, hipStream_t);
   int lds;
+  int threads;
 };
+
+// The ordered reduction of the split-K partials, after the tile kernel.
+hipError_t launch_reduce(const PrefillParams &p, hipStream_t stream) {
+  if (p.f16)
+    hipLaunchKernelGGL(prefill_reduce_kernel<true>, dim3((p.M + 255) / 256, p.tokens), dim3(256), 0, stream, p);
+  else
+    hipLaunchKernelGGL(prefill_reduce_kernel<false>, dim3((p.M + 255) / 256, p.tokens), dim3(256), 0, stream, p);
+  return hipGetLastError();
+}
+
+template <int LA>
+hipError_t launch_pair(const PrefillParams &p, hipStream_t stream) {
+  const int items = ((p.M + 127) / 128) * ((p.tokens + 255) / 256) * p.ks;
+  const int grid = ((items + kXcds - 1) / kXcds) * kXcds;
+  if (p.lut) {
+    if (p.f16)
+      hipLaunchKernelGGL((prefill_pair_kernel<true, LA, true>), dim3(grid), dim3(kPairThreads), 0, stream, p);
+    else
+      hipLaunchKernelGGL((prefill_pair_kernel<false, LA, true>), dim3(grid), dim3(kPairThreads), 0, stream, p);
+  } else if (p.f16) {
+    hipLaunchKernelGGL((prefill_pair_kernel<true, LA, false>), dim3(grid), dim3(kPairThreads), 0, stream, p);
+  } else {
+    hipLaunchKernelGGL((prefill_pair_kernel<false, LA, false>), dim3(grid), dim3(kPairThreads), 0, stream, p);
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || p.ks == 1) return e;
+  return launch_reduce(p, stream);
+}
 
 template <int TB, int RB, int LA, bool PIPE>
 hipError_t launch_tile(const PrefillParams &p, hipStream_t stream) {
@@ -482,22 +719,20 @@ hipError_t launch_tile(const PrefillParams &p, hipStream_t stream) {
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || p.ks == 1) return e;
-  if (p.f16)
-    hipLaunchKernelGGL(prefill_reduce_kernel<true>, dim3((p.M + 255) / 256, p.tokens), dim3(256), 0, stream, p);
-  else
-    hipLaunchKernelGGL(prefill_reduce_kernel<false>, dim3((p.M + 255) / 256, p.tokens), dim3(256), 0, stream, p);
-  return hipGetLastError();
+  return launch_reduce(p, stream);
 }
 
 #define TX_CANDIDATE(NAME, TB, RB, LA, PIPE)                                                            \
   Candidate {                                                                                          \
     NAME, 32 * (TB), 128 * (RB), reinterpret_cast<const void *>(&prefill_kernel<false, TB, RB, LA, PIPE, false>), \
-        &launch_tile<TB, RB, LA, PIPE>, 2 * 32 * (TB) * kTileK * 2                                    \
+        &launch_tile<TB, RB, LA, PIPE>, 2 * 32 * (TB) * kTileK * 2, kThreads                          \
   }
 
-// The two 128-token tiles pipeline their K loop; the smaller tiles run it plainly.
+// The 256- and 128-token tiles pipeline their K loop; the smaller tiles run it plainly.
 const Candidate kCandidates[] = {
-    TX_CANDIDATE("large_128x256x128", 4, 2, TX_PREFILL_LA, true),
+    Candidate{"large_256x128x128", 256, 128,
+              reinterpret_cast<const void *>(&prefill_pair_kernel<false, TX_PREFILL_LA, false>),
+              &launch_pair<TX_PREFILL_LA>, 2 * 256 * kTileK * 2 + 4 * 2 * 4 * 64 * 16, kPairThreads},
     TX_CANDIDATE("medium_128x128x128", 4, 1, TX_PREFILL_LA, true),
     TX_CANDIDATE("medium_64x256x128", 2, 2, TX_PREFILL_LA_PLAIN, false),
     TX_CANDIDATE("medium_64x128x128", 2, 1, TX_PREFILL_LA_PLAIN, false),
@@ -516,7 +751,8 @@ const std::array<int, kPrefillLast - kPrefillFirst + 1> &resident_per_cu() {
     std::array<int, kPrefillLast - kPrefillFirst + 1> out{};
     for (size_t i = 0; i < out.size(); ++i) {
       int n = 0;
-      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kCandidates[i].fn, kThreads, 0) != hipSuccess || n < 1) {
+      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kCandidates[i].fn, kCandidates[i].threads, 0) != hipSuccess ||
+          n < 1) {
         (void)hipGetLastError();
         n = 1;
       }
@@ -529,17 +765,21 @@ const std::array<int, kPrefillLast - kPrefillFirst + 1> &resident_per_cu() {
 
 }  // namespace
 
-int prefill_default_candidate(int64_t tokens) {
-  if (tokens <= 32) return 9;  // small_32x128x128
-  if (tokens <= 64) return 8;  // medium_64x128x128
-  return 6;                    // medium_128x128x128
+int prefill_default_candidate(int M, int64_t tokens, int cus) {
+  if (tokens <= 32) return 9;   // small_32x128x128
+  if (tokens <= 64) return 8;   // medium_64x128x128
+  if (tokens < 256) return 6;   // medium_128x128x128
+  // The pair-shared 256x128 tile (one workgroup per CU) while its workgroups fill at most two
+  // rounds of the CUs; beyond, the 128x128 tile's finer grain fills the last round better.
+  const int64_t pair_items = (int64_t)((M + 127) / 128) * ((tokens + 255) / 256);
+  return pair_items <= 2 * (int64_t)cus ? 5 : 6;
 }
 
 int prefill_splits(int M, int CG, int64_t tokens, int cus) {
   // Candidate-independent, so that every tile gives the same sums, and sized for the default tile
-  // of this token count: as many splits as keep all of its workgroups resident at once, each
-  // split at least 8 tile columns long, partials at most 32 MiB.
-  const int dc = prefill_default_candidate(tokens);
+  // of this shape: as many splits as keep all of its workgroups resident at once, each split at
+  // least 8 tile columns long, partials at most 32 MiB.
+  const int dc = prefill_default_candidate(M, tokens, cus);
   const Candidate *c = find(dc);
   const int64_t items = ((M + c->bn - 1) / c->bn) * ((tokens + c->bt - 1) / c->bt);
   const int64_t slots = (int64_t)resident_per_cu()[dc - kPrefillFirst] * cus;
