@@ -452,6 +452,15 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillParams p) {
 // the results are bitwise equal to theirs. Palette seeds are computed in registers: the two
 // activation buffers (64 KiB each) and the operand exchange (32 KiB) fill the 160 KiB of LDS.
 constexpr int kPairThreads = 512;
+// Scheduling regions per K step of the pair-shared tile (each 8/kPairRegions MFMA groups; the two
+// block decodes go to the first region of each half of the step).
+#ifndef TX_PAIR_REGIONS
+#define TX_PAIR_REGIONS 4
+#endif
+constexpr int kPairRegions = TX_PAIR_REGIONS;
+#ifndef TX_PAIR_LA
+#define TX_PAIR_LA TX_PREFILL_LA
+#endif
 
 template <bool F16, int LA, bool LUT>
 __global__ __launch_bounds__(kPairThreads) void prefill_pair_kernel(PrefillParams p) {
@@ -568,32 +577,35 @@ __global__ __launch_bounds__(kPairThreads) void prefill_pair_kernel(PrefillParam
         return *reinterpret_cast<const u32x4 *>(xb + (128 * HALF + 32 * tb + r32) * kTileK +
                                                 8 * ((k_offset(s) >> 3) ^ (r32 & 15)));
       };
+      constexpr int NRG = kPairRegions, SG = 8 / NRG;  // regions, MFMA groups per region
       u32x4 anext[4];
-      u32x4 bcur[2][TBH];
+      u32x4 bcur[SG][TBH];
 #pragma unroll
-      for (int e = 0; e < 2; ++e)
+      for (int e = 0; e < SG; ++e)
 #pragma unroll
         for (int tb = 0; tb < TBH; ++tb) bcur[e][tb] = read_b(tb, e);
 #pragma unroll
-      for (int rg = 0; rg < 4; ++rg) {
-        if (more) stage_part(xn, j + 1, rg * XC / 4, (rg + 1) * XC / 4);
-        u32x4 bnext[2][TBH];
-        if (rg + 1 < 4) {
+      for (int rg = 0; rg < NRG; ++rg) {
+        if (more) stage_part(xn, j + 1, rg * XC / NRG, (rg + 1) * XC / NRG);
+        u32x4 bnext[SG][TBH];
+        if (rg + 1 < NRG) {
 #pragma unroll
-          for (int e = 0; e < 2; ++e)
+          for (int e = 0; e < SG; ++e)
 #pragma unroll
-            for (int tb = 0; tb < TBH; ++tb) bnext[e][tb] = read_b(tb, 2 * rg + 2 + e);
+            for (int tb = 0; tb < TBH; ++tb) bnext[e][tb] = read_b(tb, SG * (rg + 1) + e);
         }
-        if (rg % 2 == 0) decode_one(next, rg / 2, anext);
+        const bool dec = rg % (NRG / 2) == 0;  // first region of each half of the step
+        const int jj = rg / (NRG / 2);
+        if (dec) decode_one(next, jj, anext);
 #pragma unroll
-        for (int e = 0; e < 2; ++e)
+        for (int e = 0; e < SG; ++e)
 #pragma unroll
-          for (int tb = 0; tb < TBH; ++tb) acc[tb] = mfma<F16>(operand(2 * rg + e), bcur[e][tb], acc[tb]);
-        if (rg % 2 == 0) asm volatile("" : "+v"(anext[rg]), "+v"(anext[rg + 1]));
+          for (int tb = 0; tb < TBH; ++tb) acc[tb] = mfma<F16>(operand(SG * rg + e), bcur[e][tb], acc[tb]);
+        if (dec) asm volatile("" : "+v"(anext[2 * jj]), "+v"(anext[2 * jj + 1]));
         __builtin_amdgcn_sched_barrier(0);
-        if (rg + 1 < 4) {
+        if (rg + 1 < NRG) {
 #pragma unroll
-          for (int e = 0; e < 2; ++e)
+          for (int e = 0; e < SG; ++e)
 #pragma unroll
             for (int tb = 0; tb < TBH; ++tb) bcur[e][tb] = bnext[e][tb];
         }
@@ -731,8 +743,8 @@ hipError_t launch_tile(const PrefillParams &p, hipStream_t stream) {
 // The 256- and 128-token tiles pipeline their K loop; the smaller tiles run it plainly.
 const Candidate kCandidates[] = {
     Candidate{"large_256x128x128", 256, 128,
-              reinterpret_cast<const void *>(&prefill_pair_kernel<false, TX_PREFILL_LA, false>),
-              &launch_pair<TX_PREFILL_LA>, 2 * 256 * kTileK * 2 + 4 * 2 * 4 * 64 * 16, kPairThreads},
+              reinterpret_cast<const void *>(&prefill_pair_kernel<false, TX_PAIR_LA, false>),
+              &launch_pair<TX_PAIR_LA>, 2 * 256 * kTileK * 2 + 4 * 2 * 4 * 64 * 16, kPairThreads},
     TX_CANDIDATE("medium_128x128x128", 4, 1, TX_PREFILL_LA, true),
     TX_CANDIDATE("medium_64x256x128", 2, 2, TX_PREFILL_LA_PLAIN, false),
     TX_CANDIDATE("medium_64x128x128", 2, 1, TX_PREFILL_LA_PLAIN, false),
