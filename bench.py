@@ -211,17 +211,20 @@ def kernel_only(torch, ext, runtime, hardware, device, args) -> int:
 
 def prefill_only(torch, ext, runtime, hardware, device, args) -> int:
     """Launches for counter runs: the 5120->27648 prefill GEMM at ``--prompt`` tokens (the library's
-    default tile for that token count) on ``--layers`` distinct copies, twice each."""
+    default tile for that shape, or candidate ``--tile``) on ``--layers`` distinct copies, twice each."""
     lut = hardware.device_palette(device)
     blocks, scales = encoded_weights(torch, [(INTER, HIDDEN)], lut)[(INTER, HIDDEN)]
     handles = [runtime.pack_arrays(blocks, scales)[0] for _ in range(args.layers)]
+    if args.tile:
+        for handle in handles:
+            ext.set_prefill_backend(handle, args.tile)
     x = torch.randn((args.prompt, HIDDEN), device=device).to(torch.bfloat16)
     for _ in range(2):
         for handle in handles:
             ext.linear(handle, x)
     torch.cuda.synchronize()
     runtime.free(handles)
-    print(json.dumps({"prefill_only": True, "launches": 2 * len(handles), "tokens": args.prompt,
+    print(json.dumps({"prefill_only": True, "launches": 2 * len(handles), "tokens": args.prompt, "tile": args.tile,
                       "flops_per_launch": 2 * args.prompt * INTER * HIDDEN}), flush=True)
     return 0
 
@@ -288,6 +291,8 @@ def main() -> int:
                         help="profiling mode: only the model-level prefill and decode measurement (its JSON)")
     parser.add_argument("--prefill-only", action="store_true",
                         help="profiling mode: only the gate/up prefill GEMM at --prompt tokens over the layer copies")
+    parser.add_argument("--tile", type=int, default=0, choices=range(0, 10),
+                        help="with --prefill-only: prefill tile candidate 5..9 (0: the library's default)")
     parser.add_argument("--kernel-only", action="store_true",
                         help="profiling mode: only the gate/up GEMV over the layer copies, then a plain copy of "
                              "COPY_BYTES bytes that calibrates the HBM byte counters")

@@ -298,7 +298,7 @@ int tx_linear(uint64_t value, const void *x, int x_dtype, int64_t x_numel, int64
     if (h->bias && h->bias_dtype != x_dtype)
       return fail(TX_ERR_INVALID, f16 ? "FP16 prefill requires an FP16 bias" : "BF16 prefill requires a BF16 bias");
     const int candidate = h->prefill_backend >= tx::kPrefillFirst ? h->prefill_backend
-                                                                  : tx::prefill_default_candidate(h->M, tokens, h->cus);
+                                                                  : tx::prefill_default_candidate(h->M, h->K, tokens, h->cus);
     return run_prefill(h, candidate, x, f16, tokens, y, workspace, workspace_bytes, s);
   }
   if (h->bias && h->bias_dtype != x_dtype) return fail(TX_ERR_INVALID, "input and bias dtypes must match");

@@ -53,8 +53,9 @@ bool prefill_candidate_eligible(int candidate, int M, int K);
 // Default tile by shape (the autotuner's profile overrides it): measured best on the 27B-class
 // shapes -- small_32x128 up to 32 tokens, medium_64x128 up to 64, medium_128x128 below 256 (two
 // workgroups per CU, which hide each other's LDS and decode latency), from 256 tokens
-// large_256x128 (decode shared by wave pairs) unless it would take more than two rounds of the CUs.
-int prefill_default_candidate(int M, int64_t tokens, int cus);
+// large_256x128 (decode shared by wave pairs) when its workgroups make one round of the CUs at
+// least three quarters full.
+int prefill_default_candidate(int M, int K, int64_t tokens, int cus);
 int prefill_splits(int M, int CG, int64_t tokens, int cus);
 hipError_t launch_prefill(const PrefillParams &p, int candidate, hipStream_t stream);
 hipError_t prefill_kernel_attributes(int candidate, hipFuncAttributes *attr, int *lds_bytes);

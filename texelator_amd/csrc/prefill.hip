@@ -777,21 +777,27 @@ const std::array<int, kPrefillLast - kPrefillFirst + 1> &resident_per_cu() {
 
 }  // namespace
 
-int prefill_default_candidate(int M, int64_t tokens, int cus) {
+int prefill_default_candidate(int M, int K, int64_t tokens, int cus) {
   if (tokens <= 32) return 9;   // small_32x128x128
   if (tokens <= 64) return 8;   // medium_64x128x128
   if (tokens < 256) return 6;   // medium_128x128x128
-  // The pair-shared 256x128 tile (one workgroup per CU) while its workgroups fill at most two
-  // rounds of the CUs; beyond, the 128x128 tile's finer grain fills the last round better.
-  const int64_t pair_items = (int64_t)((M + 127) / 128) * ((tokens + 255) / 256);
-  return pair_items <= 2 * (int64_t)cus ? 5 : 6;
+  // The pair-shared 256x128 tile (one workgroup per CU) when its workgroups, K splits included,
+  // make one round of the CUs at least three quarters full; otherwise the 128x128 tile, whose
+  // finer grain fills sparse grids and the last of several rounds better.
+  const int64_t items = (int64_t)((M + 127) / 128) * ((tokens + 255) / 256);
+  if (items > (int64_t)cus) return 6;
+  const int CG = (K + kTileK - 1) / kTileK;
+  int64_t ks = std::max<int64_t>(1, cus / items);
+  ks = std::min<int64_t>(ks, std::max(1, CG / 8));
+  ks = std::min(ks, std::max<int64_t>(1, (int64_t(32) << 20) / (tokens * (int64_t)((M + 15) / 16 * 16) * 4)));
+  return 4 * items * ks >= 3 * (int64_t)cus ? 5 : 6;
 }
 
 int prefill_splits(int M, int CG, int64_t tokens, int cus) {
   // Candidate-independent, so that every tile gives the same sums, and sized for the default tile
   // of this shape: as many splits as keep all of its workgroups resident at once, each split at
   // least 8 tile columns long, partials at most 32 MiB.
-  const int dc = prefill_default_candidate(M, tokens, cus);
+  const int dc = prefill_default_candidate(M, CG * kTileK, tokens, cus);
   const Candidate *c = find(dc);
   const int64_t items = ((M + c->bn - 1) / c->bn) * ((tokens + c->bt - 1) / c->bt);
   const int64_t slots = (int64_t)resident_per_cu()[dc - kPrefillFirst] * cus;
