@@ -21,6 +21,8 @@
 //     loads (no registers) one step ahead, in rows of 256 bytes whose 16-byte slots are
 //     XOR-swizzled by row;
 //   * acc[tb][rb] = D[32 rows of block rb][32 tokens of block tb].
+// Candidate 5 (prefill_pair_kernel) is the 8-wave 256-token x 128-row variant in which wave pairs
+// split each step's decode by K half and hand the operands to each other through LDS.
 // Every candidate uses the same MFMA K grouping and order, and the K splits depend only on the
 // shape, so all candidates give bitwise-identical results. With several splits the partial sums
 // are written to the caller's workspace and reduced in split order by a second kernel.
