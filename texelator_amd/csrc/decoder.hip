@@ -9,6 +9,8 @@
 // bf16 [kv_head][position][head_dim].
 #include <math.h>
 
+#include <type_traits>
+
 #include "elementwise.h"
 #include "kernels.h"
 
@@ -16,16 +18,29 @@ namespace tx {
 
 namespace {
 
+// Calls f with std::integral_constant<int, ks> for split counts 1-4 (the kernels' loop-free
+// variants) and with 0 (the generic loop) for more.
+template <typename F>
+void with_split_count(int ks, F &&f) {
+  switch (ks) {
+    case 1: f(std::integral_constant<int, 1>{}); break;
+    case 2: f(std::integral_constant<int, 2>{}); break;
+    case 3: f(std::integral_constant<int, 3>{}); break;
+    case 4: f(std::integral_constant<int, 4>{}); break;
+    default: f(std::integral_constant<int, 0>{}); break;
+  }
+}
+
 // h[row] += delta[row] (if given); out[row] = bf16(weight * bf16(h * rsqrt(mean(h^2) + eps))).
 // One block per row; each thread owns groups of 4 columns (4 * t + 4096 * i), all of whose
 // loads are issued before the reduction. hidden must be a multiple of 4.
 // With SPLIT, delta is the fp32 split-K partials of a decode GEMV: each group's partials are read
-// as float4 per split (all groups of a split in flight together) and summed in split order plus
-// the bias, exactly as split_sum does. Both variants reduce in the same order, so their outputs
+// as float4 per split (four splits of every group in flight together; KS > 0 means ks == KS, read
+// without a loop) and summed in split order plus the bias, exactly as split_sum does. Both variants reduce in the same order, so their outputs
 // are bit-identical; a row gets 1024 threads (a decode step has a single row).
 constexpr int kNormThreads = 1024;
 
-template <bool SPLIT>
+template <bool SPLIT, int KS>
 __global__ __launch_bounds__(kNormThreads) void add_rmsnorm_kernel(float *h, const uint16_t *delta, SplitSource split,
                                                                    const uint16_t *weight, float eps, uint16_t *out,
                                                                    int hidden) {
@@ -54,29 +69,63 @@ __global__ __launch_bounds__(kNormThreads) void add_rmsnorm_kernel(float *h, con
       if (one_pass) wv[u] = wr[i];
     }
     if constexpr (SPLIT) {
+      // The bias (from a valid address whether or not there is one) and four splits of partials
+      // go out before the first add; with KS (ks == KS) there is no loop, select or branch.
       const float4 *pp = reinterpret_cast<const float4 *>(split.partials + (size_t)blockIdx.x * split.Mp);
       const size_t step = (size_t)split.tokens * split.Mp / 4;
+      const uint2 *bp = reinterpret_cast<const uint2 *>(split.bias ? split.bias : reinterpret_cast<const uint16_t *>(split.partials));
+      int col[kUnroll];
+      uint2 b[kUnroll];
       float4 acc[kUnroll];
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) acc[u] = pp[min(base + u * kThreads + (int)threadIdx.x, groups - 1)];
-      for (int k = 1; k < split.ks; ++k) {
+      for (int u = 0; u < kUnroll; ++u) {
+        col[u] = min(base + u * kThreads + (int)threadIdx.x, groups - 1);
+        b[u] = bp[col[u]];
+      }
+      if constexpr (KS > 0) {
+        float4 q[KS][kUnroll];
+#pragma unroll
+        for (int k = 0; k < KS; ++k)
+#pragma unroll
+          for (int u = 0; u < kUnroll; ++u) q[k][u] = pp[(size_t)k * step + col[u]];
+        __builtin_amdgcn_sched_barrier(0);  // every load issued before the first add
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
-          const float4 q = pp[k * step + min(base + u * kThreads + (int)threadIdx.x, groups - 1)];
-          acc[u].x += q.x;
-          acc[u].y += q.y;
-          acc[u].z += q.z;
-          acc[u].w += q.w;
+          acc[u] = q[0][u];
+#pragma unroll
+          for (int k = 1; k < KS; ++k) {
+            acc[u].x += q[k][u].x;
+            acc[u].y += q[k][u].y;
+            acc[u].z += q[k][u].z;
+            acc[u].w += q[k][u].w;
+          }
+        }
+      } else {
+        constexpr int kGroup = 4;
+        for (int k0 = 0; k0 < split.ks; k0 += kGroup) {
+          float4 q[kGroup][kUnroll];
+#pragma unroll
+          for (int g = 0; g < kGroup; ++g)
+#pragma unroll
+            for (int u = 0; u < kUnroll; ++u) q[g][u] = pp[(size_t)min(k0 + g, split.ks - 1) * step + col[u]];
+#pragma unroll
+          for (int g = 0; g < kGroup; ++g) {
+            const int k = k0 + g;
+#pragma unroll
+            for (int u = 0; u < kUnroll; ++u) {
+              const float4 a = acc[u], x = q[g][u];
+              acc[u] = k == 0 ? x : (k < split.ks ? make_float4(a.x + x.x, a.y + x.y, a.z + x.z, a.w + x.w) : a);
+            }
+          }
         }
       }
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) {
         if (split.bias) {
-          const uint2 b = reinterpret_cast<const uint2 *>(split.bias)[min(base + u * kThreads + (int)threadIdx.x, groups - 1)];
-          acc[u].x += bf((uint16_t)(b.x & 0xFFFFu));
-          acc[u].y += bf((uint16_t)(b.x >> 16));
-          acc[u].z += bf((uint16_t)(b.y & 0xFFFFu));
-          acc[u].w += bf((uint16_t)(b.y >> 16));
+          acc[u].x += bf((uint16_t)(b[u].x & 0xFFFFu));
+          acc[u].y += bf((uint16_t)(b[u].x >> 16));
+          acc[u].z += bf((uint16_t)(b[u].y & 0xFFFFu));
+          acc[u].w += bf((uint16_t)(b[u].y >> 16));
         }
         d[u].x = (uint32_t)to_bf(acc[u].x) | ((uint32_t)to_bf(acc[u].y) << 16);
         d[u].y = (uint32_t)to_bf(acc[u].z) | ((uint32_t)to_bf(acc[u].w) << 16);
@@ -161,6 +210,9 @@ constexpr int kRowU4 = kHeadDim * 2 / 16;  // uint4 per cached key or value row 
 // LDS row stride of the key tile in uint4: one uint4 of padding, so the 16 keys a wave scores at
 // once (256 bytes apart unpadded) fall into different LDS banks.
 constexpr int kKeyStrideU4 = kRowU4 + 1;
+// 16 bytes as a native vector (a uint4 struct copy goes through private memory when it is
+// held across the kernel's other loads)
+typedef uint32_t dwordx4 __attribute__((ext_vector_type(4)));
 
 // Split-length decode attention for one query token. Block (kv, chunk) loads the chunk's keys and
 // values (those <= position) into LDS in one burst, scores the group's query heads against them
@@ -170,6 +222,8 @@ constexpr int kKeyStrideU4 = kRowU4 + 1;
 // (summed, rounded and rotated exactly as rope_cache_kernel<true> does, with the RoPE table rows
 // of the position gathered by the caller, so no load waits for the position); the block whose
 // chunk holds the position writes the key and value into the caches and into its own tiles.
+// Every load of a block (chunk rows, partials, RoPE row, position) goes out before the first wait:
+// the kernel's time is one memory latency plus the arithmetic, not a chain of latencies.
 // (Merging the chunks in the same launch -- each block publishing its partials behind a device
 // fence and the last one to take a ticket merging -- measured slower on MI355X: every such fence
 // writes back the XCD's L2, 64 times per XCD and layer at 4096 positions.)
@@ -181,7 +235,8 @@ struct AttnInput {
   int heads, kv_heads;
 };
 
-template <bool ROPE>
+// KS > 0 (with ROPE): the qkv GEMV has exactly KS splits, read without a loop.
+template <bool ROPE, int KS>
 __global__ __launch_bounds__(256) void decode_attention_kernel(AttnInput in, uint16_t *k_cache, uint16_t *v_cache,
                                                                const int64_t *position, int group, int64_t max_ctx,
                                                                float scale, int chunks, float *partials) {
@@ -195,53 +250,86 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(AttnInput in, uin
   const int tid = threadIdx.x;
   const int j0 = chunk * kChunk;
   float *out = partials + ((size_t)kv * chunks + chunk) * group * (kHeadDim + 2);
+  const int64_t pos = *position;
   // Issue the chunk's K/V rows (clamped into the cache) and q before the position arrives:
   // nothing waits for a load whose result only masks.
-  const uint4 *kg = reinterpret_cast<const uint4 *>(k_cache + (size_t)kv * max_ctx * kHeadDim);
-  const uint4 *vg = reinterpret_cast<const uint4 *>(v_cache + (size_t)kv * max_ctx * kHeadDim);
-  uint4 kr[4], vr[4];
+  // (32-bit byte offsets from the head's base: a head's cache is well under 4 GiB)
+  const char *kg = reinterpret_cast<const char *>(k_cache + (size_t)kv * max_ctx * kHeadDim);
+  const char *vg = reinterpret_cast<const char *>(v_cache + (size_t)kv * max_ctx * kHeadDim);
+  dwordx4 kr[4], vr[4];
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
     const int idx = u * 256 + tid;
-    const int64_t row = min((int64_t)(j0 + idx / kRowU4), max_ctx - 1);
-    kr[u] = kg[row * kRowU4 + idx % kRowU4];
-    vr[u] = vg[row * kRowU4 + idx % kRowU4];
+    const uint32_t row = (uint32_t)min((int64_t)(j0 + idx / kRowU4), max_ctx - 1);
+    const uint32_t off = (row * kRowU4 + idx % kRowU4) * 16u;
+    kr[u] = *reinterpret_cast<const dwordx4 *>(kg + off);
+    vr[u] = *reinterpret_cast<const dwordx4 *>(vg + off);
   }
+  __builtin_amdgcn_sched_barrier(0);  // the tile loads go out first, all eight of them
   constexpr int kHalf = kHeadDim / 2;
   // Without ROPE: q element u * 256 + tid of the group. With ROPE: the rotate-half pair
-  // (j, j + 64) of head g for p = u * 256 + tid = 64 g + j, as the unrotated sums x1, x2.
-  float qv[kMaxGroup * kHeadDim / 256], qw[kMaxGroup * kHeadDim / 256];
+  // (j, j + 64) of head g for p = u * 256 + tid = 64 g + j (u < 2 covers 8 heads), as the
+  // unrotated sums x1, x2, and the new token's key pair (j, j + 64) (tid < 64) or value element
+  // tid - 64 (tid < 192). Every block loads the new token's partials and the RoPE row with the
+  // rest, so no load waits for the position or for another load.
+  constexpr int kQ = ROPE ? 2 : kMaxGroup * kHeadDim / 256;
+  float qv[kQ], qw[kQ], nk[2] = {0.f, 0.f};
+  float c1 = 0.f, c2 = 0.f, s1 = 0.f, s2 = 0.f;
+  if constexpr (ROPE) {
+    const int j = tid % kHalf;
+    int64_t cols[2 * kQ + 2];
 #pragma unroll
-  for (int u = 0; u < kMaxGroup * kHeadDim / 256; ++u) {
-    const int i = u * 256 + tid;
-    if constexpr (ROPE) {
-      const int g = i / kHalf, j = i % kHalf;
-      const int64_t col = (int64_t)(kv * group + g) * kHeadDim + j;
-      qv[u] = i < group * kHalf ? split_value(in.split, 0, col) : 0.f;
-      qw[u] = i < group * kHalf ? split_value(in.split, 0, col + kHalf) : 0.f;
-    } else {
+    for (int u = 0; u < kQ; ++u) {
+      const int i = u * 256 + tid;
+      const int64_t col = i < group * kHalf ? (int64_t)(kv * group + i / kHalf) * kHeadDim + j : 0;
+      cols[2 * u] = col;
+      cols[2 * u + 1] = col + kHalf;
+    }
+    const int64_t kcol = (int64_t)(in.heads + kv) * kHeadDim + j;
+    const int64_t vcol = (int64_t)(in.heads + in.kv_heads + kv) * kHeadDim + min(max(tid - kHalf, 0), kHeadDim - 1);
+    cols[2 * kQ] = tid < kHalf ? kcol : vcol;
+    cols[2 * kQ + 1] = kcol + kHalf;
+    c1 = in.rope_row[j];
+    c2 = in.rope_row[j + kHalf];
+    s1 = in.rope_row[kHeadDim + j];
+    s2 = in.rope_row[kHeadDim + j + kHalf];
+    float sums[2 * kQ + 2];
+    split_sums<2 * kQ + 2, false, KS>(in.split, 0, cols, sums);
+#pragma unroll
+    for (int u = 0; u < kQ; ++u) {
+      qv[u] = bf(to_bf(sums[2 * u]));
+      qw[u] = bf(to_bf(sums[2 * u + 1]));
+    }
+    nk[0] = bf(to_bf(sums[2 * kQ]));
+    nk[1] = bf(to_bf(sums[2 * kQ + 1]));
+  } else {
+#pragma unroll
+    for (int u = 0; u < kQ; ++u) {
+      const int i = u * 256 + tid;
       qv[u] = i < group * kHeadDim ? bf(in.q[(size_t)kv * group * kHeadDim + i]) : 0.f;
     }
   }
-  const int64_t pos = *position;
-  const bool active = j0 <= pos;
+  // The tiles, in every block and without a branch, so the compiler keeps the tile loads where
+  // they were issued: keys as loaded, values zeroed past the position.
+  const int count = (int)min((int64_t)kChunk, max(pos - j0 + 1, (int64_t)0));  // valid keys in this chunk
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int idx = u * 256 + tid;
+    reinterpret_cast<dwordx4 *>(ks)[(idx / kRowU4) * kKeyStrideU4 + idx % kRowU4] = kr[u];
+    reinterpret_cast<dwordx4 *>(vs)[idx] = idx / kRowU4 < count ? vr[u] : dwordx4{0, 0, 0, 0};
+  }
+  const bool active = count > 0;
   if (active) {
-    const int count = (int)min((int64_t)kChunk, pos - j0 + 1);  // valid keys in this chunk
+    // With ROPE the chunk that holds the position takes that row from the partials, not from the
+    // cache (which this block writes).
+    const int fresh = ROPE && pos - j0 < kChunk ? (int)(pos - j0) : -1;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int idx = u * 256 + tid;
-      ks[(idx / kRowU4) * kKeyStrideU4 + idx % kRowU4] = kr[u];
-      vs[idx] = idx / kRowU4 < count ? vr[u] : make_uint4(0, 0, 0, 0);  // rows past the position: zero
-    }
-#pragma unroll
-    for (int u = 0; u < kMaxGroup * kHeadDim / 256; ++u) {
+    for (int u = 0; u < kQ; ++u) {
       const int i = u * 256 + tid;
       if constexpr (ROPE) {
         if (i < group * kHalf) {
           const int g = i / kHalf, j = i % kHalf;
           const float x1 = qv[u], x2 = qw[u];
-          const float c1 = in.rope_row[j], c2 = in.rope_row[j + kHalf];
-          const float s1 = in.rope_row[kHeadDim + j], s2 = in.rope_row[kHeadDim + j + kHalf];
           qs[g][j] = bf(to_bf(x1 * c1 - x2 * s1));
           qs[g][j + kHalf] = bf(to_bf(x2 * c2 + x1 * s2));
         }
@@ -249,18 +337,14 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(AttnInput in, uin
         if (i < group * kHeadDim) qs[i / kHeadDim][i % kHeadDim] = qv[u];
       }
     }
-    __syncthreads();
-    if (ROPE && pos - j0 < kChunk) {
+    if (fresh >= 0) {
       // This chunk holds the new token: rotate its key, take its value, write both to the caches
-      // and over the (not yet written) row of the tiles.
-      const int r = (int)(pos - j0);
-      uint16_t *krow = reinterpret_cast<uint16_t *>(ks + r * kKeyStrideU4);
-      uint16_t *vrow = reinterpret_cast<uint16_t *>(vs + r * kRowU4);
+      // and over the tiles' row of the position (after the barrier that orders the tile stores).
+      __syncthreads();
+      uint16_t *krow = reinterpret_cast<uint16_t *>(ks + fresh * kKeyStrideU4);
+      uint16_t *vrow = reinterpret_cast<uint16_t *>(vs + fresh * kRowU4);
       if (tid < kHalf) {
-        const int64_t col = (int64_t)(in.heads + kv) * kHeadDim + tid;
-        const float x1 = split_value(in.split, 0, col), x2 = split_value(in.split, 0, col + kHalf);
-        const float c1 = in.rope_row[tid], c2 = in.rope_row[tid + kHalf];
-        const float s1 = in.rope_row[kHeadDim + tid], s2 = in.rope_row[kHeadDim + tid + kHalf];
+        const float x1 = nk[0], x2 = nk[1];
         const uint16_t o1 = to_bf(x1 * c1 - x2 * s1), o2 = to_bf(x2 * c2 + x1 * s2);
         uint16_t *dst = k_cache + ((size_t)kv * max_ctx + pos) * kHeadDim;
         dst[tid] = o1;
@@ -269,12 +353,12 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(AttnInput in, uin
         krow[tid + kHalf] = o2;
       } else if (tid < kHalf + kHeadDim) {
         const int e = tid - kHalf;
-        const uint16_t v = to_bf(split_value(in.split, 0, (int64_t)(in.heads + in.kv_heads + kv) * kHeadDim + e));
+        const uint16_t v = to_bf(nk[0]);
         v_cache[((size_t)kv * max_ctx + pos) * kHeadDim + e] = v;
         vrow[e] = v;
       }
-      __syncthreads();
     }
+    __syncthreads();
 
     // scores: four threads per key, 32 dimensions each
     {
@@ -375,50 +459,75 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(AttnInput in, uin
   }
 }
 
-// Merge the chunks of one query head (block = head, thread = dimension) into bf16 output:
-// all chunk statistics are loaded in parallel, then every thread sums its dimension over chunks.
+// Merge the chunks of one query head (block = head, thread = dimension) into bf16 output.
+// The loads of the common case go out at once -- this thread's chunk statistics and its
+// dimension's output of the first kHeld chunks (4096 positions) -- so the merge waits for memory
+// once; chunks past kHeld are read eight at a time. The sums run over the chunks in the same
+// order either way: acc[c % 4] for the chunks below the last multiple of four, the rest into
+// acc[0], then ((acc0 + acc1) + (acc2 + acc3)) / total.
 constexpr int kMaxChunks = 1024;
 __global__ __launch_bounds__(128) void decode_attention_combine_kernel(const float *partials, int group, int chunks,
                                                                        uint16_t *out) {
+  constexpr int kHeld = 64;
+  constexpr int kPerThread = kMaxChunks / 128;
   __shared__ float weight[kMaxChunks];
   __shared__ float red[2];
   const int head = blockIdx.x;
   const int kv = head / group, g = head % group;
   const int dd = threadIdx.x;
   const float *base = partials + ((size_t)kv * chunks * group + g) * (kHeadDim + 2);
-  const size_t step = (size_t)group * (kHeadDim + 2);
-  float m = -INFINITY;
-  for (int c = dd; c < chunks; c += 128) {
-    weight[c] = base[c * step + kHeadDim];
-    m = fmaxf(m, weight[c]);
-  }
+  const uint32_t step = (uint32_t)group * (kHeadDim + 2);  // floats between chunks
+  auto at = [&](int c, int e) { return base[(uint32_t)min(c, chunks - 1) * step + e]; };
+  float o[kHeld];
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+  for (int i = 0; i < kHeld; ++i) o[i] = at(i, dd);
+  float mv[kPerThread], lv[kPerThread];
+#pragma unroll
+  for (int u = 0; u < kPerThread; ++u) {
+    mv[u] = at(dd + 128 * u, kHeadDim);
+    lv[u] = at(dd + 128 * u, kHeadDim + 1);
+  }
+  float m = -INFINITY;
+#pragma unroll
+  for (int u = 0; u < kPerThread; ++u) m = dd + 128 * u < chunks ? fmaxf(m, mv[u]) : m;
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
   if ((dd & 63) == 0) red[dd >> 6] = m;
   __syncthreads();
   m = fmaxf(red[0], red[1]);
   __syncthreads();
   float total = 0.f;
-  for (int c = dd; c < chunks; c += 128) {
-    const float w = weight[c] == -INFINITY ? 0.f : expf(weight[c] - m);
-    weight[c] = w;
-    total = __builtin_fmaf(base[c * step + kHeadDim + 1], w, total);
+#pragma unroll
+  for (int u = 0; u < kPerThread; ++u) {
+    const int c = dd + 128 * u;
+    if (c < chunks) {
+      const float w = mv[u] == -INFINITY ? 0.f : expf(mv[u] - m);
+      weight[c] = w;
+      total = __builtin_fmaf(lv[u], w, total);
+    }
   }
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) total += __shfl_xor(total, o);
+  for (int off = 32; off > 0; off >>= 1) total += __shfl_xor(total, off);
   if ((dd & 63) == 0) red[dd >> 6] = total;
   __syncthreads();
   total = red[0] + red[1];
-  float acc0 = 0.f, acc1 = 0.f, acc2 = 0.f, acc3 = 0.f;
-  int c = 0;
-  for (; c + 4 <= chunks; c += 4) {
-    acc0 = __builtin_fmaf(base[c * step + dd], weight[c], acc0);
-    acc1 = __builtin_fmaf(base[(c + 1) * step + dd], weight[c + 1], acc1);
-    acc2 = __builtin_fmaf(base[(c + 2) * step + dd], weight[c + 2], acc2);
-    acc3 = __builtin_fmaf(base[(c + 3) * step + dd], weight[c + 3], acc3);
+  const int main_end = chunks & ~3;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  auto add = [&](int c, float v) {
+    const float w = weight[min(c, chunks - 1)];
+    if (c < main_end) acc[c & 3] = __builtin_fmaf(v, w, acc[c & 3]);
+    else if (c < chunks) acc[0] = __builtin_fmaf(v, w, acc[0]);
+  };
+#pragma unroll
+  for (int i = 0; i < kHeld; ++i) add(i, o[i]);
+  for (int c0 = kHeld; c0 < chunks; c0 += 8) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = at(c0 + u, dd);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) add(c0 + u, v[u]);
   }
-  for (; c < chunks; ++c) acc0 = __builtin_fmaf(base[c * step + dd], weight[c], acc0);
-  out[(size_t)head * kHeadDim + dd] = to_bf(((acc0 + acc1) + (acc2 + acc3)) / total);
+  out[(size_t)head * kHeadDim + dd] = to_bf(((acc[0] + acc[1]) + (acc[2] + acc[3])) / total);
 }
 
 // out[r][c] = bf16(silu(g) * u) with g = gu[r][c], u = gu[r][inter + c], in fp32.
@@ -436,15 +545,18 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const uint16_t *gu, int64_t
 
 hipError_t launch_add_rmsnorm(float *h, const uint16_t *delta, const uint16_t *weight, float eps, uint16_t *out,
                               int64_t rows, int hidden, hipStream_t stream) {
-  hipLaunchKernelGGL(add_rmsnorm_kernel<false>, dim3((unsigned)rows), dim3(kNormThreads), 0, stream, h, delta, SplitSource{},
+  hipLaunchKernelGGL((add_rmsnorm_kernel<false, 0>), dim3((unsigned)rows), dim3(kNormThreads), 0, stream, h, delta, SplitSource{},
                      weight, eps, out, hidden);
   return hipGetLastError();
 }
 
 hipError_t launch_add_rmsnorm_split(float *h, const SplitSource &delta, const uint16_t *weight, float eps, uint16_t *out,
                                     int64_t rows, int hidden, hipStream_t stream) {
-  hipLaunchKernelGGL(add_rmsnorm_kernel<true>, dim3((unsigned)rows), dim3(kNormThreads), 0, stream, h, nullptr, delta, weight,
-                     eps, out, hidden);
+  auto launch = [&](auto ks) {
+    hipLaunchKernelGGL((add_rmsnorm_kernel<true, decltype(ks)::value>), dim3((unsigned)rows), dim3(kNormThreads), 0, stream,
+                       h, nullptr, delta, weight, eps, out, hidden);
+  };
+  with_split_count(delta.ks, launch);
   return hipGetLastError();
 }
 
@@ -483,8 +595,12 @@ hipError_t launch_attention(const AttnInput &in, uint16_t *k_cache, uint16_t *v_
                             hipStream_t stream) {
   const int chunks = decode_attention_chunks(length);
   const int group = in.heads / in.kv_heads;
-  hipLaunchKernelGGL((decode_attention_kernel<ROPE>), dim3(in.kv_heads, chunks), dim3(256), 0, stream, in, k_cache,
-                     v_cache, position, group, max_ctx, scale, chunks, partials);
+  auto launch = [&](auto ks) {
+    hipLaunchKernelGGL((decode_attention_kernel<ROPE, decltype(ks)::value>), dim3(in.kv_heads, chunks), dim3(256), 0,
+                       stream, in, k_cache, v_cache, position, group, max_ctx, scale, chunks, partials);
+  };
+  if constexpr (ROPE) with_split_count(in.split.ks, launch);
+  else launch(std::integral_constant<int, 0>{});
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(decode_attention_combine_kernel, dim3(in.heads), dim3(kHeadDim), 0, stream, partials, group, chunks, out);

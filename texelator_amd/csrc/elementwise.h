@@ -47,14 +47,67 @@ struct SplitSource {
   int ks, Mp, tokens;
 };
 
+// split_sum for N columns m[i] of one token at once. The loads go out four splits at a time for
+// every column (split index clamped to the last one, extra values unused) before the first add,
+// so a consumer pays the memory latency once per four splits instead of once per split and
+// column. The bias is read from a valid address whether or not there is one, and added last.
+// KS > 0: the caller guarantees ks == KS, and the code has no loop, select or branch at all, so
+// the compiler keeps the caller's own earlier loads where they were issued.
+template <int N, bool F16 = false, int KS = 0>
+__device__ __forceinline__ void split_sums(const SplitSource &s, int64_t token, const int64_t (&m)[N], float (&total)[N]) {
+  const float *p = s.partials + (size_t)token * s.Mp;
+  const size_t stride = (size_t)s.tokens * s.Mp;
+  const uint16_t *bias = s.bias ? s.bias : reinterpret_cast<const uint16_t *>(s.partials);
+  // 32-bit byte offsets from a uniform base (columns < 2^30), so each load needs one VGPR of
+  // address instead of two
+  uint32_t off4[N];
+  uint16_t b[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    off4[i] = (uint32_t)m[i] * 4u;
+    b[i] = *reinterpret_cast<const uint16_t *>(reinterpret_cast<const char *>(bias) + off4[i] / 2u);
+    total[i] = 0.f;
+  }
+  auto load = [&](int k, int i) { return *reinterpret_cast<const float *>(reinterpret_cast<const char *>(p + (size_t)k * stride) + off4[i]); };
+  if constexpr (KS > 0) {
+    float v[KS][N];
+#pragma unroll
+    for (int k = 0; k < KS; ++k)
+#pragma unroll
+      for (int i = 0; i < N; ++i) v[k][i] = load(k, i);
+    __builtin_amdgcn_sched_barrier(0);  // every load issued before the first add
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      total[i] = v[0][i];
+#pragma unroll
+      for (int k = 1; k < KS; ++k) total[i] += v[k][i];
+    }
+  } else {
+    constexpr int kGroup = 4;
+    for (int k0 = 0; k0 < s.ks; k0 += kGroup) {
+      float v[kGroup][N];
+#pragma unroll
+      for (int u = 0; u < kGroup; ++u)
+#pragma unroll
+        for (int i = 0; i < N; ++i) v[u][i] = load(min(k0 + u, s.ks - 1), i);
+#pragma unroll
+      for (int u = 0; u < kGroup; ++u) {
+        const int k = k0 + u;
+#pragma unroll
+        for (int i = 0; i < N; ++i) total[i] = k == 0 ? v[u][i] : (k < s.ks ? total[i] + v[u][i] : total[i]);
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < N; ++i) total[i] = s.bias ? total[i] + half_bits_to_float<F16>(b[i]) : total[i];
+}
+
 template <bool F16 = false>
 __device__ __forceinline__ float split_sum(const SplitSource &s, int64_t token, int64_t m) {
-  const float *p = s.partials + (size_t)token * s.Mp + m;
-  const size_t stride = (size_t)s.tokens * s.Mp;
-  float total = p[0];
-  for (int k = 1; k < s.ks; ++k) total += p[k * stride];
-  if (s.bias) total += half_bits_to_float<F16>(s.bias[m]);
-  return total;
+  const int64_t cols[1] = {m};
+  float total[1];
+  split_sums<1, F16>(s, token, cols, total);
+  return total[0];
 }
 
 __device__ __forceinline__ float split_value(const SplitSource &s, int64_t token, int64_t m) {
