@@ -93,8 +93,9 @@ void repack_rows(const uint8_t *blocks, const Handle &h, uint32_t *out, int g_be
 }
 
 // K splits of the single-token GEMV. Tall matrices (>= 1024 row groups) fill the chip without
-// splitting; shorter ones split K so that there are about six workgroups per CU, each covering at
-// least 4 tile columns. A split never covers more tile columns than the LDS x slice holds.
+// splitting; shorter ones split K so that there are about TX_GEMV_SPLIT_TARGET workgroups per CU
+// (TX_GEMV_SPLIT_TARGET_SHORT_K where K is at most 64 tile columns), each covering at least 4
+// tile columns. A split never covers more tile columns than the LDS x slice holds.
 int device_cus(int device) {
   hipDeviceProp_t prop;
   if (hipGetDeviceProperties(&prop, device) == hipSuccess && prop.multiProcessorCount > 0) return prop.multiProcessorCount;
@@ -105,11 +106,15 @@ int device_cus(int device) {
 #ifndef TX_GEMV_SPLIT_TARGET
 #define TX_GEMV_SPLIT_TARGET 4
 #endif
+#ifndef TX_GEMV_SPLIT_TARGET_SHORT_K
+#define TX_GEMV_SPLIT_TARGET_SHORT_K TX_GEMV_SPLIT_TARGET
+#endif
 
 int choose_splits(int RG, int CG, int cus) {
   int ks = 1;
   if (RG < 1024) {
-    ks = (TX_GEMV_SPLIT_TARGET * cus + RG - 1) / RG;
+    const int target = CG <= 64 ? TX_GEMV_SPLIT_TARGET_SHORT_K : TX_GEMV_SPLIT_TARGET;
+    ks = (target * cus + RG - 1) / RG;
     ks = std::min(ks, std::max(1, CG / 4));
   }
   ks = std::max(ks, (CG + tx::kGemvMaxLdsColumns - 1) / tx::kGemvMaxLdsColumns);
