@@ -213,11 +213,30 @@ constexpr int kKeyStrideU4 = kRowU4 + 1;
 // 16 bytes as a native vector (a uint4 struct copy goes through private memory when it is
 // held across the kernel's other loads)
 typedef uint32_t dwordx4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+constexpr int kPRow = kChunk + 8;  // bf16 per row of the probability operands (144 bytes: no conflicts)
+
+// D += A * B on a 16x16x32 bf16 tile: lane l holds A row l % 16 and B column l % 16, each with
+// k = 8 (l / 16) .. + 7; D column l % 16, rows 4 (l / 16) .. + 3.
+__device__ __forceinline__ f32x4_t mfma_bf16(dwordx4 a, dwordx4 b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+
+// bf16 index of value (dimension d, key) in the transposed value tile [128][64]: each row is
+// eight 16-byte slots of 8 keys, slot (key / 8) stored at (key / 8) ^ ((d + d / 8) % 8), so that
+// the PV operand reads (8 keys of 16 dimensions) and the transposing writes (16 dimensions of
+// one key) spread over the LDS banks.
+__device__ __forceinline__ int vt_index(int d, int key) {
+  return d * kChunk + 8 * ((key >> 3) ^ ((d + (d >> 3)) & 7)) + (key & 7);
+}
 
 // Split-length decode attention for one query token. Block (kv, chunk) loads the chunk's keys and
-// values (those <= position) into LDS in one burst, scores the group's query heads against them
-// in fp32, and writes the chunk's max m, sum of exp l and unnormalised output o to
-// partials[kv][chunk][g][130].
+// values (those <= position) into LDS in one burst (values transposed), scores the group's query
+// heads against them on the matrix cores (bf16 q and keys, exact products, fp32 sums), takes the
+// softmax statistics in fp32, multiplies the probabilities (as bf16 hi + lo, 16 significant
+// bits) by the values on the matrix cores, and writes the chunk's max m, sum of exp l and
+// unnormalised output o to partials[kv][chunk][g][130].
 // ROPE: q and the new token's key and value come from the qkv decode GEMV's split-K partials
 // (summed, rounded and rotated exactly as rope_cache_kernel<true> does, with the RoPE table rows
 // of the position gathered by the caller, so no load waits for the position); the block whose
@@ -240,10 +259,11 @@ template <bool ROPE, int KS>
 __global__ __launch_bounds__(256) void decode_attention_kernel(AttnInput in, uint16_t *k_cache, uint16_t *v_cache,
                                                                const int64_t *position, int group, int64_t max_ctx,
                                                                float scale, int chunks, float *partials) {
-  __shared__ uint4 ks[kChunk * kKeyStrideU4];
-  __shared__ uint4 vs[kChunk * kRowU4];
-  __shared__ float qs[kMaxGroup][kHeadDim];
-  __shared__ float probs[kMaxGroup][kChunk];
+  __shared__ uint4 ks[kChunk * kKeyStrideU4];       // keys [key][128] bf16, padded rows
+  __shared__ __align__(16) uint16_t vt[kHeadDim * kChunk];     // values [dim][key] bf16 (vt_index)
+  __shared__ uint4 qs[16 * kKeyStrideU4];             // q [head][128] bf16, padded rows, heads >= group zero
+  __shared__ float probs[kMaxGroup][kChunk];          // scores, then probabilities (fp32)
+  __shared__ __align__(16) uint16_t pb[2][16][kPRow];          // probabilities as bf16 hi + lo, heads >= group zero
   __shared__ float stats[kMaxGroup][2];
   const int kv = blockIdx.x;
   const int chunk = blockIdx.y;
@@ -315,14 +335,19 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(AttnInput in, uin
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
     const int idx = u * 256 + tid;
-    reinterpret_cast<dwordx4 *>(ks)[(idx / kRowU4) * kKeyStrideU4 + idx % kRowU4] = kr[u];
-    reinterpret_cast<dwordx4 *>(vs)[idx] = idx / kRowU4 < count ? vr[u] : dwordx4{0, 0, 0, 0};
+    const int key = idx / kRowU4, c = idx % kRowU4;
+    reinterpret_cast<dwordx4 *>(ks)[key * kKeyStrideU4 + c] = kr[u];
+    const dwordx4 v = key < count ? vr[u] : dwordx4{0, 0, 0, 0};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) vt[vt_index(8 * c + e, key)] = (uint16_t)(v[e / 2] >> (16 * (e & 1)));
   }
   const bool active = count > 0;
   if (active) {
     // With ROPE the chunk that holds the position takes that row from the partials, not from the
     // cache (which this block writes).
     const int fresh = ROPE && pos - j0 < kChunk ? (int)(pos - j0) : -1;
+    uint16_t *qh = reinterpret_cast<uint16_t *>(qs);
+    constexpr int kQRow = kKeyStrideU4 * 8;  // bf16 per padded q row
 #pragma unroll
     for (int u = 0; u < kQ; ++u) {
       const int i = u * 256 + tid;
@@ -330,19 +355,25 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(AttnInput in, uin
         if (i < group * kHalf) {
           const int g = i / kHalf, j = i % kHalf;
           const float x1 = qv[u], x2 = qw[u];
-          qs[g][j] = bf(to_bf(x1 * c1 - x2 * s1));
-          qs[g][j + kHalf] = bf(to_bf(x2 * c2 + x1 * s2));
+          qh[g * kQRow + j] = to_bf(x1 * c1 - x2 * s1);
+          qh[g * kQRow + j + kHalf] = to_bf(x2 * c2 + x1 * s2);
         }
       } else {
-        if (i < group * kHeadDim) qs[i / kHeadDim][i % kHeadDim] = qv[u];
+        if (i < group * kHeadDim) qh[(i / kHeadDim) * kQRow + i % kHeadDim] = to_bf(qv[u]);
       }
+    }
+    // the MFMA operand rows of heads past the group: zero
+    for (int i = tid; i < (16 - group) * kQRow / 2; i += 256)
+      reinterpret_cast<uint32_t *>(qh + group * kQRow)[i] = 0u;
+    for (int i = tid; i < 2 * (16 - group) * kPRow / 2; i += 256) {
+      const int h = i / (kPRow / 2), r = i % (kPRow / 2);
+      reinterpret_cast<uint32_t *>(&pb[h / (16 - group)][group + h % (16 - group)][0])[r] = 0u;
     }
     if (fresh >= 0) {
       // This chunk holds the new token: rotate its key, take its value, write both to the caches
       // and over the tiles' row of the position (after the barrier that orders the tile stores).
       __syncthreads();
       uint16_t *krow = reinterpret_cast<uint16_t *>(ks + fresh * kKeyStrideU4);
-      uint16_t *vrow = reinterpret_cast<uint16_t *>(vs + fresh * kRowU4);
       if (tid < kHalf) {
         const float x1 = nk[0], x2 = nk[1];
         const uint16_t o1 = to_bf(x1 * c1 - x2 * s1), o2 = to_bf(x2 * c2 + x1 * s2);
@@ -355,103 +386,81 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(AttnInput in, uin
         const int e = tid - kHalf;
         const uint16_t v = to_bf(nk[0]);
         v_cache[((size_t)kv * max_ctx + pos) * kHeadDim + e] = v;
-        vrow[e] = v;
+        vt[vt_index(e, fresh)] = v;
       }
     }
     __syncthreads();
 
-    // scores: four threads per key, 32 dimensions each
+    const int wave = tid >> 6, lane = tid & 63;
+    const int n = lane & 15, q4 = lane >> 4;
+    // scores on the matrix cores: wave w takes keys 16w..16w+15; A = q (16 head rows, zero past
+    // the group), B = the keys, K = the 128 dimensions in four steps. bf16 products are exact in
+    // the fp32 accumulator.
     {
-      const int jl = tid >> 2;
-      const int part = tid & 3;
-      float kf[32];
-      const uint4 *row = ks + jl * kKeyStrideU4 + part * 4;
+      const int key = 16 * wave + n;
+      const uint4 *qrow = qs + n * kKeyStrideU4;
+      const uint4 *krow = ks + key * kKeyStrideU4;
+      f32x4_t sc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const uint4 w = row[v];
-        const uint32_t words[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          kf[v * 8 + 2 * e] = bf((uint16_t)(words[e] & 0xFFFFu));
-          kf[v * 8 + 2 * e + 1] = bf((uint16_t)(words[e] >> 16));
-        }
+      for (int st = 0; st < kHeadDim / 32; ++st) {
+        const uint4 a = qrow[4 * st + q4], b = krow[4 * st + q4];
+        sc = mfma_bf16(dwordx4{a.x, a.y, a.z, a.w}, dwordx4{b.x, b.y, b.z, b.w}, sc);
       }
-      for (int g = 0; g < group; ++g) {
-        const float4 *q4 = reinterpret_cast<const float4 *>(&qs[g][part * 32]);
-        float s = 0.f;
 #pragma unroll
-        for (int e4 = 0; e4 < 8; ++e4) {
-          const float4 qq = q4[e4];
-          s = __builtin_fmaf(qq.x, kf[4 * e4], s);
-          s = __builtin_fmaf(qq.y, kf[4 * e4 + 1], s);
-          s = __builtin_fmaf(qq.z, kf[4 * e4 + 2], s);
-          s = __builtin_fmaf(qq.w, kf[4 * e4 + 3], s);
-        }
-        s += __shfl_xor(s, 1);
-        s += __shfl_xor(s, 2);
-        if (part == 0) probs[g][jl] = jl < count ? s * scale : -INFINITY;
+      for (int r = 0; r < 4; ++r) {
+        const int h = 4 * q4 + r;
+        if (h < group) probs[h][key] = key < count ? sc[r] * scale : -INFINITY;
       }
     }
     __syncthreads();
 
-    // per query head: max, exp, sum (one wave per head, one lane per key)
-    {
-      const int wave = tid >> 6, lane = tid & 63;
-      for (int g = wave; g < group; g += 4) {
-        const float a = probs[g][lane];
-        float m = a;
+    // per query head: max, exp, sum (one wave per head, one lane per key); the probabilities are
+    // kept as bf16 hi + lo (hi + lo = p to 16 significant bits) for the PV product
+    for (int g = wave; g < group; g += 4) {
+      const float a = probs[g][lane];
+      float m = a;
 #pragma unroll
-        for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
-        const float pa = expf(a - m);
-        probs[g][lane] = pa;
-        float l = pa;
+      for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+      const float pa = expf(a - m);
+      const uint16_t hi = to_bf(pa);
+      pb[0][g][lane] = hi;
+      pb[1][g][lane] = to_bf(pa - bf(hi));
+      float l = pa;
 #pragma unroll
-        for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o);
-        if (lane == 0) {
-          stats[g][0] = m;
-          stats[g][1] = l;
-        }
+      for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o);
+      if (lane == 0) {
+        stats[g][0] = m;
+        stats[g][1] = l;
       }
     }
     __syncthreads();
 
-    // o[g][dd] = sum_j p[g][j] v[j][dd]; thread (dd, half of the heads), values from LDS
-    {
-      const int dd = tid & (kHeadDim - 1);
-      const int gg = tid >> 7;
-      float acc[kMaxGroup / 2];
+    // o[g][d] = sum_j p[g][j] v[j][d] on the matrix cores: wave w takes dimensions 32w..32w+31
+    // (two 16-wide tiles); A = p as hi and lo (16 head rows), B = the transposed values, K = the
+    // 64 keys in two steps. Keys past the position have p = 0 and zeroed values.
 #pragma unroll
-      for (int u = 0; u < kMaxGroup / 2; ++u) acc[u] = 0.f;
-      const uint16_t *vcol = reinterpret_cast<const uint16_t *>(vs) + dd;
-      // four keys per pass (probabilities read as float4); keys past the position have p = 0 and
-      // zeroed values, so the padded tail adds exact zeros
-      for (int j = 0; j < count; j += 4) {
-        const float v0 = bf(vcol[j * kHeadDim]), v1 = bf(vcol[(j + 1) * kHeadDim]);
-        const float v2 = bf(vcol[(j + 2) * kHeadDim]), v3 = bf(vcol[(j + 3) * kHeadDim]);
+    for (int t = 0; t < 2; ++t) {
+      const int d = 32 * wave + 16 * t + n;
+      f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int u = 0; u < kMaxGroup / 2; ++u) {
-          const int g = gg + 2 * u;
-          if (g < group) {
-            const float4 p4 = *reinterpret_cast<const float4 *>(&probs[g][j]);
-            acc[u] = __builtin_fmaf(p4.x, v0, acc[u]);
-            acc[u] = __builtin_fmaf(p4.y, v1, acc[u]);
-            acc[u] = __builtin_fmaf(p4.z, v2, acc[u]);
-            acc[u] = __builtin_fmaf(p4.w, v3, acc[u]);
-          }
-        }
+      for (int st = 0; st < kChunk / 32; ++st) {
+        const int k0 = 32 * st + 8 * q4;
+        const uint4 b = *reinterpret_cast<const uint4 *>(&vt[vt_index(d, k0)]);
+        const uint4 ah = *reinterpret_cast<const uint4 *>(&pb[0][n][k0]);
+        const uint4 al = *reinterpret_cast<const uint4 *>(&pb[1][n][k0]);
+        const dwordx4 bv = {b.x, b.y, b.z, b.w};
+        acc = mfma_bf16(dwordx4{ah.x, ah.y, ah.z, ah.w}, bv, acc);
+        acc = mfma_bf16(dwordx4{al.x, al.y, al.z, al.w}, bv, acc);
       }
 #pragma unroll
-      for (int u = 0; u < kMaxGroup / 2; ++u) {
-        const int g = gg + 2 * u;
-        if (g < group) {
-          float *o = out + (size_t)g * (kHeadDim + 2);
-          o[dd] = acc[u];
-          if (dd == 0) {
-            o[kHeadDim] = stats[g][0];
-            o[kHeadDim + 1] = stats[g][1];
-          }
-        }
+      for (int r = 0; r < 4; ++r) {
+        const int h = 4 * q4 + r;
+        if (h < group) out[(size_t)h * (kHeadDim + 2) + d] = acc[r];
       }
+    }
+    if (tid < group) {
+      out[(size_t)tid * (kHeadDim + 2) + kHeadDim] = stats[tid][0];
+      out[(size_t)tid * (kHeadDim + 2) + kHeadDim + 1] = stats[tid][1];
     }
   } else {
     // chunk past the position: an empty partial for the merge kernel
