@@ -210,11 +210,15 @@ def _random_handle(ext, m, k, seed, bias=False):
     return ext.pack_encoded_device(blocks, scales.float(), b)
 
 
-@pytest.mark.parametrize("m,k,bias", [(5120, 5120, False), (5120, 5120, True), (16384, 256, True), (256, 512, False)])
-def test_add_rmsnorm_split_is_bit_identical(ext, m, k, bias):
-    """linear_split + add_rmsnorm_split == linear + add_rmsnorm, bit for bit (k splits 4, 1, 1)."""
+@pytest.mark.parametrize("m,k,bias,ks", [(5120, 5120, False, 4), (5120, 5120, True, 4), (16384, 256, True, 1),
+                                         (256, 512, False, 1), (8192, 1024, True, 2), (3072, 4096, False, 6),
+                                         (2048, 4096, True, 8)])
+def test_add_rmsnorm_split_is_bit_identical(ext, m, k, bias, ks):
+    """linear_split + add_rmsnorm_split == linear + add_rmsnorm, bit for bit, for K split counts
+    that take the kernel's loop-free variants (1, 2, 4) and its generic loop (6, 8)."""
     handle = _random_handle(ext, m, k, seed=m + k, bias=bias)
     try:
+        assert ext.gemv_plan(handle)[0] == ks
         g = torch.Generator(device="cuda").manual_seed(11)
         x = torch.randn(1, k, device="cuda", generator=g).to(torch.bfloat16)
         w = (1 + 0.1 * torch.randn(m, device="cuda", generator=g)).to(torch.bfloat16)
@@ -250,14 +254,18 @@ def test_rope_kv_cache_split_is_bit_identical(ext, heads, kv, k, bias):
         ext.free(handle)
 
 
-@pytest.mark.parametrize("heads,kv,k,bias,position,length", [(40, 8, 5120, True, 517, 1024), (40, 8, 5120, False, 0, 512),
-                                                             (4, 2, 256, False, 63, 512), (4, 2, 256, True, 64, 1024)])
-def test_decode_attention_split_is_bit_identical(ext, heads, kv, k, bias, position, length):
+@pytest.mark.parametrize("heads,kv,k,bias,position,length,ks", [
+    (40, 8, 5120, True, 517, 1024, 3), (40, 8, 5120, False, 0, 512, 3), (4, 2, 256, False, 63, 512, 1),
+    (4, 2, 256, True, 64, 1024, 1), (48, 8, 1024, True, 300, 512, 2), (16, 4, 4096, False, 1000, 1024, 6),
+    (8, 4, 4096, True, 127, 1024, 8)])
+def test_decode_attention_split_is_bit_identical(ext, heads, kv, k, bias, position, length, ks):
     """RoPE + KV write inside the attention kernel == rope_kv_cache_split + decode_attention, bit
-    for bit: output and both caches; repeated on the same workspace."""
+    for bit: output and both caches; repeated on the same workspace. The qkv split counts cover the
+    kernel's loop-free partial reads (1-3) and its generic loop (6, 8)."""
     d, ctx = 128, 1024
     handle = _random_handle(ext, (heads + 2 * kv) * d, k, seed=heads + position, bias=bias)
     try:
+        assert ext.gemv_plan(handle)[0] == ks
         g = torch.Generator(device="cuda").manual_seed(position + 5)
         x = torch.randn(1, k, device="cuda", generator=g).to(torch.bfloat16)
         angles = torch.rand(ctx, d, device="cuda", generator=g) * 6
