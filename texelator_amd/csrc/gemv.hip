@@ -147,6 +147,11 @@ __global__ __launch_bounds__(kThreads, LUT ? 4 : TX_GEMV_WAVES_PER_EU) void gemv
   for (int u = 0; u < LA; ++u)
     ring[u] = load_stream(wave_tiles + (size_t)min(u, max(nt - 1, 0)) * kWaves * 64 + lane);
 
+  const int i = lane & 15;   // weight row within the group; token column of the B operand
+  const int kg = lane >> 4;  // K chunk: blocks 2kg and 2kg+1 of each tile
+  const int row = g * kTileRows + i;
+  const float scale = p.scales[row];  // loaded with the tiles and x, not after the barrier
+
   if constexpr (!LUT) build_palette_tables(tables, threadIdx.x, kThreads);
   if constexpr (!MULTI) {
     for (int idx = threadIdx.x; idx < nc * 16; idx += kThreads) {
@@ -156,10 +161,6 @@ __global__ __launch_bounds__(kThreads, LUT ? 4 : TX_GEMV_WAVES_PER_EU) void gemv
   }
   __syncthreads();
 
-  const int i = lane & 15;   // weight row within the group; token column of the B operand
-  const int kg = lane >> 4;  // K chunk: blocks 2kg and 2kg+1 of each tile
-  const int row = g * kTileRows + i;
-  const float scale = p.scales[row];
   const uint32_t pm = pm_scale_pair<F16>(scale);
   // Multi-token: this lane's token column (duplicates the last token past the end).
   const uint16_t *xrow = x + (size_t)(t0 + min(i, tc - 1)) * p.K;
@@ -294,14 +295,14 @@ __global__ __launch_bounds__(kThreads, LA == 1 ? 6 : (LA == 2 ? 5 : 4)) void gem
     ring_g[u] = load_stream(gate_tiles + off);
     ring_u[u] = load_stream(up_tiles + off);
   }
+  const int i = lane & 15;
+  const int kg = lane >> 4;
+  const float scale_g = p.scales[g * kTileRows + i];  // loaded with the tiles and x
+  const float scale_u = p.scales[(g + half) * kTileRows + i];
   build_palette_tables(tables, threadIdx.x, kThreads);
   for (int idx = threadIdx.x; idx < nc * 16; idx += kThreads) xs[idx] = load_x8(x, idx * 8, p.K);
   __syncthreads();
 
-  const int i = lane & 15;
-  const int kg = lane >> 4;
-  const float scale_g = p.scales[g * kTileRows + i];
-  const float scale_u = p.scales[(g + half) * kTileRows + i];
   const uint32_t pm_g = pm_scale_pair<false>(scale_g);
   const uint32_t pm_u = pm_scale_pair<false>(scale_u);
   f32x4 ga0 = {0.f, 0.f, 0.f, 0.f}, ga1 = ga0, ua0 = ga0, ua1 = ga0;
