@@ -667,15 +667,29 @@ __global__ __launch_bounds__(kPairThreads) void prefill_pair_kernel(PrefillParam
 
 // y[t][m] = round(sum over splits in order of partials[s][t][m]), then the bias with a second
 // rounding (the reference's epilogue order); bf16, or fp16 with F16.
-template <bool F16>
+// KS > 0: exactly KS splits, every partial loaded before the first add (a runtime loop waited
+// for memory once per split); KS = 0: any count.
+template <bool F16, int KS>
 __global__ __launch_bounds__(256) void prefill_reduce_kernel(PrefillParams p) {
   const int m = blockIdx.x * 256 + threadIdx.x;
   const int t = blockIdx.y;
   if (m >= p.M) return;
+  // the bias goes out with the partials (from a valid address whether or not there is one)
+  const uint16_t b = (p.bias ? static_cast<const uint16_t *>(p.bias) : reinterpret_cast<const uint16_t *>(p.partials))[m];
   float total = 0.f;
-  for (int s = 0; s < p.ks; ++s) total += p.partials[((size_t)s * p.tokens + t) * p.Mp + m];
+  const float *src = p.partials + (size_t)t * p.Mp + m;
+  const size_t stride = (size_t)p.tokens * p.Mp;
+  if constexpr (KS > 0) {
+    float v[KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) v[s] = src[s * stride];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) total += v[s];
+  } else {
+    for (int s = 0; s < p.ks; ++s) total += src[s * stride];
+  }
   float out = round_out<F16>(total);
-  if (p.bias) out += half_bits_to_float<F16>(static_cast<const uint16_t *>(p.bias)[m]);
+  if (p.bias) out += half_bits_to_float<F16>(b);
   store_out<F16>(p.y, (size_t)t * p.M + m, out);
 }
 
@@ -689,11 +703,20 @@ struct Candidate {
 };
 
 // The ordered reduction of the split-K partials, after the tile kernel.
+template <bool F16>
+void launch_reduce_as(const PrefillParams &p, hipStream_t stream) {
+  const dim3 grid((p.M + 255) / 256, p.tokens);
+  switch (p.ks) {
+    case 2: hipLaunchKernelGGL((prefill_reduce_kernel<F16, 2>), grid, dim3(256), 0, stream, p); break;
+    case 3: hipLaunchKernelGGL((prefill_reduce_kernel<F16, 3>), grid, dim3(256), 0, stream, p); break;
+    case 4: hipLaunchKernelGGL((prefill_reduce_kernel<F16, 4>), grid, dim3(256), 0, stream, p); break;
+    default: hipLaunchKernelGGL((prefill_reduce_kernel<F16, 0>), grid, dim3(256), 0, stream, p); break;
+  }
+}
+
 hipError_t launch_reduce(const PrefillParams &p, hipStream_t stream) {
-  if (p.f16)
-    hipLaunchKernelGGL(prefill_reduce_kernel<true>, dim3((p.M + 255) / 256, p.tokens), dim3(256), 0, stream, p);
-  else
-    hipLaunchKernelGGL(prefill_reduce_kernel<false>, dim3((p.M + 255) / 256, p.tokens), dim3(256), 0, stream, p);
+  if (p.f16) launch_reduce_as<true>(p, stream);
+  else launch_reduce_as<false>(p, stream);
   return hipGetLastError();
 }
 
