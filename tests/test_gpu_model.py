@@ -172,10 +172,11 @@ def test_rope_kv_cache_kernel(ext, tiny):
 
 @pytest.mark.parametrize("position,length,ctx", [(0, 512, 1024), (100, 512, 1024), (511, 512, 1024), (700, 1024, 1024),
                                                  (1023, 1024, 1024), (33000, 33024, 33024)])
-def test_decode_attention_kernel(ext, position, length, ctx):
-    """Against an fp32 reference, up to 516 chunks; a second call on the same workspace repeats
-    the output."""
-    heads, kv, d = 40, 8, 128
+@pytest.mark.parametrize("heads,kv", [(40, 8), (64, 8), (8, 8)])
+def test_decode_attention_kernel(ext, position, length, ctx, heads, kv):
+    """Against an fp32 reference, up to 516 chunks, at 5, 8 (the most the kernel takes) and 1 query
+    heads per KV head; a second call on the same workspace repeats the output."""
+    d = 128
     g = torch.Generator(device="cuda").manual_seed(position)
     kc = torch.randn(kv, ctx, d, device="cuda", generator=g).to(torch.bfloat16)
     vc = torch.randn(kv, ctx, d, device="cuda", generator=g).to(torch.bfloat16)
