@@ -365,20 +365,36 @@ __global__ __launch_bounds__(kThreads, LA == 1 ? 6 : (LA == 2 ? 5 : 4)) void gem
 }
 
 // y[t][m] = sum over splits s (in order) of partials[s][t][m], then bias and output cast
-// (split_sum, which fused consumers of the partials use as well).
-template <bool F16, bool F32OUT>
+// (split_sums, which fused consumers of the partials use as well). KS > 0: exactly KS splits,
+// all loaded before the first add; KS = 0: any count, four at a time.
+constexpr int kReduceMaxKS = 16;
+template <bool F16, bool F32OUT, int KS>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemvParams p) {
   const int m = blockIdx.x * 256 + threadIdx.x;
   const int token = blockIdx.y;
   if (m >= p.M) return;
   const SplitSource src{p.partials, F32OUT ? nullptr : static_cast<const uint16_t *>(p.bias), p.ks, p.Mp, p.tokens};
-  const float total = split_sum<F16>(src, token, m);
+  const int64_t cols[1] = {m};
+  float sums[1];
+  split_sums<1, F16, KS>(src, token, cols, sums);
+  const float total = sums[0];
   if constexpr (F32OUT) {
     static_cast<float *>(p.y)[(size_t)token * p.M + m] = total;
   } else if constexpr (F16) {
     static_cast<_Float16 *>(p.y)[(size_t)token * p.M + m] = (_Float16)total;
   } else {
     static_cast<__bf16 *>(p.y)[(size_t)token * p.M + m] = (__bf16)total;
+  }
+}
+
+template <bool F16, bool F32OUT, int KS = 1>
+void launch_splitk_reduce(const GemvParams &p, hipStream_t stream) {
+  const dim3 grid((p.M + 255) / 256, p.tokens);
+  if constexpr (KS <= kReduceMaxKS) {
+    if (p.ks == KS) hipLaunchKernelGGL((splitk_reduce_kernel<F16, F32OUT, KS>), grid, dim3(256), 0, stream, p);
+    else launch_splitk_reduce<F16, F32OUT, KS + 1>(p, stream);
+  } else {
+    hipLaunchKernelGGL((splitk_reduce_kernel<F16, F32OUT, 0>), grid, dim3(256), 0, stream, p);
   }
 }
 
@@ -395,7 +411,7 @@ hipError_t launch_variant(const GemvParams &p, hipStream_t stream) {
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || p.ks == 1 || p.force_partials) return e;
-  hipLaunchKernelGGL((splitk_reduce_kernel<F16, F32OUT>), dim3((p.M + 255) / 256, p.tokens), dim3(256), 0, stream, p);
+  launch_splitk_reduce<F16, F32OUT>(p, stream);
   return hipGetLastError();
 }
 
