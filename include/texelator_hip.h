@@ -155,8 +155,10 @@ int tx_rope_kv_cache(const void *qkv, int64_t row_stride, int64_t tokens, const 
 int tx_decode_attention_workspace(int heads, int64_t length, int64_t *bytes);
 
 /* Attention of one query token q [heads][head_dim] over cached keys 0..*position (device int64;
- * keys up to `length`, a static bound) with fp32 scores and softmax; grouped-query (heads /
- * kv_heads query heads per KV head, at most 8); head_dim must be 128. out bf16 [heads][head_dim]. */
+ * keys up to `length`, a static bound): scores from bf16 q and keys with fp32 sums, fp32
+ * softmax, and the probabilities carried to 16 significant bits (bf16 hi + lo) into the fp32 sum
+ * over the values; grouped-query (heads / kv_heads query heads per KV head, at most 8); head_dim
+ * must be 128. out bf16 [heads][head_dim]. */
 int tx_decode_attention(const void *q, const void *k_cache, const void *v_cache, const int64_t *position,
                         int64_t length, int heads, int kv_heads, int head_dim, int64_t max_context, float scale,
                         void *workspace, int64_t workspace_bytes, void *out, void *stream);
