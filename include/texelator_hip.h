@@ -125,7 +125,10 @@ int tx_decode_dense(uint64_t handle, int dtype, uint16_t *out, void *stream);
 /* Kernel resource report for a candidate. Replaces the *_kernel_info functions
  * (texelator_cuda.cu:1514-1536, cutlass_texture_mainloop.cu:251-267). candidate 5..9: prefill
  * tiles; 100 + L: decode GEMV with lookahead L. Writes up to n of
- * [vgprs, static_lds_bytes, private_bytes, max_threads, tile_lds_bytes, tokens_tile, rows_tile, k_tile]. */
+ * [vgprs, static_lds_bytes, private_bytes, max_threads, tile_lds_bytes, tokens_tile, rows_tile, k_tile,
+ *  active_workgroups_per_cu] -- the nine values of the reference's cutlass_*_kernel_info, the last
+ * being its active_blocks occupancy query (cutlass_texture_mainloop.cu:251-267). For the GEMV ids the
+ * LDS and occupancy figures are those of a K = 5120 split (40 tile columns of staged x). */
 int tx_kernel_info(int candidate, int64_t *out, int n);
 
 /* Name of a prefill candidate (5..9) or NULL. */
@@ -145,7 +148,9 @@ int tx_add_rmsnorm(float *residual, const void *delta, const void *weight, float
 
 /* Rotate-half RoPE of the q and k heads of a packed [q | k | v] bf16 row (stride row_stride
  * elements) at positions[t]: q heads to q_out [tokens][heads][head_dim], k heads into k_cache, and
- * v heads copied into v_cache, at row positions[t]. cos/sin tables f32 [max_context][head_dim]. */
+ * v heads copied into v_cache, at row positions[t]. cos/sin tables f32 [max_context][head_dim].
+ * A token whose position lies outside [0, max_context) (device values, checked on the device) writes
+ * nothing, neither q_out nor the caches. */
 int tx_rope_kv_cache(const void *qkv, int64_t row_stride, int64_t tokens, const int64_t *positions,
                      const float *cos_table, const float *sin_table, int heads, int kv_heads, int head_dim,
                      void *q_out, void *k_cache, void *v_cache, int64_t max_context, void *stream);
@@ -167,7 +172,7 @@ int tx_decode_attention(const void *q, const void *k_cache, const void *v_cache,
  * token's key and value are the last tx_linear_split of qkv_handle ([q | k | v] rows), rotated
  * inside the attention kernel with rope_row = the RoPE tables' rows at *position (cos[head_dim]
  * then sin[head_dim], fp32, gathered by the caller once per token); the key and value are
- * written to the caches at *position. Bit-identical to the two calls. No counterpart in the
+ * written to the caches at *position (not when *position >= max_context). Bit-identical to the two calls. No counterpart in the
  * reference (its decoder layers are Hugging Face modules, docs/supported-models.md:3-5). */
 int tx_decode_attention_split(uint64_t qkv_handle, const int64_t *position, const float *rope_row, int64_t length,
                               int heads, int kv_heads, int head_dim, void *k_cache, void *v_cache,

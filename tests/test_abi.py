@@ -44,3 +44,32 @@ def test_errors_without_gpu_are_reported_not_crashing():
     assert lib.tx_free(0) == _lib.TX_ERR_INVALID
     assert lib.tx_candidate_name(5) == b"large_256x128x128"
     assert lib.tx_candidate_name(4) is None
+
+
+def test_kernel_info_wrapper_reads_nine_fields(monkeypatch):
+    """``_hip.kernel_info`` asks the library for the reference's nine fields
+    (``cutlass_texture_mainloop.cu:251-267``: ..., tile M/N/K, active blocks)."""
+    from texelator_amd import _hip, _lib
+
+    requested = []
+
+    class FakeLibrary:
+        def tx_kernel_info(self, candidate, out, n):
+            requested.append((candidate, n))
+            for i in range(n):
+                out[i] = 10 * candidate + i
+            return _lib.TX_OK
+
+    monkeypatch.setattr(_lib, "load", lambda: FakeLibrary())
+    assert _hip.kernel_info(7) == [70 + i for i in range(9)]
+    assert _hip.cutlass_smalln_kernel_info() == [90 + i for i in range(9)]
+    assert requested == [(7, 9), (9, 9)]
+
+
+def test_candidate_names_are_the_tile_table():
+    from texelator_amd import _lib, autotune
+
+    lib = _lib.load()
+    names = [lib.tx_candidate_name(c).decode() for c in range(5, 10)]
+    assert names == list(autotune.CANDIDATES)
+    assert [autotune.CANDIDATES[n] for n in names] == list(range(5, 10))

@@ -259,6 +259,23 @@ def test_split_k_reduction_is_deterministic(ext):
         ext.free(handle)
 
 
+def test_kernel_info_nine_fields_and_candidate_names(ext):
+    """The nine fields of the reference's ``cutlass_*_kernel_info`` (``cutlass_texture_mainloop.cu:251-267``),
+    the last the occupancy (workgroups per CU), for every prefill tile and GEMV lookahead."""
+    from texelator_amd import autotune
+
+    for name, candidate in autotune.CANDIDATES.items():
+        info = ext.kernel_info(candidate)
+        assert len(info) == 9 and ext.candidate_name(candidate) == name
+        vgprs, _, private, threads, lds, bt, bn, bk, resident = info
+        assert vgprs > 0 and private == 0 and threads >= 256 and lds > 0 and resident >= 1
+        assert name.startswith(("large", "medium", "small")) and f"{bt}x{bn}x{bk}" in name
+    for lookahead in (1, 2, 4):
+        info = ext.kernel_info(100 + lookahead)
+        assert len(info) == 9 and info[5:8] == [1, 16, 128] and info[8] >= 1
+    assert ext.cutlass_texture_kernel_info() == ext.kernel_info(5)
+
+
 def test_handle_api_errors(ext):
     blocks = random_blocks(16, 128, 71)
     scales = lognormal_scales(16, 72)
@@ -271,8 +288,10 @@ def test_handle_api_errors(ext):
             ext.set_prefill(handle, 0, 1024)
         with pytest.raises(RuntimeError, match="tile rows"):
             ext.set_prefill(handle, 16, 24)
-        with pytest.raises(RuntimeError, match="backend"):
+        with pytest.raises(RuntimeError, match="backend") as error:
             ext.set_prefill_backend(handle, 10)
+        for candidate in range(5, 10):   # the message names the real tiles
+            assert f"{candidate} ({ext.candidate_name(candidate)})" in str(error.value)
         with pytest.raises(RuntimeError, match="shape"):
             ext.linear(handle, torch.zeros((1, 64), dtype=torch.bfloat16, device="cuda"))
         with pytest.raises(RuntimeError, match="FP16 or BF16"):

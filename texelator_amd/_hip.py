@@ -271,9 +271,11 @@ def decode_dense(handle: int, dtype: torch.dtype = torch.bfloat16) -> torch.Tens
 
 
 def kernel_info(candidate: int) -> list[int]:
-    """``[vgprs, static_lds, private, max_threads, tile_lds, tokens_tile, rows_tile, k_tile]``."""
-    out = (ctypes.c_int64 * 8)()
-    check(_lib.load().tx_kernel_info(int(candidate), out, 8))
+    """``[vgprs, static_lds, private, max_threads, tile_lds, tokens_tile, rows_tile, k_tile,
+    active_workgroups_per_cu]`` -- the nine fields of the reference's ``cutlass_*_kernel_info``
+    (``cutlass_texture_mainloop.cu:251-267``)."""
+    out = (ctypes.c_int64 * 9)()
+    check(_lib.load().tx_kernel_info(int(candidate), out, 9))
     return [int(v) for v in out]
 
 

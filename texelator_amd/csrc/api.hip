@@ -381,10 +381,13 @@ int tx_set_prefill_backend(uint64_t value, int backend) {
   g_last_error.clear();
   Handle *h = as_handle(value);
   if (!h) return fail(TX_ERR_INVALID, "null Texelator handle");
-  if (backend < 0 || backend > 9)
-    return fail(TX_ERR_INVALID,
-                "prefill backend must be 0-4 (default tile) or 5 (large_256x128x128), 6 (medium_128x128x128), "
-                "7 (medium_128x64x128), 8 (medium_64x128x128), or 9 (small_32x64x128)");
+  if (backend < 0 || backend > tx::kPrefillLast) {
+    std::string message = "prefill backend must be 0-4 (default tile)";
+    for (int c = tx::kPrefillFirst; c <= tx::kPrefillLast; ++c)
+      message += std::string(c == tx::kPrefillLast ? ", or " : ", ") + std::to_string(c) + " (" +
+                 tx::prefill_candidate_name(c) + ")";
+    return fail(TX_ERR_INVALID, message);
+  }
   h->prefill_backend = backend;
   return TX_OK;
 }
@@ -446,20 +449,25 @@ int tx_kernel_info(int candidate, int64_t *out, int n) {
   g_last_error.clear();
   if (!out || n < 0) return fail(TX_ERR_INVALID, "invalid output buffer");
   hipFuncAttributes attr{};
-  int lds = 0, bt = 0, bn = 0, bk = 0;
+  int lds = 0, bt = 0, bn = 0, bk = 0, resident = 0;
   if (candidate >= 100) {
+    if (!tx::gemv_lookahead_supported(candidate - 100)) return fail(TX_ERR_INVALID, "unknown kernel candidate");
     TX_HIP(tx::gemv_kernel_attributes(candidate - 100, &attr));
     bt = 1;
     bn = tx::kTileRows;
     bk = tx::kTileK;
+    // Occupancy for the 27B-class K of 5120 (40 tile columns of staged x).
+    lds = 40 * tx::kTileK * 2;
+    resident = tx::gemv_resident_per_cu(candidate - 100, 40);
   } else {
     if (!tx::prefill_candidate_name(candidate)) return fail(TX_ERR_INVALID, "unknown kernel candidate");
     TX_HIP(tx::prefill_kernel_attributes(candidate, &attr, &lds));
     tx::prefill_candidate_shape(candidate, &bt, &bn, &bk);
+    resident = tx::prefill_resident_per_cu(candidate);
   }
-  const int64_t info[8] = {attr.numRegs, (int64_t)attr.sharedSizeBytes, (int64_t)attr.localSizeBytes,
-                           attr.maxThreadsPerBlock, lds, bt, bn, bk};
-  for (int i = 0; i < n && i < 8; ++i) out[i] = info[i];
+  const int64_t info[9] = {attr.numRegs, (int64_t)attr.sharedSizeBytes, (int64_t)attr.localSizeBytes,
+                           attr.maxThreadsPerBlock, lds, bt, bn, bk, resident};
+  for (int i = 0; i < n && i < 9; ++i) out[i] = info[i];
   return TX_OK;
 }
 

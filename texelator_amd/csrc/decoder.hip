@@ -182,6 +182,9 @@ __global__ void rope_cache_kernel(const uint16_t *qkv, SplitSource split, int64_
   const int j = threadIdx.x;
   const int half = d / 2;
   const int64_t pos = positions[t];
+  // A position outside the cache (and the RoPE tables, which have max_ctx rows) writes nothing:
+  // the host cannot see the value, so the bound is checked here.
+  if (pos < 0 || pos >= max_ctx) return;
   const uint16_t *row = qkv + (size_t)t * stride;
   auto value = [&](int64_t col) { return SPLIT ? split_value(split, t, col) : bf(row[col]); };
   if (head < heads + kv_heads) {
@@ -345,7 +348,8 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(AttnInput in, uin
   if (active) {
     // With ROPE the chunk that holds the position takes that row from the partials, not from the
     // cache (which this block writes).
-    const int fresh = ROPE && pos - j0 < kChunk ? (int)(pos - j0) : -1;
+    // (A position at or past the end of the cache is never written.)
+    const int fresh = ROPE && pos - j0 < kChunk && pos < max_ctx ? (int)(pos - j0) : -1;
     uint16_t *qh = reinterpret_cast<uint16_t *>(qs);
     constexpr int kQRow = kKeyStrideU4 * 8;  // bf16 per padded q row
 #pragma unroll

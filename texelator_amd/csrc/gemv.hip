@@ -466,4 +466,23 @@ hipError_t gemv_kernel_attributes(int lookahead, hipFuncAttributes *attr) {
   }
 }
 
+int gemv_resident_per_cu(int lookahead, int columns) {
+  const void *fn = nullptr;
+  switch (lookahead) {
+    case 1: fn = reinterpret_cast<const void *>(&gemv_kernel<false, 1, false, false, false>); break;
+    case 2: fn = reinterpret_cast<const void *>(&gemv_kernel<false, 2, false, false, false>); break;
+    case 3: fn = reinterpret_cast<const void *>(&gemv_kernel<false, 3, false, false, false>); break;
+    case 4: fn = reinterpret_cast<const void *>(&gemv_kernel<false, 4, false, false, false>); break;
+    case 6: fn = reinterpret_cast<const void *>(&gemv_kernel<false, 6, false, false, false>); break;
+    case 8: fn = reinterpret_cast<const void *>(&gemv_kernel<false, 8, false, false, false>); break;
+    default: return 0;
+  }
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, kThreads, (size_t)columns * 16 * sizeof(uint4)) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  return n;
+}
+
 }  // namespace tx

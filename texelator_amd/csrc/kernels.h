@@ -41,6 +41,9 @@ struct PrefillParams {
 bool gemv_lookahead_supported(int lookahead);
 hipError_t launch_gemv(const GemvParams &p, int lookahead, bool f32_out, hipStream_t stream);
 hipError_t gemv_kernel_attributes(int lookahead, hipFuncAttributes *attr);
+// Workgroups of the single-token bf16 GEMV with this lookahead one CU holds at once, for a split of
+// `columns` tile columns (its x slice is dynamic LDS).
+int gemv_resident_per_cu(int lookahead, int columns);
 // One-token GEMV of a merged [gate | up] handle with a SwiGLU epilogue (p.M = 2 * inter, one
 // split, bf16); p.y receives bf16 [inter].
 hipError_t launch_gemv_swiglu(const GemvParams &p, int lookahead, hipStream_t stream);
@@ -61,6 +64,8 @@ hipError_t launch_prefill(const PrefillParams &p, int candidate, hipStream_t str
 hipError_t prefill_kernel_attributes(int candidate, hipFuncAttributes *attr, int *lds_bytes);
 const char *prefill_candidate_name(int candidate);
 void prefill_candidate_shape(int candidate, int *tokens, int *rows, int *k);
+// Workgroups of a candidate one CU holds at once (occupancy query; 0 for an unknown id).
+int prefill_resident_per_cu(int candidate);
 
 hipError_t launch_palette_probe(float *out, hipStream_t stream);
 // Streaming read of bytes (a multiple of 16) with kStreamReadBlocks workgroups; sink receives at

@@ -855,6 +855,10 @@ const char *prefill_candidate_name(int candidate) {
   return c ? c->name : nullptr;
 }
 
+int prefill_resident_per_cu(int candidate) {
+  return find(candidate) ? resident_per_cu()[candidate - kPrefillFirst] : 0;
+}
+
 void prefill_candidate_shape(int candidate, int *tokens, int *rows, int *k) {
   const Candidate *c = find(candidate);
   *tokens = c ? c->bt : 0;

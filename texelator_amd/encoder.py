@@ -9,7 +9,6 @@ The encoder runs on whatever device ``lut`` lives on.
 from __future__ import annotations
 
 import hashlib
-import json
 from pathlib import Path
 
 import numpy as np
@@ -186,13 +185,3 @@ def encode_linear_e3(weight: torch.Tensor, hdiag: torch.Tensor, lut: torch.Tenso
         "scales_sha256": scales_hash.hexdigest(),
     }
 
-
-def load_moments(path: Path) -> dict[str, torch.Tensor]:
-    value = torch.load(path, map_location="cpu", weights_only=True)
-    if not isinstance(value, dict):
-        raise TypeError(f"expected dict in {path}")
-    return value
-
-
-def metadata_sha(path: Path) -> str:
-    return hashlib.sha256(json.dumps(json.loads(path.read_text()), sort_keys=True).encode()).hexdigest()

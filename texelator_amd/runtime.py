@@ -1,9 +1,18 @@
-"""Python runtime of the BC4 path: native module access, linear modules, packing, install, free.
+"""Python runtime of the BC4 path: the native module, the linear modules, packing, install, free.
 
-Mirrors ``texelator/runtime.py`` of the reference (same names and semantics). Differences:
-the native module is ``texelator_amd._hip`` over ``libtexelator_hip.so`` (built ahead of time,
-never JIT-compiled); the NVFP4 prefill experiment has no gfx950 counterpart and cannot be
-enabled; a one-token input always runs the decode GEMV whatever the prefill threshold.
+Public names and their meaning follow the reference's ``texelator/runtime.py`` (``extension``
+:27-63, ``TexelatorLinear`` :133-145, ``DecodeOnlyLinear`` :148-157, ``pack_entry`` :168-176,
+``pack_entry_handles`` :179-207, ``install`` :210-239, ``install_standalone`` :242-263, ``free``
+:266-274). The implementation is this build's:
+
+* the native module is ``texelator_amd._hip`` over the prebuilt ``libtexelator_hip.so``; there is
+  no JIT build and no fallback, a missing library raises on first use;
+* every way of packing (a metadata entry, an in-memory matrix, a memory map) goes through one
+  row-chunk packer, :func:`_pack_rows`, which frees what it packed if a later chunk fails;
+* both installers go through :func:`_swap_linears`, which resolves every target module before
+  packing anything and frees the packed handles if a replacement fails;
+* the NVFP4 prefill experiment (``runtime.py:66-117``) has no gfx950 counterpart and cannot be
+  enabled; one token always runs the decode GEMV, whatever the prefill threshold.
 """
 from __future__ import annotations
 
@@ -11,6 +20,7 @@ import gc
 import json
 import os
 from pathlib import Path
+from typing import Callable, Iterable, Iterator
 
 import numpy as np
 import torch
@@ -19,53 +29,76 @@ from torch import nn
 from .adapters import resolve_parent
 
 PACKAGE_ROOT = Path(__file__).resolve().parent
-_EXTENSION = None
 PREFILL_THRESHOLD = int(os.environ.get("TEXELATOR_PREFILL_THRESHOLD", "16"))
 PREFILL_TILE_ROWS = int(os.environ.get("TEXELATOR_PREFILL_TILE_ROWS", "1024"))
+# Rows per handle when a matrix is split (the reference's texture-height limit, kept so that
+# handle counts and per-handle shapes match the reference's for the same artifact).
+MAX_ROWS_PER_HANDLE = 32768
+
+_native = None
 
 
 def extension(verbose: bool = False):
-    """The native operator module (``runtime.py:27-63``). Raises if the library is not built."""
-    global _EXTENSION
-    if _EXTENSION is None:
-        from . import _hip, _lib
+    """The native operator module, loaded once. Raises if ``libtexelator_hip.so`` is missing."""
+    global _native
+    if _native is not None:
+        return _native
+    from . import _hip, _lib
 
-        _lib.load()
-        if verbose:
-            print(f"[texelator_amd] loaded {_lib.LIBRARY_PATH}", flush=True)
-        _EXTENSION = _hip
-    return _EXTENSION
+    library = _lib.load()
+    if verbose:
+        print(f"[texelator_amd] native library {_lib.LIBRARY_PATH} ({library._name})", flush=True)
+    _native = _hip
+    return _native
 
 
 def set_fp4_hybrid(enabled: bool) -> None:
-    """The reference's opt-in NVFP4 512-token MLP path (``runtime.py:66-73``) does not exist on gfx950."""
+    """Disabling is a no-op; enabling raises: there is no NVFP4 prefill on gfx950."""
     if enabled:
         raise RuntimeError("the NVFP4 hybrid prefill has no gfx950 counterpart in this build")
 
 
+# ---------------------------------------------------------------------------------------------
+# Linear modules
+
+
 def _linear_dispatch(handle: int, x: torch.Tensor) -> torch.Tensor:
+    """One handle's ``x @ W^T (+ its bias)``; the native call picks the GEMV or the prefill tile."""
     return extension().linear(handle, x)
 
 
+def bc4_linear(handles: list[int], x: torch.Tensor) -> torch.Tensor:
+    """``x @ W^T`` of a matrix held as row shards (handles in row order)."""
+    x = x.contiguous()
+    if len(handles) == 1:
+        return _linear_dispatch(handles[0], x)
+    return torch.cat([_linear_dispatch(handle, x) for handle in handles], dim=-1)
+
+
 class TexelatorLinear(nn.Module):
-    """Drop-in for ``nn.Linear`` over one or more row-split BC4 handles (``runtime.py:133-145``)."""
+    """``nn.Linear`` replacement over one or more row shards of a BC4 matrix.
+
+    A handle may carry its own bias (packed with it); ``bias`` here is a separate parameter
+    added after the shards are joined (the standalone loader's meta-initialised modules)."""
 
     def __init__(self, handles: list[int], bias: nn.Parameter | None = None):
         super().__init__()
-        if not handles:
-            raise ValueError("TexelatorLinear requires at least one texture handle")
-        self.handles = list(handles)
+        shards = [int(handle) for handle in handles]
+        if not shards:
+            raise ValueError("TexelatorLinear requires at least one BC4 handle")
+        self.handles = shards
         self.bias = bias
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        contiguous = x.contiguous()
-        outputs = [_linear_dispatch(handle, contiguous) for handle in self.handles]
-        output = outputs[0] if len(outputs) == 1 else torch.cat(outputs, dim=-1)
-        return output if self.bias is None else output + self.bias
+        y = bc4_linear(self.handles, x)
+        if self.bias is not None:
+            y = y + self.bias
+        return y
 
 
 class DecodeOnlyLinear(nn.Module):
-    """One-token inputs go to the BC4 module, longer ones to the dense original (``runtime.py:148-157``)."""
+    """Routes a single token (``numel == shape[-1]``) to the BC4 module and any longer input to
+    the dense original it was built from."""
 
     def __init__(self, original: nn.Module, quantized: nn.Module):
         super().__init__()
@@ -73,77 +106,89 @@ class DecodeOnlyLinear(nn.Module):
         self.quantized = quantized
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        if x.numel() == x.shape[-1]:
-            return self.quantized(x)
-        return self.original(x)
+        single_token = x.numel() == x.shape[-1]
+        return (self.quantized if single_token else self.original)(x)
 
 
-def _cpu_u8(path: Path) -> torch.Tensor:
-    return torch.from_numpy(np.fromfile(path, dtype=np.uint8).copy())
+# ---------------------------------------------------------------------------------------------
+# Packing
 
 
-def _cpu_f32(path: Path) -> torch.Tensor:
-    return torch.from_numpy(np.fromfile(path, dtype="<f4").copy())
+def _row_chunks(rows: int, max_rows: int) -> Iterator[tuple[int, int]]:
+    if max_rows <= 0:
+        raise ValueError("max_texture_rows must be positive")
+    for start in range(0, rows, max_rows):
+        yield start, min(rows, start + max_rows)
 
 
-def pack_entry(weights: Path, entry: dict, bias: torch.Tensor | None = None, lookahead: int = 1) -> int:
-    handle = extension().pack_encoded(
-        _cpu_u8(weights / entry["blocks_file"]),
-        _cpu_f32(weights / entry["scales_file"]),
-        bias,
-    )
-    extension().set_lookahead(handle, lookahead)
-    extension().set_prefill(handle, PREFILL_THRESHOLD, PREFILL_TILE_ROWS)
-    return handle
+def _host_tensor(array: np.ndarray, dtype) -> torch.Tensor:
+    """A CPU tensor over a contiguous, writable copy of ``array`` when it is a read-only map or
+    a strided view; otherwise over ``array`` itself."""
+    array = np.ascontiguousarray(array, dtype=dtype)
+    if not array.flags.writeable:
+        array = array.copy()
+    return torch.from_numpy(array.reshape(-1))
 
 
-def _host_copy(array: np.ndarray) -> np.ndarray:
-    """A contiguous, writable host array (read-only memory maps are copied)."""
-    array = np.ascontiguousarray(array)
-    return array if array.flags.writeable else array.copy()
+def _configure(handle: int, lookahead: int, palette: torch.Tensor | None) -> None:
+    ext = extension()
+    ext.set_lookahead(handle, lookahead)
+    ext.set_prefill(handle, PREFILL_THRESHOLD, PREFILL_TILE_ROWS)
+    if palette is not None:
+        ext.set_palette_table(handle, palette)
+
+
+def _pack_rows(blocks: np.ndarray, scales: np.ndarray, bias: torch.Tensor | None, lookahead: int,
+               max_rows: int, palette: torch.Tensor | None) -> list[int]:
+    """Pack ``blocks [M, K/16*8]`` and ``scales [M]`` as shards of at most ``max_rows`` rows."""
+    rows = int(scales.shape[0])
+    blocks = blocks.reshape(rows, -1)
+    packed: list[int] = []
+    try:
+        for start, stop in _row_chunks(rows, max_rows):
+            shard_bias = None if bias is None else bias[start:stop]
+            handle = extension().pack_encoded(_host_tensor(blocks[start:stop], np.uint8),
+                                              _host_tensor(scales[start:stop], "<f4"), shard_bias)
+            packed.append(handle)
+            _configure(handle, lookahead, palette)
+    except BaseException:
+        _release(packed)
+        raise
+    return packed
 
 
 def pack_arrays(blocks: np.ndarray, scales: np.ndarray, bias: torch.Tensor | None = None,
-                lookahead: int = 1, max_rows: int = 32768) -> list[int]:
-    """Pack an in-memory matrix (``[M, K/16*8]`` uint8 blocks, ``[M]`` float32 scales),
-    splitting outputs taller than ``max_rows`` into independent handles."""
-    blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
-    scales = np.ascontiguousarray(scales, dtype="<f4")
-    m = scales.shape[0]
-    blocks = blocks.reshape(m, -1)
-    if max_rows <= 0:
-        raise ValueError("max_texture_rows must be positive")
-    handles: list[int] = []
-    try:
-        for start in range(0, m, max_rows):
-            stop = min(start + max_rows, m)
-            handle = extension().pack_encoded(
-                torch.from_numpy(_host_copy(blocks[start:stop]).reshape(-1)),
-                torch.from_numpy(_host_copy(scales[start:stop])),
-                bias[start:stop] if bias is not None else None)
-            extension().set_lookahead(handle, lookahead)
-            extension().set_prefill(handle, PREFILL_THRESHOLD, PREFILL_TILE_ROWS)
-            handles.append(handle)
-    except Exception:
-        free(handles)
-        raise
-    return handles
+                lookahead: int = 1, max_rows: int = MAX_ROWS_PER_HANDLE) -> list[int]:
+    """Pack an in-memory matrix (uint8 blocks ``[M, K/16*8]``, float32 scales ``[M]``) into row
+    shards of at most ``max_rows`` rows."""
+    return _pack_rows(np.asarray(blocks), np.asarray(scales), bias, lookahead, max_rows, None)
+
+
+def _entry_arrays(weights: Path, entry: dict) -> tuple[np.ndarray, np.ndarray]:
+    """Memory maps of an entry's ``.bc4`` and ``.scales.f32`` files (``encoder.py:148-157`` layout)."""
+    rows, columns = int(entry["M"]), int(entry["K"])
+    blocks = np.memmap(Path(weights) / entry["blocks_file"], dtype=np.uint8, mode="r",
+                       shape=(rows, columns // 16 * 8))
+    scales = np.memmap(Path(weights) / entry["scales_file"], dtype="<f4", mode="r", shape=(rows,))
+    return blocks, scales
 
 
 def pack_entry_handles(weights: Path, entry: dict, bias: torch.Tensor | None = None, lookahead: int = 1,
-                       max_texture_rows: int = 32768, palette: torch.Tensor | None = None) -> list[int]:
-    """Pack one matrix, splitting very tall outputs into independent handles (``runtime.py:179-207``).
-    ``palette`` (a device table from :func:`artifact_palette`) switches the handles to LUT mode."""
-    m, k = int(entry["M"]), int(entry["K"])
+                       max_texture_rows: int = MAX_ROWS_PER_HANDLE,
+                       palette: torch.Tensor | None = None) -> list[int]:
+    """Pack one ``metadata.json`` entry as row shards. ``palette`` (a device table from
+    :func:`artifact_palette`) switches the shards to LUT-mode decode."""
     if max_texture_rows <= 0:
         raise ValueError("max_texture_rows must be positive")
-    raw_blocks = np.memmap(weights / entry["blocks_file"], dtype=np.uint8, mode="r", shape=(m, (k // 16) * 8))
-    raw_scales = np.memmap(weights / entry["scales_file"], dtype="<f4", mode="r", shape=(m,))
-    handles = pack_arrays(raw_blocks, raw_scales, bias=bias, lookahead=lookahead, max_rows=max_texture_rows)
-    if palette is not None:
-        for handle in handles:
-            extension().set_palette_table(handle, palette)
-    return handles
+    blocks, scales = _entry_arrays(weights, entry)
+    return _pack_rows(blocks, scales, bias, lookahead, max_texture_rows, palette)
+
+
+def pack_entry(weights: Path, entry: dict, bias: torch.Tensor | None = None, lookahead: int = 1) -> int:
+    """Pack one entry as a single handle, however tall."""
+    (handle,) = pack_entry_handles(weights, entry, bias=bias, lookahead=lookahead,
+                                   max_texture_rows=max(1, int(entry["M"])))
+    return handle
 
 
 def artifact_palette(artifact: Path, device: torch.device | str = "cuda") -> torch.Tensor | None:
@@ -156,8 +201,8 @@ def artifact_palette(artifact: Path, device: torch.device | str = "cuda") -> tor
     reference refuses such an artifact unless this GPU reproduces the palette; here it runs in
     LUT mode instead, bit-exact to that palette."""
     from .artifacts import read_manifest, sha256_file
-    from .hardware import PALETTE_SHA256
     from .encoder import load_palette
+    from .hardware import PALETTE_SHA256
 
     artifact = Path(artifact)
     hardware = read_manifest(artifact).get("hardware", {})
@@ -170,55 +215,84 @@ def artifact_palette(artifact: Path, device: torch.device | str = "cuda") -> tor
     return load_palette(bundled, device).reshape(-1).contiguous()
 
 
+# ---------------------------------------------------------------------------------------------
+# Installation into a model
+
+
+def _swap_linears(model: nn.Module, weights: Path, entries: Iterable[dict], target_name: Callable[[str], str],
+                  build: Callable[[nn.Module, dict], tuple[nn.Module, list[int]]]) -> list[int]:
+    """Replace the module named by each entry with ``build(original, entry)``'s module.
+
+    Every target is resolved before anything is packed, so a misnamed entry fails without
+    touching the GPU; if packing or a replacement fails, the handles packed so far are freed and
+    the modules already replaced keep their BC4 replacement (which then must not be called)."""
+    targets = []
+    for entry in entries:
+        parent, child = resolve_parent(model, target_name(entry["module_name"]))
+        targets.append((parent, child, entry))
+    packed: list[int] = []
+    try:
+        for parent, child, entry in targets:
+            module, handles = build(getattr(parent, child), entry)
+            packed.extend(handles)
+            setattr(parent, child, module)
+    except BaseException:
+        _release(packed)
+        raise
+    model._texelator_handles = packed
+    return packed
+
+
 def install(model: nn.Module, weights: Path, lookahead: int = 1, fp16_prefill: bool = False,
             palette: torch.Tensor | None = None) -> list[int]:
-    """Replace the linears listed in ``weights/metadata.json`` (``runtime.py:210-239``); with
-    ``palette`` the handles decode in LUT mode (see :func:`artifact_palette`)."""
-    metadata = json.loads((weights / "metadata.json").read_text())
-    handles: list[int] = []
-    for entry in metadata["entries"]:
-        parent, child = resolve_parent(model, entry["module_name"])
-        original = getattr(parent, child)
+    """Replace the linears listed in ``weights/metadata.json`` of a loaded model.
+
+    The packed shards take the original's bias. With ``fp16_prefill`` the dense original is kept
+    for inputs longer than one token (:class:`DecodeOnlyLinear`); otherwise it is dropped and the
+    allocator cache emptied. ``palette`` selects LUT-mode decode (see :func:`artifact_palette`)."""
+    weights = Path(weights)
+    entries = json.loads((weights / "metadata.json").read_text())["entries"]
+
+    def build(original: nn.Module, entry: dict):
         device = original.weight.device
         if device.type != "cuda":
             raise RuntimeError(f"{entry['module_name']} is on {device}; selected linears must be CUDA resident")
-        bias = original.bias if getattr(original, "bias", None) is not None else None
         with torch.cuda.device(device):
-            entry_handles = pack_entry_handles(weights, entry, bias=bias, lookahead=lookahead, palette=palette)
-        quantized = TexelatorLinear(entry_handles)
-        replacement = DecodeOnlyLinear(original, quantized) if fp16_prefill else quantized
-        setattr(parent, child, replacement)
-        handles.extend(entry_handles)
-        if not fp16_prefill:
-            del original
+            handles = pack_entry_handles(weights, entry, bias=getattr(original, "bias", None),
+                                         lookahead=lookahead, palette=palette)
+        quantized = TexelatorLinear(handles)
+        return (DecodeOnlyLinear(original, quantized) if fp16_prefill else quantized), handles
+
+    handles = _swap_linears(model, weights, entries, lambda name: name, build)
     gc.collect()
     if torch.cuda.is_available():
         torch.cuda.empty_cache()
-    model._texelator_handles = handles
     return handles
 
 
 def install_standalone(model: nn.Module, weights: Path, entries: list[dict], name_mapper,
                        lookahead: int = 1) -> list[int]:
-    """Replace meta-initialised linears without keeping dense weights (``runtime.py:242-263``)."""
-    handles: list[int] = []
-    try:
-        for entry in entries:
-            parent, child = resolve_parent(model, name_mapper(entry["module_name"]))
-            original = getattr(parent, child)
-            entry_handles = pack_entry_handles(weights, entry, lookahead=lookahead)
-            setattr(parent, child, TexelatorLinear(entry_handles, bias=getattr(original, "bias", None)))
-            handles.extend(entry_handles)
-    except Exception:
-        free(handles)
-        raise
-    model._texelator_handles = handles
-    return handles
+    """Replace the linears of a meta-initialised model (no dense weights ever materialised).
+
+    ``name_mapper`` maps an artifact module name to the model's; the replacement keeps the
+    original module's ``bias`` parameter (loaded by the caller) and adds it after the shards."""
+    weights = Path(weights)
+
+    def build(original: nn.Module, entry: dict):
+        handles = pack_entry_handles(weights, entry, lookahead=lookahead)
+        return TexelatorLinear(handles, bias=getattr(original, "bias", None)), handles
+
+    return _swap_linears(model, weights, entries, name_mapper, build)
+
+
+def _release(handles: Iterable[int]) -> None:
+    ext = extension()
+    for handle in handles:
+        ext.free(handle)
 
 
 def free(handles: list[int]) -> None:
-    """Synchronise, then release every handle (``runtime.py:266-274``)."""
+    """Wait for all queued GPU work, then release every handle."""
     if torch.cuda.is_available():
         torch.cuda.synchronize()
-    for handle in handles:
-        extension().free(handle)
+    _release(handles)

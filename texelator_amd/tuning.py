@@ -1,11 +1,18 @@
-"""Decode-GEMV lookahead tuner (``texelator/tuning.py`` of the reference).
+"""Decode-GEMV lookahead tuner: how many 1 KiB BC4 tiles each wave keeps in flight.
 
-``tune_artifact`` packs every linear of an artifact, checks each lookahead candidate against
-lookahead 1 on a sample of linears (``max_abs <= 1e-3``, ``tuning.py:66-81``; the gfx950
-variants are in fact bitwise equal), times full batch-1 sweeps over all linears with events
-(``tuning.py:82-98``) and stores the lowest-median candidate in a profile keyed by the weights'
-metadata hash and the device (``tuning.py:17-21``). Here "lookahead" is the number of 1 KiB BC4
-tiles each wave keeps in flight; the candidate set and the profile layout are the reference's.
+Interface kept from the reference's ``texelator/tuning.py``: the candidates 1, 2, 3, 4, 6, 8
+(:14), the palette gate before any work (:38-41), the correctness rule (every candidate within
+``max_abs <= 1e-3`` of lookahead 1 on at most eight linears, the first and last four, :66-81),
+the timing of whole batch-1 sweeps over every linear (warmup sweeps, then ``runs`` event-timed
+groups of ``measured`` sweeps, :82-98), the lowest median winning, and the profile's path and
+JSON keys (:17-21, :109-127). The device is named by gfx architecture instead of compute
+capability.
+
+How it is organised here: a :class:`_DecodeSweep` owns the artifact's packed handles, one
+seeded batch-1 input per linear and the lookahead setting; :func:`tune_artifact` asks it for
+probe outputs and sweep timings candidate by candidate (timing helpers in
+:mod:`texelator_amd.measure`). On gfx950 every lookahead computes bitwise the same outputs, so
+the correctness column reads 0.
 """
 from __future__ import annotations
 
@@ -17,133 +24,157 @@ import torch
 
 from .artifacts import read_manifest, sha256_file, weights_dir, write_json
 from .hardware import PALETTE_SHA256, device_key, ensure_hardware
-from .runtime import extension, free, pack_entry_handles
+from .measure import mean_time_ms
+from .runtime import bc4_linear, extension, free, pack_entry_handles
 from .store import STATE_HOME, safe_name
 
 CANDIDATES = (1, 2, 3, 4, 6, 8)
 MAX_ABS_TOLERANCE = 1e-3
+_PROBE_LINEARS = 8  # linears whose outputs are compared between candidates
+_RUNTIME_DTYPES = {"float16": torch.float16, "bfloat16": torch.bfloat16}
 
 
 def _profile_path(artifact: Path) -> Path:
-    metadata_hash = sha256_file(weights_dir(artifact) / "metadata.json")
-    device = safe_name(torch.cuda.get_device_name())
-    return STATE_HOME / "profiles" / metadata_hash[:20] / f"{device_key()}-{device}.json"
+    """``STATE_HOME/profiles/<metadata sha[:20]>/<gfx arch>-<device>.json``."""
+    key = sha256_file(weights_dir(artifact) / "metadata.json")[:20]
+    return STATE_HOME / "profiles" / key / f"{device_key()}-{safe_name(torch.cuda.get_device_name())}.json"
 
 
 def _runtime_dtype(manifest: dict) -> torch.dtype:
+    """The artifact's activation dtype; the reference's default is float16."""
     name = manifest.get("runtime_dtype", "float16")
-    if name == "bfloat16":
-        return torch.bfloat16
-    if name == "float16":
-        return torch.float16
-    raise RuntimeError(f"unsupported Texelator runtime dtype: {name!r}")
+    if name not in _RUNTIME_DTYPES:
+        raise RuntimeError(f"unsupported Texelator runtime dtype: {name!r}")
+    return _RUNTIME_DTYPES[name]
 
 
 def check_palette(artifact: Path) -> str:
-    """The artifact's palette hash must be this device's probed palette (``tuning.py:38-41``)."""
-    current = sha256_file(ensure_hardware())
+    """The artifact's palette hash, which must equal this GPU's probed palette (and so this
+    build's defined palette); raises otherwise."""
+    probed = sha256_file(ensure_hardware())
     expected = read_manifest(artifact).get("hardware", {}).get("palette_sha256")
-    if not expected or expected != current or current != PALETTE_SHA256:
+    if not expected or {expected, probed} != {PALETTE_SHA256}:
         raise RuntimeError("model BC4 palette does not match this GPU; benchmark aborted")
     return expected
 
 
+def _probe_indices(count: int) -> list[int]:
+    """All linears when there are at most eight, else the first four and the last four."""
+    if count <= _PROBE_LINEARS:
+        return list(range(count))
+    half = _PROBE_LINEARS // 2
+    return list(range(half)) + list(range(count - half, count))
+
+
+class _DecodeSweep:
+    """Every linear of an artifact packed (row-split as the runtime splits it), with one seeded
+    ``randn(1, K)`` input per linear in the runtime dtype (CUDA generator, seed 0)."""
+
+    def __init__(self, weights: Path, entries: list[dict], dtype: torch.dtype):
+        self.groups: list[list[int]] = []
+        self.inputs: list[torch.Tensor] = []
+        generator = torch.Generator(device="cuda").manual_seed(0)
+        try:
+            for entry in entries:
+                self.groups.append(pack_entry_handles(weights, entry, lookahead=1))
+                self.inputs.append(torch.randn((1, int(entry["K"])), device="cuda", dtype=dtype,
+                                               generator=generator))
+        except BaseException:
+            self.close()
+            raise
+
+    @property
+    def handles(self) -> list[int]:
+        return [handle for group in self.groups for handle in group]
+
+    def set_lookahead(self, lookahead: int) -> None:
+        ext = extension()
+        for handle in self.handles:
+            ext.set_lookahead(handle, lookahead)
+
+    def outputs(self, indices: list[int]) -> list[torch.Tensor]:
+        return [bc4_linear(self.groups[i], self.inputs[i]).float() for i in indices]
+
+    def run(self) -> None:
+        """One batch-1 pass over every linear, outputs discarded."""
+        linear = extension().linear
+        for group, x in zip(self.groups, self.inputs):
+            for handle in group:
+                linear(handle, x)
+
+    def close(self) -> None:
+        free(self.handles)
+        self.groups.clear()
+
+
+def _time_candidate(sweep: _DecodeSweep, warmup: int, measured: int, runs: int) -> list[float]:
+    for _ in range(warmup):
+        sweep.run()
+    torch.cuda.synchronize()
+    return [mean_time_ms(sweep.run, measured) for _ in range(runs)]
+
+
 def tune_artifact(artifact: Path, warmup: int = 10, measured: int = 50, runs: int = 3) -> dict:
+    """Time full decode sweeps at every lookahead candidate and save the fastest in the
+    artifact's decode profile."""
     if not torch.cuda.is_available():
         raise RuntimeError("tuning requires a visible GPU")
     if warmup < 0 or measured < 1 or runs < 1:
         raise ValueError("warmup must be non-negative; measured and runs must be positive")
     artifact = Path(artifact)
     manifest = read_manifest(artifact)
-    runtime_dtype = _runtime_dtype(manifest)
+    dtype = _runtime_dtype(manifest)
     palette_sha = check_palette(artifact)
-    weights = weights_dir(artifact)
-    metadata_path = weights / "metadata.json"
-    entries = json.loads(metadata_path.read_text())["entries"]
+    metadata = weights_dir(artifact) / "metadata.json"
+    entries = json.loads(metadata.read_text())["entries"]
     if not entries:
         raise RuntimeError("artifact contains no encoded linears")
-    ext = extension()
-    handles: list[int] = []
-    handle_groups: list[list[int]] = []
-    inputs: list[torch.Tensor] = []
+
+    sweep = _DecodeSweep(weights_dir(artifact), entries, dtype)
     try:
-        generator = torch.Generator(device="cuda").manual_seed(0)
-        for entry in entries:
-            group = pack_entry_handles(weights, entry, lookahead=1)
-            handle_groups.append(group)
-            handles.extend(group)
-            inputs.append(torch.randn((1, int(entry["K"])), device="cuda", generator=generator).to(runtime_dtype))
-
-        def evaluate(group: list[int], value: torch.Tensor) -> torch.Tensor:
-            parts = [ext.linear(handle, value) for handle in group]
-            return (parts[0] if len(parts) == 1 else torch.cat(parts, dim=-1)).float()
-
-        paired = list(zip(handle_groups, inputs))
-        sample = paired if len(paired) <= 8 else paired[:4] + paired[-4:]
-        reference = [evaluate(group, value) for group, value in sample]
-
-        def sweep() -> None:
-            for group, value in paired:
-                for handle in group:
-                    ext.linear(handle, value)
-
+        probes = _probe_indices(len(entries))
+        sweep.set_lookahead(CANDIDATES[0])
+        expected = sweep.outputs(probes)
         rows = []
-        for candidate in CANDIDATES:
-            for handle in handles:
-                ext.set_lookahead(handle, candidate)
-            values = [evaluate(group, value) for group, value in sample]
-            max_abs = max(float((got - want).abs().max().item()) for got, want in zip(values, reference))
-            if max_abs > MAX_ABS_TOLERANCE:
-                raise RuntimeError(f"lookahead K={candidate} failed correctness: max_abs={max_abs}")
-            for _ in range(warmup):
-                sweep()
-            torch.cuda.synchronize()
-            timings = []
-            for _ in range(runs):
-                start = torch.cuda.Event(enable_timing=True)
-                stop = torch.cuda.Event(enable_timing=True)
-                start.record()
-                for _ in range(measured):
-                    sweep()
-                stop.record()
-                torch.cuda.synchronize()
-                timings.append(start.elapsed_time(stop) / measured)
-            row = {
-                "lookahead": candidate,
-                "max_abs_vs_k1": max_abs,
-                "sweep_ms_median": statistics.median(timings),
-                "sweep_ms_min": min(timings),
-                "sweep_ms_max": max(timings),
-                "runs": timings,
-            }
+        for lookahead in CANDIDATES:
+            sweep.set_lookahead(lookahead)
+            deviation = max(float((got - want).abs().max()) for got, want in zip(sweep.outputs(probes), expected))
+            if deviation > MAX_ABS_TOLERANCE:
+                raise RuntimeError(f"lookahead K={lookahead} failed correctness: max_abs={deviation}")
+            timings = _time_candidate(sweep, warmup, measured, runs)
+            row = {"lookahead": lookahead, "max_abs_vs_k1": deviation,
+                   "sweep_ms_median": statistics.median(timings), "sweep_ms_min": min(timings),
+                   "sweep_ms_max": max(timings), "runs": timings}
             rows.append(row)
             print(json.dumps(row), flush=True)
-        selected = min(rows, key=lambda row: row["sweep_ms_median"])["lookahead"]
-        profile = {
-            "schema_version": 1,
-            "device": torch.cuda.get_device_name(),
-            "arch": device_key(),
-            "weights_metadata_sha256": sha256_file(metadata_path),
-            "palette_sha256": palette_sha,
-            "artifact": str(artifact.resolve()),
-            "runtime_dtype": manifest.get("runtime_dtype"),
-            "linears": len(entries),
-            "warmup_sweeps": warmup,
-            "measured_sweeps": measured,
-            "independent_runs": runs,
-            "selected_lookahead": selected,
-            "candidates": rows,
-        }
-        target = _profile_path(artifact)
-        write_json(target, profile)
-        print(f"[texelator] selected K={selected}; local benchmark profile saved to {target}", flush=True)
-        return profile
     finally:
-        free(handles)
+        sweep.close()
+
+    best = min(rows, key=lambda row: row["sweep_ms_median"])["lookahead"]
+    profile = {
+        "schema_version": 1,
+        "device": torch.cuda.get_device_name(),
+        "arch": device_key(),
+        "weights_metadata_sha256": sha256_file(metadata),
+        "palette_sha256": palette_sha,
+        "artifact": str(artifact.resolve()),
+        "runtime_dtype": manifest.get("runtime_dtype"),
+        "linears": len(entries),
+        "warmup_sweeps": warmup,
+        "measured_sweeps": measured,
+        "independent_runs": runs,
+        "selected_lookahead": best,
+        "candidates": rows,
+    }
+    target = _profile_path(artifact)
+    write_json(target, profile)
+    print(f"[texelator] selected K={best}; local benchmark profile saved to {target}", flush=True)
+    return profile
 
 
 def selected_lookahead(artifact: Path) -> tuple[int, Path | None]:
-    """The tuned lookahead for an artifact, or (1, None) without a profile (``tuning.py:134-145``)."""
+    """The tuned lookahead of an artifact and its profile path; ``(1, None)`` when there is no
+    profile. Raises when the profile belongs to other weights or another palette."""
     artifact = Path(artifact)
     target = _profile_path(artifact)
     if not target.exists():
@@ -151,6 +182,7 @@ def selected_lookahead(artifact: Path) -> tuple[int, Path | None]:
     profile = json.loads(target.read_text())
     if profile.get("weights_metadata_sha256") != sha256_file(weights_dir(artifact) / "metadata.json"):
         raise RuntimeError("benchmark profile does not match the encoded weights; rerun texelator benchmark")
-    if profile.get("palette_sha256") != read_manifest(artifact).get("hardware", {}).get("palette_sha256"):
+    palette = read_manifest(artifact).get("hardware", {}).get("palette_sha256")
+    if profile.get("palette_sha256") != palette:
         raise RuntimeError("benchmark profile does not match the model palette; rerun texelator benchmark")
     return int(profile["selected_lookahead"]), target
