@@ -9,9 +9,14 @@ Prints one JSON line. ``value`` is the algorithmic HBM bytes of a step (BC4 payl
 scales + bf16 x + fp32 y per linear) times the step count, divided by the timed wall time.
 ``roofline`` is the 5120->27648 (gate/up) GEMV alone: its algorithmic bytes divided by its
 average launch time over back-to-back launches timed with HIP events on the launch stream.
-``cpu_baseline`` is the C restatement of the decode + matvec on the host cores.
+``cpu_baseline`` is the CPU path on the host cores: per-shape medians of the C restatement's fused
+decode + matvec, of the decode and of the matvec alone, and the config-3 fp32 GEMM.
 ``hbm_stream_read`` is a plain streaming read of the same launch size (the achievable HBM rate);
 ``roofline.frac_of_stream_read`` is the GEMV's rate against it.
+``prefill_tok_s_512`` and ``decode_tok_s`` are the metric's other two figures on the 27B-class
+decoder: the 512-token prefill (``texelator_amd.prefill.benchmark_prefill``)
+and graph-replayed greedy decode from 512 to ``--context`` with every step timed; ``model`` holds
+the details, ``model_3b`` the same for BASELINE config 4.
 """
 from __future__ import annotations
 
@@ -73,36 +78,87 @@ def read_traffic():
     return None
 
 
-def cpu_baseline(weights, seconds: float) -> dict:
-    """Fused BC4 decode + fp32 matvec of the C restatement, over one layer's seven linears."""
-    import numpy as np
+def cpu_model() -> str:
+    """The host CPU's model name (``/proc/cpuinfo``), or the platform's processor string."""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
 
-    from oracle import clib
+
+def _median_seconds(fn, runs: int) -> float:
+    import statistics
+
+    samples = []
+    for _ in range(runs):
+        start = time.perf_counter()
+        fn()
+        samples.append(time.perf_counter() - start)
+    return statistics.median(samples)
+
+
+def cpu_baseline(weights, runs: int = 5) -> dict:
+    """The CPU path on the host cores, bounded to ~10-30 s: per distinct config-2 shape, medians
+    of ``runs`` runs of (a) the C restatement's fused BC4 decode + fp32 matvec
+    (``oracle_decode_matvec_f32``, OpenMP), (b) the BC4 -> bf16 decode alone (``oracle_decode_bf16``)
+    and (c) the fp32 matvec alone on the decoded weights (torch CPU); then the config-3 fp32 GEMM
+    on the decoded weights at T = 32, 128, 512 (torch CPU). ``value`` is one layer's seven linears
+    (algorithmic GEMV bytes) over the sum of their decode + matvec medians."""
+    import numpy as np
+    import torch
+
+    from oracle import bc4, clib
 
     cores = min(16, len(os.sched_getaffinity(0)))
     clib.set_threads(cores)
+    torch.set_num_threads(cores)
     rng = np.random.default_rng(SEED)
-    xs = {k: rng.standard_normal(k).astype(np.float32) for k in (HIDDEN, INTER)}
-    xbits = {k: (v.view(np.uint32) >> 16).astype(np.uint16) for k, v in xs.items()}
+    x32 = {k: rng.standard_normal(k).astype(np.float32) for k in (HIDDEN, INTER)}
+    xbits = {k: bc4.f32_to_bf16_bits(v) for k, v in x32.items()}
+    per_shape, decoded = {}, {}
+    started = time.perf_counter()
+    for name, m, k in LAYER:
+        if (m, k) in decoded:
+            continue
+        blocks, scales = weights[(m, k)]
+        fused = _median_seconds(lambda: clib.decode_matvec_f32(blocks, scales, xbits[k]), runs)
+        decode = _median_seconds(lambda: clib.decode_bf16_bits(blocks, scales), runs)
+        w = torch.from_numpy(bc4.bf16_bits_to_f32(clib.decode_bf16_bits(blocks, scales)))
+        xv = torch.from_numpy(bc4.bf16_bits_to_f32(xbits[k]))
+        matvec = _median_seconds(lambda: torch.mv(w, xv), runs)
+        decoded[(m, k)] = w
+        per_shape[f"{k}x{m}"] = {
+            "decode_matvec_ms": round(fused * 1e3, 3), "decode_ms": round(decode * 1e3, 3),
+            "matvec_ms": round(matvec * 1e3, 3),
+            "decode_matvec_GB/s": round(gemv_bytes(m, k) / fused / 1e9, 3), "runs": runs}
+    layer_seconds = sum(per_shape[f"{k}x{m}"]["decode_matvec_ms"] / 1e3 for _, m, k in LAYER)
     layer_bytes = sum(gemv_bytes(m, k) for _, m, k in LAYER)
-    sweeps = 0
-    start = time.perf_counter()
-    while True:
-        for _, m, k in LAYER:
-            blocks, scales = weights[(m, k)]
-            clib.decode_matvec_f32(blocks, scales, xbits[k])
-        sweeps += 1
-        elapsed = time.perf_counter() - start
-        if elapsed >= seconds:
-            break
+    gemm = {}
+    for name in PREFILL_SHAPES:
+        m, k = next((m, k) for n, m, k in LAYER if n == name)
+        w = decoded[(m, k)]
+        for tokens in PREFILL_TOKENS:
+            xt = torch.from_numpy(rng.standard_normal((tokens, k)).astype(np.float32)).to(torch.bfloat16).float()
+            seconds = _median_seconds(lambda: torch.mm(xt, w.t()), runs)
+            gemm[f"{name}_{k}x{m}_T{tokens}"] = {"ms": round(seconds * 1e3, 2),
+                                                 "GFLOP/s": round(2.0 * tokens * m * k / seconds / 1e9, 1),
+                                                 "tokens_per_s": round(tokens / seconds, 1)}
+    elapsed = time.perf_counter() - started
     return {
-        "value": round(layer_bytes * sweeps / elapsed / 1e9, 3),
+        "value": round(layer_bytes / layer_seconds / 1e9, 3),
         "unit": "GB/s",
         "cores": cores,
         "kind": "port",
-        "sample": (f"{sweeps} sweeps of one layer's 7 linears ({layer_bytes / 1e6:.1f} MB of BC4 + scales) "
-                   f"through oracle_decode_matvec_f32 (C, OpenMP, {cores} threads) on "
-                   f"{platform.processor() or platform.machine()}; {elapsed:.1f} s"),
+        "cpu_model": cpu_model(),
+        "sample": (f"one layer's 7 linears, medians of {runs} runs per distinct shape of the C restatement's "
+                   f"fused BC4 decode + fp32 matvec ({cores} OpenMP threads); per-shape decode-only and "
+                   f"matvec-only medians and the T=32/128/512 fp32 GEMM (torch CPU, {cores} threads) beside it; "
+                   f"{elapsed:.1f} s in all"),
+        "per_shape": per_shape,
+        "prefill_gemm": gemm,
     }
 
 
@@ -140,11 +196,16 @@ def prefill_section(torch, ext, stream, handles, candidates=range(5, 10), repeat
             y = torch.empty((tokens, m), device="cuda", dtype=torch.bfloat16)
             nbytes = ext.workspace_bytes(group[0][2], tokens)
             ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device="cuda")
-            times = {}
+            times, outputs = {}, {}
             for cand in candidates:
                 launch = lambda i, c=cand: ext.prefill_into(group[i % len(group)][2], c, x, y, ws)  # noqa: E731
                 launch(0)
+                outputs[cand] = y.clone()
                 times[cand] = timed_launches(torch, stream, launch, repeats * len(group))
+            first = outputs[min(outputs)]
+            equal = all(torch.equal(first, value) for value in outputs.values())
+            if not equal:
+                log(f"prefill tiles differ on {name} T={tokens}")
             best = min(times, key=times.get)
             flops = 2.0 * tokens * m * k
             tflops = flops / times[best] / 1e12
@@ -152,7 +213,7 @@ def prefill_section(torch, ext, stream, handles, candidates=range(5, 10), repeat
                 "best": ext.candidate_name(best), "us": round(times[best] * 1e6, 2),
                 "TFLOP/s": round(tflops, 1), "mfma_util": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
                 "tokens_per_s": round(tokens / times[best], 1),
-                "workspace_bytes": nbytes,
+                "workspace_bytes": nbytes, "candidates_bitwise_equal": equal,
                 "all_us": {ext.candidate_name(c): round(t * 1e6, 2) for c, t in times.items()},
             }
     return out
@@ -246,8 +307,10 @@ def model_section(torch, args, model_name: str | None = None, context: int | Non
             log(str(error))
             pre = prefill.benchmark_prefill(model, tokens=args.prompt, warmup=2, runs=5, rrms_limit=None)
             pre["correctness"]["gate_failed"] = True
-        dec = prefill.benchmark_decode(model, prompt_tokens=args.prompt, context=context,
-                                       sample_steps=args.decode_sample or None)
+        dec = prefill.benchmark_decode(model, prompt_tokens=args.prompt, context=context)
+        sampled = (prefill.benchmark_decode(model, prompt_tokens=args.prompt, context=context,
+                                            sample_steps=args.decode_sample)
+                   if args.decode_sample and context - args.prompt > args.decode_sample else None)
     finally:
         model.close()
     bytes_per_token = config.bc4_bytes() + 2 * config.vocab * config.hidden
@@ -261,8 +324,10 @@ def model_section(torch, args, model_name: str | None = None, context: int | Non
         "decode_context": [args.prompt, context],
         "decode_tok_s": round(dec["gpu_tokens_per_second"], 2),
         "decode_ms_per_token": round(dec["ms_per_token"], 3),
-        "decode_projected_from_samples": dec["projected"],
+        "decode_timed_steps": dec["timed_steps"],
         "decode_per_bucket_tok_s": {k: round(v["tokens_per_second"], 2) for k, v in dec["per_bucket"].items()},
+        "decode_tok_s_projected": round(sampled["gpu_tokens_per_second"], 2) if sampled else None,
+        "decode_projected_sample_steps": args.decode_sample if sampled else None,
         "decode_weight_bytes_per_token": bytes_per_token,
         "data": "random-init weights (BC4 blocks uniform, GPT-2 depth-scaled init), random prompt",
     }
@@ -275,7 +340,7 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=20)
     parser.add_argument("--layers", type=int, default=8, help="distinct layer copies swept per step")
     parser.add_argument("--lookahead", type=int, default=0, help="GEMV lookahead (0 = library default)")
-    parser.add_argument("--cpu-seconds", type=float, default=10.0)
+    parser.add_argument("--cpu-runs", type=int, default=5, help="runs per CPU-baseline median")
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     parser.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a graph")
     parser.add_argument("--no-prefill", action="store_true", help="skip the prefill GEMM measurements")
@@ -286,7 +351,8 @@ def main() -> int:
                         help="skip the Qwen2.5-3B-style decoder (BASELINE config 4) after the 27B-class one")
     parser.add_argument("--prompt", type=int, default=512, help="prefill tokens")
     parser.add_argument("--decode-sample", type=int, default=64,
-                        help="decode steps timed per 512-position bucket (0 = every step)")
+                        help="also report decode projected from this many steps per 512-position bucket "
+                             "(0 = only the fully timed decode)")
     parser.add_argument("--model-only", action="store_true",
                         help="profiling mode: only the model-level prefill and decode measurement (its JSON)")
     parser.add_argument("--prefill-only", action="store_true",
@@ -460,9 +526,13 @@ def main() -> int:
         # BASELINE config 4 as stated there: 512-token prompt, then 256 greedy decode steps
         log("model-level tok/s (3b)")
         result["model_3b"] = model_section(torch, args, "3b", args.prompt + 256)
+    if "model" in result:
+        # the metric's second and third figures, fully timed
+        result["prefill_tok_s_512"] = result["model"]["prefill_tok_s"]
+        result["decode_tok_s"] = result["model"]["decode_tok_s"]
     if not args.no_cpu:
         log("cpu baseline")
-        result["cpu_baseline"] = cpu_baseline(weights, args.cpu_seconds)
+        result["cpu_baseline"] = cpu_baseline(weights, args.cpu_runs)
     else:
         result["cpu_baseline"] = None
 
