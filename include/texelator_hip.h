@@ -65,6 +65,21 @@ int tx_pack_encoded_device(const uint8_t *blocks, int64_t blocks_bytes, const fl
 int tx_linear(uint64_t handle, const void *x, int x_dtype, int64_t x_numel, int64_t x_last,
               int device, void *y, void *workspace, int64_t workspace_bytes, void *stream);
 
+/* tx_linear for callers that cannot allocate (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). No counterpart in the reference. Same arguments, dispatch,
+ * checks and results (bit for bit) as tx_linear, but there is no workspace argument and the
+ * handle's own split-K buffer is not used: split-K partial sums go to a static 32 MiB device
+ * array of the library (tx_noalloc_scratch_bytes), one per GPU, kept until the process ends.
+ * No hipMalloc, hipFree or allocating library call is made. A call whose partials would exceed
+ * the array fails with TX_ERR_INVALID before launching anything. All calls on one GPU share the
+ * array: calls that overlap on one GPU (two streams, two threads) race and must be serialised by
+ * the caller; calls on one stream are ordered and safe. */
+int tx_linear_noalloc(uint64_t handle, const void *x, int x_dtype, int64_t x_numel, int64_t x_last,
+                      int device, void *y, void *stream);
+
+/* Size in bytes of tx_linear_noalloc's static scratch array. */
+int tx_noalloc_scratch_bytes(int64_t *bytes);
+
 /* Workspace bytes tx_linear's prefill path and tx_prefill need for `tokens` tokens (split-K
  * partial sums; 0 when the shape is not split). No reference counterpart (see tx_linear). */
 int tx_workspace_bytes(uint64_t handle, int64_t tokens, int64_t *bytes);

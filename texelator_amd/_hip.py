@@ -140,6 +140,24 @@ def linear(handle: int, x: torch.Tensor) -> torch.Tensor:
     return y
 
 
+def linear_noalloc_into(handle: int, x: torch.Tensor, y: torch.Tensor) -> None:
+    """``linear`` into a caller-provided ``y`` (x's dtype, ``[..., M]``) through
+    ``tx_linear_noalloc``: the library allocates nothing and keeps split-K partials in its static
+    per-GPU scratch, so calls that overlap on one GPU must be serialised by the caller."""
+    m, k = shape(handle)
+    if (x.dtype not in _DTYPE_CODE or y.dtype != x.dtype or not x.is_contiguous() or not y.is_contiguous()
+            or x.size(-1) != k or y.size(-1) != m or x.numel() // k != y.numel() // m or x.data_ptr() % 16):
+        raise TexelatorError("linear_noalloc_into: expected aligned contiguous fp16/bf16 x [..., K] and y [..., M]")
+    check(_lib.load().tx_linear_noalloc(handle, ctypes.c_void_p(x.data_ptr()), _DTYPE_CODE[x.dtype], x.numel(), k,
+                                        x.device.index, ctypes.c_void_p(y.data_ptr()), _stream(x.device)))
+
+
+def noalloc_scratch_bytes() -> int:
+    out = ctypes.c_int64(0)
+    check(_lib.load().tx_noalloc_scratch_bytes(ctypes.byref(out)))
+    return int(out.value)
+
+
 def linear_f32(handle: int, x: torch.Tensor) -> torch.Tensor:
     """Decode GEMV with a float32 output and no bias (parity entry point, ``tx_linear_f32``)."""
     _require(x.is_cuda and x.dtype == torch.bfloat16 and x.is_contiguous(), "input must be contiguous CUDA BF16")

@@ -6,6 +6,7 @@
 
 #include <algorithm>
 #include <cstring>
+#include <mutex>
 #include <new>
 #include <string>
 #include <thread>
@@ -15,6 +16,15 @@
 #include "bc4_device.h"
 #include "elementwise.h"
 #include "kernels.h"
+
+// Static scratch of tx_linear_noalloc: split-K partial sums for callers that cannot allocate.
+// File-scope device memory: every GPU the library runs on holds its own copy from the first use
+// until the process ends. In host code `scratch` is only a stand-in symbol; its device address on
+// each GPU comes from hipGetSymbolAddress (with that GPU current) and is the only form ever passed
+// to a kernel. 32 MiB holds every prefill split this library chooses (prefill_splits caps the
+// partials at 32 MiB) and the one-token GEMV splits of any matrix up to ~1M output rows.
+constexpr size_t kScratchBytes = size_t(32) << 20;
+static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
 
 namespace {
 
@@ -160,7 +170,14 @@ tx::SplitSource split_source(const Handle *h) {
   return tx::SplitSource{h->partials, static_cast<const uint16_t *>(h->bias), h->gemv_splits, h->Mp, 1};
 }
 
-int run_gemv(Handle *h, const void *x, bool f16, int64_t tokens, void *y, bool f32_out, hipStream_t stream) {
+// One-token K splits write ks * Mp fp32 partials to `partials` (the handle's own buffer, or the
+// static scratch of tx_linear_noalloc); several tokens run unsplit and write none.
+int64_t gemv_partials_bytes(const Handle *h, int64_t tokens) {
+  return tokens == 1 && h->gemv_splits > 1 ? (int64_t)h->gemv_splits * h->Mp * (int64_t)sizeof(float) : 0;
+}
+
+int run_gemv(Handle *h, const void *x, bool f16, int64_t tokens, void *y, bool f32_out, hipStream_t stream,
+             float *partials) {
   if (tokens > 65535) return fail(TX_ERR_INVALID, "token grid exceeds the HIP grid.z limit");
   tx::GemvParams p{};
   p.f16 = f16 ? 1 : 0;
@@ -178,7 +195,7 @@ int run_gemv(Handle *h, const void *x, bool f16, int64_t tokens, void *y, bool f
   p.tokens = (int)tokens;
   // One token: K splits reduced by a second kernel. Several tokens: one pass per 16 tokens.
   p.ks = tokens == 1 ? h->gemv_splits : 1;
-  p.partials = h->partials;
+  p.partials = partials;
   TX_HIP(tx::launch_gemv(p, h->lookahead, f32_out, stream));
   return TX_OK;
 }
@@ -269,6 +286,26 @@ int pack_common(const uint8_t *blocks, int64_t blocks_bytes, const float *scales
   return TX_OK;
 }
 
+// ---- Static scratch of tx_linear_noalloc (the array itself is defined above the namespace) ----
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mutex;
+float *g_scratch_address[kMaxScratchDevices] = {};
+
+// Device address of `scratch` on `device`, which must be current; looked up once per device.
+int scratch_address(int device, float **out) {
+  if (device < 0 || device >= kMaxScratchDevices) return fail(TX_ERR_INVALID, "linear_noalloc: device ordinal out of range");
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_address[device]) {
+    void *address = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&address, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !address)
+      return fail(TX_ERR_HIP, std::string("linear_noalloc: hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+    g_scratch_address[device] = static_cast<float *>(address);
+  }
+  *out = g_scratch_address[device];
+  return TX_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -307,7 +344,48 @@ int tx_linear(uint64_t value, const void *x, int x_dtype, int64_t x_numel, int64
     return run_prefill(h, candidate, x, f16, tokens, y, workspace, workspace_bytes, s);
   }
   if (h->bias && h->bias_dtype != x_dtype) return fail(TX_ERR_INVALID, "input and bias dtypes must match");
-  return run_gemv(h, x, f16, tokens, y, false, s);
+  return run_gemv(h, x, f16, tokens, y, false, s, h->partials);
+}
+
+int tx_linear_noalloc(uint64_t value, const void *x, int x_dtype, int64_t x_numel, int64_t x_last, int device, void *y,
+                      void *stream) {
+  g_last_error.clear();
+  Handle *h = as_handle(value);
+  if (!h) return fail(TX_ERR_INVALID, "null Texelator handle");
+  if (x_dtype != TX_DTYPE_BF16 && x_dtype != TX_DTYPE_F16) return fail(TX_ERR_INVALID, "input must be contiguous CUDA FP16 or BF16");
+  if (x_last != h->K || device != h->device) return fail(TX_ERR_INVALID, "input shape/device mismatch");
+  if (!x || !y) return fail(TX_ERR_INVALID, "null input or output pointer");
+  if (reinterpret_cast<uintptr_t>(x) % 16 != 0) return fail(TX_ERR_INVALID, "input must be 16-byte aligned");
+  const bool f16 = x_dtype == TX_DTYPE_F16;
+  const int64_t tokens = x_numel / h->K;
+  if (tokens <= 0) return TX_OK;
+  const bool prefill = tokens >= h->prefill_threshold && tokens > 1;
+  if (prefill && tokens > (1 << 20)) return fail(TX_ERR_INVALID, "token count exceeds the prefill limit (1048576)");
+  if (!prefill && tokens > 65535) return fail(TX_ERR_INVALID, "token grid exceeds the HIP grid.z limit");
+  const int64_t need = prefill ? prefill_workspace_bytes(h, tokens) : gemv_partials_bytes(h, tokens);
+  if (need > (int64_t)kScratchBytes)
+    return fail(TX_ERR_INVALID, "linear_noalloc: the split-K partials need " + std::to_string(need) +
+                                    " bytes, more than the 33554432-byte static scratch; use tx_linear with a workspace");
+  if (h->bias && h->bias_dtype != x_dtype)
+    return fail(TX_ERR_INVALID, prefill ? (f16 ? "FP16 prefill requires an FP16 bias" : "BF16 prefill requires a BF16 bias")
+                                        : "input and bias dtypes must match");
+  DeviceGuard guard(h->device);
+  float *partials = nullptr;
+  if (const int status = scratch_address(h->device, &partials)) return status;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (prefill) {
+    const int candidate = h->prefill_backend >= tx::kPrefillFirst ? h->prefill_backend
+                                                                  : tx::prefill_default_candidate(h->M, h->K, tokens, h->cus);
+    return run_prefill(h, candidate, x, f16, tokens, y, partials, (int64_t)kScratchBytes, s);
+  }
+  return run_gemv(h, x, f16, tokens, y, false, s, partials);
+}
+
+int tx_noalloc_scratch_bytes(int64_t *bytes) {
+  g_last_error.clear();
+  if (!bytes) return fail(TX_ERR_INVALID, "null output");
+  *bytes = (int64_t)kScratchBytes;
+  return TX_OK;
 }
 
 int tx_linear_f32(uint64_t value, const void *x, int64_t tokens, float *y, void *stream) {
@@ -318,7 +396,7 @@ int tx_linear_f32(uint64_t value, const void *x, int64_t tokens, float *y, void 
   if (reinterpret_cast<uintptr_t>(x) % 16 != 0) return fail(TX_ERR_INVALID, "input must be 16-byte aligned");
   if (tokens <= 0) return TX_OK;
   DeviceGuard guard(h->device);
-  return run_gemv(h, x, false, tokens, y, true, reinterpret_cast<hipStream_t>(stream));
+  return run_gemv(h, x, false, tokens, y, true, reinterpret_cast<hipStream_t>(stream), h->partials);
 }
 
 int tx_prefill(uint64_t value, int candidate, const void *x, int x_dtype, int64_t tokens, void *y, void *workspace,
