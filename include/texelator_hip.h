@@ -57,7 +57,9 @@ int tx_pack_encoded_device(const uint8_t *blocks, int64_t blocks_bytes, const fl
  *   x_last    size of x's last dimension (must equal K)
  *   y         device output [tokens][M] of x_dtype, allocated by the caller
  *   workspace device scratch of at least tx_workspace_bytes(handle, tokens) bytes, 16-byte
- *             aligned (may be NULL when that is 0); used only by the prefill path, stream-ordered
+ *             aligned (may be NULL when that is 0), stream-ordered: the prefill path's split-K
+ *             partials (required), or a one-token GEMV's split-K partials (optional: with NULL the
+ *             handle's own buffer is used, so two such calls on one handle must not overlap)
  * tokens >= prefill threshold (and tokens > 1) uses the prefill GEMM candidate set by
  * tx_set_prefill_backend; otherwise the decode GEMV with the configured lookahead.
  * The reference allocates its prefill scratch inside the call (texelator_cuda.cu:942-957); here
@@ -80,12 +82,14 @@ int tx_linear_noalloc(uint64_t handle, const void *x, int x_dtype, int64_t x_num
 /* Size in bytes of tx_linear_noalloc's static scratch array. */
 int tx_noalloc_scratch_bytes(int64_t *bytes);
 
-/* Workspace bytes tx_linear's prefill path and tx_prefill need for `tokens` tokens (split-K
- * partial sums; 0 when the shape is not split). No reference counterpart (see tx_linear). */
+/* Workspace bytes of tx_linear and tx_prefill for `tokens` tokens: the prefill split-K partial
+ * sums for tokens > 1, the one-token GEMV's split-K partials for tokens == 1 (0 when the shape is
+ * not split). No reference counterpart (see tx_linear). */
 int tx_workspace_bytes(uint64_t handle, int64_t tokens, int64_t *bytes);
 
 /* Decode GEMV with float32 output and no bias, for parity checks (no reference counterpart:
- * the reference only returns 16-bit outputs). x: device bf16 [tokens][K]; y: device f32. */
+ * the reference only returns 16-bit outputs). x: device bf16 [tokens][K]; y: device f32. One-token
+ * split-K partials use the handle's own buffer: calls on one handle must not overlap. */
 int tx_linear_f32(uint64_t handle, const void *x, int64_t tokens, float *y, void *stream);
 
 /* Prefill GEMM with an explicit candidate (5..9), x_dtype (BF16 or F16) in and out, bias

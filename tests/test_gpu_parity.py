@@ -259,6 +259,29 @@ def test_split_k_reduction_is_deterministic(ext):
         ext.free(handle)
 
 
+def test_one_token_linear_is_reentrant_across_streams(ext):
+    """One-token GEMVs with K splits on one handle from two streams at once: with the workspace
+    ``linear`` passes, each call's partials are its own, so every result equals the sequential one."""
+    m, k = 1024, 5120
+    handle = _pack(ext, random_blocks(m, k, 95), lognormal_scales(m, 96))
+    try:
+        assert ext.gemv_plan(handle)[0] > 1 and ext.workspace_bytes(handle, 1) > 0
+        xs = [bf16_vector((1, k), 97 + i).cuda() for i in range(2)]
+        want = [ext.linear(handle, x) for x in xs]
+        streams = [torch.cuda.Stream() for _ in xs]
+        torch.cuda.synchronize()
+        results = [[], []]
+        for _ in range(20):
+            for i, (stream, x) in enumerate(zip(streams, xs)):
+                with torch.cuda.stream(stream):
+                    results[i].append(ext.linear(handle, x))
+        torch.cuda.synchronize()
+    finally:
+        ext.free(handle)
+    for i in range(2):
+        assert all(torch.equal(want[i], value) for value in results[i])
+
+
 def test_kernel_info_nine_fields_and_candidate_names(ext):
     """The nine fields of the reference's ``cutlass_*_kernel_info`` (``cutlass_texture_mainloop.cu:251-267``),
     the last the occupancy (workgroups per CU), for every prefill tile and GEMV lookahead."""

@@ -49,8 +49,10 @@ def workspace_bytes(handle: int, tokens: int) -> int:
 
 
 def _workspace(handle: int, tokens: int, device: torch.device):
-    """Stream-ordered scratch from the caching allocator (None when the shape needs none)."""
-    nbytes = workspace_bytes(handle, tokens) if tokens > 1 else 0
+    """Stream-ordered scratch from the caching allocator (None when the shape needs none): the
+    prefill split-K partials, or a one-token GEMV's, so that calls on one handle from several
+    streams never share the handle's own buffer."""
+    nbytes = workspace_bytes(handle, tokens) if tokens >= 1 else 0
     if nbytes == 0:
         return None, ctypes.c_void_p(None), 0
     ws = torch.empty(nbytes, dtype=torch.uint8, device=device)

@@ -128,6 +128,7 @@ int choose_splits(int RG, int CG, int cus) {
     ks = std::min(ks, std::max(1, CG / 4));
   }
   ks = std::max(ks, (CG + tx::kGemvMaxLdsColumns - 1) / tx::kGemvMaxLdsColumns);
+  ks = std::min(ks, std::max(1, 0x7FFFFFFF / std::max(CG, 1)));  // the kernel's 32-bit split arithmetic
   return std::max(1, std::min(ks, CG));
 }
 
@@ -344,7 +345,11 @@ int tx_linear(uint64_t value, const void *x, int x_dtype, int64_t x_numel, int64
     return run_prefill(h, candidate, x, f16, tokens, y, workspace, workspace_bytes, s);
   }
   if (h->bias && h->bias_dtype != x_dtype) return fail(TX_ERR_INVALID, "input and bias dtypes must match");
-  return run_gemv(h, x, f16, tokens, y, false, s, h->partials);
+  // A caller workspace large enough for the one-token split-K partials keeps concurrent calls on
+  // one handle apart; without one the handle's own buffer is used (calls must then not overlap).
+  const int64_t need = gemv_partials_bytes(h, tokens);
+  const bool own = need > 0 && workspace && workspace_bytes >= need && reinterpret_cast<uintptr_t>(workspace) % 16 == 0;
+  return run_gemv(h, x, f16, tokens, y, false, s, own ? static_cast<float *>(workspace) : h->partials);
 }
 
 int tx_linear_noalloc(uint64_t value, const void *x, int x_dtype, int64_t x_numel, int64_t x_last, int device, void *y,
@@ -421,7 +426,7 @@ int tx_workspace_bytes(uint64_t value, int64_t tokens, int64_t *bytes) {
   Handle *h = as_handle(value);
   if (!h) return fail(TX_ERR_INVALID, "null Texelator handle");
   if (!bytes) return fail(TX_ERR_INVALID, "null output");
-  *bytes = tokens > 1 ? prefill_workspace_bytes(h, tokens) : 0;
+  *bytes = tokens > 1 ? prefill_workspace_bytes(h, tokens) : gemv_partials_bytes(h, tokens);
   return TX_OK;
 }
 

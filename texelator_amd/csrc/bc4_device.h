@@ -172,8 +172,26 @@ __device__ __forceinline__ void select_weights(uint32_t pk01, uint32_t pk23, uin
 }
 
 // Packed 16-bit weights (bf16, or fp16 with F16) of one block from its fp32 palette seeds.
-// eight: 8-value mode (e0 > e1); pm: the 6-value mode's slots 6 and 7 (pm_scale_pair of the same
-// type).
+// mode: all ones in 8-value mode (e0 > e1), zero in 6-value mode; pm: the 6-value mode's slots 6
+// and 7 (pm_scale_pair of the same type), merged in with one bitfield insert.
+template <bool F16 = false>
+__device__ __forceinline__ void decode_from_seeds_mode(float base, float end, float step, uint32_t mode, uint32_t a,
+                                                       uint32_t b, float scale, uint32_t pm, uint32_t w[8]) {
+  float p2 = base + step;
+  float p3 = __builtin_fmaf(2.0f, step, base);
+  float p4 = __builtin_fmaf(3.0f, step, base);
+  float p5 = __builtin_fmaf(4.0f, step, base);
+  float p6 = __builtin_fmaf(5.0f, step, base);
+  float p7 = __builtin_fmaf(6.0f, step, base);
+  uint32_t pk01 = pack_weights<F16>(base * scale, end * scale);
+  uint32_t pk23 = pack_weights<F16>(p2 * scale, p3 * scale);
+  uint32_t pk45 = pack_weights<F16>(p4 * scale, p5 * scale);
+  uint32_t pk67 = pack_weights<F16>(p6 * scale, p7 * scale);
+  pk67 = (pk67 & mode) | (pm & ~mode);  // v_bfi_b32
+  select_weights(pk01, pk23, pk45, pk67, a, b, w);
+}
+
+// The same with the mode as a flag (seeds computed in registers).
 template <bool F16 = false>
 __device__ __forceinline__ void decode_from_seeds(float base, float end, float step, bool eight, uint32_t a,
                                                   uint32_t b, float scale, uint32_t pm, uint32_t w[8]) {
@@ -225,31 +243,32 @@ __device__ __forceinline__ void decode_block(uint32_t a, uint32_t b, float scale
   decode_from_seeds<F16>(base, end, step, eight, a, b, scale, pm, w);
 }
 
-// LDS table of the palette seeds, shared by a workgroup, as 509 entries of 8 bytes:
-//   entry[i].base = RN((i - 127) / 127)                                       i = 0..254
-//   entry[i].step = RN(d / 889) if d < 0 else RN(d / 635), d = i - 254,      i = 0..508
-// (d = e1 - e0 < 0 is exactly the 8-value mode e0 > e1). Same arithmetic as decode_block. Both
-// fields are addressed by 8 * index, which is what the endpoint extraction yields.
-struct SeedEntry {
-  float base, step;
-};
+// LDS tables of the palette seeds, shared by a workgroup:
+//   base[i].x = RN((i - 127) / 127)                                   i = 0..254  (.y unused)
+//   step[j]   = {RN(d / 889) if d < 0 else RN(d / 635), mode},  d = j - 254,   j = 0..508
+// with mode = 0xFFFFFFFF for d < 0 (e1 < e0, exactly the 8-value mode) and 0 otherwise. Same
+// arithmetic as decode_block. Both tables have 8-byte entries addressed by 8 * index, which is
+// what the endpoint extraction yields; a step entry and its mode are read by one 64-bit load.
 struct PaletteTableStorage {
-  SeedEntry entry[509];
+  float2 base[255];
+  uint2 step[509];
 };
 
 __device__ __forceinline__ void build_palette_tables(PaletteTableStorage &t, int tid, int nthreads) {
   for (int idx = tid; idx < 509; idx += nthreads) {
-    const float e = (float)(idx - 127);
     const int d = idx - 254;
     const float f = (float)d;
     const float rhi = d < 0 ? kInv889Hi : kInv635Hi;
     const float rlo = d < 0 ? kInv889Lo : kInv635Lo;
-    t.entry[idx].base = idx < 255 ? __builtin_fmaf(e, kInv127Hi, e * kInv127Lo) : 0.0f;
-    t.entry[idx].step = __builtin_fmaf(f, rhi, f * rlo);
+    t.step[idx] = make_uint2(__float_as_uint(__builtin_fmaf(f, rhi, f * rlo)), d < 0 ? 0xFFFFFFFFu : 0u);
+    if (idx < 255) {
+      const float e = (float)(idx - 127);
+      t.base[idx] = make_float2(__builtin_fmaf(e, kInv127Hi, e * kInv127Lo), 0.0f);
+    }
   }
 }
 
-// 8 * eb from the 2-bit endpoint fields in bits 3-4 of each byte: a byte offset into entry[].
+// 8 * eb from the 2-bit endpoint fields in bits 3-4 of each byte: a byte offset into the tables.
 __device__ __forceinline__ uint32_t endpoint_offset(uint32_t word) {
   return __builtin_amdgcn_udot4(word & 0x18181818u, 0x40100401u, 0u, false);
 }
@@ -257,17 +276,18 @@ __device__ __forceinline__ uint32_t endpoint_offset(uint32_t word) {
 // The palette seeds of one device block, read from the LDS tables.
 struct Seeds {
   float base, end, step;
-  bool eight;
+  uint32_t mode;  // all ones in 8-value mode
 };
 
 __device__ __forceinline__ Seeds read_seeds(uint32_t a, uint32_t b, const PaletteTableStorage &t) {
   const uint32_t o0 = endpoint_offset(a);
   const uint32_t o1 = endpoint_offset(b);
   const int od = (int)o1 - (int)o0;  // 8 * (e1 - e0)
-  const char *bytes = reinterpret_cast<const char *>(t.entry);
-  const char *step_bytes = reinterpret_cast<const char *>(&t.entry[254].step);
-  return Seeds{*reinterpret_cast<const float *>(bytes + o0), *reinterpret_cast<const float *>(bytes + o1),
-               *reinterpret_cast<const float *>(step_bytes + od), od < 0};
+  const char *base_bytes = reinterpret_cast<const char *>(t.base);
+  const char *step_bytes = reinterpret_cast<const char *>(&t.step[254]);
+  const uint2 sm = *reinterpret_cast<const uint2 *>(step_bytes + od);
+  return Seeds{*reinterpret_cast<const float *>(base_bytes + o0), *reinterpret_cast<const float *>(base_bytes + o1),
+               __uint_as_float(sm.x), sm.y};
 }
 
 // Decode one device block with the palette seeds read from LDS tables.
@@ -275,7 +295,7 @@ template <bool F16 = false>
 __device__ __forceinline__ void decode_block_lds(uint32_t a, uint32_t b, float scale, uint32_t pm,
                                                  const PaletteTableStorage &t, uint32_t w[8]) {
   const Seeds s = read_seeds(a, b, t);
-  decode_from_seeds<F16>(s.base, s.end, s.step, s.eight, a, b, scale, pm, w);
+  decode_from_seeds_mode<F16>(s.base, s.end, s.step, s.mode, a, b, scale, pm, w);
 }
 
 }  // namespace tx

@@ -4,7 +4,7 @@
 // y[t,m] = bf16( sum_k bf16(P*scale[m]) * x[t,k] + bias[m] ) with fp32 accumulation; L is the
 // number of texture requests in flight per warp. Here:
 //   * a workgroup (4 waves) owns one 16-row group and one K range (a "split"); each wave streams
-//     every 4th 1 KiB tile of that range with one 128-bit load per lane, LOOKAHEAD tiles in
+//     every 4th 1 KiB tile of that range with one 128-bit buffer load per lane, LOOKAHEAD tiles in
 //     flight, and decodes its two blocks per tile in VGPRs (decode_block_lds);
 //   * the decoded bf16 weights are the A operand of v_mfma_f32_16x16x32_bf16 (lane = row x K
 //     chunk of 8), the activations the B operand with one token per column, so one pass over the
@@ -39,6 +39,25 @@ __device__ __forceinline__ f32x4 mfma(uint32_t a0, uint32_t a1, uint32_t a2, uin
   else
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, av), __builtin_bit_cast(bf16x8, bv), c, 0, 0, 0);
 }
+
+// The tiles of one wave read through a buffer descriptor based at the wave's first tile: the
+// tile offset is wave-uniform (a scalar register) and the lane's 16-byte slot a fixed vector
+// register, so a tile load costs no vector instruction for its address. Loads are non-temporal
+// (weights are read once per call). `bytes` bounds the descriptor; loads past it return zero.
+struct TileStream {
+  __amdgpu_buffer_rsrc_t rsrc;
+  int lane_offset;
+  __device__ __forceinline__ TileStream(const uint4 *first, int64_t bytes, int lane)
+      : rsrc(__builtin_amdgcn_make_buffer_rsrc(const_cast<uint4 *>(first), (short)0,
+                                               (int)(bytes < 0x7FFFFFFF ? bytes : 0x7FFFFFFF), 0x00020000)),
+        lane_offset(lane * 16) {}
+  // Tile j of the wave: `stride_tiles` tiles after tile j - 1.
+  __device__ __forceinline__ uint4 load(int j, int stride_tiles) const {
+    const int offset = __builtin_amdgcn_readfirstlane(j * stride_tiles * kTileBytes);
+    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rsrc, lane_offset, offset, 2 /* nt */);
+    return make_uint4(v.x, v.y, v.z, v.w);
+  }
+};
 
 // x of one token, 16 k-values per block: x0/x1 = block 2kg positions 0-7 / 8-15, x2/x3 = block 2kg+1.
 struct XFrag {
@@ -119,14 +138,21 @@ __global__ __launch_bounds__(kThreads, LUT ? 4 : TX_GEMV_WAVES_PER_EU) void gemv
   static_assert(!LUT || LA >= 2, "LUT mode prefetches the palette rows of the next tile");
   extern __shared__ uint4 xs[];  // single token: x slice, 16 uint4 (128 bf16) per tile column
   __shared__ PaletteTableStorage tables;
-  __shared__ float red[kWaves][16][16];  // [wave][token][row]
+  constexpr int kRedTokens = MULTI ? 16 : 1;  // one token: 256 bytes of LDS instead of 4 KiB
+  __shared__ float red[kWaves][kRedTokens][16];  // [wave][token][row]
 
   const int g = blockIdx.x;
   const int split = blockIdx.y;
   const int t0 = blockIdx.z * 16;
   const int tc = min(16, p.tokens - t0);
-  const int c_begin = (int)((int64_t)split * p.CG / p.ks);
-  const int c_end = (int)((int64_t)(split + 1) * p.CG / p.ks);
+  // Tile columns of this split. The host keeps ks * CG below 2^31, so 32-bit products are exact;
+  // an unsplit launch needs no division at all (a 64-bit one cost ~300 scalar instructions per
+  // wave before the first tile load could issue).
+  int c_begin = 0, c_end = p.CG;
+  if (p.ks > 1) {
+    c_begin = (int)((uint32_t)split * (uint32_t)p.CG / (uint32_t)p.ks);
+    c_end = (int)((uint32_t)(split + 1) * (uint32_t)p.CG / (uint32_t)p.ks);
+  }
   const int nc = c_end - c_begin;
   const uint16_t *x = static_cast<const uint16_t *>(p.x);
 
@@ -137,15 +163,15 @@ __global__ __launch_bounds__(kThreads, LUT ? 4 : TX_GEMV_WAVES_PER_EU) void gemv
   const int nt = nc > wave ? (nc - wave + kWaves - 1) / kWaves : 0;
   // Tile j of this wave is tile column c_begin + j*kWaves + wave of row group g. A wave with no
   // tile (nc < kWaves) still issues its prefetch loads: they read the split's last column.
-  const uint4 *wave_tiles = p.tiles + ((size_t)g * p.CG + c_begin + min(wave, nc - 1)) * 64;
+  const int64_t first_tile = (int64_t)g * p.CG + c_begin + min(wave, nc - 1);
+  const TileStream stream(p.tiles + first_tile * 64, ((int64_t)p.RG * p.CG - first_tile) * kTileBytes, lane);
 
   // Ring of LA+1 tile slots: while tile j is decoded, tiles j+1..j+LA are in flight. The first
   // loads are issued before the LDS set-up so that they overlap it.
   constexpr int R = LA + 1;
   uint4 ring[R];
 #pragma unroll
-  for (int u = 0; u < LA; ++u)
-    ring[u] = load_stream(wave_tiles + (size_t)min(u, max(nt - 1, 0)) * kWaves * 64 + lane);
+  for (int u = 0; u < LA; ++u) ring[u] = stream.load(min(u, max(nt - 1, 0)), kWaves);
 
   const int i = lane & 15;   // weight row within the group; token column of the B operand
   const int kg = lane >> 4;  // K chunk: blocks 2kg and 2kg+1 of each tile
@@ -198,7 +224,7 @@ __global__ __launch_bounds__(kThreads, LUT ? 4 : TX_GEMV_WAVES_PER_EU) void gemv
 #pragma unroll
       for (int u = 0; u < R; ++u) {
         const int jn = min(j0 + u + LA, nt - 1);
-        ring[(u + LA) % R] = load_stream(wave_tiles + (size_t)jn * kWaves * 64 + lane);
+        ring[(u + LA) % R] = stream.load(jn, kWaves);
         const TileRows next = tile_rows(lut, ring[(u + 1) % R]);  // tile j+1 (clamped near the end)
         load_xf(j0 + u);
         tile_mfma_lut<F16>(ring[u], cur, xf, scale, acc0, acc1);
@@ -220,7 +246,7 @@ __global__ __launch_bounds__(kThreads, LUT ? 4 : TX_GEMV_WAVES_PER_EU) void gemv
 #pragma unroll
       for (int u = 0; u < R; ++u) {
         const int jn = min(j0 + u + LA, nt - 1);
-        ring[(u + LA) % R] = load_stream(wave_tiles + (size_t)jn * kWaves * 64 + lane);
+        ring[(u + LA) % R] = stream.load(jn, kWaves);
         load_xf(j0 + u);
         tile_mfma<F16>(ring[u], xf, scale, pm, tables, acc0, acc1);
       }
@@ -238,16 +264,17 @@ __global__ __launch_bounds__(kThreads, LUT ? 4 : TX_GEMV_WAVES_PER_EU) void gemv
   const f32x4 acc = acc0 + acc1;
   if (i < tc) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) red[wave][i][kg * 4 + r] = acc[r];
+    for (int r = 0; r < 4; ++r) red[wave][MULTI ? i : 0][kg * 4 + r] = acc[r];
   }
   __syncthreads();
 
   if (threadIdx.x < tc * 16) {
     const int n = threadIdx.x >> 4;
     const int rr = threadIdx.x & 15;
-    float total = red[0][n][rr];
+    const int nn = MULTI ? n : 0;
+    float total = red[0][nn][rr];
 #pragma unroll
-    for (int w = 1; w < kWaves; ++w) total += red[w][n][rr];
+    for (int w = 1; w < kWaves; ++w) total += red[w][nn][rr];
     const int out_row = g * kTileRows + rr;
     const int token = t0 + n;
     if (p.ks > 1 || p.force_partials) {
@@ -284,16 +311,18 @@ __global__ __launch_bounds__(kThreads, LA == 1 ? 6 : (LA == 2 ? 5 : 4)) void gem
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int nt = nc > wave ? (nc - wave + kWaves - 1) / kWaves : 0;
   const int first = min(wave, nc - 1);
-  const uint4 *gate_tiles = p.tiles + ((size_t)g * p.CG + first) * 64;
-  const uint4 *up_tiles = p.tiles + ((size_t)(g + half) * p.CG + first) * 64;
+  const int64_t gate_first = (int64_t)g * p.CG + first, up_first = (int64_t)(g + half) * p.CG + first;
+  const int64_t total = (int64_t)p.RG * p.CG;
+  const TileStream gate_tiles(p.tiles + gate_first * 64, (total - gate_first) * kTileBytes, lane);
+  const TileStream up_tiles(p.tiles + up_first * 64, (total - up_first) * kTileBytes, lane);
 
   constexpr int R = LA + 1;
   uint4 ring_g[R], ring_u[R];
 #pragma unroll
   for (int u = 0; u < LA; ++u) {
-    const size_t off = (size_t)min(u, max(nt - 1, 0)) * kWaves * 64 + lane;
-    ring_g[u] = load_stream(gate_tiles + off);
-    ring_u[u] = load_stream(up_tiles + off);
+    const int j = min(u, max(nt - 1, 0));
+    ring_g[u] = gate_tiles.load(j, kWaves);
+    ring_u[u] = up_tiles.load(j, kWaves);
   }
   const int i = lane & 15;
   const int kg = lane >> 4;
@@ -323,9 +352,9 @@ __global__ __launch_bounds__(kThreads, LA == 1 ? 6 : (LA == 2 ? 5 : 4)) void gem
     progress_priority(nt - j0, nt);
 #pragma unroll
     for (int u = 0; u < R; ++u) {
-      const size_t off = (size_t)min(j0 + u + LA, nt - 1) * kWaves * 64 + lane;
-      ring_g[(u + LA) % R] = load_stream(gate_tiles + off);
-      ring_u[(u + LA) % R] = load_stream(up_tiles + off);
+      const int jn = min(j0 + u + LA, nt - 1);
+      ring_g[(u + LA) % R] = gate_tiles.load(jn, kWaves);
+      ring_u[(u + LA) % R] = up_tiles.load(jn, kWaves);
       consume(u, j0 + u);
     }
   }

@@ -107,8 +107,9 @@ __device__ __forceinline__ bool work_item(const PrefillParams &p, int BT, int BN
   w.split = rest % p.ks;
   w.t0 = (rest / p.ks) * BT;
   w.n0 = row_tile * BN;
-  w.c_begin = (int)((int64_t)w.split * p.CG / p.ks);
-  w.nc = (int)((int64_t)(w.split + 1) * p.CG / p.ks) - w.c_begin;
+  // ks * CG < 2^31 (prefill_splits), so the 32-bit products are exact.
+  w.c_begin = (int)((uint32_t)w.split * (uint32_t)p.CG / (uint32_t)p.ks);
+  w.nc = (int)((uint32_t)(w.split + 1) * (uint32_t)p.CG / (uint32_t)p.ks) - w.c_begin;
   return true;
 }
 
@@ -369,7 +370,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillParams p) {
             uint32_t wa, wb;
             block_words(q, wa, wb);
             uint32_t d[8];
-            decode_from_seeds<F16>(cur[e].base, cur[e].end, cur[e].step, cur[e].eight, wa, wb, scale[b], pm[b], d);
+            decode_from_seeds_mode<F16>(cur[e].base, cur[e].end, cur[e].step, cur[e].mode, wa, wb, scale[b], pm[b], d);
             anext[b][2 * jj] = u32x4{d[0], d[1], d[2], d[3]};
             anext[b][2 * jj + 1] = u32x4{d[4], d[5], d[6], d[7]};
           }
@@ -830,6 +831,7 @@ int prefill_splits(int M, int CG, int64_t tokens, int cus) {
   ks = std::min<int64_t>(ks, std::max(1, CG / 8));
   const int64_t cap = std::max<int64_t>(1, (int64_t(32) << 20) / (tokens * (int64_t)((M + 15) / 16 * 16) * 4));
   ks = std::min(ks, cap);
+  ks = std::min<int64_t>(ks, std::max(1, 0x7FFFFFFF / std::max(CG, 1)));  // the kernels' 32-bit split arithmetic
   return (int)std::max<int64_t>(1, ks);
 }
 
