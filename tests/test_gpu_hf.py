@@ -10,6 +10,7 @@ bf16 batched product of the math path is issued.
 from __future__ import annotations
 
 import copy
+import json
 
 import numpy as np
 import pytest
@@ -101,3 +102,57 @@ def test_hf_generate_greedy(qwen_pair):
     assert got.shape == want.shape == (1, 36)
     assert torch.equal(got[:, :24], ids)
     assert (got[:, 24:] == want[:, 24:]).float().mean() >= 0.75
+
+
+def test_calibrated_artifact_installed_standalone_matches_dense(ext, tmp_path):
+    """BASELINE-style offline pipeline (reference: converter.py:62-233, runtime.py:242-263,
+    standalone.py:102-158): E[x^2] moments from a local token file drive the GPU encoder into a
+    resumable artifact; ``install_standalone`` puts its handles into a meta-initialised Qwen2
+    whose remaining tensors are then assigned (as the standalone loader does); its logits match
+    the dense model holding the decoded weights, in the decode GEMV and the prefill GEMM."""
+    from accelerate import init_empty_weights
+
+    from texelator_amd import converter
+
+    torch.manual_seed(1)
+    config = transformers.Qwen2Config(vocab_size=512, hidden_size=256, intermediate_size=512, num_hidden_layers=2,
+                                      num_attention_heads=4, num_key_value_heads=2, max_position_embeddings=1024,
+                                      rope_theta=1e6, tie_word_embeddings=False, attn_implementation="sdpa")
+    source = transformers.Qwen2ForCausalLM(config).to("cuda").eval()
+    ids_file = tmp_path / "calibration.npy"
+    np.save(ids_file, np.random.default_rng(2).integers(0, 512, size=600).astype(np.int64))
+    ids = converter.read_token_ids(ids_file, 512)
+    with torch.no_grad(), sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.MATH]):
+        path = converter.convert_model(source, tmp_path / "art", ids, source="tiny-qwen2", chunk=256,
+                                       lut=hardware.device_palette("cuda"))
+    assert artifacts.read_manifest(path)["calibration"]["tokens"] == 512
+    entries = json.loads((artifacts.weights_dir(path) / "metadata.json").read_text())["entries"]
+    assert len(entries) == 14
+
+    with init_empty_weights():
+        model = transformers.Qwen2ForCausalLM(config)
+    handles = runtime.install_standalone(model, artifacts.weights_dir(path), entries, name_mapper=lambda name: name)
+    try:
+        linears = {entry["module_name"] for entry in entries}
+        residual = {name: value.to(torch.bfloat16) for name, value in source.state_dict().items()
+                    if name.rsplit(".", 1)[0] not in linears or not name.endswith(".weight")}
+        model.load_state_dict(residual, strict=False, assign=True)
+        model.to("cuda").eval()
+        assert not [name for name, value in model.named_parameters() if value.device.type == "meta"]
+        assert isinstance(model.get_submodule("model.layers.0.self_attn.q_proj"), runtime.TexelatorLinear)
+
+        dense = source.to(torch.bfloat16)
+        with torch.no_grad():
+            for entry in entries:
+                module = model.get_submodule(entry["module_name"])
+                decoded = torch.cat([ext.decode_dense(h) for h in module.handles], dim=0)
+                dense.get_submodule(entry["module_name"]).weight.copy_(decoded)
+        for tokens in (1, 40):
+            x = torch.randint(0, 512, (1, tokens), generator=torch.Generator().manual_seed(tokens)).cuda()
+            with torch.inference_mode(), sdpa_kernel([SDPBackend.FLASH_ATTENTION]):
+                got = model(x).logits
+                want = dense(x).logits
+            assert torch.isfinite(got).all()
+            assert rrms(want, got) < 2e-2
+    finally:
+        runtime.free(handles)

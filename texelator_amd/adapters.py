@@ -7,6 +7,8 @@ from __future__ import annotations
 
 import hashlib
 import re
+from dataclasses import asdict, dataclass
+from typing import Iterable
 
 from torch import nn
 
@@ -42,3 +44,45 @@ def resolve_parent(model: nn.Module, module_name: str) -> tuple[nn.Module, str]:
         return model, module_name
     parent_name, child = module_name.rsplit(".", 1)
     return model.get_submodule(parent_name), child
+
+
+@dataclass(frozen=True)
+class LinearSpec:
+    """One target linear of a model, with the metadata fields an artifact entry records
+    (``adapters.py:28-40``): ``supported`` is False when K is not a multiple of 16."""
+
+    module_name: str
+    artifact_key: str
+    layer: int
+    op: str
+    M: int
+    K: int
+    bias: bool
+    supported: bool
+    reason: str
+
+    def to_dict(self) -> dict:
+        return asdict(self)
+
+
+def discover_linears(model: nn.Module, suffixes: Iterable[str] = DEFAULT_SUFFIXES,
+                     include_regex: str | None = None) -> list[LinearSpec]:
+    """Every ``nn.Linear`` inside a numbered decoder layer whose last name component is one of
+    ``suffixes`` (or whose full name matches ``include_regex``), in module order
+    (``adapters.py:57-88``)."""
+    wanted = set(suffixes)
+    extra = re.compile(include_regex) if include_regex else None
+    specs = []
+    for name, module in model.named_modules():
+        layer = layer_index(name) if isinstance(module, nn.Linear) else None
+        if layer is None:
+            continue
+        op = name.rsplit(".", 1)[-1]
+        if op not in wanted and not (extra and extra.search(name)):
+            continue
+        rows, columns = (int(v) for v in module.weight.shape)
+        ok = columns % 16 == 0
+        specs.append(LinearSpec(module_name=name, artifact_key=artifact_key(name), layer=layer, op=op, M=rows,
+                                K=columns, bias=module.bias is not None, supported=ok,
+                                reason="ok" if ok else "K is not divisible by 16"))
+    return specs
