@@ -292,7 +292,7 @@ def test_kernel_info_nine_fields_and_candidate_names(ext):
         assert len(info) == 9 and ext.candidate_name(candidate) == name
         vgprs, _, private, threads, lds, bt, bn, bk, resident = info
         assert vgprs > 0 and private == 0 and threads >= 256 and lds > 0 and resident >= 1
-        assert name.startswith(("large", "medium", "small")) and f"{bt}x{bn}x{bk}" in name
+        assert name.startswith(("large", "medium", "small", "wide")) and f"{bt}x{bn}x{bk}" in name
     for lookahead in (1, 2, 4):
         info = ext.kernel_info(100 + lookahead)
         assert len(info) == 9 and info[5:8] == [1, 16, 128] and info[8] >= 1

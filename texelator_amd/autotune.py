@@ -33,7 +33,7 @@ from .store import STATE_HOME, safe_name
 CANDIDATES = {
     "large_256x128x128": 5,
     "medium_128x128x128": 6,
-    "medium_64x256x128": 7,
+    "wide_512x128x64": 7,
     "medium_64x128x128": 8,
     "small_32x128x128": 9,
 }

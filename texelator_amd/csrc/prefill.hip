@@ -67,6 +67,7 @@ constexpr int NR = TX_PREFILL_REGIONS;
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 // D += A * B on 32x32x16 tiles of packed 16-bit operands (bf16, or fp16 with F16).
 template <bool F16>
@@ -666,6 +667,307 @@ __global__ __launch_bounds__(kPairThreads) void prefill_pair_kernel(PrefillParam
   else run(std::integral_constant<int, 1>{});
 }
 
+// Wide tile: 512 tokens x 128 rows, so that at 512 tokens every weight is decoded once. K runs in
+// half steps of 64 columns (MFMAs s = 4q .. 4q + 3 of step column c, q = 0, 1: the other tiles'
+// K sets and order, so the results are bitwise equal to theirs).
+//   * decode: the workgroup's threads share the 512 blocks of a half step (2 or 1 each, seeds in
+//     registers) and write the 16-bit weights to an LDS tile [128 rows][64 columns];
+//   * activations: [512 tokens][64 columns] staged by direct global-to-LDS loads (a 1 KiB wave
+//     load covers 8 tokens x 128 bytes);
+//   * each wave multiplies its row blocks (A from the weight tile) by its 128 tokens (4 token
+//     blocks, B from the activation tile), so each LDS operand read feeds several MFMAs.
+// Both LDS tiles store the 16-byte chunk c of row (or token) r at chunk c ^ ((r >> 1) & 7) of the
+// 128-byte row: the 16 lanes one LDS pass serves then hit distinct banks.
+// Weight and activation tiles are double-buffered (160 KiB); one barrier per half step, before
+// which every load issued during the previous half step completes.
+// Waves per workgroup of the wide tile: 4 (one per SIMD, each wave all 128 rows x 128 tokens)
+// or 8 (two per SIMD, each wave 64 rows x 128 tokens).
+#ifndef TX_WIDE_WAVES
+#define TX_WIDE_WAVES 8
+#endif
+constexpr int kWideWaves = TX_WIDE_WAVES;
+constexpr int kWideThreads = 64 * kWideWaves;
+constexpr int kHalfK = kTileK / 2;
+
+// KFULL: K is a multiple of 128 (no staging of columns past K).
+template <bool F16, bool LUT, bool KFULL>
+__global__ __launch_bounds__(kWideThreads) void prefill_wide_kernel(PrefillParams p) {
+  constexpr int WV = kWideWaves;
+  static_assert(WV == 4 || WV == 8, "4 or 8 waves");
+  constexpr int BT = 512, BN = 128;
+  constexpr int TW = 4, RW = 16 / WV;   // token and row blocks (of 32) per wave
+  constexpr int NRG = 4 / RW;           // row groups: wave w owns row group w % NRG, tokens w / NRG
+  constexpr int DEC = 512 / (64 * WV);  // blocks each thread decodes per half step (2 or 1)
+  constexpr int XV = BT * kHalfK * 2 / (kWideThreads * 16);  // direct loads per thread per half step
+  constexpr int NMF = TW * RW;          // MFMAs per slice
+  constexpr int NRD = TW + RW;          // operand reads per slice
+  using Piece = std::conditional_t<DEC == 2, u32x4, u32x2>;
+  __shared__ __attribute__((aligned(128))) uint16_t ws0[BN * kHalfK];
+  __shared__ __attribute__((aligned(128))) uint16_t ws1[BN * kHalfK];
+  __shared__ __attribute__((aligned(128))) uint16_t xs0[BT * kHalfK];
+  __shared__ __attribute__((aligned(128))) uint16_t xs1[BT * kHalfK];
+
+  WorkItem w;
+  if (!work_item(p, BT, BN, w)) return;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int rg = wave % NRG, tg = wave / NRG;
+  const int r32 = lane & 31;
+  const int h = lane >> 5;
+  const int sw = (r32 >> 1) & 7;  // swizzle of every row and token this lane reads
+  const uint16_t *x = static_cast<const uint16_t *>(p.x);
+  const int nh = 2 * w.nc;  // half steps
+
+  // Decode assignment. A half step of the 128 rows is 8 tiles x 32 slots of 16 bytes (slot
+  // (row % 16) + 16*sub of tile column c's half q holds blocks 2*sub, 2*sub + 1 of that half of
+  // the row). With 4 waves thread i owns slot i (both blocks); with 8 waves threads 2j and 2j + 1
+  // own block 0 and 1 of slot j. Rows past M are clamped into the matrix (computed, never stored).
+  const int slot = DEC == 2 ? (int)threadIdx.x : (int)(threadIdx.x >> 1);
+  const int sub = (slot >> 4) & 1;
+  const int drow = 16 * (slot >> 5) + (slot & 15);  // row within the 128
+  const int g = min(w.n0 / kTileRows + (slot >> 5), p.RG - 1);
+  const uint4 *gt = p.tiles + ((size_t)g * p.CG + w.c_begin) * 64 + (slot & 15) + 16 * sub;
+  const float scale = p.scales[g * kTileRows + (slot & 15)];
+  const uint32_t pm = pm_scale_pair<F16>(scale);
+  auto load_piece = [&](int u) {
+    const int v = min(u, nh - 1);
+    const uint4 *ptr = gt + (size_t)(v >> 1) * 64 + 32 * (v & 1);
+    if constexpr (DEC == 2) return __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(ptr));
+    else return __builtin_nontemporal_load(reinterpret_cast<const u32x2 *>(ptr) + (threadIdx.x & 1));
+  };
+  // Decode block jj (0, 1) of the slot: the 16-bit weights of its two 16-byte chunks of the weight
+  // tile (chunk 4*sub + 2*jj + e holds positions 8e..8e+7).
+  auto decode_piece = [&](const Piece &piece, int jj, u32x4 (&out)[2]) __attribute__((always_inline)) {
+    const uint32_t wa = DEC == 2 && jj ? piece[2] : piece[0];
+    const uint32_t wb = DEC == 2 && jj ? piece[3] : piece[1];
+    uint32_t d[8];
+    if constexpr (LUT) {
+      const float4 *row = p.lut + 2 * (size_t)palette_row(wa, wb);
+      decode_from_palette<F16>(row[0], row[1], wa, wb, scale, d);
+    } else {
+      decode_block<F16>(wa, wb, scale, pm, d);
+    }
+    out[0] = u32x4{d[0], d[1], d[2], d[3]};
+    out[1] = u32x4{d[4], d[5], d[6], d[7]};
+  };
+  // Byte offset of this thread's chunk 4*sub (swizzled) in a weight buffer; chunk 4*sub + 2*jj + e
+  // is at that offset ^ 16*(2*jj + e) (the buffers are 128-byte aligned, so the XOR only touches
+  // the chunk index bits).
+  const uint32_t wrow = (uint32_t)(drow * kHalfK * 2 + 16 * ((4 * sub) ^ ((drow >> 1) & 7)));
+  auto lds_addr = [](const uint16_t *ptr) { return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const uint16_t *)ptr; };
+  // The weight stores are inline assembly: the compiler cannot tell them apart from the direct
+  // loads in flight to the activation buffer and would wait for those loads before each store.
+  // The barrier of the half step waits for them (lgkmcnt(0)). The offset is made opaque here so
+  // that the four addresses are derived at each store instead of being held (or spilled) across
+  // the K loop.
+  auto store_chunks = [&](uint16_t *wn, int jj, const u32x4 (&v)[2]) __attribute__((always_inline)) {
+    uint32_t o = wrow;
+    asm volatile("" : "+v"(o));
+    const uint32_t base = lds_addr(wn);
+    asm volatile("ds_write_b128 %0, %1" ::"v"(base + (o ^ (32u * jj))), "v"(v[0]));
+    asm volatile("ds_write_b128 %0, %1" ::"v"(base + (o ^ (32u * jj + 16u))), "v"(v[1]));
+  };
+  // The blocks this thread decodes per half step, and where: slice 2*i for block i.
+  auto my_block = [&](int i) { return DEC == 2 ? i : (int)(threadIdx.x & 1); };
+
+  // Direct load v of this wave fills tokens 8*(WV*v + wave) .. +7 of the activation tile; lane l
+  // lands in physical chunk l%8 of token l/8 there, so it fetches logical chunk
+  // (l%8) ^ ((token >> 1) & 7) = (l%8) ^ (4*(wave%2) + l/16).
+  const int xl_tok = lane >> 3;
+  const int xl_chunk = (lane & 7) ^ (4 * (wave & 1) + (lane >> 4));
+  const bool tile_full = w.t0 + BT <= p.tokens;  // uniform: no token past the input
+  const uint32_t lane_off = (uint32_t)(xl_tok * p.K + 8 * xl_chunk) * 2;
+  auto stage = [&](uint16_t *xn, int u) __attribute__((always_inline)) {
+    const int c = w.c_begin + (u >> 1);
+    const int k0 = c * kTileK + kHalfK * (u & 1);
+    if (KFULL || k0 + kHalfK <= p.K) {
+#pragma unroll
+      for (int v = 0; v < XV; ++v) {
+        const int tok0 = 8 * (WV * v + wave);
+        const int row0 = tile_full ? w.t0 + tok0 : min(w.t0 + tok0, p.tokens - 1);
+        const char *base = reinterpret_cast<const char *>(x + ((size_t)row0 * p.K + k0));
+        uint32_t off = lane_off;
+        if (!tile_full) off = (uint32_t)((min(w.t0 + tok0 + xl_tok, p.tokens - 1) - row0) * p.K + 8 * xl_chunk) * 2;
+        __builtin_amdgcn_global_load_lds((const void *)(base + off),
+                                         (__attribute__((address_space(3))) void *)(xn + tok0 * kHalfK), 16, 0, 0);
+      }
+    } else {
+      // The matrix's last K columns: chunks past K are staged as zeros (K is a multiple of 16,
+      // so a chunk of 8 columns is wholly inside or outside).
+      const int k = k0 + 8 * xl_chunk;
+#pragma unroll 2
+      for (int v = 0; v < XV; ++v) {
+        const int tok = 8 * (WV * v + wave) + xl_tok;
+        const int t = min(w.t0 + tok, p.tokens - 1);
+        uint4 value = make_uint4(0u, 0u, 0u, 0u);
+        if (k < p.K) value = *reinterpret_cast<const uint4 *>(x + (size_t)t * p.K + k);
+        *reinterpret_cast<uint4 *>(xn + tok * kHalfK + 8 * (lane & 7)) = value;
+      }
+    }
+  };
+
+  // Prologue: half step 0's activations and weights, half step 1's activations and the pieces
+  // of half steps 1 and 2.
+  stage(xs0, 0);
+  __builtin_amdgcn_sched_barrier(0);
+  const Piece first = load_piece(0);
+  Piece next = load_piece(1);
+  stage(xs1, 1);  // nh >= 2: every split has at least one tile column
+  __builtin_amdgcn_sched_barrier(0);
+  Piece fresh = load_piece(2);
+#pragma unroll
+  for (int i = 0; i < DEC; ++i) {
+    u32x4 v[2];
+    decode_piece(first, my_block(i), v);
+    store_chunks(ws0, my_block(i), v);
+  }
+  asm volatile("s_waitcnt vmcnt(0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" : "+v"(next), "+v"(fresh) : : "memory");
+
+  f32x16 acc[TW][RW];
+#pragma unroll
+  for (int tb = 0; tb < TW; ++tb)
+#pragma unroll
+    for (int rb = 0; rb < RW; ++rb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[tb][rb][r] = 0.f;
+
+  // Operand reads of slice sl (0..3) of a half step.
+  auto read_a = [&](const uint16_t *wb, int rb, int sl) {
+    return *reinterpret_cast<const u32x4 *>(wb + (32 * (RW * rg + rb) + r32) * kHalfK + 8 * ((4 * h + sl) ^ sw));
+  };
+  auto read_b = [&](const uint16_t *xb, int tb, int sl) {
+    return *reinterpret_cast<const u32x4 *>(xb + (128 * tg + 32 * tb + r32) * kHalfK + 8 * ((4 * h + sl) ^ sw));
+  };
+
+  // Operands of the slice being multiplied; slice 0 of half step 0 first.
+  u32x4 a[RW], b[TW];
+#pragma unroll
+  for (int rb = 0; rb < RW; ++rb) a[rb] = read_a(ws0, rb, 0);
+#pragma unroll
+  for (int tb = 0; tb < TW; ++tb) b[tb] = read_b(xs0, tb, 0);
+
+  // One half step u, multiplying buffers (wb, xb) while the weights of half step u + 1 are
+  // decoded into wn: four regions, one per slice, each holding the slice's MFMAs, the next
+  // slice's LDS reads (in the region's first MFMAs, so they land before the region ends) and, in
+  // slice 2i, the decode of this thread's block i of `next` (the piece of half step u + 1),
+  // interleaved by scheduling groups; the decoded chunks are stored after the region's MFMAs.
+  // The barrier sits halfway through slice 3: it waits for every load and LDS access issued
+  // before it. Then, while the rest of slice 3's MFMAs run, the operands of half step u + 1's
+  // slice 0 are read, the direct loads of half step u + 2 go to the buffer just released (xb)
+  // and the piece of half step u + 3 is loaded: each load has a whole half step to land.
+  // Empty statements right after the barrier redefine `fresh` (the piece of half step u + 2) and
+  // the slice-3 operands still to be used, so the compiler does not wait for the loads and reads
+  // issued after the barrier before it uses them.
+  auto half_step = [&](int u, const uint16_t *wb, uint16_t *xb, uint16_t *wn, const uint16_t *xn) __attribute__((always_inline)) {
+#pragma unroll
+    for (int sl = 0; sl < 3; ++sl) {
+      u32x4 an[RW], bn[TW];
+#pragma unroll
+      for (int rb = 0; rb < RW; ++rb) an[rb] = read_a(wb, rb, sl + 1);
+#pragma unroll
+      for (int tb = 0; tb < TW; ++tb) bn[tb] = read_b(xb, tb, sl + 1);
+      const bool dec = (sl & 1) == 0 && (sl >> 1) < DEC;
+      u32x4 dv[2];
+      if (dec) decode_piece(next, my_block(sl >> 1), dv);
+#pragma unroll
+      for (int tb = 0; tb < TW; ++tb)
+#pragma unroll
+        for (int rb = 0; rb < RW; ++rb) acc[tb][rb] = mfma<F16>(a[rb], b[tb], acc[tb][rb]);
+      // The reads two per MFMA from the first MFMA on; a decode's VALU spread over the MFMAs.
+#pragma unroll
+      for (int i = 0; i < NMF; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        if (2 * i < NRD) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        if (dec && 2 * i < NRD) __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+        if (dec && 2 * i >= NRD) __builtin_amdgcn_sched_group_barrier(0x002, WV == 4 ? 5 : 8, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      if (dec) store_chunks(wn, my_block(sl >> 1), dv);
+#pragma unroll
+      for (int rb = 0; rb < RW; ++rb) a[rb] = an[rb];
+#pragma unroll
+      for (int tb = 0; tb < TW; ++tb) b[tb] = bn[tb];
+    }
+    // Slice 3: token blocks 0-1, the barrier, the next half step's loads, token blocks 2-3.
+#pragma unroll
+    for (int tb = 0; tb < TW / 2; ++tb)
+#pragma unroll
+      for (int rb = 0; rb < RW; ++rb) acc[tb][rb] = mfma<F16>(a[rb], b[tb], acc[tb][rb]);
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_waitcnt vmcnt(0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    asm volatile("" : "+v"(fresh));
+#pragma unroll
+    for (int rb = 0; rb < RW; ++rb) asm volatile("" : "+v"(a[rb]));
+#pragma unroll
+    for (int tb = TW / 2; tb < TW; ++tb) asm volatile("" : "+v"(b[tb]));
+    next = fresh;
+    __builtin_amdgcn_sched_barrier(0);
+    // Past the end the reads take buffers that were never staged (unused), and the staging
+    // repeats the last half step into the released buffer (never read again).
+    u32x4 an[RW], bn[TW];
+#pragma unroll
+    for (int rb = 0; rb < RW; ++rb) an[rb] = read_a(wn, rb, 0);
+#pragma unroll
+    for (int tb = 0; tb < TW; ++tb) bn[tb] = read_b(xn, tb, 0);
+    stage(xb, min(u + 2, nh - 1));
+    fresh = load_piece(u + 3);
+#pragma unroll
+    for (int tb = TW / 2; tb < TW; ++tb)
+#pragma unroll
+      for (int rb = 0; rb < RW; ++rb) acc[tb][rb] = mfma<F16>(a[rb], b[tb], acc[tb][rb]);
+    // (MFMA, 2 reads, loads) from the first MFMA on; the reads land while the last MFMAs run.
+#pragma unroll
+    for (int i = 0; i < NMF / 2; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      if (2 * i < NRD) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x010, (XV + 1 + NMF / 2 - 1) / (NMF / 2), 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int rb = 0; rb < RW; ++rb) a[rb] = an[rb];
+#pragma unroll
+    for (int tb = 0; tb < TW; ++tb) b[tb] = bn[tb];
+  };
+  for (int u = 0; u < nh; u += 2) {
+    half_step(u, ws0, xs0, ws1, xs1);
+    half_step(u + 1, ws1, xs1, ws0, xs0);
+  }
+  // The last half step's repeated staging lands before the workgroup's LDS is released.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+  // acc[tb][rb][r] = D[row 8(r/4) + 4h + r%4 of row block RW*rg + rb][token 128*tg + 32*tb + r32].
+  const uint16_t *bias = static_cast<const uint16_t *>(p.bias);
+#pragma unroll
+  for (int tb = 0; tb < TW; ++tb) {
+    const int t = w.t0 + 128 * tg + tb * 32 + r32;
+    if (t >= p.tokens) continue;
+#pragma unroll
+    for (int rb = 0; rb < RW; ++rb) {
+      __builtin_amdgcn_sched_barrier(0);  // one accumulator at a time: no spills
+#pragma unroll
+      for (int rq = 0; rq < 4; ++rq) {
+        const int row0 = w.n0 + 32 * (RW * rg + rb) + 8 * rq + 4 * h;
+        const f32x16 &v = acc[tb][rb];
+        if (p.ks > 1) {
+          float *dst = p.partials + ((size_t)w.split * p.tokens + t) * p.Mp + row0;
+          if (row0 < p.Mp) *reinterpret_cast<float4 *>(dst) = make_float4(v[4 * rq], v[4 * rq + 1], v[4 * rq + 2], v[4 * rq + 3]);
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int n = row0 + r;
+            if (n < p.M) {
+              float out = round_out<F16>(v[4 * rq + r]);
+              if (bias) out += half_bits_to_float<F16>(bias[n]);
+              store_out<F16>(p.y, (size_t)t * p.M + n, out);
+            }
+          }
+        }
+      }
+    }
+  }
+}
+
 // y[t][m] = round(sum over splits in order of partials[s][t][m]), then the bias with a second
 // rounding (the reference's epilogue order); bf16, or fp16 with F16.
 // KS > 0: exactly KS splits, every partial loaded before the first add (a runtime loop waited
@@ -696,7 +998,7 @@ __global__ __launch_bounds__(256) void prefill_reduce_kernel(PrefillParams p) {
 
 struct Candidate {
   const char *name;
-  int bt, bn;
+  int bt, bn, bk;
   const void *fn;
   hipError_t (*launch)(const PrefillParams &, hipStream_t);
   int lds;
@@ -740,6 +1042,30 @@ hipError_t launch_pair(const PrefillParams &p, hipStream_t stream) {
   return launch_reduce(p, stream);
 }
 
+template <bool F16, bool LUT>
+void launch_wide_as(const PrefillParams &p, int grid, hipStream_t stream) {
+  if (p.K % kTileK == 0)
+    hipLaunchKernelGGL((prefill_wide_kernel<F16, LUT, true>), dim3(grid), dim3(kWideThreads), 0, stream, p);
+  else
+    hipLaunchKernelGGL((prefill_wide_kernel<F16, LUT, false>), dim3(grid), dim3(kWideThreads), 0, stream, p);
+}
+
+hipError_t launch_wide(const PrefillParams &p, hipStream_t stream) {
+  const int items = ((p.M + 127) / 128) * ((p.tokens + 511) / 512) * p.ks;
+  const int grid = ((items + kXcds - 1) / kXcds) * kXcds;
+  if (p.lut) {
+    if (p.f16) launch_wide_as<true, true>(p, grid, stream);
+    else launch_wide_as<false, true>(p, grid, stream);
+  } else if (p.f16) {
+    launch_wide_as<true, false>(p, grid, stream);
+  } else {
+    launch_wide_as<false, false>(p, grid, stream);
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || p.ks == 1) return e;
+  return launch_reduce(p, stream);
+}
+
 template <int TB, int RB, int LA, bool PIPE>
 hipError_t launch_tile(const PrefillParams &p, hipStream_t stream) {
   constexpr int BT = 32 * TB, BN = 128 * RB;
@@ -762,17 +1088,19 @@ hipError_t launch_tile(const PrefillParams &p, hipStream_t stream) {
 
 #define TX_CANDIDATE(NAME, TB, RB, LA, PIPE)                                                            \
   Candidate {                                                                                          \
-    NAME, 32 * (TB), 128 * (RB), reinterpret_cast<const void *>(&prefill_kernel<false, TB, RB, LA, PIPE, false>), \
+    NAME, 32 * (TB), 128 * (RB), kTileK, reinterpret_cast<const void *>(&prefill_kernel<false, TB, RB, LA, PIPE, false>), \
         &launch_tile<TB, RB, LA, PIPE>, 2 * 32 * (TB) * kTileK * 2, kThreads                          \
   }
 
 // The 256- and 128-token tiles pipeline their K loop; the smaller tiles run it plainly.
 const Candidate kCandidates[] = {
-    Candidate{"large_256x128x128", 256, 128,
+    Candidate{"large_256x128x128", 256, 128, kTileK,
               reinterpret_cast<const void *>(&prefill_pair_kernel<false, TX_PAIR_LA, false>),
               &launch_pair<TX_PAIR_LA>, 2 * 256 * kTileK * 2 + 4 * 2 * 4 * 64 * 16, kPairThreads},
     TX_CANDIDATE("medium_128x128x128", 4, 1, TX_PREFILL_LA, true),
-    TX_CANDIDATE("medium_64x256x128", 2, 2, TX_PREFILL_LA_PLAIN, false),
+    Candidate{"wide_512x128x64", 512, 128, kHalfK,
+              reinterpret_cast<const void *>(&prefill_wide_kernel<false, false, true>),
+              &launch_wide, 2 * (512 + 128) * kHalfK * 2, kWideThreads},
     TX_CANDIDATE("medium_64x128x128", 2, 1, TX_PREFILL_LA_PLAIN, false),
     TX_CANDIDATE("small_32x128x128", 1, 1, TX_PREFILL_LA_PLAIN, false),
 };
@@ -807,16 +1135,31 @@ int prefill_default_candidate(int M, int K, int64_t tokens, int cus) {
   if (tokens <= 32) return 9;   // small_32x128x128
   if (tokens <= 64) return 8;   // medium_64x128x128
   if (tokens < 256) return 6;   // medium_128x128x128
+  const int CG = (K + kTileK - 1) / kTileK;
+  // K splits of a one-workgroup-per-CU tile with `items` workgroups per split (the rule of
+  // prefill_splits).
+  auto splits = [&](int64_t items) {
+    int64_t ks = std::max<int64_t>(1, cus / items);
+    ks = std::min<int64_t>(ks, std::max(1, CG / 8));
+    return std::min(ks, std::max<int64_t>(1, (int64_t(32) << 20) / (tokens * (int64_t)((M + 15) / 16 * 16) * 4)));
+  };
+  // The 512-token wide tile from 384 tokens (at most a quarter of its MFMA work past the
+  // tokens) when its workgroups make one round of the CUs at least three quarters full, or
+  // several rounds at least four fifths full on average.
+  if (tokens >= 384) {
+    const int64_t wi = (int64_t)((M + 127) / 128) * ((tokens + 511) / 512);
+    if (wi > (int64_t)cus) {
+      if (5 * wi >= 4 * (int64_t)cus * ((wi + cus - 1) / cus)) return 7;
+    } else if (4 * wi * splits(wi) >= 3 * (int64_t)cus) {
+      return 7;
+    }
+  }
   // The pair-shared 256x128 tile (one workgroup per CU) when its workgroups, K splits included,
   // make one round of the CUs at least three quarters full; otherwise the 128x128 tile, whose
   // finer grain fills sparse grids and the last of several rounds better.
   const int64_t items = (int64_t)((M + 127) / 128) * ((tokens + 255) / 256);
   if (items > (int64_t)cus) return 6;
-  const int CG = (K + kTileK - 1) / kTileK;
-  int64_t ks = std::max<int64_t>(1, cus / items);
-  ks = std::min<int64_t>(ks, std::max(1, CG / 8));
-  ks = std::min(ks, std::max<int64_t>(1, (int64_t(32) << 20) / (tokens * (int64_t)((M + 15) / 16 * 16) * 4)));
-  return 4 * items * ks >= 3 * (int64_t)cus ? 5 : 6;
+  return 4 * items * splits(items) >= 3 * (int64_t)cus ? 5 : 6;
 }
 
 int prefill_splits(int M, int CG, int64_t tokens, int cus) {
@@ -865,7 +1208,7 @@ void prefill_candidate_shape(int candidate, int *tokens, int *rows, int *k) {
   const Candidate *c = find(candidate);
   *tokens = c ? c->bt : 0;
   *rows = c ? c->bn : 0;
-  *k = c ? kTileK : 0;
+  *k = c ? c->bk : 0;
 }
 
 }  // namespace tx
