@@ -58,7 +58,7 @@ int tx_pack_encoded_device(const uint8_t *blocks, int64_t blocks_bytes, const fl
  *   y         device output [tokens][M] of x_dtype, allocated by the caller
  *   workspace device scratch of at least tx_workspace_bytes(handle, tokens) bytes, 16-byte
  *             aligned (may be NULL when that is 0), stream-ordered: the prefill path's split-K
- *             partials (required), or a one-token GEMV's split-K partials (optional: with NULL the
+ *             partials or backend 1's dense rows (required), or a one-token GEMV's split-K partials (optional: with NULL the
  *             handle's own buffer is used, so two such calls on one handle must not overlap)
  * tokens >= prefill threshold (and tokens > 1) uses the prefill GEMM candidate set by
  * tx_set_prefill_backend; otherwise the decode GEMV with the configured lookahead.
@@ -83,8 +83,10 @@ int tx_linear_noalloc(uint64_t handle, const void *x, int x_dtype, int64_t x_num
 int tx_noalloc_scratch_bytes(int64_t *bytes);
 
 /* Workspace bytes of tx_linear and tx_prefill for `tokens` tokens: the prefill split-K partial
- * sums for tokens > 1, the one-token GEMV's split-K partials for tokens == 1 (0 when the shape is
- * not split). No reference counterpart (see tx_linear). */
+ * sums for tokens > 1 (with backend 1 and tokens >= the prefill threshold: the dense scratch of
+ * min(tile_rows, M) decoded rows of K 16-bit weights, 256-byte aligned, plus 8 MiB for the library
+ * GEMM), the one-token GEMV's split-K partials for
+ * tokens == 1 (0 when the shape is not split). No reference counterpart (see tx_linear). */
 int tx_workspace_bytes(uint64_t handle, int64_t tokens, int64_t *bytes);
 
 /* Decode GEMV with float32 output and no bias, for parity checks (no reference counterpart:
@@ -102,11 +104,15 @@ int tx_prefill(uint64_t handle, int candidate, const void *x, int x_dtype, int64
 int tx_set_lookahead(uint64_t handle, int lookahead);
 
 /* Replaces texelator_set_prefill (texelator_cuda.cu:1480-1488): threshold >= 1,
- * tile_rows a positive multiple of 16 (accepted and stored; no scratch path uses it here). */
+ * tile_rows a positive multiple of 16: the rows backend 1 decodes per library GEMM. */
 int tx_set_prefill(uint64_t handle, int threshold, int tile_rows);
 
 /* Replaces texelator_set_prefill_backend (texelator_cuda.cu:1490-1503): 0..9. Ids 5..9 name the
- * gfx950 tile candidates; 0..4 (the reference's CUDA-only backends) select the default tile. */
+ * gfx950 tile candidates. 1 is the dense-scratch path of the reference's backend 1
+ * (texelator_cuda.cu:937-990): tile_rows rows at a time decoded into the workspace, one hipBLASLt
+ * GEMM (fp32 accumulation) per row tile, then the bias with a second rounding; hipBLASLt is
+ * opened at its first call. 0 and 2..4 (the reference's fused and CUDA-only 512-token kernels)
+ * select the default tile. */
 int tx_set_prefill_backend(uint64_t handle, int backend);
 
 /* LUT-mode decode (no reference counterpart: on NVIDIA the texture unit is the palette). With a

@@ -61,7 +61,7 @@ def build(verbose: bool = False, output: Path | None = None, defines: tuple[str,
     with concurrent.futures.ThreadPoolExecutor(max_workers=workers) as pool:
         objects = list(pool.map(lambda src: _compile(src, build_dir, tuple(defines)), srcs))
     tmp = library.with_suffix(".so.tmp")
-    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objects), "-o", str(tmp)]
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objects), "-ldl", "-o", str(tmp)]
     result = subprocess.run(cmd, capture_output=True, text=True)
     if result.returncode != 0:
         raise RuntimeError(f"link failed:\n{result.stderr}")

@@ -138,8 +138,53 @@ int64_t prefill_workspace_bytes(const Handle *h, int64_t tokens) {
   return ks > 1 ? (int64_t)ks * tokens * h->Mp * (int64_t)sizeof(float) : 0;
 }
 
+// The dense-scratch backend (the reference's backend 1, texelator_cuda.cu:937-990): its scratch
+// holds min(tile_rows, M) decoded rows of K 16-bit weights, then the library GEMM's workspace.
+constexpr int kDenseBackend = 1;
+
+int dense_tile_rows(const Handle *h) { return std::min(h->prefill_tile_rows, h->M); }
+
+int64_t dense_rows_bytes(const Handle *h) { return ((int64_t)dense_tile_rows(h) * h->K * 2 + 255) / 256 * 256; }
+
+int64_t dense_workspace_bytes(const Handle *h) { return dense_rows_bytes(h) + (int64_t)tx::kDenseGemmWorkspace; }
+
+// The backend a prefill-sized call of `tokens` tokens runs: the dense-scratch path, or a tile id.
+int prefill_choice(const Handle *h, int64_t tokens) {
+  if (h->prefill_backend == kDenseBackend) return kDenseBackend;
+  return h->prefill_backend >= tx::kPrefillFirst ? h->prefill_backend
+                                                 : tx::prefill_default_candidate(h->M, h->K, tokens, h->cus);
+}
+
+// Workspace bytes of a prefill-sized call.
+int64_t prefill_call_bytes(const Handle *h, int64_t tokens) {
+  return prefill_choice(h, tokens) == kDenseBackend ? dense_workspace_bytes(h) : prefill_workspace_bytes(h, tokens);
+}
+
+// Rows decoded tile_rows at a time into the workspace, one hipBLASLt GEMM per row tile writing
+// its columns of y, then the bias with a second rounding (texelator_cuda.cu:960-989).
+int run_dense_prefill(Handle *h, const void *x, bool f16, int64_t tokens, void *y, void *workspace,
+                      int64_t workspace_bytes, hipStream_t stream) {
+  if (tokens > (1 << 20)) return fail(TX_ERR_INVALID, "token count exceeds the prefill limit (1048576)");
+  if (!workspace || workspace_bytes < dense_workspace_bytes(h) || reinterpret_cast<uintptr_t>(workspace) % 16 != 0)
+    return fail(TX_ERR_INVALID, "dense prefill workspace missing or too small (see tx_workspace_bytes)");
+  uint16_t *dense = static_cast<uint16_t *>(workspace);
+  void *gemm_workspace = static_cast<char *>(workspace) + dense_rows_bytes(h);
+  const int tile = dense_tile_rows(h);
+  for (int row = 0; row < h->M; row += tile) {
+    const int rows = std::min(tile, h->M - row);
+    TX_HIP(tx::launch_decode_rows(h->tiles, h->scales, h->lut, h->M, h->K, h->CG, row, rows, f16, dense, stream));
+    std::string error;
+    if (!tx::dense_gemm(h->device, f16, rows, tokens, h->K, dense, x, static_cast<uint16_t *>(y) + row, h->M,
+                        gemm_workspace, stream, error))
+      return fail(TX_ERR_HIP, "dense prefill: " + error);
+  }
+  if (h->bias) TX_HIP(tx::launch_add_bias(y, h->bias, tokens, h->M, f16, stream));
+  return TX_OK;
+}
+
 int run_prefill(Handle *h, int candidate, const void *x, bool f16, int64_t tokens, void *y, void *workspace,
                 int64_t workspace_bytes, hipStream_t stream) {
+  if (candidate == kDenseBackend) return run_dense_prefill(h, x, f16, tokens, y, workspace, workspace_bytes, stream);
   tx::PrefillParams p{};
   p.f16 = f16 ? 1 : 0;
   p.lut = h->lut;
@@ -340,9 +385,7 @@ int tx_linear(uint64_t value, const void *x, int x_dtype, int64_t x_numel, int64
   if (tokens >= h->prefill_threshold && tokens > 1) {
     if (h->bias && h->bias_dtype != x_dtype)
       return fail(TX_ERR_INVALID, f16 ? "FP16 prefill requires an FP16 bias" : "BF16 prefill requires a BF16 bias");
-    const int candidate = h->prefill_backend >= tx::kPrefillFirst ? h->prefill_backend
-                                                                  : tx::prefill_default_candidate(h->M, h->K, tokens, h->cus);
-    return run_prefill(h, candidate, x, f16, tokens, y, workspace, workspace_bytes, s);
+    return run_prefill(h, prefill_choice(h, tokens), x, f16, tokens, y, workspace, workspace_bytes, s);
   }
   if (h->bias && h->bias_dtype != x_dtype) return fail(TX_ERR_INVALID, "input and bias dtypes must match");
   // A caller workspace large enough for the one-token split-K partials keeps concurrent calls on
@@ -367,9 +410,9 @@ int tx_linear_noalloc(uint64_t value, const void *x, int x_dtype, int64_t x_nume
   const bool prefill = tokens >= h->prefill_threshold && tokens > 1;
   if (prefill && tokens > (1 << 20)) return fail(TX_ERR_INVALID, "token count exceeds the prefill limit (1048576)");
   if (!prefill && tokens > 65535) return fail(TX_ERR_INVALID, "token grid exceeds the HIP grid.z limit");
-  const int64_t need = prefill ? prefill_workspace_bytes(h, tokens) : gemv_partials_bytes(h, tokens);
+  const int64_t need = prefill ? prefill_call_bytes(h, tokens) : gemv_partials_bytes(h, tokens);
   if (need > (int64_t)kScratchBytes)
-    return fail(TX_ERR_INVALID, "linear_noalloc: the split-K partials need " + std::to_string(need) +
+    return fail(TX_ERR_INVALID, "linear_noalloc: the call's scratch needs " + std::to_string(need) +
                                     " bytes, more than the 33554432-byte static scratch; use tx_linear with a workspace");
   if (h->bias && h->bias_dtype != x_dtype)
     return fail(TX_ERR_INVALID, prefill ? (f16 ? "FP16 prefill requires an FP16 bias" : "BF16 prefill requires a BF16 bias")
@@ -378,11 +421,7 @@ int tx_linear_noalloc(uint64_t value, const void *x, int x_dtype, int64_t x_nume
   float *partials = nullptr;
   if (const int status = scratch_address(h->device, &partials)) return status;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  if (prefill) {
-    const int candidate = h->prefill_backend >= tx::kPrefillFirst ? h->prefill_backend
-                                                                  : tx::prefill_default_candidate(h->M, h->K, tokens, h->cus);
-    return run_prefill(h, candidate, x, f16, tokens, y, partials, (int64_t)kScratchBytes, s);
-  }
+  if (prefill) return run_prefill(h, prefill_choice(h, tokens), x, f16, tokens, y, partials, (int64_t)kScratchBytes, s);
   return run_gemv(h, x, f16, tokens, y, false, s, partials);
 }
 
@@ -426,7 +465,8 @@ int tx_workspace_bytes(uint64_t value, int64_t tokens, int64_t *bytes) {
   Handle *h = as_handle(value);
   if (!h) return fail(TX_ERR_INVALID, "null Texelator handle");
   if (!bytes) return fail(TX_ERR_INVALID, "null output");
-  *bytes = tokens > 1 ? prefill_workspace_bytes(h, tokens) : gemv_partials_bytes(h, tokens);
+  if (tokens > 1 && tokens >= h->prefill_threshold) *bytes = prefill_call_bytes(h, tokens);
+  else *bytes = tokens > 1 ? prefill_workspace_bytes(h, tokens) : gemv_partials_bytes(h, tokens);
   return TX_OK;
 }
 
@@ -465,7 +505,7 @@ int tx_set_prefill_backend(uint64_t value, int backend) {
   Handle *h = as_handle(value);
   if (!h) return fail(TX_ERR_INVALID, "null Texelator handle");
   if (backend < 0 || backend > tx::kPrefillLast) {
-    std::string message = "prefill backend must be 0-4 (default tile)";
+    std::string message = "prefill backend must be 0 or 2-4 (default tile), 1 (dense scratch and hipBLASLt)";
     for (int c = tx::kPrefillFirst; c <= tx::kPrefillLast; ++c)
       message += std::string(c == tx::kPrefillLast ? ", or " : ", ") + std::to_string(c) + " (" +
                  tx::prefill_candidate_name(c) + ")";

@@ -2,6 +2,8 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+
+#include <string>
 #include <stdint.h>
 
 namespace tx {
@@ -76,6 +78,20 @@ hipError_t launch_stream_read(const void *data, size_t bytes, uint32_t *sink, hi
 hipError_t launch_repack(const uint8_t *blocks, int M, int bpr, int RG, int CG, uint4 *tiles, hipStream_t stream);
 hipError_t launch_decode_dense(const uint4 *tiles, const float *scales, const float4 *lut, int M, int K, int RG, int CG,
                                bool f16, uint16_t *out, hipStream_t stream);
+// Rows row_begin .. row_begin + rows - 1 (row_begin a multiple of 16) decoded into the dense
+// row-major out[rows][K].
+hipError_t launch_decode_rows(const uint4 *tiles, const float *scales, const float4 *lut, int M, int K, int CG,
+                              int row_begin, int rows, bool f16, uint16_t *out, hipStream_t stream);
+
+// Dense-scratch prefill pieces (dense.hip). dense_gemm: y[t][m] (row-major, row stride ldy) =
+// round(sum_k x[t][k] * w[m][k]) for m < rows, fp32 accumulation on hipBLASLt (loaded at first
+// use); false with `error` set when the library or the call fails. add_bias: y[t][m] =
+// round(y[t][m] + bias[m]) over tokens x M (the reference's second rounding).
+// gemm_workspace: kDenseGemmWorkspace bytes of device scratch for the library (256-aligned).
+constexpr size_t kDenseGemmWorkspace = size_t(8) << 20;
+bool dense_gemm(int device, bool f16, int rows, int64_t tokens, int K, const void *w, const void *x, void *y,
+                int64_t ldy, void *gemm_workspace, hipStream_t stream, std::string &error);
+hipError_t launch_add_bias(void *y, const void *bias, int64_t tokens, int M, bool f16, hipStream_t stream);
 
 // Decoder-layer helpers (decoder.hip).
 struct SplitSource;

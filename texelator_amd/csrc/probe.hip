@@ -31,19 +31,21 @@ __global__ void palette_probe_kernel(float *out) {
   dst[1] = make_float4(pal.p[4], pal.p[5], pal.p[6], pal.p[7]);
 }
 
-// One thread per lane-slot of a tile: decodes two blocks into out[M][K] (bf16 bits, or fp16
-// bits with F16).
+// One thread per lane-slot of a tile of row groups g_begin .. g_begin + groups - 1: decodes two
+// blocks of row `row` into out[row - row_begin][K] for rows below row_end (bf16 bits, or fp16 bits
+// with F16).
 template <bool F16>
-__global__ void decode_dense_kernel(const uint4 *tiles, const float *scales, const float4 *lut, int M, int K, int RG,
-                                    int CG, uint16_t *out) {
-  const size_t slot = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (slot >= (size_t)RG * CG * 64) return;
-  const int lane = slot & 63;
-  const size_t tile = slot >> 6;
-  const int g = (int)(tile / CG);
+__global__ void decode_dense_kernel(const uint4 *tiles, const float *scales, const float4 *lut, int M, int K, int CG,
+                                    int g_begin, int groups, int row_end, uint16_t *out) {
+  const size_t local = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (local >= (size_t)groups * CG * 64) return;
+  const int lane = local & 63;
+  const size_t tile = local >> 6;
+  const int g = g_begin + (int)(tile / CG);
   const int c = (int)(tile % CG);
   const int row = g * kTileRows + (lane & 15);
-  if (row >= M) return;
+  if (row >= M || row >= row_end) return;
+  const size_t slot = (size_t)g_begin * CG * 64 + local;
   const uint4 cur = tiles[slot];
   const float scale = scales[row];
   const uint32_t pm = pm_scale_pair<F16>(scale);
@@ -61,7 +63,7 @@ __global__ void decode_dense_kernel(const uint4 *tiles, const float *scales, con
   for (int h = 0; h < 2; ++h) {
     const int k0 = (c * kTileBlocks + 2 * (lane >> 4) + h) * 16;
     if (k0 >= K) continue;
-    uint16_t *dst = out + (size_t)row * K + k0;
+    uint16_t *dst = out + (size_t)(row - g_begin * kTileRows) * K + k0;
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
       dst[2 * q] = (uint16_t)(w[h][q] & 0xFFFFu);
@@ -105,15 +107,26 @@ hipError_t launch_palette_probe(float *out, hipStream_t stream) {
   return hipGetLastError();
 }
 
-hipError_t launch_decode_dense(const uint4 *tiles, const float *scales, const float4 *lut, int M, int K, int RG, int CG,
-                               bool f16, uint16_t *out, hipStream_t stream) {
-  const size_t slots = (size_t)RG * CG * 64;
+hipError_t launch_decode_rows(const uint4 *tiles, const float *scales, const float4 *lut, int M, int K, int CG,
+                              int row_begin, int rows, bool f16, uint16_t *out, hipStream_t stream) {
+  const int g_begin = row_begin / kTileRows;
+  const int row_end = row_begin + rows;
+  const int groups = (row_end + kTileRows - 1) / kTileRows - g_begin;
+  const size_t slots = (size_t)groups * CG * 64;
   const dim3 grid((unsigned)((slots + 255) / 256));
   if (f16)
-    hipLaunchKernelGGL(decode_dense_kernel<true>, grid, dim3(256), 0, stream, tiles, scales, lut, M, K, RG, CG, out);
+    hipLaunchKernelGGL(decode_dense_kernel<true>, grid, dim3(256), 0, stream, tiles, scales, lut, M, K, CG, g_begin,
+                       groups, row_end, out);
   else
-    hipLaunchKernelGGL(decode_dense_kernel<false>, grid, dim3(256), 0, stream, tiles, scales, lut, M, K, RG, CG, out);
+    hipLaunchKernelGGL(decode_dense_kernel<false>, grid, dim3(256), 0, stream, tiles, scales, lut, M, K, CG, g_begin,
+                       groups, row_end, out);
   return hipGetLastError();
+}
+
+hipError_t launch_decode_dense(const uint4 *tiles, const float *scales, const float4 *lut, int M, int K, int RG, int CG,
+                               bool f16, uint16_t *out, hipStream_t stream) {
+  (void)RG;
+  return launch_decode_rows(tiles, scales, lut, M, K, CG, 0, M, f16, out, stream);
 }
 
 }  // namespace tx
