@@ -79,6 +79,27 @@ int tx_linear(uint64_t handle, const void *x, int x_dtype, int64_t x_numel, int6
 int tx_linear_noalloc(uint64_t handle, const void *x, int x_dtype, int64_t x_numel, int64_t x_last,
                       int device, void *y, void *stream);
 
+/* FP4 hybrid prefill staging and GEMM. Replace texelator_quantize_activation_fp4[_out]
+ * (texelator_cuda.cu:1154-1178, :1202-1233), texelator_decode_weight_fp4[_out] (:1179-1201,
+ * :1234-1260) and the torch._scaled_mm call of texelator/runtime.py:110-116. The format is gfx950's
+ * block-scaled MFMA format, MXFP4 (OCP MX v1.0): E2M1 values, two per byte with the even column in
+ * the low nibble, row-major [rows][K/2]; one E8M0 scale (2^(e - 127)) per 32 values, row-major
+ * [rows][K/32]. The reference writes NVFP4 (an E4M3 scale per 16 values, Blackwell's blocked scale
+ * layout) for its own FP4 GEMM. Group quantization: e = floor(log2(amax)) - 2 + 127 clamped to
+ * [0, 254] (0 for an all-zero group); value v -> E2M1 of v * 2^(127 - e), nearest, ties to even,
+ * saturated at 6, sign bit = sign of v.
+ *   tx_quantize_activation_fp4: x device bf16 [tokens][K], K a multiple of 32.
+ *   tx_decode_weight_fp4: the handle's fp32 products palette * row scale (before 16-bit
+ *     rounding, as the reference's quantizer), M rows; K a multiple of 32.
+ *   tx_fp4_gemm: y [tokens][M] bf16 = round(sum_k deq(x)[t][k] * deq(w)[m][k]) with fp32
+ *     accumulation (v_mfma_scale_f32_32x32x64_f8f6f4), then + bias [M] (bf16, or NULL) with a
+ *     second rounding; K a multiple of 64. Packed operands 16-byte aligned. */
+int tx_quantize_activation_fp4(const void *x, int x_dtype, int64_t tokens, int64_t K, uint8_t *packed,
+                               uint8_t *scales, int device, void *stream);
+int tx_decode_weight_fp4(uint64_t handle, uint8_t *packed, uint8_t *scales, void *stream);
+int tx_fp4_gemm(const uint8_t *x_packed, const uint8_t *x_scales, const uint8_t *w_packed, const uint8_t *w_scales,
+                const void *bias, int64_t tokens, int64_t M, int64_t K, void *y, int device, void *stream);
+
 /* Size in bytes of tx_linear_noalloc's static scratch array. */
 int tx_noalloc_scratch_bytes(int64_t *bytes);
 

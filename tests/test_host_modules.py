@@ -104,10 +104,56 @@ def test_decode_only_linear_routes_single_tokens():
     assert calls == ["bc4", "dense"]
 
 
-def test_fp4_hybrid_cannot_be_enabled():
-    runtime.set_fp4_hybrid(False)
-    with pytest.raises(RuntimeError, match="no gfx950 counterpart"):
-        runtime.set_fp4_hybrid(True)
+def test_fp4_hybrid_dispatch(monkeypatch):
+    """The hybrid takes only bf16 calls of 512 tokens on its MLP shapes while it is on
+    (reference runtime.py:119-131); ``free`` turns it off."""
+    calls = []
+
+    class Ext:
+        @staticmethod
+        def shape(handle):
+            return {1: (5120, 17408), 2: (17408, 5120), 3: (5120, 5120)}[handle]
+
+        @staticmethod
+        def linear(handle, x):
+            calls.append(("linear", handle, x.shape[0]))
+            return torch.zeros(x.shape[0], Ext.shape(handle)[0])
+
+        @staticmethod
+        def quantize_activation_fp4_out(x, packed, scales):
+            assert packed.shape == (x.shape[0], x.shape[1] // 2) and scales.shape == (x.shape[0], x.shape[1] // 32)
+            calls.append(("quantize", x.shape[0]))
+
+        @staticmethod
+        def decode_weight_fp4_out(handle, packed, scales):
+            calls.append(("decode", handle))
+
+        @staticmethod
+        def fp4_gemm(xp, xs, wp, ws):
+            calls.append(("gemm", xp.shape[0], wp.shape[0]))
+            return torch.zeros(xp.shape[0], wp.shape[0], dtype=torch.bfloat16)
+
+        @staticmethod
+        def free(handle):
+            calls.append(("free", handle))
+
+    monkeypatch.setattr(runtime, "extension", lambda verbose=False: Ext)
+    x512 = torch.zeros(512, 17408, dtype=torch.bfloat16)
+    runtime._linear_dispatch(1, x512)
+    assert calls == [("linear", 1, 512)]          # off by default
+    calls.clear()
+    runtime.set_fp4_hybrid(True)
+    assert runtime._linear_dispatch(1, x512).shape == (512, 5120)
+    assert calls == [("quantize", 512), ("decode", 1), ("gemm", 512, 5120)]
+    calls.clear()
+    runtime._linear_dispatch(1, torch.zeros(511, 17408, dtype=torch.bfloat16))
+    runtime._linear_dispatch(1, torch.zeros(512, 17408, dtype=torch.float16))
+    runtime._linear_dispatch(3, torch.zeros(512, 5120, dtype=torch.bfloat16))
+    assert [c[0] for c in calls] == ["linear", "linear", "linear"]
+    calls.clear()
+    runtime.free([1])
+    runtime._linear_dispatch(2, torch.zeros(512, 5120, dtype=torch.bfloat16))
+    assert calls == [("free", 1), ("linear", 2, 512)]
 
 
 @pytest.mark.parametrize("tokens,bucket", [(1, 32), (32, 32), (33, 128), (512, 512), (513, 2048), (65535, 65535)])

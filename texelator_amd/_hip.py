@@ -331,10 +331,83 @@ def _no_counterpart(name: str):
     return unsupported
 
 
-# The reference's CUDA-only diagnostics and NVFP4 staging (texelator_cuda.cu:1085-1152, :1514-1536).
+# The reference's CUDA-only diagnostics (texelator_cuda.cu:1514-1536).
 pipeline_kernel_info = _no_counterpart("pipeline_kernel_info")
 graphics_kernel_info = _no_counterpart("graphics_kernel_info")
-quantize_activation_fp4 = _no_counterpart("quantize_activation_fp4")
-decode_weight_fp4 = _no_counterpart("decode_weight_fp4")
-quantize_activation_fp4_out = _no_counterpart("quantize_activation_fp4_out")
-decode_weight_fp4_out = _no_counterpart("decode_weight_fp4_out")
+
+
+# FP4 hybrid staging (texelator_cuda.cu:1154-1260) in gfx950's MXFP4 format: packed E2M1 values
+# uint8 [rows][K/2] (even column in the low nibble) and one E8M0 scale uint8 per 32 values
+# [rows][K/32]. The reference's NVFP4 scales (E4M3 per 16, blocked) feed Blackwell's FP4 GEMM;
+# these feed fp4_gemm.
+def _fp4_buffers(rows: int, k: int, device: torch.device) -> tuple[torch.Tensor, torch.Tensor]:
+    return (torch.empty((rows, k // 2), dtype=torch.uint8, device=device),
+            torch.empty((rows, k // 32), dtype=torch.uint8, device=device))
+
+
+def _check_fp4_out(packed: torch.Tensor, scales: torch.Tensor, rows: int, k: int, device: torch.device) -> None:
+    _require(packed.is_cuda and packed.is_contiguous() and packed.dtype == torch.uint8 and
+             tuple(packed.shape) == (rows, k // 2) and packed.device == device,
+             f"packed must be contiguous CUDA uint8 [{rows}, {k // 2}]")
+    _require(scales.is_cuda and scales.is_contiguous() and scales.dtype == torch.uint8 and
+             tuple(scales.shape) == (rows, k // 32) and scales.device == device,
+             f"scales must be contiguous CUDA uint8 [{rows}, {k // 32}]")
+
+
+def quantize_activation_fp4_out(x: torch.Tensor, packed: torch.Tensor, scales: torch.Tensor) -> None:
+    _require(x.is_cuda and x.is_contiguous() and x.dtype == torch.bfloat16 and x.dim() == 2,
+             "activation must be contiguous CUDA BF16 [tokens,K]")
+    rows, k = x.shape
+    _require(k % 32 == 0, "activation K must be divisible by 32")
+    _check_fp4_out(packed, scales, rows, k, x.device)
+    x = _aligned(x)
+    check(_lib.load().tx_quantize_activation_fp4(ctypes.c_void_p(x.data_ptr()), _DTYPE_CODE[x.dtype], rows, k,
+                                                  ctypes.c_void_p(packed.data_ptr()), ctypes.c_void_p(scales.data_ptr()),
+                                                  x.device.index, _stream(x.device)))
+
+
+def quantize_activation_fp4(x: torch.Tensor) -> list[torch.Tensor]:
+    _require(x.is_cuda and x.dim() == 2, "activation must be contiguous CUDA BF16 [tokens,K]")
+    packed, scales = _fp4_buffers(x.shape[0], x.shape[1], x.device)
+    quantize_activation_fp4_out(x, packed, scales)
+    return [packed, scales]
+
+
+def decode_weight_fp4_out(handle: int, packed: torch.Tensor, scales: torch.Tensor) -> None:
+    _require(bool(handle), "null Texelator handle")
+    m, k = shape(handle)
+    device = packed.device
+    _check_fp4_out(packed, scales, m, k, device)
+    check(_lib.load().tx_decode_weight_fp4(handle, ctypes.c_void_p(packed.data_ptr()),
+                                           ctypes.c_void_p(scales.data_ptr()), _stream(device)))
+
+
+def decode_weight_fp4(handle: int) -> list[torch.Tensor]:
+    _require(bool(handle), "null Texelator handle")
+    m, k = shape(handle)
+    packed, scales = _fp4_buffers(m, k, torch.device("cuda", torch.cuda.current_device()))
+    decode_weight_fp4_out(handle, packed, scales)
+    return [packed, scales]
+
+
+def fp4_gemm(x_packed: torch.Tensor, x_scales: torch.Tensor, w_packed: torch.Tensor, w_scales: torch.Tensor,
+             bias: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """``y = deq(x) @ deq(w)^T`` (bf16, fp32 accumulation) ``(+ bias)``, the block-scaled GEMM the
+    reference runs as ``torch._scaled_mm`` (``runtime.py:110-116``)."""
+    tokens, m = x_packed.shape[0], w_packed.shape[0]
+    k = 2 * x_packed.shape[1]
+    device = x_packed.device
+    _check_fp4_out(x_packed, x_scales, tokens, k, device)
+    _check_fp4_out(w_packed, w_scales, m, k, device)
+    _require(k % 64 == 0, "FP4 GEMM K must be a multiple of 64")
+    if bias is not None:
+        _require(bias.is_cuda and bias.dtype == torch.bfloat16 and bias.numel() == m and bias.is_contiguous(),
+                 "bias must be contiguous CUDA BF16 [M]")
+    y = torch.empty((tokens, m), dtype=torch.bfloat16, device=device) if out is None else out
+    _require(y.dtype == torch.bfloat16 and y.is_contiguous() and tuple(y.shape) == (tokens, m),
+             f"output must be contiguous BF16 [{tokens}, {m}]")
+    check(_lib.load().tx_fp4_gemm(ctypes.c_void_p(x_packed.data_ptr()), ctypes.c_void_p(x_scales.data_ptr()),
+                                  ctypes.c_void_p(w_packed.data_ptr()), ctypes.c_void_p(w_scales.data_ptr()),
+                                  ctypes.c_void_p(None if bias is None else bias.data_ptr()), tokens, m, k,
+                                  ctypes.c_void_p(y.data_ptr()), device.index, _stream(device)))
+    return y

@@ -36,6 +36,9 @@ SIGNATURES = {
     "tx_workspace_bytes": (_I32, [_U64, _I64, ctypes.POINTER(_I64)]),
     "tx_linear_noalloc": (_I32, [_U64, _P, _I32, _I64, _I64, _I32, _P, _P]),
     "tx_noalloc_scratch_bytes": (_I32, [ctypes.POINTER(_I64)]),
+    "tx_quantize_activation_fp4": (_I32, [_P, _I32, _I64, _I64, _P, _P, _I32, _P]),
+    "tx_decode_weight_fp4": (_I32, [_U64, _P, _P, _P]),
+    "tx_fp4_gemm": (_I32, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _P, _I32, _P]),
     "tx_linear_f32": (_I32, [_U64, _P, _I64, _P, _P]),
     "tx_prefill": (_I32, [_U64, _I32, _P, _I32, _I64, _P, _P, _I64, _P]),
     "tx_set_lookahead": (_I32, [_U64, _I32]),

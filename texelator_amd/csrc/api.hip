@@ -425,6 +425,51 @@ int tx_linear_noalloc(uint64_t value, const void *x, int x_dtype, int64_t x_nume
   return run_gemv(h, x, f16, tokens, y, false, s, partials);
 }
 
+int tx_quantize_activation_fp4(const void *x, int x_dtype, int64_t tokens, int64_t K, uint8_t *packed, uint8_t *scales,
+                               int device, void *stream) {
+  g_last_error.clear();
+  if (x_dtype != TX_DTYPE_BF16) return fail(TX_ERR_INVALID, "activation must be contiguous CUDA BF16 [tokens,K]");
+  if (K <= 0 || K % 32 != 0) return fail(TX_ERR_INVALID, "activation K must be a positive multiple of 32");
+  if (tokens < 0 || tokens * (K / 32) > 0x7FFFFFFF) return fail(TX_ERR_INVALID, "activation too large");
+  if (!x || !packed || !scales) return fail(TX_ERR_INVALID, "null pointer");
+  if (reinterpret_cast<uintptr_t>(x) % 16 != 0 || reinterpret_cast<uintptr_t>(packed) % 16 != 0)
+    return fail(TX_ERR_INVALID, "activation and packed output must be 16-byte aligned");
+  if (tokens == 0) return TX_OK;
+  DeviceGuard guard(device);
+  TX_HIP(tx::launch_quantize_activation_fp4(static_cast<const uint16_t *>(x), tokens, (int)K, packed, scales,
+                                            reinterpret_cast<hipStream_t>(stream)));
+  return TX_OK;
+}
+
+int tx_decode_weight_fp4(uint64_t value, uint8_t *packed, uint8_t *scales, void *stream) {
+  g_last_error.clear();
+  Handle *h = as_handle(value);
+  if (!h) return fail(TX_ERR_INVALID, "null Texelator handle");
+  if (h->K % 32 != 0) return fail(TX_ERR_INVALID, "weight K must be a multiple of 32");
+  if (!packed || !scales) return fail(TX_ERR_INVALID, "null pointer");
+  if (reinterpret_cast<uintptr_t>(packed) % 16 != 0) return fail(TX_ERR_INVALID, "packed output must be 16-byte aligned");
+  DeviceGuard guard(h->device);
+  TX_HIP(tx::launch_quantize_weight_fp4(h->tiles, h->scales, h->M, h->K, h->RG, h->CG, packed, scales,
+                                        reinterpret_cast<hipStream_t>(stream)));
+  return TX_OK;
+}
+
+int tx_fp4_gemm(const uint8_t *x_packed, const uint8_t *x_scales, const uint8_t *w_packed, const uint8_t *w_scales,
+                const void *bias, int64_t tokens, int64_t M, int64_t K, void *y, int device, void *stream) {
+  g_last_error.clear();
+  if (K <= 0 || K % 64 != 0) return fail(TX_ERR_INVALID, "FP4 GEMM K must be a positive multiple of 64");
+  if (M <= 0 || M > 0x7FFFFFFF || tokens < 0 || tokens > 0x7FFFFFFF) return fail(TX_ERR_INVALID, "FP4 GEMM shape out of range");
+  if (!x_packed || !x_scales || !w_packed || !w_scales || !y) return fail(TX_ERR_INVALID, "null pointer");
+  if (reinterpret_cast<uintptr_t>(x_packed) % 16 != 0 || reinterpret_cast<uintptr_t>(w_packed) % 16 != 0)
+    return fail(TX_ERR_INVALID, "packed operands must be 16-byte aligned");
+  if (tokens == 0) return TX_OK;
+  DeviceGuard guard(device);
+  TX_HIP(tx::launch_fp4_gemm(x_packed, x_scales, w_packed, w_scales, static_cast<const uint16_t *>(bias),
+                             static_cast<uint16_t *>(y), (int)tokens, (int)M, (int)K,
+                             reinterpret_cast<hipStream_t>(stream)));
+  return TX_OK;
+}
+
 int tx_noalloc_scratch_bytes(int64_t *bytes) {
   g_last_error.clear();
   if (!bytes) return fail(TX_ERR_INVALID, "null output");

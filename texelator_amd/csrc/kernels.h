@@ -93,6 +93,15 @@ bool dense_gemm(int device, bool f16, int rows, int64_t tokens, int K, const voi
                 int64_t ldy, void *gemm_workspace, hipStream_t stream, std::string &error);
 hipError_t launch_add_bias(void *y, const void *bias, int64_t tokens, int M, bool f16, hipStream_t stream);
 
+// MXFP4 staging and GEMM of the FP4 hybrid prefill (fp4.hip). Groups of 32 along K (K a multiple
+// of 64 for the GEMM): packed E2M1 [rows][K/2], E8M0 scales [rows][K/32].
+hipError_t launch_quantize_activation_fp4(const uint16_t *x, int64_t tokens, int K, uint8_t *packed, uint8_t *scales,
+                                          hipStream_t stream);
+hipError_t launch_quantize_weight_fp4(const uint4 *tiles, const float *scales, int M, int K, int RG, int CG,
+                                      uint8_t *packed, uint8_t *group_scales, hipStream_t stream);
+hipError_t launch_fp4_gemm(const uint8_t *xq, const uint8_t *xs, const uint8_t *wq, const uint8_t *ws,
+                           const uint16_t *bias, uint16_t *y, int tokens, int M, int K, hipStream_t stream);
+
 // Decoder-layer helpers (decoder.hip).
 struct SplitSource;
 hipError_t launch_add_rmsnorm(float *h, const uint16_t *delta, const uint16_t *weight, float eps, uint16_t *out,

@@ -11,8 +11,9 @@ Public names and their meaning follow the reference's ``texelator/runtime.py`` (
   row-chunk packer, :func:`_pack_rows`, which frees what it packed if a later chunk fails;
 * both installers go through :func:`_swap_linears`, which resolves every target module before
   packing anything and frees the packed handles if a replacement fails;
-* the NVFP4 prefill experiment (``runtime.py:66-117``) has no gfx950 counterpart and cannot be
-  enabled; one token always runs the decode GEMV, whatever the prefill threshold.
+* the opt-in FP4 hybrid prefill (``runtime.py:21-23, 66-131``) quantizes to MXFP4, the format
+  of gfx950's block-scaled MFMA, where the reference quantizes to NVFP4 for Blackwell; one token
+  always runs the decode GEMV, whatever the prefill threshold.
 """
 from __future__ import annotations
 
@@ -52,10 +53,46 @@ def extension(verbose: bool = False):
     return _native
 
 
+# ---------------------------------------------------------------------------------------------
+# FP4 hybrid prefill (opt-in)
+
+# The (M, K) shapes and the token count the hybrid path takes (the reference's MLP shapes).
+FP4_HYBRID_SHAPES = frozenset({(5120, 17408), (17408, 5120)})
+FP4_HYBRID_TOKENS = 512
+
+
+class _Fp4State:
+    """Whether the hybrid is on, and its staging buffers per (device, tokens, M, K)."""
+
+    enabled = False
+    buffers: dict[tuple[int, int, int, int], tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]] = {}
+
+
 def set_fp4_hybrid(enabled: bool) -> None:
-    """Disabling is a no-op; enabling raises: there is no NVFP4 prefill on gfx950."""
-    if enabled:
-        raise RuntimeError("the NVFP4 hybrid prefill has no gfx950 counterpart in this build")
+    """Turn the FP4 hybrid prefill on or off (off by default; ``free`` turns it off)."""
+    _Fp4State.enabled = bool(enabled)
+
+
+def _fp4_staging(device: torch.device, tokens: int, m: int, k: int):
+    key = (device.index or 0, tokens, m, k)
+    staged = _Fp4State.buffers.get(key)
+    if staged is None:
+        def uint8(*shape):
+            return torch.empty(shape, dtype=torch.uint8, device=device)
+        staged = (uint8(tokens, k // 2), uint8(tokens, k // 32), uint8(m, k // 2), uint8(m, k // 32))
+        _Fp4State.buffers[key] = staged
+    return staged
+
+
+def _fp4_linear(handle: int, x: torch.Tensor, m: int, k: int) -> torch.Tensor:
+    """The activation and the handle's weights quantized to MXFP4, then the block-scaled GEMM
+    (bf16 output). As on the reference's path, the handle's bias is not added."""
+    ext = extension()
+    flat = x.reshape(-1, k)
+    x_packed, x_scales, w_packed, w_scales = _fp4_staging(x.device, flat.shape[0], m, k)
+    ext.quantize_activation_fp4_out(flat, x_packed, x_scales)
+    ext.decode_weight_fp4_out(handle, w_packed, w_scales)
+    return ext.fp4_gemm(x_packed, x_scales, w_packed, w_scales).reshape(*x.shape[:-1], m)
 
 
 # ---------------------------------------------------------------------------------------------
@@ -63,8 +100,14 @@ def set_fp4_hybrid(enabled: bool) -> None:
 
 
 def _linear_dispatch(handle: int, x: torch.Tensor) -> torch.Tensor:
-    """One handle's ``x @ W^T (+ its bias)``; the native call picks the GEMV or the prefill tile."""
-    return extension().linear(handle, x)
+    """One handle's ``x @ W^T (+ its bias)``: the FP4 hybrid for its shapes at 512 tokens when it
+    is on, otherwise the native call, which picks the GEMV or the prefill tile."""
+    ext = extension()
+    if _Fp4State.enabled and x.dtype == torch.bfloat16:
+        m, k = ext.shape(handle)
+        if x.numel() == FP4_HYBRID_TOKENS * k and (m, k) in FP4_HYBRID_SHAPES:
+            return _fp4_linear(handle, x, m, k)
+    return ext.linear(handle, x)
 
 
 def bc4_linear(handles: list[int], x: torch.Tensor) -> torch.Tensor:
@@ -292,7 +335,10 @@ def _release(handles: Iterable[int]) -> None:
 
 
 def free(handles: list[int]) -> None:
-    """Wait for all queued GPU work, then release every handle."""
+    """Wait for all queued GPU work, release every handle, and turn the FP4 hybrid off (dropping
+    its staging buffers)."""
     if torch.cuda.is_available():
         torch.cuda.synchronize()
     _release(handles)
+    _Fp4State.enabled = False
+    _Fp4State.buffers.clear()
