@@ -36,6 +36,49 @@ def test_palette_probe_bitwise_equals_cpu_palette(ext):
     assert hashlib.sha256(probe.astype("<f4").tobytes()).hexdigest() == bc4.palette_sha256()
 
 
+def _every_endpoint_pair_blocks() -> np.ndarray:
+    """255 rows x 255 blocks: row r has e0 = r - 127, block b has e1 = b - 127, and position p of
+    every block selects palette slot p % 8, so all 65025 endpoint pairs and all eight slots occur."""
+    field = sum((p % 8) << (3 * p) for p in range(16)).to_bytes(6, "little")
+    blocks = np.empty((255, 255, 8), dtype=np.uint8)
+    blocks[:, :, 0] = (np.arange(255) - 127).astype(np.int8).view(np.uint8)[:, None]
+    blocks[:, :, 1] = (np.arange(255) - 127).astype(np.int8).view(np.uint8)[None, :]
+    blocks[:, :, 2:] = np.frombuffer(field, dtype=np.uint8)
+    return blocks.reshape(255, 255 * 8)
+
+
+def test_every_endpoint_pair_decodes_exactly_in_gemv_and_prefill(ext, oracle_threads):
+    """The decoded weights inside the GEMV and the prefill kernels, read back exactly: one-hot
+    activations make every output a single decoded weight (times 1.0, plus exact zeros). Covers
+    every endpoint pair and palette slot, i.e. every entry of the palette-seed tables the
+    kernels copy into LDS, through the one-token and the 16-token GEMV and every prefill tile
+    (identity activations over the ragged K = 4080: the prefill returns W^T)."""
+    blocks = _every_endpoint_pair_blocks()
+    scales = lognormal_scales(255, 901)
+    m, k = 255, 255 * 16
+    want = clib.decode_bf16_bits(blocks, scales).view(np.int16)
+    want = torch.from_numpy(want).view(torch.bfloat16).float().numpy()
+    handle = _pack(ext, blocks, scales)
+    try:
+        for b in range(255):  # 16-token GEMV: the 16 positions of block b
+            x = torch.zeros((16, k), dtype=torch.bfloat16)
+            x[torch.arange(16), 16 * b + torch.arange(16)] = 1.0
+            got = ext.linear_f32(handle, x.cuda()).cpu().numpy()
+            assert np.array_equal(got, want[:, 16 * b:16 * b + 16].T), f"16-token GEMV, block {b}"
+        for col in (0, 7, 15, 1600, 4079):  # one-token GEMV
+            x = torch.zeros((1, k), dtype=torch.bfloat16)
+            x[0, col] = 1.0
+            got = ext.linear_f32(handle, x.cuda()).cpu().numpy()
+            assert np.array_equal(got[0], want[:, col]), f"one-token GEMV, column {col}"
+        eye = torch.eye(k, dtype=torch.bfloat16).cuda()
+        for candidate in range(5, 10):
+            got = ext.prefill(handle, candidate, eye).float().cpu().numpy()
+            assert np.array_equal(got, want.T), f"prefill candidate {candidate}"
+        torch.cuda.synchronize()
+    finally:
+        ext.free(handle)
+
+
 @pytest.mark.parametrize("m,k,seed", [(16, 128, 1), (37, 272, 2), (100, 16, 3), (64, 4096, 4), (5, 2064, 5)])
 def test_decode_dense_bit_exact(ext, oracle_threads, m, k, seed):
     blocks = random_blocks(m, k, seed)

@@ -252,20 +252,43 @@ __device__ __forceinline__ void decode_block(uint32_t a, uint32_t b, float scale
 struct PaletteTableStorage {
   float2 base[255];
   uint2 step[509];
+  uint2 pad[4];  // 6144 bytes: six whole 1 KiB wave loads (copy_seed_tables)
+};
+constexpr int kSeedTableBytes = 6144;
+
+// The same tables as a compile-time image in device memory (words in LDS order), so that a
+// workgroup copies them instead of computing them. Each quotient is the correctly rounded float
+// RN(n/d); double division rounded to float gives exactly that for every entry here (n and d
+// below 2^10: checked exhaustively against exact rational rounding), which is also what
+// decode_block's fma with a split reciprocal yields for every numerator here.
+struct SeedTableImage {
+  uint32_t words[kSeedTableBytes / 4];
 };
 
-__device__ __forceinline__ void build_palette_tables(PaletteTableStorage &t, int tid, int nthreads) {
-  for (int idx = tid; idx < 509; idx += nthreads) {
-    const int d = idx - 254;
-    const float f = (float)d;
-    const float rhi = d < 0 ? kInv889Hi : kInv635Hi;
-    const float rlo = d < 0 ? kInv889Lo : kInv635Lo;
-    t.step[idx] = make_uint2(__float_as_uint(__builtin_fmaf(f, rhi, f * rlo)), d < 0 ? 0xFFFFFFFFu : 0u);
-    if (idx < 255) {
-      const float e = (float)(idx - 127);
-      t.base[idx] = make_float2(__builtin_fmaf(e, kInv127Hi, e * kInv127Lo), 0.0f);
-    }
+constexpr SeedTableImage make_seed_table_image() {
+  SeedTableImage t{};
+  for (int i = 0; i < 255; ++i) t.words[2 * i] = __builtin_bit_cast(uint32_t, (float)((double)(i - 127) / 127.0));
+  for (int j = 0; j < 509; ++j) {
+    const int d = j - 254;
+    const double q = d < 0 ? (double)d / 889.0 : (double)d / 635.0;
+    t.words[510 + 2 * j] = __builtin_bit_cast(uint32_t, (float)q);
+    t.words[511 + 2 * j] = d < 0 ? 0xFFFFFFFFu : 0u;
   }
+  return t;
+}
+
+static __device__ const SeedTableImage kSeedTableImage = make_seed_table_image();
+
+// Copy the seed tables into LDS with direct buffer-to-LDS loads (1 KiB per wave load, waves
+// 0..nwaves-1 of the workgroup). The caller waits for them (vmcnt) before the barrier that
+// publishes them.
+__device__ __forceinline__ void copy_seed_tables(PaletteTableStorage &t, int wave, int lane, int nwaves) {
+  const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<SeedTableImage *>(&kSeedTableImage), (short)0, kSeedTableBytes, 0x00020000);
+  for (int q = wave; q < kSeedTableBytes / 1024; q += nwaves)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        rsrc, (__attribute__((address_space(3))) void *)(reinterpret_cast<char *>(&t) + 1024 * q), 16,
+        1024 * q + 16 * lane, 0, 0, 0);
 }
 
 // 8 * eb from the 2-bit endpoint fields in bits 3-4 of each byte: a byte offset into the tables.

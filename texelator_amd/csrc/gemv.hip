@@ -68,6 +68,25 @@ __device__ __forceinline__ uint4 load_x8(const uint16_t *x, int k, int K) {
   return k < K ? *reinterpret_cast<const uint4 *>(x + k) : make_uint4(0, 0, 0, 0);
 }
 
+// LDS chunks (16 bytes, 8 activations) the one-token x slice of `columns` tile columns occupies:
+// whole 1 KiB wave loads, so a multiple of 64.
+__host__ __device__ constexpr int x_stage_chunks(int columns) { return (columns * 16 + 63) / 64 * 64; }
+
+// One-token x slice into LDS: chunks first .. first + count - 1 of x (a K-element bf16 vector,
+// 16-byte aligned) to xs[0 ..], by direct buffer-to-LDS loads (no registers, no VALU per chunk;
+// wave w issues the 1 KiB loads w, w + 4, ...). The buffer descriptor ends at K, so chunks at or
+// past K read as zeros (K is a multiple of 16: a chunk is wholly in or out). Up to
+// x_stage_chunks(count / 16) chunks are written. The caller waits for the loads (vmcnt) before
+// the barrier that publishes them.
+__device__ __forceinline__ void stage_x_lds(uint4 *xs, const uint16_t *x, int K, int first, int count, int wave,
+                                            int lane) {
+  const __amdgpu_buffer_rsrc_t rsrc =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(x), (short)0, K * 2, 0x00020000);
+  for (int base = wave * 64; base < count; base += kThreads)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void *)(xs + base), 16,
+                                             (first + base + lane) * 16, 0, 0, 0);
+}
+
 // One tile for one lane: decode both blocks and accumulate 4 MFMAs (block 0 into acc0, block 1
 // into acc1; the two are added at the end in a fixed order).
 template <bool F16>
@@ -137,7 +156,7 @@ template <bool F16, int LA, bool MULTI, bool F32OUT, bool LUT>
 __global__ __launch_bounds__(kThreads, LUT ? 4 : TX_GEMV_WAVES_PER_EU) void gemv_kernel(GemvParams p) {
   static_assert(!LUT || LA >= 2, "LUT mode prefetches the palette rows of the next tile");
   extern __shared__ uint4 xs[];  // single token: x slice, 16 uint4 (128 bf16) per tile column
-  __shared__ PaletteTableStorage tables;
+  __shared__ __attribute__((aligned(16))) PaletteTableStorage tables;
   constexpr int kRedTokens = MULTI ? 16 : 1;  // one token: 256 bytes of LDS instead of 4 KiB
   __shared__ float red[kWaves][kRedTokens][16];  // [wave][token][row]
 
@@ -178,13 +197,9 @@ __global__ __launch_bounds__(kThreads, LUT ? 4 : TX_GEMV_WAVES_PER_EU) void gemv
   const int row = g * kTileRows + i;
   const float scale = p.scales[row];  // loaded with the tiles and x, not after the barrier
 
-  if constexpr (!LUT) build_palette_tables(tables, threadIdx.x, kThreads);
-  if constexpr (!MULTI) {
-    for (int idx = threadIdx.x; idx < nc * 16; idx += kThreads) {
-      const int k0 = (c_begin * 16 + idx) * 8;
-      xs[idx] = load_x8(x, k0, p.K);  // K is a multiple of 16: a chunk of 8 is wholly in or out
-    }
-  }
+  if constexpr (!MULTI) stage_x_lds(xs, x, p.K, c_begin * 16, nc * 16, wave, lane);
+  if constexpr (!LUT) copy_seed_tables(tables, wave, lane, kWaves);
+  if constexpr (!MULTI || !LUT) __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): x and the tables have landed
   __syncthreads();
 
   const uint32_t pm = pm_scale_pair<F16>(scale);
@@ -192,10 +207,9 @@ __global__ __launch_bounds__(kThreads, LUT ? 4 : TX_GEMV_WAVES_PER_EU) void gemv
   const uint16_t *xrow = x + (size_t)(t0 + min(i, tc - 1)) * p.K;
 
   f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-  // Single token: only B-operand column 0 (lanes with i == 0) carries x; the other columns
-  // produce output columns that are never read, so their lanes skip the LDS reads and keep
-  // whatever their registers hold.
-  XFrag xf = {};
+  // Single token: every B-operand column gets the same x (the 16 lanes of a K chunk read one LDS
+  // address, a broadcast); only output column 0 is read.
+  XFrag xf;
   auto load_xf = [&](int j) {
     const int col = j * kWaves + wave;  // tile column within this split
     if constexpr (MULTI) {
@@ -204,7 +218,7 @@ __global__ __launch_bounds__(kThreads, LUT ? 4 : TX_GEMV_WAVES_PER_EU) void gemv
       xf.x1 = load_x8(xrow, k + 8, p.K);
       xf.x2 = load_x8(xrow, k + 16, p.K);
       xf.x3 = load_x8(xrow, k + 24, p.K);
-    } else if (i == 0) {
+    } else {
       const uint4 *xv = xs + col * 16 + kg * 4;
       xf.x0 = xv[0];
       xf.x1 = xv[1];
@@ -300,7 +314,7 @@ __global__ __launch_bounds__(kThreads, LUT ? 4 : TX_GEMV_WAVES_PER_EU) void gemv
 template <int LA>
 __global__ __launch_bounds__(kThreads, LA == 1 ? 6 : (LA == 2 ? 5 : 4)) void gemv_swiglu_kernel(GemvParams p) {
   extern __shared__ uint4 xs[];
-  __shared__ PaletteTableStorage tables;
+  __shared__ __attribute__((aligned(16))) PaletteTableStorage tables;
   __shared__ float red[2][kWaves][16];  // [gate|up][wave][row]
 
   const int g = blockIdx.x;
@@ -328,16 +342,17 @@ __global__ __launch_bounds__(kThreads, LA == 1 ? 6 : (LA == 2 ? 5 : 4)) void gem
   const int kg = lane >> 4;
   const float scale_g = p.scales[g * kTileRows + i];  // loaded with the tiles and x
   const float scale_u = p.scales[(g + half) * kTileRows + i];
-  build_palette_tables(tables, threadIdx.x, kThreads);
-  for (int idx = threadIdx.x; idx < nc * 16; idx += kThreads) xs[idx] = load_x8(x, idx * 8, p.K);
+  stage_x_lds(xs, x, p.K, 0, nc * 16, wave, lane);
+  copy_seed_tables(tables, wave, lane, kWaves);
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): x and the tables have landed
   __syncthreads();
 
   const uint32_t pm_g = pm_scale_pair<false>(scale_g);
   const uint32_t pm_u = pm_scale_pair<false>(scale_u);
   f32x4 ga0 = {0.f, 0.f, 0.f, 0.f}, ga1 = ga0, ua0 = ga0, ua1 = ga0;
-  XFrag xf = {};
+  XFrag xf;  // every column gets x (broadcast LDS reads); only output column 0 is read
   auto consume = [&](int u, int j) {
-    if (i == 0) {
+    {
       const uint4 *xv = xs + (j * kWaves + wave) * 16 + kg * 4;
       xf.x0 = xv[0];
       xf.x1 = xv[1];
@@ -430,7 +445,7 @@ void launch_splitk_reduce(const GemvParams &p, hipStream_t stream) {
 template <bool F16, int LA, bool MULTI, bool F32OUT>
 hipError_t launch_variant(const GemvParams &p, hipStream_t stream) {
   const int max_cols = (p.CG + p.ks - 1) / p.ks;
-  const size_t lds = MULTI ? 0 : (size_t)max_cols * 16 * sizeof(uint4);
+  const size_t lds = MULTI ? 0 : (size_t)x_stage_chunks(max_cols) * sizeof(uint4);
   dim3 grid(p.RG, p.ks, (p.tokens + 15) / 16);
   if (p.lut) {
     constexpr int kLutLA = LA < 2 ? 2 : LA;  // the palette-row prefetch needs a second tile in flight
@@ -459,7 +474,7 @@ hipError_t launch_la(const GemvParams &p, bool f32_out, hipStream_t stream) {
 }  // namespace
 
 hipError_t launch_gemv_swiglu(const GemvParams &p, int lookahead, hipStream_t stream) {
-  const size_t lds = (size_t)p.CG * 16 * sizeof(uint4);
+  const size_t lds = (size_t)x_stage_chunks(p.CG) * sizeof(uint4);
   const dim3 grid(p.RG / 2);
   switch (lookahead) {
     case 1: hipLaunchKernelGGL(gemv_swiglu_kernel<1>, grid, dim3(kThreads), lds, stream, p); break;
@@ -507,7 +522,7 @@ int gemv_resident_per_cu(int lookahead, int columns) {
     default: return 0;
   }
   int n = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, kThreads, (size_t)columns * 16 * sizeof(uint4)) != hipSuccess) {
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, kThreads, (size_t)x_stage_chunks(columns) * sizeof(uint4)) != hipSuccess) {
     (void)hipGetLastError();
     return 0;
   }

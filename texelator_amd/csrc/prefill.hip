@@ -131,7 +131,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillParams p) {
   // one from the direct-to-LDS loads that fill the other and does not make them wait.
   __shared__ __attribute__((aligned(16))) uint16_t xs0[BT * kTileK];
   __shared__ __attribute__((aligned(16))) uint16_t xs1[BT * kTileK];
-  __shared__ PaletteTableStorage tables;
+  __shared__ __attribute__((aligned(16))) PaletteTableStorage tables;
 
   WorkItem w;
   if (!work_item(p, BT, BN, w)) return;
@@ -224,7 +224,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillParams p) {
   if constexpr (PIPE) load_tiles(first, 0);
 #pragma unroll
   for (int u = 0; u < NS; ++u) load_tiles(ring[u], u + D);
-  if constexpr (!LUT) build_palette_tables(tables, threadIdx.x, kThreads);
+  if constexpr (!LUT) copy_seed_tables(tables, wave, lane, kThreads / 64);
   __builtin_amdgcn_s_waitcnt(0x0F70);
   __syncthreads();
 
