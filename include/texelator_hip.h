@@ -107,7 +107,9 @@ int tx_noalloc_scratch_bytes(int64_t *bytes);
  * sums for tokens > 1 (with backend 1 and tokens >= the prefill threshold: the dense scratch of
  * min(tile_rows, M) decoded rows of K 16-bit weights, 256-byte aligned, plus 8 MiB for the library
  * GEMM), the one-token GEMV's split-K partials for
- * tokens == 1 (0 when the shape is not split). No reference counterpart (see tx_linear). */
+ * tokens == 1 (0 when the shape is not split, or when one workgroup per 16-row group runs all of
+ * its splits: 2 to 4 splits, row groups spreading evenly over the CUs, arithmetic palette). No
+ * reference counterpart (see tx_linear). */
 int tx_workspace_bytes(uint64_t handle, int64_t tokens, int64_t *bytes);
 
 /* Decode GEMV with float32 output and no bias, for parity checks (no reference counterpart:

@@ -79,6 +79,38 @@ def test_every_endpoint_pair_decodes_exactly_in_gemv_and_prefill(ext, oracle_thr
         ext.free(handle)
 
 
+@pytest.mark.parametrize("m,k", [(300, 2064), (7168, 5120), (2048, 2048), (256, 2048), (11008, 2048)])
+def test_fused_one_token_gemv_bitwise_equals_split_path(ext, oracle_threads, m, k):
+    """Shapes whose K splits run in one workgroup (row groups spread evenly over the CUs) give
+    exactly the split GEMV + reduce result. LUT mode with the defined palette decodes the same
+    weights but always takes the split path, so every output is compared bit for bit: fp32, bf16
+    with a bias, and the no-allocation entry point; such calls need no workspace."""
+    blocks = random_blocks(m, k, 951)
+    scales = lognormal_scales(m, 952)
+    bias = bf16_vector((m,), 953, scale=0.5).cuda()
+    x = bf16_vector((1, k), 954).cuda()
+    fused = _pack(ext, blocks, scales, bias)
+    split = _pack(ext, blocks, scales, bias)
+    try:
+        ext.set_palette_table(split, torch.from_numpy(bc4.palette()).cuda())
+        assert ext.workspace_bytes(fused, 1) == 0
+        assert ext.workspace_bytes(split, 1) > 0, "the shape must be split for the comparison to mean anything"
+        assert torch.equal(ext.linear_f32(fused, x), ext.linear_f32(split, x))
+        y = ext.linear(fused, x)
+        assert torch.equal(y, ext.linear(split, x))
+        y_noalloc = torch.empty_like(y)
+        ext.linear_noalloc_into(fused, x, y_noalloc)
+        assert torch.equal(y, y_noalloc)
+        torch.cuda.synchronize()
+        w = clib.decode_bf16_bits(blocks, scales)
+        ref = clib.matvec_f64(w, bf16_bits(x[0].cpu()))
+        got = ext.linear_f32(fused, x)[0].double().cpu().numpy()
+        assert max_rel_err_floor(ref, got) <= GEMV_TOL
+    finally:
+        ext.free(fused)
+        ext.free(split)
+
+
 @pytest.mark.parametrize("m,k,seed", [(16, 128, 1), (37, 272, 2), (100, 16, 3), (64, 4096, 4), (5, 2064, 5)])
 def test_decode_dense_bit_exact(ext, oracle_threads, m, k, seed):
     blocks = random_blocks(m, k, seed)

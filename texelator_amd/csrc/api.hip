@@ -218,8 +218,14 @@ tx::SplitSource split_source(const Handle *h) {
 
 // One-token K splits write ks * Mp fp32 partials to `partials` (the handle's own buffer, or the
 // static scratch of tx_linear_noalloc); several tokens run unsplit and write none.
+// One-token calls of this handle run every K split in one workgroup (gemv_fused_kernel).
+bool one_token_fused(const Handle *h) {
+  return !h->lut && tx::gemv_fused_profitable(h->RG, h->CG, h->gemv_splits, h->cus);
+}
+
 int64_t gemv_partials_bytes(const Handle *h, int64_t tokens) {
-  return tokens == 1 && h->gemv_splits > 1 ? (int64_t)h->gemv_splits * h->Mp * (int64_t)sizeof(float) : 0;
+  if (tokens != 1 || h->gemv_splits == 1 || one_token_fused(h)) return 0;
+  return (int64_t)h->gemv_splits * h->Mp * (int64_t)sizeof(float);
 }
 
 int run_gemv(Handle *h, const void *x, bool f16, int64_t tokens, void *y, bool f32_out, hipStream_t stream,
@@ -242,6 +248,7 @@ int run_gemv(Handle *h, const void *x, bool f16, int64_t tokens, void *y, bool f
   // One token: K splits reduced by a second kernel. Several tokens: one pass per 16 tokens.
   p.ks = tokens == 1 ? h->gemv_splits : 1;
   p.partials = partials;
+  p.fused = tokens == 1 && one_token_fused(h) ? 1 : 0;
   TX_HIP(tx::launch_gemv(p, h->lookahead, f32_out, stream));
   return TX_OK;
 }

@@ -11,7 +11,9 @@
 //     weights serves up to 16 tokens and the K reduction across lanes happens inside the MFMA;
 //   * the four waves' accumulators are summed through LDS in wave order;
 //   * with several splits each workgroup writes an fp32 partial row and a second kernel sums
-//     the partials in split order, so results never depend on scheduling.
+//     the partials in split order, so results never depend on scheduling; where the row groups
+//     spread evenly over the CUs, one workgroup instead runs every split of its row group and sums
+//     them in the same order (gemv_fused_kernel: the same bits, one launch).
 // Single-token calls stage x in LDS; multi-token calls read x through the cache hierarchy.
 #include "bc4_device.h"
 #include "elementwise.h"
@@ -74,15 +76,15 @@ __host__ __device__ constexpr int x_stage_chunks(int columns) { return (columns 
 
 // One-token x slice into LDS: chunks first .. first + count - 1 of x (a K-element bf16 vector,
 // 16-byte aligned) to xs[0 ..], by direct buffer-to-LDS loads (no registers, no VALU per chunk;
-// wave w issues the 1 KiB loads w, w + 4, ...). The buffer descriptor ends at K, so chunks at or
-// past K read as zeros (K is a multiple of 16: a chunk is wholly in or out). Up to
+// wave w of `waves` issues the 1 KiB loads w, w + waves, ...). The buffer descriptor ends at K, so
+// chunks at or past K read as zeros (K is a multiple of 16: a chunk is wholly in or out). Up to
 // x_stage_chunks(count / 16) chunks are written. The caller waits for the loads (vmcnt) before
 // the barrier that publishes them.
 __device__ __forceinline__ void stage_x_lds(uint4 *xs, const uint16_t *x, int K, int first, int count, int wave,
-                                            int lane) {
+                                            int lane, int waves = kWaves) {
   const __amdgpu_buffer_rsrc_t rsrc =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(x), (short)0, K * 2, 0x00020000);
-  for (int base = wave * 64; base < count; base += kThreads)
+  for (int base = wave * 64; base < count; base += 64 * waves)
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void *)(xs + base), 16,
                                              (first + base + lane) * 16, 0, 0, 0);
 }
@@ -305,6 +307,105 @@ __global__ __launch_bounds__(kThreads, LUT ? 4 : TX_GEMV_WAVES_PER_EU) void gemv
   }
 }
 
+// One token, every K split in one workgroup: 4 * ks waves (ks <= kFusedMaxSplits) for one 16-row
+// group, wave w doing exactly what wave w % 4 of split w / 4 does in gemv_kernel (same tile columns
+// and order, same MFMA chains, same acc0 + acc1), so each split's sum over its four waves (in wave
+// order) is gemv_kernel's partial, and the splits are then summed in split order, bias added and
+// the result cast as splitk_reduce_kernel does: bit-identical to gemv_kernel + the reduce, in one
+// launch and without partials in memory. The whole x row is staged in LDS once.
+constexpr int kFusedMaxSplits = 4;
+
+template <bool F16, int LA, bool F32OUT>
+__global__ __launch_bounds__(kThreads * kFusedMaxSplits, TX_GEMV_WAVES_PER_EU) void gemv_fused_kernel(GemvParams p) {
+  extern __shared__ uint4 xs[];  // the whole x row: 16 uint4 per tile column
+  __shared__ __attribute__((aligned(16))) PaletteTableStorage tables;
+  __shared__ float red[kWaves * kFusedMaxSplits][16];  // [wave][row]
+
+  const int g = blockIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int waves = kWaves * p.ks;
+  const int split = wave / kWaves, wq = wave % kWaves;  // split, and the wave's place within it
+  int c_begin = 0, c_end = p.CG;
+  if (p.ks > 1) {
+    c_begin = (int)((uint32_t)split * (uint32_t)p.CG / (uint32_t)p.ks);
+    c_end = (int)((uint32_t)(split + 1) * (uint32_t)p.CG / (uint32_t)p.ks);
+  }
+  const int nc = c_end - c_begin;
+  const int nt = nc > wq ? (nc - wq + kWaves - 1) / kWaves : 0;
+  const int64_t first_tile = (int64_t)g * p.CG + c_begin + min(wq, nc - 1);
+  const TileStream stream(p.tiles + first_tile * 64, ((int64_t)p.RG * p.CG - first_tile) * kTileBytes, lane);
+
+  constexpr int R = LA + 1;
+  uint4 ring[R];
+#pragma unroll
+  for (int u = 0; u < LA; ++u) ring[u] = stream.load(min(u, max(nt - 1, 0)), kWaves);
+
+  const int i = lane & 15;
+  const int kg = lane >> 4;
+  const float scale = p.scales[g * kTileRows + i];
+  stage_x_lds(xs, static_cast<const uint16_t *>(p.x), p.K, 0, p.CG * 16, wave, lane, waves);
+  copy_seed_tables(tables, wave, lane, waves);
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): x and the tables have landed
+  __syncthreads();
+
+  const uint32_t pm = pm_scale_pair<F16>(scale);
+  f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+  XFrag xf;
+  auto load_xf = [&](int j) {
+    const uint4 *xv = xs + (c_begin + j * kWaves + wq) * 16 + kg * 4;
+    xf.x0 = xv[0];
+    xf.x1 = xv[1];
+    xf.x2 = xv[2];
+    xf.x3 = xv[3];
+  };
+  int j0 = 0;
+  for (; j0 + R <= nt; j0 += R) {
+    progress_priority(nt - j0, nt);
+#pragma unroll
+    for (int u = 0; u < R; ++u) {
+      const int jn = min(j0 + u + LA, nt - 1);
+      ring[(u + LA) % R] = stream.load(jn, kWaves);
+      load_xf(j0 + u);
+      tile_mfma<F16>(ring[u], xf, scale, pm, tables, acc0, acc1);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < LA; ++u)
+    if (j0 + u < nt) {
+      load_xf(j0 + u);
+      tile_mfma<F16>(ring[u], xf, scale, pm, tables, acc0, acc1);
+    }
+
+  const f32x4 acc = acc0 + acc1;  // partial y[row 4kg + r] of this wave
+  if (i == 0) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) red[wave][kg * 4 + r] = acc[r];
+  }
+  __syncthreads();
+
+  if (threadIdx.x < 16) {
+    const int rr = threadIdx.x;
+    float total = 0.f;
+    for (int s = 0; s < p.ks; ++s) {
+      float part = red[kWaves * s][rr];
+#pragma unroll
+      for (int w = 1; w < kWaves; ++w) part += red[kWaves * s + w][rr];
+      total = s == 0 ? part : total + part;
+    }
+    const int out_row = g * kTileRows + rr;
+    if (out_row < p.M) {
+      if constexpr (F32OUT) {
+        static_cast<float *>(p.y)[out_row] = total;
+      } else {
+        if (p.bias) total += half_bits_to_float<F16>(static_cast<const uint16_t *>(p.bias)[out_row]);
+        if constexpr (F16) static_cast<_Float16 *>(p.y)[out_row] = (_Float16)total;
+        else static_cast<__bf16 *>(p.y)[out_row] = (__bf16)total;
+      }
+    }
+  }
+}
+
 // One-token GEMV of a merged [gate | up] handle (M = 2 * inter, inter a multiple of 16, one K
 // split) whose epilogue applies SwiGLU: out[r] = bf16(silu(bf16(gate_r)) * bf16(up_r)), exactly the
 // values tx_linear followed by tx_swiglu produce. Workgroup g computes gate row group g and up row
@@ -442,8 +543,24 @@ void launch_splitk_reduce(const GemvParams &p, hipStream_t stream) {
   }
 }
 
+// Tile columns up to which the fused kernel stages the whole x row (56 KiB of LDS: two workgroups
+// per CU with the seed tables).
+constexpr int kFusedMaxColumns = 224;
+
+bool fused_eligible(const GemvParams &p) {
+  return p.fused && p.tokens == 1 && !p.lut && !p.force_partials && p.ks > 1 && p.ks <= kFusedMaxSplits &&
+         p.CG <= kFusedMaxColumns;
+}
+
 template <bool F16, int LA, bool MULTI, bool F32OUT>
 hipError_t launch_variant(const GemvParams &p, hipStream_t stream) {
+  if constexpr (!MULTI) {
+    if (fused_eligible(p)) {
+      const size_t lds = (size_t)x_stage_chunks(p.CG) * sizeof(uint4);
+      hipLaunchKernelGGL((gemv_fused_kernel<F16, LA, F32OUT>), dim3(p.RG), dim3(kThreads * p.ks), lds, stream, p);
+      return hipGetLastError();
+    }
+  }
   const int max_cols = (p.CG + p.ks - 1) / p.ks;
   const size_t lds = MULTI ? 0 : (size_t)x_stage_chunks(max_cols) * sizeof(uint4);
   dim3 grid(p.RG, p.ks, (p.tokens + 15) / 16);
@@ -482,6 +599,12 @@ hipError_t launch_gemv_swiglu(const GemvParams &p, int lookahead, hipStream_t st
     default: hipLaunchKernelGGL(gemv_swiglu_kernel<4>, grid, dim3(kThreads), lds, stream, p); break;
   }
   return hipGetLastError();
+}
+
+bool gemv_fused_profitable(int RG, int CG, int ks, int cus) {
+  if (ks < 2 || ks > kFusedMaxSplits || CG > kFusedMaxColumns) return false;
+  const int tiles_per_wave = ((CG + ks - 1) / ks + kWaves - 1) / kWaves;
+  return tiles_per_wave <= 8 && (RG <= cus || 2 * RG >= 3 * cus);
 }
 
 bool gemv_lookahead_supported(int la) { return la == 1 || la == 2 || la == 3 || la == 4 || la == 6 || la == 8; }

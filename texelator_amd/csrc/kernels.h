@@ -21,7 +21,14 @@ struct GemvParams {
   int force_partials;      // write fp32 partials (no bias, no reduction) even when ks == 1
   int f16;                 // x, bias and y are fp16 (weights rounded to fp16) instead of bf16
   const float4 *lut;       // LUT mode: 255 x 255 x 8 fp32 palette table, or nullptr (defined palette)
+  int fused;               // one token: every K split in one workgroup (gemv_fused_profitable)
 };
+
+// Whether a one-token GEMV of RG row groups, CG tile columns and ks K splits runs all its splits in
+// one workgroup per row group (no partials in memory, no reduce launch; bit-identical results):
+// 2 to 4 splits, at most 8 tiles per wave, the whole x row in 56 KiB of LDS, and row groups that
+// spread evenly over `cus` CUs (at most one per CU, or at least one and a half).
+bool gemv_fused_profitable(int RG, int CG, int ks, int cus);
 
 // Single-token GEMV stages the x slice of a split in LDS: at most this many tile columns
 // (128 input features each) per split.
