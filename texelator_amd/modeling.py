@@ -128,14 +128,15 @@ class BC4Decoder:
 
     def __init__(self, config: DecoderConfig, max_context: int, device: torch.device | str = "cuda", seed: int = 0,
                  lookahead: int = 1, linear_source=None, depth_scaled: bool = True, embed_std: float = 1.0,
-                 fused: bool = True, split_decode: bool = True, gate_up_lookahead: int = 2):
+                 fused: bool = True, split_decode: bool = True, gate_up_lookahead: int = 1):
         """``linear_source(layer, name, m, k)`` may return ``(blocks, scales)`` device tensors for a
         linear (reference block layout). By default every linear is a seeded random BC4 matrix.
 
         ``lookahead`` is the decode GEMV lookahead of every handle but gate|up, which takes
-        ``gate_up_lookahead``: its fused SwiGLU GEMV with two tiles in flight measured 2% faster
-        on the 27B decode step (163.1 vs 160.0 tok/s; lookahead 4 158.4, and 2-4 on the split
-        q|k|v, o and down GEMVs 2-11% slower).
+        ``gate_up_lookahead``. Since the GEMV prologue copies x and the seed tables into LDS
+        without VALU work, one tile in flight is fastest for the fused SwiGLU GEMV too (37.8 vs
+        39.7 us per call at two, interleaved on one GPU); before that, two measured 2% faster on
+        the decode step. Lookahead 2-4 makes the split q|k|v, o and down GEMVs slower.
 
         The random init follows Hugging Face's for Qwen2: weights N(0, 0.02) (here as BC4), norms
         1, and q/k/v biases 0. The biases are still passed to the handles, so the kernels' bias
