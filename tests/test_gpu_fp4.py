@@ -79,6 +79,28 @@ def test_fp4_gemm_matches_dequantized_product(ext, tokens, m, k):
     assert torch.equal(yb, (y.float() + bias.cuda().float()[None, :]).to(torch.bfloat16))
 
 
+@pytest.mark.parametrize("tokens,m,k", [(37, 200, 1024), (130, 300, 5120), (256, 128, 128)])
+def test_fp4_gemm_staged_and_direct_kernels_agree_bitwise(ext, tokens, m, k):
+    """K a multiple of 128 with word-aligned scales takes the LDS-staged kernel; the same scales one
+    byte off a word boundary take the direct kernel. Same MFMAs in the same K order: same bits."""
+    x = _activations(tokens, k, 841)
+    w = _activations(m, k, 842)
+    xc, xe = mxfp4.quantize(x.float().numpy())
+    wc, we = mxfp4.quantize(w.float().numpy())
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+    def shifted(scales):  # the same bytes at an address one past a word boundary
+        flat = torch.empty(scales.size + 4, dtype=torch.uint8, device="cuda")
+        view = flat[1:1 + scales.size].view(scales.shape)
+        view.copy_(dev(scales))
+        return view
+
+    xp, wp = dev(mxfp4.pack(xc)), dev(mxfp4.pack(wc))
+    staged = ext.fp4_gemm(xp, dev(xe), wp, dev(we))
+    direct = ext.fp4_gemm(xp, shifted(xe), wp, shifted(we))
+    assert torch.equal(staged, direct)
+
+
 def test_fp4_hybrid_dispatch_on_a_reference_shape(ext):
     """At 512 tokens on (5120, 17408) the hybrid runs the explicit pipeline (bitwise), and stays
     within FP4 quantization error of the bf16 prefill of the same weights."""
