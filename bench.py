@@ -290,6 +290,46 @@ def prefill_only(torch, ext, runtime, hardware, device, args) -> int:
     return 0
 
 
+# The reference's FP4 hybrid shapes (texelator/runtime.py:66-131: its MLP at 512 tokens), as (M, K).
+FP4_SHAPES = [(17408, 5120), (5120, 17408)]
+
+
+def fp4_only(torch, ext, runtime, hardware, device, args) -> int:
+    """The FP4 hybrid prefill at ``--prompt`` tokens on the reference's two MLP shapes, each stage
+    timed over ``--layers`` distinct weight copies (back-to-back launches, HIP events): activation
+    quantization, weight requantization from the BC4 tiles, the block-scaled GEMM, and the bf16
+    prefill GEMM of the same matrices for comparison."""
+    lut = hardware.device_palette(device)
+    weights = encoded_weights(torch, FP4_SHAPES, lut)
+    stream = torch.cuda.current_stream()
+    tokens = args.prompt
+    out = {}
+    for m, k in FP4_SHAPES:
+        blocks, scales = weights[(m, k)]
+        handles = [runtime.pack_arrays(blocks, scales)[0] for _ in range(args.layers)]
+        x = torch.randn((tokens, k), device=device).to(torch.bfloat16)
+        xp, xs = ext.quantize_activation_fp4(x)
+        staged = [ext.decode_weight_fp4(h) for h in handles]
+        n = len(handles)
+        for h in handles:
+            ext.linear(h, x)
+        times = {
+            "bf16_prefill_us": timed_launches(torch, stream, lambda i: ext.linear(handles[i % n], x), 2 * n),
+            "quantize_us": timed_launches(torch, stream, lambda i: ext.quantize_activation_fp4_out(x, xp, xs), 2 * n),
+            "requantize_us": timed_launches(torch, stream, lambda i: ext.decode_weight_fp4_out(handles[i % n], *staged[i % n]),
+                                            2 * n),
+            "gemm_us": timed_launches(torch, stream, lambda i: ext.fp4_gemm(xp, xs, *staged[i % n]), 2 * n),
+        }
+        row = {key: round(value * 1e6, 2) for key, value in times.items()}
+        row["fp4_total_us"] = round(row["quantize_us"] + row["requantize_us"] + row["gemm_us"], 2)
+        row["gemm_tflops"] = round(2 * tokens * m * k / (times["gemm_us"] * 1e12), 1)
+        out[f"{m}x{k}"] = row
+        del staged
+        runtime.free(handles)
+    print(json.dumps({"fp4_only": True, "tokens": tokens, "copies": args.layers, "shapes": out}), flush=True)
+    return 0
+
+
 def model_section(torch, args, model_name: str | None = None, context: int | None = None) -> dict:
     """Prefill tok/s at ``--prompt`` tokens (reference protocol, texelator/prefill.py:63-131) and
     graph-replayed greedy decode tok/s from the prompt up to ``context``, on a random-init BC4
@@ -359,6 +399,9 @@ def main() -> int:
                         help="profiling mode: only the gate/up prefill GEMM at --prompt tokens over the layer copies")
     parser.add_argument("--tile", type=int, default=0, choices=range(0, 10),
                         help="with --prefill-only: prefill tile candidate 5..9 (0: the library's default)")
+    parser.add_argument("--fp4-only", action="store_true",
+                        help="only the FP4 hybrid prefill stages and the bf16 prefill on the reference's MLP "
+                             "shapes at --prompt tokens (its JSON)")
     parser.add_argument("--kernel-only", action="store_true",
                         help="profiling mode: only the gate/up GEMV over the layer copies, then a plain copy of "
                              "COPY_BYTES bytes that calibrates the HBM byte counters")
@@ -384,6 +427,8 @@ def main() -> int:
         return kernel_only(torch, ext, runtime, hardware, device, args)
     if args.prefill_only:
         return prefill_only(torch, ext, runtime, hardware, device, args)
+    if args.fp4_only:
+        return fp4_only(torch, ext, runtime, hardware, device, args)
     if args.model_only:
         print(json.dumps({"model_only": True, "model": model_section(torch, args)}), flush=True)
         return 0
