@@ -79,14 +79,51 @@ def read_traffic():
 
 
 def cpu_model() -> str:
-    """The host CPU's model name (``/proc/cpuinfo``), or the platform's processor string."""
+    """The host CPU's model name (``/proc/cpuinfo``, with its family/model/stepping numbers, which
+    name the part where a virtualised host reports only a vendor string), or the platform's
+    processor string."""
+    fields = {}
     try:
         for line in Path("/proc/cpuinfo").read_text().splitlines():
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
+            key, _, value = line.partition(":")
+            key = key.strip()
+            if key in ("model name", "cpu family", "model", "stepping") and key not in fields:
+                fields[key] = value.strip()
+            if not line.strip() and fields:
+                break
     except OSError:
         pass
-    return platform.processor() or platform.machine()
+    if "model name" not in fields:
+        return platform.processor() or platform.machine()
+    ids = ", ".join(f"{k} {fields[k]}" for k in ("cpu family", "model", "stepping") if k in fields)
+    return f"{fields['model name']} ({ids})" if ids else fields["model name"]
+
+
+def cpu_quota() -> float | None:
+    """CPUs' worth of time the cgroup allows this process (``cpu.max``), or None if unlimited."""
+    for path in ("/sys/fs/cgroup/cpu.max",):
+        try:
+            quota, period = Path(path).read_text().split()[:2]
+        except (OSError, ValueError):
+            continue
+        if quota != "max":
+            return int(quota) / int(period)
+    try:
+        quota = int(Path("/sys/fs/cgroup/cpu/cpu.cfs_quota_us").read_text())
+        period = int(Path("/sys/fs/cgroup/cpu/cpu.cfs_period_us").read_text())
+        return quota / period if quota > 0 else None
+    except (OSError, ValueError):
+        return None
+
+
+def cpu_threads() -> tuple[int, int, float | None]:
+    """(threads used, cores in this process's affinity mask, cgroup CPU quota). Every affinity core
+    is used unless the cgroup grants fewer CPUs' worth of time, where more threads than that only
+    time-slice against each other."""
+    affinity = len(os.sched_getaffinity(0))
+    quota = cpu_quota()
+    threads = affinity if quota is None else max(1, min(affinity, int(quota)))
+    return threads, affinity, quota
 
 
 def _median_seconds(fn, runs: int) -> float:
@@ -112,7 +149,7 @@ def cpu_baseline(weights, runs: int = 5) -> dict:
 
     from oracle import bc4, clib
 
-    cores = min(16, len(os.sched_getaffinity(0)))
+    cores, affinity, quota = cpu_threads()
     clib.set_threads(cores)
     torch.set_num_threads(cores)
     rng = np.random.default_rng(SEED)
@@ -153,6 +190,9 @@ def cpu_baseline(weights, runs: int = 5) -> dict:
         "cores": cores,
         "kind": "port",
         "cpu_model": cpu_model(),
+        "affinity_cores": affinity,
+        "host_cpus": os.cpu_count(),
+        "cgroup_cpu_quota": quota,
         "sample": (f"one layer's 7 linears, medians of {runs} runs per distinct shape of the C restatement's "
                    f"fused BC4 decode + fp32 matvec ({cores} OpenMP threads); per-shape decode-only and "
                    f"matvec-only medians and the T=32/128/512 fp32 GEMM (torch CPU, {cores} threads) beside it; "

@@ -73,7 +73,9 @@ int tx_linear(uint64_t handle, const void *x, int x_dtype, int64_t x_numel, int6
  * handle's own split-K buffer is not used: split-K partial sums go to a static 32 MiB device
  * array of the library (tx_noalloc_scratch_bytes), one per GPU, kept until the process ends.
  * No hipMalloc, hipFree or allocating library call is made. A call whose partials would exceed
- * the array fails with TX_ERR_INVALID before launching anything. All calls on one GPU share the
+ * the array fails with TX_ERR_INVALID before launching anything; a prefill-sized call on a handle
+ * set to prefill backend 1 (dense scratch + library GEMM, which creates library state on first
+ * use) fails with TX_ERR_UNSUPPORTED before launching anything. All calls on one GPU share the
  * array: calls that overlap on one GPU (two streams, two threads) race and must be serialised by
  * the caller; calls on one stream are ordered and safe. */
 int tx_linear_noalloc(uint64_t handle, const void *x, int x_dtype, int64_t x_numel, int64_t x_last,
@@ -90,7 +92,8 @@ int tx_linear_noalloc(uint64_t handle, const void *x, int x_dtype, int64_t x_num
  * saturated at 6, sign bit = sign of v.
  *   tx_quantize_activation_fp4: x device bf16 [tokens][K], K a multiple of 32.
  *   tx_decode_weight_fp4: the handle's fp32 products palette * row scale (before 16-bit
- *     rounding, as the reference's quantizer), M rows; K a multiple of 32.
+ *     rounding, as the reference's quantizer; in LUT mode the palette values are the handle's
+ *     table rows, as for every other kernel of that handle), M rows; K a multiple of 32.
  *   tx_fp4_gemm: y [tokens][M] bf16 = round(sum_k deq(x)[t][k] * deq(w)[m][k]) with fp32
  *     accumulation (v_mfma_scale_f32_32x32x64_f8f6f4), then + bias [M] (bf16, or NULL) with a
  *     second rounding; K a multiple of 64. Packed operands 16-byte aligned. */
@@ -105,8 +108,9 @@ int tx_noalloc_scratch_bytes(int64_t *bytes);
 
 /* Workspace bytes of tx_linear and tx_prefill for `tokens` tokens: the prefill split-K partial
  * sums for tokens > 1 (with backend 1 and tokens >= the prefill threshold: the dense scratch of
- * min(tile_rows, M) decoded rows of K 16-bit weights, 256-byte aligned, plus 8 MiB for the library
- * GEMM), the one-token GEMV's split-K partials for
+ * min(tile_rows, M) decoded rows of K 16-bit weights rounded up to 256 bytes, 256 bytes of slack
+ * and 8 MiB for the library GEMM, whose workspace starts at the first 256-byte boundary after the
+ * rows; the caller's workspace need only be 16-byte aligned), the one-token GEMV's split-K partials for
  * tokens == 1 (0 when the shape is not split, or when one workgroup per 16-row group runs all of
  * its splits: 2 to 4 splits, row groups spreading evenly over the CUs, arithmetic palette). No
  * reference counterpart (see tx_linear). */

@@ -18,6 +18,7 @@
  */
 #include <math.h>
 #include <stdint.h>
+#include <stdlib.h>
 #include <string.h>
 
 #ifdef _OPENMP
@@ -110,18 +111,47 @@ void oracle_matvec_f64(const uint16_t *w, const uint16_t *x, int64_t M, int64_t 
   }
 }
 
-/* Y[t][m] = sum_k x[t][k] * w[m][k] in double. */
+/* Y[t][m] = sum_k x[t][k] * w[m][k] in double (each product of two bf16 values is exact in double).
+ * x is converted to double once; each weight row once per thread; four tokens share each pass over
+ * the row (four independent accumulators), so a whole prefill shape finishes in seconds. */
 void oracle_gemm_f64(const uint16_t *x, const uint16_t *w, int64_t T, int64_t M, int64_t K, double *y) {
-#pragma omp parallel for schedule(static)
-  for (int64_t m = 0; m < M; ++m) {
-    const uint16_t *row = w + (size_t)m * K;
-    for (int64_t t = 0; t < T; ++t) {
-      const uint16_t *xr = x + (size_t)t * K;
-      double acc = 0.0;
-      for (int64_t k = 0; k < K; ++k) acc += (double)bf16_to_f32(row[k]) * (double)bf16_to_f32(xr[k]);
-      y[(size_t)t * M + m] = acc;
+  double *xd = (double *)malloc((size_t)T * (size_t)K * sizeof(double));
+  if (!xd) return;
+  for (int64_t i = 0; i < T * K; ++i) xd[i] = (double)bf16_to_f32(x[i]);
+#pragma omp parallel
+  {
+    double *wd = (double *)malloc((size_t)K * sizeof(double));
+#pragma omp for schedule(static)
+    for (int64_t m = 0; m < M; ++m) {
+      if (!wd) continue;
+      const uint16_t *row = w + (size_t)m * K;
+      for (int64_t k = 0; k < K; ++k) wd[k] = (double)bf16_to_f32(row[k]);
+      int64_t t = 0;
+      for (; t + 4 <= T; t += 4) {
+        const double *x0 = xd + (size_t)t * K, *x1 = x0 + K, *x2 = x1 + K, *x3 = x2 + K;
+        double a0 = 0.0, a1 = 0.0, a2 = 0.0, a3 = 0.0;
+        for (int64_t k = 0; k < K; ++k) {
+          const double v = wd[k];
+          a0 += v * x0[k];
+          a1 += v * x1[k];
+          a2 += v * x2[k];
+          a3 += v * x3[k];
+        }
+        y[(size_t)t * M + m] = a0;
+        y[(size_t)(t + 1) * M + m] = a1;
+        y[(size_t)(t + 2) * M + m] = a2;
+        y[(size_t)(t + 3) * M + m] = a3;
+      }
+      for (; t < T; ++t) {
+        const double *xr = xd + (size_t)t * K;
+        double acc = 0.0;
+        for (int64_t k = 0; k < K; ++k) acc += wd[k] * xr[k];
+        y[(size_t)t * M + m] = acc;
+      }
     }
+    free(wd);
   }
+  free(xd);
 }
 
 /* CPU baseline: fused decode + fp32 matvec (the CPU analogue of the GEMV), y in float.

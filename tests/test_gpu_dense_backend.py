@@ -46,7 +46,7 @@ def test_dense_backend_matches_oracle_with_row_tiles(ext, oracle_threads, m, k, 
             _dense(ext, handle, tile_rows)
         assert ext.handle_info(plain)[3:5] == [tile_rows, DENSE]
         rows = min(tile_rows, m)
-        assert ext.workspace_bytes(plain, tokens) == (rows * k * 2 + 255) // 256 * 256 + (8 << 20)
+        assert ext.workspace_bytes(plain, tokens) == (rows * k * 2 + 255) // 256 * 256 + 256 + (8 << 20)
         y0 = ext.linear(plain, x.cuda())
         y1 = ext.linear(biased, x.cuda())
         tile = ext.prefill(plain, 6, x.cuda())
@@ -87,9 +87,8 @@ def test_dense_backend_f16(ext, oracle_threads):
     assert bc4.relative_rms(ref, y0.double().cpu().numpy()) <= PREFILL_RRMS_TOL
 
 
-def test_dense_backend_lut_mode_and_noalloc_agree(ext):
-    """LUT-mode decode with the device's own palette feeds the GEMM the same weights; the
-    allocation-free entry point runs the same decode and GEMM on its static scratch."""
+def test_dense_backend_lut_mode_agrees(ext):
+    """LUT-mode decode with the device's own palette feeds the GEMM the same weights."""
     m, k, tokens = 256, 2048, 64
     blocks = random_blocks(m, k, 721)
     scales = lognormal_scales(m, 722)
@@ -99,10 +98,7 @@ def test_dense_backend_lut_mode_and_noalloc_agree(ext):
     try:
         _dense(ext, handle, 128)
         plain = ext.linear(handle, x)
-        y = torch.empty_like(plain)
-        ext.linear_noalloc_into(handle, x, y)
         torch.cuda.synchronize()
-        assert torch.equal(plain, y)
         ext.set_palette_table(handle, table)
         lut = ext.linear(handle, x)
         torch.cuda.synchronize()

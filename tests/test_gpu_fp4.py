@@ -60,6 +60,30 @@ def test_weight_quantizer_bitwise(ext, m, k):
     assert np.array_equal(packed.cpu().numpy(), mxfp4.pack(codes))
 
 
+def test_weight_quantizer_reads_the_palette_table_in_lut_mode(ext):
+    """A LUT-mode handle (another GPU's palette) quantizes the products of ITS table's values, as
+    every other kernel of that handle decodes them: bitwise the oracle on the table's palette, and
+    different from the arithmetic palette's codes (so a quantizer that ignored the table fails)."""
+    from tests.test_gpu_lut import foreign_palette
+
+    m, k = 300, 2048
+    blocks = random_blocks(m, k, 815)
+    scales = lognormal_scales(m, 816)
+    lut = foreign_palette(17)
+    handle = _pack(ext, blocks, scales)
+    try:
+        ext.set_palette_table(handle, torch.from_numpy(lut.reshape(-1)).cuda())
+        packed, group_scales = ext.decode_weight_fp4(handle)
+        torch.cuda.synchronize()
+    finally:
+        ext.free(handle)
+    codes, exponents = mxfp4.quantize(bc4.decode_f32_weights(blocks, scales, lut))
+    assert np.array_equal(group_scales.cpu().numpy(), exponents)
+    assert np.array_equal(packed.cpu().numpy(), mxfp4.pack(codes))
+    plain, _ = mxfp4.quantize(bc4.decode_f32_weights(blocks, scales))
+    assert not np.array_equal(mxfp4.pack(plain), mxfp4.pack(codes))
+
+
 @pytest.mark.parametrize("tokens,m,k", [(1, 64, 64), (37, 200, 1024), (130, 300, 5120), (256, 128, 128)])
 def test_fp4_gemm_matches_dequantized_product(ext, tokens, m, k):
     x = _activations(tokens, k, 821)
@@ -101,18 +125,23 @@ def test_fp4_gemm_staged_and_direct_kernels_agree_bitwise(ext, tokens, m, k):
     assert torch.equal(staged, direct)
 
 
-def test_fp4_hybrid_dispatch_on_a_reference_shape(ext):
-    """At 512 tokens on (5120, 17408) the hybrid runs the explicit pipeline (bitwise), and stays
-    within FP4 quantization error of the bf16 prefill of the same weights."""
-    m, k, tokens = 5120, 17408, 512
-    blocks = random_blocks(m, k, 831)
-    scales = lognormal_scales(m, 832)
-    x = bf16_vector((tokens, k), 833, scale=0.5).cuda()
+@pytest.mark.parametrize("m,k", sorted(runtime.FP4_HYBRID_SHAPES))
+def test_fp4_hybrid_dispatch_on_a_reference_shape(ext, m, k):
+    """At 512 tokens on the reference's MLP shapes the hybrid runs the explicit pipeline (bitwise)
+    and stays within FP4 quantization error of the bf16 prefill of the same weights; at 511 tokens
+    the same handle keeps the bf16 prefill, bit for bit."""
+    tokens = runtime.FP4_HYBRID_TOKENS
+    blocks = random_blocks(m, k, 831 + m)
+    scales = lognormal_scales(m, 832 + m)
+    x = bf16_vector((tokens, k), 833 + m, scale=0.5).cuda()
+    x511 = x[:tokens - 1].contiguous()
     handle = _pack(ext, blocks, scales)
     try:
         exact = runtime._linear_dispatch(handle, x)
+        exact511 = ext.linear(handle, x511)
         runtime.set_fp4_hybrid(True)
         hybrid = runtime._linear_dispatch(handle, x)
+        hybrid511 = runtime._linear_dispatch(handle, x511)
         xp, xs = ext.quantize_activation_fp4(x)
         wp, ws = ext.decode_weight_fp4(handle)
         explicit = ext.fp4_gemm(xp, xs, wp, ws)
@@ -121,6 +150,7 @@ def test_fp4_hybrid_dispatch_on_a_reference_shape(ext):
         runtime.free([handle])
     assert not runtime._Fp4State.enabled
     assert torch.equal(hybrid, explicit)
+    assert torch.equal(hybrid511, exact511)
     assert bc4.relative_rms(exact.double().cpu().numpy(), hybrid.double().cpu().numpy()) <= 0.3
 
 

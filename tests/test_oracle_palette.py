@@ -41,6 +41,54 @@ def test_endpoints_correctly_rounded():
         assert np.all(PAL[e + 127, :, 1] == want)
 
 
+def _header_constant(name: str) -> float:
+    """A float literal of the device header (``constexpr float name = 0x...f;``)."""
+    import re
+    from pathlib import Path
+
+    text = (Path(__file__).resolve().parents[1] / "texelator_amd/csrc/bc4_device.h").read_text()
+    match = re.search(r"constexpr float " + name + r" = (-?0x[0-9a-fA-F.p+-]+)f;", text)
+    assert match, name
+    return float.fromhex(match.group(1))
+
+
+def _split_reciprocal_quotient(n: np.ndarray, hi: float, lo: float) -> np.ndarray:
+    """float32 fma(n, hi, RN32(n * lo)), the device's quotient: n*hi (n < 2^10, hi 24 bits) and
+    the float32 n*lo are exact in float64 and so is their sum (< 50 significant bits), so the
+    single float64 -> float32 conversion is the fma's one rounding."""
+    n = n.astype(np.float64)
+    inner = (n * np.float64(np.float32(lo))).astype(np.float32).astype(np.float64)
+    return (n * np.float64(np.float32(hi)) + inner).astype(np.float32)
+
+
+def test_seed_quotients_exactly_rounded_exhaustive():
+    """Every seed quotient the decoders use, against exact rational rounding (fractions): the
+    endpoint values RN(e/127), e = -127..127, and the step values RN(d/889) and RN(d/635) for every
+    difference d = e1 - e0 in -254..254 under both denominators (1,273 quotients). Three methods
+    must each give the correctly rounded float32: the oracle's float64 division, the double
+    division rounded to float that builds the device's compile-time seed-table image, and the
+    device's fma with a split reciprocal (constants read from the device header)."""
+    cases = [(127, np.arange(-127, 128), "kInv127Hi", "kInv127Lo"),
+             (889, np.arange(-254, 255), "kInv889Hi", "kInv889Lo"),
+             (635, np.arange(-254, 255), "kInv635Hi", "kInv635Lo")]
+    checked = 0
+    for den, nums, hi_name, lo_name in cases:
+        hi, lo = _header_constant(hi_name), _header_constant(lo_name)
+        assert np.float32(hi) == _cr(Fraction(1, den))          # hi = RN(1/d)
+        assert np.float32(lo) == _cr(Fraction(1, den) - Fraction(float(np.float32(hi))))
+        exact = np.array([_cr(Fraction(int(n), den)) for n in nums], dtype=np.float32)
+        image = np.array([np.float32(float(int(n)) / float(den)) for n in nums], dtype=np.float32)
+        device = _split_reciprocal_quotient(nums, hi, lo)
+        for got in (bc4.crdiv_f32(nums, den), image, device):
+            assert np.array_equal(got.view(np.uint32), exact.view(np.uint32)), den
+        # the 8x-prescaled pairs of the register decoder give the same quotients of 8n
+        hi8, lo8 = _header_constant(hi_name) / 8.0, _header_constant(lo_name) / 8.0
+        device8 = _split_reciprocal_quotient(8 * nums, hi8, lo8)
+        assert np.array_equal(device8.view(np.uint32), exact.view(np.uint32)), den
+        checked += nums.size
+    assert checked == 255 + 2 * 509
+
+
 def test_interpolants_close_to_exact_bc4_values():
     """Exhaustive over all 65,025 pairs. 8-value mode: ((8-s)e0 + (s-1)e1)/(7*127);
     6-value mode: ((6-s)e0 + (s-1)e1)/(5*127).

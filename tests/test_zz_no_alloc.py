@@ -112,3 +112,26 @@ def test_errors_are_reported_before_any_launch(ext):
             ext.free(bf_bias)
     finally:
         ext.free(handle)
+
+
+def test_dense_backend_is_refused_before_any_launch(ext):
+    """Backend 1 (dense scratch + library GEMM) creates library state on first use, so the
+    allocation-free entry point refuses its prefill-sized calls; one-token calls of the same
+    handle still run the GEMV and match tx_linear."""
+    from texelator_amd import _lib
+
+    m, k = 256, 2048
+    handle = _pack(ext, m, k, 51)
+    try:
+        ext.set_prefill(handle, 16, 128)
+        ext.set_prefill_backend(handle, 1)
+        x = bf16_vector((64, k), 52).cuda()
+        y = torch.full((64, m), float("nan"), dtype=torch.bfloat16, device="cuda")
+        with pytest.raises(_lib.UnsupportedError, match="backend 1"):
+            ext.linear_noalloc_into(handle, x, y)
+        torch.cuda.synchronize()
+        assert torch.isnan(y.float()).all()  # nothing was launched
+        x1 = bf16_vector((1, k), 53).cuda()
+        assert torch.equal(ext.linear(handle, x1), _noalloc(ext, handle, x1))
+    finally:
+        ext.free(handle)

@@ -146,7 +146,9 @@ int dense_tile_rows(const Handle *h) { return std::min(h->prefill_tile_rows, h->
 
 int64_t dense_rows_bytes(const Handle *h) { return ((int64_t)dense_tile_rows(h) * h->K * 2 + 255) / 256 * 256; }
 
-int64_t dense_workspace_bytes(const Handle *h) { return dense_rows_bytes(h) + (int64_t)tx::kDenseGemmWorkspace; }
+// The library GEMM's workspace starts at the first 256-byte boundary after the decoded rows (the
+// caller's workspace need only be 16-byte aligned): 256 bytes of slack cover the alignment.
+int64_t dense_workspace_bytes(const Handle *h) { return dense_rows_bytes(h) + 256 + (int64_t)tx::kDenseGemmWorkspace; }
 
 // The backend a prefill-sized call of `tokens` tokens runs: the dense-scratch path, or a tile id.
 int prefill_choice(const Handle *h, int64_t tokens) {
@@ -168,7 +170,8 @@ int run_dense_prefill(Handle *h, const void *x, bool f16, int64_t tokens, void *
   if (!workspace || workspace_bytes < dense_workspace_bytes(h) || reinterpret_cast<uintptr_t>(workspace) % 16 != 0)
     return fail(TX_ERR_INVALID, "dense prefill workspace missing or too small (see tx_workspace_bytes)");
   uint16_t *dense = static_cast<uint16_t *>(workspace);
-  void *gemm_workspace = static_cast<char *>(workspace) + dense_rows_bytes(h);
+  const uintptr_t rows_end = reinterpret_cast<uintptr_t>(workspace) + (uintptr_t)dense_rows_bytes(h);
+  void *gemm_workspace = reinterpret_cast<void *>((rows_end + 255) & ~uintptr_t(255));
   const int tile = dense_tile_rows(h);
   for (int row = 0; row < h->M; row += tile) {
     const int rows = std::min(tile, h->M - row);
@@ -415,6 +418,11 @@ int tx_linear_noalloc(uint64_t value, const void *x, int x_dtype, int64_t x_nume
   const int64_t tokens = x_numel / h->K;
   if (tokens <= 0) return TX_OK;
   const bool prefill = tokens >= h->prefill_threshold && tokens > 1;
+  // The dense-scratch backend runs a library GEMM that creates handles, descriptors and plans on
+  // first use: not allocation-free, so this entry point refuses it before launching anything.
+  if (prefill && prefill_choice(h, tokens) == kDenseBackend)
+    return fail(TX_ERR_UNSUPPORTED, "linear_noalloc: prefill backend 1 (dense scratch + library GEMM) allocates; "
+                                    "use tx_linear with a workspace or another prefill backend");
   if (prefill && tokens > (1 << 20)) return fail(TX_ERR_INVALID, "token count exceeds the prefill limit (1048576)");
   if (!prefill && tokens > 65535) return fail(TX_ERR_INVALID, "token grid exceeds the HIP grid.z limit");
   const int64_t need = prefill ? prefill_call_bytes(h, tokens) : gemv_partials_bytes(h, tokens);
@@ -456,7 +464,7 @@ int tx_decode_weight_fp4(uint64_t value, uint8_t *packed, uint8_t *scales, void 
   if (!packed || !scales) return fail(TX_ERR_INVALID, "null pointer");
   if (reinterpret_cast<uintptr_t>(packed) % 16 != 0) return fail(TX_ERR_INVALID, "packed output must be 16-byte aligned");
   DeviceGuard guard(h->device);
-  TX_HIP(tx::launch_quantize_weight_fp4(h->tiles, h->scales, h->M, h->K, h->RG, h->CG, packed, scales,
+  TX_HIP(tx::launch_quantize_weight_fp4(h->tiles, h->scales, h->lut, h->M, h->K, h->RG, h->CG, packed, scales,
                                         reinterpret_cast<hipStream_t>(stream)));
   return TX_OK;
 }

@@ -33,6 +33,9 @@ struct BlasLt {
   decltype(&hipblasLtMatmulPreferenceSetAttribute) pref_set = nullptr;
   decltype(&hipblasLtMatmulAlgoGetHeuristic) heuristic = nullptr;
   decltype(&hipblasLtMatmul) matmul = nullptr;
+  decltype(&hipblasLtMatmulDescDestroy) desc_destroy = nullptr;
+  decltype(&hipblasLtMatrixLayoutDestroy) layout_destroy = nullptr;
+  decltype(&hipblasLtMatmulPreferenceDestroy) pref_destroy = nullptr;
   std::string error;  // why the library could not be opened, if it could not
 };
 
@@ -58,6 +61,9 @@ const BlasLt &blaslt() {
     sym(a.pref_set, "hipblasLtMatmulPreferenceSetAttribute");
     sym(a.heuristic, "hipblasLtMatmulAlgoGetHeuristic");
     sym(a.matmul, "hipblasLtMatmul");
+    sym(a.desc_destroy, "hipblasLtMatmulDescDestroy");
+    sym(a.layout_destroy, "hipblasLtMatrixLayoutDestroy");
+    sym(a.pref_destroy, "hipblasLtMatmulPreferenceDestroy");
     return a;
   }();
   return api;
@@ -66,16 +72,30 @@ const BlasLt &blaslt() {
 // A prepared GEMM for one (device, dtype, rows, tokens, K, ldy): descriptors and the first
 // algorithm the heuristic offers whose state is success and whose workspace fits the
 // kDenseGemmWorkspace bytes the caller provides (split-K algorithms of long-K, few-row shapes use
-// one). Plans are kept until the process ends.
+// one). At most kMaxPlans are kept (a server with many prompt lengths would otherwise add one per
+// length); the least recently used is destroyed to make room. Plans are created, used and
+// destroyed under g_mutex, so no call ever holds a destroyed descriptor.
 struct Plan {
   hipblasLtMatmulDesc_t desc = nullptr;
   hipblasLtMatrixLayout_t a = nullptr, b = nullptr, d = nullptr;
   hipblasLtMatmulAlgo_t algo{};
+  uint64_t last_use = 0;
 };
+
+constexpr size_t kMaxPlans = 64;
+
+void destroy_plan(const BlasLt &api, Plan &plan) {
+  if (plan.desc) api.desc_destroy(plan.desc);
+  if (plan.a) api.layout_destroy(plan.a);
+  if (plan.b) api.layout_destroy(plan.b);
+  if (plan.d) api.layout_destroy(plan.d);
+  plan = Plan{};
+}
 
 std::mutex g_mutex;
 std::map<int, hipblasLtHandle_t> g_handles;
 std::map<std::tuple<int, bool, int, int64_t, int, int64_t>, Plan> g_plans;
+uint64_t g_use_clock = 0;
 
 std::string status_text(const char *what, hipblasStatus_t status) {
   return std::string("hipBLASLt ") + what + " failed (status " + std::to_string((int)status) + ")";
@@ -100,66 +120,75 @@ bool dense_gemm(int device, bool f16, int rows, int64_t tokens, int K, const voi
     error = api.error;
     return false;
   }
-  Plan plan;
+  std::lock_guard<std::mutex> lock(g_mutex);
   hipblasLtHandle_t handle = nullptr;
-  {
-    std::lock_guard<std::mutex> lock(g_mutex);
-    auto found = g_handles.find(device);
-    if (found == g_handles.end()) {
-      const hipblasStatus_t s = api.create(&handle);
-      if (s != HIPBLAS_STATUS_SUCCESS) {
-        error = status_text("handle creation", s);
-        return false;
-      }
-      g_handles[device] = handle;
-    } else {
-      handle = found->second;
+  auto found = g_handles.find(device);
+  if (found == g_handles.end()) {
+    const hipblasStatus_t s = api.create(&handle);
+    if (s != HIPBLAS_STATUS_SUCCESS) {
+      error = status_text("handle creation", s);
+      return false;
     }
-    const auto key = std::make_tuple(device, f16, rows, tokens, K, ldy);
-    auto cached = g_plans.find(key);
-    if (cached != g_plans.end()) {
-      plan = cached->second;
-    } else {
-      // Column-major view of the row-major operands: D (rows x tokens, ld ldy) =
-      // op(A) * B with A = W^T (K x rows, ld K) transposed and B = X^T (K x tokens, ld K).
-      const hipDataType type = f16 ? HIP_R_16F : HIP_R_16BF;
-      hipblasStatus_t s = api.desc_create(&plan.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F);
-      const int32_t trans_a = HIPBLAS_OP_T, trans_b = HIPBLAS_OP_N;
-      if (s == HIPBLAS_STATUS_SUCCESS) s = api.desc_set(plan.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &trans_a, sizeof(trans_a));
-      if (s == HIPBLAS_STATUS_SUCCESS) s = api.desc_set(plan.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &trans_b, sizeof(trans_b));
-      if (s == HIPBLAS_STATUS_SUCCESS) s = api.layout_create(&plan.a, type, (uint64_t)K, (uint64_t)rows, K);
-      if (s == HIPBLAS_STATUS_SUCCESS) s = api.layout_create(&plan.b, type, (uint64_t)K, (uint64_t)tokens, K);
-      if (s == HIPBLAS_STATUS_SUCCESS) s = api.layout_create(&plan.d, type, (uint64_t)rows, (uint64_t)tokens, ldy);
-      if (s != HIPBLAS_STATUS_SUCCESS) {
-        error = status_text("descriptor creation", s);
-        return false;
-      }
-      hipblasLtMatmulPreference_t pref = nullptr;
-      s = api.pref_create(&pref);
-      const uint64_t max_workspace = kDenseGemmWorkspace;
-      if (s == HIPBLAS_STATUS_SUCCESS)
-        s = api.pref_set(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &max_workspace, sizeof(max_workspace));
-      constexpr int kAsk = 8;
-      hipblasLtMatmulHeuristicResult_t results[kAsk]{};
-      int count = 0;
-      if (s == HIPBLAS_STATUS_SUCCESS)
-        s = api.heuristic(handle, plan.desc, plan.a, plan.b, plan.d, plan.d, pref, kAsk, results, &count);
-      if (s != HIPBLAS_STATUS_SUCCESS) {
-        error = status_text("heuristic", s);
-        return false;
-      }
-      int pick = -1;
-      for (int i = 0; i < std::min(count, kAsk) && pick < 0; ++i)
-        if (results[i].state == HIPBLAS_STATUS_SUCCESS && results[i].workspaceSize <= kDenseGemmWorkspace) pick = i;
-      if (pick < 0) {
-        error = "hipBLASLt offers no algorithm for this shape within " + std::to_string(kDenseGemmWorkspace) +
-                " bytes of workspace";
-        return false;
-      }
-      plan.algo = results[pick].algo;
-      g_plans[key] = plan;
-    }
+    g_handles[device] = handle;
+  } else {
+    handle = found->second;
   }
+  const auto key = std::make_tuple(device, f16, rows, tokens, K, ldy);
+  auto cached = g_plans.find(key);
+  if (cached == g_plans.end()) {
+    // Column-major view of the row-major operands: D (rows x tokens, ld ldy) =
+    // op(A) * B with A = W^T (K x rows, ld K) transposed and B = X^T (K x tokens, ld K).
+    Plan plan;
+    const hipDataType type = f16 ? HIP_R_16F : HIP_R_16BF;
+    hipblasStatus_t s = api.desc_create(&plan.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F);
+    const int32_t trans_a = HIPBLAS_OP_T, trans_b = HIPBLAS_OP_N;
+    if (s == HIPBLAS_STATUS_SUCCESS) s = api.desc_set(plan.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &trans_a, sizeof(trans_a));
+    if (s == HIPBLAS_STATUS_SUCCESS) s = api.desc_set(plan.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &trans_b, sizeof(trans_b));
+    if (s == HIPBLAS_STATUS_SUCCESS) s = api.layout_create(&plan.a, type, (uint64_t)K, (uint64_t)rows, K);
+    if (s == HIPBLAS_STATUS_SUCCESS) s = api.layout_create(&plan.b, type, (uint64_t)K, (uint64_t)tokens, K);
+    if (s == HIPBLAS_STATUS_SUCCESS) s = api.layout_create(&plan.d, type, (uint64_t)rows, (uint64_t)tokens, ldy);
+    if (s != HIPBLAS_STATUS_SUCCESS) {
+      destroy_plan(api, plan);
+      error = status_text("descriptor creation", s);
+      return false;
+    }
+    hipblasLtMatmulPreference_t pref = nullptr;
+    s = api.pref_create(&pref);
+    const uint64_t max_workspace = kDenseGemmWorkspace;
+    if (s == HIPBLAS_STATUS_SUCCESS)
+      s = api.pref_set(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &max_workspace, sizeof(max_workspace));
+    constexpr int kAsk = 8;
+    hipblasLtMatmulHeuristicResult_t results[kAsk]{};
+    int count = 0;
+    if (s == HIPBLAS_STATUS_SUCCESS)
+      s = api.heuristic(handle, plan.desc, plan.a, plan.b, plan.d, plan.d, pref, kAsk, results, &count);
+    if (pref) api.pref_destroy(pref);
+    if (s != HIPBLAS_STATUS_SUCCESS) {
+      destroy_plan(api, plan);
+      error = status_text("heuristic", s);
+      return false;
+    }
+    int pick = -1;
+    for (int i = 0; i < std::min(count, kAsk) && pick < 0; ++i)
+      if (results[i].state == HIPBLAS_STATUS_SUCCESS && results[i].workspaceSize <= kDenseGemmWorkspace) pick = i;
+    if (pick < 0) {
+      destroy_plan(api, plan);
+      error = "hipBLASLt offers no algorithm for this shape within " + std::to_string(kDenseGemmWorkspace) +
+              " bytes of workspace";
+      return false;
+    }
+    plan.algo = results[pick].algo;
+    if (g_plans.size() >= kMaxPlans) {
+      auto oldest = g_plans.begin();
+      for (auto it = g_plans.begin(); it != g_plans.end(); ++it)
+        if (it->second.last_use < oldest->second.last_use) oldest = it;
+      destroy_plan(api, oldest->second);
+      g_plans.erase(oldest);
+    }
+    cached = g_plans.emplace(key, plan).first;
+  }
+  Plan &plan = cached->second;
+  plan.last_use = ++g_use_clock;
   const float alpha = 1.f, beta = 0.f;
   const hipblasStatus_t s = api.matmul(handle, plan.desc, &alpha, w, plan.a, x, plan.b, &beta, y, plan.d, y, plan.d,
                                        &plan.algo, gemm_workspace, kDenseGemmWorkspace, stream);

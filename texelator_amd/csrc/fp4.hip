@@ -96,11 +96,21 @@ struct BlockEntries {
   uint32_t sel[4];
 };
 
-__device__ __forceinline__ BlockEntries block_entries(uint32_t a, uint32_t b, float scale) {
+// With a palette table (LUT mode, probe layout) the 8 values come from the block's table row,
+// as every other kernel of a LUT-mode handle reads them; otherwise they are computed.
+__device__ __forceinline__ BlockEntries block_entries(uint32_t a, uint32_t b, float scale, const float4 *lut) {
   BlockEntries out;
-  const Palette pal = palette8(a, b);
+  if (lut) {
+    const float4 *r = lut + 2 * (size_t)palette_row(a, b);
+    const float4 p03 = r[0], p47 = r[1];
+    const float p[8] = {p03.x, p03.y, p03.z, p03.w, p47.x, p47.y, p47.z, p47.w};
 #pragma unroll
-  for (int s = 0; s < 8; ++s) out.q[s] = pal.p[s] * scale;
+    for (int s = 0; s < 8; ++s) out.q[s] = p[s] * scale;
+  } else {
+    const Palette pal = palette8(a, b);
+#pragma unroll
+    for (int s = 0; s < 8; ++s) out.q[s] = pal.p[s] * scale;
+  }
   out.sel[0] = (a >> 5) & 0x07070707u;
   out.sel[1] = a & 0x07070707u;
   out.sel[2] = (b >> 5) & 0x07070707u;
@@ -150,8 +160,9 @@ __device__ __forceinline__ void block_codes(const BlockEntries &e, float inv, ui
 }
 
 // One thread per 16-byte tile slot: two consecutive blocks of one row = one group of 32.
-__global__ __launch_bounds__(256) void quantize_weight_kernel(const uint4 *tiles, const float *row_scales, int M, int K,
-                                                              int RG, int CG, uint8_t *packed, uint8_t *scales) {
+__global__ __launch_bounds__(256) void quantize_weight_kernel(const uint4 *tiles, const float *row_scales, const float4 *lut,
+                                                              int M, int K, int RG, int CG, uint8_t *packed,
+                                                              uint8_t *scales) {
   const size_t slot = (size_t)blockIdx.x * 256 + threadIdx.x;
   if (slot >= (size_t)RG * CG * 64) return;
   const int lane = slot & 63;
@@ -163,8 +174,8 @@ __global__ __launch_bounds__(256) void quantize_weight_kernel(const uint4 *tiles
   if (row >= M || group >= groups) return;
   const uint4 cur = tiles[slot];
   const float scale = row_scales[row];
-  const BlockEntries b0 = block_entries(cur.x, cur.y, scale);
-  const BlockEntries b1 = block_entries(cur.z, cur.w, scale);
+  const BlockEntries b0 = block_entries(cur.x, cur.y, scale, lut);
+  const BlockEntries b1 = block_entries(cur.z, cur.w, scale, lut);
   const uint32_t e = group_exponent(__uint_as_float(max(used_amax_bits(b0), used_amax_bits(b1))));
   const float inv = __uint_as_float((254u - e) << 23);  // 2^(127 - e), exact
   uint4 out;
@@ -395,11 +406,11 @@ hipError_t launch_quantize_activation_fp4(const uint16_t *x, int64_t tokens, int
   return hipGetLastError();
 }
 
-hipError_t launch_quantize_weight_fp4(const uint4 *tiles, const float *scales, int M, int K, int RG, int CG,
-                                      uint8_t *packed, uint8_t *group_scales, hipStream_t stream) {
+hipError_t launch_quantize_weight_fp4(const uint4 *tiles, const float *scales, const float4 *lut, int M, int K,
+                                      int RG, int CG, uint8_t *packed, uint8_t *group_scales, hipStream_t stream) {
   const size_t slots = (size_t)RG * CG * 64;
   hipLaunchKernelGGL(quantize_weight_kernel, dim3((unsigned)((slots + 255) / 256)), dim3(256), 0, stream, tiles,
-                     scales, M, K, RG, CG, packed, group_scales);
+                     scales, lut, M, K, RG, CG, packed, group_scales);
   return hipGetLastError();
 }
 

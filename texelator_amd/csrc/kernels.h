@@ -104,8 +104,9 @@ hipError_t launch_add_bias(void *y, const void *bias, int64_t tokens, int M, boo
 // of 64 for the GEMM): packed E2M1 [rows][K/2], E8M0 scales [rows][K/32].
 hipError_t launch_quantize_activation_fp4(const uint16_t *x, int64_t tokens, int K, uint8_t *packed, uint8_t *scales,
                                           hipStream_t stream);
-hipError_t launch_quantize_weight_fp4(const uint4 *tiles, const float *scales, int M, int K, int RG, int CG,
-                                      uint8_t *packed, uint8_t *group_scales, hipStream_t stream);
+// lut: the handle's palette table in LUT mode (nullptr: the computed palette).
+hipError_t launch_quantize_weight_fp4(const uint4 *tiles, const float *scales, const float4 *lut, int M, int K,
+                                      int RG, int CG, uint8_t *packed, uint8_t *group_scales, hipStream_t stream);
 hipError_t launch_fp4_gemm(const uint8_t *xq, const uint8_t *xs, const uint8_t *wq, const uint8_t *ws,
                            const uint16_t *bias, uint16_t *y, int tokens, int M, int K, hipStream_t stream);
 
