@@ -14,9 +14,12 @@ decode + matvec, of the decode and of the matvec alone, and the config-3 fp32 GE
 ``hbm_stream_read`` is a plain streaming read of the same launch size (the achievable HBM rate);
 ``roofline.frac_of_stream_read`` is the GEMV's rate against it.
 ``prefill_tok_s_512`` and ``decode_tok_s`` are the metric's other two figures on the 27B-class
-decoder: the 512-token prefill (``texelator_amd.prefill.benchmark_prefill``)
-and graph-replayed greedy decode from 512 to ``--context`` with every step timed; ``model`` holds
-the details, ``model_3b`` the same for BASELINE config 4.
+decoder (linears BC4-encoded from random-init weights): the 512-token prefill
+(``texelator_amd.prefill.benchmark_prefill``; null with ``prefill_gate_failed`` if the prefill path
+fails the reference protocol's correctness gate) and graph-replayed greedy decode from 512 to
+``--context`` with every step timed; ``model`` holds the details, ``model_3b`` the same for BASELINE
+config 4, and ``model_3b_hf`` config 4 through the reference's own calling path (a Hugging Face
+Qwen2 with TexelatorLinear modules: prefill protocol and greedy ``generate``).
 """
 from __future__ import annotations
 
@@ -373,43 +376,83 @@ def fp4_only(torch, ext, runtime, hardware, device, args) -> int:
 def model_section(torch, args, model_name: str | None = None, context: int | None = None) -> dict:
     """Prefill tok/s at ``--prompt`` tokens (reference protocol, texelator/prefill.py:63-131) and
     graph-replayed greedy decode tok/s from the prompt up to ``context``, on a random-init BC4
-    decoder of BASELINE config 5 (27b) or 4 (3b)."""
+    decoder of BASELINE config 5 (27b) or 4 (3b) whose linears are BC4-encoded by this build's
+    encoder (``--model-weights uniform``: uniform random block bytes instead). If the prefill path
+    fails the protocol's correctness gate, the failure is reported and the prefill is not timed."""
     from texelator_amd import modeling, prefill
 
     model_name = model_name or args.model
     context = context or args.context
     config = modeling.DecoderConfig.class_27b() if model_name == "27b" else modeling.DecoderConfig.qwen25_3b_style()
-    model = modeling.BC4Decoder(config, max_context=context, seed=SEED)
+    model = modeling.BC4Decoder(config, max_context=context, seed=SEED, weights=args.model_weights)
+    gate_failed = None
     try:
         try:
             pre = prefill.benchmark_prefill(model, tokens=args.prompt, warmup=2, runs=5)
-        except RuntimeError as error:        # gate failed: still time it, and say so
+        except prefill.GateFailed as error:
             log(str(error))
-            pre = prefill.benchmark_prefill(model, tokens=args.prompt, warmup=2, runs=5, rrms_limit=None)
-            pre["correctness"]["gate_failed"] = True
+            pre, gate_failed = None, error.correctness
         dec = prefill.benchmark_decode(model, prompt_tokens=args.prompt, context=context)
-        sampled = (prefill.benchmark_decode(model, prompt_tokens=args.prompt, context=context,
-                                            sample_steps=args.decode_sample)
-                   if args.decode_sample and context - args.prompt > args.decode_sample else None)
     finally:
         model.close()
     bytes_per_token = config.bc4_bytes() + 2 * config.vocab * config.hidden
-    return {
+    weights = ("BC4-encoded (this build's PTQ encoder on the GPU) N(0, 0.02^2) weights, "
+               f"{modeling.DISTINCT_LAYERS} distinct layer sets" if args.model_weights == "encoded"
+               else "uniform random BC4 block bytes")
+    out = {
         "config": model_name, "layers": config.layers, "hidden": config.hidden, "bc4_bytes": config.bc4_bytes(),
+        "weights": args.model_weights,
         "prefill_tokens": args.prompt,
-        "prefill_tok_s": round(pre["fused_bc4_mfma"]["gpu_tokens_per_second"], 1),
-        "prefill_ms": round(pre["fused_bc4_mfma"]["gpu_seconds_median"] * 1e3, 2),
-        "prefill_gemv_only_tok_s": round(pre["scalar_gemv"]["gpu_tokens_per_second"], 1),
-        "prefill_correctness": pre["correctness"],
+        "prefill_tok_s": round(pre["fused_bc4_mfma"]["gpu_tokens_per_second"], 1) if pre else None,
+        "prefill_ms": round(pre["fused_bc4_mfma"]["gpu_seconds_median"] * 1e3, 2) if pre else None,
+        "prefill_gemv_only_tok_s": round(pre["scalar_gemv"]["gpu_tokens_per_second"], 1) if pre else None,
+        "prefill_correctness": pre["correctness"] if pre else gate_failed,
+        "prefill_gate_failed": gate_failed is not None,
         "decode_context": [args.prompt, context],
         "decode_tok_s": round(dec["gpu_tokens_per_second"], 2),
         "decode_ms_per_token": round(dec["ms_per_token"], 3),
         "decode_timed_steps": dec["timed_steps"],
         "decode_per_bucket_tok_s": {k: round(v["tokens_per_second"], 2) for k, v in dec["per_bucket"].items()},
-        "decode_tok_s_projected": round(sampled["gpu_tokens_per_second"], 2) if sampled else None,
-        "decode_projected_sample_steps": args.decode_sample if sampled else None,
         "decode_weight_bytes_per_token": bytes_per_token,
-        "data": "random-init weights (BC4 blocks uniform, GPT-2 depth-scaled init), random prompt",
+        "data": f"random-init {weights} (GPT-2 depth-scaled init), uniform random prompt",
+    }
+    return out
+
+
+def hf_section(torch, args) -> dict:
+    """BASELINE config 4 through the reference's calling path: a Hugging Face Qwen2 with
+    TexelatorLinear modules (``texelator_amd.hf.build_qwen2``), the reference's prefill protocol on
+    it (``model.model(input_ids=...)``) and greedy ``model.generate`` of 256 tokens after a 512-token
+    prompt, timed on the host clock (``hf.benchmark_generate``)."""
+    from texelator_amd import hf, modeling, prefill
+    from texelator_amd.runtime import free
+
+    config = modeling.DecoderConfig.qwen25_3b_style()
+    model, handles = hf.build_qwen2(config, seed=SEED, weights=args.model_weights)
+    try:
+        try:
+            pre = prefill.benchmark_prefill(model, tokens=args.prompt, warmup=1, runs=3)
+            gate_failed = None
+        except prefill.GateFailed as error:
+            log(str(error))
+            pre, gate_failed = None, error.correctness
+        gen = hf.benchmark_generate(model, prompt_tokens=args.prompt, new_tokens=256, runs=2)
+    finally:
+        free(handles)
+        del model
+        torch.cuda.empty_cache()
+    return {
+        "config": "3b", "path": "transformers Qwen2ForCausalLM + TexelatorLinear (install_standalone form)",
+        "weights": args.model_weights,
+        "prefill_tokens": args.prompt,
+        "prefill_tok_s": round(pre["fused_bc4_mfma"]["gpu_tokens_per_second"], 1) if pre else None,
+        "prefill_gemv_only_tok_s": round(pre["scalar_gemv"]["gpu_tokens_per_second"], 1) if pre else None,
+        "prefill_correctness": pre["correctness"] if pre else gate_failed,
+        "prefill_gate_failed": gate_failed is not None,
+        "generate_new_tokens": gen["new_tokens"],
+        "decode_tok_s": round(gen["decode_tok_s"], 2),
+        "generate_tok_s": round(gen["generate_tok_s"], 2),
+        "generate_seconds": round(gen["generate_seconds"], 3),
     }
 
 
@@ -430,9 +473,10 @@ def main() -> int:
     parser.add_argument("--no-small-model", action="store_true",
                         help="skip the Qwen2.5-3B-style decoder (BASELINE config 4) after the 27B-class one")
     parser.add_argument("--prompt", type=int, default=512, help="prefill tokens")
-    parser.add_argument("--decode-sample", type=int, default=64,
-                        help="also report decode projected from this many steps per 512-position bucket "
-                             "(0 = only the fully timed decode)")
+    parser.add_argument("--model-weights", choices=("encoded", "uniform"), default="encoded",
+                        help="BC4 data of the model-level decoders: encoded random-init weights or uniform bytes")
+    parser.add_argument("--no-hf", action="store_true",
+                        help="skip the Hugging Face (reference calling path) measurement of BASELINE config 4")
     parser.add_argument("--model-only", action="store_true",
                         help="profiling mode: only the model-level prefill and decode measurement (its JSON)")
     parser.add_argument("--prefill-only", action="store_true",
@@ -611,9 +655,14 @@ def main() -> int:
         # BASELINE config 4 as stated there: 512-token prompt, then 256 greedy decode steps
         log("model-level tok/s (3b)")
         result["model_3b"] = model_section(torch, args, "3b", args.prompt + 256)
+    if args.model != "none" and not args.no_hf:
+        log("model-level tok/s (3b, Hugging Face calling path)")
+        result["model_3b_hf"] = hf_section(torch, args)
     if "model" in result:
-        # the metric's second and third figures, fully timed
+        # the metric's second and third figures, fully timed; a prefill that
+        # fails the reference protocol's correctness gate is reported as failed, not timed
         result["prefill_tok_s_512"] = result["model"]["prefill_tok_s"]
+        result["prefill_gate_failed"] = result["model"]["prefill_gate_failed"]
         result["decode_tok_s"] = result["model"]["decode_tok_s"]
     if not args.no_cpu:
         log("cpu baseline")

@@ -156,3 +156,29 @@ def test_calibrated_artifact_installed_standalone_matches_dense(ext, tmp_path):
             assert rrms(want, got) < 2e-2
     finally:
         runtime.free(handles)
+
+
+def test_build_qwen2_reference_prefill_protocol_and_generate(ext):
+    """The reference's calling path at BASELINE config-4 shapes (4 of its 36 layers, so the test
+    stays short): ``hf.build_qwen2`` puts TexelatorLinear modules holding GPU-encoded random-init
+    weights into a meta-initialised Qwen2, ``prefill.benchmark_prefill`` runs the reference's
+    protocol on it (``model.model(input_ids=...)``, scalar-vs-hybrid gate on 32 tokens), and
+    greedy ``generate`` decodes through the same linears."""
+    from dataclasses import replace
+
+    from texelator_amd import hf, modeling, prefill
+
+    config = replace(modeling.DecoderConfig.qwen25_3b_style(), layers=4)
+    model, handles = hf.build_qwen2(config, seed=7)
+    try:
+        assert len(handles) == 4 * 7
+        assert isinstance(model.get_submodule("model.layers.3.mlp.down_proj"), runtime.TexelatorLinear)
+        result = prefill.benchmark_prefill(model, tokens=128, warmup=0, runs=1)
+        assert result["correctness"]["tokens"] == prefill.CORRECTNESS_TOKENS
+        assert result["correctness"]["relative_rms"] <= prefill.RRMS_LIMIT
+        assert result["model"]["num_hidden_layers"] == 4
+        assert result["fused_bc4_mfma"]["gpu_tokens_per_second"] > 0
+        timing = hf.benchmark_generate(model, prompt_tokens=64, new_tokens=4, runs=1)
+        assert timing["new_tokens"] == 4 and timing["decode_tok_s"] > 0
+    finally:
+        runtime.free(handles)

@@ -271,3 +271,57 @@ def test_runtime_dtype_gate():
     assert tuning._runtime_dtype({}) is torch.float16
     with pytest.raises(RuntimeError, match="unsupported"):
         tuning._runtime_dtype({"runtime_dtype": "float32"})
+
+
+def test_device_block_packing_matches_host_packing():
+    """``pack_blocks_tensor`` (on the endpoints' device) writes the bytes of ``pack_blocks``,
+    extreme endpoints and every selector value included."""
+    from texelator_amd import encoder
+
+    g = torch.Generator().manual_seed(11)
+    n = 257
+    e0 = torch.randint(-127, 128, (n,), generator=g, dtype=torch.int16)
+    e1 = torch.randint(-127, 128, (n,), generator=g, dtype=torch.int16)
+    e0[:3] = torch.tensor([-127, 127, 0], dtype=torch.int16)
+    e1[:3] = torch.tensor([127, -127, -1], dtype=torch.int16)
+    idx = torch.randint(0, 8, (n, 16), generator=g, dtype=torch.uint8)
+    idx[0] = 7
+    want = encoder.pack_blocks(e0, e1, idx)
+    got = encoder.pack_blocks_tensor(e0, e1, idx).numpy()
+    assert got.dtype == np.uint8 and got.shape == (n, 8)
+    assert np.array_equal(got, want)
+
+
+def test_tensor_encoder_matches_array_encoder():
+    """``encode_matrix_tensor`` keeps the result on the device and returns the bytes and scales of
+    ``encode_matrix`` for the same rows (here on the CPU, rows in several chunks)."""
+    from texelator_amd import encoder
+
+    g = torch.Generator().manual_seed(12)
+    w = torch.randn(37, 64, generator=g) * 0.02
+    hdiag = torch.ones(64)
+    lut = torch.from_numpy(bc4.palette())
+    want_blocks, want_scales = encoder.encode_matrix(w, hdiag, lut, rows_per_chunk=16)
+    blocks, scales = encoder.encode_matrix_tensor(w, hdiag, lut, rows_per_chunk=16)
+    assert np.array_equal(blocks.numpy(), want_blocks)
+    assert np.array_equal(scales.numpy(), want_scales)
+
+
+def test_qwen2_config_of_decoder_config():
+    """The Hugging Face model that stands in for BASELINE config 4 has its shapes."""
+    pytest.importorskip("transformers")
+    from texelator_amd import hf, modeling
+
+    c = modeling.DecoderConfig.qwen25_3b_style()
+    q = hf.qwen2_config(c)
+    assert (q.num_hidden_layers, q.hidden_size, q.intermediate_size) == (36, 2048, 11008)
+    assert (q.num_attention_heads, q.num_key_value_heads, q.head_dim) == (16, 2, 128)
+    assert (q.vocab_size, q.rms_norm_eps, q.tie_word_embeddings) == (151936, 1e-6, False)
+    assert q.rope_parameters["rope_theta"] == 1e6
+
+
+def test_prefill_benchmark_rejects_plain_models():
+    from texelator_amd import prefill
+
+    with pytest.raises(TypeError, match="installed Texelator linears"):
+        prefill._Target(nn.Linear(4, 4))

@@ -128,6 +128,39 @@ def pack_blocks(endpoint0: torch.Tensor, endpoint1: torch.Tensor, indices: torch
     return packed
 
 
+def pack_blocks_tensor(endpoint0: torch.Tensor, endpoint1: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:
+    """:func:`pack_blocks` on the endpoints' own device: ``[N, 8]`` uint8 tensor, same bytes."""
+    fields = torch.zeros(indices.shape[0], dtype=torch.int64, device=indices.device)
+    for position in range(16):
+        fields |= (indices[:, position].to(torch.int64) & 7) << (3 * position)
+    packed = torch.empty((indices.shape[0], 8), dtype=torch.uint8, device=indices.device)
+    packed[:, 0] = endpoint0.to(torch.int16).to(torch.uint8)     # two's complement byte
+    packed[:, 1] = endpoint1.to(torch.int16).to(torch.uint8)
+    for byte in range(6):
+        packed[:, 2 + byte] = ((fields >> (8 * byte)) & 0xFF).to(torch.uint8)
+    return packed
+
+
+@torch.inference_mode()
+def encode_matrix_tensor(weight: torch.Tensor, hdiag: torch.Tensor, lut: torch.Tensor,
+                         rows_per_chunk: int = 2048) -> tuple[torch.Tensor, torch.Tensor]:
+    """:func:`encode_matrix` kept on ``lut``'s device: ``(blocks [M, K/16*8] uint8, scales [M]
+    float32)`` tensors, the same bytes (no host round trip, for building large models)."""
+    m, k = map(int, weight.shape)
+    if k % 16:
+        raise ValueError(f"unsupported K={k}; BC4 needs K % 16 == 0")
+    hdiag = hdiag.to(lut.device)
+    blocks = torch.empty((m, k // 16 * 8), dtype=torch.uint8, device=lut.device)
+    scales = torch.empty(m, dtype=torch.float32, device=lut.device)
+    for start in range(0, m, rows_per_chunk):
+        rows = weight[start:start + rows_per_chunk].detach().float().to(lut.device)
+        row_scales = rows.abs().amax(1).clamp_min(1e-12)
+        e0, e1, idx = endpoint_opt(rows, hdiag, row_scales, lut)
+        blocks[start:start + rows.shape[0]] = pack_blocks_tensor(e0, e1, idx).reshape(rows.shape[0], -1)
+        scales[start:start + rows.shape[0]] = row_scales
+    return blocks, scales
+
+
 @torch.inference_mode()
 def encode_rows(weight: torch.Tensor, hdiag: torch.Tensor, lut: torch.Tensor,
                 rows_per_chunk: int = 128):

@@ -83,6 +83,19 @@ def random_bc4(m: int, k: int, generator: torch.Generator, device: torch.device,
     return blocks, scales
 
 
+def encoded_bc4(m: int, k: int, generator: torch.Generator, lut: torch.Tensor, std: float = 0.02
+                ) -> tuple[torch.Tensor, torch.Tensor]:
+    """A random-init dense weight ``N(0, std^2)`` [M, K], BC4-encoded on the device by this build's
+    PTQ encoder (no activation moments): ``(blocks, scales)`` device tensors in the reference's
+    block layout. This is what a converted random-init model holds."""
+    from .encoder import encode_matrix_tensor
+
+    weight = torch.randn((m, k), device=lut.device, generator=generator) * std
+    blocks, scales = encode_matrix_tensor(weight, torch.ones(k, device=lut.device), lut)
+    del weight
+    return blocks.reshape(-1), scales
+
+
 def init_std(config: "DecoderConfig", name: str, depth_scaled: bool) -> float:
     """Random-init standard deviation of a linear: Hugging Face's ``initializer_range`` 0.02.
     With ``depth_scaled``, the two projections that write into the residual stream (o_proj,
@@ -90,6 +103,11 @@ def init_std(config: "DecoderConfig", name: str, depth_scaled: bool) -> float:
     if depth_scaled and name in ("self_attn.o_proj", "mlp.down_proj"):
         return 0.02 / math.sqrt(2 * config.layers)
     return 0.02
+
+
+# Distinct encoded weight sets of a random-init model (layer i uses set i % DISTINCT_LAYERS; each
+# layer still holds its own copy in memory, so every decode step streams the whole model from HBM).
+DISTINCT_LAYERS = 4
 
 
 # Merged handles of a layer: rows of q, k, v (one launch) and of gate, up (one launch).
@@ -128,7 +146,8 @@ class BC4Decoder:
 
     def __init__(self, config: DecoderConfig, max_context: int, device: torch.device | str = "cuda", seed: int = 0,
                  lookahead: int = 1, linear_source=None, depth_scaled: bool = True, embed_std: float = 1.0,
-                 fused: bool = True, split_decode: bool = True, gate_up_lookahead: int = 1):
+                 fused: bool = True, split_decode: bool = True, gate_up_lookahead: int = 1,
+                 weights: str = "encoded", distinct_layers: int = DISTINCT_LAYERS):
         """``linear_source(layer, name, m, k)`` may return ``(blocks, scales)`` device tensors for a
         linear (reference block layout). By default every linear is a seeded random BC4 matrix.
 
@@ -146,7 +165,19 @@ class BC4Decoder:
         the decode and prefill kernels are not amplified chaotically through 64 layers:
         - ``depth_scaled``: GPT-2's 1/sqrt(2 * layers) on o_proj and down_proj;
         - a unit-scale embedding (``embed_std``).
-        ``depth_scaled=False, embed_std=0.02`` gives Hugging Face's plain init."""
+        ``depth_scaled=False, embed_std=0.02`` gives Hugging Face's plain init.
+
+        ``weights`` chooses the BC4 data of the linears that ``linear_source`` does not supply:
+        ``"encoded"`` (the default) encodes dense ``N(0, std^2)`` weights with this build's PTQ
+        encoder on the GPU, as a converted random-init model holds; ``distinct_layers`` such
+        weight sets are encoded and layer i takes set ``i % distinct_layers`` (each layer still
+        has its own copy in memory). ``"uniform"`` draws every block byte uniformly (every
+        endpoint and selector value occurs), with row scales setting the weights' spread."""
+        if weights not in ("encoded", "uniform"):
+            raise ValueError("weights must be 'encoded' or 'uniform'")
+        if distinct_layers < 1:
+            raise ValueError("distinct_layers must be positive")
+        self.weights = weights
         self.config = config
         self.device = torch.device(device)
         self.max_context = int(max_context)
@@ -169,6 +200,26 @@ class BC4Decoder:
         self.handles: list[int] = []
         self.layers: list[_Layer] = []
         shapes = {name: (m, k) for name, m, k in c.linear_shapes()}
+        encoded_sets: dict[tuple[int, str], tuple[torch.Tensor, torch.Tensor]] = {}
+        lut = None
+        if weights == "encoded" and linear_source is None:
+            from .hardware import device_palette
+
+            lut = device_palette(self.device).reshape(255, 255, 8)
+
+        def weight_source(index: int, name: str, m: int, k: int):
+            if linear_source is not None:
+                source = linear_source(index, name, m, k)
+                if source is not None:
+                    return source
+            std = init_std(c, name, depth_scaled)
+            if weights == "uniform":
+                return random_bc4(m, k, g, self.device, std)
+            key = (index % distinct_layers, name)
+            if key not in encoded_sets:
+                encoded_sets[key] = encoded_bc4(m, k, g, lut, std)
+            return encoded_sets[key]
+
         try:
             for index in range(c.layers):
                 layer = _Layer()
@@ -178,9 +229,7 @@ class BC4Decoder:
                     parts_blocks, parts_scales, row = [], [], 0
                     for name in names:
                         m, k = shapes[name]
-                        source = linear_source(index, name, m, k) if linear_source else None
-                        blocks, scales = source if source is not None else random_bc4(
-                            m, k, g, self.device, init_std(c, name, depth_scaled))
+                        blocks, scales = weight_source(index, name, m, k)
                         parts_blocks.append(blocks.reshape(-1))
                         parts_scales.append(scales.reshape(-1).float())
                         layer.rows[name] = (row, m)
@@ -200,6 +249,8 @@ class BC4Decoder:
         except Exception:
             free(self.handles)
             raise
+        finally:
+            encoded_sets.clear()
         # K and V caches [layer, kv_head, position, head_dim]
         shape = (c.layers, c.kv_heads, self.max_context, c.head_dim)
         self.k_cache = torch.zeros(shape, device=self.device, dtype=bf16)

@@ -1,6 +1,7 @@
-"""Prefill and decode benchmarks of a BC4 decoder (``texelator/prefill.py`` of the reference).
+"""Prefill and decode benchmarks of a BC4 model (``texelator/prefill.py`` of the reference).
 
-``benchmark_prefill`` keeps the reference's protocol (``prefill.py:63-131``):
+``benchmark_prefill`` keeps the reference's protocol (``prefill.py:63-131``), which defines what its
+prefill tok/s means:
 1. Correctness on the first <= 32 prompt tokens. The "scalar" path sends every token through the
    decode GEMV (prefill threshold 1<<30); the hybrid path uses the prefill GEMM (threshold 1).
    Their final hidden states must agree within relative RMS 0.02 (``prefill.py:88-108``).
@@ -8,143 +9,174 @@
    (``prefill.py:29-60``).
 
 The prompt is ``randint(0, vocab, (tokens,))`` from a CPU generator seeded 0 (``prefill.py:82-85``).
-The model is a :class:`texelator_amd.modeling.BC4Decoder`, either passed in or loaded from an
-artifact whose manifest carries a ``decoder`` config.
+The model is either this build's :class:`texelator_amd.modeling.BC4Decoder` or, as in the
+reference, a Hugging Face causal LM whose linears are ``TexelatorLinear`` modules
+(``runtime.install``, ``runtime.install_standalone``, :func:`texelator_amd.hf.build_qwen2`), whose
+forward is ``model.model(input_ids=...)`` (``prefill.py:24-26``).
 
-``benchmark_decode`` times greedy decode steps replayed as HIP graphs, from the prompt length up
-to a context length.
+``benchmark_decode`` times greedy decode steps of a ``BC4Decoder`` replayed as HIP graphs, from the
+prompt length up to a context length.
 """
 from __future__ import annotations
 
-import json
 import math
 import statistics
 import time
 from dataclasses import asdict
 from pathlib import Path
+from typing import NamedTuple
 
-import numpy as np
 import torch
 
-from .artifacts import environment_snapshot, read_manifest, weights_dir, write_json
-from .modeling import BC4Decoder, DecoderConfig
-from .runtime import PREFILL_THRESHOLD, PREFILL_TILE_ROWS
+from .artifacts import environment_snapshot, write_json
+from .modeling import BC4Decoder
+from .runtime import PREFILL_THRESHOLD, PREFILL_TILE_ROWS, extension
 
 CORRECTNESS_TOKENS = 32
 RRMS_LIMIT = 0.02
 
 
-def load_decoder(artifact: Path, max_context: int, lookahead: int = 1, seed: int = 0) -> BC4Decoder:
-    """A decoder whose linears come from an artifact (``model.layers.{i}.{self_attn|mlp}.*_proj``
-    entries) and whose other parameters are seeded random; the manifest's ``decoder`` holds the
-    :class:`DecoderConfig` fields."""
-    manifest = read_manifest(artifact)
-    if "decoder" not in manifest:
-        raise RuntimeError("the prefill benchmark requires an artifact with a 'decoder' config")
-    config = DecoderConfig(**manifest["decoder"])
-    weights = weights_dir(artifact)
-    entries = {e["module_name"]: e for e in json.loads((weights / "metadata.json").read_text())["entries"]}
+class GateFailed(RuntimeError):
+    """The hybrid path missed the correctness gate; ``correctness`` holds the figures."""
 
-    def source(layer: int, name: str, m: int, k: int):
-        entry = entries.get(f"model.layers.{layer}.{name}")
-        if entry is None:
-            raise RuntimeError(f"artifact has no entry for model.layers.{layer}.{name}")
-        if (int(entry["M"]), int(entry["K"])) != (m, k):
-            raise RuntimeError(f"model.layers.{layer}.{name} is {entry['M']}x{entry['K']}, expected {m}x{k}")
-        blocks = torch.from_numpy(np.fromfile(weights / entry["blocks_file"], dtype=np.uint8)).cuda()
-        scales = torch.from_numpy(np.fromfile(weights / entry["scales_file"], dtype="<f4")).cuda()
-        return blocks, scales
-
-    return BC4Decoder(config, max_context, lookahead=lookahead, seed=seed, linear_source=source)
+    def __init__(self, correctness: dict):
+        super().__init__(f"hybrid prefill correctness failed: {correctness}")
+        self.correctness = correctness
 
 
-def _forward(model: BC4Decoder, ids: torch.Tensor) -> torch.Tensor:
-    with torch.inference_mode():
-        return model.hidden_states(ids, model.key_positions[:ids.numel()], ids.numel())
+class _Target:
+    """What the protocol drives: a forward over one token row returning the final hidden states
+    ``[tokens, hidden]``, and the prefill threshold of every BC4 handle of the model."""
+
+    def __init__(self, model):
+        if isinstance(model, BC4Decoder):
+            self.handles = list(model.handles)
+            self.vocab = model.config.vocab
+            self.device = model.device
+            self.description = asdict(model.config)
+            self._forward = lambda ids, cache: model.hidden_states(ids, model.key_positions[:ids.numel()], ids.numel())
+            return
+        handles = getattr(model, "_texelator_handles", None)
+        if not handles or not hasattr(model, "model"):
+            raise TypeError("benchmark_prefill needs a BC4Decoder or a causal LM with installed Texelator linears")
+        from torch.nn.attention import SDPBackend, sdpa_kernel
+
+        self.handles = list(handles)
+        self.vocab = int(model.get_input_embeddings().weight.shape[0])
+        self.device = model.get_input_embeddings().weight.device
+        self.description = {"hf_class": type(model).__name__, **{
+            key: getattr(model.config, key, None) for key in
+            ("num_hidden_layers", "hidden_size", "intermediate_size", "num_attention_heads", "num_key_value_heads")}}
+
+        def forward(ids, cache):
+            with sdpa_kernel([SDPBackend.FLASH_ATTENTION]):
+                out = model.model(input_ids=ids[None, :], use_cache=cache, return_dict=True)
+            return out.last_hidden_state[0]
+
+        self._forward = forward
+
+    def set_threshold(self, threshold: int) -> None:
+        ext = extension()
+        for handle in self.handles:
+            ext.set_prefill(handle, threshold, PREFILL_TILE_ROWS)
+
+    def forward(self, ids: torch.Tensor, use_cache: bool = False) -> torch.Tensor:
+        """Final hidden states; ``use_cache`` lets a Hugging Face model build its KV cache, as the
+        reference's timed forwards do (``prefill.py:29-60``)."""
+        with torch.inference_mode():
+            return self._forward(ids, use_cache)
 
 
-def _measure(model: BC4Decoder, ids: torch.Tensor, warmup: int, runs: int) -> dict:
+class _Sample(NamedTuple):
+    wall: float
+    gpu: float
+
+
+def _timed(target: _Target, ids: torch.Tensor, warmup: int, runs: int) -> dict:
+    """Median wall-clock and event time of ``runs`` forwards after ``warmup`` untimed ones."""
     for _ in range(warmup):
-        _forward(model, ids)
+        target.forward(ids, use_cache=True)
     torch.cuda.synchronize()
-    wall, gpu = [], []
-    for _ in range(runs):
-        start = torch.cuda.Event(enable_timing=True)
-        stop = torch.cuda.Event(enable_timing=True)
-        before = time.perf_counter()
-        start.record()
-        _forward(model, ids)
-        stop.record()
+    samples: list[_Sample] = []
+    while len(samples) < runs:
+        begin, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        started = time.perf_counter()
+        begin.record()
+        target.forward(ids, use_cache=True)
+        end.record()
         torch.cuda.synchronize()
-        wall.append(time.perf_counter() - before)
-        gpu.append(start.elapsed_time(stop) / 1000.0)
+        samples.append(_Sample(time.perf_counter() - started, begin.elapsed_time(end) / 1e3))
     tokens = int(ids.numel())
-    return {
-        "tokens": tokens, "warmup": warmup, "runs": runs, "wall_seconds": wall, "gpu_seconds": gpu,
-        "wall_seconds_median": statistics.median(wall), "gpu_seconds_median": statistics.median(gpu),
-        "wall_tokens_per_second": tokens / statistics.median(wall),
-        "gpu_tokens_per_second": tokens / statistics.median(gpu),
-    }
+    wall = statistics.median(s.wall for s in samples)
+    gpu = statistics.median(s.gpu for s in samples)
+    return {"tokens": tokens, "warmup": warmup, "runs": runs,
+            "wall_seconds": [s.wall for s in samples], "gpu_seconds": [s.gpu for s in samples],
+            "wall_seconds_median": wall, "gpu_seconds_median": gpu,
+            "wall_tokens_per_second": tokens / wall, "gpu_tokens_per_second": tokens / gpu}
 
 
-def prompt_ids(model: BC4Decoder, tokens: int, seed: int = 0) -> torch.Tensor:
+def _agreement(reference: torch.Tensor, candidate: torch.Tensor) -> dict:
+    """Relative RMS, largest absolute difference and cosine of two hidden-state tensors."""
+    ref, cand = reference.float().reshape(-1), candidate.float().reshape(-1)
+    ref_rms = float(ref.square().mean().sqrt())
+    diff = cand - ref
+    return {"max_abs": float(diff.abs().max()),
+            "relative_rms": float(diff.square().mean().sqrt()) / max(ref_rms, 1e-12),
+            "cosine": float(torch.nn.functional.cosine_similarity(ref[None], cand[None]))}
+
+
+def prompt_ids(model, tokens: int, seed: int = 0) -> torch.Tensor:
+    """The protocol's prompt: ``tokens`` ids uniform over the vocabulary, CPU generator ``seed``."""
+    target = model if isinstance(model, _Target) else _Target(model)
     generator = torch.Generator(device="cpu").manual_seed(seed)
-    return torch.randint(0, model.config.vocab, (tokens,), generator=generator, dtype=torch.int64).to(model.device)
+    return torch.randint(0, target.vocab, (tokens,), generator=generator, dtype=torch.int64).to(target.device)
 
 
-def benchmark_prefill(source, tokens: int, warmup: int, runs: int, output: Path | None = None,
-                      max_context: int | None = None, rrms_limit: float | None = RRMS_LIMIT) -> dict:
-    """``rrms_limit=None`` reports the correctness figures without enforcing the gate."""
+def benchmark_prefill(model, tokens: int, warmup: int, runs: int, output: Path | None = None,
+                      rrms_limit: float | None = RRMS_LIMIT) -> dict:
+    """The reference's prefill benchmark on ``model`` (a ``BC4Decoder`` or a Hugging Face model
+    with Texelator linears). Raises if the hybrid path fails the correctness gate; with
+    ``rrms_limit=None`` the figures are reported without the gate."""
     if not torch.cuda.is_available():
         raise RuntimeError("prefill benchmark requires a visible GPU")
     if tokens < PREFILL_THRESHOLD:
         raise ValueError(f"tokens must be at least the hybrid threshold ({PREFILL_THRESHOLD})")
     if warmup < 0 or runs < 1:
         raise ValueError("warmup must be non-negative and runs must be positive")
-    owned = not isinstance(source, BC4Decoder)
-    model = load_decoder(Path(source), max_context or tokens) if owned else source
+    target = _Target(model)
     try:
-        ids = prompt_ids(model, tokens)
-        check_ids = ids[:min(tokens, CORRECTNESS_TOKENS)]
-        model.set_prefill(1 << 30, PREFILL_TILE_ROWS)
-        reference = _forward(model, check_ids).float()
-        model.set_prefill(1, PREFILL_TILE_ROWS)
-        candidate = _forward(model, check_ids).float()
-        difference = candidate - reference
-        reference_rms = float(torch.sqrt(torch.mean(reference * reference)).item())
-        correctness = {
-            "tokens": int(check_ids.numel()),
-            "max_abs": float(difference.abs().max().item()),
-            "relative_rms": float(torch.sqrt(torch.mean(difference * difference)).item()) / max(reference_rms, 1e-12),
-            "cosine": float(torch.nn.functional.cosine_similarity(reference.reshape(1, -1),
-                                                                  candidate.reshape(1, -1)).item()),
-        }
-        correctness["limit"] = rrms_limit
-        if rrms_limit is not None and (not math.isfinite(correctness["relative_rms"])
-                                       or correctness["relative_rms"] > rrms_limit):
-            raise RuntimeError(f"hybrid prefill correctness failed: {correctness}")
-        model.set_prefill(1 << 30, PREFILL_TILE_ROWS)
-        scalar = _measure(model, ids, warmup, runs)
-        model.set_prefill(1, PREFILL_TILE_ROWS)
-        hybrid = _measure(model, ids, warmup, runs)
+        ids = prompt_ids(target, tokens)
+        check = ids[:min(tokens, CORRECTNESS_TOKENS)]
+        hidden = {}
+        for path, threshold in (("scalar", 1 << 30), ("hybrid", 1)):
+            target.set_threshold(threshold)
+            hidden[path] = target.forward(check).float()
+        correctness = {"tokens": int(check.numel()), **_agreement(hidden["scalar"], hidden["hybrid"]),
+                       "limit": rrms_limit}
+        del hidden
+        failed = not math.isfinite(correctness["relative_rms"]) or (
+            rrms_limit is not None and correctness["relative_rms"] > rrms_limit)
+        if rrms_limit is not None and failed:
+            raise GateFailed(correctness)
+        timings = {}
+        for path, threshold in (("scalar_gemv", 1 << 30), ("fused_bc4_mfma", 1)):
+            target.set_threshold(threshold)
+            timings[path] = _timed(target, ids, warmup, runs)
         result = {
             "schema_version": 1,
-            "model": asdict(model.config),
+            "model": target.description,
             "prefill_tile_rows": PREFILL_TILE_ROWS,
             "correctness": correctness,
-            "scalar_gemv": scalar,
-            "fused_bc4_mfma": hybrid,
-            "speedup_wall": scalar["wall_seconds_median"] / hybrid["wall_seconds_median"],
-            "speedup_gpu": scalar["gpu_seconds_median"] / hybrid["gpu_seconds_median"],
+            **timings,
+            "speedup_wall": timings["scalar_gemv"]["wall_seconds_median"] / timings["fused_bc4_mfma"]["wall_seconds_median"],
+            "speedup_gpu": timings["scalar_gemv"]["gpu_seconds_median"] / timings["fused_bc4_mfma"]["gpu_seconds_median"],
             "environment": environment_snapshot(),
         }
         if output is not None:
             write_json(Path(output), result)
         return result
     finally:
-        model.set_prefill(PREFILL_THRESHOLD, PREFILL_TILE_ROWS)
-        if owned:
-            model.close()
+        target.set_threshold(PREFILL_THRESHOLD)
 
 
 def benchmark_decode(model: BC4Decoder, prompt_tokens: int, context: int, warmup_steps: int = 8,
