@@ -249,6 +249,15 @@ int tx_linear_split(uint64_t handle, const void *x, void *stream);
  * GEMV unsplit without LUT mode (TX_ERR_UNSUPPORTED otherwise: use tx_linear + tx_swiglu). */
 int tx_linear_swiglu(uint64_t handle, const void *x, void *out, void *stream);
 
+/* The prefill of a merged [gate (inter) | up (inter)] handle with SwiGLU applied in the GEMM's
+ * epilogue (no reference counterpart: the reference's prefill writes the linear output and Hugging
+ * Face applies the activation): out bf16 [tokens][inter] = tx_swiglu(tx_linear(handle, x)), bit
+ * for bit, in one kernel and without the [tokens][2 * inter] intermediate. x bf16 [tokens][K].
+ * Needs inter % 16 == 0, a BF16 bias or none, tokens at or above the handle's prefill threshold,
+ * and a call whose prefill runs the wide tile (candidate 7) without a K split
+ * (TX_ERR_UNSUPPORTED otherwise: use tx_linear + tx_swiglu). */
+int tx_linear_swiglu_prefill(uint64_t handle, const void *x, int64_t tokens, void *out, void *stream);
+
 /* tx_add_rmsnorm for one row whose delta is the output of delta_handle (M == hidden). */
 int tx_add_rmsnorm_split(float *residual, uint64_t delta_handle, const void *weight, float eps, void *out,
                          int64_t hidden, void *stream);

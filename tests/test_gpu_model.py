@@ -6,6 +6,7 @@ from __future__ import annotations
 
 import math
 
+import numpy as np
 import pytest
 import torch
 from torch.nn import functional
@@ -374,3 +375,79 @@ def test_prompt_flash_attention_matches_cached_attention(ext, tiny):
         finally:
             tiny.flash_prompt_attention = True
     assert rrms(b, a) < 1e-2
+
+
+@pytest.mark.parametrize("inter,k,tokens,bias,forced", [
+    (27648, 5120, 512, False, False),   # the 27B gate|up: its default prefill is the wide tile, unsplit
+    (1024, 512, 512, True, True),
+    (208, 272, 300, False, True),       # a partial row tile, K not a multiple of 128, a partial token tile
+    (2048, 384, 700, True, True),       # two token tiles
+])
+def test_linear_swiglu_prefill_is_bit_identical(ext, inter, k, tokens, bias, forced):
+    """The gate|up prefill GEMM with the SwiGLU epilogue == linear + swiglu, bit for bit."""
+    handle = _random_handle(ext, 2 * inter, k, seed=inter + tokens, bias=bias)
+    try:
+        if forced:
+            ext.set_prefill_backend(handle, 7)
+        g = torch.Generator(device="cuda").manual_seed(19)
+        for scale in (1.0, 30.0):  # large inputs drive silu into both saturated ends
+            x = (scale * torch.randn(tokens, k, device="cuda", generator=g)).to(torch.bfloat16)
+            want = layers.swiglu(ext.linear(handle, x))
+            got = layers.linear_swiglu_prefill(handle, x)
+            assert got.shape == (tokens, inter)
+            assert torch.equal(want, got)
+    finally:
+        ext.free(handle)
+
+
+def test_linear_swiglu_prefill_lut_mode_is_bit_identical(ext):
+    """The same with the palette read from a table (a perturbed palette)."""
+    from oracle import bc4
+
+    rng = np.random.default_rng(23)
+    table = (bc4.palette() * (1 + 0.01 * rng.standard_normal((255, 255, 8)))).astype(np.float32)
+    handle = _random_handle(ext, 2 * 512, 640, seed=29, bias=True)
+    try:
+        ext.set_palette_table(handle, torch.from_numpy(table).cuda())
+        ext.set_prefill_backend(handle, 7)
+        x = torch.randn(512, 640, device="cuda", generator=torch.Generator(device="cuda").manual_seed(31)).to(torch.bfloat16)
+        want = layers.swiglu(ext.linear(handle, x))
+        assert torch.equal(want, layers.linear_swiglu_prefill(handle, x))
+    finally:
+        ext.free(handle)
+
+
+def test_linear_swiglu_prefill_refuses_other_calls(ext):
+    handle = _random_handle(ext, 2 * 1024, 5120, seed=3)
+    odd = _random_handle(ext, 48, 256, seed=4)
+    x = torch.zeros(128, 5120, device="cuda", dtype=torch.bfloat16)
+    try:
+        with pytest.raises(_lib.UnsupportedError):   # 128 tokens: the default prefill is another tile
+            layers.linear_swiglu_prefill(handle, x)
+        with pytest.raises(_lib.UnsupportedError):   # below the prefill threshold
+            layers.linear_swiglu_prefill(handle, x[:8])
+        with pytest.raises(_lib.TexelatorError, match="16-row aligned"):
+            layers.linear_swiglu_prefill(odd, x[:, :256].contiguous())
+    finally:
+        ext.free(handle)
+        ext.free(odd)
+
+
+def test_decoder_prefill_with_fused_swiglu_is_bit_identical(ext):
+    """Two layers of the 27B-class decoder: the 512-token prefill whose gate|up GEMM applies SwiGLU
+    in its epilogue gives the hidden states of the GEMM + SwiGLU kernels, bit for bit."""
+    from dataclasses import replace
+
+    model = modeling.BC4Decoder(replace(modeling.DecoderConfig.class_27b(), layers=2), max_context=512, seed=5)
+    try:
+        ids = prefill.prompt_ids(model, 512)
+        positions = model.key_positions[:512]
+        x = torch.zeros(512, model.config.hidden, device="cuda", dtype=torch.bfloat16)
+        layers.linear_swiglu_prefill(model.layers[0].handles["gate_up"], x)   # the fused path applies
+        with torch.inference_mode():
+            fused = model.hidden_states(ids, positions, 512).clone()
+            model.gate_up_swiglu_prefill = False
+            plain = model.hidden_states(ids, positions, 512)
+        assert torch.equal(fused, plain)
+    finally:
+        model.close()

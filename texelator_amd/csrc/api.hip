@@ -706,6 +706,43 @@ int tx_linear_swiglu(uint64_t value, const void *x, void *out, void *stream) {
   return TX_OK;
 }
 
+// The prefill tile with the SwiGLU epilogue (wide_512x128x64).
+constexpr int kWideCandidate = 7;
+
+int tx_linear_swiglu_prefill(uint64_t value, const void *x, int64_t tokens, void *out, void *stream) {
+  g_last_error.clear();
+  Handle *h = as_handle(value);
+  if (!h) return fail(TX_ERR_INVALID, "null Texelator handle");
+  if (!x || !out) return fail(TX_ERR_INVALID, "null input or output pointer");
+  if (reinterpret_cast<uintptr_t>(x) % 16 != 0) return fail(TX_ERR_INVALID, "input must be 16-byte aligned");
+  if (h->M % 32 != 0) return fail(TX_ERR_INVALID, "linear_swiglu_prefill: the handle must hold [gate | up] with 16-row aligned halves");
+  if (h->bias && h->bias_dtype != TX_DTYPE_BF16) return fail(TX_ERR_INVALID, "linear_swiglu_prefill: the bias must be BF16");
+  if (tokens > (1 << 20)) return fail(TX_ERR_INVALID, "token count exceeds the prefill limit (1048576)");
+  if (tokens < 2 || tokens < h->prefill_threshold)
+    return fail(TX_ERR_UNSUPPORTED, "linear_swiglu_prefill: the call is below the prefill threshold (use tx_linear_swiglu "
+                                    "for one token, tx_linear + tx_swiglu otherwise)");
+  if (prefill_choice(h, tokens) != kWideCandidate || tx::prefill_splits(h->M, h->CG, tokens, h->cus) != 1)
+    return fail(TX_ERR_UNSUPPORTED, "linear_swiglu_prefill: this call's prefill runs another tile or splits K "
+                                    "(use tx_linear + tx_swiglu)");
+  DeviceGuard guard(h->device);
+  tx::PrefillParams p{};
+  p.lut = h->lut;
+  p.tiles = h->tiles;
+  p.scales = h->scales;
+  p.x = x;
+  p.bias = h->bias;
+  p.y = out;
+  p.M = h->M;
+  p.K = h->K;
+  p.Mp = h->Mp;
+  p.RG = h->RG;
+  p.CG = h->CG;
+  p.tokens = (int)tokens;
+  p.ks = 1;
+  TX_HIP(tx::launch_prefill_swiglu(p, reinterpret_cast<hipStream_t>(stream)));
+  return TX_OK;
+}
+
 int tx_add_rmsnorm_split(float *residual, uint64_t delta_handle, const void *weight, float eps, void *out, int64_t hidden,
                          void *stream) {
   g_last_error.clear();

@@ -95,9 +95,10 @@ struct WorkItem {
   int t0, n0, c_begin, nc, split;
 };
 
-// Token-tile-major, then split, then row tile; contiguous ranges go to one XCD.
-__device__ __forceinline__ bool work_item(const PrefillParams &p, int BT, int BN, WorkItem &w) {
-  const int n_rows = (p.M + BN - 1) / BN;
+// Token-tile-major, then split, then row tile; contiguous ranges go to one XCD. `rows` rows are
+// tiled (p.M unless given).
+__device__ __forceinline__ bool work_item(const PrefillParams &p, int BT, int BN, WorkItem &w, int rows = -1) {
+  const int n_rows = ((rows < 0 ? p.M : rows) + BN - 1) / BN;
   const int n_tok = (p.tokens + BT - 1) / BT;
   const int items = n_rows * n_tok * p.ks;
   const int per_xcd = (items + kXcds - 1) / kXcds;
@@ -690,8 +691,16 @@ constexpr int kWideThreads = 64 * kWideWaves;
 constexpr int kHalfK = kTileK / 2;
 
 // KFULL: K is a multiple of 128 (no staging of columns past K).
-template <bool F16, bool LUT, bool KFULL>
+// SWIGLU: p holds a merged [gate | up] matrix (M = 2 * inter, inter a multiple of 16, one K
+// split, bf16): the workgroup's 128 rows are gate rows n0..n0+63 and the matching up rows, as row
+// blocks [gate 0-31 | up 0-31 | gate 32-63 | up 32-63], so each wave holds a gate accumulator and
+// the up accumulator of the same rows and tokens; the epilogue writes
+// y[t][n] = bf16(silu(G) * U) for inter columns, with G and U the bf16 outputs the plain epilogue
+// would store (bias added with its second rounding) -- the bits of the GEMM followed by the
+// SwiGLU kernel, without the [tokens][2 * inter] intermediate.
+template <bool F16, bool LUT, bool KFULL, bool SWIGLU = false>
 __global__ __launch_bounds__(kWideThreads) void prefill_wide_kernel(PrefillParams p) {
+  static_assert(!SWIGLU || !F16, "the SwiGLU epilogue is bf16");
   constexpr int WV = kWideWaves;
   static_assert(WV == 4 || WV == 8, "4 or 8 waves");
   constexpr int BT = 512, BN = 128;
@@ -708,7 +717,7 @@ __global__ __launch_bounds__(kWideThreads) void prefill_wide_kernel(PrefillParam
   __shared__ __attribute__((aligned(128))) uint16_t xs1[BT * kHalfK];
 
   WorkItem w;
-  if (!work_item(p, BT, BN, w)) return;
+  if (!work_item(p, BT, SWIGLU ? BN / 2 : BN, w, SWIGLU ? p.M / 2 : -1)) return;
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -726,7 +735,15 @@ __global__ __launch_bounds__(kWideThreads) void prefill_wide_kernel(PrefillParam
   const int slot = DEC == 2 ? (int)threadIdx.x : (int)(threadIdx.x >> 1);
   const int sub = (slot >> 4) & 1;
   const int drow = 16 * (slot >> 5) + (slot & 15);  // row within the 128
-  const int g = min(w.n0 / kTileRows + (slot >> 5), p.RG - 1);
+  int g;
+  if constexpr (SWIGLU) {
+    // 16-row group q of the workgroup: row block q / 2 (gate if even, up if odd) of pair q / 4
+    const int q = slot >> 5, half_rg = p.RG / 2;
+    const int gate_rg = min(w.n0 / kTileRows + 2 * (q >> 2) + (q & 1), half_rg - 1);
+    g = gate_rg + (((q >> 1) & 1) ? half_rg : 0);
+  } else {
+    g = min(w.n0 / kTileRows + (slot >> 5), p.RG - 1);
+  }
   const uint4 *gt = p.tiles + ((size_t)g * p.CG + w.c_begin) * 64 + (slot & 15) + 16 * sub;
   const float scale = p.scales[g * kTileRows + (slot & 15)];
   const uint32_t pm = pm_scale_pair<F16>(scale);
@@ -938,6 +955,36 @@ __global__ __launch_bounds__(kWideThreads) void prefill_wide_kernel(PrefillParam
 
   // acc[tb][rb][r] = D[row 8(r/4) + 4h + r%4 of row block RW*rg + rb][token 128*tg + 32*tb + r32].
   const uint16_t *bias = static_cast<const uint16_t *>(p.bias);
+  if constexpr (SWIGLU) {
+    // Row blocks RW*rg + 2i (gate) and + 1 (up) cover gate-space rows 32*(RW/2*rg + i) of the 64.
+    const int inter = p.M / 2;
+#pragma unroll
+    for (int tb = 0; tb < TW; ++tb) {
+      const int t = w.t0 + 128 * tg + tb * 32 + r32;
+      if (t >= p.tokens) continue;
+#pragma unroll
+      for (int i = 0; i < RW / 2; ++i) {
+        __builtin_amdgcn_sched_barrier(0);
+        const f32x16 &vg = acc[tb][2 * i], &vu = acc[tb][2 * i + 1];
+#pragma unroll
+        for (int rq = 0; rq < 4; ++rq) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int n = w.n0 + 32 * (RW / 2 * rg + i) + 8 * rq + 4 * h + r;
+            if (n < inter) {
+              float gv = round_out<false>(vg[4 * rq + r]), uv = round_out<false>(vu[4 * rq + r]);
+              if (bias) {
+                gv = round_out<false>(gv + bf(bias[n]));
+                uv = round_out<false>(uv + bf(bias[inter + n]));
+              }
+              static_cast<uint16_t *>(p.y)[(size_t)t * inter + n] = to_bf(swiglu_value(gv, uv));
+            }
+          }
+        }
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int tb = 0; tb < TW; ++tb) {
     const int t = w.t0 + 128 * tg + tb * 32 + r32;
@@ -1066,6 +1113,14 @@ hipError_t launch_wide(const PrefillParams &p, hipStream_t stream) {
   return launch_reduce(p, stream);
 }
 
+template <bool LUT>
+void launch_wide_swiglu_as(const PrefillParams &p, int grid, hipStream_t stream) {
+  if (p.K % kTileK == 0)
+    hipLaunchKernelGGL((prefill_wide_kernel<false, LUT, true, true>), dim3(grid), dim3(kWideThreads), 0, stream, p);
+  else
+    hipLaunchKernelGGL((prefill_wide_kernel<false, LUT, false, true>), dim3(grid), dim3(kWideThreads), 0, stream, p);
+}
+
 template <int TB, int RB, int LA, bool PIPE>
 hipError_t launch_tile(const PrefillParams &p, hipStream_t stream) {
   constexpr int BT = 32 * TB, BN = 128 * RB;
@@ -1180,6 +1235,15 @@ int prefill_splits(int M, int CG, int64_t tokens, int cus) {
 
 bool prefill_candidate_eligible(int candidate, int M, int K) {
   return find(candidate) != nullptr && M > 0 && K > 0 && K % 16 == 0;
+}
+
+hipError_t launch_prefill_swiglu(const PrefillParams &p, hipStream_t stream) {
+  if (p.f16 || p.ks != 1 || p.M % 32 != 0) return hipErrorInvalidValue;
+  const int items = ((p.M / 2 + 63) / 64) * ((p.tokens + 511) / 512);
+  const int grid = ((items + kXcds - 1) / kXcds) * kXcds;
+  if (p.lut) launch_wide_swiglu_as<true>(p, grid, stream);
+  else launch_wide_swiglu_as<false>(p, grid, stream);
+  return hipGetLastError();
 }
 
 hipError_t launch_prefill(const PrefillParams &p, int candidate, hipStream_t stream) {

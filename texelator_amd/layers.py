@@ -154,6 +154,22 @@ def linear_swiglu(handle: int, x: torch.Tensor, out: torch.Tensor | None = None)
     return out
 
 
+def linear_swiglu_prefill(handle: int, x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """``swiglu(linear(handle, x))`` for a prefill-sized ``x`` [tokens, K] of a merged ``[gate | up]``
+    handle, in one GEMM whose epilogue applies SwiGLU (bit-identical to the two calls). Raises
+    ``UnsupportedError`` where the call's prefill would not run the wide tile unsplit."""
+    _expect(x.is_cuda and x.dtype == torch.bfloat16 and x.is_contiguous() and x.dim() == 2 and x.data_ptr() % 16 == 0,
+            "x must be a contiguous, 16-byte aligned CUDA bf16 [tokens, K] tensor")
+    m, k = _hip_shape(handle)
+    _expect(x.shape[1] == k, "x has the wrong width for this handle")
+    tokens = x.shape[0]
+    if out is None:
+        out = torch.empty((tokens, m // 2), dtype=torch.bfloat16, device=x.device)
+    _expect(out.dtype == torch.bfloat16 and out.is_contiguous() and out.shape == (tokens, m // 2), "bad output")
+    check(_lib.load().tx_linear_swiglu_prefill(handle, _ptr(x), tokens, _ptr(out), _stream(x)))
+    return out
+
+
 def add_rmsnorm_split(residual: torch.Tensor, delta_handle: int, weight: torch.Tensor, eps: float,
                       out: torch.Tensor) -> torch.Tensor:
     """:func:`add_rmsnorm` of one row whose delta is the last :func:`linear_split` of ``delta_handle``."""

@@ -29,6 +29,7 @@ from torch.nn import functional
 from torch.nn.attention import SDPBackend, sdpa_kernel
 
 from . import layers
+from ._lib import UnsupportedError
 from .runtime import TexelatorLinear, extension, free
 
 
@@ -184,6 +185,8 @@ class BC4Decoder:
         self.fused = fused
         self.split_decode = fused and split_decode
         self.flash_prompt_attention = fused
+        # prefill of the merged gate|up handle with the SwiGLU epilogue where the call allows it
+        self.gate_up_swiglu_prefill = fused
         ext = extension()
         c = config
         if fused and not layers.decode_attention_supported(c):
@@ -390,7 +393,7 @@ class BC4Decoder:
             else:
                 attn = self._cached_attention(index, q.view(tokens, c.heads, c.head_dim), positions, length)
             layers.add_rmsnorm(h, layer.linears["o"](attn), layer.post_norm, c.rms_eps, out=x)
-            act = layers.swiglu(layer.linears["gate_up"](x))
+            act = self._gate_up_swiglu_tokens(layer, x)
             following = self.layers[index + 1].input_norm if index + 1 < len(self.layers) else self.final_norm
             layers.add_rmsnorm(h, layer.linears["down"](act), following, c.rms_eps, out=x)
         return x
@@ -420,6 +423,17 @@ class BC4Decoder:
         splits, lut = extension().gemv_plan(handle)
         if splits == 1 and not lut and self.config.intermediate % 16 == 0:
             return layers.linear_swiglu(handle, x, out=self.act_buffer)
+        return layers.swiglu(layer.linears["gate_up"](x))
+
+    def _gate_up_swiglu_tokens(self, layer: _Layer, x: torch.Tensor) -> torch.Tensor:
+        """SwiGLU of the merged gate|up projection of several tokens: one prefill GEMM with the
+        SwiGLU epilogue where the call runs the wide tile unsplit (bit-identical to the GEMM +
+        SwiGLU kernels it replaces), else those two kernels."""
+        if x.shape[0] > 1 and self.gate_up_swiglu_prefill:
+            try:
+                return layers.linear_swiglu_prefill(layer.handles["gate_up"], x)
+            except UnsupportedError:
+                pass
         return layers.swiglu(layer.linears["gate_up"](x))
 
     def logits(self, hidden: torch.Tensor) -> torch.Tensor:
