@@ -254,8 +254,8 @@ int tx_linear_swiglu(uint64_t handle, const void *x, void *out, void *stream);
  * Face applies the activation): out bf16 [tokens][inter] = tx_swiglu(tx_linear(handle, x)), bit
  * for bit, in one kernel and without the [tokens][2 * inter] intermediate. x bf16 [tokens][K].
  * Needs inter % 16 == 0, a BF16 bias or none, tokens at or above the handle's prefill threshold,
- * and a call whose prefill runs the wide tile (candidate 7) without a K split
- * (TX_ERR_UNSUPPORTED otherwise: use tx_linear + tx_swiglu). */
+ * and a call whose prefill runs tile 6, 7, 8 or 9 without a K split (TX_ERR_UNSUPPORTED otherwise,
+ * e.g. for the pair tile 5 or the dense backend 1: use tx_linear + tx_swiglu). */
 int tx_linear_swiglu_prefill(uint64_t handle, const void *x, int64_t tokens, void *out, void *stream);
 
 /* tx_add_rmsnorm for one row whose delta is the output of delta_handle (M == hidden). */

@@ -377,18 +377,26 @@ def test_prompt_flash_attention_matches_cached_attention(ext, tiny):
     assert rrms(b, a) < 1e-2
 
 
-@pytest.mark.parametrize("inter,k,tokens,bias,forced", [
-    (27648, 5120, 512, False, False),   # the 27B gate|up: its default prefill is the wide tile, unsplit
-    (1024, 512, 512, True, True),
-    (208, 272, 300, False, True),       # a partial row tile, K not a multiple of 128, a partial token tile
-    (2048, 384, 700, True, True),       # two token tiles
+@pytest.mark.parametrize("inter,k,tokens,bias,tile", [
+    (27648, 5120, 512, False, None),    # the 27B gate|up: its default prefill is the wide tile, unsplit
+    (11008, 2048, 512, True, None),     # the 3B gate|up: the 128-token tile, unsplit
+    (1024, 512, 512, True, 7),
+    (208, 272, 300, False, 7),          # a partial row tile, K not a multiple of 128, a partial token tile
+    (2048, 384, 700, True, 7),          # two token tiles
+    (1024, 512, 128, True, 6),
+    (208, 272, 100, False, 6),
+    (1024, 512, 64, False, 8),
+    (208, 272, 40, True, 8),
+    (1024, 512, 32, True, 9),
+    (208, 272, 17, False, 9),
 ])
-def test_linear_swiglu_prefill_is_bit_identical(ext, inter, k, tokens, bias, forced):
-    """The gate|up prefill GEMM with the SwiGLU epilogue == linear + swiglu, bit for bit."""
+def test_linear_swiglu_prefill_is_bit_identical(ext, inter, k, tokens, bias, tile):
+    """The gate|up prefill GEMM with the SwiGLU epilogue == linear + swiglu, bit for bit, on the
+    wide tile and the 128-, 64- and 32-token tiles."""
     handle = _random_handle(ext, 2 * inter, k, seed=inter + tokens, bias=bias)
     try:
-        if forced:
-            ext.set_prefill_backend(handle, 7)
+        if tile is not None:
+            ext.set_prefill_backend(handle, tile)
         g = torch.Generator(device="cuda").manual_seed(19)
         for scale in (1.0, 30.0):  # large inputs drive silu into both saturated ends
             x = (scale * torch.randn(tokens, k, device="cuda", generator=g)).to(torch.bfloat16)
@@ -422,10 +430,14 @@ def test_linear_swiglu_prefill_refuses_other_calls(ext):
     odd = _random_handle(ext, 48, 256, seed=4)
     x = torch.zeros(128, 5120, device="cuda", dtype=torch.bfloat16)
     try:
-        with pytest.raises(_lib.UnsupportedError):   # 128 tokens: the default prefill is another tile
+        with pytest.raises(_lib.UnsupportedError):   # 128 tokens over 40 tile columns: K is split
             layers.linear_swiglu_prefill(handle, x)
         with pytest.raises(_lib.UnsupportedError):   # below the prefill threshold
             layers.linear_swiglu_prefill(handle, x[:8])
+        ext.set_prefill_backend(odd, 5)
+        ext.set_prefill_backend(handle, 5)
+        with pytest.raises(_lib.UnsupportedError):   # the pair tile has no SwiGLU epilogue
+            layers.linear_swiglu_prefill(handle, torch.zeros(512, 5120, device="cuda", dtype=torch.bfloat16))
         with pytest.raises(_lib.TexelatorError, match="16-row aligned"):
             layers.linear_swiglu_prefill(odd, x[:, :256].contiguous())
     finally:

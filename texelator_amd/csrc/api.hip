@@ -706,9 +706,6 @@ int tx_linear_swiglu(uint64_t value, const void *x, void *out, void *stream) {
   return TX_OK;
 }
 
-// The prefill tile with the SwiGLU epilogue (wide_512x128x64).
-constexpr int kWideCandidate = 7;
-
 int tx_linear_swiglu_prefill(uint64_t value, const void *x, int64_t tokens, void *out, void *stream) {
   g_last_error.clear();
   Handle *h = as_handle(value);
@@ -721,9 +718,10 @@ int tx_linear_swiglu_prefill(uint64_t value, const void *x, int64_t tokens, void
   if (tokens < 2 || tokens < h->prefill_threshold)
     return fail(TX_ERR_UNSUPPORTED, "linear_swiglu_prefill: the call is below the prefill threshold (use tx_linear_swiglu "
                                     "for one token, tx_linear + tx_swiglu otherwise)");
-  if (prefill_choice(h, tokens) != kWideCandidate || tx::prefill_splits(h->M, h->CG, tokens, h->cus) != 1)
-    return fail(TX_ERR_UNSUPPORTED, "linear_swiglu_prefill: this call's prefill runs another tile or splits K "
-                                    "(use tx_linear + tx_swiglu)");
+  const int candidate = prefill_choice(h, tokens);
+  if (!tx::prefill_swiglu_supported(candidate) || tx::prefill_splits(h->M, h->CG, tokens, h->cus) != 1)
+    return fail(TX_ERR_UNSUPPORTED, "linear_swiglu_prefill: this call's prefill runs the pair tile or the dense "
+                                    "backend, or splits K (use tx_linear + tx_swiglu)");
   DeviceGuard guard(h->device);
   tx::PrefillParams p{};
   p.lut = h->lut;
@@ -739,7 +737,7 @@ int tx_linear_swiglu_prefill(uint64_t value, const void *x, int64_t tokens, void
   p.CG = h->CG;
   p.tokens = (int)tokens;
   p.ks = 1;
-  TX_HIP(tx::launch_prefill_swiglu(p, reinterpret_cast<hipStream_t>(stream)));
+  TX_HIP(tx::launch_prefill_swiglu(p, candidate, reinterpret_cast<hipStream_t>(stream)));
   return TX_OK;
 }
 

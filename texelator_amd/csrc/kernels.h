@@ -70,10 +70,11 @@ bool prefill_candidate_eligible(int candidate, int M, int K);
 int prefill_default_candidate(int M, int K, int64_t tokens, int cus);
 int prefill_splits(int M, int CG, int64_t tokens, int cus);
 hipError_t launch_prefill(const PrefillParams &p, int candidate, hipStream_t stream);
-// The wide tile (candidate 7) on a merged [gate | up] matrix (p.M = 2 * inter, inter a multiple of
-// 16, p.ks == 1, bf16) with a SwiGLU epilogue: p.y receives bf16 [tokens][inter], the bits of
-// launch_prefill(p, 7) followed by launch_swiglu.
-hipError_t launch_prefill_swiglu(const PrefillParams &p, hipStream_t stream);
+// Tile `candidate` (6-9) on a merged [gate | up] matrix (p.M = 2 * inter, inter a multiple of 16,
+// p.ks == 1, bf16) with a SwiGLU epilogue: p.y receives bf16 [tokens][inter], the bits of
+// launch_prefill(p, candidate) followed by launch_swiglu.
+bool prefill_swiglu_supported(int candidate);
+hipError_t launch_prefill_swiglu(const PrefillParams &p, int candidate, hipStream_t stream);
 hipError_t prefill_kernel_attributes(int candidate, hipFuncAttributes *attr, int *lds_bytes);
 const char *prefill_candidate_name(int candidate);
 void prefill_candidate_shape(int candidate, int *tokens, int *rows, int *k);

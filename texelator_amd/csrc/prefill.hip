@@ -120,9 +120,15 @@ __device__ __forceinline__ bool work_item(const PrefillParams &p, int BT, int BN
 // the bias with a second fp16 rounding, :630-635).
 // PIPE: software-pipelined K loop (tile j+1 decoded while tile j is multiplied). LUT: palettes
 // read from p.lut (a 255 x 255 x 8 fp32 table) instead of computed.
-template <bool F16, int TB, int RB, int LA, bool PIPE, bool LUT>
+// SWIGLU (RB = 1, bf16, one K split): p holds a merged [gate | up] matrix (M = 2 * inter, inter a
+// multiple of 16); wave w owns gate rows n0 + 32 * (w / 2) .. + 31 (w even) or the matching up rows
+// (w odd), and the epilogue writes y[t][n] = bf16(silu(G) * U) for inter columns, G and U being
+// the bf16 outputs the plain epilogue would store: each up wave hands its accumulators to its gate
+// partner through LDS. The bits of the GEMM followed by the SwiGLU kernel.
+template <bool F16, int TB, int RB, int LA, bool PIPE, bool LUT, bool SWIGLU = false>
 __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillParams p) {
   static_assert(!PIPE || LA >= 2, "the pipelined K loop needs two weight tiles in flight");
+  static_assert(!SWIGLU || (RB == 1 && !F16), "the SwiGLU epilogue pairs the waves' row blocks (bf16)");
   constexpr int BT = 32 * TB;
   constexpr int BN = 128 * RB;
   constexpr int XC = BT * 16 / kThreads;  // 16-byte activation chunks staged per thread per step
@@ -135,7 +141,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillParams p) {
   __shared__ __attribute__((aligned(16))) PaletteTableStorage tables;
 
   WorkItem w;
-  if (!work_item(p, BT, BN, w)) return;
+  if (!work_item(p, BT, SWIGLU ? BN / 2 : BN, w, SWIGLU ? p.M / 2 : -1)) return;
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -153,7 +159,13 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillParams p) {
   uint32_t pm[RB];
 #pragma unroll
   for (int b = 0; b < RB; ++b) {
-    const int g = min(w.n0 / kTileRows + (wave * RB + b) * 2 + (r32 >> 4), p.RG - 1);
+    int g;
+    if constexpr (SWIGLU) {
+      const int half_rg = p.RG / 2;
+      g = min(w.n0 / kTileRows + (wave >> 1) * 2 + (r32 >> 4), half_rg - 1) + ((wave & 1) ? half_rg : 0);
+    } else {
+      g = min(w.n0 / kTileRows + (wave * RB + b) * 2 + (r32 >> 4), p.RG - 1);
+    }
     gtiles[b] = p.tiles + ((size_t)g * p.CG + w.c_begin) * 64 + (lane & 15) + 16 * h;
     scale[b] = p.scales[g * kTileRows + (lane & 15)];
     pm[b] = pm_scale_pair<F16>(scale[b]);
@@ -420,6 +432,44 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillParams p) {
 
   // acc[tb][b][r] = D[row 8(r/4) + 4h + r%4 of row block b][token tb*32 + r32].
   const uint16_t *bias = static_cast<const uint16_t *>(p.bias);
+  if constexpr (SWIGLU) {
+    // Up waves (odd) hand their accumulators to their gate partners through the activation
+    // buffer, laid out [pair][tb][r][lane] (every LDS access of the K loop ended at its last
+    // barrier); gate waves then apply SwiGLU to matching elements.
+    float *xch = reinterpret_cast<float *>(xs0);
+    const int pair = wave >> 1;
+    if (wave & 1) {
+#pragma unroll
+      for (int tb = 0; tb < TB; ++tb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) xch[((pair * TB + tb) * 16 + r) * 64 + lane] = acc[tb][0][r];
+    }
+    __syncthreads();
+    if (wave & 1) return;
+    const int inter = p.M / 2;
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb) {
+      const int t = w.t0 + tb * 32 + r32;
+      if (t >= p.tokens) continue;
+#pragma unroll
+      for (int rq = 0; rq < 4; ++rq) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int n = w.n0 + 32 * pair + 8 * rq + 4 * h + r;
+          if (n < inter) {
+            float gv = round_out<false>(acc[tb][0][4 * rq + r]);
+            float uv = round_out<false>(xch[((pair * TB + tb) * 16 + 4 * rq + r) * 64 + lane]);
+            if (bias) {
+              gv = round_out<false>(gv + bf(bias[n]));
+              uv = round_out<false>(uv + bf(bias[inter + n]));
+            }
+            static_cast<uint16_t *>(p.y)[(size_t)t * inter + n] = to_bf(swiglu_value(gv, uv));
+          }
+        }
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int tb = 0; tb < TB; ++tb) {
     const int t = w.t0 + tb * 32 + r32;
@@ -1237,13 +1287,34 @@ bool prefill_candidate_eligible(int candidate, int M, int K) {
   return find(candidate) != nullptr && M > 0 && K > 0 && K % 16 == 0;
 }
 
-hipError_t launch_prefill_swiglu(const PrefillParams &p, hipStream_t stream) {
-  if (p.f16 || p.ks != 1 || p.M % 32 != 0) return hipErrorInvalidValue;
-  const int items = ((p.M / 2 + 63) / 64) * ((p.tokens + 511) / 512);
+template <int TB, int LA, bool PIPE>
+hipError_t launch_tile_swiglu(const PrefillParams &p, hipStream_t stream) {
+  const int items = ((p.M / 2 + 63) / 64) * ((p.tokens + 32 * TB - 1) / (32 * TB));
   const int grid = ((items + kXcds - 1) / kXcds) * kXcds;
-  if (p.lut) launch_wide_swiglu_as<true>(p, grid, stream);
-  else launch_wide_swiglu_as<false>(p, grid, stream);
+  if (p.lut)
+    hipLaunchKernelGGL((prefill_kernel<false, TB, 1, LA, PIPE, true, true>), dim3(grid), dim3(kThreads), 0, stream, p);
+  else
+    hipLaunchKernelGGL((prefill_kernel<false, TB, 1, LA, PIPE, false, true>), dim3(grid), dim3(kThreads), 0, stream, p);
   return hipGetLastError();
+}
+
+bool prefill_swiglu_supported(int candidate) { return candidate >= 6 && candidate <= 9; }
+
+hipError_t launch_prefill_swiglu(const PrefillParams &p, int candidate, hipStream_t stream) {
+  if (p.f16 || p.ks != 1 || p.M % 32 != 0) return hipErrorInvalidValue;
+  switch (candidate) {
+    case 6: return launch_tile_swiglu<4, TX_PREFILL_LA, true>(p, stream);
+    case 8: return launch_tile_swiglu<2, TX_PREFILL_LA_PLAIN, false>(p, stream);
+    case 9: return launch_tile_swiglu<1, TX_PREFILL_LA_PLAIN, false>(p, stream);
+    case 7: {
+      const int items = ((p.M / 2 + 63) / 64) * ((p.tokens + 511) / 512);
+      const int grid = ((items + kXcds - 1) / kXcds) * kXcds;
+      if (p.lut) launch_wide_swiglu_as<true>(p, grid, stream);
+      else launch_wide_swiglu_as<false>(p, grid, stream);
+      return hipGetLastError();
+    }
+    default: return hipErrorInvalidValue;
+  }
 }
 
 hipError_t launch_prefill(const PrefillParams &p, int candidate, hipStream_t stream) {

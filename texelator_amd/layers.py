@@ -157,7 +157,8 @@ def linear_swiglu(handle: int, x: torch.Tensor, out: torch.Tensor | None = None)
 def linear_swiglu_prefill(handle: int, x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
     """``swiglu(linear(handle, x))`` for a prefill-sized ``x`` [tokens, K] of a merged ``[gate | up]``
     handle, in one GEMM whose epilogue applies SwiGLU (bit-identical to the two calls). Raises
-    ``UnsupportedError`` where the call's prefill would not run the wide tile unsplit."""
+    ``UnsupportedError`` where the call's prefill would run the pair tile or the dense backend, or
+    split K."""
     _expect(x.is_cuda and x.dtype == torch.bfloat16 and x.is_contiguous() and x.dim() == 2 and x.data_ptr() % 16 == 0,
             "x must be a contiguous, 16-byte aligned CUDA bf16 [tokens, K] tensor")
     m, k = _hip_shape(handle)

@@ -427,7 +427,7 @@ class BC4Decoder:
 
     def _gate_up_swiglu_tokens(self, layer: _Layer, x: torch.Tensor) -> torch.Tensor:
         """SwiGLU of the merged gate|up projection of several tokens: one prefill GEMM with the
-        SwiGLU epilogue where the call runs the wide tile unsplit (bit-identical to the GEMM +
+        SwiGLU epilogue where the call's tile supports it unsplit (bit-identical to the GEMM +
         SwiGLU kernels it replaces), else those two kernels."""
         if x.shape[0] > 1 and self.gate_up_swiglu_prefill:
             try:
