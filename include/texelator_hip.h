@@ -220,6 +220,17 @@ int tx_decode_attention(const void *q, const void *k_cache, const void *v_cache,
                         int64_t length, int heads, int kv_heads, int head_dim, int64_t max_context, float scale,
                         void *workspace, int64_t workspace_bytes, void *out, void *stream);
 
+/* Causal self-attention of a prompt: query tokens 0..tokens-1 against cached keys and values
+ * 0..tokens-1 (caches [kv_heads][max_context][head_dim] bf16, written for the prompt by
+ * tx_rope_kv_cache), grouped-query (heads a multiple of kv_heads); head_dim must be 128. q bf16
+ * rows of heads * head_dim values every q_stride elements (16-byte aligned); out bf16 rows every
+ * out_stride elements. Scores from bf16 q and keys with fp32 sums, online fp32 softmax, the
+ * probabilities rounded to bf16 into the fp32 sum over the values (as flash attention does). No
+ * counterpart in the reference (its attention is the Hugging Face module's sdpa call). */
+int tx_prefill_attention(const void *q, int64_t q_stride, const void *k_cache, const void *v_cache, int64_t tokens,
+                         int heads, int kv_heads, int head_dim, int64_t max_context, float scale, void *out,
+                         int64_t out_stride, void *stream);
+
 /* tx_rope_kv_cache_split followed by tx_decode_attention, one kernel launch fewer: q and the new
  * token's key and value are the last tx_linear_split of qkv_handle ([q | k | v] rows), rotated
  * inside the attention kernel with rope_row = the RoPE tables' rows at *position (cos[head_dim]

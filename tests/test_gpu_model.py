@@ -463,3 +463,45 @@ def test_decoder_prefill_with_fused_swiglu_is_bit_identical(ext):
         assert torch.equal(fused, plain)
     finally:
         model.close()
+
+
+@pytest.mark.parametrize("tokens,heads,kv_heads", [(512, 40, 8), (300, 16, 2), (64, 4, 4), (1, 8, 1), (1000, 12, 4)])
+def test_prefill_attention_matches_fp32_reference(ext, tokens, heads, kv_heads):
+    """The prompt-attention kernel against a float32 causal softmax attention on the same bf16
+    inputs; cache rows past the prompt hold NaN, which must not reach any output."""
+    d, ctx = 128, 1088
+    g = torch.Generator(device="cuda").manual_seed(tokens + heads)
+    q = (torch.randn(tokens, heads * d, device="cuda", generator=g) * 2).to(torch.bfloat16)
+    kc = torch.full((kv_heads, ctx, d), float("nan"), device="cuda").to(torch.bfloat16)
+    vc = kc.clone()
+    kc[:, :tokens] = torch.randn(kv_heads, tokens, d, device="cuda", generator=g).to(torch.bfloat16)
+    vc[:, :tokens] = torch.randn(kv_heads, tokens, d, device="cuda", generator=g).to(torch.bfloat16)
+    scale = 1 / math.sqrt(d)
+    got = layers.prefill_attention(q, kc, vc, heads, kv_heads, scale)
+    torch.cuda.synchronize()
+    group = heads // kv_heads
+    qf = q.float().view(tokens, heads, d).transpose(0, 1)                        # [H, T, d]
+    kf = kc[:, :tokens].float().repeat_interleave(group, 0)                     # [H, T, d]
+    vf = vc[:, :tokens].float().repeat_interleave(group, 0)
+    scores = torch.matmul(qf, kf.transpose(1, 2).contiguous()) * scale          # fp32
+    mask = torch.triu(torch.ones(tokens, tokens, dtype=torch.bool, device="cuda"), 1)
+    probs = torch.softmax(scores.masked_fill(mask, float("-inf")), dim=-1)
+    want = torch.matmul(probs, vf).transpose(0, 1).reshape(tokens, heads * d)
+    assert torch.isfinite(got.float()).all()
+    assert rrms(want, got.float()) < 5e-3
+
+
+def test_decoder_prompt_attention_kernel_matches_flash(ext, tiny):
+    """The decoder's prompt with this library's attention kernel and with torch's flash kernel give
+    hidden states equal to within bf16 noise."""
+    ids = torch.randint(0, tiny.config.vocab, (200,), device="cuda", generator=torch.Generator(device="cuda").manual_seed(37))
+    positions = tiny.key_positions[:200]
+    with torch.inference_mode():
+        assert tiny.prompt_attention_kernel
+        own = tiny.hidden_states(ids, positions, 200).clone()
+        tiny.prompt_attention_kernel = False
+        try:
+            flash = tiny.hidden_states(ids, positions, 200)
+        finally:
+            tiny.prompt_attention_kernel = True
+    assert rrms(flash.float(), own.float()) < 1e-2

@@ -818,6 +818,25 @@ int tx_decode_attention(const void *q, const void *k_cache, const void *v_cache,
   return TX_OK;
 }
 
+int tx_prefill_attention(const void *q, int64_t q_stride, const void *k_cache, const void *v_cache, int64_t tokens,
+                         int heads, int kv_heads, int head_dim, int64_t max_context, float scale, void *out,
+                         int64_t out_stride, void *stream) {
+  g_last_error.clear();
+  if (!q || !k_cache || !v_cache || !out) return fail(TX_ERR_INVALID, "prefill_attention: null pointer");
+  if (!tx::prefill_attention_supported(heads, kv_heads, head_dim))
+    return fail(TX_ERR_UNSUPPORTED, "prefill_attention: needs head_dim 128 and heads a multiple of kv_heads");
+  if (tokens <= 0) return TX_OK;
+  if (tokens > max_context) return fail(TX_ERR_INVALID, "prefill_attention: more tokens than the cache holds");
+  if (tokens > (int64_t)65535 * 64) return fail(TX_ERR_INVALID, "prefill_attention: token grid exceeds the launch limit");
+  if (q_stride < (int64_t)heads * head_dim || out_stride < (int64_t)heads * head_dim || q_stride % 8 != 0 ||
+      reinterpret_cast<uintptr_t>(q) % 16 != 0)
+    return fail(TX_ERR_INVALID, "prefill_attention: q rows must be 16-byte aligned and hold heads * head_dim values");
+  TX_HIP(tx::launch_prefill_attention(static_cast<const uint16_t *>(q), q_stride, static_cast<const uint16_t *>(k_cache),
+                                      static_cast<const uint16_t *>(v_cache), tokens, heads, kv_heads, max_context, scale,
+                                      static_cast<uint16_t *>(out), out_stride, reinterpret_cast<hipStream_t>(stream)));
+  return TX_OK;
+}
+
 int tx_decode_attention_split(uint64_t qkv_handle, const int64_t *position, const float *rope_row, int64_t length,
                               int heads, int kv_heads, int head_dim, void *k_cache, void *v_cache,
                               int64_t max_context, float scale, void *workspace, int64_t workspace_bytes, void *out,

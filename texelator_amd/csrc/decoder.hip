@@ -543,6 +543,147 @@ __global__ __launch_bounds__(128) void decode_attention_combine_kernel(const flo
   out[(size_t)head * kHeadDim + dd] = to_bf(((acc[0] + acc[1]) + (acc[2] + acc[3])) / total);
 }
 
+// Causal self-attention of a prompt: query tokens 0..T-1 against keys 0..T-1 (the prompt's own
+// cache rows), grouped-query, head_dim 128. Block (query block of 64, head): wave w owns queries
+// 64*qb + 16w .. +15. For each key block of 64 keys up to the diagonal: the block's keys (padded
+// rows) and values (transposed, vt_index) go to LDS, staged through registers one block ahead;
+// scores S = q k^T on the matrix cores (bf16 products, fp32 sums), scaled and masked causally on
+// the diagonal block; an online softmax in fp32 (running max m and sum l per query, the output
+// rescaled by exp(m_old - m_new)); the probabilities rounded to bf16 (their rounded values summed
+// into l) and multiplied by the values on the matrix cores (fp32 sums). out = bf16(O / l).
+// Values of keys past the prompt are zeroed, so stale cache rows never reach the sums.
+constexpr int kPromptQueries = 64;
+
+__global__ __launch_bounds__(256) void prefill_attention_kernel(const uint16_t *q, int64_t q_stride, const uint16_t *k_cache,
+                                                                const uint16_t *v_cache, int tokens, int group,
+                                                                int64_t max_ctx, float scale, uint16_t *out,
+                                                                int64_t out_stride) {
+  __shared__ uint4 ks[kChunk * kKeyStrideU4];                // keys [key][128] bf16, padded rows
+  __shared__ __align__(16) uint16_t vt[kHeadDim * kChunk];    // values [dim][key] bf16 (vt_index)
+  __shared__ __align__(16) uint16_t ps[4][16][kPRow];         // per wave: probabilities [query][key] bf16
+  const int qb = blockIdx.x, head = blockIdx.y, kv = head / group;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int n = lane & 15, q4 = lane >> 4;
+  const int q0 = qb * kPromptQueries + 16 * wave;  // this wave's first query
+  // q as MFMA A operands: row n = query q0 + n (clamped into the prompt), dimensions 32 st + 8 q4 ..
+  dwordx4 qa[4];
+  {
+    const uint16_t *qr = q + (size_t)min(q0 + n, tokens - 1) * q_stride + (size_t)head * kHeadDim;
+#pragma unroll
+    for (int st = 0; st < 4; ++st) qa[st] = *reinterpret_cast<const dwordx4 *>(qr + 32 * st + 8 * q4);
+  }
+  // (32-bit byte offsets from the head's base: a head's cache is well under 4 GiB)
+  const char *kg = reinterpret_cast<const char *>(k_cache + (size_t)kv * max_ctx * kHeadDim);
+  const char *vg = reinterpret_cast<const char *>(v_cache + (size_t)kv * max_ctx * kHeadDim);
+  dwordx4 kr[4], vr[4];
+  auto load_block = [&](int kb) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int idx = u * 256 + tid;
+      const uint32_t row = (uint32_t)min((int64_t)(kb * kChunk + idx / kRowU4), max_ctx - 1);
+      const uint32_t off = (row * kRowU4 + idx % kRowU4) * 16u;
+      kr[u] = *reinterpret_cast<const dwordx4 *>(kg + off);
+      vr[u] = *reinterpret_cast<const dwordx4 *>(vg + off);
+    }
+  };
+  float m[4], l[4];  // running max and sum of the lane's rows, queries q0 + 4 q4 + r
+  f32x4_t o[8];      // o[dt][r] = O[query q0 + 4 q4 + r][dimension 16 dt + n]
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    m[r] = -INFINITY;
+    l[r] = 0.f;
+  }
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt) o[dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  load_block(0);
+  for (int kb = 0; kb <= qb; ++kb) {
+    __syncthreads();  // the previous block's tiles are no longer read
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int idx = u * 256 + tid;
+      const int key = idx / kRowU4, c = idx % kRowU4;
+      reinterpret_cast<dwordx4 *>(ks)[key * kKeyStrideU4 + c] = kr[u];
+      const dwordx4 v = kb * kChunk + key < tokens ? vr[u] : dwordx4{0, 0, 0, 0};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) vt[vt_index(8 * c + e, key)] = (uint16_t)(v[e / 2] >> (16 * (e & 1)));
+    }
+    __syncthreads();
+    if (kb < qb) load_block(kb + 1);  // in flight while this block is multiplied
+    // scores of sub-tile s (keys 16 s .. 16 s + 15 of the block): sc[s][r] = S[query q0+4q4+r][key 16s+n]
+    f32x4_t sc[4];
+#pragma unroll
+    for (int s4 = 0; s4 < 4; ++s4) {
+      const uint4 *krow = ks + (16 * s4 + n) * kKeyStrideU4;
+      f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int st = 0; st < 4; ++st) {
+        const uint4 b = krow[4 * st + q4];
+        acc = mfma_bf16(qa[st], dwordx4{b.x, b.y, b.z, b.w}, acc);
+      }
+      sc[s4] = acc;
+    }
+    const bool diagonal = kb == qb;
+    float mx[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      mx[r] = -INFINITY;
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4) {
+        const int key = kb * kChunk + 16 * s4 + n, query = q0 + 4 * q4 + r;
+        float v = sc[s4][r] * scale;
+        if (diagonal && (key > query || key >= tokens)) v = -INFINITY;
+        sc[s4][r] = v;
+        mx[r] = fmaxf(mx[r], v);
+      }
+#pragma unroll
+      for (int off = 1; off < 16; off <<= 1) mx[r] = fmaxf(mx[r], __shfl_xor(mx[r], off));
+    }
+    // Every row has an unmasked key in block 0 (key 0), so the running max is finite from there on.
+    float alpha[4], rs[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float mnew = fmaxf(m[r], mx[r]);
+      alpha[r] = expf(m[r] - mnew);
+      m[r] = mnew;
+      rs[r] = 0.f;
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4) {
+        const uint16_t pb = to_bf(expf(sc[s4][r] - mnew));
+        ps[wave][4 * q4 + r][16 * s4 + n] = pb;
+        rs[r] += bf(pb);
+      }
+#pragma unroll
+      for (int off = 1; off < 16; off <<= 1) rs[r] += __shfl_xor(rs[r], off);
+      l[r] = l[r] * alpha[r] + rs[r];
+    }
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) o[dt][r] *= alpha[r];
+    __syncthreads();  // the probabilities are in LDS
+    // O += P V: A = the probabilities (row n, keys 32 kst + 8 q4 ..), B = the transposed values
+#pragma unroll
+    for (int kst = 0; kst < kChunk / 32; ++kst) {
+      const uint4 a = *reinterpret_cast<const uint4 *>(&ps[wave][n][32 * kst + 8 * q4]);
+      const dwordx4 av = {a.x, a.y, a.z, a.w};
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) {
+        const uint4 b = *reinterpret_cast<const uint4 *>(&vt[vt_index(16 * dt + n, 32 * kst + 8 * q4)]);
+        o[dt] = mfma_bf16(av, dwordx4{b.x, b.y, b.z, b.w}, o[dt]);
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int query = q0 + 4 * q4 + r;
+    if (query >= tokens) continue;
+    const float inv = 1.0f / l[r];
+    uint16_t *dst = out + (size_t)query * out_stride + (size_t)head * kHeadDim + n;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) dst[16 * dt] = to_bf(o[dt][r] * inv);
+  }
+}
+
 // out[r][c] = bf16(silu(g) * u) with g = gu[r][c], u = gu[r][inter + c], in fp32.
 __global__ __launch_bounds__(256) void swiglu_kernel(const uint16_t *gu, int64_t rows, int64_t inter, uint16_t *out) {
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;   // one group of 8 columns
@@ -620,6 +761,19 @@ hipError_t launch_attention(const AttnInput &in, uint16_t *k_cache, uint16_t *v_
   return hipGetLastError();
 }
 }  // namespace
+
+bool prefill_attention_supported(int heads, int kv_heads, int head_dim) {
+  return head_dim == kHeadDim && kv_heads > 0 && heads % kv_heads == 0;
+}
+
+hipError_t launch_prefill_attention(const uint16_t *q, int64_t q_stride, const uint16_t *k_cache,
+                                    const uint16_t *v_cache, int64_t tokens, int heads, int kv_heads, int64_t max_ctx,
+                                    float scale, uint16_t *out, int64_t out_stride, hipStream_t stream) {
+  const dim3 grid((unsigned)((tokens + kPromptQueries - 1) / kPromptQueries), (unsigned)heads);
+  hipLaunchKernelGGL(prefill_attention_kernel, grid, dim3(256), 0, stream, q, q_stride, k_cache, v_cache, (int)tokens,
+                     heads / kv_heads, max_ctx, scale, out, out_stride);
+  return hipGetLastError();
+}
 
 hipError_t launch_decode_attention(const uint16_t *q, const uint16_t *k_cache, const uint16_t *v_cache,
                                    const int64_t *position, int64_t length, int heads, int kv_heads, int64_t max_ctx,

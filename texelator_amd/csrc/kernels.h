@@ -144,6 +144,12 @@ hipError_t launch_decode_attention_split(const SplitSource &qkv, const int64_t *
                                          int64_t length, int heads, int kv_heads,
                                          uint16_t *k_cache, uint16_t *v_cache, int64_t max_ctx, float scale,
                                          float *partials, uint16_t *out, hipStream_t stream);
+// Causal self-attention of a prompt (queries and keys 0..tokens-1, keys and values from the
+// caches [kv_heads][max_ctx][128]); q and out bf16 rows of heads * 128 with the given strides.
+bool prefill_attention_supported(int heads, int kv_heads, int head_dim);
+hipError_t launch_prefill_attention(const uint16_t *q, int64_t q_stride, const uint16_t *k_cache,
+                                    const uint16_t *v_cache, int64_t tokens, int heads, int kv_heads, int64_t max_ctx,
+                                    float scale, uint16_t *out, int64_t out_stride, hipStream_t stream);
 hipError_t launch_swiglu(const uint16_t *gu, int64_t rows, int64_t inter, uint16_t *out, hipStream_t stream);
 
 }  // namespace tx

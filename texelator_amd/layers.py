@@ -102,6 +102,28 @@ def decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
     return out
 
 
+def prefill_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, heads: int, kv_heads: int,
+                      scale: float, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Causal self-attention of a prompt: ``q`` bf16 ``[tokens, heads * head_dim]`` (rows 16-byte
+    aligned) at positions 0..tokens-1 against cache rows 0..tokens-1 of ``k_cache``/``v_cache``
+    (bf16 ``[kv_heads, max_context, head_dim]``). Returns bf16 ``[tokens, heads * head_dim]``."""
+    _expect(q.is_cuda and q.dtype == torch.bfloat16 and q.dim() == 2 and q.stride(1) == 1, "q must be bf16 [tokens, width]")
+    head_dim = k_cache.shape[2]
+    tokens = q.shape[0]
+    _expect(q.shape[1] == heads * head_dim, "q width must be heads * head_dim")
+    for cache in (k_cache, v_cache):
+        _expect(cache.dtype == torch.bfloat16 and cache.is_contiguous() and cache.shape[0] == kv_heads and
+                cache.device == q.device, "bad cache")
+    if out is None:
+        out = torch.empty((tokens, heads * head_dim), dtype=torch.bfloat16, device=q.device)
+    _expect(out.dtype == torch.bfloat16 and out.dim() == 2 and out.stride(1) == 1 and out.shape == (tokens, heads * head_dim),
+            "bad output")
+    check(_lib.load().tx_prefill_attention(_ptr(q), q.stride(0), _ptr(k_cache), _ptr(v_cache), tokens, heads, kv_heads,
+                                           head_dim, k_cache.shape[1], float(scale), _ptr(out), out.stride(0),
+                                           _stream(q)))
+    return out
+
+
 def decode_attention_split(qkv_handle: int, positions: torch.Tensor, rope_row: torch.Tensor, heads: int,
                            kv_heads: int, head_dim: int, k_cache: torch.Tensor, v_cache: torch.Tensor, length: int,
                            scale: float, workspace: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:

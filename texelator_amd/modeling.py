@@ -106,6 +106,11 @@ def init_std(config: "DecoderConfig", name: str, depth_scaled: bool) -> float:
     return 0.02
 
 
+def prompt_attention_supported(config: "DecoderConfig") -> bool:
+    """Whether the prompt-attention kernel handles this configuration (head_dim 128, grouped heads)."""
+    return config.head_dim == 128 and config.heads % config.kv_heads == 0
+
+
 # Distinct encoded weight sets of a random-init model (layer i uses set i % DISTINCT_LAYERS; each
 # layer still holds its own copy in memory, so every decode step streams the whole model from HBM).
 DISTINCT_LAYERS = 4
@@ -187,6 +192,8 @@ class BC4Decoder:
         self.flash_prompt_attention = fused
         # prefill of the merged gate|up handle with the SwiGLU epilogue where the call allows it
         self.gate_up_swiglu_prefill = fused
+        # a prompt's causal attention with this library's kernel (else torch's flash attention)
+        self.prompt_attention_kernel = fused and prompt_attention_supported(config)
         ext = extension()
         c = config
         if fused and not layers.decode_attention_supported(c):
@@ -312,12 +319,16 @@ class BC4Decoder:
         return (xf * cos + rotated * sin).to(torch.bfloat16)
 
     def _prompt_attention(self, index: int, q: torch.Tensor) -> torch.Tensor:
-        """Causal attention of a prompt (positions 0..T-1) over its own keys, q [T, heads, d], with
-        torch's flash-attention kernel (bf16 in, fp32 softmax); the prompt's keys and values are
-        the cache rows 0..T-1 that ``rope_kv_cache`` just wrote. Only the flash backend is allowed,
-        so an unsupported shape raises instead of running the unfused math path."""
+        """Causal attention of a prompt (positions 0..T-1) over its own keys, q [T, heads, d]; the
+        prompt's keys and values are the cache rows 0..T-1 that ``rope_kv_cache`` just wrote. This
+        library's prompt-attention kernel (bf16 in, online fp32 softmax), or, with
+        ``prompt_attention_kernel`` off, torch's flash-attention kernel (only the flash backend is
+        allowed, so an unsupported shape raises instead of running the unfused math path)."""
         c = self.config
         tokens = q.shape[0]
+        if self.prompt_attention_kernel:
+            return layers.prefill_attention(q.reshape(tokens, c.heads * c.head_dim), self.k_cache[index],
+                                            self.v_cache[index], c.heads, c.kv_heads, 1.0 / math.sqrt(c.head_dim))
         keys = self.k_cache[index, :, :tokens].unsqueeze(0)        # [1, kv, T, d]
         values = self.v_cache[index, :, :tokens].unsqueeze(0)
         with sdpa_kernel([SDPBackend.FLASH_ATTENTION]):
