@@ -544,27 +544,50 @@ __global__ __launch_bounds__(128) void decode_attention_combine_kernel(const flo
 }
 
 // Causal self-attention of a prompt: query tokens 0..T-1 against keys 0..T-1 (the prompt's own
-// cache rows), grouped-query, head_dim 128. Block (query block of 64, head): wave w owns queries
-// 64*qb + 16w .. +15. For each key block of 64 keys up to the diagonal: the block's keys (padded
-// rows) and values (transposed, vt_index) go to LDS, staged through registers one block ahead;
-// scores S = q k^T on the matrix cores (bf16 products, fp32 sums), scaled and masked causally on
-// the diagonal block; an online softmax in fp32 (running max m and sum l per query, the output
-// rescaled by exp(m_old - m_new)); the probabilities rounded to bf16 (their rounded values summed
-// into l) and multiplied by the values on the matrix cores (fp32 sums). out = bf16(O / l).
-// Values of keys past the prompt are zeroed, so stale cache rows never reach the sums.
+// cache rows), grouped-query, head_dim 128. Block (query block of 64, head), heaviest query blocks
+// first: wave w owns queries 64*qb + 16w .. +15. For each key block of 64 keys up to the diagonal:
+// the block's keys (padded rows) and values (transposed: lane l loads dimensions 2l, 2l+1 of eight
+// consecutive keys, one coalesced 256-byte key row per load, and writes them as two 8-key runs)
+// go to LDS, staged through registers one block ahead; scores S = q k^T on the matrix cores
+// (bf16 products, fp32 sums), scaled by scale*log2(e) and masked causally on the diagonal block;
+// an online softmax in fp32 with exp2 (running max m and sum l per query; row reductions over the
+// 16 lanes of a DPP row), the output rescaled by exp2(m_old - m_new); the probabilities rounded to
+// bf16 (their rounded values summed into l) and multiplied by the values on the matrix cores (fp32
+// sums). out = bf16(O / l). Values of keys past the prompt are zeroed, so stale cache rows never
+// reach the sums.
 constexpr int kPromptQueries = 64;
 
-__global__ __launch_bounds__(256) void prefill_attention_kernel(const uint16_t *q, int64_t q_stride, const uint16_t *k_cache,
+// Reductions over the 16 lanes of a DPP row (xor 1, xor 2, half-row mirror, row mirror): every
+// lane of the row ends with the same value.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp_mov<0xB1>(v));   // quad_perm [1,0,3,2]
+  v = fmaxf(v, dpp_mov<0x4E>(v));   // quad_perm [2,3,0,1]
+  v = fmaxf(v, dpp_mov<0x141>(v));  // row_half_mirror
+  return fmaxf(v, dpp_mov<0x140>(v));  // row_mirror
+}
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp_mov<0xB1>(v);
+  v += dpp_mov<0x4E>(v);
+  v += dpp_mov<0x141>(v);
+  return v + dpp_mov<0x140>(v);
+}
+
+__global__ __launch_bounds__(256, 2) void prefill_attention_kernel(const uint16_t *q, int64_t q_stride, const uint16_t *k_cache,
                                                                 const uint16_t *v_cache, int tokens, int group,
                                                                 int64_t max_ctx, float scale, uint16_t *out,
                                                                 int64_t out_stride) {
   __shared__ uint4 ks[kChunk * kKeyStrideU4];                // keys [key][128] bf16, padded rows
   __shared__ __align__(16) uint16_t vt[kHeadDim * kChunk];    // values [dim][key] bf16 (vt_index)
   __shared__ __align__(16) uint16_t ps[4][16][kPRow];         // per wave: probabilities [query][key] bf16
-  const int qb = blockIdx.x, head = blockIdx.y, kv = head / group;
+  const int qb = (int)gridDim.x - 1 - (int)blockIdx.x, head = blockIdx.y, kv = head / group;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int n = lane & 15, q4 = lane >> 4;
   const int q0 = qb * kPromptQueries + 16 * wave;  // this wave's first query
+  const float sl2 = scale * 1.44269504088896340736f;  // scores in log2 units
   // q as MFMA A operands: row n = query q0 + n (clamped into the prompt), dimensions 32 st + 8 q4 ..
   dwordx4 qa[4];
   {
@@ -575,18 +598,24 @@ __global__ __launch_bounds__(256) void prefill_attention_kernel(const uint16_t *
   // (32-bit byte offsets from the head's base: a head's cache is well under 4 GiB)
   const char *kg = reinterpret_cast<const char *>(k_cache + (size_t)kv * max_ctx * kHeadDim);
   const char *vg = reinterpret_cast<const char *>(v_cache + (size_t)kv * max_ctx * kHeadDim);
-  dwordx4 kr[4], vr[4];
-  auto load_block = [&](int kb) {
+  struct Block {
+    dwordx4 k[4];      // keys: 16-byte pieces idx = u * 256 + tid (key idx / 16, dimensions 8 (idx % 16) ..)
+    uint32_t v[16];    // values: dimensions 2 lane, 2 lane + 1 of keys 8 (2 wave + j / 8) + j % 8
+  };
+  auto load_block = [&](Block &b, int kb) {
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int idx = u * 256 + tid;
       const uint32_t row = (uint32_t)min((int64_t)(kb * kChunk + idx / kRowU4), max_ctx - 1);
-      const uint32_t off = (row * kRowU4 + idx % kRowU4) * 16u;
-      kr[u] = *reinterpret_cast<const dwordx4 *>(kg + off);
-      vr[u] = *reinterpret_cast<const dwordx4 *>(vg + off);
+      b.k[u] = *reinterpret_cast<const dwordx4 *>(kg + (row * kRowU4 + idx % kRowU4) * 16u);
+    }
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const uint32_t row = (uint32_t)min((int64_t)(kb * kChunk + 16 * wave + j), max_ctx - 1);
+      b.v[j] = *reinterpret_cast<const uint32_t *>(vg + (row * kHeadDim + 2 * lane) * 2u);
     }
   };
-  float m[4], l[4];  // running max and sum of the lane's rows, queries q0 + 4 q4 + r
+  float m[4], l[4];  // running max (log2 units) and sum of the lane's rows, queries q0 + 4 q4 + r
   f32x4_t o[8];      // o[dt][r] = O[query q0 + 4 q4 + r][dimension 16 dt + n]
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
@@ -595,20 +624,30 @@ __global__ __launch_bounds__(256) void prefill_attention_kernel(const uint16_t *
   }
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt) o[dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  load_block(0);
+  Block cur;
+  load_block(cur, 0);
   for (int kb = 0; kb <= qb; ++kb) {
     __syncthreads();  // the previous block's tiles are no longer read
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int idx = u * 256 + tid;
-      const int key = idx / kRowU4, c = idx % kRowU4;
-      reinterpret_cast<dwordx4 *>(ks)[key * kKeyStrideU4 + c] = kr[u];
-      const dwordx4 v = kb * kChunk + key < tokens ? vr[u] : dwordx4{0, 0, 0, 0};
+      reinterpret_cast<dwordx4 *>(ks)[(idx / kRowU4) * kKeyStrideU4 + idx % kRowU4] = cur.k[u];
+    }
 #pragma unroll
-      for (int e = 0; e < 8; ++e) vt[vt_index(8 * c + e, key)] = (uint16_t)(v[e / 2] >> (16 * (e & 1)));
+    for (int half = 0; half < 2; ++half) {
+      const int key0 = 16 * wave + 8 * half;  // eight keys of this thread's run
+      uint32_t w[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) w[j] = kb * kChunk + key0 + j < tokens ? cur.v[8 * half + j] : 0u;
+      const uint4 lo = make_uint4(__builtin_amdgcn_perm(w[1], w[0], 0x05040100u), __builtin_amdgcn_perm(w[3], w[2], 0x05040100u),
+                                  __builtin_amdgcn_perm(w[5], w[4], 0x05040100u), __builtin_amdgcn_perm(w[7], w[6], 0x05040100u));
+      const uint4 hi = make_uint4(__builtin_amdgcn_perm(w[1], w[0], 0x07060302u), __builtin_amdgcn_perm(w[3], w[2], 0x07060302u),
+                                  __builtin_amdgcn_perm(w[5], w[4], 0x07060302u), __builtin_amdgcn_perm(w[7], w[6], 0x07060302u));
+      *reinterpret_cast<uint4 *>(&vt[vt_index(2 * lane, key0)]) = lo;
+      *reinterpret_cast<uint4 *>(&vt[vt_index(2 * lane + 1, key0)]) = hi;
     }
     __syncthreads();
-    if (kb < qb) load_block(kb + 1);  // in flight while this block is multiplied
+    if (kb < qb) load_block(cur, kb + 1);  // in flight while this block is multiplied
     // scores of sub-tile s (keys 16 s .. 16 s + 15 of the block): sc[s][r] = S[query q0+4q4+r][key 16s+n]
     f32x4_t sc[4];
 #pragma unroll
@@ -623,38 +662,30 @@ __global__ __launch_bounds__(256) void prefill_attention_kernel(const uint16_t *
       sc[s4] = acc;
     }
     const bool diagonal = kb == qb;
-    float mx[4];
+    float alpha[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      mx[r] = -INFINITY;
+      float mx = -INFINITY;
 #pragma unroll
       for (int s4 = 0; s4 < 4; ++s4) {
         const int key = kb * kChunk + 16 * s4 + n, query = q0 + 4 * q4 + r;
-        float v = sc[s4][r] * scale;
+        float v = sc[s4][r] * sl2;
         if (diagonal && (key > query || key >= tokens)) v = -INFINITY;
         sc[s4][r] = v;
-        mx[r] = fmaxf(mx[r], v);
+        mx = fmaxf(mx, v);
       }
-#pragma unroll
-      for (int off = 1; off < 16; off <<= 1) mx[r] = fmaxf(mx[r], __shfl_xor(mx[r], off));
-    }
-    // Every row has an unmasked key in block 0 (key 0), so the running max is finite from there on.
-    float alpha[4], rs[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float mnew = fmaxf(m[r], mx[r]);
-      alpha[r] = expf(m[r] - mnew);
+      // Every row has an unmasked key in block 0 (key 0), so the running max is finite from there on.
+      const float mnew = fmaxf(m[r], row16_max(mx));
+      alpha[r] = __builtin_amdgcn_exp2f(m[r] - mnew);
       m[r] = mnew;
-      rs[r] = 0.f;
+      float rs = 0.f;
 #pragma unroll
       for (int s4 = 0; s4 < 4; ++s4) {
-        const uint16_t pb = to_bf(expf(sc[s4][r] - mnew));
+        const uint16_t pb = to_bf(__builtin_amdgcn_exp2f(sc[s4][r] - mnew));
         ps[wave][4 * q4 + r][16 * s4 + n] = pb;
-        rs[r] += bf(pb);
+        rs += bf(pb);
       }
-#pragma unroll
-      for (int off = 1; off < 16; off <<= 1) rs[r] += __shfl_xor(rs[r], off);
-      l[r] = l[r] * alpha[r] + rs[r];
+      l[r] = l[r] * alpha[r] + row16_sum(rs);
     }
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt)
