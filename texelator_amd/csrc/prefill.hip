@@ -1005,9 +1005,59 @@ __global__ __launch_bounds__(kWideThreads) void prefill_wide_kernel(PrefillParam
 
   // acc[tb][rb][r] = D[row 8(r/4) + 4h + r%4 of row block RW*rg + rb][token 128*tg + 32*tb + r32].
   const uint16_t *bias = static_cast<const uint16_t *>(p.bias);
+  // 16-bit outputs leave through LDS where whole 16-byte chunks can be stored: each lane holds four
+  // consecutive rows of one token, so direct stores would be 2-byte writes to a different token row
+  // per lane. Staged, a token's outputs are contiguous and every store covers 8 columns.
+  const bool staged = p.ks == 1 && ((SWIGLU ? p.M / 2 : p.M) & 7) == 0 && (reinterpret_cast<uintptr_t>(p.y) & 15) == 0;
+  if (staged) __syncthreads();  // every operand read of the K loop is done: the activation tiles are free
   if constexpr (SWIGLU) {
     // Row blocks RW*rg + 2i (gate) and + 1 (up) cover gate-space rows 32*(RW/2*rg + i) of the 64.
     const int inter = p.M / 2;
+    if (staged) {
+      // Tile [512 tokens][64 columns] in xs0: token row of 128 bytes, chunk c (8 columns) at c ^ (token % 8).
+#pragma unroll
+      for (int tb = 0; tb < TW; ++tb) {
+        const int tl = 128 * tg + 32 * tb + r32;
+#pragma unroll
+        for (int i = 0; i < RW / 2; ++i) {
+          __builtin_amdgcn_sched_barrier(0);
+          const f32x16 &vg = acc[tb][2 * i], &vu = acc[tb][2 * i + 1];
+#pragma unroll
+          for (int rq = 0; rq < 4; ++rq) {
+            const int col = 32 * (RW / 2 * rg + i) + 8 * rq + 4 * h;  // column within the 64
+            uint32_t packed[2];
+#pragma unroll
+            for (int r = 0; r < 4; r += 2) {
+              uint16_t pair[2];
+#pragma unroll
+              for (int e = 0; e < 2; ++e) {
+                const int n = min(w.n0 + col + r + e, inter - 1);
+                float gv = round_out<false>(vg[4 * rq + r + e]), uv = round_out<false>(vu[4 * rq + r + e]);
+                if (bias) {
+                  gv = round_out<false>(gv + bf(bias[n]));
+                  uv = round_out<false>(uv + bf(bias[inter + n]));
+                }
+                pair[e] = to_bf(swiglu_value(gv, uv));
+              }
+              packed[r / 2] = (uint32_t)pair[0] | ((uint32_t)pair[1] << 16);
+            }
+            *reinterpret_cast<uint2 *>(xs0 + tl * 64 + 8 * ((col >> 3) ^ (tl & 7)) + (col & 7)) =
+                make_uint2(packed[0], packed[1]);
+          }
+        }
+      }
+      __syncthreads();
+#pragma unroll
+      for (int it = 0; it < BT * 8 / kWideThreads; ++it) {
+        const int id = it * kWideThreads + (int)threadIdx.x;
+        const int tl = id >> 3, c = id & 7;
+        const int t = w.t0 + tl, n = w.n0 + 8 * c;
+        if (t < p.tokens && n < inter)
+          *reinterpret_cast<uint4 *>(static_cast<uint16_t *>(p.y) + (size_t)t * inter + n) =
+              *reinterpret_cast<const uint4 *>(xs0 + tl * 64 + 8 * (c ^ (tl & 7)));
+      }
+      return;
+    }
 #pragma unroll
     for (int tb = 0; tb < TW; ++tb) {
       const int t = w.t0 + 128 * tg + tb * 32 + r32;
@@ -1032,6 +1082,49 @@ __global__ __launch_bounds__(kWideThreads) void prefill_wide_kernel(PrefillParam
           }
         }
       }
+    }
+    return;
+  }
+  if (staged) {
+    // Tile [512 tokens][128 rows]: tokens 0-255 in xs0, 256-511 in xs1 (which one is uniform per
+    // wave); a token row of 256 bytes, chunk c (rows 8c..8c+7) at c ^ (token % 16).
+    uint16_t *half_tile = tg < 2 ? xs0 : xs1;
+#pragma unroll
+    for (int tb = 0; tb < TW; ++tb) {
+      const int tl = (128 * tg + 32 * tb + r32) & 255;
+#pragma unroll
+      for (int rb = 0; rb < RW; ++rb) {
+        __builtin_amdgcn_sched_barrier(0);
+        const f32x16 &v = acc[tb][rb];
+#pragma unroll
+        for (int rq = 0; rq < 4; ++rq) {
+          const int row = 32 * (RW * rg + rb) + 8 * rq + 4 * h;  // row within the 128
+          uint32_t packed[2];
+#pragma unroll
+          for (int r = 0; r < 4; r += 2) {
+            uint16_t pair[2];
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+              float out = round_out<F16>(v[4 * rq + r + e]);
+              if (bias) out += half_bits_to_float<F16>(bias[min(w.n0 + row + r + e, p.M - 1)]);
+              pair[e] = F16 ? __builtin_bit_cast(uint16_t, (_Float16)out) : to_bf(out);
+            }
+            packed[r / 2] = (uint32_t)pair[0] | ((uint32_t)pair[1] << 16);
+          }
+          *reinterpret_cast<uint2 *>(half_tile + tl * 128 + 8 * ((row >> 3) ^ (tl & 15)) + (row & 7)) =
+              make_uint2(packed[0], packed[1]);
+        }
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int it = 0; it < BT * 16 / kWideThreads; ++it) {
+      const int id = it * kWideThreads + (int)threadIdx.x;
+      const int tl = id >> 4, c = id & 15;
+      const int t = w.t0 + tl, n = w.n0 + 8 * c;
+      if (t < p.tokens && n < p.M)
+        *reinterpret_cast<uint4 *>(static_cast<uint16_t *>(p.y) + (size_t)t * p.M + n) =
+            *reinterpret_cast<const uint4 *>((tl < 256 ? xs0 : xs1) + (tl & 255) * 128 + 8 * (c ^ (tl & 15)));
     }
     return;
   }
