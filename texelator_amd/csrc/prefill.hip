@@ -115,6 +115,46 @@ __device__ __forceinline__ bool work_item(const PrefillParams &p, int BT, int BN
   return true;
 }
 
+// Output staging through LDS for tiles of 128 rows. In the accumulators each lane holds four
+// consecutive rows of one token, so direct stores are 2-byte (16-bit outputs) or 16-byte (fp32
+// partials) writes to a different token row per lane; staged, a token's outputs are contiguous and
+// every store writes a whole 16-byte chunk. A staged token row is 256 bytes (16 chunks), chunk c
+// stored at c ^ (token % 16): 16-bit outputs keep all 128 rows in one buffer (chunk = 8 rows);
+// fp32 partials keep rows 0-63 in one buffer and rows 64-127 in another (chunk = 4 rows).
+__device__ __forceinline__ void stage_out16(uint16_t *buf, int token, int row, uint32_t lo, uint32_t hi) {
+  *reinterpret_cast<uint2 *>(buf + token * 128 + 8 * ((row >> 3) ^ (token & 15)) + (row & 7)) = make_uint2(lo, hi);
+}
+__device__ __forceinline__ void stage_out32(uint16_t *buf, int token, int row, float4 v) {
+  *reinterpret_cast<float4 *>(buf + token * 128 + 8 * (((row & 63) >> 2) ^ (token & 15))) = v;
+}
+// 16-bit value of an output (the plain epilogue's rounding, bias with a second rounding).
+template <bool F16>
+__device__ __forceinline__ uint16_t out_bits(float acc, const uint16_t *bias, int n) {
+  float out = round_out<F16>(acc);
+  if (bias) out += half_bits_to_float<F16>(bias[n]);
+  return F16 ? __builtin_bit_cast(uint16_t, (_Float16)out) : __builtin_bit_cast(uint16_t, (__bf16)out);
+}
+// Copy a staged tile of `bt` tokens out with `threads` threads (after a barrier): 16-bit outputs
+// to y [tokens][M] (M % 8 == 0, y 16-byte aligned), or fp32 partials to the split's [tokens][Mp].
+template <bool F32>
+__device__ __forceinline__ void store_staged(const PrefillParams &p, const WorkItem &w, const uint16_t *buf0,
+                                             const uint16_t *buf1, int bt, int threads) {
+  const int chunks = bt * (F32 ? 32 : 16);
+  for (int id = (int)threadIdx.x; id < chunks; id += threads) {
+    const int c = id & 15, t = (id >> 4) % bt, half = F32 ? (id >> 4) / bt : 0;
+    const uint4 v = *reinterpret_cast<const uint4 *>((half ? buf1 : buf0) + t * 128 + 8 * (c ^ (t & 15)));
+    const int token = w.t0 + t;
+    if (token >= p.tokens) continue;
+    if constexpr (F32) {
+      const int row = w.n0 + 64 * half + 4 * c;
+      if (row < p.Mp) *reinterpret_cast<uint4 *>(p.partials + ((size_t)w.split * p.tokens + token) * p.Mp + row) = v;
+    } else {
+      const int n = w.n0 + 8 * c;
+      if (n < p.M) *reinterpret_cast<uint4 *>(static_cast<uint16_t *>(p.y) + (size_t)token * p.M + n) = v;
+    }
+  }
+}
+
 // F16: fp16 activations, bias and output, weights rounded to fp16 (the reference's FP16 prefill
 // decodes __float2half(P*scale) into its scratch matrix, texelator_cuda.cu:604-628, and adds
 // the bias with a second fp16 rounding, :630-635).
@@ -470,6 +510,34 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillParams p) {
     }
     return;
   }
+  if constexpr (RB == 1) {
+    const bool f32 = p.ks > 1;
+    if (f32 || ((p.M & 7) == 0 && (reinterpret_cast<uintptr_t>(p.y) & 15) == 0)) {
+      __syncthreads();  // the activation tiles are free
+      uint16_t *buf = f32 && wave >= 2 ? xs1 : xs0;
+#pragma unroll
+      for (int tb = 0; tb < TB; ++tb) {
+        const int tl = tb * 32 + r32;
+        const f32x16 &v = acc[tb][0];
+#pragma unroll
+        for (int rq = 0; rq < 4; ++rq) {
+          const int row = wave * 32 + 8 * rq + 4 * h;
+          if (f32) {
+            stage_out32(buf, tl, row, make_float4(v[4 * rq], v[4 * rq + 1], v[4 * rq + 2], v[4 * rq + 3]));
+          } else {
+            const int n = min(w.n0 + row, p.M - 4);
+            stage_out16(buf, tl, row,
+                        (uint32_t)out_bits<F16>(v[4 * rq], bias, n) | ((uint32_t)out_bits<F16>(v[4 * rq + 1], bias, n + 1) << 16),
+                        (uint32_t)out_bits<F16>(v[4 * rq + 2], bias, n + 2) | ((uint32_t)out_bits<F16>(v[4 * rq + 3], bias, n + 3) << 16));
+          }
+        }
+      }
+      __syncthreads();
+      if (f32) store_staged<true>(p, w, xs0, xs1, BT, kThreads);
+      else store_staged<false>(p, w, xs0, xs1, BT, kThreads);
+      return;
+    }
+  }
 #pragma unroll
   for (int tb = 0; tb < TB; ++tb) {
     const int t = w.t0 + tb * 32 + r32;
@@ -689,6 +757,32 @@ __global__ __launch_bounds__(kPairThreads) void prefill_pair_kernel(PrefillParam
 
     // acc[tb][r] = D[row 8(r/4) + 4h + r%4 of row block rb][token 128*HALF + 32*tb + r32].
     const uint16_t *bias = static_cast<const uint16_t *>(p.bias);
+    const bool f32 = p.ks > 1;
+    if (f32 || ((p.M & 7) == 0 && (reinterpret_cast<uintptr_t>(p.y) & 15) == 0)) {
+      __syncthreads();  // the activation tiles are free
+      uint16_t *buf = f32 && rb >= 2 ? xs1 : xs0;
+#pragma unroll
+      for (int tb = 0; tb < TBH; ++tb) {
+        const int tl = 128 * HALF + 32 * tb + r32;
+        const f32x16 &v = acc[tb];
+#pragma unroll
+        for (int rq = 0; rq < 4; ++rq) {
+          const int row = rb * 32 + 8 * rq + 4 * h;
+          if (f32) {
+            stage_out32(buf, tl, row, make_float4(v[4 * rq], v[4 * rq + 1], v[4 * rq + 2], v[4 * rq + 3]));
+          } else {
+            const int n = min(w.n0 + row, p.M - 4);
+            stage_out16(buf, tl, row,
+                        (uint32_t)out_bits<F16>(v[4 * rq], bias, n) | ((uint32_t)out_bits<F16>(v[4 * rq + 1], bias, n + 1) << 16),
+                        (uint32_t)out_bits<F16>(v[4 * rq + 2], bias, n + 2) | ((uint32_t)out_bits<F16>(v[4 * rq + 3], bias, n + 3) << 16));
+          }
+        }
+      }
+      __syncthreads();
+      if (f32) store_staged<true>(p, w, xs0, xs1, BT, kPairThreads);
+      else store_staged<false>(p, w, xs0, xs1, BT, kPairThreads);
+      return;
+    }
 #pragma unroll
     for (int tb = 0; tb < TBH; ++tb) {
       const int t = w.t0 + 128 * HALF + tb * 32 + r32;
