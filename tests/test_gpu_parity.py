@@ -256,6 +256,49 @@ def test_prefill_candidates_bitwise_equal_and_within_rrms(ext, oracle_threads, t
     assert bc4.relative_rms(ref, got) <= PREFILL_RRMS_TOL
 
 
+@pytest.mark.parametrize("mode", ["bf16", "f16_bias", "lut"])
+@pytest.mark.parametrize("tokens", [2, 17, 32])
+def test_prefill_split_group_tile_matches_other_tiles(ext, mode, tokens):
+    """Up to 32 tokens with exactly four K splits, candidate 9 runs the split-group tile (the four
+    splits of a 32-row block in one workgroup, summed there in split order): bitwise equal to the
+    tiles that write split partials for the reduce kernel, and within the prefill tolerance of the
+    float64 product on sampled rows. 26624 rows make 208 workgroups of 128 rows: four splits on a
+    256-CU MI355X."""
+    m, k = 26624, 4096
+    blocks = random_blocks(m, k, 611)
+    scales = lognormal_scales(m, 612)
+    f16 = mode == "f16_bias"
+    x = f16_vector((tokens, k), 613, scale=0.125) if f16 else (bf16_vector((tokens, k), 613).float() * 0.125).to(torch.bfloat16)
+    bias = f16_vector((m,), 614, scale=0.1).cuda() if f16 else None
+    handle = _pack(ext, blocks, scales, bias)
+    lut = None
+    if mode == "lut":
+        rng = np.random.default_rng(615)
+        base = bc4.palette()
+        lut = (base * (1 + 0.01 * rng.standard_normal(base.shape))).astype(np.float32)
+        ext.set_palette_table(handle, torch.from_numpy(lut).cuda())
+    try:
+        mp = (m + 15) // 16 * 16
+        if ext.workspace_bytes(handle, tokens) != 4 * tokens * mp * 4:
+            pytest.skip("this GPU splits the shape other than four ways")
+        outputs = {c: ext.prefill(handle, c, x.cuda()) for c in (9, 8, 6)}
+        torch.cuda.synchronize()
+    finally:
+        ext.free(handle)
+    for c in (8, 6):
+        assert torch.equal(outputs[9], outputs[c]), f"candidate 9 differs from candidate {c}"
+    rows = np.random.default_rng(616).choice(m, 512, replace=False)
+    if f16:
+        w = bc4.decode_f16_bits(blocks[rows], scales[rows]).view(np.float16).astype(np.float64)
+        ref = x.double().numpy() @ w.T + bias.double().cpu().numpy()[rows][None, :]
+        got = outputs[9].double().cpu().numpy()[:, rows]
+    else:
+        w = clib.decode_bf16_bits(blocks[rows], scales[rows], lut)
+        ref = clib.gemm_f64(bf16_bits(x), w)
+        got = outputs[9].float().cpu().numpy()[:, rows]
+    assert bc4.relative_rms(ref, got) <= PREFILL_RRMS_TOL
+
+
 @pytest.mark.parametrize("m,k,tokens", [(96, 4096, 20), (300, 27648, 32), (1024, 5120, 130)])
 def test_prefill_split_k_matches_oracle(ext, oracle_threads, m, k, tokens):
     """Shapes whose prefill is split along K (partials in the workspace, ordered reduction):

@@ -567,6 +567,171 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillParams p) {
   }
 }
 
+// Split-group tile (candidate 9 with exactly four K splits, up to 32 tokens, K a multiple of
+// 128): a workgroup holds the four splits of one (32-token tile, 32-row block), one per wave, and
+// each wave runs its split on its own -- weights decoded in registers as in prefill_kernel,
+// activations staged by the wave itself into its own LDS buffers (direct global-to-LDS loads, 1 KiB
+// contiguous per load) half a step at a time -- so the K loop has no workgroup barrier. At the end
+// the four splits are summed in split order through LDS, as prefill_reduce_kernel sums them: no
+// partials leave the workgroup and no reduce kernel runs. Same lane layouts, K sets and order as
+// prefill_kernel, hence the same bits.
+#ifndef TX_SMALL_WAVE
+#define TX_SMALL_WAVE 1
+#endif
+
+template <bool F16, bool LUT>
+__global__ __launch_bounds__(kThreads) void prefill_wave_kernel(PrefillParams p) {
+  // Per wave, K columns 0-63 (xlo) and 64-127 (xhi) of a step for its 32 tokens: token row r takes
+  // 128 bytes, its 16-byte slot q holds columns 8*(q ^ (r % 8)).. +7 of the half. The two halves
+  // are separate LDS objects, so the compiler can tell reads of one from loads into the other.
+  __shared__ __attribute__((aligned(16))) uint16_t xlo[4][32 * 64];
+  __shared__ __attribute__((aligned(16))) uint16_t xhi[4][32 * 64];
+  __shared__ __attribute__((aligned(16))) PaletteTableStorage tables;
+
+  const int lane = threadIdx.x & 63;
+  const int split = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // = wave
+  const int r32 = lane & 31;
+  const int h = lane >> 5;
+  const int row_blocks = (p.M + 31) / 32;
+  const int wgs = row_blocks * ((p.tokens + 31) / 32);
+  const int per_xcd = (wgs + kXcds - 1) / kXcds;
+  const int q = (int)(blockIdx.x % kXcds) * per_xcd + (int)(blockIdx.x / kXcds);
+  if (q >= wgs) return;
+  if constexpr (!LUT) copy_seed_tables(tables, split, lane, kThreads / 64);
+  const int rb = q % row_blocks;
+  const int t0 = (q / row_blocks) * 32;
+  const int c_begin = (int)((uint32_t)split * (uint32_t)p.CG / 4u);
+  const int nc = (int)((uint32_t)(split + 1) * (uint32_t)p.CG / 4u) - c_begin;
+  const int n0 = rb * 32;
+
+  // A operands: lane slot (row & 15) + 16h of tile group 2rb + (r32 >> 4) (clamped into the matrix;
+  // rows past M are computed, never stored), as in prefill_kernel.
+  const int g = min(2 * rb + (r32 >> 4), p.RG - 1);
+  const uint4 *gtile = p.tiles + ((size_t)g * p.CG + c_begin) * 64 + (lane & 15) + 16 * h;
+  const float scale = p.scales[g * kTileRows + (lane & 15)];
+  const uint32_t pm = pm_scale_pair<F16>(scale);
+  auto load_tiles = [&](uint4 (&slot)[2], int j) {
+    const size_t off = (size_t)j * 64;
+    slot[0] = load_stream(gtile + off);
+    slot[1] = load_stream(gtile + off + 32);
+  };
+
+  // Staging of half `hf` of step j (K is a multiple of 128 here): load v brings token rows
+  // 8v .. 8v + 7, lane l landing in slot l % 8 of row 8v + l / 8. Rows past the tokens repeat the
+  // last token (never stored).
+  const uint16_t *x = static_cast<const uint16_t *>(p.x);
+  const int srow = lane >> 3;                // row within the load's eight, = row % 8
+  const int scol = ((lane & 7) ^ srow) * 8;  // column of the half this lane stages
+  uint32_t row_off[4];                       // element offsets of this lane's four token rows
+#pragma unroll
+  for (int v = 0; v < 4; ++v) row_off[v] = (uint32_t)min(t0 + 8 * v + srow, p.tokens - 1) * (uint32_t)p.K;
+  const uint16_t *xsplit = x + (size_t)c_begin * kTileK + scol;
+  auto stage = [&](uint16_t *buf, int j, int hf) {
+    const uint16_t *src = xsplit + (size_t)j * kTileK + 64 * hf;
+#pragma unroll
+    for (int v = 0; v < 4; ++v)
+      __builtin_amdgcn_global_load_lds((const void *)(src + row_off[v]),
+                                       (__attribute__((address_space(3))) void *)(buf + 8 * v * 64), 16, 0, 0);
+  };
+  // B operand of MFMA 4*hf + s (s < 4): columns 32h + 16*(s>>1) + 8*(s&1) .. +7 of half hf.
+  auto read_b = [&](const uint16_t *buf, int s) {
+    return *reinterpret_cast<const u32x4 *>(buf + r32 * 64 + 8 * ((4 * h + s) ^ (r32 & 7)));
+  };
+
+  uint16_t *mylo = xlo[split];
+  uint16_t *myhi = xhi[split];
+  uint4 ta[2], tb[2];  // weight tiles of the even and the odd steps
+  stage(mylo, 0, 0);
+  load_tiles(ta, 0);
+  stage(myhi, 0, 1);
+  if constexpr (!LUT) {
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    __syncthreads();  // the seed tables
+  }
+
+  f32x16 acc;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+
+  // Block jj of weight tile `tile` into MFMAs 2jj, 2jj + 1.
+  auto block = [&](const uint4 (&tile)[2], int jj, const u32x4 &b0, const u32x4 &b1) {
+    const uint4 &piece = tile[jj >> 1];
+    const uint32_t wa = (jj & 1) ? piece.z : piece.x;
+    const uint32_t wb = (jj & 1) ? piece.w : piece.y;
+    uint32_t d[8];
+    if constexpr (LUT) {
+      const float4 *row = p.lut + 2 * (size_t)palette_row(wa, wb);
+      decode_from_palette<F16>(row[0], row[1], wa, wb, scale, d);
+    } else {
+      decode_block_lds<F16>(wa, wb, scale, pm, tables, d);
+    }
+    acc = mfma<F16>(u32x4{d[0], d[1], d[2], d[3]}, b0, acc);
+    acc = mfma<F16>(u32x4{d[4], d[5], d[6], d[7]}, b1, acc);
+  };
+  // Step j multiplies weight tile `cur` (loaded during step j - 1) and loads tile j + 1 into
+  // `next`. Each half buffer is read into registers, then refilled with the next step's half while
+  // this step's blocks are decoded and multiplied. Loads are issued low half, weights, high half:
+  // six later loads stay in flight at each half buffer's wait.
+  auto step = [&](int j, const uint4 (&cur)[2], uint4 (&next)[2]) {
+    const int jn = min(j + 1, nc - 1);
+    u32x4 b[4];
+    __builtin_amdgcn_s_waitcnt(0x0F76);  // vmcnt(6): the low half of step j has landed
+#pragma unroll
+    for (int s = 0; s < 4; ++s) b[s] = read_b(mylo, s);
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the reads are done before the refill
+    __builtin_amdgcn_sched_barrier(0);
+    stage(mylo, jn, 0);
+    load_tiles(next, jn);
+    __builtin_amdgcn_sched_barrier(0);
+    block(cur, 0, b[0], b[1]);
+    block(cur, 1, b[2], b[3]);
+    __builtin_amdgcn_s_waitcnt(0x0F76);  // vmcnt(6): the high half of step j has landed
+#pragma unroll
+    for (int s = 0; s < 4; ++s) b[s] = read_b(myhi, s);
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_sched_barrier(0);
+    stage(myhi, jn, 1);
+    __builtin_amdgcn_sched_barrier(0);
+    block(cur, 2, b[0], b[1]);
+    block(cur, 3, b[2], b[3]);
+  };
+  int j = 0;
+  for (; j + 2 <= nc; j += 2) {
+    step(j, ta, tb);
+    step(j + 1, tb, ta);
+  }
+  if (j < nc) step(j, ta, tb);
+
+  // acc[r] = D[row 8(r/4) + 4h + r%4 of the block][token t0 + r32]. The four splits are summed in
+  // split order from zero through each wave's low buffer (after its last refill has landed); wave
+  // w finishes rows 8w + 4h .. + 3.
+  const int t = t0 + r32;
+  const uint16_t *bias = static_cast<const uint16_t *>(p.bias);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  float *mine = reinterpret_cast<float *>(mylo);
+#pragma unroll
+  for (int r = 0; r < 16; ++r) mine[r * 64 + lane] = acc[r];
+  __syncthreads();
+  if (t >= p.tokens) return;
+  const int n = n0 + 8 * split + 4 * h;
+  uint32_t out[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    float total = 0.f;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) total += reinterpret_cast<const float *>(xlo[s])[(4 * split + r) * 64 + lane];
+    out[r] = n + r < p.M ? out_bits<F16>(total, bias, n + r) : 0u;
+  }
+  uint16_t *y = static_cast<uint16_t *>(p.y) + (size_t)t * p.M;
+  if (n + 3 < p.M && ((reinterpret_cast<uintptr_t>(y + n) & 7) == 0)) {
+    *reinterpret_cast<uint2 *>(y + n) = make_uint2(out[0] | (out[1] << 16), out[2] | (out[3] << 16));
+  } else {
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      if (n + r < p.M) y[n + r] = (uint16_t)out[r];
+  }
+}
+
 // Pair-shared tile: 8 waves, 256 tokens x 128 rows. Waves w and w + 4 own the same 32-row block
 // (rb = w % 4) for token halves 0 and 1. Per K step each of the two decodes only the blocks of
 // one 64-wide half of the step (h2 = its token half, MFMAs s = 4*h2 .. 4*h2 + 3) and hands the
@@ -1378,6 +1543,32 @@ hipError_t launch_tile(const PrefillParams &p, hipStream_t stream) {
   return launch_reduce(p, stream);
 }
 
+template <bool F16, bool LUT>
+void launch_wave_as(const PrefillParams &p, int grid, hipStream_t stream) {
+  hipLaunchKernelGGL((prefill_wave_kernel<F16, LUT>), dim3(grid), dim3(kThreads), 0, stream, p);
+}
+
+// Candidate 9: the split-group tile where a workgroup holds all four K splits of a 32-row block
+// (exactly four splits, up to 32 tokens, K a multiple of 128): no reduce launch, and measured
+// faster there (gate 5120 -> 27648: 35.1 vs 36.6 us at 32 tokens, 30.6 vs 34.3 us at 20). Elsewhere
+// the register-decoding 32-token tile, which was faster with split partials (down 27648 -> 5120 at
+// 32 tokens: 40.1 vs 42.0 us). Both give the same bits.
+hipError_t launch_small(const PrefillParams &p, hipStream_t stream) {
+  if (!TX_SMALL_WAVE || p.ks != 4 || p.tokens > 32 || p.K % kTileK != 0)
+    return launch_tile<1, 1, TX_PREFILL_LA_PLAIN, false>(p, stream);
+  const int wgs = ((p.M + 31) / 32) * ((p.tokens + 31) / 32);
+  const int grid = ((wgs + kXcds - 1) / kXcds) * kXcds;
+  if (p.lut) {
+    if (p.f16) launch_wave_as<true, true>(p, grid, stream);
+    else launch_wave_as<false, true>(p, grid, stream);
+  } else if (p.f16) {
+    launch_wave_as<true, false>(p, grid, stream);
+  } else {
+    launch_wave_as<false, false>(p, grid, stream);
+  }
+  return hipGetLastError();  // the four splits are summed in the tile
+}
+
 #define TX_CANDIDATE(NAME, TB, RB, LA, PIPE)                                                            \
   Candidate {                                                                                          \
     NAME, 32 * (TB), 128 * (RB), kTileK, reinterpret_cast<const void *>(&prefill_kernel<false, TB, RB, LA, PIPE, false>), \
@@ -1394,7 +1585,9 @@ const Candidate kCandidates[] = {
               reinterpret_cast<const void *>(&prefill_wide_kernel<false, false, true>),
               &launch_wide, 2 * (512 + 128) * kHalfK * 2, kWideThreads},
     TX_CANDIDATE("medium_64x128x128", 2, 1, TX_PREFILL_LA_PLAIN, false),
-    TX_CANDIDATE("small_32x128x128", 1, 1, TX_PREFILL_LA_PLAIN, false),
+    Candidate{"small_32x128x128", 32, 128, kTileK,
+              reinterpret_cast<const void *>(&prefill_kernel<false, 1, 1, TX_PREFILL_LA_PLAIN, false, false>),
+              &launch_small, 2 * 32 * kTileK * 2, kThreads},
 };
 
 const Candidate *find(int candidate) {
