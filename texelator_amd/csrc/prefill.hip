@@ -473,40 +473,72 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillParams p) {
   // acc[tb][b][r] = D[row 8(r/4) + 4h + r%4 of row block b][token tb*32 + r32].
   const uint16_t *bias = static_cast<const uint16_t *>(p.bias);
   if constexpr (SWIGLU) {
-    // Up waves (odd) hand their accumulators to their gate partners through the activation
-    // buffer, laid out [pair][tb][r][lane] (every LDS access of the K loop ended at its last
-    // barrier); gate waves then apply SwiGLU to matching elements.
+    // Each wave pair (gate wave 2q, up wave 2q + 1, the same rows and tokens) splits the SwiGLU
+    // work: the gate wave takes accumulator groups e = 4*tb + rq < 2*TB, the up wave the rest. Each
+    // hands the groups its partner takes through the first activation buffer ([wave][e'][r][lane],
+    // e' counting the handed groups; every LDS access of the K loop ended at its last barrier). The
+    // outputs are staged in the second buffer as [BT tokens][64 columns] (128-byte token rows, chunk
+    // c at c ^ (token % 8)) and leave in 16-byte chunks.
     float *xch = reinterpret_cast<float *>(xs0);
     const int pair = wave >> 1;
-    if (wave & 1) {
+    const bool up = wave & 1;
+    constexpr int G = 4 * TB;  // accumulator groups of four rows
 #pragma unroll
-      for (int tb = 0; tb < TB; ++tb)
+    for (int e = 0; e < G; ++e) {
+      const bool mine = up ? e >= G / 2 : e < G / 2;
+      if (!mine) {
+        const int slot = up ? e : e - G / 2;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) xch[((pair * TB + tb) * 16 + r) * 64 + lane] = acc[tb][0][r];
+        for (int r = 0; r < 4; ++r) xch[((wave * (G / 2) + slot) * 4 + r) * 64 + lane] = acc[e >> 2][0][4 * (e & 3) + r];
+      }
     }
     __syncthreads();
-    if (wave & 1) return;
     const int inter = p.M / 2;
+    const int partner = wave ^ 1;
+    const bool staged = (inter & 7) == 0 && (reinterpret_cast<uintptr_t>(p.y) & 15) == 0;
 #pragma unroll
-    for (int tb = 0; tb < TB; ++tb) {
-      const int t = w.t0 + tb * 32 + r32;
-      if (t >= p.tokens) continue;
+    for (int e = 0; e < G; ++e) {
+      const bool mine = up ? e >= G / 2 : e < G / 2;
+      if (!mine) continue;
+      const int tb = e >> 2, rq = e & 3;
+      const int slot = up ? e - G / 2 : e;  // where the partner put this group
+      const int tl = tb * 32 + r32;
+      const int col = 32 * pair + 8 * rq + 4 * h;  // column within the workgroup's 64
+      uint16_t outv[4];
 #pragma unroll
-      for (int rq = 0; rq < 4; ++rq) {
+      for (int r = 0; r < 4; ++r) {
+        const float other = xch[((partner * (G / 2) + slot) * 4 + r) * 64 + lane];
+        const float own = acc[tb][0][4 * rq + r];
+        const int n = min(w.n0 + col + r, inter - 1);
+        float gv = round_out<false>(up ? other : own), uv = round_out<false>(up ? own : other);
+        if (bias) {
+          gv = round_out<false>(gv + bf(bias[n]));
+          uv = round_out<false>(uv + bf(bias[inter + n]));
+        }
+        outv[r] = to_bf(swiglu_value(gv, uv));
+      }
+      if (staged) {
+        *reinterpret_cast<uint2 *>(xs1 + tl * 64 + 8 * ((col >> 3) ^ (tl & 7)) + (col & 7)) =
+            make_uint2((uint32_t)outv[0] | ((uint32_t)outv[1] << 16), (uint32_t)outv[2] | ((uint32_t)outv[3] << 16));
+      } else {
+        const int t = w.t0 + tl;
+        if (t < p.tokens) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int n = w.n0 + 32 * pair + 8 * rq + 4 * h + r;
-          if (n < inter) {
-            float gv = round_out<false>(acc[tb][0][4 * rq + r]);
-            float uv = round_out<false>(xch[((pair * TB + tb) * 16 + 4 * rq + r) * 64 + lane]);
-            if (bias) {
-              gv = round_out<false>(gv + bf(bias[n]));
-              uv = round_out<false>(uv + bf(bias[inter + n]));
-            }
-            static_cast<uint16_t *>(p.y)[(size_t)t * inter + n] = to_bf(swiglu_value(gv, uv));
-          }
+          for (int r = 0; r < 4; ++r)
+            if (w.n0 + col + r < inter) static_cast<uint16_t *>(p.y)[(size_t)t * inter + w.n0 + col + r] = outv[r];
         }
       }
+    }
+    if (!staged) return;
+    __syncthreads();
+#pragma unroll
+    for (int it = 0; it < BT * 8 / kThreads; ++it) {
+      const int id = it * kThreads + (int)threadIdx.x;
+      const int tl = id >> 3, c = id & 7;
+      const int t = w.t0 + tl, n = w.n0 + 8 * c;
+      if (t < p.tokens && n < inter)
+        *reinterpret_cast<uint4 *>(static_cast<uint16_t *>(p.y) + (size_t)t * inter + n) =
+            *reinterpret_cast<const uint4 *>(xs1 + tl * 64 + 8 * (c ^ (tl & 7)));
     }
     return;
   }
