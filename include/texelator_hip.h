@@ -278,6 +278,28 @@ int tx_rope_kv_cache_split(uint64_t qkv_handle, const int64_t *positions, const 
                            const float *sin_table, int heads, int kv_heads, int head_dim, void *q_out,
                            void *k_cache, void *v_cache, int64_t max_context, void *stream);
 
+/* The prefill GEMM of a call of `tokens` tokens (bf16 x [tokens][K], at or above the handle's
+ * prefill threshold) that leaves its fp32 K-split partials [ks][tokens][Mp] in `workspace` (at
+ * least tx_workspace_bytes for the call) instead of reducing them, for the two prefill split
+ * consumers below; *splits receives ks. TX_ERR_UNSUPPORTED when the call does not split K or runs
+ * the dense backend (use tx_linear). No counterpart in the reference (its prefill writes the
+ * linear output and Hugging Face's modules consume it); for callers that own the layer around the
+ * linears, as the decode split consumers do. */
+int tx_prefill_split(uint64_t handle, const void *x, int64_t tokens, void *workspace, int64_t workspace_bytes,
+                     int *splits, void *stream);
+
+/* tx_add_rmsnorm for `tokens` rows whose delta is tx_linear's output of delta_handle (M ==
+ * hidden), read from the partials tx_prefill_split left: summed in split order and rounded as the
+ * prefill reduce does (the bias added with a second rounding), bit for bit. */
+int tx_add_rmsnorm_prefill_split(float *residual, uint64_t delta_handle, const void *partials, int64_t tokens,
+                                 const void *weight, float eps, void *out, int64_t hidden, void *stream);
+
+/* tx_rope_kv_cache for `tokens` tokens whose [q | k | v] rows are tx_linear's output of
+ * qkv_handle, read from the partials tx_prefill_split left (same rounding as the prefill reduce). */
+int tx_rope_kv_cache_prefill_split(uint64_t qkv_handle, const void *partials, int64_t tokens, const int64_t *positions,
+                                   const float *cos_table, const float *sin_table, int heads, int kv_heads, int head_dim,
+                                   void *q_out, void *k_cache, void *v_cache, int64_t max_context, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

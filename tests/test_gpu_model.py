@@ -256,6 +256,99 @@ def test_rope_kv_cache_split_is_bit_identical(ext, heads, kv, k, bias):
         ext.free(handle)
 
 
+def _prefill_workspace(ext, handle, tokens):
+    return torch.empty(max(ext.workspace_bytes(handle, tokens), 16), dtype=torch.uint8, device="cuda")
+
+
+@pytest.mark.parametrize("m,k,tokens,bias", [(5120, 5120, 512, True), (2048, 11008, 512, False),
+                                             (5120, 27648, 300, True), (2048, 4096, 64, True), (5120, 5120, 20, False)])
+def test_add_rmsnorm_prefill_split_is_bit_identical(ext, m, k, tokens, bias):
+    """prefill_split + add_rmsnorm_prefill_split == linear + add_rmsnorm over several tokens, bit
+    for bit (the prefill reduce's rounding: the bias added after the sum's bf16 rounding), for split
+    counts that take the consumer's loop-free variants and its generic loop."""
+    handle = _random_handle(ext, m, k, seed=m + k + tokens, bias=bias)
+    try:
+        g = torch.Generator(device="cuda").manual_seed(tokens)
+        x = torch.randn(tokens, k, device="cuda", generator=g).to(torch.bfloat16)
+        w = (1 + 0.1 * torch.randn(m, device="cuda", generator=g)).to(torch.bfloat16)
+        h0 = torch.randn(tokens, m, device="cuda", generator=g)
+        h1, h2 = h0.clone(), h0.clone()
+        want = layers.add_rmsnorm(h1, ext.linear(handle, x), w, 1e-6)
+        ws = _prefill_workspace(ext, handle, tokens)
+        splits = layers.prefill_split(handle, x, ws)
+        assert splits > 1
+        got = layers.add_rmsnorm_prefill_split(h2, handle, ws, w, 1e-6, out=torch.empty_like(want))
+        assert torch.equal(h1, h2)
+        assert torch.equal(want, got)
+    finally:
+        ext.free(handle)
+
+
+@pytest.mark.parametrize("heads,kv,k,tokens", [(40, 8, 5120, 512), (16, 2, 2048, 300), (28, 4, 3584, 64)])
+def test_rope_kv_cache_prefill_split_is_bit_identical(ext, heads, kv, k, tokens):
+    """prefill_split + rope_kv_cache_prefill_split == linear + rope_kv_cache over a prompt, bit for
+    bit, with a nonzero q/k/v bias (added after the sum's bf16 rounding, as the prefill reduce does)."""
+    d, ctx = 128, 1024
+    handle = _random_handle(ext, (heads + 2 * kv) * d, k, seed=heads + tokens, bias=True)
+    try:
+        g = torch.Generator(device="cuda").manual_seed(17)
+        x = torch.randn(tokens, k, device="cuda", generator=g).to(torch.bfloat16)
+        angles = torch.rand(ctx, d, device="cuda", generator=g) * 6
+        cos, sin = angles.cos().contiguous(), angles.sin().contiguous()
+        pos = torch.arange(100, 100 + tokens, device="cuda")
+        caches = [torch.zeros(kv, ctx, d, device="cuda", dtype=torch.bfloat16) for _ in range(4)]
+        want = layers.rope_kv_cache(ext.linear(handle, x), pos, cos, sin, heads, kv, d, caches[0], caches[1])
+        ws = _prefill_workspace(ext, handle, tokens)
+        assert layers.prefill_split(handle, x, ws) > 1
+        got = layers.rope_kv_cache_prefill_split(handle, ws, pos, cos, sin, heads, kv, d, caches[2], caches[3])
+        assert torch.equal(want, got)
+        assert torch.equal(caches[0], caches[2]) and torch.equal(caches[1], caches[3])
+    finally:
+        ext.free(handle)
+
+
+def test_prefill_split_refusals(ext):
+    """prefill_split runs nothing where its call would not split K (a 512-token gate GEMM on the
+    wide tile), below the prefill threshold, or on the dense backend: UnsupportedError."""
+    handle = _random_handle(ext, 27648, 5120, seed=3)
+    try:
+        x = torch.zeros(512, 5120, device="cuda", dtype=torch.bfloat16)
+        ws = torch.empty(1 << 20, dtype=torch.uint8, device="cuda")
+        with pytest.raises(_lib.UnsupportedError):
+            layers.prefill_split(handle, x, ws)
+        ext.set_prefill(handle, 64, 1024)
+        with pytest.raises(_lib.UnsupportedError):
+            layers.prefill_split(handle, x[:32], ws)
+        ext.set_prefill(handle, 16, 1024)
+        ext.set_prefill_backend(handle, 1)
+        with pytest.raises(_lib.UnsupportedError):
+            layers.prefill_split(handle, x[:64], ws)
+    finally:
+        ext.free(handle)
+
+
+@pytest.mark.parametrize("config", ["class_27b", "qwen25_3b_style"])
+def test_decoder_prefill_with_split_consumers_is_bit_identical(ext, config):
+    """Two layers of the 27B- and 3B-class decoders: the 512-token prefill whose q|k|v, o and down
+    GEMMs leave their K-split partials to RoPE and add+RMSNorm gives the hidden states, keys and
+    values of the GEMM + reduce path, bit for bit."""
+    from dataclasses import replace
+
+    model = modeling.BC4Decoder(replace(getattr(modeling.DecoderConfig, config)(), layers=2), max_context=512, seed=7)
+    try:
+        ids = prefill.prompt_ids(model, 512)
+        positions = model.key_positions[:512]
+        with torch.inference_mode():
+            split = model.hidden_states(ids, positions, 512).clone()
+            kc, vc = model.k_cache.clone(), model.v_cache.clone()
+            model.split_prefill = False
+            plain = model.hidden_states(ids, positions, 512)
+        assert torch.equal(split, plain)
+        assert torch.equal(kc, model.k_cache) and torch.equal(vc, model.v_cache)
+    finally:
+        model.close()
+
+
 @pytest.mark.parametrize("heads,kv,k,bias,position,length,ks", [
     (40, 8, 5120, True, 517, 1024, 3), (40, 8, 5120, False, 0, 512, 3), (4, 2, 256, False, 63, 512, 1),
     (4, 2, 256, True, 64, 1024, 1), (48, 8, 1024, True, 300, 512, 2), (16, 4, 4096, False, 1000, 1024, 6),

@@ -65,6 +65,9 @@ SIGNATURES = {
     "tx_stream_read": (_I32, [_P, _I64, _P, _P]),
     "tx_add_rmsnorm_split": (_I32, [_P, _U64, _P, ctypes.c_float, _P, _I64, _P]),
     "tx_rope_kv_cache_split": (_I32, [_U64, _P, _P, _P, _I32, _I32, _I32, _P, _P, _P, _I64, _P]),
+    "tx_prefill_split": (_I32, [_U64, _P, _I64, _P, _I64, ctypes.POINTER(ctypes.c_int), _P]),
+    "tx_add_rmsnorm_prefill_split": (_I32, [_P, _U64, _P, _I64, _P, ctypes.c_float, _P, _I64, _P]),
+    "tx_rope_kv_cache_prefill_split": (_I32, [_U64, _P, _I64, _P, _P, _P, _I32, _I32, _I32, _P, _P, _P, _I64, _P]),
 }
 
 _LIB = None

@@ -741,6 +741,88 @@ int tx_linear_swiglu_prefill(uint64_t value, const void *x, int64_t tokens, void
   return TX_OK;
 }
 
+// The prefill-sized K-split partials of a handle for `tokens` tokens in a caller's buffer
+// (tx_prefill_split), as the prefill reduce sums and rounds them.
+tx::SplitSource prefill_split_source(const Handle *h, const void *partials, int64_t tokens) {
+  return tx::SplitSource{static_cast<const float *>(partials), static_cast<const uint16_t *>(h->bias),
+                         tx::prefill_splits(h->M, h->CG, tokens, h->cus), h->Mp, (int)tokens, 1};
+}
+
+int tx_prefill_split(uint64_t value, const void *x, int64_t tokens, void *workspace, int64_t workspace_bytes,
+                     int *splits_out, void *stream) {
+  g_last_error.clear();
+  Handle *h = as_handle(value);
+  if (!h) return fail(TX_ERR_INVALID, "null Texelator handle");
+  if (!x || !splits_out) return fail(TX_ERR_INVALID, "prefill_split: null input or splits pointer");
+  if (reinterpret_cast<uintptr_t>(x) % 16 != 0) return fail(TX_ERR_INVALID, "input must be 16-byte aligned");
+  if (h->bias && h->bias_dtype != TX_DTYPE_BF16) return fail(TX_ERR_INVALID, "prefill_split: the bias must be BF16");
+  if (tokens > (1 << 20)) return fail(TX_ERR_INVALID, "token count exceeds the prefill limit (1048576)");
+  if (tokens < 2 || tokens < h->prefill_threshold)
+    return fail(TX_ERR_UNSUPPORTED, "prefill_split: the call is below the prefill threshold (tx_linear runs the GEMV)");
+  const int candidate = prefill_choice(h, tokens);
+  if (candidate == kDenseBackend) return fail(TX_ERR_UNSUPPORTED, "prefill_split: the dense backend has no K splits");
+  const int ks = tx::prefill_splits(h->M, h->CG, tokens, h->cus);
+  if (ks == 1) return fail(TX_ERR_UNSUPPORTED, "prefill_split: this call does not split K (use tx_linear)");
+  if (!workspace || workspace_bytes < prefill_workspace_bytes(h, tokens) || reinterpret_cast<uintptr_t>(workspace) % 16 != 0)
+    return fail(TX_ERR_INVALID, "prefill_split: workspace missing or too small (see tx_workspace_bytes)");
+  DeviceGuard guard(h->device);
+  tx::PrefillParams p{};
+  p.lut = h->lut;
+  p.tiles = h->tiles;
+  p.scales = h->scales;
+  p.x = x;
+  p.bias = h->bias;
+  p.M = h->M;
+  p.K = h->K;
+  p.Mp = h->Mp;
+  p.RG = h->RG;
+  p.CG = h->CG;
+  p.tokens = (int)tokens;
+  p.ks = ks;
+  p.partials = static_cast<float *>(workspace);
+  p.no_reduce = 1;
+  TX_HIP(tx::launch_prefill(p, candidate, reinterpret_cast<hipStream_t>(stream)));
+  *splits_out = ks;
+  return TX_OK;
+}
+
+int tx_add_rmsnorm_prefill_split(float *residual, uint64_t delta_handle, const void *partials, int64_t tokens,
+                                 const void *weight, float eps, void *out, int64_t hidden, void *stream) {
+  g_last_error.clear();
+  Handle *h = as_handle(delta_handle);
+  if (!h) return fail(TX_ERR_INVALID, "null Texelator handle");
+  if (!residual || !partials || !weight || !out || hidden <= 0 || hidden > (1 << 24) || hidden % 4 || tokens < 2 ||
+      tokens > (1 << 20))
+    return fail(TX_ERR_INVALID, "add_rmsnorm_prefill_split: invalid arguments (hidden a positive multiple of 4, 2..1048576 tokens)");
+  if (h->M != hidden) return fail(TX_ERR_INVALID, "add_rmsnorm_prefill_split: the handle's output size must equal hidden");
+  if (h->bias && h->bias_dtype != TX_DTYPE_BF16) return fail(TX_ERR_INVALID, "add_rmsnorm_prefill_split: the bias must be BF16");
+  DeviceGuard guard(h->device);
+  TX_HIP(tx::launch_add_rmsnorm_split(residual, prefill_split_source(h, partials, tokens), static_cast<const uint16_t *>(weight),
+                                      eps, static_cast<uint16_t *>(out), tokens, (int)hidden,
+                                      reinterpret_cast<hipStream_t>(stream)));
+  return TX_OK;
+}
+
+int tx_rope_kv_cache_prefill_split(uint64_t qkv_handle, const void *partials, int64_t tokens, const int64_t *positions,
+                                   const float *cos_table, const float *sin_table, int heads, int kv_heads, int head_dim,
+                                   void *q_out, void *k_cache, void *v_cache, int64_t max_context, void *stream) {
+  g_last_error.clear();
+  Handle *h = as_handle(qkv_handle);
+  if (!h) return fail(TX_ERR_INVALID, "null Texelator handle");
+  if (!partials || !positions || !cos_table || !sin_table || !q_out || !k_cache || !v_cache)
+    return fail(TX_ERR_INVALID, "rope_kv_cache_prefill_split: null pointer");
+  if (heads <= 0 || kv_heads <= 0 || head_dim <= 0 || head_dim % 2 || head_dim > 1024 || max_context <= 0 || tokens < 2 ||
+      tokens > 65535 || (int64_t)h->M < (int64_t)(heads + 2 * kv_heads) * head_dim)
+    return fail(TX_ERR_INVALID, "rope_kv_cache_prefill_split: invalid shape");
+  if (h->bias && h->bias_dtype != TX_DTYPE_BF16) return fail(TX_ERR_INVALID, "rope_kv_cache_prefill_split: the bias must be BF16");
+  DeviceGuard guard(h->device);
+  TX_HIP(tx::launch_rope_cache_split(prefill_split_source(h, partials, tokens), tokens, positions, cos_table, sin_table,
+                                     heads, kv_heads, head_dim, static_cast<uint16_t *>(q_out),
+                                     static_cast<uint16_t *>(k_cache), static_cast<uint16_t *>(v_cache), max_context,
+                                     reinterpret_cast<hipStream_t>(stream)));
+  return TX_OK;
+}
+
 int tx_add_rmsnorm_split(float *residual, uint64_t delta_handle, const void *weight, float eps, void *out, int64_t hidden,
                          void *stream) {
   g_last_error.clear();

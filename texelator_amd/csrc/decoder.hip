@@ -121,6 +121,12 @@ __global__ __launch_bounds__(kNormThreads) void add_rmsnorm_kernel(float *h, con
       }
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) {
+        if (split.round_first && split.bias) {  // the prefill epilogue: the bias with a second rounding
+          acc[u].x = bf(to_bf(acc[u].x));
+          acc[u].y = bf(to_bf(acc[u].y));
+          acc[u].z = bf(to_bf(acc[u].z));
+          acc[u].w = bf(to_bf(acc[u].w));
+        }
         if (split.bias) {
           acc[u].x += bf((uint16_t)(b[u].x & 0xFFFFu));
           acc[u].y += bf((uint16_t)(b[u].x >> 16));

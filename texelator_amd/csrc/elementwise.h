@@ -41,10 +41,14 @@ __device__ __forceinline__ uint4 swiglu8(uint4 gv, uint4 uv) {
 // Output m of token t of a split-K GEMV: the fp32 partials [ks][tokens][Mp] summed in split
 // order starting from split 0, plus the bf16 bias, rounded to bf16 (returned widened to fp32).
 // The decode GEMV's own reduction uses this, so fused consumers reproduce its output bits.
+// round_first: the prefill GEMM's epilogue instead -- the sum rounded to bf16 first, the bias
+// added with a second rounding (prefill_reduce_kernel), so consumers of prefill partials
+// reproduce its output bits.
 struct SplitSource {
   const float *partials;
   const uint16_t *bias;  // [M] of the activation type (bf16, or fp16 with F16), or nullptr
   int ks, Mp, tokens;
+  int round_first;
 };
 
 // split_sum for N columns m[i] of one token at once. The loads go out four splits at a time for
@@ -99,7 +103,10 @@ __device__ __forceinline__ void split_sums(const SplitSource &s, int64_t token, 
     }
   }
 #pragma unroll
-  for (int i = 0; i < N; ++i) total[i] = s.bias ? total[i] + half_bits_to_float<F16>(b[i]) : total[i];
+  for (int i = 0; i < N; ++i) {
+    if (s.round_first) total[i] = F16 ? (float)(_Float16)total[i] : bf(to_bf(total[i]));
+    total[i] = s.bias ? total[i] + half_bits_to_float<F16>(b[i]) : total[i];
+  }
 }
 
 template <bool F16 = false>

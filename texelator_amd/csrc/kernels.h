@@ -44,6 +44,7 @@ struct PrefillParams {
   int M, K, Mp, RG, CG, tokens, ks;
   int f16;                 // x, bias and y are fp16 (weights rounded to fp16) instead of bf16
   const float4 *lut;       // LUT mode: 255 x 255 x 8 fp32 palette table, or nullptr (defined palette)
+  int no_reduce;           // with ks > 1: leave the partials for a consumer (no reduce kernel)
 };
 
 // GEMV variants selected by the lookahead knob (number of 1 KiB tiles in flight per wave).

@@ -1519,7 +1519,7 @@ hipError_t launch_pair(const PrefillParams &p, hipStream_t stream) {
     hipLaunchKernelGGL((prefill_pair_kernel<false, LA, false>), dim3(grid), dim3(kPairThreads), 0, stream, p);
   }
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess || p.ks == 1) return e;
+  if (e != hipSuccess || p.ks == 1 || p.no_reduce) return e;
   return launch_reduce(p, stream);
 }
 
@@ -1543,7 +1543,7 @@ hipError_t launch_wide(const PrefillParams &p, hipStream_t stream) {
     launch_wide_as<false, false>(p, grid, stream);
   }
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess || p.ks == 1) return e;
+  if (e != hipSuccess || p.ks == 1 || p.no_reduce) return e;
   return launch_reduce(p, stream);
 }
 
@@ -1571,7 +1571,7 @@ hipError_t launch_tile(const PrefillParams &p, hipStream_t stream) {
     hipLaunchKernelGGL((prefill_kernel<false, TB, RB, LA, PIPE, false>), dim3(grid), dim3(kThreads), 0, stream, p);
   }
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess || p.ks == 1) return e;
+  if (e != hipSuccess || p.ks == 1 || p.no_reduce) return e;
   return launch_reduce(p, stream);
 }
 
@@ -1581,12 +1581,13 @@ void launch_wave_as(const PrefillParams &p, int grid, hipStream_t stream) {
 }
 
 // Candidate 9: the split-group tile where a workgroup holds all four K splits of a 32-row block
-// (exactly four splits, up to 32 tokens, K a multiple of 128): no reduce launch, and measured
+// (exactly four splits, up to 32 tokens, K a multiple of 128, partials not wanted by the caller):
+// no reduce launch, and measured
 // faster there (gate 5120 -> 27648: 35.1 vs 36.6 us at 32 tokens, 30.6 vs 34.3 us at 20). Elsewhere
 // the register-decoding 32-token tile, which was faster with split partials (down 27648 -> 5120 at
 // 32 tokens: 40.1 vs 42.0 us). Both give the same bits.
 hipError_t launch_small(const PrefillParams &p, hipStream_t stream) {
-  if (!TX_SMALL_WAVE || p.ks != 4 || p.tokens > 32 || p.K % kTileK != 0)
+  if (!TX_SMALL_WAVE || p.ks != 4 || p.tokens > 32 || p.K % kTileK != 0 || p.no_reduce)
     return launch_tile<1, 1, TX_PREFILL_LA_PLAIN, false>(p, stream);
   const int wgs = ((p.M + 31) / 32) * ((p.tokens + 31) / 32);
   const int grid = ((wgs + kXcds - 1) / kXcds) * kXcds;

@@ -193,6 +193,66 @@ def linear_swiglu_prefill(handle: int, x: torch.Tensor, out: torch.Tensor | None
     return out
 
 
+def prefill_split(handle: int, x: torch.Tensor, workspace: torch.Tensor) -> int:
+    """The prefill GEMM of ``x`` [tokens, K] (bf16, at or above the handle's prefill threshold)
+    leaving its fp32 K-split partials in ``workspace`` (at least ``workspace_bytes(handle, tokens)``
+    bytes) for :func:`add_rmsnorm_prefill_split` or :func:`rope_kv_cache_prefill_split`; returns
+    the split count. Raises ``UnsupportedError`` when the call does not split K or runs the dense
+    backend (then :func:`linear` is the path)."""
+    _expect(x.is_cuda and x.dtype == torch.bfloat16 and x.is_contiguous() and x.dim() == 2 and x.data_ptr() % 16 == 0,
+            "x must be a contiguous, 16-byte aligned CUDA bf16 [tokens, K] tensor")
+    _expect(x.shape[1] == _hip_shape(handle)[1], "x has the wrong width for this handle")
+    _expect(workspace.is_cuda and workspace.is_contiguous() and workspace.data_ptr() % 16 == 0,
+            "workspace must be a contiguous, 16-byte aligned CUDA tensor")
+    splits = ctypes.c_int(0)
+    check(_lib.load().tx_prefill_split(handle, _ptr(x), x.shape[0], _ptr(workspace),
+                                       workspace.numel() * workspace.element_size(), ctypes.byref(splits), _stream(x)))
+    return splits.value
+
+
+def add_rmsnorm_prefill_split(residual: torch.Tensor, delta_handle: int, partials: torch.Tensor, weight: torch.Tensor,
+                              eps: float, out: torch.Tensor) -> torch.Tensor:
+    """:func:`add_rmsnorm` of ``tokens`` rows whose delta is ``linear(delta_handle, x)``, read from
+    the partials :func:`prefill_split` left (bit-identical)."""
+    _expect(residual.is_cuda and residual.dtype == torch.float32 and residual.is_contiguous() and residual.dim() == 2,
+            "residual must be a contiguous CUDA float32 [tokens, hidden]")
+    tokens, hidden = residual.shape
+    _expect(_hip_shape(delta_handle)[0] == hidden, "the delta handle's output size must equal hidden")
+    _expect(weight.dtype == torch.bfloat16 and weight.is_contiguous() and weight.numel() == hidden, "weight must be bf16 [hidden]")
+    _expect(out.dtype == torch.bfloat16 and out.is_contiguous() and out.shape == residual.shape, "bad output")
+    _expect(partials.is_cuda and partials.is_contiguous(), "partials must be the workspace prefill_split filled")
+    check(_lib.load().tx_add_rmsnorm_prefill_split(_ptr(residual), delta_handle, _ptr(partials), tokens, _ptr(weight),
+                                                   float(eps), _ptr(out), hidden, _stream(residual)))
+    return out
+
+
+def rope_kv_cache_prefill_split(qkv_handle: int, partials: torch.Tensor, positions: torch.Tensor, cos: torch.Tensor,
+                                sin: torch.Tensor, heads: int, kv_heads: int, head_dim: int, k_cache: torch.Tensor,
+                                v_cache: torch.Tensor, q_out: torch.Tensor | None = None) -> torch.Tensor:
+    """:func:`rope_kv_cache` of ``tokens`` tokens whose ``[q | k | v]`` rows are
+    ``linear(qkv_handle, x)``, read from the partials :func:`prefill_split` left (bit-identical);
+    returns the rotated q ``[tokens, heads * head_dim]``."""
+    _expect(_hip_shape(qkv_handle)[0] >= (heads + 2 * kv_heads) * head_dim, "qkv handle too narrow for the heads")
+    _expect(positions.dtype == torch.int64 and positions.is_contiguous() and positions.dim() == 1,
+            "positions must be int64 [tokens]")
+    tokens = positions.numel()
+    max_ctx = k_cache.shape[1]
+    for cache in (k_cache, v_cache):
+        _expect(cache.dtype == torch.bfloat16 and cache.is_contiguous() and tuple(cache.shape) == (kv_heads, max_ctx, head_dim),
+                "caches must be contiguous bf16 [kv_heads, max_context, head_dim]")
+    for table in (cos, sin):
+        _expect(table.dtype == torch.float32 and table.is_contiguous() and tuple(table.shape) == (max_ctx, head_dim),
+                "rope tables must be float32 [max_context, head_dim]")
+    _expect(partials.is_cuda and partials.is_contiguous(), "partials must be the workspace prefill_split filled")
+    if q_out is None:
+        q_out = torch.empty((tokens, heads * head_dim), dtype=torch.bfloat16, device=positions.device)
+    _expect(q_out.dtype == torch.bfloat16 and q_out.is_contiguous() and q_out.numel() == tokens * heads * head_dim, "bad q_out")
+    check(_lib.load().tx_rope_kv_cache_prefill_split(qkv_handle, _ptr(partials), tokens, _ptr(positions), _ptr(cos),
+                                                     _ptr(sin), heads, kv_heads, head_dim, _ptr(q_out), _ptr(k_cache),
+                                                     _ptr(v_cache), max_ctx, _stream(positions)))
+    return q_out
+
+
 def add_rmsnorm_split(residual: torch.Tensor, delta_handle: int, weight: torch.Tensor, eps: float,
                       out: torch.Tensor) -> torch.Tensor:
     """:func:`add_rmsnorm` of one row whose delta is the last :func:`linear_split` of ``delta_handle``."""

@@ -197,6 +197,8 @@ class BC4Decoder:
         self.flash_prompt_attention = fused
         # prefill of the merged gate|up handle with the SwiGLU epilogue where the call allows it
         self.gate_up_swiglu_prefill = fused
+        # prefill GEMMs that split K leave their partials to RoPE and add+RMSNorm (no reduce kernel)
+        self.split_prefill = fused
         # a prompt's causal attention with this library's kernel (else torch's flash attention)
         self.prompt_attention_kernel = fused and prompt_attention_supported(config)
         ext = extension()
@@ -398,10 +400,16 @@ class BC4Decoder:
         # a prompt at positions 0..T-1 attending to itself only: causal flash attention
         prompt = (tokens > 1 and length == tokens and positions.data_ptr() == self.key_positions.data_ptr()
                   and self.flash_prompt_attention)
+        workspace = self._split_workspace(tokens)
         for index, layer in enumerate(self.layers):
-            qkv = layer.linears["qkv"](x)
-            q = layers.rope_kv_cache(qkv, positions, self.rope_cos, self.rope_sin, c.heads, c.kv_heads, c.head_dim,
-                                     self.k_cache[index], self.v_cache[index])
+            if self._prefill_partials(layer.handles["qkv"], x, workspace):
+                q = layers.rope_kv_cache_prefill_split(layer.handles["qkv"], workspace, positions, self.rope_cos,
+                                                       self.rope_sin, c.heads, c.kv_heads, c.head_dim,
+                                                       self.k_cache[index], self.v_cache[index])
+            else:
+                qkv = layer.linears["qkv"](x)
+                q = layers.rope_kv_cache(qkv, positions, self.rope_cos, self.rope_sin, c.heads, c.kv_heads, c.head_dim,
+                                         self.k_cache[index], self.v_cache[index])
             if tokens == 1:
                 attn = layers.decode_attention(q, self.k_cache[index], self.v_cache[index], positions, length, c.heads,
                                                c.kv_heads, scale, self.attention_workspace)
@@ -409,11 +417,40 @@ class BC4Decoder:
                 attn = self._prompt_attention(index, q.view(tokens, c.heads, c.head_dim))
             else:
                 attn = self._cached_attention(index, q.view(tokens, c.heads, c.head_dim), positions, length)
-            layers.add_rmsnorm(h, layer.linears["o"](attn), layer.post_norm, c.rms_eps, out=x)
+            self._add_rmsnorm_tokens(h, layer.handles["o"], layer.linears["o"], attn, layer.post_norm, x, workspace)
             act = self._gate_up_swiglu_tokens(layer, x)
             following = self.layers[index + 1].input_norm if index + 1 < len(self.layers) else self.final_norm
-            layers.add_rmsnorm(h, layer.linears["down"](act), following, c.rms_eps, out=x)
+            self._add_rmsnorm_tokens(h, layer.handles["down"], layer.linears["down"], act, following, x, workspace)
         return x
+
+    def _split_workspace(self, tokens: int) -> torch.Tensor | None:
+        """Workspace for the partials of this call's K-split prefill GEMMs (None if none is used)."""
+        if not self.split_prefill or tokens < 2:
+            return None
+        ext = extension()
+        layer = self.layers[0]
+        need = max(ext.workspace_bytes(layer.handles[key], tokens) for key in ("qkv", "o", "down"))
+        return torch.empty(max(need, 16), dtype=torch.uint8, device=self.device) if need else None
+
+    def _prefill_partials(self, handle: int, x: torch.Tensor, workspace: torch.Tensor | None) -> bool:
+        """The prefill GEMM of ``x`` leaving its K-split partials in ``workspace``; False (nothing
+        run) where the call does not split K, so the caller runs the plain linear."""
+        if workspace is None or x.shape[0] < 2:
+            return False
+        try:
+            layers.prefill_split(handle, x, workspace)
+        except UnsupportedError:
+            return False
+        return True
+
+    def _add_rmsnorm_tokens(self, h: torch.Tensor, handle: int, linear: TexelatorLinear, x_in: torch.Tensor,
+                            weight: torch.Tensor, out: torch.Tensor, workspace: torch.Tensor | None) -> None:
+        """``h += linear(x_in)``, ``out = rmsnorm(h) * weight``: from the GEMM's K-split partials where
+        it splits (bit-identical, one reduce launch fewer), else through the linear's output."""
+        if self._prefill_partials(handle, x_in, workspace):
+            layers.add_rmsnorm_prefill_split(h, handle, workspace, weight, self.config.rms_eps, out=out)
+        else:
+            layers.add_rmsnorm(h, linear(x_in), weight, self.config.rms_eps, out=out)
 
     def _decode_split(self, h: torch.Tensor, x: torch.Tensor, positions: torch.Tensor, length: int,
                       scale: float) -> torch.Tensor:
