@@ -614,8 +614,10 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillParams p) {
 template <bool F16, bool LUT>
 __global__ __launch_bounds__(kThreads) void prefill_wave_kernel(PrefillParams p) {
   // Per wave, K columns 0-63 (xlo) and 64-127 (xhi) of a step for its 32 tokens: token row r takes
-  // 128 bytes, its 16-byte slot q holds columns 8*(q ^ (r % 8)).. +7 of the half. The two halves
-  // are separate LDS objects, so the compiler can tell reads of one from loads into the other.
+  // 128 bytes, its 16-byte slot q holds columns 8*(q ^ ((r >> 1) % 8)).. +7 of the half (the 16
+  // rows one operand read serves per LDS pass then fall on distinct banks: even and odd rows sit in
+  // opposite halves of the banks). The two halves are separate LDS objects, so the compiler can
+  // tell reads of one from loads into the other.
   __shared__ __attribute__((aligned(16))) uint16_t xlo[4][32 * 64];
   __shared__ __attribute__((aligned(16))) uint16_t xhi[4][32 * 64];
   __shared__ __attribute__((aligned(16))) PaletteTableStorage tables;
@@ -649,15 +651,15 @@ __global__ __launch_bounds__(kThreads) void prefill_wave_kernel(PrefillParams p)
   };
 
   // Staging of half `hf` of step j (K is a multiple of 128 here): load v brings token rows
-  // 8v .. 8v + 7, lane l landing in slot l % 8 of row 8v + l / 8. Rows past the tokens repeat the
-  // last token (never stored).
+  // 8v .. 8v + 7, lane l landing in slot l % 8 of row 8v + l / 8, so it fetches the half's chunk
+  // (l % 8) ^ (((8v + l / 8) >> 1) % 8). Rows past the tokens repeat the last token (never stored).
   const uint16_t *x = static_cast<const uint16_t *>(p.x);
-  const int srow = lane >> 3;                // row within the load's eight, = row % 8
-  const int scol = ((lane & 7) ^ srow) * 8;  // column of the half this lane stages
-  uint32_t row_off[4];                       // element offsets of this lane's four token rows
+  const int srow = lane >> 3;  // row within the load's eight
+  uint32_t row_off[4];         // element offsets of this lane's four token rows and chunks
 #pragma unroll
-  for (int v = 0; v < 4; ++v) row_off[v] = (uint32_t)min(t0 + 8 * v + srow, p.tokens - 1) * (uint32_t)p.K;
-  const uint16_t *xsplit = x + (size_t)c_begin * kTileK + scol;
+  for (int v = 0; v < 4; ++v)
+    row_off[v] = (uint32_t)min(t0 + 8 * v + srow, p.tokens - 1) * (uint32_t)p.K + 8u * (uint32_t)((lane & 7) ^ ((4 * v + (srow >> 1)) & 7));
+  const uint16_t *xsplit = x + (size_t)c_begin * kTileK;
   auto stage = [&](uint16_t *buf, int j, int hf) {
     const uint16_t *src = xsplit + (size_t)j * kTileK + 64 * hf;
 #pragma unroll
@@ -667,7 +669,7 @@ __global__ __launch_bounds__(kThreads) void prefill_wave_kernel(PrefillParams p)
   };
   // B operand of MFMA 4*hf + s (s < 4): columns 32h + 16*(s>>1) + 8*(s&1) .. +7 of half hf.
   auto read_b = [&](const uint16_t *buf, int s) {
-    return *reinterpret_cast<const u32x4 *>(buf + r32 * 64 + 8 * ((4 * h + s) ^ (r32 & 7)));
+    return *reinterpret_cast<const u32x4 *>(buf + r32 * 64 + 8 * ((4 * h + s) ^ ((r32 >> 1) & 7)));
   };
 
   uint16_t *mylo = xlo[split];
