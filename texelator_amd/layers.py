@@ -11,6 +11,7 @@ import ctypes
 import torch
 
 from . import _lib
+from ._hip import _stream as _device_stream
 from ._hip import shape as _hip_shape
 from ._lib import TexelatorError, check
 
@@ -20,7 +21,7 @@ def _ptr(t: torch.Tensor | None) -> ctypes.c_void_p:
 
 
 def _stream(t: torch.Tensor) -> ctypes.c_void_p:
-    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+    return _device_stream(t.device)
 
 
 def _expect(condition: bool, message: str) -> None:
