@@ -261,11 +261,14 @@ def _prefill_workspace(ext, handle, tokens):
 
 
 @pytest.mark.parametrize("m,k,tokens,bias", [(5120, 5120, 512, True), (2048, 11008, 512, False),
-                                             (5120, 27648, 300, True), (2048, 4096, 64, True), (5120, 5120, 20, False)])
+                                             (5120, 27648, 300, True), (2048, 4096, 64, True), (5120, 5120, 20, False),
+                                             (27648, 5120, 32, True)])
 def test_add_rmsnorm_prefill_split_is_bit_identical(ext, m, k, tokens, bias):
     """prefill_split + add_rmsnorm_prefill_split == linear + add_rmsnorm over several tokens, bit
     for bit (the prefill reduce's rounding: the bias added after the sum's bf16 rounding), for split
-    counts that take the consumer's loop-free variants and its generic loop."""
+    counts that take the consumer's loop-free variants and its generic loop. 27648 rows at 32
+    tokens split four ways, where linear runs the split-group tile (no partials) and prefill_split
+    the partial-writing 32-token tile."""
     handle = _random_handle(ext, m, k, seed=m + k + tokens, bias=bias)
     try:
         g = torch.Generator(device="cuda").manual_seed(tokens)
