@@ -245,6 +245,17 @@ int tx_decode_attention_split(uint64_t qkv_handle, const int64_t *position, cons
 /* out[r][c] = bf16(silu(g) * u) for gate_up rows [g (intermediate) | u (intermediate)], fp32 math. */
 int tx_swiglu(const void *gate_up, int64_t rows, int64_t intermediate, void *out, void *stream);
 
+/* Greedy next token of a dense bf16 lm_head (no reference counterpart: the reference leaves the
+ * head and the sampling to Hugging Face): *token (int64, device memory) = the first row v with the
+ * largest bf16(sum_k x[k] * weight[v][k]) (fp32 sums), i.e. argmax over the bf16 logits of the
+ * linear layer, in two kernel launches instead of a GEMM and an argmax. weight bf16 [vocab][hidden]
+ * row-major, x bf16 [hidden] (hidden a multiple of 128, at most 16384; both 16-byte aligned); logits
+ * (bf16 [vocab]) written too unless null. workspace: at least tx_lm_head_argmax_workspace bytes,
+ * 16-byte aligned. NaN logits are not ranked. */
+int tx_lm_head_argmax_workspace(int64_t *bytes);
+int tx_lm_head_argmax(const void *weight, int64_t vocab, int64_t hidden, const void *x, void *logits, void *workspace,
+                      int64_t workspace_bytes, int64_t *token, void *stream);
+
 /* ---- Fused single-token decode (no reference counterpart; same role as the helpers above) ----
  * tx_linear_split runs a handle's one-token decode GEMV (x bf16 [K]) but leaves its output as
  * the fp32 split-K partials in the handle's own buffer; the *_split consumers below read them,

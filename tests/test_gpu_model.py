@@ -256,6 +256,49 @@ def test_rope_kv_cache_split_is_bit_identical(ext, heads, kv, k, bias):
         ext.free(handle)
 
 
+@pytest.mark.parametrize("vocab,hidden", [(151936, 2048), (32003, 5120), (1000, 128), (17, 256)])
+def test_lm_head_argmax_matches_float64_logits(ext, vocab, hidden):
+    """The lm_head GEMV + argmax: its bf16 logits are the float64 products rounded once (to fp32
+    summation error), and the token is the first row among the largest of those logits, as
+    torch.argmax picks it."""
+    g = torch.Generator(device="cuda").manual_seed(vocab + hidden)
+    w = (torch.randn(vocab, hidden, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+    x = torch.randn(1, hidden, device="cuda", generator=g).to(torch.bfloat16)
+    ws = torch.empty(layers.lm_head_argmax_workspace_bytes(), dtype=torch.uint8, device="cuda")
+    logits = torch.empty(vocab, dtype=torch.bfloat16, device="cuda")
+    token = layers.lm_head_argmax(w, x, ws, logits=logits)
+    ref = (w.double() @ x.double().t()).view(-1)
+    err = (logits.double() - ref).abs()
+    assert bool((err <= ref.abs() * 2.0 ** -8 + 1e-4).all())
+    assert int(token) == int(torch.argmax(logits.float()))
+
+
+def test_lm_head_argmax_takes_the_first_of_equal_logits(ext):
+    """Rows that are copies of one another tie exactly; the first of them wins, across workgroups."""
+    vocab, hidden = 40000, 1024
+    g = torch.Generator(device="cuda").manual_seed(3)
+    w = (torch.randn(vocab, hidden, device="cuda", generator=g) * 0.01).to(torch.bfloat16)
+    x = torch.randn(1, hidden, device="cuda", generator=g).to(torch.bfloat16)
+    best = torch.randn(hidden, device="cuda", generator=g).sign().to(torch.bfloat16) * x.view(-1).sign()
+    for row in (39000, 777, 20001):  # the same winning row at three places, the smallest not first written
+        w[row] = best
+    ws = torch.empty(layers.lm_head_argmax_workspace_bytes(), dtype=torch.uint8, device="cuda")
+    assert int(layers.lm_head_argmax(w, x, ws)) == 777
+
+
+def test_decoder_greedy_token_agrees_with_torch_head(ext, tiny):
+    """The decoder's fused head picks torch's argmax token, or one whose logit is within rounding
+    of it (the two sum the dot products in different orders)."""
+    ids = prefill.prompt_ids(tiny, 40, seed=12)
+    with torch.inference_mode():
+        hidden = tiny.hidden_states(ids, tiny.key_positions[:40], 40)
+        for t in range(40):
+            h = hidden[t:t + 1].contiguous()
+            got = int(tiny.greedy_token(h))
+            logits = tiny.logits(h).float().view(-1)
+            assert logits[got] >= logits.max() - 2.0 ** -7 * logits.abs().max()
+
+
 def _prefill_workspace(ext, handle, tokens):
     return torch.empty(max(ext.workspace_bytes(handle, tokens), 16), dtype=torch.uint8, device="cuda")
 

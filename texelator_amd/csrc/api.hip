@@ -946,6 +946,28 @@ int tx_decode_attention_split(uint64_t qkv_handle, const int64_t *position, cons
   return TX_OK;
 }
 
+int tx_lm_head_argmax_workspace(int64_t *bytes) {
+  g_last_error.clear();
+  if (!bytes) return fail(TX_ERR_INVALID, "lm_head_argmax_workspace: null output");
+  *bytes = tx::lm_head_argmax_workspace();
+  return TX_OK;
+}
+
+int tx_lm_head_argmax(const void *weight, int64_t vocab, int64_t hidden, const void *x, void *logits, void *workspace,
+                      int64_t workspace_bytes, int64_t *token, void *stream) {
+  g_last_error.clear();
+  if (!weight || !x || !token || !workspace) return fail(TX_ERR_INVALID, "lm_head_argmax: null pointer");
+  if (vocab <= 0 || vocab > 0x7FFFFFFF || hidden <= 0 || hidden > 16384 || hidden % 128)
+    return fail(TX_ERR_INVALID, "lm_head_argmax: vocab must be 1..2^31-1 and hidden a multiple of 128 up to 16384");
+  if (workspace_bytes < tx::lm_head_argmax_workspace() || reinterpret_cast<uintptr_t>(workspace) % 16 != 0)
+    return fail(TX_ERR_INVALID, "lm_head_argmax: workspace missing or too small (see tx_lm_head_argmax_workspace)");
+  if (reinterpret_cast<uintptr_t>(weight) % 16 != 0 || reinterpret_cast<uintptr_t>(x) % 16 != 0)
+    return fail(TX_ERR_INVALID, "lm_head_argmax: weight and x must be 16-byte aligned");
+  TX_HIP(tx::launch_lm_head_argmax(static_cast<const uint16_t *>(weight), vocab, (int)hidden, static_cast<const uint16_t *>(x),
+                                   static_cast<uint16_t *>(logits), workspace, token, reinterpret_cast<hipStream_t>(stream)));
+  return TX_OK;
+}
+
 int tx_swiglu(const void *gate_up, int64_t rows, int64_t intermediate, void *out, void *stream) {
   g_last_error.clear();
   if (!gate_up || !out || rows < 0 || intermediate <= 0 || intermediate % 8)

@@ -779,6 +779,140 @@ __global__ __launch_bounds__(256 * HALVES, HALVES == 1 ? 2 : 1) void prefill_att
   }
 }
 
+// Greedy next token of a dense bf16 lm_head W [vocab][hidden] for one hidden state x [hidden]:
+// token = the first v with the largest bf16(sum_k x[k] W[v][k]) (fp32 sums), as argmax over the
+// bf16 logits of a linear layer picks it. First pass: workgroup b takes a contiguous range of
+// rows; its waves take four rows at a time, sixteen lanes per row streaming the row in 16-byte
+// chunks (chunk 16c + lane of the row; x as fp32 in LDS), four accumulators per lane summed in a
+// fixed order, then over the row's sixteen lanes by DPP. Each lane group keeps its best (value,
+// row); the workgroup's best goes to the partials. Second pass: one workgroup reduces those. The
+// order (larger value, then smaller row) is total, so the result does not depend on the
+// reduction order. NaN logits are not ranked. Optionally the bf16 logits are written too.
+constexpr int kHeadThreads = 256;
+constexpr int kHeadBlocks = 1024;  // first-pass workgroups: partials of kHeadBlocks (value, row)
+
+__device__ __forceinline__ bool head_better(float v, int i, float bv, int bi) { return v > bv || (v == bv && i < bi); }
+
+__global__ __launch_bounds__(kHeadThreads) void lm_head_argmax_kernel(const uint16_t *w, int64_t vocab, int hidden,
+                                                                      const uint16_t *x, uint16_t *logits,
+                                                                      float *part_val, int *part_idx) {
+  extern __shared__ float xs[];  // x as fp32 [hidden]
+  __shared__ float wave_val[kHeadThreads / 64];
+  __shared__ int wave_idx[kHeadThreads / 64];
+  for (int i = threadIdx.x; i < hidden / 8; i += kHeadThreads) {
+    const uint4 v = reinterpret_cast<const uint4 *>(x)[i];
+    reinterpret_cast<float4 *>(xs)[2 * i] = make_float4(__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xFFFF0000u),
+                                                        __uint_as_float(v.y << 16), __uint_as_float(v.y & 0xFFFF0000u));
+    reinterpret_cast<float4 *>(xs)[2 * i + 1] = make_float4(__uint_as_float(v.z << 16), __uint_as_float(v.z & 0xFFFF0000u),
+                                                            __uint_as_float(v.w << 16), __uint_as_float(v.w & 0xFFFF0000u));
+  }
+  __syncthreads();
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, grp = lane >> 4, l16 = lane & 15;
+  const int64_t per = (vocab + gridDim.x - 1) / gridDim.x;
+  const int64_t v0 = (int64_t)blockIdx.x * per, v1 = min(vocab, v0 + per);
+  const int chunks = hidden / 128;  // 16-byte chunks of a row per lane (hidden % 128 == 0)
+  float best = -INFINITY;
+  int best_row = 0x7FFFFFFF;
+  for (int64_t base = v0; base < v1; base += 16) {
+    const int64_t row = base + 4 * wave + grp;
+    const bool valid = row < v1;
+    const dwordx4 *wr = reinterpret_cast<const dwordx4 *>(w + (size_t)min(row, v1 - 1) * hidden) + l16;
+    const float4 *xr = reinterpret_cast<const float4 *>(xs) + 2 * l16;
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    auto madd = [&](const dwordx4 &q, int c) {
+      const float4 a = xr[32 * c], b = xr[32 * c + 1];
+      const uint32_t wq[4] = {q[0], q[1], q[2], q[3]};
+      const float xv[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        acc[e] = __builtin_fmaf(__uint_as_float(wq[e] << 16), xv[2 * e], acc[e]);
+        acc[e] = __builtin_fmaf(__uint_as_float(wq[e] & 0xFFFF0000u), xv[2 * e + 1], acc[e]);
+      }
+    };
+    constexpr int kBatch = 8;  // loads in flight per lane, issued before the first multiply
+    int c0 = 0;
+    for (; c0 + kBatch <= chunks; c0 += kBatch) {
+      dwordx4 q[kBatch];  // streamed once: nontemporal
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) q[u] = __builtin_nontemporal_load(wr + 16 * (c0 + u));
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) madd(q[u], c0 + u);
+    }
+    for (; c0 < chunks; ++c0) madd(__builtin_nontemporal_load(wr + 16 * c0), c0);
+    const float total = row16_sum((acc[0] + acc[1]) + (acc[2] + acc[3]));
+    const uint16_t bits = to_bf(total);
+    if (valid) {
+      if (logits && l16 == 0) logits[row] = bits;
+      const float value = bf(bits);
+      if (head_better(value, (int)row, best, best_row)) {
+        best = value;
+        best_row = (int)row;
+      }
+    }
+  }
+  // The wave's four lane groups, then the workgroup's waves.
+#pragma unroll
+  for (int off = 16; off < 64; off <<= 1) {
+    const float ov = __shfl_xor(best, off);
+    const int oi = __shfl_xor(best_row, off);
+    if (head_better(ov, oi, best, best_row)) {
+      best = ov;
+      best_row = oi;
+    }
+  }
+  if (lane == 0) {
+    wave_val[wave] = best;
+    wave_idx[wave] = best_row;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int i = 1; i < kHeadThreads / 64; ++i)
+      if (head_better(wave_val[i], wave_idx[i], best, best_row)) {
+        best = wave_val[i];
+        best_row = wave_idx[i];
+      }
+    part_val[blockIdx.x] = best;
+    part_idx[blockIdx.x] = best_row;
+  }
+}
+
+__global__ __launch_bounds__(kHeadThreads) void lm_head_argmax_final_kernel(const float *part_val, const int *part_idx,
+                                                                            int parts, int64_t *token) {
+  __shared__ float wave_val[kHeadThreads / 64];
+  __shared__ int wave_idx[kHeadThreads / 64];
+  float best = -INFINITY;
+  int best_row = 0x7FFFFFFF;
+  for (int i = threadIdx.x; i < parts; i += kHeadThreads)
+    if (head_better(part_val[i], part_idx[i], best, best_row)) {
+      best = part_val[i];
+      best_row = part_idx[i];
+    }
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const float ov = __shfl_xor(best, off);
+    const int oi = __shfl_xor(best_row, off);
+    if (head_better(ov, oi, best, best_row)) {
+      best = ov;
+      best_row = oi;
+    }
+  }
+  if ((threadIdx.x & 63) == 0) {
+    wave_val[threadIdx.x >> 6] = best;
+    wave_idx[threadIdx.x >> 6] = best_row;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int i = 1; i < kHeadThreads / 64; ++i)
+      if (head_better(wave_val[i], wave_idx[i], best, best_row)) {
+        best = wave_val[i];
+        best_row = wave_idx[i];
+      }
+    // every row's logit was NaN: row 0
+    token[0] = best_row == 0x7FFFFFFF ? 0 : (int64_t)best_row;
+  }
+}
+
 // out[r][c] = bf16(silu(g) * u) with g = gu[r][c], u = gu[r][inter + c], in fp32.
 __global__ __launch_bounds__(256) void swiglu_kernel(const uint16_t *gu, int64_t rows, int64_t inter, uint16_t *out) {
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;   // one group of 8 columns
@@ -805,7 +939,9 @@ hipError_t launch_add_rmsnorm_split(float *h, const SplitSource &delta, const ui
     hipLaunchKernelGGL((add_rmsnorm_kernel<true, decltype(ks)::value>), dim3((unsigned)rows), dim3(kNormThreads), 0, stream,
                        h, nullptr, delta, weight, eps, out, hidden);
   };
-  with_split_count(delta.ks, launch);
+  // Eight splits (the 3B-class down GEMV, one token or a 512-token prompt) also read loop-free.
+  if (delta.ks == 8) launch(std::integral_constant<int, 8>{});
+  else with_split_count(delta.ks, launch);
   return hipGetLastError();
 }
 
@@ -900,6 +1036,21 @@ hipError_t launch_decode_attention_split(const SplitSource &qkv, const int64_t *
   in.heads = heads;
   in.kv_heads = kv_heads;
   return launch_attention<true>(in, k_cache, v_cache, position, length, max_ctx, scale, partials, out, stream);
+}
+
+int64_t lm_head_argmax_workspace() { return (int64_t)kHeadBlocks * (int64_t)(sizeof(float) + sizeof(int)); }
+
+hipError_t launch_lm_head_argmax(const uint16_t *weight, int64_t vocab, int hidden, const uint16_t *x, uint16_t *logits,
+                                 void *workspace, int64_t *token, hipStream_t stream) {
+  float *part_val = static_cast<float *>(workspace);
+  int *part_idx = reinterpret_cast<int *>(part_val + kHeadBlocks);
+  const int blocks = (int)std::min<int64_t>(kHeadBlocks, (vocab + 15) / 16);
+  hipLaunchKernelGGL(lm_head_argmax_kernel, dim3(blocks), dim3(kHeadThreads), (size_t)hidden * sizeof(float), stream, weight,
+                     vocab, hidden, x, logits, part_val, part_idx);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(lm_head_argmax_final_kernel, dim3(1), dim3(kHeadThreads), 0, stream, part_val, part_idx, blocks, token);
+  return hipGetLastError();
 }
 
 hipError_t launch_swiglu(const uint16_t *gu, int64_t rows, int64_t inter, uint16_t *out, hipStream_t stream) {

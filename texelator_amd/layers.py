@@ -290,6 +290,34 @@ def rope_kv_cache_split(qkv_handle: int, positions: torch.Tensor, cos: torch.Ten
     return q_out
 
 
+def lm_head_argmax_workspace_bytes() -> int:
+    """Device scratch of :func:`lm_head_argmax`."""
+    out = ctypes.c_int64(0)
+    check(_lib.load().tx_lm_head_argmax_workspace(ctypes.byref(out)))
+    return int(out.value)
+
+
+def lm_head_argmax(weight: torch.Tensor, x: torch.Tensor, workspace: torch.Tensor, out: torch.Tensor | None = None,
+                   logits: torch.Tensor | None = None) -> torch.Tensor:
+    """Greedy next token ``argmax(bf16(x @ weight^T))`` (the first row among equal maxima) for one
+    bf16 hidden state ``x`` [hidden] or [1, hidden], written to ``out`` (int64 [1]); the bf16
+    logits [vocab] too when ``logits`` is given."""
+    _expect(weight.is_cuda and weight.dtype == torch.bfloat16 and weight.is_contiguous() and weight.dim() == 2,
+            "weight must be a contiguous CUDA bf16 [vocab, hidden] tensor")
+    vocab, hidden = weight.shape
+    _expect(x.dtype == torch.bfloat16 and x.is_contiguous() and x.numel() == hidden and x.data_ptr() % 16 == 0,
+            "x must be one contiguous, 16-byte aligned bf16 hidden state")
+    _expect(workspace.is_cuda and workspace.is_contiguous(), "workspace must be a contiguous CUDA tensor")
+    if out is None:
+        out = torch.empty(1, dtype=torch.int64, device=x.device)
+    _expect(out.dtype == torch.int64 and out.is_contiguous() and out.numel() == 1, "out must be int64 [1]")
+    if logits is not None:
+        _expect(logits.dtype == torch.bfloat16 and logits.is_contiguous() and logits.numel() == vocab, "logits must be bf16 [vocab]")
+    check(_lib.load().tx_lm_head_argmax(_ptr(weight), vocab, hidden, _ptr(x), _ptr(logits), _ptr(workspace),
+                                        workspace.numel() * workspace.element_size(), _ptr(out), _stream(x)))
+    return out
+
+
 def swiglu(gate_up: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
     """``bf16(silu(g) * u)`` for rows ``[g | u]``."""
     _expect(gate_up.dtype == torch.bfloat16 and gate_up.is_contiguous() and gate_up.dim() == 2 and gate_up.shape[1] % 2 == 0,

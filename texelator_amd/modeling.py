@@ -199,6 +199,8 @@ class BC4Decoder:
         self.gate_up_swiglu_prefill = fused
         # prefill GEMMs that split K leave their partials to RoPE and add+RMSNorm (no reduce kernel)
         self.split_prefill = fused
+        # greedy next token by this library's lm_head GEMV + argmax (else torch's linear + argmax)
+        self.fused_head = fused and config.hidden % 128 == 0
         # a prompt's causal attention with this library's kernel (else torch's flash attention)
         self.prompt_attention_kernel = fused and prompt_attention_supported(config)
         ext = extension()
@@ -288,6 +290,8 @@ class BC4Decoder:
         self.attn_buffer = torch.empty(1, c.heads * c.head_dim, dtype=bf16, device=self.device)
         self.act_buffer = torch.empty((1, c.intermediate), dtype=bf16, device=self.device)
         self.token = torch.zeros(1, dtype=torch.long, device=self.device)
+        self.head_workspace = torch.empty(layers.lm_head_argmax_workspace_bytes() if self.fused_head else 16,
+                                          dtype=torch.uint8, device=self.device)
         self.position = torch.zeros(1, dtype=torch.long, device=self.device)
         self.graphs: dict[int, torch.cuda.CUDAGraph] = {}
         self._pool = None
@@ -493,6 +497,18 @@ class BC4Decoder:
     def logits(self, hidden: torch.Tensor) -> torch.Tensor:
         return functional.linear(hidden, self.lm_head)
 
+    def greedy_token(self, hidden: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+        """``argmax(logits(hidden))`` of one hidden state [1, hidden] (int64 [1]): the lm_head GEMV
+        with the argmax in its epilogue (the first of equal bf16 logits, as argmax picks it), or
+        torch's linear + argmax without ``fused_head``."""
+        if self.fused_head:
+            return layers.lm_head_argmax(self.lm_head, hidden, self.head_workspace, out=out)
+        token = self.logits(hidden).argmax(-1)
+        if out is None:
+            return token
+        out.copy_(token)
+        return out
+
     # ---------------------------------------------------------------- prefill and decode
     @torch.inference_mode()
     def prefill(self, ids: torch.Tensor) -> torch.Tensor:
@@ -502,7 +518,7 @@ class BC4Decoder:
             raise ValueError("prompt longer than the cache")
         positions = self.key_positions[:tokens]
         hidden = self.hidden_states(ids.view(-1), positions, tokens)
-        next_token = self.logits(hidden[-1:]).argmax(-1)
+        next_token = self.greedy_token(hidden[-1:])
         self.token.copy_(next_token)
         self.position.fill_(tokens)
         return next_token
@@ -512,7 +528,7 @@ class BC4Decoder:
 
     def _step(self, length: int) -> None:
         hidden = self.hidden_states(self.token, self.position, length)
-        self.token.copy_(self.logits(hidden).argmax(-1))
+        self.greedy_token(hidden, out=self.token)
         self.position.add_(1)
 
     @torch.inference_mode()
