@@ -423,7 +423,8 @@ def hf_section(torch, args) -> dict:
     """BASELINE config 4 through the reference's calling path: a Hugging Face Qwen2 with
     TexelatorLinear modules (``texelator_amd.hf.build_qwen2``), the reference's prefill protocol on
     it (``model.model(input_ids=...)``) and greedy ``model.generate`` of 256 tokens after a 512-token
-    prompt, timed on the host clock (``hf.benchmark_generate``)."""
+    prompt, timed on the host clock (``hf.benchmark_generate``); then the same model decoding 256
+    tokens through ``hf.GraphedGreedy`` (static cache, the library's attention, graph replays)."""
     from texelator_amd import hf, modeling, prefill
     from texelator_amd.runtime import free
 
@@ -437,6 +438,7 @@ def hf_section(torch, args) -> dict:
             log(str(error))
             pre, gate_failed = None, error.correctness
         gen = hf.benchmark_generate(model, prompt_tokens=args.prompt, new_tokens=256, runs=2)
+        graphed = hf.GraphedGreedy(model, max_cache_len=args.prompt + 264).benchmark(args.prompt, 256)
     finally:
         free(handles)
         del model
@@ -453,6 +455,9 @@ def hf_section(torch, args) -> dict:
         "decode_tok_s": round(gen["decode_tok_s"], 2),
         "generate_tok_s": round(gen["generate_tok_s"], 2),
         "generate_seconds": round(gen["generate_seconds"], 3),
+        "graphed_decode_tok_s": round(graphed["decode_tok_s"], 2),
+        "graphed_path": "hf.GraphedGreedy: static KV cache, the library's attention kernels, the one-token "
+                        "forward replayed from a HIP graph (device clock)",
     }
 
 

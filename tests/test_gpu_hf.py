@@ -182,3 +182,55 @@ def test_build_qwen2_reference_prefill_protocol_and_generate(ext):
         assert timing["new_tokens"] == 4 and timing["decode_tok_s"] > 0
     finally:
         runtime.free(handles)
+
+
+@pytest.fixture(scope="module")
+def tiny_bc4(ext):
+    """A two-layer Qwen2 (head_dim 128) whose linears are GPU-encoded BC4 handles."""
+    from texelator_amd import hf, modeling
+
+    model, handles = hf.build_qwen2(modeling.DecoderConfig.tiny(), seed=11)
+    yield model
+    runtime.free(handles)
+
+
+def test_texelator_attention_prompt_matches_flash(tiny_bc4):
+    """The ``"texelator"`` attention (the library's prompt attention kernel) inside the Hugging Face
+    forward gives the logits of torch's flash attention on a 40-token prompt."""
+    from texelator_amd import hf
+
+    ids = torch.randint(0, 512, (1, 40), generator=torch.Generator().manual_seed(21)).cuda()
+    try:
+        with torch.inference_mode(), sdpa_kernel([SDPBackend.FLASH_ATTENTION]):
+            tiny_bc4.set_attn_implementation("sdpa")
+            want = tiny_bc4(ids).logits
+            hf.use_texelator_attention(tiny_bc4)
+            got = tiny_bc4(ids).logits
+    finally:
+        tiny_bc4.set_attn_implementation("sdpa")
+    assert torch.isfinite(got).all()
+    assert rrms(want, got) < 2e-2
+
+
+def test_graphed_greedy_replays_equal_eager_steps(tiny_bc4):
+    """``GraphedGreedy``: every graph replay (embedding, BC4 linears, decode attention over the
+    static cache, norms, argmax) yields the token of the same step run eagerly, twice over from a
+    reset cache; and the tokens mostly agree with Hugging Face ``generate`` on flash attention and a
+    dynamic cache (bf16 attention sums differ in rounding)."""
+    from texelator_amd import hf
+
+    ids = torch.randint(0, 512, (1, 30), generator=torch.Generator().manual_seed(22)).cuda()
+    try:
+        runner = hf.GraphedGreedy(tiny_bc4, max_cache_len=256)
+        eager = runner.generate(ids, 24, eager=True)
+        graphed = runner.generate(ids, 24)
+        again = runner.generate(ids, 24)
+        assert torch.equal(eager, graphed) and torch.equal(graphed, again)
+        with torch.inference_mode(), sdpa_kernel([SDPBackend.FLASH_ATTENTION]):
+            tiny_bc4.set_attn_implementation("sdpa")
+            want = tiny_bc4.generate(ids, max_new_tokens=24, do_sample=False, pad_token_id=0)[0, 30:]
+        assert (graphed == want).float().mean() >= 0.75
+        timing = runner.benchmark(prompt_tokens=30, new_tokens=16)
+        assert timing["decode_tok_s"] > 0
+    finally:
+        tiny_bc4.set_attn_implementation("sdpa")

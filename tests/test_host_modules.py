@@ -320,6 +320,39 @@ def test_qwen2_config_of_decoder_config():
     assert q.rope_parameters["rope_theta"] == 1e6
 
 
+def test_texelator_attention_registration_and_refusals():
+    """``use_texelator_attention`` registers the ``"texelator"`` implementation and switches a
+    Hugging Face model to it; the attention function refuses, before any launch, the calls its
+    kernels do not take (head_dim other than 128, batch > 1, a mask, a prompt not at position 0)."""
+    transformers = pytest.importorskip("transformers")
+    from texelator_amd import hf
+    from texelator_amd._lib import TexelatorError
+
+    config = transformers.Qwen2Config(vocab_size=64, hidden_size=64, intermediate_size=128, num_hidden_layers=1,
+                                      num_attention_heads=4, num_key_value_heads=2, head_dim=16,
+                                      tie_word_embeddings=False)
+    model = transformers.Qwen2ForCausalLM(config).eval()
+    hf.use_texelator_attention(model)
+    assert model.config._attn_implementation == hf.ATTENTION
+    module = model.model.layers[0].self_attn
+    positions = torch.arange(3)[None]
+
+    def call(q_shape, k_shape, mask=None, position_ids=positions):
+        q, k = torch.zeros(q_shape, dtype=torch.bfloat16), torch.zeros(k_shape, dtype=torch.bfloat16)
+        return hf.texelator_attention(module, q, k, k, mask, scaling=0.1, position_ids=position_ids)
+
+    with pytest.raises(TexelatorError, match="head_dim 128"):
+        call((1, 4, 3, 16), (1, 2, 8, 16))
+    with pytest.raises(TexelatorError, match="batch 1"):
+        call((2, 4, 3, 128), (2, 2, 8, 128))
+    with pytest.raises(TexelatorError, match="no mask"):
+        call((1, 4, 3, 128), (1, 2, 8, 128), mask=torch.ones(1, 1, 3, 8, dtype=torch.bool))
+    with pytest.raises(TexelatorError, match="position 0"):
+        call((1, 4, 3, 128), (1, 2, 8, 128), position_ids=torch.arange(2, 5)[None])
+    with pytest.raises(TexelatorError, match="at most 8"):
+        call((1, 36, 1, 128), (1, 2, 8, 128), position_ids=torch.tensor([[4]]))
+
+
 def test_prefill_benchmark_rejects_plain_models():
     from texelator_amd import prefill
 

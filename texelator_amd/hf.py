@@ -10,7 +10,11 @@ model, its linears BC4-encoded on the GPU (or uniform blocks) with the same init
 :class:`~texelator_amd.modeling.BC4Decoder`; :func:`benchmark_generate` times greedy ``generate``.
 
 Attention runs through torch's flash kernel (``sdpa``): the math path would issue bf16 batched
-products with transposed operands.
+products with transposed operands. :func:`use_texelator_attention` switches a model to this
+library's decode and prompt attention kernels instead (the ``"texelator"`` attention
+implementation), and :class:`GraphedGreedy` decodes such a model from a static KV cache with the
+one-token forward captured in a HIP graph, which removes the per-token host cost of the Hugging Face
+modules.
 """
 from __future__ import annotations
 
@@ -20,6 +24,7 @@ import time
 import torch
 from torch import nn
 
+from ._lib import TexelatorError
 from .modeling import DISTINCT_LAYERS, DecoderConfig, encoded_bc4, init_std, random_bc4
 from .runtime import PREFILL_THRESHOLD, PREFILL_TILE_ROWS, TexelatorLinear, extension, free
 
@@ -109,6 +114,155 @@ def build_qwen2(config: DecoderConfig, seed: int = 0, weights: str = "encoded", 
         cache.clear()
     model._texelator_handles = handles
     return model, handles
+
+
+ATTENTION = "texelator"
+
+
+def texelator_attention(module: nn.Module, query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+                        attention_mask: torch.Tensor | None, scaling: float | None = None, dropout: float = 0.0,
+                        **kwargs) -> tuple[torch.Tensor, None]:
+    """The Hugging Face attention implementation ``"texelator"`` (see :func:`use_texelator_attention`):
+    one query token through the library's decode attention kernel, a prompt starting at position 0
+    through its prompt attention kernel. Arguments as Hugging Face passes them to an attention
+    function: ``query`` ``[1, heads, T, 128]`` after RoPE, ``key``/``value`` the layer's whole cache
+    ``[1, kv_heads, L, 128]`` just updated (a static cache's ``L`` is its capacity; the keys that
+    count are those at positions 0..position), ``position_ids`` ``[1, T]`` in ``kwargs``. No mask is
+    read: decode attends to positions 0..position, a prompt causally. Returns ``[1, T, heads, 128]``
+    as the Hugging Face attention functions do. No reference counterpart: the reference runs the
+    stock ``sdpa`` attention (``runtime.py:210-239`` replaces only the linears)."""
+    from . import layers
+
+    batch, heads, tokens, head_dim = query.shape
+    kv_heads, length = key.shape[1], key.shape[2]
+    positions = kwargs.get("position_ids")
+    if batch != 1 or head_dim != 128 or heads % kv_heads or dropout or positions is None:
+        raise TexelatorError("texelator attention: batch 1, head_dim 128, heads a multiple of kv_heads, "
+                             "no dropout, position_ids given")
+    if attention_mask is not None:
+        raise TexelatorError("texelator attention reads no mask (padding is not supported)")
+    k_cache, v_cache = key[0], value[0]
+    scale = float(scaling if scaling is not None else head_dim ** -0.5)
+    if tokens == 1:
+        if heads // kv_heads > 8:
+            raise TexelatorError("texelator attention: at most 8 query heads per KV head in decode")
+        workspace = torch.empty(layers.decode_attention_workspace_bytes(heads, length), dtype=torch.uint8,
+                                device=query.device)
+        out = layers.decode_attention(query.reshape(heads * head_dim), k_cache, v_cache, positions.reshape(1), length,
+                                      heads, kv_heads, scale, workspace)
+        return out.view(1, 1, heads, head_dim), None
+    if int(positions[0, 0]) != 0:
+        raise TexelatorError("texelator attention: a prompt must start at position 0 (no chunked prefill)")
+    q = query.transpose(1, 2).reshape(tokens, heads * head_dim)
+    out = layers.prefill_attention(q, k_cache, v_cache, heads, kv_heads, scale)
+    return out.view(1, tokens, heads, head_dim), None
+
+
+def use_texelator_attention(model: nn.Module) -> None:
+    """Register :func:`texelator_attention` with Hugging Face as ``"texelator"`` and switch
+    ``model`` to it."""
+    from transformers import AttentionInterface
+
+    AttentionInterface.register(ATTENTION, texelator_attention)
+    model.set_attn_implementation(ATTENTION)
+
+
+class GraphedGreedy:
+    """Greedy decoding of a Hugging Face causal LM at batch 1 with a static KV cache, the
+    one-token forward captured once in a HIP graph: each replay embeds the previous token, runs
+    every layer (the BC4 linears, the ``"texelator"`` attention, Hugging Face's norms, RoPE and
+    cache writes), appends to the cache and leaves the argmax as the next input. The host only
+    replays; nothing syncs between tokens. The prompt runs eagerly (:meth:`prefill`). Switches
+    ``model`` to the ``"texelator"`` attention. The same model and cache work without the graph
+    (``eager=True``), token for token the same."""
+
+    def __init__(self, model: nn.Module, max_cache_len: int):
+        import transformers
+
+        use_texelator_attention(model)
+        self.model = model
+        self.max_cache_len = int(max_cache_len)
+        self.cache = transformers.StaticCache(config=model.config, max_cache_len=self.max_cache_len)
+        self.token = torch.zeros((1, 1), dtype=torch.long, device=model.device)
+        self.length = 0  # tokens in the cache, as the host counts them
+        self.graph: torch.cuda.CUDAGraph | None = None
+
+    def _step(self) -> None:
+        logits = self.model(input_ids=self.token, past_key_values=self.cache, use_cache=True).logits
+        torch.argmax(logits[:, -1], dim=-1, keepdim=True, out=self.token)
+
+    @torch.inference_mode()
+    def prefill(self, ids: torch.Tensor) -> torch.Tensor:
+        """Reset the cache, run the prompt ``ids`` ``[1, T]`` and return the first new token."""
+        if ids.dim() != 2 or ids.shape[0] != 1 or not 0 < ids.shape[1] < self.max_cache_len:
+            raise ValueError("prefill takes one prompt [1, T] shorter than the cache")
+        self.cache.reset()
+        logits = self.model(input_ids=ids, past_key_values=self.cache, use_cache=True, logits_to_keep=1).logits
+        torch.argmax(logits[:, -1], dim=-1, keepdim=True, out=self.token)
+        self.length = ids.shape[1]
+        return self.token.clone()
+
+    @torch.inference_mode()
+    def _capture(self) -> None:
+        # a warm-up step outside the graph, then the capture; the cache lengths and the token are
+        # put back, so the cache holds exactly the prompt afterwards
+        lengths = [layer.cumulative_length.clone() for layer in self.cache.layers]
+        token = self.token.clone()
+        stream = torch.cuda.Stream(self.token.device)
+        stream.wait_stream(torch.cuda.current_stream(self.token.device))
+        with torch.cuda.stream(stream):
+            self._step()
+        torch.cuda.current_stream(self.token.device).wait_stream(stream)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            self._step()
+        for layer, saved in zip(self.cache.layers, lengths):
+            layer.cumulative_length.copy_(saved)
+        self.token.copy_(token)
+        self.graph = graph
+
+    @torch.inference_mode()
+    def decode(self, steps: int, out: torch.Tensor | None = None, eager: bool = False) -> None:
+        """``steps`` greedy tokens after the current one; token i goes to ``out[i]`` when given."""
+        if self.length == 0:
+            raise RuntimeError("prefill first")
+        if self.length + steps >= self.max_cache_len:
+            raise ValueError("decode would run past the static cache")
+        if not eager and self.graph is None:
+            self._capture()
+        for i in range(steps):
+            if eager:
+                self._step()
+            else:
+                self.graph.replay()
+            if out is not None:
+                out[i].copy_(self.token[0, 0])
+        self.length += steps
+
+    def generate(self, ids: torch.Tensor, new_tokens: int, eager: bool = False) -> torch.Tensor:
+        """Greedy generation: the ``new_tokens`` new token ids (the first from the prompt's logits)."""
+        out = torch.empty(new_tokens, dtype=torch.long, device=self.token.device)
+        out[0] = self.prefill(ids)[0, 0]
+        self.decode(new_tokens - 1, out=out[1:], eager=eager)
+        return out
+
+    def benchmark(self, prompt_tokens: int, new_tokens: int) -> dict:
+        """Decode tok/s of graph replays after a seeded random prompt (device clock, prompt excluded)."""
+        generator = torch.Generator(device="cpu").manual_seed(0)
+        vocab = self.model.get_input_embeddings().weight.shape[0]
+        ids = torch.randint(0, vocab, (1, prompt_tokens), generator=generator).to(self.token.device)
+        self.prefill(ids)
+        self.decode(4)  # capture and first replays
+        self.prefill(ids)
+        torch.cuda.synchronize()
+        begin, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        begin.record()
+        self.decode(new_tokens)
+        end.record()
+        end.synchronize()
+        seconds = begin.elapsed_time(end) / 1000.0
+        return {"prompt_tokens": prompt_tokens, "new_tokens": new_tokens, "seconds": seconds,
+                "decode_tok_s": new_tokens / seconds}
 
 
 def _generate(model: nn.Module, ids: torch.Tensor, new_tokens: int) -> torch.Tensor:
