@@ -232,5 +232,34 @@ def test_graphed_greedy_replays_equal_eager_steps(tiny_bc4):
         assert (graphed == want).float().mean() >= 0.75
         timing = runner.benchmark(prompt_tokens=30, new_tokens=16)
         assert timing["decode_tok_s"] > 0
+        # with the norms on the library kernel too: replays still equal eager steps
+        replaced = hf.use_texelator_norms(tiny_bc4)
+        try:
+            assert len(replaced) == 2 * 2 + 1
+            runner = hf.GraphedGreedy(tiny_bc4, max_cache_len=256)
+            assert torch.equal(runner.generate(ids, 24, eager=True), runner.generate(ids, 24))
+        finally:
+            hf.restore_modules(replaced)
     finally:
         tiny_bc4.set_attn_implementation("sdpa")
+
+
+@pytest.mark.parametrize("shape", [(7, 256), (1, 3, 2048), (2, 5120)])
+def test_texelator_rmsnorm_matches_hf_rmsnorm(ext, shape):
+    """``TexelatorRMSNorm`` against the Hugging Face module on the same weight: the same formula and
+    roundings, so almost every value is bitwise equal and none is more than one bf16 step apart
+    (the fp32 sums of squares add in different orders)."""
+    from transformers.models.qwen2.modeling_qwen2 import Qwen2RMSNorm
+
+    from texelator_amd import hf
+
+    g = torch.Generator(device="cuda").manual_seed(shape[-1])
+    x = (torch.randn(shape, device="cuda", generator=g) * 3).to(torch.bfloat16)
+    norm = Qwen2RMSNorm(shape[-1], eps=1e-6).to(device="cuda", dtype=torch.bfloat16)
+    with torch.no_grad():
+        norm.weight.copy_(1 + 0.2 * torch.randn(shape[-1], device="cuda", generator=g))
+        want = norm(x)
+        got = hf.TexelatorRMSNorm(norm.weight, norm.variance_epsilon)(x)
+    assert got.shape == want.shape and got.dtype == torch.bfloat16
+    assert (got == want).float().mean() >= 0.99
+    assert torch.allclose(got.float(), want.float(), rtol=2 ** -7, atol=0)

@@ -353,6 +353,30 @@ def test_texelator_attention_registration_and_refusals():
         call((1, 36, 1, 128), (1, 2, 8, 128), position_ids=torch.tensor([[4]]))
 
 
+def test_texelator_norm_replacement_and_restore():
+    """``use_texelator_norms`` swaps every bf16 RMSNorm of a Hugging Face model (two per layer and the
+    final one) for ``TexelatorRMSNorm`` sharing the weight, and ``restore_modules`` puts them back;
+    fp32 norms are left alone."""
+    transformers = pytest.importorskip("transformers")
+    from texelator_amd import hf
+
+    config = transformers.Qwen2Config(vocab_size=64, hidden_size=64, intermediate_size=128, num_hidden_layers=2,
+                                      num_attention_heads=4, num_key_value_heads=2, head_dim=16,
+                                      tie_word_embeddings=False)
+    model = transformers.Qwen2ForCausalLM(config).eval()
+    assert hf.use_texelator_norms(model) == []  # fp32 weights
+    model.to(torch.bfloat16)
+    original = model.model.layers[1].post_attention_layernorm
+    replaced = hf.use_texelator_norms(model)
+    assert len(replaced) == 2 * 2 + 1
+    swapped = model.model.layers[1].post_attention_layernorm
+    assert isinstance(swapped, hf.TexelatorRMSNorm) and swapped.weight is original.weight
+    assert swapped.variance_epsilon == original.variance_epsilon
+    assert hf.use_texelator_norms(model) == []  # already swapped
+    hf.restore_modules(replaced)
+    assert model.model.layers[1].post_attention_layernorm is original
+
+
 def test_prefill_benchmark_rejects_plain_models():
     from texelator_amd import prefill
 

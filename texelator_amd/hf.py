@@ -167,6 +167,50 @@ def use_texelator_attention(model: nn.Module) -> None:
     model.set_attn_implementation(ATTENTION)
 
 
+class TexelatorRMSNorm(nn.Module):
+    """A Hugging Face RMSNorm (Qwen2/Llama form: ``weight * bf16(x * rsqrt(mean(x^2) + eps))``, x in
+    fp32) through the library's add+RMSNorm kernel: two launches (the fp32 copy of x and the
+    kernel) instead of the module's six or seven elementwise ones. The same formula and roundings;
+    the fp32 sum of squares runs in the kernel's order, so a row's result can differ from torch's in
+    the last bit where the two sums round apart. bf16 activations and weight, hidden a multiple of 4."""
+
+    def __init__(self, weight: nn.Parameter, eps: float):
+        super().__init__()
+        self.weight = weight
+        self.variance_epsilon = float(eps)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        from . import layers
+
+        shape = x.shape
+        h = x.reshape(-1, shape[-1]).float()
+        return layers.add_rmsnorm(h, None, self.weight, self.variance_epsilon).view(shape)
+
+
+def use_texelator_norms(model: nn.Module) -> list[tuple[nn.Module, str, nn.Module]]:
+    """Replace every bf16 ``*RMSNorm`` module of ``model`` (weight and ``variance_epsilon``, hidden a
+    multiple of 4) with :class:`TexelatorRMSNorm`; returns ``(parent, name, original)`` per
+    replacement, for :func:`restore_modules`."""
+    replaced = []
+    for name, module in list(model.named_modules()):
+        weight = getattr(module, "weight", None)
+        if (not type(module).__name__.endswith("RMSNorm") or isinstance(module, TexelatorRMSNorm)
+                or not hasattr(module, "variance_epsilon") or weight is None or weight.dtype != torch.bfloat16
+                or weight.dim() != 1 or weight.numel() % 4):
+            continue
+        parent_name, _, child = name.rpartition(".")
+        parent = model.get_submodule(parent_name) if parent_name else model
+        setattr(parent, child, TexelatorRMSNorm(weight, module.variance_epsilon))
+        replaced.append((parent, child, module))
+    return replaced
+
+
+def restore_modules(replaced: list[tuple[nn.Module, str, nn.Module]]) -> None:
+    """Put back the modules :func:`use_texelator_norms` replaced."""
+    for parent, child, original in replaced:
+        setattr(parent, child, original)
+
+
 class GraphedGreedy:
     """Greedy decoding of a Hugging Face causal LM at batch 1 with a static KV cache, the
     one-token forward captured once in a HIP graph: each replay embeds the previous token, runs
