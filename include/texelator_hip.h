@@ -242,6 +242,20 @@ int tx_decode_attention_split(uint64_t qkv_handle, const int64_t *position, cons
                               int64_t max_context, float scale, void *workspace, int64_t workspace_bytes, void *out,
                               void *stream);
 
+/* tx_decode_attention_split followed by tx_linear_split of o_handle on its output, one launch fewer:
+ * the attention leaves its chunk partials in `workspace` and every workgroup of the o projection's
+ * one-token GEMV merges the heads of its K split from them itself (the attention's merge, done
+ * where its output is consumed), so o_handle's split-K partials end bitwise as after the two calls
+ * (read them with tx_add_rmsnorm_split); the key and value are written to the caches as there. The
+ * attention output itself is not written. o_handle: K = heads * head_dim, BF16 bias or none.
+ * TX_ERR_UNSUPPORTED, with nothing launched, where the merge does not fit the o GEMV: a LUT-mode o
+ * handle, a length of more than 16 chunks of 64 positions, or more than 64 (heads of one o split) x
+ * chunks. No counterpart in the reference (its decoder layers are Hugging Face modules). */
+int tx_decode_attention_o_split(uint64_t qkv_handle, uint64_t o_handle, const int64_t *position, const float *rope_row,
+                                int64_t length, int heads, int kv_heads, int head_dim, void *k_cache, void *v_cache,
+                                int64_t max_context, float scale, void *workspace, int64_t workspace_bytes,
+                                void *stream);
+
 /* out[r][c] = bf16(silu(g) * u) for gate_up rows [g (intermediate) | u (intermediate)], fp32 math. */
 int tx_swiglu(const void *gate_up, int64_t rows, int64_t intermediate, void *out, void *stream);
 

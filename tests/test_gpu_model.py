@@ -486,20 +486,114 @@ def test_split_decode_with_fused_swiglu_is_bit_identical(ext):
         model.close()
 
 
-def test_split_decode_step_is_bit_identical(ext, tiny):
-    """A decode step through the split-K consumers equals the unsplit fused step, bit for bit."""
+def test_capture_after_the_cache_is_full(ext):
+    """A decode that fills the cache leaves the model at position max_context. Capturing a step
+    from there (benchmark_decode captures before its prefill) runs the warm-up step at the last row,
+    inside the RoPE table, and leaves the cache, the token and the position as they were; the
+    benchmark then runs twice in a row on a model whose context is its whole cache."""
+    model = modeling.BC4Decoder(modeling.DecoderConfig.tiny(), max_context=96, seed=5)
+    try:
+        ids = prefill.prompt_ids(model, 40, seed=4)
+        with torch.inference_mode():
+            model.prefill(ids)
+            model.decode(56, 40)  # positions 40..95: the cache is full
+            assert int(model.position) == 96
+            k, v, token = model.k_cache.clone(), model.v_cache.clone(), model.token.clone()
+            model.graphs.clear()
+            model.capture(96)
+            torch.cuda.synchronize()
+        assert int(model.position) == 96 and torch.equal(model.token, token)
+        assert torch.equal(model.k_cache, k) and torch.equal(model.v_cache, v)
+        for _ in range(2):
+            assert prefill.benchmark_decode(model, prompt_tokens=40, context=96)["steps"] == 56
+    finally:
+        model.close()
+
+
+@pytest.mark.parametrize("attention_in_o", [True, False])
+def test_split_decode_step_is_bit_identical(ext, tiny, attention_in_o):
+    """A decode step through the split-K consumers equals the unsplit fused step, bit for bit, with
+    the attention's chunk merge inside the o GEMV and as its own kernel."""
     ids = prefill.prompt_ids(tiny, 30, seed=6)
-    with torch.inference_mode():
-        tiny.prefill(ids)
-        token = ids[-1:]
-        tiny.split_decode = False
-        a = tiny.hidden_states(token, tiny.key_positions[30:31], 512).clone()
-        ka = tiny.k_cache[:, :, 30].clone()
-        tiny.split_decode = True
-        b = tiny.hidden_states(token, tiny.key_positions[30:31], 512)
-        kb = tiny.k_cache[:, :, 30].clone()
+    try:
+        tiny.attention_in_o = attention_in_o
+        with torch.inference_mode():
+            tiny.prefill(ids)
+            token = ids[-1:]
+            tiny.split_decode = False
+            a = tiny.hidden_states(token, tiny.key_positions[30:31], 512).clone()
+            ka = tiny.k_cache[:, :, 30].clone()
+            tiny.split_decode = True
+            b = tiny.hidden_states(token, tiny.key_positions[30:31], 512)
+            kb = tiny.k_cache[:, :, 30].clone()
+    finally:
+        tiny.attention_in_o = True
     assert torch.equal(a, b)
     assert torch.equal(ka, kb)
+
+
+@pytest.mark.parametrize("heads,kv,k,position,length,bias", [
+    (16, 2, 2048, 600, 768, True), (16, 2, 2048, 0, 64, False), (16, 2, 2048, 1023, 1024, True),
+    (16, 2, 2048, 100, 512, False), (12, 2, 1536, 300, 640, True), (40, 8, 5120, 200, 256, True),
+    (8, 8, 1024, 63, 128, False)])
+def test_decode_attention_o_split_is_bit_identical(ext, heads, kv, k, position, length, bias):
+    """RoPE + attention with the chunk merge inside the o GEMV == decode_attention_split +
+    linear_split(o), bit for bit: the add+RMSNorm read of o's split partials, the residual and both
+    caches; group sizes 8, 6, 5 and 1, o split 1-4 ways, 1-16 chunks, twice on the same workspace."""
+    d, ctx = 128, 1024
+    qkv = _random_handle(ext, (heads + 2 * kv) * d, k, seed=heads + position, bias=bias)
+    o = _random_handle(ext, k, heads * d, seed=heads + position + 1, bias=bias)
+    try:
+        g = torch.Generator(device="cuda").manual_seed(position + 9)
+        x = torch.randn(1, k, device="cuda", generator=g).to(torch.bfloat16)
+        angles = torch.rand(ctx, d, device="cuda", generator=g) * 6
+        rope_row = torch.cat([angles[position].cos(), angles[position].sin()]).contiguous()
+        pos = torch.tensor([position], device="cuda")
+        kc = torch.randn(kv, ctx, d, device="cuda", generator=g).to(torch.bfloat16)
+        vc = torch.randn(kv, ctx, d, device="cuda", generator=g).to(torch.bfloat16)
+        h0 = torch.randn(1, k, device="cuda", generator=g)
+        w = (1 + 0.1 * torch.randn(k, device="cuda", generator=g)).to(torch.bfloat16)
+        ws = torch.empty(layers.decode_attention_workspace_bytes(heads, length), dtype=torch.uint8, device="cuda")
+        scale = 1 / math.sqrt(d)
+        layers.linear_split(qkv, x)
+        caches = [kc.clone(), vc.clone()]
+        attn = layers.decode_attention_split(qkv, pos, rope_row, heads, kv, d, caches[0], caches[1], length, scale, ws)
+        layers.linear_split(o, attn)
+        h_want = h0.clone()
+        want = layers.add_rmsnorm_split(h_want, o, w, 1e-6, torch.empty(1, k, device="cuda", dtype=torch.bfloat16))
+        for _ in range(2):
+            got_caches = [kc.clone(), vc.clone()]
+            assert layers.decode_attention_o_split(qkv, o, pos, rope_row, heads, kv, d, got_caches[0], got_caches[1],
+                                                   length, scale, ws)
+            h_got = h0.clone()
+            got = layers.add_rmsnorm_split(h_got, o, w, 1e-6, torch.empty(1, k, device="cuda", dtype=torch.bfloat16))
+            assert torch.equal(want, got) and torch.equal(h_want, h_got)
+            assert torch.equal(caches[0], got_caches[0]) and torch.equal(caches[1], got_caches[1])
+    finally:
+        ext.free(qkv)
+        ext.free(o)
+
+
+def test_decode_attention_o_split_refusals(ext):
+    """Where the merge does not fit the o GEMV (more than 16 chunks, or 40 heads x 16 chunks per o
+    workgroup) the call returns False and launches nothing: the caches stay as they were."""
+    heads, kv, k, d, ctx = 40, 8, 5120, 128, 2048
+    qkv = _random_handle(ext, (heads + 2 * kv) * d, k, seed=3)
+    o = _random_handle(ext, k, heads * d, seed=4)
+    try:
+        kc = torch.zeros(kv, ctx, d, device="cuda", dtype=torch.bfloat16)
+        vc = torch.zeros_like(kc)
+        pos = torch.tensor([5], device="cuda")
+        rope_row = torch.ones(2 * d, device="cuda")
+        layers.linear_split(qkv, torch.ones(1, k, device="cuda", dtype=torch.bfloat16))
+        for length in (1088, 1024):
+            ws = torch.empty(layers.decode_attention_workspace_bytes(heads, length), dtype=torch.uint8, device="cuda")
+            assert not layers.decode_attention_o_split(qkv, o, pos, rope_row, heads, kv, d, kc, vc, length, 0.1, ws)
+        torch.cuda.synchronize()
+        assert not kc.any() and not vc.any()
+    finally:
+        ext.free(qkv)
+        ext.free(o)
 
 
 def test_prompt_flash_attention_matches_cached_attention(ext, tiny):

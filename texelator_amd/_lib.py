@@ -57,6 +57,8 @@ SIGNATURES = {
     "tx_decode_attention": (_I32, [_P, _P, _P, _P, _I64, _I32, _I32, _I32, _I64, ctypes.c_float, _P, _I64, _P, _P]),
     "tx_decode_attention_split": (_I32, [_U64, _P, _P, _I64, _I32, _I32, _I32, _P, _P, _I64, ctypes.c_float, _P, _I64,
                                          _P, _P]),
+    "tx_decode_attention_o_split": (_I32, [_U64, _U64, _P, _P, _I64, _I32, _I32, _I32, _P, _P, _I64, ctypes.c_float,
+                                           _P, _I64, _P]),
     "tx_swiglu": (_I32, [_P, _I64, _I64, _P, _P]),
     "tx_lm_head_argmax_workspace": (_I32, [ctypes.POINTER(ctypes.c_int64)]),
     "tx_lm_head_argmax": (_I32, [_P, _I64, _I64, _P, _P, _P, _I64, _P, _P]),

@@ -215,6 +215,10 @@ int run_prefill(Handle *h, int candidate, const void *x, bool f16, int64_t token
 }
 
 // The single-token split-K partials a handle's last tx_linear_split wrote.
+// Heads times chunks up to which an o GEMV workgroup merges the attention partials itself (the
+// merge reads that many 520-byte rows per workgroup).
+constexpr int kMergeMaxChunkHeads = 64;
+
 tx::SplitSource split_source(const Handle *h) {
   return tx::SplitSource{h->partials, static_cast<const uint16_t *>(h->bias), h->gemv_splits, h->Mp, 1};
 }
@@ -943,6 +947,61 @@ int tx_decode_attention_split(uint64_t qkv_handle, const int64_t *position, cons
                                            static_cast<uint16_t *>(k_cache), static_cast<uint16_t *>(v_cache),
                                            max_context, scale, static_cast<float *>(workspace),
                                            static_cast<uint16_t *>(out), reinterpret_cast<hipStream_t>(stream)));
+  return TX_OK;
+}
+
+int tx_decode_attention_o_split(uint64_t qkv_handle, uint64_t o_handle, const int64_t *position, const float *rope_row,
+                                int64_t length, int heads, int kv_heads, int head_dim, void *k_cache, void *v_cache,
+                                int64_t max_context, float scale, void *workspace, int64_t workspace_bytes,
+                                void *stream) {
+  g_last_error.clear();
+  Handle *h = as_handle(qkv_handle);
+  Handle *o = as_handle(o_handle);
+  if (!h || !o) return fail(TX_ERR_INVALID, "null Texelator handle");
+  if (!position || !rope_row || !k_cache || !v_cache || !workspace)
+    return fail(TX_ERR_INVALID, "decode_attention_o_split: null pointer");
+  if (!tx::decode_attention_supported(heads, kv_heads, head_dim))
+    return fail(TX_ERR_UNSUPPORTED, "decode_attention_o_split: needs head_dim 128 and at most 8 query heads per KV head");
+  if ((int64_t)h->M < (int64_t)(heads + 2 * kv_heads) * head_dim)
+    return fail(TX_ERR_INVALID, "decode_attention_o_split: qkv handle too narrow for the heads");
+  if (o->K != heads * head_dim) return fail(TX_ERR_INVALID, "decode_attention_o_split: o handle K must be heads * head_dim");
+  if (o->device != h->device) return fail(TX_ERR_INVALID, "decode_attention_o_split: handles on different devices");
+  if ((h->bias && h->bias_dtype != TX_DTYPE_BF16) || (o->bias && o->bias_dtype != TX_DTYPE_BF16))
+    return fail(TX_ERR_INVALID, "decode_attention_o_split: biases must be BF16");
+  if (length <= 0 || length > max_context || length > tx::decode_attention_max_length())
+    return fail(TX_ERR_INVALID, "decode_attention_o_split: length outside the cache or above 65536");
+  int64_t need = 0;
+  tx_decode_attention_workspace(heads, length, &need);
+  if (workspace_bytes < need) return fail(TX_ERR_INVALID, "decode_attention_o_split: workspace too small");
+  // Each o workgroup merges the heads of its K split from every chunk: worth it while that is small.
+  const int chunks = tx::decode_attention_chunks(length);
+  const int heads_per_split = (o->CG + o->gemv_splits - 1) / o->gemv_splits;
+  if (o->lut || chunks > tx::kMergeMaxChunks || heads_per_split * chunks > kMergeMaxChunkHeads)
+    return fail(TX_ERR_UNSUPPORTED, "decode_attention_o_split: the merge does not fit the o GEMV (LUT handle, more "
+                                    "than 16 chunks, or too many heads per split); use tx_decode_attention_split + "
+                                    "tx_linear_split");
+  DeviceGuard guard(h->device);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  float *partials = static_cast<float *>(workspace);
+  TX_HIP(tx::launch_decode_attention_split_partials(split_source(h), position, rope_row, length, heads, kv_heads,
+                                                    static_cast<uint16_t *>(k_cache), static_cast<uint16_t *>(v_cache),
+                                                    max_context, scale, partials, s));
+  tx::GemvParams p{};
+  p.tiles = o->tiles;
+  p.scales = o->scales;
+  p.M = o->M;
+  p.K = o->K;
+  p.Mp = o->Mp;
+  p.RG = o->RG;
+  p.CG = o->CG;
+  p.tokens = 1;
+  p.ks = o->gemv_splits;
+  p.partials = o->partials;
+  p.force_partials = 1;
+  p.attn = partials;
+  p.attn_chunks = chunks;
+  p.attn_group = heads / kv_heads;
+  TX_HIP(tx::launch_gemv(p, o->lookahead, true, s));
   return TX_OK;
 }
 

@@ -974,10 +974,11 @@ int64_t decode_attention_workspace(int heads, int64_t length) {
 }
 
 namespace {
+// combine false: the chunk partials are left for a GEMV that merges them (GemvParams::attn).
 template <bool ROPE>
 hipError_t launch_attention(const AttnInput &in, uint16_t *k_cache, uint16_t *v_cache, const int64_t *position,
                             int64_t length, int64_t max_ctx, float scale, float *partials, uint16_t *out,
-                            hipStream_t stream) {
+                            hipStream_t stream, bool combine = true) {
   const int chunks = decode_attention_chunks(length);
   const int group = in.heads / in.kv_heads;
   auto launch = [&](auto ks) {
@@ -987,7 +988,7 @@ hipError_t launch_attention(const AttnInput &in, uint16_t *k_cache, uint16_t *v_
   if constexpr (ROPE) with_split_count(in.split.ks, launch);
   else launch(std::integral_constant<int, 0>{});
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
+  if (e != hipSuccess || !combine) return e;
   hipLaunchKernelGGL(decode_attention_combine_kernel, dim3(in.heads), dim3(kHeadDim), 0, stream, partials, group, chunks, out);
   return hipGetLastError();
 }
@@ -1036,6 +1037,20 @@ hipError_t launch_decode_attention_split(const SplitSource &qkv, const int64_t *
   in.heads = heads;
   in.kv_heads = kv_heads;
   return launch_attention<true>(in, k_cache, v_cache, position, length, max_ctx, scale, partials, out, stream);
+}
+
+hipError_t launch_decode_attention_split_partials(const SplitSource &qkv, const int64_t *position, const float *rope_row,
+                                                  int64_t length, int heads, int kv_heads, uint16_t *k_cache,
+                                                  uint16_t *v_cache, int64_t max_ctx, float scale, float *partials,
+                                                  hipStream_t stream) {
+  static_assert(kAttnRow == kHeadDim + 2 && kMergeMaxChunks <= 64, "the partials layout the GEMV merge reads");
+  AttnInput in{};
+  in.split = qkv;
+  in.rope_row = rope_row;
+  in.heads = heads;
+  in.kv_heads = kv_heads;
+  return launch_attention<true>(in, k_cache, v_cache, position, length, max_ctx, scale, partials, nullptr, stream,
+                                false);
 }
 
 int64_t lm_head_argmax_workspace() { return (int64_t)kHeadBlocks * (int64_t)(sizeof(float) + sizeof(int)); }

@@ -89,6 +89,60 @@ __device__ __forceinline__ void stage_x_lds(uint4 *xs, const uint16_t *x, int K,
                                              (first + base + lane) * 16, 0, 0, 0);
 }
 
+// x of a split whose tile columns are attention heads (GemvParams::attn): head c_begin + j (j <
+// nc, one wave per head at a time) merged from the decode attention's chunk partials, exactly as
+// decode_attention_combine_kernel merges a head: M = the chunks' maximum m_c, weights w_c =
+// exp(m_c - M) (0 for an empty chunk), total = the 64-lane butterfly sum of l_c * w_c (lane c holds
+// chunk c), four fma chains acc[c % 4] over the chunks below the last multiple of four and the rest
+// into acc[0], in chunk order, and x = bf16(((acc0 + acc1) + (acc2 + acc3)) / total) -- so x is
+// bitwise the merge kernel's output. Lane l produces dimensions l and l + 64 and writes them as
+// stage_x_lds would place them. Every load of a head (all its chunks' values, clamped to the last
+// chunk, and the lane's chunk statistics) goes out before the first wait.
+__device__ __forceinline__ void merge_attention_x(uint4 *xs, const GemvParams &p, int c_begin, int nc, int wave,
+                                                  int lane) {
+  const int chunks = p.attn_chunks, group = p.attn_group;
+  const uint32_t step = (uint32_t)group * kAttnRow;  // floats between chunks of one head
+  const int main_end = chunks & ~3;
+  uint16_t *xh = reinterpret_cast<uint16_t *>(xs);
+  for (int j = wave; j < nc; j += kWaves) {
+    const int head = c_begin + j, kv = head / group, g = head % group;
+    const float *base = p.attn + ((size_t)kv * chunks * group + g) * kAttnRow;
+    float o0[kMergeMaxChunks], o1[kMergeMaxChunks];
+#pragma unroll
+    for (int c = 0; c < kMergeMaxChunks; ++c) {
+      const float *row = base + (uint32_t)min(c, chunks - 1) * step;
+      o0[c] = row[lane];
+      o1[c] = row[lane + 64];
+    }
+    const float *srow = base + (uint32_t)min(lane, chunks - 1) * step;
+    const float ms = srow[kAttnRow - 2], ls = srow[kAttnRow - 1];
+    const float mv = lane < chunks ? ms : -INFINITY;
+    float m = mv;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    const float w = mv == -INFINITY ? 0.f : expf(mv - m);
+    float total = lane < chunks ? __builtin_fmaf(ls, w, 0.f) : 0.f;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) total += __shfl_xor(total, off);
+    float a0[4] = {0.f, 0.f, 0.f, 0.f}, a1[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < kMergeMaxChunks; ++c) {
+      if (c < chunks) {
+        const float wc = __shfl(w, c);
+        if (c < main_end) {
+          a0[c & 3] = __builtin_fmaf(o0[c], wc, a0[c & 3]);
+          a1[c & 3] = __builtin_fmaf(o1[c], wc, a1[c & 3]);
+        } else {
+          a0[0] = __builtin_fmaf(o0[c], wc, a0[0]);
+          a1[0] = __builtin_fmaf(o1[c], wc, a1[0]);
+        }
+      }
+    }
+    xh[j * kTileK + lane] = to_bf(((a0[0] + a0[1]) + (a0[2] + a0[3])) / total);
+    xh[j * kTileK + lane + 64] = to_bf(((a1[0] + a1[1]) + (a1[2] + a1[3])) / total);
+  }
+}
+
 // One tile for one lane: decode both blocks and accumulate 4 MFMAs (block 0 into acc0, block 1
 // into acc1; the two are added at the end in a fixed order).
 template <bool F16>
@@ -154,8 +208,12 @@ __device__ __forceinline__ void progress_priority(int remaining, int total) {
 // relative per weight).
 // LUT: the palette of every block is read from a 255 x 255 x 8 table (p.lut) instead of being
 // computed; the rows of tile j+1 are fetched while tile j is decoded (needs LA >= 2).
-template <bool F16, int LA, bool MULTI, bool F32OUT, bool LUT>
-__global__ __launch_bounds__(kThreads, LUT ? 4 : TX_GEMV_WAVES_PER_EU) void gemv_kernel(GemvParams p) {
+// MERGE (one token): x is merged from the decode attention's chunk partials (merge_attention_x)
+// instead of read; its o projections have few row groups, so the register bound is relaxed for the
+// merge's per-chunk values.
+template <bool F16, int LA, bool MULTI, bool F32OUT, bool LUT, bool MERGE = false>
+__global__ __launch_bounds__(kThreads, LUT || MERGE ? 4 : TX_GEMV_WAVES_PER_EU) void gemv_kernel(GemvParams p) {
+  static_assert(!MERGE || (!MULTI && !LUT), "the attention merge feeds one token's staged x");
   static_assert(!LUT || LA >= 2, "LUT mode prefetches the palette rows of the next tile");
   extern __shared__ uint4 xs[];  // single token: x slice, 16 uint4 (128 bf16) per tile column
   __shared__ __attribute__((aligned(16))) PaletteTableStorage tables;
@@ -199,8 +257,13 @@ __global__ __launch_bounds__(kThreads, LUT ? 4 : TX_GEMV_WAVES_PER_EU) void gemv
   const int row = g * kTileRows + i;
   const float scale = p.scales[row];  // loaded with the tiles and x, not after the barrier
 
-  if constexpr (!MULTI) stage_x_lds(xs, x, p.K, c_begin * 16, nc * 16, wave, lane);
-  if constexpr (!LUT) copy_seed_tables(tables, wave, lane, kWaves);
+  if constexpr (MERGE) {
+    copy_seed_tables(tables, wave, lane, kWaves);  // in flight while the heads are merged
+    merge_attention_x(xs, p, c_begin, nc, wave, lane);
+  } else {
+    if constexpr (!MULTI) stage_x_lds(xs, x, p.K, c_begin * 16, nc * 16, wave, lane);
+    if constexpr (!LUT) copy_seed_tables(tables, wave, lane, kWaves);
+  }
   if constexpr (!MULTI || !LUT) __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): x and the tables have landed
   __syncthreads();
 
@@ -548,7 +611,7 @@ void launch_splitk_reduce(const GemvParams &p, hipStream_t stream) {
 constexpr int kFusedMaxColumns = 224;
 
 bool fused_eligible(const GemvParams &p) {
-  return p.fused && p.tokens == 1 && !p.lut && !p.force_partials && p.ks > 1 && p.ks <= kFusedMaxSplits &&
+  return p.fused && p.tokens == 1 && !p.lut && !p.force_partials && !p.attn && p.ks > 1 && p.ks <= kFusedMaxSplits &&
          p.CG <= kFusedMaxColumns;
 }
 
@@ -564,6 +627,12 @@ hipError_t launch_variant(const GemvParams &p, hipStream_t stream) {
   const int max_cols = (p.CG + p.ks - 1) / p.ks;
   const size_t lds = MULTI ? 0 : (size_t)x_stage_chunks(max_cols) * sizeof(uint4);
   dim3 grid(p.RG, p.ks, (p.tokens + 15) / 16);
+  if constexpr (!MULTI && !F16 && F32OUT) {
+    if (p.attn) {  // the caller checked: one token, force_partials, no LUT, K = heads * 128
+      hipLaunchKernelGGL((gemv_kernel<false, LA, false, true, false, true>), grid, dim3(kThreads), lds, stream, p);
+      return hipGetLastError();
+    }
+  }
   if (p.lut) {
     constexpr int kLutLA = LA < 2 ? 2 : LA;  // the palette-row prefetch needs a second tile in flight
     hipLaunchKernelGGL((gemv_kernel<F16, kLutLA, MULTI, F32OUT, true>), grid, dim3(kThreads), lds, stream, p);

@@ -22,7 +22,18 @@ struct GemvParams {
   int f16;                 // x, bias and y are fp16 (weights rounded to fp16) instead of bf16
   const float4 *lut;       // LUT mode: 255 x 255 x 8 fp32 palette table, or nullptr (defined palette)
   int fused;               // one token: every K split in one workgroup (gemv_fused_profitable)
+  // One token, K = heads * 128 (tile column j = attention head j): x is not read; each workgroup
+  // merges its heads' decode attention chunk partials (attn, attn_chunks chunks, attn_group query
+  // heads per KV head) into x itself, as the attention's merge kernel would. nullptr: x is read.
+  const float *attn;
+  int attn_chunks, attn_group;
 };
+
+// A row of the decode attention's chunk partials [kv_head][chunk][query head of the group]: the
+// chunk's unnormalised output o[128], then its score maximum m and sum of exponentials l.
+constexpr int kAttnRow = 130;
+// Chunks (of 64 positions) up to which a one-token GEMV merges the attention's partials itself.
+constexpr int kMergeMaxChunks = 16;
 
 // Whether a one-token GEMV of RG row groups, CG tile columns and ks K splits runs all its splits in
 // one workgroup per row group (no partials in memory, no reduce launch; bit-identical results):
@@ -145,6 +156,12 @@ hipError_t launch_decode_attention_split(const SplitSource &qkv, const int64_t *
                                          int64_t length, int heads, int kv_heads,
                                          uint16_t *k_cache, uint16_t *v_cache, int64_t max_ctx, float scale,
                                          float *partials, uint16_t *out, hipStream_t stream);
+// The same without the merge kernel: the chunk partials stay in `partials` for a one-token GEMV
+// with GemvParams::attn (the o projection), which merges them itself.
+hipError_t launch_decode_attention_split_partials(const SplitSource &qkv, const int64_t *position, const float *rope_row,
+                                         int64_t length, int heads, int kv_heads,
+                                         uint16_t *k_cache, uint16_t *v_cache, int64_t max_ctx, float scale,
+                                         float *partials, hipStream_t stream);
 // Causal self-attention of a prompt (queries and keys 0..tokens-1, keys and values from the
 // caches [kv_heads][max_ctx][128]); q and out bf16 rows of heads * 128 with the given strides.
 bool prefill_attention_supported(int heads, int kv_heads, int head_dim);

@@ -153,6 +153,34 @@ def decode_attention_split(qkv_handle: int, positions: torch.Tensor, rope_row: t
     return out
 
 
+def decode_attention_o_split(qkv_handle: int, o_handle: int, positions: torch.Tensor, rope_row: torch.Tensor,
+                             heads: int, kv_heads: int, head_dim: int, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                             length: int, scale: float, workspace: torch.Tensor) -> bool:
+    """:func:`decode_attention_split` then :func:`linear_split` of ``o_handle`` on its output, with
+    the attention's chunk merge done inside the o GEMV (one launch fewer, o's split-K partials
+    bitwise the same; read them with :func:`add_rmsnorm_split`). Returns False, with nothing
+    launched, where the merge does not fit the o GEMV (more than 16 chunks of 64 positions, too many
+    heads per o split, a LUT handle): then make the two calls."""
+    _expect(positions.dtype == torch.int64 and positions.is_contiguous() and positions.numel() == 1,
+            "positions must be int64 [1]")
+    _expect(rope_row.dtype == torch.float32 and rope_row.is_contiguous() and rope_row.numel() == 2 * head_dim,
+            "rope_row must be float32 [2 * head_dim]")
+    max_ctx = k_cache.shape[1]
+    for cache in (k_cache, v_cache):
+        _expect(cache.dtype == torch.bfloat16 and cache.is_contiguous() and tuple(cache.shape) == (kv_heads, max_ctx, head_dim),
+                "caches must be contiguous bf16 [kv_heads, max_context, head_dim]")
+    need = decode_attention_workspace_bytes(heads, length)
+    _expect(workspace.is_cuda and workspace.numel() * workspace.element_size() >= need, "decode attention workspace too small")
+    status = _lib.load().tx_decode_attention_o_split(qkv_handle, o_handle, _ptr(positions), _ptr(rope_row), int(length),
+                                                    heads, kv_heads, head_dim, _ptr(k_cache), _ptr(v_cache), max_ctx,
+                                                    float(scale), _ptr(workspace),
+                                                    workspace.numel() * workspace.element_size(), _stream(positions))
+    if status == _lib.TX_ERR_UNSUPPORTED:
+        return False
+    check(status)
+    return True
+
+
 def linear_split(handle: int, x: torch.Tensor) -> None:
     """One-token decode GEMV of ``handle`` (``x`` bf16 ``[K]``) whose output stays as split-K
     partials inside the handle, for :func:`add_rmsnorm_split` or :func:`rope_kv_cache_split`."""

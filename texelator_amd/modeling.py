@@ -201,6 +201,8 @@ class BC4Decoder:
         self.split_prefill = fused
         # greedy next token by this library's lm_head GEMV + argmax (else torch's linear + argmax)
         self.fused_head = fused and config.hidden % 128 == 0
+        # short caches: the attention's chunk merge inside the o GEMV (tx_decode_attention_o_split)
+        self.attention_in_o = fused
         # a prompt's causal attention with this library's kernel (else torch's flash attention)
         self.prompt_attention_kernel = fused and prompt_attention_supported(config)
         ext = extension()
@@ -458,15 +460,19 @@ class BC4Decoder:
 
     def _decode_split(self, h: torch.Tensor, x: torch.Tensor, positions: torch.Tensor, length: int,
                       scale: float) -> torch.Tensor:
-        """One token through every layer with the split-K consumers (eight kernels a layer)."""
+        """One token through every layer with the split-K consumers (eight kernels a layer; seven where
+        the attention's merge runs inside the o GEMV)."""
         c = self.config
         torch.index_select(self.rope_cs, 0, positions, out=self.rope_row)
         for index, layer in enumerate(self.layers):
             layers.linear_split(layer.handles["qkv"], x)
-            attn = layers.decode_attention_split(layer.handles["qkv"], positions, self.rope_row, c.heads, c.kv_heads,
-                                                 c.head_dim, self.k_cache[index], self.v_cache[index], length, scale,
-                                                 self.attention_workspace, out=self.attn_buffer)
-            layers.linear_split(layer.handles["o"], attn)
+            if not (self.attention_in_o and layers.decode_attention_o_split(
+                    layer.handles["qkv"], layer.handles["o"], positions, self.rope_row, c.heads, c.kv_heads, c.head_dim,
+                    self.k_cache[index], self.v_cache[index], length, scale, self.attention_workspace)):
+                attn = layers.decode_attention_split(layer.handles["qkv"], positions, self.rope_row, c.heads, c.kv_heads,
+                                                     c.head_dim, self.k_cache[index], self.v_cache[index], length, scale,
+                                                     self.attention_workspace, out=self.attn_buffer)
+                layers.linear_split(layer.handles["o"], attn)
             layers.add_rmsnorm_split(h, layer.handles["o"], layer.post_norm, c.rms_eps, out=x)
             layers.linear_split(layer.handles["down"], self._gate_up_swiglu(layer, x))
             following = self.layers[index + 1].input_norm if index + 1 < len(self.layers) else self.final_norm
@@ -537,6 +543,12 @@ class BC4Decoder:
         if length in self.graphs:
             return self.graphs[length]
         saved_token, saved_position = self.token.clone(), self.position.clone()
+        # The warm-up step runs for real: at the model's position, which after a decode that filled
+        # the cache is max_context, a row past the RoPE table (whose gather traps on it). It runs at
+        # the last row then, and the cache rows it writes are put back afterwards.
+        row = min(int(saved_position), self.max_context - 1)
+        self.position.fill_(row)
+        saved_rows = (self.k_cache[:, :, row].clone(), self.v_cache[:, :, row].clone())
         stream = torch.cuda.Stream(self.device)
         stream.wait_stream(torch.cuda.current_stream(self.device))
         with torch.cuda.stream(stream):
@@ -550,6 +562,8 @@ class BC4Decoder:
         self.graphs[length] = graph
         self.token.copy_(saved_token)
         self.position.copy_(saved_position)
+        self.k_cache[:, :, row] = saved_rows[0]
+        self.v_cache[:, :, row] = saved_rows[1]
         return graph
 
     @torch.inference_mode()
