@@ -98,6 +98,12 @@ __device__ __forceinline__ void stage_x_lds(uint4 *xs, const uint16_t *x, int K,
 // bitwise the merge kernel's output. Lane l produces dimensions l and l + 64 and writes them as
 // stage_x_lds would place them. Every load of a head (all its chunks' values, clamped to the last
 // chunk, and the lane's chunk statistics) goes out before the first wait.
+// A lane's float from the lane `CTRL` (a DPP control) names within its 16-lane row.
+template <int CTRL>
+__device__ __forceinline__ float row_dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
 __device__ __forceinline__ void merge_attention_x(uint4 *xs, const GemvParams &p, int c_begin, int nc, int wave,
                                                   int lane) {
   const int chunks = p.attn_chunks, group = p.attn_group;
@@ -116,19 +122,30 @@ __device__ __forceinline__ void merge_attention_x(uint4 *xs, const GemvParams &p
     }
     const float *srow = base + (uint32_t)min(lane, chunks - 1) * step;
     const float ms = srow[kAttnRow - 2], ls = srow[kAttnRow - 1];
+    // With at most 16 chunks only the first 16-lane row holds any: the 64-lane butterfly's xor-32
+    // and xor-16 steps add exact zeros there, and its xor-8, 4, 2, 1 steps are row rotations by 8
+    // and 4 (after the xor-8 step lanes i and i ^ 8 hold the same sum, so a rotation by 4 meets
+    // lane i ^ 4's value) and quad permutations -- the same sums in the same tree. The maximum is
+    // exact in any order.
     const float mv = lane < chunks ? ms : -INFINITY;
     float m = mv;
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    m = fmaxf(m, row_dpp<0x128>(m));  // row_ror:8
+    m = fmaxf(m, row_dpp<0x124>(m));  // row_ror:4
+    m = fmaxf(m, row_dpp<0x4E>(m));   // quad_perm [2,3,0,1]
+    m = fmaxf(m, row_dpp<0xB1>(m));   // quad_perm [1,0,3,2]
+    m = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(m)));
     const float w = mv == -INFINITY ? 0.f : expf(mv - m);
     float total = lane < chunks ? __builtin_fmaf(ls, w, 0.f) : 0.f;
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) total += __shfl_xor(total, off);
+    total += row_dpp<0x128>(total);
+    total += row_dpp<0x124>(total);
+    total += row_dpp<0x4E>(total);
+    total += row_dpp<0xB1>(total);
+    total = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(total)));
     float a0[4] = {0.f, 0.f, 0.f, 0.f}, a1[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int c = 0; c < kMergeMaxChunks; ++c) {
       if (c < chunks) {
-        const float wc = __shfl(w, c);
+        const float wc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), c));
         if (c < main_end) {
           a0[c & 3] = __builtin_fmaf(o0[c], wc, a0[c & 3]);
           a1[c & 3] = __builtin_fmaf(o1[c], wc, a1[c & 3]);
