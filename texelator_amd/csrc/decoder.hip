@@ -151,8 +151,7 @@ __global__ __launch_bounds__(kNormThreads) void add_rmsnorm_kernel(float *h, con
       ss += (v[u].x * v[u].x + v[u].y * v[u].y) + (v[u].z * v[u].z + v[u].w * v[u].w);
     }
   }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+  ss = wave_sum(ss);
   if ((threadIdx.x & 63) == 0) partial[threadIdx.x >> 6] = ss;
   __syncthreads();
   float total = 0.f;
@@ -428,16 +427,12 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(AttnInput in, uin
     // kept as bf16 hi + lo (hi + lo = p to 16 significant bits) for the PV product
     for (int g = wave; g < group; g += 4) {
       const float a = probs[g][lane];
-      float m = a;
-#pragma unroll
-      for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+      const float m = wave_max(a);
       const float pa = expf(a - m);
       const uint16_t hi = to_bf(pa);
       pb[0][g][lane] = hi;
       pb[1][g][lane] = to_bf(pa - bf(hi));
-      float l = pa;
-#pragma unroll
-      for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o);
+      const float l = wave_sum(pa);
       if (lane == 0) {
         stats[g][0] = m;
         stats[g][1] = l;
@@ -509,8 +504,7 @@ __global__ __launch_bounds__(128) void decode_attention_combine_kernel(const flo
   float m = -INFINITY;
 #pragma unroll
   for (int u = 0; u < kPerThread; ++u) m = dd + 128 * u < chunks ? fmaxf(m, mv[u]) : m;
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+  m = wave_max(m);
   if ((dd & 63) == 0) red[dd >> 6] = m;
   __syncthreads();
   m = fmaxf(red[0], red[1]);
@@ -525,8 +519,7 @@ __global__ __launch_bounds__(128) void decode_attention_combine_kernel(const flo
       total = __builtin_fmaf(lv[u], w, total);
     }
   }
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) total += __shfl_xor(total, off);
+  total = wave_sum(total);
   if ((dd & 63) == 0) red[dd >> 6] = total;
   __syncthreads();
   total = red[0] + red[1];
@@ -567,24 +560,6 @@ __global__ __launch_bounds__(128) void decode_attention_combine_kernel(const flo
 // rows never reach the sums.
 constexpr int kPromptQueries = 64;
 
-// Reductions over the 16 lanes of a DPP row (xor 1, xor 2, half-row mirror, row mirror): every
-// lane of the row ends with the same value.
-template <int CTRL>
-__device__ __forceinline__ float dpp_mov(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
-}
-__device__ __forceinline__ float row16_max(float v) {
-  v = fmaxf(v, dpp_mov<0xB1>(v));   // quad_perm [1,0,3,2]
-  v = fmaxf(v, dpp_mov<0x4E>(v));   // quad_perm [2,3,0,1]
-  v = fmaxf(v, dpp_mov<0x141>(v));  // row_half_mirror
-  return fmaxf(v, dpp_mov<0x140>(v));  // row_mirror
-}
-__device__ __forceinline__ float row16_sum(float v) {
-  v += dpp_mov<0xB1>(v);
-  v += dpp_mov<0x4E>(v);
-  v += dpp_mov<0x141>(v);
-  return v + dpp_mov<0x140>(v);
-}
 
 constexpr int kKeyTileBytes = kChunk * kKeyStrideU4 * 16;   // keys [key][128] bf16, padded rows
 constexpr int kValueTileBytes = kHeadDim * kChunk * 2;      // values [dim][key] bf16 (vt_index)

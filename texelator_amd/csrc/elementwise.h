@@ -22,6 +22,40 @@ __device__ __forceinline__ float half_bits_to_float(uint16_t v) {
 // Round to bf16, nearest-even.
 __device__ __forceinline__ uint16_t to_bf(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
 
+// Reductions over the 16 lanes of a DPP row (xor 1, xor 2, half-row mirror, row mirror): every
+// lane of the row ends with the same value.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp_mov<0xB1>(v));   // quad_perm [1,0,3,2]
+  v = fmaxf(v, dpp_mov<0x4E>(v));   // quad_perm [2,3,0,1]
+  v = fmaxf(v, dpp_mov<0x141>(v));  // row_half_mirror
+  return fmaxf(v, dpp_mov<0x140>(v));  // row_mirror
+}
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp_mov<0xB1>(v);
+  v += dpp_mov<0x4E>(v);
+  v += dpp_mov<0x141>(v);
+  return v + dpp_mov<0x140>(v);
+}
+__device__ __forceinline__ float lane_value(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+// Sum over the 64 lanes of a wave in one fixed tree: each 16-lane row by row16_sum, then the rows
+// as (r0 + r1) + (r2 + r3). Every lane gets the result; no LDS round trip. A wave whose rows 1-3
+// hold zeros gets row 0's sum exactly (adding +0 changes nothing for a sum of non-negative values).
+__device__ __forceinline__ float wave_sum(float v) {
+  v = row16_sum(v);
+  return (lane_value(v, 0) + lane_value(v, 16)) + (lane_value(v, 32) + lane_value(v, 48));
+}
+// Maximum over the 64 lanes of a wave (exact in any order).
+__device__ __forceinline__ float wave_max(float v) {
+  v = row16_max(v);
+  return fmaxf(fmaxf(lane_value(v, 0), lane_value(v, 16)), fmaxf(lane_value(v, 32), lane_value(v, 48)));
+}
+
 // SwiGLU of one pair in fp32: silu(g) * u.
 __device__ __forceinline__ float swiglu_value(float g, float u) { return g / (1.0f + expf(-g)) * u; }
 

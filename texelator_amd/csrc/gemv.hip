@@ -92,18 +92,14 @@ __device__ __forceinline__ void stage_x_lds(uint4 *xs, const uint16_t *x, int K,
 // x of a split whose tile columns are attention heads (GemvParams::attn): head c_begin + j (j <
 // nc, one wave per head at a time) merged from the decode attention's chunk partials, exactly as
 // decode_attention_combine_kernel merges a head: M = the chunks' maximum m_c, weights w_c =
-// exp(m_c - M) (0 for an empty chunk), total = the 64-lane butterfly sum of l_c * w_c (lane c holds
-// chunk c), four fma chains acc[c % 4] over the chunks below the last multiple of four and the rest
-// into acc[0], in chunk order, and x = bf16(((acc0 + acc1) + (acc2 + acc3)) / total) -- so x is
-// bitwise the merge kernel's output. Lane l produces dimensions l and l + 64 and writes them as
+// exp(m_c - M) (0 for an empty chunk), total = the sum of l_c * w_c in wave_sum's tree (lane c
+// holds chunk c; with at most 16 chunks only the first 16-lane row holds any, so that is row16_sum
+// of that row: the other rows add exact zeros), four fma chains acc[c % 4] over the chunks below
+// the last multiple of four and the rest into acc[0], in chunk order, and x = bf16(((acc0 + acc1) +
+// (acc2 + acc3)) / total) -- so x is bitwise the merge kernel's output. The weights reach every
+// lane by v_readlane: no LDS round trip. Lane l produces dimensions l and l + 64 and writes them as
 // stage_x_lds would place them. Every load of a head (all its chunks' values, clamped to the last
 // chunk, and the lane's chunk statistics) goes out before the first wait.
-// A lane's float from the lane `CTRL` (a DPP control) names within its 16-lane row.
-template <int CTRL>
-__device__ __forceinline__ float row_dpp(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
-}
-
 __device__ __forceinline__ void merge_attention_x(uint4 *xs, const GemvParams &p, int c_begin, int nc, int wave,
                                                   int lane) {
   const int chunks = p.attn_chunks, group = p.attn_group;
@@ -122,30 +118,15 @@ __device__ __forceinline__ void merge_attention_x(uint4 *xs, const GemvParams &p
     }
     const float *srow = base + (uint32_t)min(lane, chunks - 1) * step;
     const float ms = srow[kAttnRow - 2], ls = srow[kAttnRow - 1];
-    // With at most 16 chunks only the first 16-lane row holds any: the 64-lane butterfly's xor-32
-    // and xor-16 steps add exact zeros there, and its xor-8, 4, 2, 1 steps are row rotations by 8
-    // and 4 (after the xor-8 step lanes i and i ^ 8 hold the same sum, so a rotation by 4 meets
-    // lane i ^ 4's value) and quad permutations -- the same sums in the same tree. The maximum is
-    // exact in any order.
     const float mv = lane < chunks ? ms : -INFINITY;
-    float m = mv;
-    m = fmaxf(m, row_dpp<0x128>(m));  // row_ror:8
-    m = fmaxf(m, row_dpp<0x124>(m));  // row_ror:4
-    m = fmaxf(m, row_dpp<0x4E>(m));   // quad_perm [2,3,0,1]
-    m = fmaxf(m, row_dpp<0xB1>(m));   // quad_perm [1,0,3,2]
-    m = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(m)));
+    const float m = lane_value(row16_max(mv), 0);
     const float w = mv == -INFINITY ? 0.f : expf(mv - m);
-    float total = lane < chunks ? __builtin_fmaf(ls, w, 0.f) : 0.f;
-    total += row_dpp<0x128>(total);
-    total += row_dpp<0x124>(total);
-    total += row_dpp<0x4E>(total);
-    total += row_dpp<0xB1>(total);
-    total = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(total)));
+    const float total = lane_value(row16_sum(lane < chunks ? __builtin_fmaf(ls, w, 0.f) : 0.f), 0);
     float a0[4] = {0.f, 0.f, 0.f, 0.f}, a1[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int c = 0; c < kMergeMaxChunks; ++c) {
       if (c < chunks) {
-        const float wc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), c));
+        const float wc = lane_value(w, c);
         if (c < main_end) {
           a0[c & 3] = __builtin_fmaf(o0[c], wc, a0[c & 3]);
           a1[c & 3] = __builtin_fmaf(o1[c], wc, a1[c & 3]);
