@@ -298,6 +298,25 @@ int tx_linear_swiglu_prefill(uint64_t handle, const void *x, int64_t tokens, voi
 int tx_add_rmsnorm_split(float *residual, uint64_t delta_handle, const void *weight, float eps, void *out,
                          int64_t hidden, void *stream);
 
+/* tx_add_rmsnorm_split(residual, delta_handle, weight, eps, x) followed by tx_linear_split(handle,
+ * x), one launch fewer: every workgroup of the one-token GEMV computes the normalized x of its K
+ * range itself from residual_in and delta_handle's last tx_linear_split (the same sums and roundings
+ * as the separate kernel, so x and the GEMV's split partials are bitwise the same), and one of them
+ * writes residual_in + delta to residual_out, which must be another buffer than residual_in (the
+ * other workgroups still read it). handle K = delta_handle M = hidden; residuals fp32 [hidden],
+ * weight bf16 [hidden], all 16-byte aligned. TX_ERR_UNSUPPORTED, with nothing launched, for a LUT
+ * handle, hidden above 2048, a delta split more than 8 ways, or a grid whose workgroups would read
+ * more than 64 MiB in all (each reads the whole row and every split of the delta): then make the
+ * two calls. No counterpart
+ * in the reference (its decoder layers are Hugging Face modules). */
+int tx_linear_split_norm(uint64_t handle, const float *residual_in, float *residual_out, uint64_t delta_handle,
+                         const void *weight, float eps, void *stream);
+
+/* The same for tx_linear_swiglu: tx_add_rmsnorm_split followed by tx_linear_swiglu(handle, x, out),
+ * one launch fewer, with the requirements of both. */
+int tx_linear_swiglu_norm(uint64_t handle, const float *residual_in, float *residual_out, uint64_t delta_handle,
+                          const void *weight, float eps, void *out, void *stream);
+
 /* tx_rope_kv_cache for one token whose [q | k | v] row is the output of qkv_handle. */
 int tx_rope_kv_cache_split(uint64_t qkv_handle, const int64_t *positions, const float *cos_table,
                            const float *sin_table, int heads, int kv_heads, int head_dim, void *q_out,

@@ -510,13 +510,15 @@ def test_capture_after_the_cache_is_full(ext):
         model.close()
 
 
-@pytest.mark.parametrize("attention_in_o", [True, False])
-def test_split_decode_step_is_bit_identical(ext, tiny, attention_in_o):
+@pytest.mark.parametrize("attention_in_o,norm_in_gemv", [(True, True), (True, False), (False, True), (False, False)])
+def test_split_decode_step_is_bit_identical(ext, tiny, attention_in_o, norm_in_gemv):
     """A decode step through the split-K consumers equals the unsplit fused step, bit for bit, with
-    the attention's chunk merge inside the o GEMV and as its own kernel."""
+    the attention's chunk merge inside the o GEMV or as its own kernel, and the add+RMSNorms inside
+    the following GEMVs or as their own kernels."""
     ids = prefill.prompt_ids(tiny, 30, seed=6)
     try:
         tiny.attention_in_o = attention_in_o
+        tiny.norm_in_gemv = norm_in_gemv
         with torch.inference_mode():
             tiny.prefill(ids)
             token = ids[-1:]
@@ -528,8 +530,100 @@ def test_split_decode_step_is_bit_identical(ext, tiny, attention_in_o):
             kb = tiny.k_cache[:, :, 30].clone()
     finally:
         tiny.attention_in_o = True
+        tiny.norm_in_gemv = True
     assert torch.equal(a, b)
     assert torch.equal(ka, kb)
+
+
+def _norm_reference(ext, delta, hidden, g, bias_scale=1.0):
+    """Residual, weight and eps for a norm-consumer test, with delta's partials written."""
+    k = _hip_shape_k(ext, delta)
+    layers.linear_split(delta, (torch.randn(1, k, device="cuda", generator=g) * bias_scale).to(torch.bfloat16))
+    h0 = torch.randn(1, hidden, device="cuda", generator=g)
+    w = (1 + 0.1 * torch.randn(hidden, device="cuda", generator=g)).to(torch.bfloat16)
+    return h0, w, 1e-6
+
+
+def _hip_shape_k(ext, handle):
+    from texelator_amd import _hip
+    return _hip.shape(handle)[1]
+
+
+@pytest.mark.parametrize("hidden,dk,cm,bias", [(2048, 2048, 2560, True), (2048, 11008, 2048, False),
+                                               (256, 512, 1024, True), (1024, 4096, 1024, False)])
+def test_linear_split_norm_is_bit_identical(ext, hidden, dk, cm, bias):
+    """add_rmsnorm_split + linear_split == linear_split_norm, bit for bit: the updated residual and
+    the consumer's split partials (read back through add_rmsnorm_split), for producers split 1-8 ways
+    and consumers split 1-4 ways, twice in a row."""
+    delta = _random_handle(ext, hidden, dk, seed=hidden + dk, bias=bias)
+    consumer = _random_handle(ext, cm, hidden, seed=cm + 1, bias=bias)
+    try:
+        g = torch.Generator(device="cuda").manual_seed(hidden + cm)
+        h0, w, eps = _norm_reference(ext, delta, hidden, g)
+        w2 = (1 + 0.1 * torch.randn(cm, device="cuda", generator=g)).to(torch.bfloat16)
+        r0 = torch.randn(1, cm, device="cuda", generator=g)
+        h_want = h0.clone()
+        x = layers.add_rmsnorm_split(h_want, delta, w, eps, torch.empty(1, hidden, device="cuda", dtype=torch.bfloat16))
+        layers.linear_split(consumer, x)
+        r_want = r0.clone()
+        read_want = layers.add_rmsnorm_split(r_want, consumer, w2, eps, torch.empty(1, cm, device="cuda", dtype=torch.bfloat16))
+        for _ in range(2):
+            h_in, h_out = h0.clone(), torch.full_like(h0, float("nan"))
+            assert layers.linear_split_norm(consumer, h_in, h_out, delta, w, eps)
+            r_got = r0.clone()
+            read_got = layers.add_rmsnorm_split(r_got, consumer, w2, eps, torch.empty(1, cm, device="cuda", dtype=torch.bfloat16))
+            assert torch.equal(h_out, h_want) and torch.equal(h_in, h0)
+            assert torch.equal(r_got, r_want) and torch.equal(read_got, read_want)
+    finally:
+        ext.free(delta)
+        ext.free(consumer)
+
+
+@pytest.mark.parametrize("hidden,dk,inter,bias", [(2048, 2048, 11008, True), (256, 512, 512, False),
+                                                  (1024, 4096, 8192, True)])
+def test_linear_swiglu_norm_is_bit_identical(ext, hidden, dk, inter, bias):
+    """add_rmsnorm_split + linear_swiglu == linear_swiglu_norm, bit for bit (the activations and the
+    updated residual), twice in a row."""
+    delta = _random_handle(ext, hidden, dk, seed=hidden + dk + 3, bias=bias)
+    gate_up = _random_handle(ext, 2 * inter, hidden, seed=inter, bias=bias)
+    try:
+        assert ext.gemv_plan(gate_up) == (1, False)
+        g = torch.Generator(device="cuda").manual_seed(inter)
+        h0, w, eps = _norm_reference(ext, delta, hidden, g)
+        h_want = h0.clone()
+        x = layers.add_rmsnorm_split(h_want, delta, w, eps, torch.empty(1, hidden, device="cuda", dtype=torch.bfloat16))
+        want = layers.linear_swiglu(gate_up, x).clone()
+        for _ in range(2):
+            h_in, h_out = h0.clone(), torch.full_like(h0, float("nan"))
+            got = torch.full_like(want, float("nan"))
+            assert layers.linear_swiglu_norm(gate_up, h_in, h_out, delta, w, eps, got)
+            assert torch.equal(got, want) and torch.equal(h_out, h_want) and torch.equal(h_in, h0)
+    finally:
+        ext.free(delta)
+        ext.free(gate_up)
+
+
+def test_linear_norm_refusals(ext):
+    """The same buffer for both residuals is refused; a 27B-class gate|up GEMV (hidden 5120, above
+    the 2048 the prologue holds) returns False and launches nothing."""
+    from texelator_amd._lib import TexelatorError
+
+    delta = _random_handle(ext, 5120, 5120, seed=1)
+    gate_up = _random_handle(ext, 2 * 27648, 5120, seed=2)
+    try:
+        layers.linear_split(delta, torch.ones(1, 5120, device="cuda", dtype=torch.bfloat16))
+        h = torch.zeros(1, 5120, device="cuda")
+        w = torch.ones(5120, device="cuda", dtype=torch.bfloat16)
+        with pytest.raises(TexelatorError, match="another buffer"):
+            layers.linear_split_norm(delta, h, h, delta, w, 1e-6)
+        out = torch.zeros(1, 27648, device="cuda", dtype=torch.bfloat16)
+        h_out = torch.zeros_like(h)
+        assert not layers.linear_swiglu_norm(gate_up, h, h_out, delta, w, 1e-6, out)
+        torch.cuda.synchronize()
+        assert not out.any() and not h_out.any()
+    finally:
+        ext.free(delta)
+        ext.free(gate_up)
 
 
 @pytest.mark.parametrize("heads,kv,k,position,length,bias", [

@@ -366,6 +366,42 @@ int scratch_address(int device, float **out) {
   return TX_OK;
 }
 
+// Bytes the workgroups of a one-token GEMV of `h` read in all to normalize their x themselves (each
+// reads the whole residual, every split of the producer's partials, its bias and the weight), up to
+// which tx_linear_split_norm and tx_linear_swiglu_norm run.
+constexpr int64_t kNormReadBudget = 64ll << 20;
+
+// GemvParams::norm_* for tx_linear_split_norm and tx_linear_swiglu_norm (`workgroups`: the GEMV's);
+// TX_OK, or the failure status with nothing launched.
+int set_norm_source(tx::GemvParams &p, const Handle *h, const Handle *d, const float *residual_in, float *residual_out,
+                    const void *weight, float eps, int64_t workgroups, const char *who) {
+  if (!d) return fail(TX_ERR_INVALID, std::string(who) + ": null delta handle");
+  if (!residual_in || !residual_out || !weight) return fail(TX_ERR_INVALID, std::string(who) + ": null pointer");
+  if (residual_in == residual_out)
+    return fail(TX_ERR_INVALID, std::string(who) + ": the updated residual needs its own buffer (the GEMV's "
+                                                   "workgroups read residual_in while one writes residual_out)");
+  if (reinterpret_cast<uintptr_t>(residual_in) % 16 || reinterpret_cast<uintptr_t>(residual_out) % 16 ||
+      reinterpret_cast<uintptr_t>(weight) % 16)
+    return fail(TX_ERR_INVALID, std::string(who) + ": residuals and weight must be 16-byte aligned");
+  if (d->M != h->K) return fail(TX_ERR_INVALID, std::string(who) + ": the delta handle's output size must equal K");
+  if (d->device != h->device) return fail(TX_ERR_INVALID, std::string(who) + ": handles on different devices");
+  if (d->bias && d->bias_dtype != TX_DTYPE_BF16) return fail(TX_ERR_INVALID, std::string(who) + ": the delta bias must be BF16");
+  const int64_t reads = workgroups * (int64_t)h->K * (4 * (d->gemv_splits + 1) + 4);
+  if (h->lut || h->K > tx::kNormMaxHidden || d->gemv_splits > tx::kNormMaxSplits || reads > kNormReadBudget)
+    return fail(TX_ERR_UNSUPPORTED, std::string(who) + ": the normalization does not fit the GEMV (LUT handle, "
+                                                       "K above 2048, more than 8 delta splits, or too many "
+                                                       "workgroups reading the whole row); use "
+                                                       "tx_add_rmsnorm_split and the plain call");
+  p.norm_h = residual_in;
+  p.norm_h_out = residual_out;
+  p.norm_partials = d->partials;
+  p.norm_bias = static_cast<const uint16_t *>(d->bias);
+  p.norm_weight = static_cast<const uint16_t *>(weight);
+  p.norm_eps = eps;
+  p.norm_ks = d->gemv_splits;
+  p.norm_Mp = d->Mp;
+  return TX_OK;
+}
 }  // namespace
 
 extern "C" {
@@ -839,6 +875,62 @@ int tx_add_rmsnorm_split(float *residual, uint64_t delta_handle, const void *wei
   DeviceGuard guard(h->device);
   TX_HIP(tx::launch_add_rmsnorm_split(residual, split_source(h), static_cast<const uint16_t *>(weight), eps,
                                       static_cast<uint16_t *>(out), 1, (int)hidden, reinterpret_cast<hipStream_t>(stream)));
+  return TX_OK;
+}
+
+int tx_linear_split_norm(uint64_t value, const float *residual_in, float *residual_out, uint64_t delta_handle,
+                         const void *weight, float eps, void *stream) {
+  g_last_error.clear();
+  Handle *h = as_handle(value);
+  if (!h) return fail(TX_ERR_INVALID, "null Texelator handle");
+  if (h->bias && h->bias_dtype != TX_DTYPE_BF16) return fail(TX_ERR_INVALID, "linear_split_norm: the bias must be BF16");
+  tx::GemvParams p{};
+  p.tiles = h->tiles;
+  p.scales = h->scales;
+  p.M = h->M;
+  p.K = h->K;
+  p.Mp = h->Mp;
+  p.RG = h->RG;
+  p.CG = h->CG;
+  p.tokens = 1;
+  p.ks = h->gemv_splits;
+  p.partials = h->partials;
+  p.force_partials = 1;
+  const int status = set_norm_source(p, h, as_handle(delta_handle), residual_in, residual_out, weight, eps,
+                                     (int64_t)h->RG * h->gemv_splits, "linear_split_norm");
+  if (status != TX_OK) return status;
+  DeviceGuard guard(h->device);
+  TX_HIP(tx::launch_gemv(p, h->lookahead, true, reinterpret_cast<hipStream_t>(stream)));
+  return TX_OK;
+}
+
+int tx_linear_swiglu_norm(uint64_t value, const float *residual_in, float *residual_out, uint64_t delta_handle,
+                          const void *weight, float eps, void *out, void *stream) {
+  g_last_error.clear();
+  Handle *h = as_handle(value);
+  if (!h) return fail(TX_ERR_INVALID, "null Texelator handle");
+  if (!out) return fail(TX_ERR_INVALID, "linear_swiglu_norm: null output pointer");
+  if (h->M % 32 != 0) return fail(TX_ERR_INVALID, "linear_swiglu_norm: the handle must hold [gate | up] with 16-row aligned halves");
+  if (h->gemv_splits != 1 || h->CG > tx::kGemvMaxLdsColumns || h->lut)
+    return fail(TX_ERR_UNSUPPORTED, "linear_swiglu_norm: needs a one-split, non-LUT handle with K <= 16384");
+  if (h->bias && h->bias_dtype != TX_DTYPE_BF16) return fail(TX_ERR_INVALID, "linear_swiglu_norm: the bias must be BF16");
+  tx::GemvParams p{};
+  p.tiles = h->tiles;
+  p.scales = h->scales;
+  p.bias = h->bias;
+  p.y = out;
+  p.M = h->M;
+  p.K = h->K;
+  p.Mp = h->Mp;
+  p.RG = h->RG;
+  p.CG = h->CG;
+  p.ks = 1;
+  p.tokens = 1;
+  const int status = set_norm_source(p, h, as_handle(delta_handle), residual_in, residual_out, weight, eps,
+                                     (int64_t)h->RG / 2, "linear_swiglu_norm");
+  if (status != TX_OK) return status;
+  DeviceGuard guard(h->device);
+  TX_HIP(tx::launch_gemv_swiglu(p, h->lookahead, reinterpret_cast<hipStream_t>(stream)));
   return TX_OK;
 }
 

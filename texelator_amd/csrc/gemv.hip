@@ -141,6 +141,100 @@ __device__ __forceinline__ void merge_attention_x(uint4 *xs, const GemvParams &p
   }
 }
 
+// x of a one-token GEMV (GemvParams::norm_h) as add_rmsnorm_kernel<true, *> writes it, for hidden
+// = p.K <= 2048 and at most 8 producer splits. That kernel's thread t handles the group of four
+// columns i = t (t < 512 here); this lane stands for its threads t = 256 j + tid (j < 4; only j < 2
+// hold a group). Per group: delta = bf16(partials summed in split order + bias), v = h + delta,
+// the sum of squares (x^2 + y^2) + (z^2 + w^2); each of that kernel's 16 waves summed by wave_sum
+// (its wave 4j + w is this wave's j-th sum; j >= 2 sum zeros) and the 16 added in order from zero;
+// inv = rsqrt(total / hidden + eps); x = bf16(weight * bf16(v * inv)). So x and the updated
+// residual are bitwise that kernel's. Every load (the residual, all splits clamped to the last,
+// the bias and the weight of both groups) goes out before the first wait. Only the x of the
+// workgroup's tile columns [c_begin, c_begin + nc) is written to xs (where stage_x_lds puts it);
+// `writer` writes every updated group to norm_h_out.
+constexpr int kNormStand = 1024 / kThreads;  // add_rmsnorm threads this lane stands for
+constexpr int kNormSlots = 2;                 // of which hold a group (hidden <= 2048)
+__device__ __forceinline__ void norm_x_lds(uint4 *xs, float *wave_sums, const GemvParams &p, int c_begin, int nc,
+                                           int wave, int lane, bool writer) {
+  const int hidden = p.K, groups = hidden / 4, ks = p.norm_ks;
+  const int tid = wave * 64 + lane;
+  const float4 *hr = reinterpret_cast<const float4 *>(p.norm_h);
+  const float4 *pp = reinterpret_cast<const float4 *>(p.norm_partials);
+  const int step = p.norm_Mp / 4;  // float4 between splits (one token)
+  const uint2 *br = reinterpret_cast<const uint2 *>(p.norm_bias ? p.norm_bias : p.norm_weight);
+  const uint2 *wr = reinterpret_cast<const uint2 *>(p.norm_weight);
+  float4 hv[kNormSlots], q[kNormSlots][kNormMaxSplits];
+  uint2 bv[kNormSlots], wv[kNormSlots];
+#pragma unroll
+  for (int j = 0; j < kNormSlots; ++j) {
+    const int ic = min(j * kThreads + tid, groups - 1);
+    hv[j] = hr[ic];
+#pragma unroll
+    for (int k = 0; k < kNormMaxSplits; ++k) q[j][k] = pp[min(k, ks - 1) * step + ic];
+    bv[j] = br[ic];
+    wv[j] = wr[ic];
+  }
+  __builtin_amdgcn_sched_barrier(0);  // every load issued before the first add
+  float4 v[kNormSlots];
+  float ss[kNormStand] = {};
+  float4 *ho = reinterpret_cast<float4 *>(p.norm_h_out);
+#pragma unroll
+  for (int j = 0; j < kNormSlots; ++j) {
+    const int i = j * kThreads + tid;
+    float4 acc = q[j][0];
+#pragma unroll
+    for (int k = 1; k < kNormMaxSplits; ++k) {
+      if (k < ks) {
+        acc.x += q[j][k].x;
+        acc.y += q[j][k].y;
+        acc.z += q[j][k].z;
+        acc.w += q[j][k].w;
+      }
+    }
+    if (p.norm_bias) {
+      acc.x += bf((uint16_t)(bv[j].x & 0xFFFFu));
+      acc.y += bf((uint16_t)(bv[j].x >> 16));
+      acc.z += bf((uint16_t)(bv[j].y & 0xFFFFu));
+      acc.w += bf((uint16_t)(bv[j].y >> 16));
+    }
+    float4 h = hv[j];
+    h.x += bf(to_bf(acc.x));
+    h.y += bf(to_bf(acc.y));
+    h.z += bf(to_bf(acc.z));
+    h.w += bf(to_bf(acc.w));
+    v[j] = h;
+    if (i < groups) {
+      ss[j] = (h.x * h.x + h.y * h.y) + (h.z * h.z + h.w * h.w);
+      if (writer) ho[i] = h;
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < kNormStand; ++j) {
+    const float s = wave_sum(ss[j]);
+    if (lane == 0) wave_sums[j * kWaves + wave] = s;
+  }
+  __syncthreads();
+  float total = 0.f;
+#pragma unroll
+  for (int w = 0; w < kNormStand * kWaves; ++w) total += wave_sums[w];
+  const float inv = rsqrtf(total / (float)hidden + p.norm_eps);
+  uint2 *xo = reinterpret_cast<uint2 *>(xs);
+  const int g_begin = c_begin * (kTileK / 4), g_end = (c_begin + nc) * (kTileK / 4);
+#pragma unroll
+  for (int j = 0; j < kNormSlots; ++j) {
+    const int i = j * kThreads + tid;
+    if (i < groups && i >= g_begin && i < g_end) {
+      const float4 h = v[j];
+      const uint2 w = wv[j];
+      const float n0 = bf(to_bf(h.x * inv)), n1 = bf(to_bf(h.y * inv)), n2 = bf(to_bf(h.z * inv)),
+                  n3 = bf(to_bf(h.w * inv));
+      xo[i - g_begin] = make_uint2(
+          (uint32_t)to_bf(bf((uint16_t)(w.x & 0xFFFFu)) * n0) | ((uint32_t)to_bf(bf((uint16_t)(w.x >> 16)) * n1) << 16),
+          (uint32_t)to_bf(bf((uint16_t)(w.y & 0xFFFFu)) * n2) | ((uint32_t)to_bf(bf((uint16_t)(w.y >> 16)) * n3) << 16));
+    }
+  }
+}
+
 // One tile for one lane: decode both blocks and accumulate 4 MFMAs (block 0 into acc0, block 1
 // into acc1; the two are added at the end in a fixed order).
 template <bool F16>
@@ -206,12 +300,15 @@ __device__ __forceinline__ void progress_priority(int remaining, int total) {
 // relative per weight).
 // LUT: the palette of every block is read from a 255 x 255 x 8 table (p.lut) instead of being
 // computed; the rows of tile j+1 are fetched while tile j is decoded (needs LA >= 2).
-// MERGE (one token): x is merged from the decode attention's chunk partials (merge_attention_x)
-// instead of read; its o projections have few row groups, so the register bound is relaxed for the
-// merge's per-chunk values.
-template <bool F16, int LA, bool MULTI, bool F32OUT, bool LUT, bool MERGE = false>
-__global__ __launch_bounds__(kThreads, LUT || MERGE ? 4 : TX_GEMV_WAVES_PER_EU) void gemv_kernel(GemvParams p) {
-  static_assert(!MERGE || (!MULTI && !LUT), "the attention merge feeds one token's staged x");
+// Where a one-token GEMV's x comes from: read (staged from p.x), merged from the decode attention's
+// chunk partials (merge_attention_x), or normalized from the residual and a producer's partials
+// (norm_x_lds). The last two run on grids of few row groups, so their register bound is relaxed.
+enum XSource : int { kXRead = 0, kXMerge = 1, kXNorm = 2 };
+
+template <bool F16, int LA, bool MULTI, bool F32OUT, bool LUT, int XSRC = kXRead>
+__global__ __launch_bounds__(kThreads, LUT || XSRC != kXRead ? 4 : TX_GEMV_WAVES_PER_EU) void gemv_kernel(GemvParams p) {
+  static_assert(XSRC == kXRead || (!MULTI && !LUT), "a merged or normalized x feeds one token's staged x");
+  constexpr bool MERGE = XSRC == kXMerge;
   static_assert(!LUT || LA >= 2, "LUT mode prefetches the palette rows of the next tile");
   extern __shared__ uint4 xs[];  // single token: x slice, 16 uint4 (128 bf16) per tile column
   __shared__ __attribute__((aligned(16))) PaletteTableStorage tables;
@@ -258,6 +355,10 @@ __global__ __launch_bounds__(kThreads, LUT || MERGE ? 4 : TX_GEMV_WAVES_PER_EU) 
   if constexpr (MERGE) {
     copy_seed_tables(tables, wave, lane, kWaves);  // in flight while the heads are merged
     merge_attention_x(xs, p, c_begin, nc, wave, lane);
+  } else if constexpr (XSRC == kXNorm) {
+    __shared__ float norm_sums[kNormStand * kWaves];
+    copy_seed_tables(tables, wave, lane, kWaves);  // in flight while x is normalized
+    norm_x_lds(xs, norm_sums, p, c_begin, nc, wave, lane, blockIdx.x == 0 && blockIdx.y == 0);
   } else {
     if constexpr (!MULTI) stage_x_lds(xs, x, p.K, c_begin * 16, nc * 16, wave, lane);
     if constexpr (!LUT) copy_seed_tables(tables, wave, lane, kWaves);
@@ -473,8 +574,9 @@ __global__ __launch_bounds__(kThreads * kFusedMaxSplits, TX_GEMV_WAVES_PER_EU) v
 // group g + RG/2 with the same four-wave K split, tile order and MFMA chains as gemv_kernel, so
 // each of the two row groups' sums is bit-identical to the plain GEMV's. Two rings of LA + 1 tiles
 // are in flight, so the occupancy bound falls with LA (no spills).
-template <int LA>
-__global__ __launch_bounds__(kThreads, LA == 1 ? 6 : (LA == 2 ? 5 : 4)) void gemv_swiglu_kernel(GemvParams p) {
+// NORM: x computed by norm_x_lds (GemvParams::norm_h) instead of read.
+template <int LA, bool NORM = false>
+__global__ __launch_bounds__(kThreads, NORM ? 4 : (LA == 1 ? 6 : (LA == 2 ? 5 : 4))) void gemv_swiglu_kernel(GemvParams p) {
   extern __shared__ uint4 xs[];
   __shared__ __attribute__((aligned(16))) PaletteTableStorage tables;
   __shared__ float red[2][kWaves][16];  // [gate|up][wave][row]
@@ -504,8 +606,14 @@ __global__ __launch_bounds__(kThreads, LA == 1 ? 6 : (LA == 2 ? 5 : 4)) void gem
   const int kg = lane >> 4;
   const float scale_g = p.scales[g * kTileRows + i];  // loaded with the tiles and x
   const float scale_u = p.scales[(g + half) * kTileRows + i];
-  stage_x_lds(xs, x, p.K, 0, nc * 16, wave, lane);
-  copy_seed_tables(tables, wave, lane, kWaves);
+  if constexpr (NORM) {
+    __shared__ float norm_sums[kNormStand * kWaves];
+    copy_seed_tables(tables, wave, lane, kWaves);  // in flight while x is normalized
+    norm_x_lds(xs, norm_sums, p, 0, nc, wave, lane, blockIdx.x == 0);
+  } else {
+    stage_x_lds(xs, x, p.K, 0, nc * 16, wave, lane);
+    copy_seed_tables(tables, wave, lane, kWaves);
+  }
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): x and the tables have landed
   __syncthreads();
 
@@ -609,7 +717,7 @@ void launch_splitk_reduce(const GemvParams &p, hipStream_t stream) {
 constexpr int kFusedMaxColumns = 224;
 
 bool fused_eligible(const GemvParams &p) {
-  return p.fused && p.tokens == 1 && !p.lut && !p.force_partials && !p.attn && p.ks > 1 && p.ks <= kFusedMaxSplits &&
+  return p.fused && p.tokens == 1 && !p.lut && !p.force_partials && !p.attn && !p.norm_h && p.ks > 1 && p.ks <= kFusedMaxSplits &&
          p.CG <= kFusedMaxColumns;
 }
 
@@ -627,7 +735,11 @@ hipError_t launch_variant(const GemvParams &p, hipStream_t stream) {
   dim3 grid(p.RG, p.ks, (p.tokens + 15) / 16);
   if constexpr (!MULTI && !F16 && F32OUT) {
     if (p.attn) {  // the caller checked: one token, force_partials, no LUT, K = heads * 128
-      hipLaunchKernelGGL((gemv_kernel<false, LA, false, true, false, true>), grid, dim3(kThreads), lds, stream, p);
+      hipLaunchKernelGGL((gemv_kernel<false, LA, false, true, false, kXMerge>), grid, dim3(kThreads), lds, stream, p);
+      return hipGetLastError();
+    }
+    if (p.norm_h) {  // the caller checked: one token, force_partials, no LUT, K <= 8192
+      hipLaunchKernelGGL((gemv_kernel<false, LA, false, true, false, kXNorm>), grid, dim3(kThreads), lds, stream, p);
       return hipGetLastError();
     }
   }
@@ -660,6 +772,14 @@ hipError_t launch_la(const GemvParams &p, bool f32_out, hipStream_t stream) {
 hipError_t launch_gemv_swiglu(const GemvParams &p, int lookahead, hipStream_t stream) {
   const size_t lds = (size_t)x_stage_chunks(p.CG) * sizeof(uint4);
   const dim3 grid(p.RG / 2);
+  if (p.norm_h) {
+    switch (lookahead) {
+      case 1: hipLaunchKernelGGL((gemv_swiglu_kernel<1, true>), grid, dim3(kThreads), lds, stream, p); break;
+      case 2: hipLaunchKernelGGL((gemv_swiglu_kernel<2, true>), grid, dim3(kThreads), lds, stream, p); break;
+      default: hipLaunchKernelGGL((gemv_swiglu_kernel<4, true>), grid, dim3(kThreads), lds, stream, p); break;
+    }
+    return hipGetLastError();
+  }
   switch (lookahead) {
     case 1: hipLaunchKernelGGL(gemv_swiglu_kernel<1>, grid, dim3(kThreads), lds, stream, p); break;
     case 2: hipLaunchKernelGGL(gemv_swiglu_kernel<2>, grid, dim3(kThreads), lds, stream, p); break;

@@ -27,7 +27,25 @@ struct GemvParams {
   // heads per KV head) into x itself, as the attention's merge kernel would. nullptr: x is read.
   const float *attn;
   int attn_chunks, attn_group;
+  // One token, K = hidden <= 2048, at most 8 producer splits: x is not read either; every workgroup
+  // computes it as
+  // add_rmsnorm_kernel<true> would from the residual norm_h and a producer GEMV's split partials
+  // (norm_ks splits, row stride norm_Mp, bias norm_bias or nullptr), with the RMSNorm weight
+  // norm_weight; workgroup 0 writes the updated residual to norm_h_out (not norm_h: the other
+  // workgroups still read it). nullptr: x is read (or merged).
+  const float *norm_h;
+  float *norm_h_out;
+  const float *norm_partials;
+  const uint16_t *norm_bias;
+  const uint16_t *norm_weight;
+  float norm_eps;
+  int norm_ks, norm_Mp;
 };
+
+// Hidden sizes and producer splits up to which a one-token GEMV computes the add+RMSNorm of its
+// input itself.
+constexpr int kNormMaxHidden = 2048;
+constexpr int kNormMaxSplits = 8;
 
 // A row of the decode attention's chunk partials [kv_head][chunk][query head of the group]: the
 // chunk's unnormalised output o[128], then its score maximum m and sum of exponentials l.

@@ -205,6 +205,48 @@ def linear_swiglu(handle: int, x: torch.Tensor, out: torch.Tensor | None = None)
     return out
 
 
+def _norm_args(residual_in: torch.Tensor, residual_out: torch.Tensor, weight: torch.Tensor, k: int) -> None:
+    for name, t in (("residual_in", residual_in), ("residual_out", residual_out)):
+        _expect(t.is_cuda and t.dtype == torch.float32 and t.is_contiguous() and t.numel() == k and t.data_ptr() % 16 == 0,
+                f"{name} must be a contiguous, 16-byte aligned CUDA float32 row of K values")
+    _expect(residual_in.data_ptr() != residual_out.data_ptr(), "residual_out must be another buffer than residual_in")
+    _expect(weight.dtype == torch.bfloat16 and weight.is_contiguous() and weight.numel() == k and weight.data_ptr() % 16 == 0,
+            "weight must be a contiguous, 16-byte aligned bf16 [K]")
+
+
+def linear_split_norm(handle: int, residual_in: torch.Tensor, residual_out: torch.Tensor, delta_handle: int,
+                      weight: torch.Tensor, eps: float) -> bool:
+    """:func:`add_rmsnorm_split` of ``residual_in`` and ``delta_handle``'s last :func:`linear_split`,
+    then :func:`linear_split` of ``handle`` on the result, in one launch: the GEMV's workgroups
+    normalize their x themselves (bitwise the same partials) and the updated residual goes to
+    ``residual_out``. Returns False, with nothing launched, where that does not fit the GEMV (K
+    above 2048, a delta split more than 8 ways, a LUT handle, or too many workgroups); then make the
+    two calls."""
+    _norm_args(residual_in, residual_out, weight, _hip_shape(handle)[1])
+    status = _lib.load().tx_linear_split_norm(handle, _ptr(residual_in), _ptr(residual_out), delta_handle, _ptr(weight),
+                                             float(eps), _stream(residual_in))
+    if status == _lib.TX_ERR_UNSUPPORTED:
+        return False
+    check(status)
+    return True
+
+
+def linear_swiglu_norm(handle: int, residual_in: torch.Tensor, residual_out: torch.Tensor, delta_handle: int,
+                       weight: torch.Tensor, eps: float, out: torch.Tensor) -> bool:
+    """:func:`linear_split_norm` for :func:`linear_swiglu`: the add+RMSNorm of the residual and
+    ``delta_handle``'s partials, then the gate|up GEMV with its SwiGLU epilogue into ``out``, in one
+    launch; False, with nothing launched, where that does not fit."""
+    m, k = _hip_shape(handle)
+    _norm_args(residual_in, residual_out, weight, k)
+    _expect(out.dtype == torch.bfloat16 and out.is_contiguous() and out.numel() == m // 2, "bad output")
+    status = _lib.load().tx_linear_swiglu_norm(handle, _ptr(residual_in), _ptr(residual_out), delta_handle, _ptr(weight),
+                                              float(eps), _ptr(out), _stream(residual_in))
+    if status == _lib.TX_ERR_UNSUPPORTED:
+        return False
+    check(status)
+    return True
+
+
 def linear_swiglu_prefill(handle: int, x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
     """``swiglu(linear(handle, x))`` for a prefill-sized ``x`` [tokens, K] of a merged ``[gate | up]``
     handle, in one GEMM whose epilogue applies SwiGLU (bit-identical to the two calls). Raises

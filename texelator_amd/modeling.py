@@ -203,6 +203,8 @@ class BC4Decoder:
         self.fused_head = fused and config.hidden % 128 == 0
         # short caches: the attention's chunk merge inside the o GEMV (tx_decode_attention_o_split)
         self.attention_in_o = fused
+        # the add+RMSNorms inside the following GEMV where it fits (tx_linear_swiglu_norm, _split_norm)
+        self.norm_in_gemv = fused
         # a prompt's causal attention with this library's kernel (else torch's flash attention)
         self.prompt_attention_kernel = fused and prompt_attention_supported(config)
         ext = extension()
@@ -461,11 +463,16 @@ class BC4Decoder:
     def _decode_split(self, h: torch.Tensor, x: torch.Tensor, positions: torch.Tensor, length: int,
                       scale: float) -> torch.Tensor:
         """One token through every layer with the split-K consumers (eight kernels a layer; seven where
-        the attention's merge runs inside the o GEMV)."""
+        the attention's merge runs inside the o GEMV, five where the two add+RMSNorms also run inside
+        the gate|up and the next q|k|v GEMVs, whose updated residual then alternates between h and a
+        second buffer)."""
         c = self.config
         torch.index_select(self.rope_cs, 0, positions, out=self.rope_row)
+        other = torch.empty_like(h) if self.norm_in_gemv else None
+        qkv_done = False
         for index, layer in enumerate(self.layers):
-            layers.linear_split(layer.handles["qkv"], x)
+            if not qkv_done:
+                layers.linear_split(layer.handles["qkv"], x)
             if not (self.attention_in_o and layers.decode_attention_o_split(
                     layer.handles["qkv"], layer.handles["o"], positions, self.rope_row, c.heads, c.kv_heads, c.head_dim,
                     self.k_cache[index], self.v_cache[index], length, scale, self.attention_workspace)):
@@ -473,19 +480,41 @@ class BC4Decoder:
                                                      c.head_dim, self.k_cache[index], self.v_cache[index], length, scale,
                                                      self.attention_workspace, out=self.attn_buffer)
                 layers.linear_split(layer.handles["o"], attn)
-            layers.add_rmsnorm_split(h, layer.handles["o"], layer.post_norm, c.rms_eps, out=x)
-            layers.linear_split(layer.handles["down"], self._gate_up_swiglu(layer, x))
-            following = self.layers[index + 1].input_norm if index + 1 < len(self.layers) else self.final_norm
-            layers.add_rmsnorm_split(h, layer.handles["down"], following, c.rms_eps, out=x)
+            gate_up = layer.handles["gate_up"]
+            if (self.norm_in_gemv and self._gate_up_unsplit(layer)
+                    and layers.linear_swiglu_norm(gate_up, h, other, layer.handles["o"], layer.post_norm, c.rms_eps,
+                                                  self.act_buffer)):
+                h, other = other, h
+                act = self.act_buffer
+            else:
+                layers.add_rmsnorm_split(h, layer.handles["o"], layer.post_norm, c.rms_eps, out=x)
+                act = self._gate_up_swiglu(layer, x)
+            layers.linear_split(layer.handles["down"], act)
+            qkv_done = False
+            if index + 1 < len(self.layers):
+                following = self.layers[index + 1]
+                if self.norm_in_gemv and layers.linear_split_norm(following.handles["qkv"], h, other,
+                                                                  layer.handles["down"], following.input_norm,
+                                                                  c.rms_eps):
+                    h, other = other, h
+                    qkv_done = True
+                    continue
+                layers.add_rmsnorm_split(h, layer.handles["down"], following.input_norm, c.rms_eps, out=x)
+            else:
+                layers.add_rmsnorm_split(h, layer.handles["down"], self.final_norm, c.rms_eps, out=x)
         return x
+
+    def _gate_up_unsplit(self, layer: _Layer) -> bool:
+        """Whether the merged gate|up GEMV of one token runs unsplit (its SwiGLU epilogue applies)."""
+        splits, lut = extension().gemv_plan(layer.handles["gate_up"])
+        return splits == 1 and not lut and self.config.intermediate % 16 == 0
 
     def _gate_up_swiglu(self, layer: _Layer, x: torch.Tensor) -> torch.Tensor:
         """SwiGLU of the merged gate|up projection of one token: one GEMV with the SwiGLU epilogue
         when the handle's GEMV runs unsplit (bit-identical to the GEMV + SwiGLU kernels it
         replaces), else those two kernels."""
         handle = layer.handles["gate_up"]
-        splits, lut = extension().gemv_plan(handle)
-        if splits == 1 and not lut and self.config.intermediate % 16 == 0:
+        if self._gate_up_unsplit(layer):
             return layers.linear_swiglu(handle, x, out=self.act_buffer)
         return layers.swiglu(layer.linears["gate_up"](x))
 
