@@ -312,6 +312,14 @@ int tx_add_rmsnorm_split(float *residual, uint64_t delta_handle, const void *wei
 int tx_linear_split_norm(uint64_t handle, const float *residual_in, float *residual_out, uint64_t delta_handle,
                          const void *weight, float eps, void *stream);
 
+/* The first layer's form of tx_linear_split_norm: the residual is row *token (device int64,
+ * clamped into [0, vocab)) of the bf16 embedding table embed [vocab][hidden], widened to fp32 and
+ * written to residual_out; x = its RMSNorm (tx_add_rmsnorm without a delta) feeds
+ * tx_linear_split(handle, x), all in one launch, bitwise as the gather, tx_add_rmsnorm and
+ * tx_linear_split. hidden = handle K <= 2048; TX_ERR_UNSUPPORTED as tx_linear_split_norm. */
+int tx_linear_split_embed_norm(uint64_t handle, const void *embed, int64_t vocab, const int64_t *token,
+                               float *residual_out, const void *weight, float eps, void *stream);
+
 /* The same for tx_linear_swiglu: tx_add_rmsnorm_split followed by tx_linear_swiglu(handle, x, out),
  * one launch fewer, with the requirements of both. */
 int tx_linear_swiglu_norm(uint64_t handle, const float *residual_in, float *residual_out, uint64_t delta_handle,

@@ -603,6 +603,34 @@ def test_linear_swiglu_norm_is_bit_identical(ext, hidden, dk, inter, bias):
         ext.free(gate_up)
 
 
+@pytest.mark.parametrize("hidden,cm,vocab,token", [(2048, 2560, 4096, 17), (256, 1024, 512, 511), (1024, 1024, 300, 1000)])
+def test_linear_split_embed_norm_is_bit_identical(ext, hidden, cm, vocab, token):
+    """Embedding row + add_rmsnorm (no delta) + linear_split == linear_split_embed_norm, bit for bit
+    (the residual and the consumer's partials read back through add_rmsnorm_split); a token past the
+    table takes its last row."""
+    consumer = _random_handle(ext, cm, hidden, seed=cm + vocab, bias=True)
+    try:
+        g = torch.Generator(device="cuda").manual_seed(hidden + token)
+        embed = torch.randn(vocab, hidden, device="cuda", generator=g).to(torch.bfloat16)
+        w = (1 + 0.1 * torch.randn(hidden, device="cuda", generator=g)).to(torch.bfloat16)
+        w2 = (1 + 0.1 * torch.randn(cm, device="cuda", generator=g)).to(torch.bfloat16)
+        r0 = torch.randn(1, cm, device="cuda", generator=g)
+        tok = torch.tensor([token], device="cuda")
+        h_want = embed[min(token, vocab - 1)].float().view(1, hidden).clone()
+        x = layers.add_rmsnorm(h_want, None, w, 1e-6)
+        layers.linear_split(consumer, x)
+        r_want = r0.clone()
+        read_want = layers.add_rmsnorm_split(r_want, consumer, w2, 1e-6, torch.empty(1, cm, device="cuda", dtype=torch.bfloat16))
+        h_got = torch.full((1, hidden), float("nan"), device="cuda")
+        assert layers.linear_split_embed_norm(consumer, embed, tok, h_got, w, 1e-6)
+        r_got = r0.clone()
+        read_got = layers.add_rmsnorm_split(r_got, consumer, w2, 1e-6, torch.empty(1, cm, device="cuda", dtype=torch.bfloat16))
+        assert torch.equal(h_got, h_want)
+        assert torch.equal(r_got, r_want) and torch.equal(read_got, read_want)
+    finally:
+        ext.free(consumer)
+
+
 def test_linear_norm_refusals(ext):
     """The same buffer for both residuals is refused; a 27B-class gate|up GEMV (hidden 5120, above
     the 2048 the prologue holds) returns False and launches nothing."""

@@ -70,6 +70,7 @@ SIGNATURES = {
     "tx_add_rmsnorm_split": (_I32, [_P, _U64, _P, ctypes.c_float, _P, _I64, _P]),
     "tx_linear_split_norm": (_I32, [_U64, _P, _P, _U64, _P, ctypes.c_float, _P]),
     "tx_linear_swiglu_norm": (_I32, [_U64, _P, _P, _U64, _P, ctypes.c_float, _P, _P]),
+    "tx_linear_split_embed_norm": (_I32, [_U64, _P, _I64, _P, _P, _P, ctypes.c_float, _P]),
     "tx_rope_kv_cache_split": (_I32, [_U64, _P, _P, _P, _I32, _I32, _I32, _P, _P, _P, _I64, _P]),
     "tx_prefill_split": (_I32, [_U64, _P, _I64, _P, _I64, ctypes.POINTER(ctypes.c_int), _P]),
     "tx_add_rmsnorm_prefill_split": (_I32, [_P, _U64, _P, _I64, _P, ctypes.c_float, _P, _I64, _P]),

@@ -904,6 +904,44 @@ int tx_linear_split_norm(uint64_t value, const float *residual_in, float *residu
   return TX_OK;
 }
 
+int tx_linear_split_embed_norm(uint64_t value, const void *embed, int64_t vocab, const int64_t *token,
+                               float *residual_out, const void *weight, float eps, void *stream) {
+  g_last_error.clear();
+  Handle *h = as_handle(value);
+  if (!h) return fail(TX_ERR_INVALID, "null Texelator handle");
+  if (!embed || !token || !residual_out || !weight) return fail(TX_ERR_INVALID, "linear_split_embed_norm: null pointer");
+  if (vocab <= 0) return fail(TX_ERR_INVALID, "linear_split_embed_norm: vocab must be positive");
+  if (reinterpret_cast<uintptr_t>(embed) % 16 || reinterpret_cast<uintptr_t>(residual_out) % 16 ||
+      reinterpret_cast<uintptr_t>(weight) % 16)
+    return fail(TX_ERR_INVALID, "linear_split_embed_norm: table, residual and weight must be 16-byte aligned");
+  if (h->bias && h->bias_dtype != TX_DTYPE_BF16) return fail(TX_ERR_INVALID, "linear_split_embed_norm: the bias must be BF16");
+  const int64_t reads = (int64_t)h->RG * h->gemv_splits * h->K * 4;
+  if (h->lut || h->K > tx::kNormMaxHidden || reads > kNormReadBudget)
+    return fail(TX_ERR_UNSUPPORTED, "linear_split_embed_norm: the normalization does not fit the GEMV (LUT handle, "
+                                    "K above 2048, or too many workgroups); gather, tx_add_rmsnorm and tx_linear_split");
+  tx::GemvParams p{};
+  p.tiles = h->tiles;
+  p.scales = h->scales;
+  p.M = h->M;
+  p.K = h->K;
+  p.Mp = h->Mp;
+  p.RG = h->RG;
+  p.CG = h->CG;
+  p.tokens = 1;
+  p.ks = h->gemv_splits;
+  p.partials = h->partials;
+  p.force_partials = 1;
+  p.norm_embed = static_cast<const uint16_t *>(embed);
+  p.norm_token = token;
+  p.norm_vocab = vocab;
+  p.norm_h_out = residual_out;
+  p.norm_weight = static_cast<const uint16_t *>(weight);
+  p.norm_eps = eps;
+  DeviceGuard guard(h->device);
+  TX_HIP(tx::launch_gemv(p, h->lookahead, true, reinterpret_cast<hipStream_t>(stream)));
+  return TX_OK;
+}
+
 int tx_linear_swiglu_norm(uint64_t value, const float *residual_in, float *residual_out, uint64_t delta_handle,
                           const void *weight, float eps, void *out, void *stream) {
   g_last_error.clear();

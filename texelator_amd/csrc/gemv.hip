@@ -141,7 +141,7 @@ __device__ __forceinline__ void merge_attention_x(uint4 *xs, const GemvParams &p
   }
 }
 
-// x of a one-token GEMV (GemvParams::norm_h) as add_rmsnorm_kernel<true, *> writes it, for hidden
+// x of a one-token GEMV (GemvParams::norm_h or norm_embed) as add_rmsnorm_kernel writes it, for hidden
 // = p.K <= 2048 and at most 8 producer splits. That kernel's thread t handles the group of four
 // columns i = t (t < 512 here); this lane stands for its threads t = 256 j + tid (j < 4; only j < 2
 // hold a group). Per group: delta = bf16(partials summed in split order + bias), v = h + delta,
@@ -158,7 +158,13 @@ __device__ __forceinline__ void norm_x_lds(uint4 *xs, float *wave_sums, const Ge
                                            int wave, int lane, bool writer) {
   const int hidden = p.K, groups = hidden / 4, ks = p.norm_ks;
   const int tid = wave * 64 + lane;
+  const bool embed = p.norm_embed != nullptr, delta = p.norm_partials != nullptr;
   const float4 *hr = reinterpret_cast<const float4 *>(p.norm_h);
+  const uint2 *er = nullptr;
+  if (embed) {
+    const int64_t token = min(max(*p.norm_token, (int64_t)0), p.norm_vocab - 1);
+    er = reinterpret_cast<const uint2 *>(p.norm_embed + (size_t)token * hidden);
+  }
   const float4 *pp = reinterpret_cast<const float4 *>(p.norm_partials);
   const int step = p.norm_Mp / 4;  // float4 between splits (one token)
   const uint2 *br = reinterpret_cast<const uint2 *>(p.norm_bias ? p.norm_bias : p.norm_weight);
@@ -168,10 +174,18 @@ __device__ __forceinline__ void norm_x_lds(uint4 *xs, float *wave_sums, const Ge
 #pragma unroll
   for (int j = 0; j < kNormSlots; ++j) {
     const int ic = min(j * kThreads + tid, groups - 1);
-    hv[j] = hr[ic];
+    if (embed) {
+      const uint2 e = er[ic];
+      hv[j] = make_float4(bf((uint16_t)(e.x & 0xFFFFu)), bf((uint16_t)(e.x >> 16)), bf((uint16_t)(e.y & 0xFFFFu)),
+                          bf((uint16_t)(e.y >> 16)));
+    } else {
+      hv[j] = hr[ic];
+    }
+    if (delta) {
 #pragma unroll
-    for (int k = 0; k < kNormMaxSplits; ++k) q[j][k] = pp[min(k, ks - 1) * step + ic];
-    bv[j] = br[ic];
+      for (int k = 0; k < kNormMaxSplits; ++k) q[j][k] = pp[min(k, ks - 1) * step + ic];
+      bv[j] = br[ic];
+    }
     wv[j] = wr[ic];
   }
   __builtin_amdgcn_sched_barrier(0);  // every load issued before the first add
@@ -181,27 +195,29 @@ __device__ __forceinline__ void norm_x_lds(uint4 *xs, float *wave_sums, const Ge
 #pragma unroll
   for (int j = 0; j < kNormSlots; ++j) {
     const int i = j * kThreads + tid;
-    float4 acc = q[j][0];
-#pragma unroll
-    for (int k = 1; k < kNormMaxSplits; ++k) {
-      if (k < ks) {
-        acc.x += q[j][k].x;
-        acc.y += q[j][k].y;
-        acc.z += q[j][k].z;
-        acc.w += q[j][k].w;
-      }
-    }
-    if (p.norm_bias) {
-      acc.x += bf((uint16_t)(bv[j].x & 0xFFFFu));
-      acc.y += bf((uint16_t)(bv[j].x >> 16));
-      acc.z += bf((uint16_t)(bv[j].y & 0xFFFFu));
-      acc.w += bf((uint16_t)(bv[j].y >> 16));
-    }
     float4 h = hv[j];
-    h.x += bf(to_bf(acc.x));
-    h.y += bf(to_bf(acc.y));
-    h.z += bf(to_bf(acc.z));
-    h.w += bf(to_bf(acc.w));
+    if (delta) {  // without a delta the residual is taken as it is (add_rmsnorm with delta NULL)
+      float4 acc = q[j][0];
+#pragma unroll
+      for (int k = 1; k < kNormMaxSplits; ++k) {
+        if (k < ks) {
+          acc.x += q[j][k].x;
+          acc.y += q[j][k].y;
+          acc.z += q[j][k].z;
+          acc.w += q[j][k].w;
+        }
+      }
+      if (p.norm_bias) {
+        acc.x += bf((uint16_t)(bv[j].x & 0xFFFFu));
+        acc.y += bf((uint16_t)(bv[j].x >> 16));
+        acc.z += bf((uint16_t)(bv[j].y & 0xFFFFu));
+        acc.w += bf((uint16_t)(bv[j].y >> 16));
+      }
+      h.x += bf(to_bf(acc.x));
+      h.y += bf(to_bf(acc.y));
+      h.z += bf(to_bf(acc.z));
+      h.w += bf(to_bf(acc.w));
+    }
     v[j] = h;
     if (i < groups) {
       ss[j] = (h.x * h.x + h.y * h.y) + (h.z * h.z + h.w * h.w);
@@ -717,7 +733,8 @@ void launch_splitk_reduce(const GemvParams &p, hipStream_t stream) {
 constexpr int kFusedMaxColumns = 224;
 
 bool fused_eligible(const GemvParams &p) {
-  return p.fused && p.tokens == 1 && !p.lut && !p.force_partials && !p.attn && !p.norm_h && p.ks > 1 && p.ks <= kFusedMaxSplits &&
+  return p.fused && p.tokens == 1 && !p.lut && !p.force_partials && !p.attn && !p.norm_h && !p.norm_embed && p.ks > 1 &&
+         p.ks <= kFusedMaxSplits &&
          p.CG <= kFusedMaxColumns;
 }
 
@@ -738,7 +755,7 @@ hipError_t launch_variant(const GemvParams &p, hipStream_t stream) {
       hipLaunchKernelGGL((gemv_kernel<false, LA, false, true, false, kXMerge>), grid, dim3(kThreads), lds, stream, p);
       return hipGetLastError();
     }
-    if (p.norm_h) {  // the caller checked: one token, force_partials, no LUT, K <= 8192
+    if (p.norm_h || p.norm_embed) {  // the caller checked: one token, force_partials, no LUT, K <= 2048
       hipLaunchKernelGGL((gemv_kernel<false, LA, false, true, false, kXNorm>), grid, dim3(kThreads), lds, stream, p);
       return hipGetLastError();
     }
@@ -772,7 +789,7 @@ hipError_t launch_la(const GemvParams &p, bool f32_out, hipStream_t stream) {
 hipError_t launch_gemv_swiglu(const GemvParams &p, int lookahead, hipStream_t stream) {
   const size_t lds = (size_t)x_stage_chunks(p.CG) * sizeof(uint4);
   const dim3 grid(p.RG / 2);
-  if (p.norm_h) {
+  if (p.norm_h || p.norm_embed) {
     switch (lookahead) {
       case 1: hipLaunchKernelGGL((gemv_swiglu_kernel<1, true>), grid, dim3(kThreads), lds, stream, p); break;
       case 2: hipLaunchKernelGGL((gemv_swiglu_kernel<2, true>), grid, dim3(kThreads), lds, stream, p); break;

@@ -33,8 +33,14 @@ struct GemvParams {
   // (norm_ks splits, row stride norm_Mp, bias norm_bias or nullptr), with the RMSNorm weight
   // norm_weight; workgroup 0 writes the updated residual to norm_h_out (not norm_h: the other
   // workgroups still read it). nullptr: x is read (or merged).
+  // Or, with norm_embed (norm_h nullptr, no delta): the residual is row *norm_token (clamped into
+  // [0, norm_vocab)) of the bf16 table norm_embed [norm_vocab][K], widened to fp32 and written to
+  // norm_h_out by workgroup 0.
   const float *norm_h;
   float *norm_h_out;
+  const uint16_t *norm_embed;
+  const int64_t *norm_token;
+  int64_t norm_vocab;
   const float *norm_partials;
   const uint16_t *norm_bias;
   const uint16_t *norm_weight;

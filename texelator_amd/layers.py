@@ -231,6 +231,28 @@ def linear_split_norm(handle: int, residual_in: torch.Tensor, residual_out: torc
     return True
 
 
+def linear_split_embed_norm(handle: int, embed: torch.Tensor, token: torch.Tensor, residual_out: torch.Tensor,
+                            weight: torch.Tensor, eps: float) -> bool:
+    """The first layer's :func:`linear_split_norm`: ``residual_out`` = row ``token`` (device int64
+    [1], clamped into the table) of the bf16 embedding table ``embed`` [vocab, K] in fp32, then
+    :func:`add_rmsnorm` of it (no delta) and :func:`linear_split` of ``handle``, in one launch.
+    False, with nothing launched, where that does not fit the GEMV."""
+    k = _hip_shape(handle)[1]
+    _expect(embed.is_cuda and embed.dtype == torch.bfloat16 and embed.is_contiguous() and embed.dim() == 2 and
+            embed.shape[1] == k and embed.data_ptr() % 16 == 0, "embed must be a contiguous CUDA bf16 [vocab, K] table")
+    _expect(token.dtype == torch.int64 and token.numel() == 1 and token.is_contiguous(), "token must be int64 [1]")
+    _expect(residual_out.is_cuda and residual_out.dtype == torch.float32 and residual_out.is_contiguous() and
+            residual_out.numel() == k and residual_out.data_ptr() % 16 == 0, "residual_out must be float32 [K]")
+    _expect(weight.dtype == torch.bfloat16 and weight.is_contiguous() and weight.numel() == k and weight.data_ptr() % 16 == 0,
+            "weight must be a contiguous, 16-byte aligned bf16 [K]")
+    status = _lib.load().tx_linear_split_embed_norm(handle, _ptr(embed), embed.shape[0], _ptr(token), _ptr(residual_out),
+                                                   _ptr(weight), float(eps), _stream(residual_out))
+    if status == _lib.TX_ERR_UNSUPPORTED:
+        return False
+    check(status)
+    return True
+
+
 def linear_swiglu_norm(handle: int, residual_in: torch.Tensor, residual_out: torch.Tensor, delta_handle: int,
                        weight: torch.Tensor, eps: float, out: torch.Tensor) -> bool:
     """:func:`linear_split_norm` for :func:`linear_swiglu`: the add+RMSNorm of the residual and

@@ -395,6 +395,8 @@ class BC4Decoder:
         (positions ``key_positions[:T]``, ``length == T``) torch's causal flash attention, and any
         other multi-token call the cached fp32 attention."""
         c = self.config
+        if self.fused and ids.numel() == 1 and self.split_decode:
+            return self._decode_split(ids, positions, length, 1.0 / math.sqrt(c.head_dim))
         h = self.embed.index_select(0, ids).float()
         if not self.fused:
             for index, layer in enumerate(self.layers):
@@ -403,8 +405,6 @@ class BC4Decoder:
         tokens = ids.numel()
         scale = 1.0 / math.sqrt(c.head_dim)
         x = layers.add_rmsnorm(h, None, self.layers[0].input_norm, c.rms_eps)
-        if tokens == 1 and self.split_decode:
-            return self._decode_split(h, x, positions, length, scale)
         # a prompt at positions 0..T-1 attending to itself only: causal flash attention
         prompt = (tokens > 1 and length == tokens and positions.data_ptr() == self.key_positions.data_ptr()
                   and self.flash_prompt_attention)
@@ -460,16 +460,22 @@ class BC4Decoder:
         else:
             layers.add_rmsnorm(h, linear(x_in), weight, self.config.rms_eps, out=out)
 
-    def _decode_split(self, h: torch.Tensor, x: torch.Tensor, positions: torch.Tensor, length: int,
-                      scale: float) -> torch.Tensor:
+    def _decode_split(self, ids: torch.Tensor, positions: torch.Tensor, length: int, scale: float) -> torch.Tensor:
         """One token through every layer with the split-K consumers (eight kernels a layer; seven where
         the attention's merge runs inside the o GEMV, five where the two add+RMSNorms also run inside
         the gate|up and the next q|k|v GEMVs, whose updated residual then alternates between h and a
         second buffer)."""
         c = self.config
         torch.index_select(self.rope_cs, 0, positions, out=self.rope_row)
+        h = torch.empty((1, c.hidden), dtype=torch.float32, device=self.device)
+        x = torch.empty((1, c.hidden), dtype=torch.bfloat16, device=self.device)
         other = torch.empty_like(h) if self.norm_in_gemv else None
-        qkv_done = False
+        # the embedding row, the first input norm and the first q|k|v GEMV: one launch where it fits
+        qkv_done = self.norm_in_gemv and layers.linear_split_embed_norm(
+            self.layers[0].handles["qkv"], self.embed, ids.view(1), h, self.layers[0].input_norm, c.rms_eps)
+        if not qkv_done:
+            h.copy_(self.embed.index_select(0, ids.view(1)))
+            layers.add_rmsnorm(h, None, self.layers[0].input_norm, c.rms_eps, out=x)
         for index, layer in enumerate(self.layers):
             if not qkv_done:
                 layers.linear_split(layer.handles["qkv"], x)
