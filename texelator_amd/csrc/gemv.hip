@@ -252,14 +252,27 @@ __device__ __forceinline__ void norm_x_lds(uint4 *xs, float *wave_sums, const Ge
 }
 
 // Single-token B operands: only output column 0 of a tile is used, so only the lanes of B column 0
-// (lane % 16 == 0) read x; the other fifteen columns read a zeroed 256-byte slot placed after the
-// staged x (TX_GEMV_ZERO_COLUMNS: zero operands switch fewer multiplier bits than fifteen copies of x,
-// and the clock of this power-bound kernel follows the switching). Column 0's products and sums are
-// the same either way.
+// (lane % 16 == 0) read x; the other fifteen columns keep the zeros they start with
+// (TX_GEMV_ZERO_COLUMNS; else every column reads x, a broadcast). Zero operands switch fewer
+// multiplier bits than fifteen copies of x, the reads skipped spare LDS bandwidth, and the clock of
+// this power-bound kernel follows the switching. Column 0's products and sums are the same either way.
 #ifndef TX_GEMV_ZERO_COLUMNS
 #define TX_GEMV_ZERO_COLUMNS 1
 #endif
-constexpr int kZeroSlotU4 = TX_GEMV_ZERO_COLUMNS ? 16 : 0;
+// x of tile column `col` into xf: one lane in sixteen, or all.
+__device__ __forceinline__ void read_x_columns(XFrag &xf, const uint4 *xs, int col, int kg, int lane) {
+  if (!TX_GEMV_ZERO_COLUMNS || (lane & 15) == 0) {
+    const uint4 *xv = xs + col * 16 + kg * 4;
+    xf.x0 = xv[0];
+    xf.x1 = xv[1];
+    xf.x2 = xv[2];
+    xf.x3 = xv[3];
+  }
+}
+// The same without the per-tile branch, for the two-ring SwiGLU kernel (measured faster there): the
+// fifteen other columns read a zeroed 256-byte slot placed after the staged x instead of skipping
+// the read.
+constexpr int kZeroSlotU4 = 16;
 struct XColumns {
   const uint4 *base;  // the staged x (column 0) or the zero slot
   uint32_t mask;      // keeps the tile column's offset for column 0, drops it for the others
@@ -267,14 +280,10 @@ struct XColumns {
     return base + (((uint32_t)col * 16u) & mask) + kg * 4;
   }
 };
-__device__ __forceinline__ XColumns x_columns(const uint4 *xs, int zero_slot, int lane) {
-  if constexpr (!TX_GEMV_ZERO_COLUMNS) return XColumns{xs, 0xFFFFFFFFu};
-  const bool x_lane = (lane & 15) == 0;
-  return XColumns{x_lane ? xs : xs + zero_slot, x_lane ? 0xFFFFFFFFu : 0u};
-}
-// The zero slot (before the barrier that publishes the staged x).
-__device__ __forceinline__ void zero_x_slot(uint4 *xs, int zero_slot) {
+__device__ __forceinline__ XColumns x_columns(uint4 *xs, int zero_slot, int lane) {
   if (TX_GEMV_ZERO_COLUMNS && threadIdx.x < 16) xs[zero_slot + threadIdx.x] = make_uint4(0, 0, 0, 0);
+  const bool x_lane = !TX_GEMV_ZERO_COLUMNS || (lane & 15) == 0;
+  return XColumns{x_lane ? xs : xs + zero_slot, x_lane ? 0xFFFFFFFFu : 0u};
 }
 
 // One tile for one lane: decode both blocks and accumulate 4 MFMAs (block 0 into acc0, block 1
@@ -405,8 +414,6 @@ __global__ __launch_bounds__(kThreads, LUT || XSRC != kXRead ? 4 : TX_GEMV_WAVES
     if constexpr (!MULTI) stage_x_lds(xs, x, p.K, c_begin * 16, nc * 16, wave, lane);
     if constexpr (!LUT) copy_seed_tables(tables, wave, lane, kWaves);
   }
-  const int zero_slot = x_stage_chunks((p.CG + p.ks - 1) / p.ks);
-  if constexpr (!MULTI) zero_x_slot(xs, zero_slot);
   if constexpr (!MULTI || !LUT) __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): x and the tables have landed
   __syncthreads();
 
@@ -415,10 +422,9 @@ __global__ __launch_bounds__(kThreads, LUT || XSRC != kXRead ? 4 : TX_GEMV_WAVES
   const uint16_t *xrow = x + (size_t)(t0 + min(i, tc - 1)) * p.K;
 
   f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-  // Single token: B column 0 gets x (the lanes of a K chunk read one LDS address, a broadcast), the
-  // others zeros or x (x_columns); only output column 0 is read.
-  const XColumns xcols = x_columns(xs, zero_slot, lane);
-  XFrag xf;
+  // Single token: B column 0 gets x (read_x_columns), the others zeros or x; only output column 0
+  // is read.
+  XFrag xf{};
   auto load_xf = [&](int j) {
     const int col = j * kWaves + wave;  // tile column within this split
     if constexpr (MULTI) {
@@ -428,11 +434,7 @@ __global__ __launch_bounds__(kThreads, LUT || XSRC != kXRead ? 4 : TX_GEMV_WAVES
       xf.x2 = load_x8(xrow, k + 16, p.K);
       xf.x3 = load_x8(xrow, k + 24, p.K);
     } else {
-      const uint4 *xv = xcols.at(col, kg);
-      xf.x0 = xv[0];
-      xf.x1 = xv[1];
-      xf.x2 = xv[2];
-      xf.x3 = xv[3];
+      read_x_columns(xf, xs, col, kg, lane);
     }
   };
 
@@ -553,22 +555,13 @@ __global__ __launch_bounds__(kThreads * kFusedMaxSplits, TX_GEMV_WAVES_PER_EU) v
   const float scale = p.scales[g * kTileRows + i];
   stage_x_lds(xs, static_cast<const uint16_t *>(p.x), p.K, 0, p.CG * 16, wave, lane, waves);
   copy_seed_tables(tables, wave, lane, waves);
-  const int zero_slot = x_stage_chunks(p.CG);
-  zero_x_slot(xs, zero_slot);
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): x and the tables have landed
   __syncthreads();
-  const XColumns xcols = x_columns(xs, zero_slot, lane);
 
   const uint32_t pm = pm_scale_pair<F16>(scale);
   f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-  XFrag xf;
-  auto load_xf = [&](int j) {
-    const uint4 *xv = xcols.at(c_begin + j * kWaves + wq, kg);
-    xf.x0 = xv[0];
-    xf.x1 = xv[1];
-    xf.x2 = xv[2];
-    xf.x3 = xv[3];
-  };
+  XFrag xf{};
+  auto load_xf = [&](int j) { read_x_columns(xf, xs, c_begin + j * kWaves + wq, kg, lane); };
   int j0 = 0;
   for (; j0 + R <= nt; j0 += R) {
     progress_priority(nt - j0, nt);
@@ -662,16 +655,14 @@ __global__ __launch_bounds__(kThreads, NORM ? 4 : (LA == 1 ? 6 : (LA == 2 ? 5 : 
     stage_x_lds(xs, x, p.K, 0, nc * 16, wave, lane);
     copy_seed_tables(tables, wave, lane, kWaves);
   }
-  const int zero_slot = x_stage_chunks(p.CG);
-  zero_x_slot(xs, zero_slot);
+  const XColumns xcols = x_columns(xs, x_stage_chunks(p.CG), lane);  // zeroes the slot before the barrier
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): x and the tables have landed
   __syncthreads();
-  const XColumns xcols = x_columns(xs, zero_slot, lane);
 
   const uint32_t pm_g = pm_scale_pair<false>(scale_g);
   const uint32_t pm_u = pm_scale_pair<false>(scale_u);
   f32x4 ga0 = {0.f, 0.f, 0.f, 0.f}, ga1 = ga0, ua0 = ga0, ua1 = ga0;
-  XFrag xf;  // B column 0 gets x (x_columns); only output column 0 is read
+  XFrag xf;  // B column 0 gets x, the others zeros (x_columns); only output column 0 is read
   auto consume = [&](int u, int j) {
     {
       const uint4 *xv = xcols.at(j * kWaves + wave, kg);
@@ -777,13 +768,13 @@ template <bool F16, int LA, bool MULTI, bool F32OUT>
 hipError_t launch_variant(const GemvParams &p, hipStream_t stream) {
   if constexpr (!MULTI) {
     if (fused_eligible(p)) {
-      const size_t lds = (size_t)(x_stage_chunks(p.CG) + kZeroSlotU4) * sizeof(uint4);
+      const size_t lds = (size_t)x_stage_chunks(p.CG) * sizeof(uint4);
       hipLaunchKernelGGL((gemv_fused_kernel<F16, LA, F32OUT>), dim3(p.RG), dim3(kThreads * p.ks), lds, stream, p);
       return hipGetLastError();
     }
   }
   const int max_cols = (p.CG + p.ks - 1) / p.ks;
-  const size_t lds = MULTI ? 0 : (size_t)(x_stage_chunks(max_cols) + kZeroSlotU4) * sizeof(uint4);
+  const size_t lds = MULTI ? 0 : (size_t)x_stage_chunks(max_cols) * sizeof(uint4);
   dim3 grid(p.RG, p.ks, (p.tokens + 15) / 16);
   if constexpr (!MULTI && !F16 && F32OUT) {
     if (p.attn) {  // the caller checked: one token, force_partials, no LUT, K = heads * 128
@@ -884,7 +875,7 @@ int gemv_resident_per_cu(int lookahead, int columns) {
     default: return 0;
   }
   int n = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, kThreads, (size_t)(x_stage_chunks(columns) + kZeroSlotU4) * sizeof(uint4)) != hipSuccess) {
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, kThreads, (size_t)x_stage_chunks(columns) * sizeof(uint4)) != hipSuccess) {
     (void)hipGetLastError();
     return 0;
   }
