@@ -256,15 +256,18 @@ def test_prefill_candidates_bitwise_equal_and_within_rrms(ext, oracle_threads, t
     assert bc4.relative_rms(ref, got) <= PREFILL_RRMS_TOL
 
 
+@pytest.mark.parametrize("m", [26624, 16416, 8224])
 @pytest.mark.parametrize("mode", ["bf16", "f16_bias", "lut"])
 @pytest.mark.parametrize("tokens", [2, 17, 32])
-def test_prefill_split_group_tile_matches_other_tiles(ext, mode, tokens):
+def test_prefill_split_group_tile_matches_other_tiles(ext, mode, tokens, m):
     """Up to 32 tokens with exactly four K splits, candidate 9 runs the split-group tile (the four
-    splits of a 32-row block in one workgroup, summed there in split order): bitwise equal to the
-    tiles that write split partials for the reduce kernel, and within the prefill tolerance of the
-    float64 product on sampled rows. 26624 rows make 208 workgroups of 128 rows: four splits on a
-    256-CU MI355X."""
-    m, k = 26624, 4096
+    splits of one or two 32-row blocks in one workgroup, summed there in split order): bitwise
+    equal to the tiles that write split partials for the reduce kernel, and within the prefill
+    tolerance of the float64 product on sampled rows. With K = 4096 every row count here splits
+    four ways on a 256-CU MI355X. 26624 rows (832 blocks) and 16416 rows (513 blocks: the last
+    wave repeats its one real block, never stored) run two blocks per wave; 8224 rows (257 blocks,
+    129 two-block workgroups, fewer than the CUs) run one."""
+    k = 4096
     blocks = random_blocks(m, k, 611)
     scales = lognormal_scales(m, 612)
     f16 = mode == "f16_bias"

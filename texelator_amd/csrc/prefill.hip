@@ -600,19 +600,26 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillParams p) {
 }
 
 // Split-group tile (candidate 9 with exactly four K splits, up to 32 tokens, K a multiple of
-// 128): a workgroup holds the four splits of one (32-token tile, 32-row block), one per wave, and
-// each wave runs its split on its own -- weights decoded in registers as in prefill_kernel,
-// activations staged by the wave itself into its own LDS buffers (direct global-to-LDS loads, 1 KiB
-// contiguous per load) half a step at a time -- so the K loop has no workgroup barrier. At the end
-// the four splits are summed in split order through LDS, as prefill_reduce_kernel sums them: no
-// partials leave the workgroup and no reduce kernel runs. Same lane layouts, K sets and order as
-// prefill_kernel, hence the same bits.
+// 128): a workgroup holds the four splits of one (32-token tile, RBW x 32-row blocks), one per
+// wave, and each wave runs its split on its own -- weights decoded in registers as in
+// prefill_kernel, activations staged by the wave itself into its own LDS buffers (direct
+// buffer-to-LDS loads, 1 KiB contiguous per load) half a step at a time -- so the K loop has no
+// workgroup barrier. With RBW = 2 a wave multiplies one staged activation slice by two row blocks
+// (two independent MFMA chains): the activations are read from L2 once per 64 rows instead of once
+// per 32, which was the kernel's bound (per K column, 32 tokens of bf16 activations are 64 bytes
+// against 16 bytes of weights in a 32-row block). At the end the four splits are summed in split order
+// through LDS, as prefill_reduce_kernel sums them: no partials leave the workgroup and no reduce
+// kernel runs. Same lane layouts, K sets and order as prefill_kernel, hence the same bits.
 #ifndef TX_SMALL_WAVE
 #define TX_SMALL_WAVE 1
 #endif
+#ifndef TX_WAVE_RBW2_MIN_WGS
+#define TX_WAVE_RBW2_MIN_WGS 256
+#endif
 
-template <bool F16, bool LUT>
+template <bool F16, bool LUT, int RBW>
 __global__ __launch_bounds__(kThreads) void prefill_wave_kernel(PrefillParams p) {
+  static_assert(RBW == 1 || RBW == 2, "one or two 32-row blocks per wave");
   // Per wave, K columns 0-63 (xlo) and 64-127 (xhi) of a step for its 32 tokens: token row r takes
   // 128 bytes, its 16-byte slot q holds columns 8*(q ^ ((r >> 1) % 8)).. +7 of the half (the 16
   // rows one operand read serves per LDS pass then fall on distinct banks: even and odd rows sit in
@@ -627,27 +634,53 @@ __global__ __launch_bounds__(kThreads) void prefill_wave_kernel(PrefillParams p)
   const int r32 = lane & 31;
   const int h = lane >> 5;
   const int row_blocks = (p.M + 31) / 32;
-  const int wgs = row_blocks * ((p.tokens + 31) / 32);
+  const int row_groups = (row_blocks + RBW - 1) / RBW;
+  const int wgs = row_groups * ((p.tokens + 31) / 32);
   const int per_xcd = (wgs + kXcds - 1) / kXcds;
   const int q = (int)(blockIdx.x % kXcds) * per_xcd + (int)(blockIdx.x / kXcds);
   if (q >= wgs) return;
   if constexpr (!LUT) copy_seed_tables(tables, split, lane, kThreads / 64);
-  const int rb = q % row_blocks;
-  const int t0 = (q / row_blocks) * 32;
+  const int rg = q % row_groups;
+  const int t0 = (q / row_groups) * 32;
   const int c_begin = (int)((uint32_t)split * (uint32_t)p.CG / 4u);
   const int nc = (int)((uint32_t)(split + 1) * (uint32_t)p.CG / 4u) - c_begin;
-  const int n0 = rb * 32;
 
-  // A operands: lane slot (row & 15) + 16h of tile group 2rb + (r32 >> 4) (clamped into the matrix;
-  // rows past M are computed, never stored), as in prefill_kernel.
-  const int g = min(2 * rb + (r32 >> 4), p.RG - 1);
-  const uint4 *gtile = p.tiles + ((size_t)g * p.CG + c_begin) * 64 + (lane & 15) + 16 * h;
-  const float scale = p.scales[g * kTileRows + (lane & 15)];
-  const uint32_t pm = pm_scale_pair<F16>(scale);
-  auto load_tiles = [&](uint4 (&slot)[2], int j) {
-    const size_t off = (size_t)j * 64;
-    slot[0] = load_stream(gtile + off);
-    slot[1] = load_stream(gtile + off + 32);
+  // A operands of row block rb_b = RBW*rg + b (clamped to the last block; a duplicate block is
+  // computed, never stored): lane slot (row & 15) + 16h of tile group 2rb_b + (r32 >> 4) (clamped
+  // into the matrix; rows past M are computed, never stored), as in prefill_kernel.
+  int n0[RBW];
+  float scale[RBW];
+  uint32_t pm[RBW], tlane[RBW];
+  // Weights and activations are read through buffer descriptors (wave-uniform base and step
+  // offset, per-lane offset). With only buffer loads in flight the compiler waits for exactly the
+  // loads a use needs (vmcnt(N)); global_load_lds in flight beside global loads made it wait for
+  // every load (vmcnt(0)) before each use of a weight tile. The tile descriptor starts at tile
+  // (gbase, c_begin), gbase = the first group of the wave's first block (<= RG - 1).
+  const int gbase = 2 * RBW * rg;
+#pragma unroll
+  for (int b = 0; b < RBW; ++b) {
+    const int rb = min(RBW * rg + b, row_blocks - 1);
+    n0[b] = (RBW * rg + b) * 32;
+    const int g = min(2 * rb + (r32 >> 4), p.RG - 1);
+    scale[b] = p.scales[g * kTileRows + (lane & 15)];
+    pm[b] = pm_scale_pair<F16>(scale[b]);
+    tlane[b] = (uint32_t)(((g - gbase) * p.CG * 64 + (lane & 15) + 16 * h) * 16);
+  }
+  const int64_t first_tile = (int64_t)gbase * p.CG + c_begin;
+  const int64_t tile_bytes = ((int64_t)p.RG * p.CG - first_tile) * kTileBytes;
+  const __amdgpu_buffer_rsrc_t trsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint4 *>(p.tiles + first_tile * 64), (short)0, (int)(tile_bytes < 0x7FFFFFFF ? tile_bytes : 0x7FFFFFFF),
+      0x00020000);
+  typedef uint4 Tiles[RBW][2];
+  auto load_tiles = [&](Tiles &slot, int j) {
+    const int off = __builtin_amdgcn_readfirstlane(j * kTileBytes);
+#pragma unroll
+    for (int b = 0; b < RBW; ++b) {
+      const u32x4 v0 = __builtin_amdgcn_raw_buffer_load_b128(trsrc, tlane[b], off, 2 /* nt */);
+      const u32x4 v1 = __builtin_amdgcn_raw_buffer_load_b128(trsrc, tlane[b], off + 512, 2 /* nt */);
+      slot[b][0] = make_uint4(v0.x, v0.y, v0.z, v0.w);
+      slot[b][1] = make_uint4(v1.x, v1.y, v1.z, v1.w);
+    }
   };
 
   // Staging of half `hf` of step j (K is a multiple of 128 here): load v brings token rows
@@ -655,17 +688,21 @@ __global__ __launch_bounds__(kThreads) void prefill_wave_kernel(PrefillParams p)
   // (l % 8) ^ (((8v + l / 8) >> 1) % 8). Rows past the tokens repeat the last token (never stored).
   const uint16_t *x = static_cast<const uint16_t *>(p.x);
   const int srow = lane >> 3;  // row within the load's eight
-  uint32_t row_off[4];         // element offsets of this lane's four token rows and chunks
+  uint32_t row_off[4];         // byte offsets of this lane's four token rows and chunks
 #pragma unroll
   for (int v = 0; v < 4; ++v)
-    row_off[v] = (uint32_t)min(t0 + 8 * v + srow, p.tokens - 1) * (uint32_t)p.K + 8u * (uint32_t)((lane & 7) ^ ((4 * v + (srow >> 1)) & 7));
-  const uint16_t *xsplit = x + (size_t)c_begin * kTileK;
+    row_off[v] = 2u * ((uint32_t)min(t0 + 8 * v + srow, p.tokens - 1) * (uint32_t)p.K +
+                       8u * (uint32_t)((lane & 7) ^ ((4 * v + (srow >> 1)) & 7)));
+  const int64_t x_bytes = ((int64_t)p.tokens * p.K - (int64_t)c_begin * kTileK) * 2;
+  const __amdgpu_buffer_rsrc_t xrsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t *>(x + (size_t)c_begin * kTileK), (short)0, (int)(x_bytes < 0x7FFFFFFF ? x_bytes : 0x7FFFFFFF),
+      0x00020000);
   auto stage = [&](uint16_t *buf, int j, int hf) {
-    const uint16_t *src = xsplit + (size_t)j * kTileK + 64 * hf;
+    const int off = __builtin_amdgcn_readfirstlane((j * kTileK + 64 * hf) * 2);
 #pragma unroll
     for (int v = 0; v < 4; ++v)
-      __builtin_amdgcn_global_load_lds((const void *)(src + row_off[v]),
-                                       (__attribute__((address_space(3))) void *)(buf + 8 * v * 64), 16, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(xrsrc, (__attribute__((address_space(3))) void *)(buf + 8 * v * 64), 16,
+                                               row_off[v], off, 0, 0);
   };
   // B operand of MFMA 4*hf + s (s < 4): columns 32h + 16*(s>>1) + 8*(s&1) .. +7 of half hf.
   auto read_b = [&](const uint16_t *buf, int s) {
@@ -674,7 +711,7 @@ __global__ __launch_bounds__(kThreads) void prefill_wave_kernel(PrefillParams p)
 
   uint16_t *mylo = xlo[split];
   uint16_t *myhi = xhi[split];
-  uint4 ta[2], tb[2];  // weight tiles of the even and the odd steps
+  Tiles ta, tb;  // weight tiles of the even and the odd steps
   stage(mylo, 0, 0);
   load_tiles(ta, 0);
   stage(myhi, 0, 1);
@@ -683,51 +720,59 @@ __global__ __launch_bounds__(kThreads) void prefill_wave_kernel(PrefillParams p)
     __syncthreads();  // the seed tables
   }
 
-  f32x16 acc;
+  f32x16 acc[RBW];
 #pragma unroll
-  for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+  for (int b = 0; b < RBW; ++b)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[b][r] = 0.f;
 
-  // Block jj of weight tile `tile` into MFMAs 2jj, 2jj + 1.
-  auto block = [&](const uint4 (&tile)[2], int jj, const u32x4 &b0, const u32x4 &b1) {
-    const uint4 &piece = tile[jj >> 1];
+  // Block jj of row block b's weight tile into that block's MFMAs 2jj, 2jj + 1.
+  auto block = [&](const Tiles &tile, int b, int jj, const u32x4 &b0, const u32x4 &b1) {
+    const uint4 &piece = tile[b][jj >> 1];
     const uint32_t wa = (jj & 1) ? piece.z : piece.x;
     const uint32_t wb = (jj & 1) ? piece.w : piece.y;
     uint32_t d[8];
     if constexpr (LUT) {
       const float4 *row = p.lut + 2 * (size_t)palette_row(wa, wb);
-      decode_from_palette<F16>(row[0], row[1], wa, wb, scale, d);
+      decode_from_palette<F16>(row[0], row[1], wa, wb, scale[b], d);
     } else {
-      decode_block_lds<F16>(wa, wb, scale, pm, tables, d);
+      decode_block_lds<F16>(wa, wb, scale[b], pm[b], tables, d);
     }
-    acc = mfma<F16>(u32x4{d[0], d[1], d[2], d[3]}, b0, acc);
-    acc = mfma<F16>(u32x4{d[4], d[5], d[6], d[7]}, b1, acc);
+    acc[b] = mfma<F16>(u32x4{d[0], d[1], d[2], d[3]}, b0, acc[b]);
+    acc[b] = mfma<F16>(u32x4{d[4], d[5], d[6], d[7]}, b1, acc[b]);
   };
-  // Step j multiplies weight tile `cur` (loaded during step j - 1) and loads tile j + 1 into
+  // Step j multiplies weight tiles `cur` (loaded during step j - 1) and loads tiles j + 1 into
   // `next`. Each half buffer is read into registers, then refilled with the next step's half while
-  // this step's blocks are decoded and multiplied. Loads are issued low half, weights, high half:
-  // six later loads stay in flight at each half buffer's wait.
-  auto step = [&](int j, const uint4 (&cur)[2], uint4 (&next)[2]) {
+  // this step's blocks are decoded and multiplied. Loads are issued low half (4), weights (2 RBW),
+  // high half (4): 4 + 2 RBW later loads stay in flight at each half buffer's wait.
+  constexpr int kLaterLoads = 4 + 2 * RBW;
+  constexpr int kHalfWait = 0x0F70 | kLaterLoads;  // vmcnt(kLaterLoads), lgkmcnt and expcnt free
+  auto step = [&](int j, const Tiles &cur, Tiles &next) {
     const int jn = min(j + 1, nc - 1);
-    u32x4 b[4];
-    __builtin_amdgcn_s_waitcnt(0x0F76);  // vmcnt(6): the low half of step j has landed
+    u32x4 bv[4];
+    __builtin_amdgcn_s_waitcnt(kHalfWait);  // the low half of step j has landed
 #pragma unroll
-    for (int s = 0; s < 4; ++s) b[s] = read_b(mylo, s);
+    for (int s = 0; s < 4; ++s) bv[s] = read_b(mylo, s);
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the reads are done before the refill
     __builtin_amdgcn_sched_barrier(0);
     stage(mylo, jn, 0);
     load_tiles(next, jn);
     __builtin_amdgcn_sched_barrier(0);
-    block(cur, 0, b[0], b[1]);
-    block(cur, 1, b[2], b[3]);
-    __builtin_amdgcn_s_waitcnt(0x0F76);  // vmcnt(6): the high half of step j has landed
 #pragma unroll
-    for (int s = 0; s < 4; ++s) b[s] = read_b(myhi, s);
+    for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+      for (int b = 0; b < RBW; ++b) block(cur, b, jj, bv[2 * jj], bv[2 * jj + 1]);
+    __builtin_amdgcn_s_waitcnt(kHalfWait);  // the high half of step j has landed
+#pragma unroll
+    for (int s = 0; s < 4; ++s) bv[s] = read_b(myhi, s);
     __builtin_amdgcn_s_waitcnt(0xC07F);
     __builtin_amdgcn_sched_barrier(0);
     stage(myhi, jn, 1);
     __builtin_amdgcn_sched_barrier(0);
-    block(cur, 2, b[0], b[1]);
-    block(cur, 3, b[2], b[3]);
+#pragma unroll
+    for (int jj = 2; jj < 4; ++jj)
+#pragma unroll
+      for (int b = 0; b < RBW; ++b) block(cur, b, jj, bv[2 * jj - 4], bv[2 * jj - 3]);
   };
   int j = 0;
   for (; j + 2 <= nc; j += 2) {
@@ -736,33 +781,46 @@ __global__ __launch_bounds__(kThreads) void prefill_wave_kernel(PrefillParams p)
   }
   if (j < nc) step(j, ta, tb);
 
-  // acc[r] = D[row 8(r/4) + 4h + r%4 of the block][token t0 + r32]. The four splits are summed in
-  // split order from zero through each wave's low buffer (after its last refill has landed); wave
-  // w finishes rows 8w + 4h .. + 3.
+  // acc[b][r] = D[row 8(r/4) + 4h + r%4 of block b][token t0 + r32]. The four splits are summed in
+  // split order from zero through each wave's buffers (after its last refill has landed), two
+  // blocks at a time (block 2i in the low buffer, 2i + 1 in the high one); wave w finishes rows
+  // 8w + 4h .. + 3 of each block.
   const int t = t0 + r32;
   const uint16_t *bias = static_cast<const uint16_t *>(p.bias);
+  uint16_t *y = static_cast<uint16_t *>(p.y) + (size_t)min(t, p.tokens - 1) * p.M;
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  float *mine = reinterpret_cast<float *>(mylo);
 #pragma unroll
-  for (int r = 0; r < 16; ++r) mine[r * 64 + lane] = acc[r];
-  __syncthreads();
-  if (t >= p.tokens) return;
-  const int n = n0 + 8 * split + 4 * h;
-  uint32_t out[4];
+  for (int b0 = 0; b0 < RBW; b0 += 2) {
+    if (b0 > 0) __syncthreads();  // the previous pair's sums are read
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    float total = 0.f;
+    for (int b = b0; b < b0 + 2 && b < RBW; ++b) {
+      float *mine = reinterpret_cast<float *>(b == b0 ? mylo : myhi);
 #pragma unroll
-    for (int s = 0; s < 4; ++s) total += reinterpret_cast<const float *>(xlo[s])[(4 * split + r) * 64 + lane];
-    out[r] = n + r < p.M ? out_bits<F16>(total, bias, n + r) : 0u;
-  }
-  uint16_t *y = static_cast<uint16_t *>(p.y) + (size_t)t * p.M;
-  if (n + 3 < p.M && ((reinterpret_cast<uintptr_t>(y + n) & 7) == 0)) {
-    *reinterpret_cast<uint2 *>(y + n) = make_uint2(out[0] | (out[1] << 16), out[2] | (out[3] << 16));
-  } else {
+      for (int r = 0; r < 16; ++r) mine[r * 64 + lane] = acc[b][r];
+    }
+    __syncthreads();
+    if (t < p.tokens) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-      if (n + r < p.M) y[n + r] = (uint16_t)out[r];
+      for (int b = b0; b < b0 + 2 && b < RBW; ++b) {
+        const int n = n0[b] + 8 * split + 4 * h;
+        uint32_t out[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float total = 0.f;
+#pragma unroll
+          for (int s = 0; s < 4; ++s)
+            total += reinterpret_cast<const float *>(b == b0 ? xlo[s] : xhi[s])[(4 * split + r) * 64 + lane];
+          out[r] = n + r < p.M ? out_bits<F16>(total, bias, n + r) : 0u;
+        }
+        if (n + 3 < p.M && ((reinterpret_cast<uintptr_t>(y + n) & 7) == 0)) {
+          *reinterpret_cast<uint2 *>(y + n) = make_uint2(out[0] | (out[1] << 16), out[2] | (out[3] << 16));
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (n + r < p.M) y[n + r] = (uint16_t)out[r];
+        }
+      }
+    }
   }
 }
 
@@ -1578,28 +1636,36 @@ hipError_t launch_tile(const PrefillParams &p, hipStream_t stream) {
 }
 
 template <bool F16, bool LUT>
-void launch_wave_as(const PrefillParams &p, int grid, hipStream_t stream) {
-  hipLaunchKernelGGL((prefill_wave_kernel<F16, LUT>), dim3(grid), dim3(kThreads), 0, stream, p);
+void launch_wave_as(const PrefillParams &p, hipStream_t stream) {
+  // Two row blocks per wave when that still gives every CU of the MI355X (256) a workgroup
+  // (measured: gate 5120 -> 27648 at 32 tokens 35.0 -> 27.6 us; three blocks per wave, 288
+  // workgroups, 35.9 us; four, 216 workgroups, 31.5 us).
+  const int row_blocks = (p.M + 31) / 32, token_tiles = (p.tokens + 31) / 32;
+  const int wide = (row_blocks + 1) / 2 * token_tiles;
+  if (wide >= TX_WAVE_RBW2_MIN_WGS) {
+    hipLaunchKernelGGL((prefill_wave_kernel<F16, LUT, 2>), dim3((wide + kXcds - 1) / kXcds * kXcds), dim3(kThreads), 0,
+                       stream, p);
+  } else {
+    const int wgs = row_blocks * token_tiles;
+    hipLaunchKernelGGL((prefill_wave_kernel<F16, LUT, 1>), dim3((wgs + kXcds - 1) / kXcds * kXcds), dim3(kThreads), 0,
+                       stream, p);
+  }
 }
 
-// Candidate 9: the split-group tile where a workgroup holds all four K splits of a 32-row block
-// (exactly four splits, up to 32 tokens, K a multiple of 128, partials not wanted by the caller):
-// no reduce launch, and measured
-// faster there (gate 5120 -> 27648: 35.1 vs 36.6 us at 32 tokens, 30.6 vs 34.3 us at 20). Elsewhere
-// the register-decoding 32-token tile, which was faster with split partials (down 27648 -> 5120 at
-// 32 tokens: 40.1 vs 42.0 us). Both give the same bits.
+// Candidate 9: the split-group tile where a workgroup holds all four K splits of a 32- or 64-row
+// block (exactly four splits, up to 32 tokens, K a multiple of 128, partials not wanted by the
+// caller): no reduce launch. Elsewhere the register-decoding 32-token tile, which was faster with
+// split partials (down 27648 -> 5120 at 32 tokens: 40.1 vs 42.0 us). Both give the same bits.
 hipError_t launch_small(const PrefillParams &p, hipStream_t stream) {
   if (!TX_SMALL_WAVE || p.ks != 4 || p.tokens > 32 || p.K % kTileK != 0 || p.no_reduce)
     return launch_tile<1, 1, TX_PREFILL_LA_PLAIN, false>(p, stream);
-  const int wgs = ((p.M + 31) / 32) * ((p.tokens + 31) / 32);
-  const int grid = ((wgs + kXcds - 1) / kXcds) * kXcds;
   if (p.lut) {
-    if (p.f16) launch_wave_as<true, true>(p, grid, stream);
-    else launch_wave_as<false, true>(p, grid, stream);
+    if (p.f16) launch_wave_as<true, true>(p, stream);
+    else launch_wave_as<false, true>(p, stream);
   } else if (p.f16) {
-    launch_wave_as<true, false>(p, grid, stream);
+    launch_wave_as<true, false>(p, stream);
   } else {
-    launch_wave_as<false, false>(p, grid, stream);
+    launch_wave_as<false, false>(p, stream);
   }
   return hipGetLastError();  // the four splits are summed in the tile
 }
