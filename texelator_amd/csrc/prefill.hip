@@ -727,52 +727,63 @@ __global__ __launch_bounds__(kThreads) void prefill_wave_kernel(PrefillParams p)
     for (int r = 0; r < 16; ++r) acc[b][r] = 0.f;
 
   // Block jj of row block b's weight tile into that block's MFMAs 2jj, 2jj + 1.
-  auto block = [&](const Tiles &tile, int b, int jj, const u32x4 &b0, const u32x4 &b1) {
+  auto words = [](const Tiles &tile, int b, int jj, uint32_t &wa, uint32_t &wb) {
     const uint4 &piece = tile[b][jj >> 1];
-    const uint32_t wa = (jj & 1) ? piece.z : piece.x;
-    const uint32_t wb = (jj & 1) ? piece.w : piece.y;
-    uint32_t d[8];
+    wa = (jj & 1) ? piece.z : piece.x;
+    wb = (jj & 1) ? piece.w : piece.y;
+  };
+  // Block jj of row block b's weight tile into that block's MFMAs 2jj, 2jj + 1 (palette seeds
+  // already read from the LDS tables, or the palette row from p.lut).
+  auto block = [&](const Tiles &tile, int b, int jj, const Seeds &sd, const u32x4 &b0, const u32x4 &b1) {
+    uint32_t wa, wb, d[8];
+    words(tile, b, jj, wa, wb);
     if constexpr (LUT) {
       const float4 *row = p.lut + 2 * (size_t)palette_row(wa, wb);
       decode_from_palette<F16>(row[0], row[1], wa, wb, scale[b], d);
     } else {
-      decode_block_lds<F16>(wa, wb, scale[b], pm[b], tables, d);
+      decode_from_seeds_mode<F16>(sd.base, sd.end, sd.step, sd.mode, wa, wb, scale[b], pm[b], d);
     }
     acc[b] = mfma<F16>(u32x4{d[0], d[1], d[2], d[3]}, b0, acc[b]);
     acc[b] = mfma<F16>(u32x4{d[4], d[5], d[6], d[7]}, b1, acc[b]);
   };
   // Step j multiplies weight tiles `cur` (loaded during step j - 1) and loads tiles j + 1 into
-  // `next`. Each half buffer is read into registers, then refilled with the next step's half while
-  // this step's blocks are decoded and multiplied. Loads are issued low half (4), weights (2 RBW),
-  // high half (4): 4 + 2 RBW later loads stay in flight at each half buffer's wait.
+  // `next`. Each half buffer is read into registers together with the palette seeds of the half's
+  // blocks (one LDS wait for both, so no seed read waits inside a decode), then refilled with the
+  // next step's half while this step's blocks are decoded and multiplied. Loads are issued low
+  // half (4), weights (2 RBW), high half (4): 4 + 2 RBW later loads stay in flight at each half
+  // buffer's wait.
   constexpr int kLaterLoads = 4 + 2 * RBW;
   constexpr int kHalfWait = 0x0F70 | kLaterLoads;  // vmcnt(kLaterLoads), lgkmcnt and expcnt free
-  auto step = [&](int j, const Tiles &cur, Tiles &next) {
-    const int jn = min(j + 1, nc - 1);
+  auto half = [&](int jn, int hf, uint16_t *buf, const Tiles &cur, Tiles &next) {
     u32x4 bv[4];
-    __builtin_amdgcn_s_waitcnt(kHalfWait);  // the low half of step j has landed
+    Seeds sd[2][RBW];
+    __builtin_amdgcn_s_waitcnt(kHalfWait);  // this half of step j has landed
 #pragma unroll
-    for (int s = 0; s < 4; ++s) bv[s] = read_b(mylo, s);
+    for (int s = 0; s < 4; ++s) bv[s] = read_b(buf, s);
+    if constexpr (!LUT) {
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+        for (int b = 0; b < RBW; ++b) {
+          uint32_t wa, wb;
+          words(cur, b, 2 * hf + jj, wa, wb);
+          sd[jj][b] = read_seeds(wa, wb, tables);
+        }
+    }
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the reads are done before the refill
     __builtin_amdgcn_sched_barrier(0);
-    stage(mylo, jn, 0);
-    load_tiles(next, jn);
+    stage(buf, jn, hf);
+    if (hf == 0) load_tiles(next, jn);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int jj = 0; jj < 2; ++jj)
 #pragma unroll
-      for (int b = 0; b < RBW; ++b) block(cur, b, jj, bv[2 * jj], bv[2 * jj + 1]);
-    __builtin_amdgcn_s_waitcnt(kHalfWait);  // the high half of step j has landed
-#pragma unroll
-    for (int s = 0; s < 4; ++s) bv[s] = read_b(myhi, s);
-    __builtin_amdgcn_s_waitcnt(0xC07F);
-    __builtin_amdgcn_sched_barrier(0);
-    stage(myhi, jn, 1);
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int jj = 2; jj < 4; ++jj)
-#pragma unroll
-      for (int b = 0; b < RBW; ++b) block(cur, b, jj, bv[2 * jj - 4], bv[2 * jj - 3]);
+      for (int b = 0; b < RBW; ++b) block(cur, b, 2 * hf + jj, sd[jj][b], bv[2 * jj], bv[2 * jj + 1]);
+  };
+  auto step = [&](int j, const Tiles &cur, Tiles &next) {
+    const int jn = min(j + 1, nc - 1);
+    half(jn, 0, mylo, cur, next);
+    half(jn, 1, myhi, cur, next);
   };
   int j = 0;
   for (; j + 2 <= nc; j += 2) {
