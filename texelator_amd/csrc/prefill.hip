@@ -115,6 +115,29 @@ __device__ __forceinline__ bool work_item(const PrefillParams &p, int BT, int BN
   return true;
 }
 
+// Buffer descriptor over `bytes` bytes from `base` (records clamped to 2^31 - 1; loads past the
+// end return zeros, direct-to-LDS loads past it write zeros). The tile kernels read weights and
+// stage activations through descriptors: with only buffer loads in flight the compiler counts
+// them exactly and waits for just the loads a use needs (vmcnt(N)); global_load_lds in flight
+// beside global loads made it wait for every load (vmcnt(0)), so a step's fresh loads were waited
+// for as soon as an older one was used.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *base, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0,
+                                           (int)(bytes < 0x7FFFFFFF ? bytes : 0x7FFFFFFF), 0x00020000);
+}
+
+// 16 bytes at voffset + soffset of a weight descriptor (streaming: weights are read once).
+__device__ __forceinline__ uint4 load_weights16(__amdgpu_buffer_rsrc_t r, uint32_t voffset, int soffset) {
+  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, voffset, soffset, 2 /* nt */);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// Descriptor over the tiles from tile (g, c) to the end of the matrix.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const PrefillParams &p, int g, int c) {
+  const int64_t first = (int64_t)g * p.CG + c;
+  return buffer_rsrc(p.tiles + first * 64, ((int64_t)p.RG * p.CG - first) * kTileBytes);
+}
+
 // Output staging through LDS for tiles of 128 rows. In the accumulators each lane holds four
 // consecutive rows of one token, so direct stores are 2-byte (16-bit outputs) or 16-byte (fp32
 // partials) writes to a different token row per lane; staged, a token's outputs are contiguous and
@@ -194,7 +217,17 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillParams p) {
   // Row blocks of this wave: 32 rows = tile groups 2b and 2b+1 (clamped into the matrix; rows
   // past M are computed, never stored). Lane slot (row & 15) + 16h of a tile holds blocks
   // 2h, 2h+1 of that row; slot + 32 holds blocks 4+2h, 5+2h.
-  const uint4 *gtiles[RB];
+  // The wave's tiles are read through a descriptor based at its first tile group g0 (wave-uniform;
+  // every g of the wave is at or above it), lane offsets in bytes.
+  int g0;
+  if constexpr (SWIGLU) {
+    const int half_rg = p.RG / 2;
+    g0 = min(w.n0 / kTileRows + (wave >> 1) * 2, half_rg - 1) + ((wave & 1) ? half_rg : 0);
+  } else {
+    g0 = min(w.n0 / kTileRows + wave * RB * 2, p.RG - 1);
+  }
+  const __amdgpu_buffer_rsrc_t trsrc = tile_rsrc(p, g0, w.c_begin);
+  uint32_t tlane[RB];
   float scale[RB];
   uint32_t pm[RB];
 #pragma unroll
@@ -206,17 +239,17 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillParams p) {
     } else {
       g = min(w.n0 / kTileRows + (wave * RB + b) * 2 + (r32 >> 4), p.RG - 1);
     }
-    gtiles[b] = p.tiles + ((size_t)g * p.CG + w.c_begin) * 64 + (lane & 15) + 16 * h;
+    tlane[b] = (uint32_t)(((g - g0) * p.CG * 64 + (lane & 15) + 16 * h) * 16);
     scale[b] = p.scales[g * kTileRows + (lane & 15)];
     pm[b] = pm_scale_pair<F16>(scale[b]);
   }
   // The two 16-byte pieces of each row block for one K step (past the end: the last step's).
   auto load_tiles = [&](uint4 (&slot)[RB][2], int j) {
-    const size_t off = (size_t)min(j, w.nc - 1) * 64;
+    const int off = __builtin_amdgcn_readfirstlane(min(j, w.nc - 1) * kTileBytes);
 #pragma unroll
     for (int b = 0; b < RB; ++b) {
-      slot[b][0] = load_stream(gtiles[b] + off);
-      slot[b][1] = load_stream(gtiles[b] + off + 32);
+      slot[b][0] = load_weights16(trsrc, tlane[b], off);
+      slot[b][1] = load_weights16(trsrc, tlane[b], off + 512);
     }
   };
 
@@ -228,31 +261,34 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillParams p) {
   const int scol = ((threadIdx.x & 15) ^ srow) * 8;  // step column of the chunk this thread stages
   const bool tile_full = w.t0 + BT <= p.tokens;      // uniform: no row past the tokens
   const uint32_t lane_off = (uint32_t)(srow * p.K + scol) * 2;  // bytes from row 16v, column 0
+  // Activations of the token tile through a descriptor based at its first row.
+  const __amdgpu_buffer_rsrc_t xrsrc =
+      buffer_rsrc(x + (size_t)w.t0 * p.K, (int64_t)min(BT, p.tokens - w.t0) * p.K * 2);
   auto stage_part = [&](uint16_t *buf, int j, int v0, int v1) {
     const int c = w.c_begin + j;
     if ((c + 1) * kTileK <= p.K) {
-      // Direct loads: a uniform base (row 16v of the tile, the step's first column) plus a 32-bit
-      // lane offset. Rows past the tokens repeat the last token; their outputs are never stored.
-      // The base row is clamped too, so the offset is never negative.
+      // Direct loads: a uniform offset (row 16v of the tile, the step's first column) plus a
+      // 32-bit lane offset. Rows past the tokens repeat the last token; their outputs are never
+      // stored. The base row is clamped too, so the offset is never negative.
 #pragma unroll
       for (int v = v0; v < v1; ++v) {
         const int row0 = tile_full ? w.t0 + 16 * v : min(w.t0 + 16 * v, p.tokens - 1);
-        const char *base = reinterpret_cast<const char *>(x + ((size_t)row0 * p.K + c * kTileK));
+        const int base = __builtin_amdgcn_readfirstlane(((row0 - w.t0) * p.K + c * kTileK) * 2);
         uint32_t off = lane_off;
         if (!tile_full) off = (uint32_t)((min(w.t0 + 16 * v + srow, p.tokens - 1) - row0) * p.K + scol) * 2;
-        __builtin_amdgcn_global_load_lds((const void *)(base + off),
-                                         (__attribute__((address_space(3))) void *)(buf + (16 * v + 4 * wave) * kTileK),
-                                         16, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            xrsrc, (__attribute__((address_space(3))) void *)(buf + (16 * v + 4 * wave) * kTileK), 16, off, base, 0, 0);
       }
     } else if (v0 == 0) {
-      // The matrix's last, partial K tile: columns past K are staged as zeros.
+      // The matrix's last, partial K tile: columns past K are staged as zeros (read from an
+      // offset past the descriptor's end, which returns zeros).
       const int k = c * kTileK + scol;
 #pragma unroll 2
       for (int v = 0; v < XC; ++v) {
         const int t = min(w.t0 + 16 * v + srow, p.tokens - 1);
-        uint4 value = make_uint4(0u, 0u, 0u, 0u);
-        if (k < p.K) value = *reinterpret_cast<const uint4 *>(x + (size_t)t * p.K + k);
-        *reinterpret_cast<uint4 *>(buf + (16 * v + srow) * kTileK + (threadIdx.x & 15) * 8) = value;
+        const uint32_t off = k < p.K ? (uint32_t)((t - w.t0) * p.K + k) * 2 : 0xFFFFFFF0u;
+        const u32x4 value = __builtin_amdgcn_raw_buffer_load_b128(xrsrc, off, 0, 0);
+        *reinterpret_cast<u32x4 *>(buf + (16 * v + srow) * kTileK + (threadIdx.x & 15) * 8) = value;
       }
     }
   };
@@ -878,10 +914,14 @@ __global__ __launch_bounds__(kPairThreads) void prefill_pair_kernel(PrefillParam
   // This wave's piece of each step: lane slot (row & 15) + 16h + 32*half of the row block's tiles,
   // i.e. blocks 4*half + 2h (words x, y) and 4*half + 2h + 1 (words z, w) of row l % 32.
   const int g = min(w.n0 / kTileRows + rb * 2 + (r32 >> 4), p.RG - 1);
-  const uint4 *gt = p.tiles + ((size_t)g * p.CG + w.c_begin) * 64 + (lane & 15) + 16 * h + 32 * half;
+  const int g0 = min(w.n0 / kTileRows + rb * 2, p.RG - 1);  // wave-uniform, <= g
+  const __amdgpu_buffer_rsrc_t trsrc = tile_rsrc(p, g0, w.c_begin);
+  const uint32_t tlane = (uint32_t)(((g - g0) * p.CG * 64 + (lane & 15) + 16 * h + 32 * half) * 16);
   const float scale = p.scales[g * kTileRows + (lane & 15)];
   const uint32_t pm = pm_scale_pair<F16>(scale);
-  auto load_piece = [&](int j) { return load_stream(gt + (size_t)min(j, w.nc - 1) * 64); };
+  auto load_piece = [&](int j) {
+    return load_weights16(trsrc, tlane, __builtin_amdgcn_readfirstlane(min(j, w.nc - 1) * kTileBytes));
+  };
   // Operands a[2jj + e] = positions 8e..8e+7 of local block jj (MFMA s = 4*half + 2jj + e).
   auto decode_one = [&](const uint4 &piece, int jj, u32x4 (&a)[4]) {
     const uint32_t wa = jj ? piece.z : piece.x;
@@ -903,27 +943,29 @@ __global__ __launch_bounds__(kPairThreads) void prefill_pair_kernel(PrefillParam
   const int scol = ((threadIdx.x & 15) ^ (srow & 15)) * 8;
   const bool tile_full = w.t0 + BT <= p.tokens;
   const uint32_t lane_off = (uint32_t)(srow * p.K + scol) * 2;
+  const __amdgpu_buffer_rsrc_t xrsrc =
+      buffer_rsrc(x + (size_t)w.t0 * p.K, (int64_t)min(BT, p.tokens - w.t0) * p.K * 2);
   auto stage_part = [&](uint16_t *buf, int j, int v0, int v1) {
     const int c = w.c_begin + j;
     if ((c + 1) * kTileK <= p.K) {
 #pragma unroll
       for (int v = v0; v < v1; ++v) {
         const int row0 = tile_full ? w.t0 + 32 * v : min(w.t0 + 32 * v, p.tokens - 1);
-        const char *base = reinterpret_cast<const char *>(x + ((size_t)row0 * p.K + c * kTileK));
+        const int base = __builtin_amdgcn_readfirstlane(((row0 - w.t0) * p.K + c * kTileK) * 2);
         uint32_t off = lane_off;
         if (!tile_full) off = (uint32_t)((min(w.t0 + 32 * v + srow, p.tokens - 1) - row0) * p.K + scol) * 2;
-        __builtin_amdgcn_global_load_lds((const void *)(base + off),
-                                         (__attribute__((address_space(3))) void *)(buf + (32 * v + 4 * wave) * kTileK),
-                                         16, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            xrsrc, (__attribute__((address_space(3))) void *)(buf + (32 * v + 4 * wave) * kTileK), 16, off, base, 0, 0);
       }
     } else if (v0 == 0) {
+      // Columns past K are staged as zeros (an offset past the descriptor's end reads zeros).
       const int k = c * kTileK + scol;
 #pragma unroll 2
       for (int v = 0; v < XC; ++v) {
         const int t = min(w.t0 + 32 * v + srow, p.tokens - 1);
-        uint4 value = make_uint4(0u, 0u, 0u, 0u);
-        if (k < p.K) value = *reinterpret_cast<const uint4 *>(x + (size_t)t * p.K + k);
-        *reinterpret_cast<uint4 *>(buf + (32 * v + srow) * kTileK + (threadIdx.x & 15) * 8) = value;
+        const uint32_t off = k < p.K ? (uint32_t)((t - w.t0) * p.K + k) * 2 : 0xFFFFFFF0u;
+        const u32x4 value = __builtin_amdgcn_raw_buffer_load_b128(xrsrc, off, 0, 0);
+        *reinterpret_cast<u32x4 *>(buf + (32 * v + srow) * kTileK + (threadIdx.x & 15) * 8) = value;
       }
     }
   };
