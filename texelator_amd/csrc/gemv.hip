@@ -47,16 +47,24 @@ __device__ __forceinline__ f32x4 mfma(uint32_t a0, uint32_t a1, uint32_t a2, uin
 // register, so a tile load costs no vector instruction for its address. Loads are non-temporal
 // (weights are read once per call). `bytes` bounds the descriptor; loads past it return zero.
 struct TileStream {
-  __amdgpu_buffer_rsrc_t rsrc;
+  __amdgpu_buffer_rsrc_t rsrc, spare;
   int lane_offset;
   __device__ __forceinline__ TileStream(const uint4 *first, int64_t bytes, int lane)
       : rsrc(__builtin_amdgcn_make_buffer_rsrc(const_cast<uint4 *>(first), (short)0,
                                                (int)(bytes < 0x7FFFFFFF ? bytes : 0x7FFFFFFF), 0x00020000)),
+        spare(__builtin_amdgcn_make_buffer_rsrc(const_cast<SeedTableImage *>(&kSeedTableImage), (short)0,
+                                                kSeedTableBytes, 0x00020000)),
         lane_offset(lane * 16) {}
-  // Tile j of the wave: `stride_tiles` tiles after tile j - 1.
-  __device__ __forceinline__ uint4 load(int j, int stride_tiles) const {
-    const int offset = __builtin_amdgcn_readfirstlane(j * stride_tiles * kTileBytes);
-    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rsrc, lane_offset, offset, 2 /* nt */);
+  // Tile j of the wave (`stride_tiles` tiles after tile j - 1) if j < n. The K loops issue one
+  // load per step whatever is left, so each decode waits for its own tile only; a load past the
+  // wave's n tiles reads the seed table image instead (1 KiB that every workgroup copies, so it
+  // stays in L2) and its value is never used. Re-reading the wave's last tile there, as the loops
+  // once did, fetched it from HBM again once the streaming loads had evicted it: ~7 MB per launch
+  // of the 5120 -> 27648 shape (one tile per wave).
+  __device__ __forceinline__ uint4 load(int j, int n, int stride_tiles) const {
+    const bool real = j < n;
+    const int offset = __builtin_amdgcn_readfirstlane(real ? j * stride_tiles * kTileBytes : 0);
+    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(real ? rsrc : spare, lane_offset, offset, 2 /* nt */);
     return make_uint4(v.x, v.y, v.z, v.w);
   }
 };
@@ -387,7 +395,7 @@ __global__ __launch_bounds__(kThreads, LUT || XSRC != kXRead ? 4 : TX_GEMV_WAVES
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int nt = nc > wave ? (nc - wave + kWaves - 1) / kWaves : 0;
   // Tile j of this wave is tile column c_begin + j*kWaves + wave of row group g. A wave with no
-  // tile (nc < kWaves) still issues its prefetch loads: they read the split's last column.
+  // tile (nc < kWaves) still issues its prefetch loads (TileStream::load sends them to the spare).
   const int64_t first_tile = (int64_t)g * p.CG + c_begin + min(wave, nc - 1);
   const TileStream stream(p.tiles + first_tile * 64, ((int64_t)p.RG * p.CG - first_tile) * kTileBytes, lane);
 
@@ -396,7 +404,7 @@ __global__ __launch_bounds__(kThreads, LUT || XSRC != kXRead ? 4 : TX_GEMV_WAVES
   constexpr int R = LA + 1;
   uint4 ring[R];
 #pragma unroll
-  for (int u = 0; u < LA; ++u) ring[u] = stream.load(min(u, max(nt - 1, 0)), kWaves);
+  for (int u = 0; u < LA; ++u) ring[u] = stream.load(u, nt, kWaves);
 
   const int i = lane & 15;   // weight row within the group; token column of the B operand
   const int kg = lane >> 4;  // K chunk: blocks 2kg and 2kg+1 of each tile
@@ -448,8 +456,7 @@ __global__ __launch_bounds__(kThreads, LUT || XSRC != kXRead ? 4 : TX_GEMV_WAVES
       progress_priority(nt - j0, nt);
 #pragma unroll
       for (int u = 0; u < R; ++u) {
-        const int jn = min(j0 + u + LA, nt - 1);
-        ring[(u + LA) % R] = stream.load(jn, kWaves);
+        ring[(u + LA) % R] = stream.load(j0 + u + LA, nt, kWaves);
         const TileRows next = tile_rows(lut, ring[(u + 1) % R]);  // tile j+1 (clamped near the end)
         load_xf(j0 + u);
         tile_mfma_lut<F16>(ring[u], cur, xf, scale, acc0, acc1);
@@ -470,8 +477,7 @@ __global__ __launch_bounds__(kThreads, LUT || XSRC != kXRead ? 4 : TX_GEMV_WAVES
       progress_priority(nt - j0, nt);
 #pragma unroll
       for (int u = 0; u < R; ++u) {
-        const int jn = min(j0 + u + LA, nt - 1);
-        ring[(u + LA) % R] = stream.load(jn, kWaves);
+        ring[(u + LA) % R] = stream.load(j0 + u + LA, nt, kWaves);
         load_xf(j0 + u);
         tile_mfma<F16>(ring[u], xf, scale, pm, tables, acc0, acc1);
       }
@@ -548,7 +554,7 @@ __global__ __launch_bounds__(kThreads * kFusedMaxSplits, TX_GEMV_WAVES_PER_EU) v
   constexpr int R = LA + 1;
   uint4 ring[R];
 #pragma unroll
-  for (int u = 0; u < LA; ++u) ring[u] = stream.load(min(u, max(nt - 1, 0)), kWaves);
+  for (int u = 0; u < LA; ++u) ring[u] = stream.load(u, nt, kWaves);
 
   const int i = lane & 15;
   const int kg = lane >> 4;
@@ -567,8 +573,7 @@ __global__ __launch_bounds__(kThreads * kFusedMaxSplits, TX_GEMV_WAVES_PER_EU) v
     progress_priority(nt - j0, nt);
 #pragma unroll
     for (int u = 0; u < R; ++u) {
-      const int jn = min(j0 + u + LA, nt - 1);
-      ring[(u + LA) % R] = stream.load(jn, kWaves);
+      ring[(u + LA) % R] = stream.load(j0 + u + LA, nt, kWaves);
       load_xf(j0 + u);
       tile_mfma<F16>(ring[u], xf, scale, pm, tables, acc0, acc1);
     }
@@ -639,9 +644,8 @@ __global__ __launch_bounds__(kThreads, NORM ? 4 : (LA == 1 ? 6 : (LA == 2 ? 5 : 
   uint4 ring_g[R], ring_u[R];
 #pragma unroll
   for (int u = 0; u < LA; ++u) {
-    const int j = min(u, max(nt - 1, 0));
-    ring_g[u] = gate_tiles.load(j, kWaves);
-    ring_u[u] = up_tiles.load(j, kWaves);
+    ring_g[u] = gate_tiles.load(u, nt, kWaves);
+    ring_u[u] = up_tiles.load(u, nt, kWaves);
   }
   const int i = lane & 15;
   const int kg = lane >> 4;
@@ -679,9 +683,8 @@ __global__ __launch_bounds__(kThreads, NORM ? 4 : (LA == 1 ? 6 : (LA == 2 ? 5 : 
     progress_priority(nt - j0, nt);
 #pragma unroll
     for (int u = 0; u < R; ++u) {
-      const int jn = min(j0 + u + LA, nt - 1);
-      ring_g[(u + LA) % R] = gate_tiles.load(jn, kWaves);
-      ring_u[(u + LA) % R] = up_tiles.load(jn, kWaves);
+      ring_g[(u + LA) % R] = gate_tiles.load(j0 + u + LA, nt, kWaves);
+      ring_u[(u + LA) % R] = up_tiles.load(j0 + u + LA, nt, kWaves);
       consume(u, j0 + u);
     }
   }
