@@ -708,12 +708,17 @@ __global__ __launch_bounds__(kThreads) void prefill_wave_kernel(PrefillParams p)
       const_cast<uint4 *>(p.tiles + first_tile * 64), (short)0, (int)(tile_bytes < 0x7FFFFFFF ? tile_bytes : 0x7FFFFFFF),
       0x00020000);
   typedef uint4 Tiles[RBW][2];
+  // Tiles of step j; past the split's last step (the K loop loads one step ahead whatever is
+  // left) through an empty descriptor, whose loads return zeros without touching memory, instead
+  // of re-reading the last tiles from HBM once the streaming loads have evicted them.
+  const __amdgpu_buffer_rsrc_t none = buffer_rsrc(p.tiles, 0);
   auto load_tiles = [&](Tiles &slot, int j) {
-    const int off = __builtin_amdgcn_readfirstlane(j * kTileBytes);
+    const bool real = j < nc;
+    const int off = __builtin_amdgcn_readfirstlane(real ? j * kTileBytes : 0);
 #pragma unroll
     for (int b = 0; b < RBW; ++b) {
-      const u32x4 v0 = __builtin_amdgcn_raw_buffer_load_b128(trsrc, tlane[b], off, 2 /* nt */);
-      const u32x4 v1 = __builtin_amdgcn_raw_buffer_load_b128(trsrc, tlane[b], off + 512, 2 /* nt */);
+      const u32x4 v0 = __builtin_amdgcn_raw_buffer_load_b128(real ? trsrc : none, tlane[b], off, 2 /* nt */);
+      const u32x4 v1 = __builtin_amdgcn_raw_buffer_load_b128(real ? trsrc : none, tlane[b], off + 512, 2 /* nt */);
       slot[b][0] = make_uint4(v0.x, v0.y, v0.z, v0.w);
       slot[b][1] = make_uint4(v1.x, v1.y, v1.z, v1.w);
     }
@@ -790,7 +795,7 @@ __global__ __launch_bounds__(kThreads) void prefill_wave_kernel(PrefillParams p)
   // buffer's wait.
   constexpr int kLaterLoads = 4 + 2 * RBW;
   constexpr int kHalfWait = 0x0F70 | kLaterLoads;  // vmcnt(kLaterLoads), lgkmcnt and expcnt free
-  auto half = [&](int jn, int hf, uint16_t *buf, const Tiles &cur, Tiles &next) {
+  auto half = [&](int jn, int jt, int hf, uint16_t *buf, const Tiles &cur, Tiles &next) {
     u32x4 bv[4];
     Seeds sd[2][RBW];
     __builtin_amdgcn_s_waitcnt(kHalfWait);  // this half of step j has landed
@@ -809,7 +814,7 @@ __global__ __launch_bounds__(kThreads) void prefill_wave_kernel(PrefillParams p)
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the reads are done before the refill
     __builtin_amdgcn_sched_barrier(0);
     stage(buf, jn, hf);
-    if (hf == 0) load_tiles(next, jn);
+    if (hf == 0) load_tiles(next, jt);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int jj = 0; jj < 2; ++jj)
@@ -818,8 +823,8 @@ __global__ __launch_bounds__(kThreads) void prefill_wave_kernel(PrefillParams p)
   };
   auto step = [&](int j, const Tiles &cur, Tiles &next) {
     const int jn = min(j + 1, nc - 1);
-    half(jn, 0, mylo, cur, next);
-    half(jn, 1, myhi, cur, next);
+    half(jn, j + 1, 0, mylo, cur, next);
+    half(jn, j + 1, 1, myhi, cur, next);
   };
   int j = 0;
   for (; j + 2 <= nc; j += 2) {
