@@ -286,7 +286,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillParams p) {
 #pragma unroll 2
       for (int v = 0; v < XC; ++v) {
         const int t = min(w.t0 + 16 * v + srow, p.tokens - 1);
-        const uint32_t off = k < p.K ? (uint32_t)((t - w.t0) * p.K + k) * 2 : 0xFFFFFFF0u;
+        const uint32_t off = k < p.K ? (uint32_t)((t - w.t0) * p.K + k) * 2 : 0x7FFFFFF0u;
         const u32x4 value = __builtin_amdgcn_raw_buffer_load_b128(xrsrc, off, 0, 0);
         *reinterpret_cast<u32x4 *>(buf + (16 * v + srow) * kTileK + (threadIdx.x & 15) * 8) = value;
       }
@@ -968,7 +968,7 @@ __global__ __launch_bounds__(kPairThreads) void prefill_pair_kernel(PrefillParam
 #pragma unroll 2
       for (int v = 0; v < XC; ++v) {
         const int t = min(w.t0 + 32 * v + srow, p.tokens - 1);
-        const uint32_t off = k < p.K ? (uint32_t)((t - w.t0) * p.K + k) * 2 : 0xFFFFFFF0u;
+        const uint32_t off = k < p.K ? (uint32_t)((t - w.t0) * p.K + k) * 2 : 0x7FFFFFF0u;
         const u32x4 value = __builtin_amdgcn_raw_buffer_load_b128(xrsrc, off, 0, 0);
         *reinterpret_cast<u32x4 *>(buf + (32 * v + srow) * kTileK + (threadIdx.x & 15) * 8) = value;
       }
