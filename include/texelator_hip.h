@@ -285,6 +285,13 @@ int tx_linear_split(uint64_t handle, const void *x, void *stream);
  * GEMV unsplit without LUT mode (TX_ERR_UNSUPPORTED otherwise: use tx_linear + tx_swiglu). */
 int tx_linear_swiglu(uint64_t handle, const void *x, void *out, void *stream);
 
+/* The same over two handles of one shape [inter][K], gate and up (a Hugging Face MLP's
+ * gate_proj and up_proj, each a TexelatorLinear of the reference, texelator/runtime.py:133-145,
+ * whose two GEMVs and activation product this call replaces): out bf16 [inter] bit for bit what
+ * tx_linear_swiglu gives on the merged [gate | up] handle of the two matrices. x bf16 [K], one
+ * token. TX_ERR_UNSUPPORTED for LUT-mode handles, handles with a bias or K > 16384. */
+int tx_linear_swiglu_pair(uint64_t gate, uint64_t up, const void *x, void *out, void *stream);
+
 /* The prefill of a merged [gate (inter) | up (inter)] handle with SwiGLU applied in the GEMM's
  * epilogue (no reference counterpart: the reference's prefill writes the linear output and Hugging
  * Face applies the activation): out bf16 [tokens][inter] = tx_swiglu(tx_linear(handle, x)), bit

@@ -244,6 +244,46 @@ def test_graphed_greedy_replays_equal_eager_steps(tiny_bc4):
         tiny_bc4.set_attn_implementation("sdpa")
 
 
+def test_texelator_mlp_matches_the_module_and_replays(tiny_bc4):
+    """``use_texelator_mlp``: one token through the fused gate/up SwiGLU GEMV gives the Hugging
+    Face MLP's output up to the product's single rounding (``bf16(silu(G) * U)`` against
+    ``bf16(bf16(silu(G)) * U)`` before the down projection); longer inputs take the module itself,
+    bitwise; ``GraphedGreedy`` replays still equal eager steps, with tokens mostly those of the
+    unfused model; and the modules come back on restore."""
+    from texelator_amd import hf
+
+    hidden = tiny_bc4.config.hidden_size
+    g = torch.Generator(device="cuda").manual_seed(23)
+    ids = torch.randint(0, 512, (1, 30), generator=torch.Generator().manual_seed(24)).cuda()
+    try:
+        runner = hf.GraphedGreedy(tiny_bc4, max_cache_len=256)
+        unfused = runner.generate(ids, 24)
+        originals = [layer.mlp for layer in tiny_bc4.model.layers]
+        replaced = hf.use_texelator_mlp(tiny_bc4)
+        try:
+            assert [r[2] for r in replaced] == originals
+            assert all(isinstance(layer.mlp, hf.TexelatorMLP) for layer in tiny_bc4.model.layers)
+            assert hf.use_texelator_mlp(tiny_bc4) == []  # nothing left to replace
+            mlp = tiny_bc4.model.layers[0].mlp
+            with torch.inference_mode():
+                x = torch.randn(1, 1, hidden, device="cuda", generator=g).to(torch.bfloat16)
+                got, want = mlp(x), mlp.original(x)
+                assert mlp.fused and got.shape == want.shape and got.dtype == torch.bfloat16
+                assert rrms(want, got) < 1e-2
+                xs = torch.randn(1, 5, hidden, device="cuda", generator=g).to(torch.bfloat16)
+                assert torch.equal(mlp(xs), mlp.original(xs))
+            runner = hf.GraphedGreedy(tiny_bc4, max_cache_len=256)
+            eager = runner.generate(ids, 24, eager=True)
+            graphed = runner.generate(ids, 24)
+            assert torch.equal(eager, graphed)
+            assert (graphed == unfused).float().mean() >= 0.75
+        finally:
+            hf.restore_modules(replaced)
+        assert [layer.mlp for layer in tiny_bc4.model.layers] == originals
+    finally:
+        tiny_bc4.set_attn_implementation("sdpa")
+
+
 @pytest.mark.parametrize("shape", [(7, 256), (1, 3, 2048), (2, 5120)])
 def test_texelator_rmsnorm_matches_hf_rmsnorm(ext, shape):
     """``TexelatorRMSNorm`` against the Hugging Face module on the same weight: the same formula and

@@ -465,6 +465,59 @@ def test_linear_swiglu_refuses_unsupported_handles(ext):
         ext.free(odd)
 
 
+@pytest.mark.parametrize("inter,k,lookahead", [(11008, 2048, 1), (27648, 5120, 2), (1000, 1024, 4)])
+def test_linear_swiglu_pair_is_bit_identical(ext, inter, k, lookahead):
+    """The SwiGLU GEMV over separate gate and up handles == the SwiGLU GEMV of the merged [gate | up]
+    handle of the same blocks and == linear + swiglu of that (unsplit) handle, bit for bit (inter %
+    16 == 0); against linear + linear + swiglu of the two handles, whose GEMVs may split K and sum
+    in another order, within bf16 rounding. 1000 rows leave the last row group partly empty."""
+    g = torch.Generator(device="cuda").manual_seed(inter + k)
+    blocks = [torch.randint(0, 256, (inter * k // 2,), device="cuda", dtype=torch.uint8, generator=g) for _ in range(2)]
+    scales = [(0.02 * torch.exp(0.3 * torch.randn(inter, device="cuda", generator=g))).float() for _ in range(2)]
+    gate = ext.pack_encoded_device(blocks[0], scales[0], None)
+    up = ext.pack_encoded_device(blocks[1], scales[1], None)
+    merged = ext.pack_encoded_device(torch.cat(blocks), torch.cat(scales), None) if inter % 16 == 0 else None
+    try:
+        for h in (gate, up, merged):
+            if h is not None:
+                ext.set_lookahead(h, lookahead)
+        for scale in (1.0, 30.0):  # large inputs drive silu into both saturated ends
+            x = (scale * torch.randn(1, k, device="cuda", generator=g)).to(torch.bfloat16)
+            got = layers.linear_swiglu_pair(gate, up, x)
+            assert got.shape == (1, inter)
+            near = layers.swiglu(torch.cat([ext.linear(gate, x), ext.linear(up, x)], dim=-1)).float()
+            err = (got.float() - near).norm() / near.norm()
+            assert err < 1e-2, f"relative RMS {err:.3g}"
+            if merged is not None:
+                assert ext.gemv_plan(merged)[0] == 1
+                assert torch.equal(layers.linear_swiglu(merged, x), got)
+                assert torch.equal(layers.swiglu(ext.linear(merged, x)), got)
+            again = torch.empty_like(got)
+            layers.linear_swiglu_pair(gate, up, x, again)
+            assert torch.equal(got, again)
+    finally:
+        for h in (gate, up, merged):
+            if h is not None:
+                ext.free(h)
+
+
+def test_linear_swiglu_pair_refusals(ext):
+    gate = _random_handle(ext, 256, 1024, seed=5)
+    up_bias = _random_handle(ext, 256, 1024, seed=6, bias=True)
+    other = _random_handle(ext, 512, 1024, seed=7)
+    x = torch.zeros(1, 1024, device="cuda", dtype=torch.bfloat16)
+    try:
+        with pytest.raises(_lib.UnsupportedError):
+            layers.linear_swiglu_pair(gate, up_bias, x)
+        with pytest.raises(_lib.TexelatorError, match="same shape"):
+            layers.linear_swiglu_pair(gate, other, x)
+        with pytest.raises(_lib.TexelatorError, match="wrong length"):
+            layers.linear_swiglu_pair(gate, gate, x[:, :512])
+    finally:
+        for h in (gate, up_bias, other):
+            ext.free(h)
+
+
 def test_split_decode_with_fused_swiglu_is_bit_identical(ext):
     """A model whose gate|up GEMV runs unsplit takes the fused SwiGLU epilogue in its split decode
     step; the step still equals the unsplit fused step bit for bit."""

@@ -377,6 +377,40 @@ def test_texelator_norm_replacement_and_restore():
     assert model.model.layers[1].post_attention_layernorm is original
 
 
+def test_texelator_mlp_replacement_and_restore():
+    """``use_texelator_mlp`` swaps a Hugging Face gated SiLU MLP whose gate and up projections are
+    single-handle TexelatorLinear modules without a separate bias (no GPU call: only the module
+    tree changes), leaves dense MLPs, biased, sharded or non-SiLU ones alone, and
+    ``restore_modules`` puts the originals back."""
+    transformers = pytest.importorskip("transformers")
+    from texelator_amd import hf
+    from texelator_amd.runtime import TexelatorLinear
+
+    config = transformers.Qwen2Config(vocab_size=64, hidden_size=64, intermediate_size=128, num_hidden_layers=4,
+                                      num_attention_heads=4, num_key_value_heads=2, head_dim=16,
+                                      tie_word_embeddings=False)
+    model = transformers.Qwen2ForCausalLM(config).eval()
+    assert hf.use_texelator_mlp(model) == []  # dense linears
+    layers = model.model.layers
+    for i, layer in enumerate(layers):
+        layer.mlp.gate_proj = TexelatorLinear([10 * i + 1])
+        layer.mlp.up_proj = TexelatorLinear([10 * i + 2])
+        layer.mlp.down_proj = TexelatorLinear([10 * i + 3])
+    layers[1].mlp.gate_proj = TexelatorLinear([11], bias=nn.Parameter(torch.zeros(128)))  # a separate bias
+    layers[2].mlp.up_proj = TexelatorLinear([22, 23])  # two row shards
+    layers[3].mlp.act_fn = nn.GELU()
+    originals = [layer.mlp for layer in layers]
+    replaced = hf.use_texelator_mlp(model)
+    assert [r[2] for r in replaced] == [originals[0]]
+    fused = layers[0].mlp
+    assert isinstance(fused, hf.TexelatorMLP) and fused.original is originals[0]
+    assert (fused.gate, fused.up) == (1, 2)
+    assert all(layers[i].mlp is originals[i] for i in (1, 2, 3))
+    assert hf.use_texelator_mlp(model) == []  # already swapped
+    hf.restore_modules(replaced)
+    assert [layer.mlp for layer in layers] == originals
+
+
 def test_prefill_benchmark_rejects_plain_models():
     from texelator_amd import prefill
 

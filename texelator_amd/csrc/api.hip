@@ -746,6 +746,36 @@ int tx_linear_swiglu(uint64_t value, const void *x, void *out, void *stream) {
   return TX_OK;
 }
 
+int tx_linear_swiglu_pair(uint64_t gate, uint64_t up, const void *x, void *out, void *stream) {
+  g_last_error.clear();
+  Handle *hg = as_handle(gate);
+  Handle *hu = as_handle(up);
+  if (!hg || !hu) return fail(TX_ERR_INVALID, "null Texelator handle");
+  if (!x || !out) return fail(TX_ERR_INVALID, "null input or output pointer");
+  if (reinterpret_cast<uintptr_t>(x) % 16 != 0) return fail(TX_ERR_INVALID, "input must be 16-byte aligned");
+  if (hg->M != hu->M || hg->K != hu->K || hg->device != hu->device)
+    return fail(TX_ERR_INVALID, "linear_swiglu_pair: gate and up must have the same shape and device");
+  if (hg->CG > tx::kGemvMaxLdsColumns || hg->lut || hu->lut || hg->bias || hu->bias)
+    return fail(TX_ERR_UNSUPPORTED, "linear_swiglu_pair: needs non-LUT handles without a bias, K <= 16384");
+  DeviceGuard guard(hg->device);
+  tx::GemvParams p{};
+  p.tiles = hg->tiles;
+  p.scales = hg->scales;
+  p.tiles_up = hu->tiles;
+  p.scales_up = hu->scales;
+  p.x = x;
+  p.y = out;
+  p.M = 2 * hg->M;
+  p.K = hg->K;
+  p.Mp = hg->Mp;
+  p.RG = hg->RG;
+  p.CG = hg->CG;
+  p.ks = 1;
+  p.tokens = 1;
+  TX_HIP(tx::launch_gemv_swiglu(p, hg->lookahead, reinterpret_cast<hipStream_t>(stream)));
+  return TX_OK;
+}
+
 int tx_linear_swiglu_prefill(uint64_t value, const void *x, int64_t tokens, void *out, void *stream) {
   g_last_error.clear();
   Handle *h = as_handle(value);

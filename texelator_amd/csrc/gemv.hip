@@ -621,6 +621,9 @@ __global__ __launch_bounds__(kThreads * kFusedMaxSplits, TX_GEMV_WAVES_PER_EU) v
 // each of the two row groups' sums is bit-identical to the plain GEMV's. Two rings of LA + 1 tiles
 // are in flight, so the occupancy bound falls with LA (no spills).
 // NORM: x computed by norm_x_lds (GemvParams::norm_h) instead of read.
+// With GemvParams::tiles_up the up rows come from a second handle of the same shape (row group g
+// of each; RG row groups, M = 2 * inter): the same sums, bit for bit, as the merged handle of the
+// two matrices.
 template <int LA, bool NORM = false>
 __global__ __launch_bounds__(kThreads, NORM ? 4 : (LA == 1 ? 6 : (LA == 2 ? 5 : 4))) void gemv_swiglu_kernel(GemvParams p) {
   extern __shared__ uint4 xs[];
@@ -628,7 +631,8 @@ __global__ __launch_bounds__(kThreads, NORM ? 4 : (LA == 1 ? 6 : (LA == 2 ? 5 : 
   __shared__ float red[2][kWaves][16];  // [gate|up][wave][row]
 
   const int g = blockIdx.x;
-  const int half = p.RG / 2;
+  const bool pair = p.tiles_up != nullptr;
+  const int half = pair ? 0 : p.RG / 2;  // up row group of g: g + half of tiles, or g of tiles_up
   const int nc = p.CG;
   const uint16_t *x = static_cast<const uint16_t *>(p.x);
   const int lane = threadIdx.x & 63;
@@ -637,8 +641,10 @@ __global__ __launch_bounds__(kThreads, NORM ? 4 : (LA == 1 ? 6 : (LA == 2 ? 5 : 
   const int first = min(wave, nc - 1);
   const int64_t gate_first = (int64_t)g * p.CG + first, up_first = (int64_t)(g + half) * p.CG + first;
   const int64_t total = (int64_t)p.RG * p.CG;
+  const uint4 *up_base = pair ? p.tiles_up : p.tiles;
+  const float *up_scales = pair ? p.scales_up : p.scales;
   const TileStream gate_tiles(p.tiles + gate_first * 64, (total - gate_first) * kTileBytes, lane);
-  const TileStream up_tiles(p.tiles + up_first * 64, (total - up_first) * kTileBytes, lane);
+  const TileStream up_tiles(up_base + up_first * 64, (total - up_first) * kTileBytes, lane);
 
   constexpr int R = LA + 1;
   uint4 ring_g[R], ring_u[R];
@@ -650,7 +656,7 @@ __global__ __launch_bounds__(kThreads, NORM ? 4 : (LA == 1 ? 6 : (LA == 2 ? 5 : 
   const int i = lane & 15;
   const int kg = lane >> 4;
   const float scale_g = p.scales[g * kTileRows + i];  // loaded with the tiles and x
-  const float scale_u = p.scales[(g + half) * kTileRows + i];
+  const float scale_u = up_scales[(g + half) * kTileRows + i];
   if constexpr (NORM) {
     __shared__ float norm_sums[kNormStand * kWaves];
     copy_seed_tables(tables, wave, lane, kWaves);  // in flight while x is normalized
@@ -817,7 +823,7 @@ hipError_t launch_la(const GemvParams &p, bool f32_out, hipStream_t stream) {
 
 hipError_t launch_gemv_swiglu(const GemvParams &p, int lookahead, hipStream_t stream) {
   const size_t lds = (size_t)(x_stage_chunks(p.CG) + kZeroSlotU4) * sizeof(uint4);
-  const dim3 grid(p.RG / 2);
+  const dim3 grid(p.tiles_up ? p.RG : p.RG / 2);
   if (p.norm_h || p.norm_embed) {
     switch (lookahead) {
       case 1: hipLaunchKernelGGL((gemv_swiglu_kernel<1, true>), grid, dim3(kThreads), lds, stream, p); break;

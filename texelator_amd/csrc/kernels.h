@@ -46,6 +46,10 @@ struct GemvParams {
   const uint16_t *norm_weight;
   float norm_eps;
   int norm_ks, norm_Mp;
+  // SwiGLU GEMV over two handles (gemv_swiglu_kernel): the up matrix's tiles and scales, laid out
+  // as the gate matrix's (tiles/scales, RG row groups each). nullptr: one merged [gate | up] handle.
+  const uint4 *tiles_up;
+  const float *scales_up;
 };
 
 // Hidden sizes and producer splits up to which a one-token GEMV computes the add+RMSNorm of its

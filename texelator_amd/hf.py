@@ -205,8 +205,67 @@ def use_texelator_norms(model: nn.Module) -> list[tuple[nn.Module, str, nn.Modul
     return replaced
 
 
+class TexelatorMLP(nn.Module):
+    """A Hugging Face gated MLP (``down(act(gate(x)) * up(x))`` with SiLU, Qwen2/Llama form) whose
+    gate and up projections are single-handle :class:`~texelator_amd.runtime.TexelatorLinear`
+    modules: one token runs gate, up and the SwiGLU product as one kernel
+    (:func:`~texelator_amd.layers.linear_swiglu_pair`) instead of two GEMVs, their reductions and
+    two elementwise kernels; longer inputs, and handles the fused kernel refuses (a bias, LUT mode),
+    run the original module. The product is ``bf16(silu(G) * U)`` from the bf16 projections G and
+    U, one rounding, where the original rounds ``silu(G)`` first: a token's result can differ from
+    the module's in the last bit."""
+
+    def __init__(self, original: nn.Module):
+        super().__init__()
+        self.original = original
+        self.gate = int(original.gate_proj.handles[0])
+        self.up = int(original.up_proj.handles[0])
+        self.fused = True
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        from . import layers
+        from ._lib import UnsupportedError
+
+        if self.fused and x.dtype == torch.bfloat16 and x.numel() == x.shape[-1]:
+            xc = x.contiguous()
+            if xc.data_ptr() % 16:
+                xc = xc.clone()
+            try:
+                act = layers.linear_swiglu_pair(self.gate, self.up, xc.view(-1))
+            except UnsupportedError:
+                self.fused = False
+            else:
+                return self.original.down_proj(act.view(*x.shape[:-1], act.shape[-1]))
+        return self.original(x)
+
+
+def use_texelator_mlp(model: nn.Module) -> list[tuple[nn.Module, str, nn.Module]]:
+    """Replace every gated SiLU MLP of ``model`` whose gate and up projections are single-handle
+    TexelatorLinear modules without a separate bias with :class:`TexelatorMLP`; returns ``(parent,
+    name, original)`` per replacement, for :func:`restore_modules`."""
+    from .runtime import TexelatorLinear
+
+    replaced = []
+    wrapped = [name for name, module in model.named_modules() if isinstance(module, TexelatorMLP)]
+    for name, module in list(model.named_modules()):
+        if any(name == w or name.startswith(w + ".") for w in wrapped):
+            continue  # a TexelatorMLP or the original it holds
+        gate, up = getattr(module, "gate_proj", None), getattr(module, "up_proj", None)
+        act = getattr(module, "act_fn", None)
+        if (not isinstance(gate, TexelatorLinear)
+                or not isinstance(up, TexelatorLinear) or getattr(module, "down_proj", None) is None
+                or len(gate.handles) != 1 or len(up.handles) != 1 or gate.bias is not None or up.bias is not None
+                or not (isinstance(act, nn.SiLU) or "SiLU" in type(act).__name__)):
+            continue
+        parent_name, _, child = name.rpartition(".")
+        parent = model.get_submodule(parent_name) if parent_name else model
+        setattr(parent, child, TexelatorMLP(module))
+        replaced.append((parent, child, module))
+    return replaced
+
+
 def restore_modules(replaced: list[tuple[nn.Module, str, nn.Module]]) -> None:
-    """Put back the modules :func:`use_texelator_norms` replaced."""
+    """Put back the modules :func:`use_texelator_norms` or :func:`use_texelator_mlp` replaced."""
     for parent, child, original in replaced:
         setattr(parent, child, original)
 

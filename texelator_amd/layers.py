@@ -205,6 +205,22 @@ def linear_swiglu(handle: int, x: torch.Tensor, out: torch.Tensor | None = None)
     return out
 
 
+def linear_swiglu_pair(gate: int, up: int, x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """``swiglu(linear(gate, x), linear(up, x))`` for one token over two handles of one shape, in one
+    kernel: bit for bit :func:`linear_swiglu` of the merged ``[gate | up]`` handle. Raises
+    ``UnsupportedError`` for LUT-mode handles or handles with a bias."""
+    _expect(x.is_cuda and x.dtype == torch.bfloat16 and x.is_contiguous() and x.data_ptr() % 16 == 0,
+            "x must be a contiguous, 16-byte aligned CUDA bf16 tensor")
+    m, k = _hip_shape(gate)
+    _expect(_hip_shape(up) == (m, k), "gate and up must have the same shape")
+    _expect(x.numel() == k, "x has the wrong length for these handles")
+    if out is None:
+        out = torch.empty((1, m), dtype=torch.bfloat16, device=x.device)
+    _expect(out.dtype == torch.bfloat16 and out.is_contiguous() and out.numel() == m, "bad output")
+    check(_lib.load().tx_linear_swiglu_pair(gate, up, _ptr(x), _ptr(out), _stream(x)))
+    return out
+
+
 def _norm_args(residual_in: torch.Tensor, residual_out: torch.Tensor, weight: torch.Tensor, k: int) -> None:
     for name, t in (("residual_in", residual_in), ("residual_out", residual_out)):
         _expect(t.is_cuda and t.dtype == torch.float32 and t.is_contiguous() and t.numel() == k and t.data_ptr() % 16 == 0,
