@@ -424,8 +424,8 @@ def hf_section(torch, args) -> dict:
     TexelatorLinear modules (``texelator_amd.hf.build_qwen2``), the reference's prefill protocol on
     it (``model.model(input_ids=...)``) and greedy ``model.generate`` of 256 tokens after a 512-token
     prompt, timed on the host clock (``hf.benchmark_generate``); then the same model decoding 256
-    tokens through ``hf.GraphedGreedy`` (static cache, the library's attention, norms and fused
-    gate/up SwiGLU GEMV, graph replays)."""
+    tokens through ``hf.GraphedGreedy`` (static cache, the library's attention, norms, fused gate/up
+    SwiGLU GEMV and rotary embedding kernel, graph replays)."""
     from texelator_amd import hf, modeling, prefill
     from texelator_amd.runtime import free
 
@@ -441,6 +441,7 @@ def hf_section(torch, args) -> dict:
         gen = hf.benchmark_generate(model, prompt_tokens=args.prompt, new_tokens=256, runs=2)
         hf.use_texelator_norms(model)
         hf.use_texelator_mlp(model)
+        hf.use_texelator_rope(model)
         graphed = hf.GraphedGreedy(model, max_cache_len=args.prompt + 264).benchmark(args.prompt, 256)
     finally:
         free(handles)
@@ -460,8 +461,9 @@ def hf_section(torch, args) -> dict:
         "generate_seconds": round(gen["generate_seconds"], 3),
         "graphed_decode_tok_s": round(graphed["decode_tok_s"], 2),
         "graphed_path": "hf.GraphedGreedy: static KV cache, the library's attention and RMSNorm kernels "
-                        "(hf.use_texelator_norms), the gate/up SwiGLU GEMV (hf.use_texelator_mlp), the one-token "
-                        "forward replayed from a HIP graph (device clock)",
+                        "(hf.use_texelator_norms), the gate/up SwiGLU GEMV (hf.use_texelator_mlp), the rotary "
+                        "embedding kernel (hf.use_texelator_rope), the one-token forward replayed from a HIP graph "
+                        "(device clock)",
     }
 
 

@@ -292,6 +292,15 @@ int tx_linear_swiglu(uint64_t handle, const void *x, void *out, void *stream);
  * token. TX_ERR_UNSUPPORTED for LUT-mode handles, handles with a bias or K > 16384. */
 int tx_linear_swiglu_pair(uint64_t gate, uint64_t up, const void *x, void *out, void *stream);
 
+/* Rotary embedding of q bf16 [tokens][heads][head_dim] and k bf16 [tokens][kv_heads][head_dim] in
+ * the "rotate half" form of a Hugging Face Llama/Qwen2 attention module (its
+ * apply_rotary_pos_emb, which the reference's Hugging Face path runs as several elementwise
+ * kernels; no counterpart in the reference's own code) with cos/sin bf16 [tokens][head_dim]:
+ * out = bf16(bf16(x * cos) + bf16(rotate_half(x) * sin)), bit for bit torch's bf16 result, into
+ * q_out and k_out (same shapes) in one launch. head_dim even, at most 512. */
+int tx_rope_rotate_half(const void *q, const void *k, int64_t tokens, int heads, int kv_heads, int head_dim,
+                        const void *cos, const void *sin, void *q_out, void *k_out, void *stream);
+
 /* The prefill of a merged [gate (inter) | up (inter)] handle with SwiGLU applied in the GEMM's
  * epilogue (no reference counterpart: the reference's prefill writes the linear output and Hugging
  * Face applies the activation): out bf16 [tokens][inter] = tx_swiglu(tx_linear(handle, x)), bit

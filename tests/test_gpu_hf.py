@@ -284,6 +284,59 @@ def test_texelator_mlp_matches_the_module_and_replays(tiny_bc4):
         tiny_bc4.set_attn_implementation("sdpa")
 
 
+@pytest.mark.parametrize("batch,tokens,heads,kv_heads,dim", [(1, 1, 16, 2, 128), (1, 7, 16, 2, 128),
+                                                            (2, 5, 8, 8, 64), (1, 3, 40, 8, 128)])
+def test_rope_rotate_half_matches_hf(ext, batch, tokens, heads, kv_heads, dim):
+    """``layers.rope_rotate_half`` == Hugging Face's ``apply_rotary_pos_emb`` on bf16 q, k and the
+    model's own cos/sin, bit for bit (the same bf16 roundings of both products and of the sum)."""
+    from transformers import Qwen2Config
+    from transformers.models.qwen2.modeling_qwen2 import Qwen2RotaryEmbedding, apply_rotary_pos_emb
+
+    from texelator_amd import layers
+
+    g = torch.Generator(device="cuda").manual_seed(tokens * heads + dim)
+    q = (3 * torch.randn(batch, tokens, heads, dim, device="cuda", generator=g)).to(torch.bfloat16)
+    k = (3 * torch.randn(batch, tokens, kv_heads, dim, device="cuda", generator=g)).to(torch.bfloat16)
+    config = Qwen2Config(hidden_size=heads * dim, num_attention_heads=heads, num_key_value_heads=kv_heads,
+                         head_dim=dim, rope_theta=1e6)
+    rotary = Qwen2RotaryEmbedding(config).to("cuda")
+    positions = torch.randint(0, 4096, (batch, tokens), device="cuda", generator=g)
+    cos, sin = rotary(q, positions)
+    want_q, want_k = apply_rotary_pos_emb(q.transpose(1, 2), k.transpose(1, 2), cos, sin)
+    got_q, got_k = layers.rope_rotate_half(q, k, cos.contiguous(), sin.contiguous())
+    assert torch.equal(want_q.transpose(1, 2), got_q) and torch.equal(want_k.transpose(1, 2), got_k)
+
+
+def test_texelator_rope_model_is_bitwise_the_module(tiny_bc4):
+    """``use_texelator_rope`` on the BC4 Qwen2: prompt logits bitwise those of the unchanged model
+    (the kernel reproduces the module's rotary embedding exactly), ``GraphedGreedy`` tokens the
+    unchanged runner's, replays equal to eager steps; ``restore_rope`` undoes it."""
+    from texelator_amd import hf
+
+    ids = torch.randint(0, 512, (1, 30), generator=torch.Generator().manual_seed(25)).cuda()
+    try:
+        tiny_bc4.set_attn_implementation("sdpa")
+        with torch.inference_mode():
+            want = tiny_bc4(ids).logits
+        runner = hf.GraphedGreedy(tiny_bc4, max_cache_len=256)
+        unchanged = runner.generate(ids, 24)
+        changed = hf.use_texelator_rope(tiny_bc4)
+        try:
+            assert len(changed) == len(tiny_bc4.model.layers)
+            tiny_bc4.set_attn_implementation("sdpa")
+            with torch.inference_mode():
+                assert torch.equal(want, tiny_bc4(ids).logits)
+            runner = hf.GraphedGreedy(tiny_bc4, max_cache_len=256)
+            eager = runner.generate(ids, 24, eager=True)
+            graphed = runner.generate(ids, 24)
+            assert torch.equal(eager, graphed) and torch.equal(graphed, unchanged)
+        finally:
+            hf.restore_rope(changed)
+        assert all("forward" not in layer.self_attn.__dict__ for layer in tiny_bc4.model.layers)
+    finally:
+        tiny_bc4.set_attn_implementation("sdpa")
+
+
 @pytest.mark.parametrize("shape", [(7, 256), (1, 3, 2048), (2, 5120)])
 def test_texelator_rmsnorm_matches_hf_rmsnorm(ext, shape):
     """``TexelatorRMSNorm`` against the Hugging Face module on the same weight: the same formula and

@@ -411,6 +411,31 @@ def test_texelator_mlp_replacement_and_restore():
     assert [layer.mlp for layer in layers] == originals
 
 
+def test_texelator_rope_forward_replacement_and_restore():
+    """``use_texelator_rope`` gives every Qwen2 attention module a forward that runs the module's own
+    steps around the rotary embedding; off the GPU (here: fp32 on the CPU) it takes Hugging Face's
+    ``apply_rotary_pos_emb``, so the model's logits are bitwise the unchanged model's; a second call
+    changes nothing and ``restore_rope`` gives back the class's forward."""
+    transformers = pytest.importorskip("transformers")
+    from texelator_amd import hf
+
+    config = transformers.Qwen2Config(vocab_size=64, hidden_size=64, intermediate_size=128, num_hidden_layers=2,
+                                      num_attention_heads=4, num_key_value_heads=2, head_dim=16,
+                                      tie_word_embeddings=False)
+    torch.manual_seed(5)
+    model = transformers.Qwen2ForCausalLM(config).eval()
+    ids = torch.randint(0, 64, (1, 9), generator=torch.Generator().manual_seed(6))
+    with torch.no_grad():
+        want = model(ids).logits
+        changed = hf.use_texelator_rope(model)
+        assert len(changed) == 2 and all("forward" in m.__dict__ for m in changed)
+        assert hf.use_texelator_rope(model) == []
+        got = model(ids).logits
+    assert torch.equal(want, got)
+    hf.restore_rope(changed)
+    assert all("forward" not in m.__dict__ for m in changed)
+
+
 def test_prefill_benchmark_rejects_plain_models():
     from texelator_amd import prefill
 

@@ -1197,4 +1197,19 @@ int tx_swiglu(const void *gate_up, int64_t rows, int64_t intermediate, void *out
   return TX_OK;
 }
 
+int tx_rope_rotate_half(const void *q, const void *k, int64_t tokens, int heads, int kv_heads, int head_dim,
+                        const void *cos, const void *sin, void *q_out, void *k_out, void *stream) {
+  g_last_error.clear();
+  if (!q || !k || !cos || !sin || !q_out || !k_out) return fail(TX_ERR_INVALID, "rope_rotate_half: null pointer");
+  if (tokens < 0 || heads <= 0 || kv_heads <= 0 || head_dim <= 0 || head_dim % 2 || head_dim > 512 ||
+      tokens > 0x7FFFFFFF || heads + kv_heads > 65535)
+    return fail(TX_ERR_INVALID, "rope_rotate_half: bad shape (head_dim even and at most 512)");
+  if (tokens == 0) return TX_OK;
+  TX_HIP(tx::launch_rope_rotate_half(static_cast<const uint16_t *>(q), static_cast<const uint16_t *>(k), tokens, heads,
+                                     kv_heads, head_dim, static_cast<const uint16_t *>(cos),
+                                     static_cast<const uint16_t *>(sin), static_cast<uint16_t *>(q_out),
+                                     static_cast<uint16_t *>(k_out), reinterpret_cast<hipStream_t>(stream)));
+  return TX_OK;
+}
+
 }  // extern "C"

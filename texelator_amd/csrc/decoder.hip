@@ -899,6 +899,31 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const uint16_t *gu, int64_t
   *reinterpret_cast<uint4 *>(out + r * inter + c) = swiglu8(gv, uv);
 }
 
+// Rotary embedding in the "rotate half" form of Hugging Face's Llama/Qwen2 models, with their
+// bf16 rounding steps: for the head row x of token t (halves x1 = x[:d/2], x2 = x[d/2:]) and that
+// token's cos/sin rows, out = bf16(bf16(x * cos) + bf16(rotate_half(x) * sin)), rotate_half(x) =
+// [-x2, x1]: each bf16 product exact in fp32 then rounded, the sum in fp32 then rounded, which is
+// what torch's bf16 elementwise kernels compute for q * cos + rotate_half(q) * sin. Block (t, r):
+// row r of token t, query heads then key heads; thread i handles positions i and i + d/2.
+__global__ __launch_bounds__(256) void rope_rotate_half_kernel(const uint16_t *q, const uint16_t *k, int heads,
+                                                               int kv_heads, int dim, const uint16_t *cos,
+                                                               const uint16_t *sin, uint16_t *q_out,
+                                                               uint16_t *k_out) {
+  const int64_t t = blockIdx.x;
+  const int r = blockIdx.y;
+  const int i = threadIdx.x, half = dim / 2;
+  const bool is_q = r < heads;
+  const int64_t row = is_q ? t * heads + r : t * kv_heads + (r - heads);
+  const uint16_t *x = (is_q ? q : k) + row * dim;
+  uint16_t *o = (is_q ? q_out : k_out) + row * dim;
+  const uint16_t *c = cos + t * dim, *s = sin + t * dim;
+  const float x1 = bf(x[i]), x2 = bf(x[i + half]);
+  const float lo = bf(to_bf(x1 * bf(c[i]))) + bf(to_bf(-x2 * bf(s[i])));
+  const float hi = bf(to_bf(x2 * bf(c[i + half]))) + bf(to_bf(x1 * bf(s[i + half])));
+  o[i] = to_bf(lo);
+  o[i + half] = to_bf(hi);
+}
+
 }  // namespace
 
 hipError_t launch_add_rmsnorm(float *h, const uint16_t *delta, const uint16_t *weight, float eps, uint16_t *out,
@@ -1040,6 +1065,14 @@ hipError_t launch_lm_head_argmax(const uint16_t *weight, int64_t vocab, int hidd
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(lm_head_argmax_final_kernel, dim3(1), dim3(kHeadThreads), 0, stream, part_val, part_idx, blocks, token);
+  return hipGetLastError();
+}
+
+hipError_t launch_rope_rotate_half(const uint16_t *q, const uint16_t *k, int64_t tokens, int heads, int kv_heads,
+                                   int dim, const uint16_t *cos, const uint16_t *sin, uint16_t *q_out, uint16_t *k_out,
+                                   hipStream_t stream) {
+  hipLaunchKernelGGL(rope_rotate_half_kernel, dim3((unsigned)tokens, (unsigned)(heads + kv_heads)), dim3(dim / 2), 0,
+                     stream, q, k, heads, kv_heads, dim, cos, sin, q_out, k_out);
   return hipGetLastError();
 }
 

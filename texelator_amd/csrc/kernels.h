@@ -197,6 +197,11 @@ hipError_t launch_prefill_attention(const uint16_t *q, int64_t q_stride, const u
                                     const uint16_t *v_cache, int64_t tokens, int heads, int kv_heads, int64_t max_ctx,
                                     float scale, uint16_t *out, int64_t out_stride, hipStream_t stream);
 hipError_t launch_swiglu(const uint16_t *gu, int64_t rows, int64_t inter, uint16_t *out, hipStream_t stream);
+// Hugging Face's "rotate half" rotary embedding with its bf16 rounding steps: q [tokens][heads][dim]
+// and k [tokens][kv_heads][dim] with cos/sin [tokens][dim], all bf16 (dim even, <= 512).
+hipError_t launch_rope_rotate_half(const uint16_t *q, const uint16_t *k, int64_t tokens, int heads, int kv_heads,
+                                   int dim, const uint16_t *cos, const uint16_t *sin, uint16_t *q_out, uint16_t *k_out,
+                                   hipStream_t stream);
 // Greedy next token of a dense bf16 lm_head [vocab][hidden] (hidden a multiple of 128, at most
 // 16384) for one bf16 hidden state: token[0] = the first row with the largest bf16 logit (fp32
 // sums); logits (bf16 [vocab]) written too unless null. Workspace: lm_head_argmax_workspace() bytes.

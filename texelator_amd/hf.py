@@ -264,6 +264,58 @@ def use_texelator_mlp(model: nn.Module) -> list[tuple[nn.Module, str, nn.Module]
     return replaced
 
 
+def _rope_attention_forward(self, hidden_states: torch.Tensor, position_embeddings: tuple[torch.Tensor, torch.Tensor],
+                            attention_mask: torch.Tensor | None, past_key_values=None, **kwargs):
+    """A Qwen2 attention module's forward with its rotary embedding on the library's kernel
+    (:func:`~texelator_amd.layers.rope_rotate_half`: one launch, bitwise the module's result) and
+    every other step as the module does it: the projections, the cache update, the configured
+    attention function and the output projection."""
+    import sys
+
+    from . import layers
+
+    hf_module = sys.modules[type(self).__module__]
+    input_shape = hidden_states.shape[:-1]
+    hidden_shape = (*input_shape, -1, self.head_dim)
+    q = self.q_proj(hidden_states).view(hidden_shape)  # [batch, tokens, heads, head_dim]
+    k = self.k_proj(hidden_states).view(hidden_shape)
+    v = self.v_proj(hidden_states).view(hidden_shape).transpose(1, 2)
+    cos, sin = position_embeddings  # [batch, tokens, head_dim]
+    if q.is_cuda and q.dtype == cos.dtype == torch.bfloat16 and cos.shape[:-1] == q.shape[:-2]:
+        q, k = layers.rope_rotate_half(q.contiguous(), k.contiguous(), cos.contiguous(), sin.contiguous())
+        q, k = q.transpose(1, 2), k.transpose(1, 2)
+    else:
+        q, k = hf_module.apply_rotary_pos_emb(q.transpose(1, 2), k.transpose(1, 2), cos, sin)
+    if past_key_values is not None:
+        k, v = past_key_values.update(k, v, self.layer_idx)
+    attention = hf_module.ALL_ATTENTION_FUNCTIONS.get_interface(self.config._attn_implementation,
+                                                                 hf_module.eager_attention_forward)
+    out, weights = attention(self, q, k, v, attention_mask, dropout=0.0 if not self.training else self.attention_dropout,
+                             scaling=self.scaling, sliding_window=self.sliding_window, **kwargs)
+    return self.o_proj(out.reshape(*input_shape, -1).contiguous()), weights
+
+
+def use_texelator_rope(model: nn.Module) -> list[nn.Module]:
+    """Give every Qwen2 attention module of ``model`` :func:`_rope_attention_forward` (its rotary
+    embedding as one library kernel instead of Hugging Face's elementwise ones, bit for bit the
+    same); returns the modules changed, for :func:`restore_rope`."""
+    import types
+
+    changed = []
+    for module in model.modules():
+        if type(module).__name__ != "Qwen2Attention" or "forward" in module.__dict__:
+            continue
+        module.forward = types.MethodType(_rope_attention_forward, module)
+        changed.append(module)
+    return changed
+
+
+def restore_rope(changed: list[nn.Module]) -> None:
+    """Give the modules :func:`use_texelator_rope` changed their class's forward back."""
+    for module in changed:
+        module.__dict__.pop("forward", None)
+
+
 def restore_modules(replaced: list[tuple[nn.Module, str, nn.Module]]) -> None:
     """Put back the modules :func:`use_texelator_norms` or :func:`use_texelator_mlp` replaced."""
     for parent, child, original in replaced:

@@ -426,6 +426,26 @@ def lm_head_argmax(weight: torch.Tensor, x: torch.Tensor, workspace: torch.Tenso
     return out
 
 
+def rope_rotate_half(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Hugging Face's ``apply_rotary_pos_emb`` (rotate-half form) on ``q`` ``[..., tokens, heads,
+    dim]`` and ``k`` ``[..., tokens, kv_heads, dim]`` (contiguous bf16, the projections' own layout)
+    with ``cos``/``sin`` ``[..., tokens, dim]`` bf16, bit for bit, in one kernel; returns new
+    ``(q, k)`` of the same shapes."""
+    _expect(all(t.is_cuda and t.dtype == torch.bfloat16 and t.is_contiguous() for t in (q, k, cos, sin)),
+            "q, k, cos and sin must be contiguous CUDA bf16 tensors")
+    dim = q.shape[-1]
+    tokens = cos.numel() // dim
+    _expect(cos.shape == sin.shape and cos.shape[-1] == dim and k.shape[-1] == dim and q.dim() >= 2 and k.dim() >= 2,
+            "cos and sin must be [tokens, dim] rows of the heads' dim")
+    _expect(q.numel() % (tokens * dim) == 0 and k.numel() % (tokens * dim) == 0, "q and k must hold whole tokens")
+    heads, kv_heads = q.numel() // (tokens * dim), k.numel() // (tokens * dim)
+    _expect(q.shape[-2] == heads and k.shape[-2] == kv_heads, "q and k must be [tokens, heads, dim]")
+    q_out, k_out = torch.empty_like(q), torch.empty_like(k)
+    check(_lib.load().tx_rope_rotate_half(_ptr(q), _ptr(k), tokens, heads, kv_heads, dim, _ptr(cos), _ptr(sin),
+                                          _ptr(q_out), _ptr(k_out), _stream(q)))
+    return q_out, k_out
+
+
 def swiglu(gate_up: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
     """``bf16(silu(g) * u)`` for rows ``[g | u]``."""
     _expect(gate_up.dtype == torch.bfloat16 and gate_up.is_contiguous() and gate_up.dim() == 2 and gate_up.shape[1] % 2 == 0,
