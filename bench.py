@@ -462,7 +462,8 @@ def hf_section(torch, args) -> dict:
         "graphed_decode_tok_s": round(graphed["decode_tok_s"], 2),
         "graphed_path": "hf.GraphedGreedy: static KV cache, the library's attention and RMSNorm kernels "
                         "(hf.use_texelator_norms), the gate/up SwiGLU GEMV (hf.use_texelator_mlp), the rotary "
-                        "embedding kernel (hf.use_texelator_rope), the one-token forward replayed from a HIP graph "
+                        "embedding kernel (hf.use_texelator_rope), q/k/v biases added in the GEMV epilogue "
+                        "(tx_linear_add_bias), the one-token forward replayed from a HIP graph "
                         "(device clock)",
     }
 

@@ -292,6 +292,14 @@ int tx_linear_swiglu(uint64_t handle, const void *x, void *out, void *stream);
  * token. TX_ERR_UNSUPPORTED for LUT-mode handles, handles with a bias or K > 16384. */
 int tx_linear_swiglu_pair(uint64_t gate, uint64_t up, const void *x, void *out, void *stream);
 
+/* One token: y bf16 [M] = bf16(bf16(x W^T) + bias), x bf16 [K], bias bf16 [M], for a handle without a
+ * bias of its own: tx_linear followed by a bf16 add of a separate bias parameter (the reference's
+ * TexelatorLinear with a module bias, texelator/runtime.py:141-145, y = linear(x) + bias; the
+ * standalone loader's modules carry their bias that way), bit for bit, with the add done in the
+ * GEMV's own epilogue or reduction. Uses the handle's split-K buffer (calls on one handle must not
+ * overlap). */
+int tx_linear_add_bias(uint64_t handle, const void *x, const void *bias, void *y, void *stream);
+
 /* Rotary embedding of q bf16 [tokens][heads][head_dim] and k bf16 [tokens][kv_heads][head_dim] in
  * the "rotate half" form of a Hugging Face Llama/Qwen2 attention module (its
  * apply_rotary_pos_emb, which the reference's Hugging Face path runs as several elementwise

@@ -11,7 +11,7 @@ import pytest
 import torch
 from torch.nn import functional
 
-from texelator_amd import _lib, layers, modeling, prefill
+from texelator_amd import _lib, layers, modeling, prefill, runtime
 
 pytestmark = pytest.mark.gpu
 
@@ -516,6 +516,43 @@ def test_linear_swiglu_pair_refusals(ext):
     finally:
         for h in (gate, up_bias, other):
             ext.free(h)
+
+
+@pytest.mark.parametrize("m,k", [(2560, 2048), (5120, 5120), (1024, 5120), (16384, 256), (1000, 1024)])
+def test_linear_add_bias_is_bit_identical(ext, m, k):
+    """linear_add_bias == linear(x) + bias in bf16 (two roundings), bit for bit, whatever the
+    handle's one-token plan: every K split in one workgroup, split partials plus the reduce kernel,
+    or unsplit; at two lookaheads and at inputs large enough that the second rounding matters."""
+    handle = _random_handle(ext, m, k, seed=m + k)
+    try:
+        g = torch.Generator(device="cuda").manual_seed(m - k)
+        bias = (0.5 * torch.randn(m, device="cuda", generator=g)).to(torch.bfloat16)
+        for la in (1, 2):
+            ext.set_lookahead(handle, la)
+            for scale in (1.0, 40.0):
+                x = (scale * torch.randn(1, k, device="cuda", generator=g)).to(torch.bfloat16)
+                want = ext.linear(handle, x) + bias
+                got = layers.linear_add_bias(handle, x, bias)
+                assert got.shape == (1, m)
+                assert torch.equal(got, want), (la, scale)
+        module = runtime.TexelatorLinear([handle], bias=torch.nn.Parameter(bias, requires_grad=False))
+        x3 = x.reshape(1, 1, k)
+        assert torch.equal(module(x3), (ext.linear(handle, x) + bias).reshape(1, 1, m))
+    finally:
+        ext.free(handle)
+
+
+def test_linear_add_bias_refuses_a_handle_with_its_own_bias(ext):
+    handle = _random_handle(ext, 256, 1024, seed=9, bias=True)
+    try:
+        x = torch.zeros(1, 1024, device="cuda", dtype=torch.bfloat16)
+        bias = torch.zeros(256, device="cuda", dtype=torch.bfloat16)
+        with pytest.raises(_lib.TexelatorError, match="own bias"):
+            layers.linear_add_bias(handle, x, bias)
+        with pytest.raises(_lib.TexelatorError, match="one token"):
+            layers.linear_add_bias(handle, torch.zeros(2, 1024, device="cuda", dtype=torch.bfloat16), bias)
+    finally:
+        ext.free(handle)
 
 
 def test_split_decode_with_fused_swiglu_is_bit_identical(ext):

@@ -66,6 +66,7 @@ SIGNATURES = {
     "tx_linear_swiglu": (_I32, [_U64, _P, _P, _P]),
     "tx_linear_swiglu_pair": (_I32, [_U64, _U64, _P, _P, _P]),
     "tx_rope_rotate_half": (_I32, [_P, _P, _I64, _I32, _I32, _I32, _P, _P, _P, _P, _P]),
+    "tx_linear_add_bias": (_I32, [_U64, _P, _P, _P, _P]),
     "tx_linear_swiglu_prefill": (_I32, [_U64, _P, _I64, _P, _P]),
     "tx_prefill_attention": (_I32, [_P, _I64, _P, _P, _I64, _I32, _I32, _I32, _I64, ctypes.c_float, _P, _I64, _P]),
     "tx_stream_read": (_I32, [_P, _I64, _P, _P]),

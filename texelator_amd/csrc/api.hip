@@ -445,6 +445,36 @@ int tx_linear(uint64_t value, const void *x, int x_dtype, int64_t x_numel, int64
   return run_gemv(h, x, f16, tokens, y, false, s, own ? static_cast<float *>(workspace) : h->partials);
 }
 
+int tx_linear_add_bias(uint64_t value, const void *x, const void *bias, void *y, void *stream) {
+  g_last_error.clear();
+  Handle *h = as_handle(value);
+  if (!h) return fail(TX_ERR_INVALID, "null Texelator handle");
+  if (!x || !bias || !y) return fail(TX_ERR_INVALID, "null input, bias or output pointer");
+  if (reinterpret_cast<uintptr_t>(x) % 16 != 0) return fail(TX_ERR_INVALID, "input must be 16-byte aligned");
+  if (reinterpret_cast<uintptr_t>(bias) % 2 != 0) return fail(TX_ERR_INVALID, "bias must be 2-byte aligned");
+  if (h->bias) return fail(TX_ERR_INVALID, "linear_add_bias: the handle carries its own bias");
+  DeviceGuard guard(h->device);
+  tx::GemvParams p{};
+  p.lut = h->lut;
+  p.tiles = h->tiles;
+  p.scales = h->scales;
+  p.x = x;
+  p.bias = bias;
+  p.bias_round_first = 1;
+  p.y = y;
+  p.M = h->M;
+  p.K = h->K;
+  p.Mp = h->Mp;
+  p.RG = h->RG;
+  p.CG = h->CG;
+  p.tokens = 1;
+  p.ks = h->gemv_splits;
+  p.partials = h->partials;
+  p.fused = one_token_fused(h) ? 1 : 0;
+  TX_HIP(tx::launch_gemv(p, h->lookahead, false, reinterpret_cast<hipStream_t>(stream)));
+  return TX_OK;
+}
+
 int tx_linear_noalloc(uint64_t value, const void *x, int x_dtype, int64_t x_numel, int64_t x_last, int device, void *y,
                       void *stream) {
   g_last_error.clear();

@@ -514,7 +514,10 @@ __global__ __launch_bounds__(kThreads, LUT || XSRC != kXRead ? 4 : TX_GEMV_WAVES
       if constexpr (F32OUT) {
         static_cast<float *>(p.y)[(size_t)token * p.M + out_row] = total;
       } else {
-        if (p.bias) total += half_bits_to_float<F16>(static_cast<const uint16_t *>(p.bias)[out_row]);
+        if (p.bias) {
+          if (p.bias_round_first) total = F16 ? (float)(_Float16)total : bf(to_bf(total));
+          total += half_bits_to_float<F16>(static_cast<const uint16_t *>(p.bias)[out_row]);
+        }
         if constexpr (F16) static_cast<_Float16 *>(p.y)[(size_t)token * p.M + out_row] = (_Float16)total;
         else static_cast<__bf16 *>(p.y)[(size_t)token * p.M + out_row] = (__bf16)total;
       }
@@ -606,7 +609,10 @@ __global__ __launch_bounds__(kThreads * kFusedMaxSplits, TX_GEMV_WAVES_PER_EU) v
       if constexpr (F32OUT) {
         static_cast<float *>(p.y)[out_row] = total;
       } else {
-        if (p.bias) total += half_bits_to_float<F16>(static_cast<const uint16_t *>(p.bias)[out_row]);
+        if (p.bias) {
+          if (p.bias_round_first) total = F16 ? (float)(_Float16)total : bf(to_bf(total));
+          total += half_bits_to_float<F16>(static_cast<const uint16_t *>(p.bias)[out_row]);
+        }
         if constexpr (F16) static_cast<_Float16 *>(p.y)[out_row] = (_Float16)total;
         else static_cast<__bf16 *>(p.y)[out_row] = (__bf16)total;
       }
@@ -738,7 +744,8 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemvParams p) {
   const int m = blockIdx.x * 256 + threadIdx.x;
   const int token = blockIdx.y;
   if (m >= p.M) return;
-  const SplitSource src{p.partials, F32OUT ? nullptr : static_cast<const uint16_t *>(p.bias), p.ks, p.Mp, p.tokens};
+  const SplitSource src{p.partials, F32OUT ? nullptr : static_cast<const uint16_t *>(p.bias), p.ks, p.Mp, p.tokens,
+                        F32OUT ? 0 : p.bias_round_first};
   const int64_t cols[1] = {m};
   float sums[1];
   split_sums<1, F16, KS>(src, token, cols, sums);

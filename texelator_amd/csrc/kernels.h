@@ -50,6 +50,9 @@ struct GemvParams {
   // as the gate matrix's (tiles/scales, RG row groups each). nullptr: one merged [gate | up] handle.
   const uint4 *tiles_up;
   const float *scales_up;
+  // One token: the sum is rounded to the output type before the bias is added (then rounded again),
+  // as a caller adding a separate bias to the GEMV's output would; 0: one rounding of sum + bias.
+  int bias_round_first;
 };
 
 // Hidden sizes and producer splits up to which a one-token GEMV computes the add+RMSNorm of its

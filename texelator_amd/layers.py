@@ -205,6 +205,23 @@ def linear_swiglu(handle: int, x: torch.Tensor, out: torch.Tensor | None = None)
     return out
 
 
+def linear_add_bias(handle: int, x: torch.Tensor, bias: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """``linear(handle, x) + bias`` for one bf16 token and a separate bf16 bias ``[M]`` (the handle
+    has none of its own): the GEMV's bf16 output plus the bias rounded again, bit for bit the two
+    operations, in the GEMV's own launches. Returns ``[..., M]`` shaped like ``x``."""
+    _expect(x.is_cuda and x.dtype == torch.bfloat16 and x.is_contiguous() and x.data_ptr() % 16 == 0,
+            "x must be a contiguous, 16-byte aligned CUDA bf16 tensor")
+    m, k = _hip_shape(handle)
+    _expect(x.numel() == k and x.shape[-1] == k, "x must be one token of this handle's K")
+    _expect(bias.is_cuda and bias.dtype == torch.bfloat16 and bias.is_contiguous() and bias.numel() == m,
+            "bias must be a contiguous CUDA bf16 [M]")
+    if out is None:
+        out = torch.empty((*x.shape[:-1], m), dtype=torch.bfloat16, device=x.device)
+    _expect(out.dtype == torch.bfloat16 and out.is_contiguous() and out.numel() == m, "bad output")
+    check(_lib.load().tx_linear_add_bias(handle, _ptr(x), _ptr(bias), _ptr(out), _stream(x)))
+    return out
+
+
 def linear_swiglu_pair(gate: int, up: int, x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
     """``swiglu(linear(gate, x), linear(up, x))`` for one token over two handles of one shape, in one
     kernel: bit for bit :func:`linear_swiglu` of the merged ``[gate | up]`` handle. Raises
