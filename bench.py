@@ -425,7 +425,8 @@ def hf_section(torch, args) -> dict:
     it (``model.model(input_ids=...)``) and greedy ``model.generate`` of 256 tokens after a 512-token
     prompt, timed on the host clock (``hf.benchmark_generate``); then the same model decoding 256
     tokens through ``hf.GraphedGreedy`` (static cache, the library's attention, norms, fused gate/up
-    SwiGLU GEMV and rotary embedding kernel, graph replays)."""
+    SwiGLU GEMV, rotary embedding kernel, joined q|k|v GEMV with its biases in the epilogue, graph
+    replays)."""
     from texelator_amd import hf, modeling, prefill
     from texelator_amd.runtime import free
 
@@ -442,6 +443,7 @@ def hf_section(torch, args) -> dict:
         hf.use_texelator_norms(model)
         hf.use_texelator_mlp(model)
         hf.use_texelator_rope(model)
+        handles += hf.use_texelator_qkv(model)
         graphed = hf.GraphedGreedy(model, max_cache_len=args.prompt + 264).benchmark(args.prompt, 256)
     finally:
         free(handles)
@@ -462,8 +464,9 @@ def hf_section(torch, args) -> dict:
         "graphed_decode_tok_s": round(graphed["decode_tok_s"], 2),
         "graphed_path": "hf.GraphedGreedy: static KV cache, the library's attention and RMSNorm kernels "
                         "(hf.use_texelator_norms), the gate/up SwiGLU GEMV (hf.use_texelator_mlp), the rotary "
-                        "embedding kernel (hf.use_texelator_rope), q/k/v biases added in the GEMV epilogue "
-                        "(tx_linear_add_bias), the one-token forward replayed from a HIP graph "
+                        "embedding kernel (hf.use_texelator_rope), one GEMV over the joined q|k|v handle with the "
+                        "biases in its epilogue (hf.use_texelator_qkv, tx_concat_rows + tx_linear_add_bias), "
+                        "the one-token forward replayed from a HIP graph "
                         "(device clock)",
     }
 

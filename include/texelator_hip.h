@@ -46,6 +46,15 @@ int tx_pack_encoded(const uint8_t *blocks, int64_t blocks_bytes, const float *sc
 int tx_pack_encoded_device(const uint8_t *blocks, int64_t blocks_bytes, const float *scales, int64_t rows,
                            const void *bias, int bias_dtype, int device, uint64_t *handle_out);
 
+/* A new handle holding the rows of `count` handles of one K in order (their row concatenation):
+ * one GEMV launch where a caller ran one per matrix, e.g. the q, k and v projections of an
+ * attention module installed as three separate modules (the reference's Hugging Face path keeps
+ * them separate, texelator/runtime.py:133-145; a fused q/k/v handle has no counterpart there).
+ * Every handle but the last must have a multiple of 16 rows; all or none carry a bias (one dtype);
+ * one palette table or none. The lookahead and prefill settings are the first handle's. The
+ * sources stay valid and independent (the new handle copies their tiles); free it with tx_free. */
+int tx_concat_rows(const uint64_t *handles, int count, uint64_t *handle_out);
+
 /* y = x W^T (+ bias). Replaces texelator_linear (texelator_cuda.cu:1329-1469; extension.cpp:30).
  *   x         device, contiguous, 16-byte aligned [tokens][K] of x_dtype (BF16 or F16). With F16
  *             the weights are rounded to fp16 before the fp32-accumulating MFMA; the reference's

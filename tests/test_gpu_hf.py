@@ -337,6 +337,56 @@ def test_texelator_rope_model_is_bitwise_the_module(tiny_bc4):
         tiny_bc4.set_attn_implementation("sdpa")
 
 
+def test_texelator_qkv_joins_the_projections(ext, tiny_bc4):
+    """``use_texelator_qkv`` (with ``use_texelator_rope``'s forward) on the BC4 Qwen2 with non-zero
+    biases: one token's q, k and v from the joined handle match the three projections within bf16
+    rounding (the joined GEMV may split K differently); prompts still take the three projections
+    (logits bitwise the unchanged model's); graphed tokens equal eager ones and mostly the
+    unchanged runner's; ``restore_qkv`` undoes it."""
+    from texelator_amd import hf
+
+    ids = torch.randint(0, 512, (1, 30), generator=torch.Generator().manual_seed(26)).cuda()
+    attention = [layer.self_attn for layer in tiny_bc4.model.layers]
+    saved = [[p.bias.detach().clone() for p in (a.q_proj, a.k_proj, a.v_proj)] for a in attention]
+    g = torch.Generator(device="cuda").manual_seed(27)
+    try:
+        for a in attention:
+            for p in (a.q_proj, a.k_proj, a.v_proj):
+                p.bias.data.copy_((0.3 * torch.randn(p.bias.shape, device="cuda", generator=g)).to(torch.bfloat16))
+        tiny_bc4.set_attn_implementation("sdpa")
+        with torch.inference_mode():
+            want = tiny_bc4(ids).logits
+        unchanged = hf.GraphedGreedy(tiny_bc4, max_cache_len=256).generate(ids, 24)
+        changed = hf.use_texelator_rope(tiny_bc4)
+        created = hf.use_texelator_qkv(tiny_bc4)
+        try:
+            assert len(created) == len(attention) and hf.use_texelator_qkv(tiny_bc4) == []
+            x = torch.randn(1, 1, tiny_bc4.config.hidden_size, device="cuda", generator=g).to(torch.bfloat16)
+            for a in attention:
+                got = hf._projections(a, x)
+                for part, p in zip(got, (a.q_proj, a.k_proj, a.v_proj)):
+                    ref = p(x).float()
+                    assert part.shape == ref.shape
+                    assert float((part.float() - ref).norm() / ref.norm()) < 1e-2
+            tiny_bc4.set_attn_implementation("sdpa")
+            with torch.inference_mode():
+                assert torch.equal(want, tiny_bc4(ids).logits)
+            runner = hf.GraphedGreedy(tiny_bc4, max_cache_len=256)
+            eager = runner.generate(ids, 24, eager=True)
+            graphed = runner.generate(ids, 24)
+            assert torch.equal(eager, graphed)
+            assert (graphed == unchanged).float().mean() >= 0.75
+        finally:
+            hf.restore_rope(changed)
+            hf.restore_qkv(tiny_bc4, created)
+        assert all("_texelator_qkv" not in a.__dict__ for a in attention)
+    finally:
+        for a, biases in zip(attention, saved):
+            for p, b in zip((a.q_proj, a.k_proj, a.v_proj), biases):
+                p.bias.data.copy_(b)
+        tiny_bc4.set_attn_implementation("sdpa")
+
+
 @pytest.mark.parametrize("shape", [(7, 256), (1, 3, 2048), (2, 5120)])
 def test_texelator_rmsnorm_matches_hf_rmsnorm(ext, shape):
     """``TexelatorRMSNorm`` against the Hugging Face module on the same weight: the same formula and

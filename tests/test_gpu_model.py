@@ -542,6 +542,51 @@ def test_linear_add_bias_is_bit_identical(ext, m, k):
         ext.free(handle)
 
 
+@pytest.mark.parametrize("rows,k,bias", [((2048, 256, 256), 2048, False), ((5120, 1024, 1024), 5120, True),
+                                         ((64, 48, 100), 1024, True)])
+def test_concat_rows_joins_the_matrices(ext, rows, k, bias):
+    """A joined handle decodes to the sources' dense weights stacked in order, bit for bit (the tile
+    copy keeps every row group and scale in place, the last source's ragged rows included), and
+    its GEMV and prefill results match the sources' within bf16 rounding (the joined shape may split
+    K differently); settings follow the first handle; the sources keep working."""
+    handles = [_random_handle(ext, m, k, seed=m + i, bias=bias) for i, m in enumerate(rows)]
+    ext.set_lookahead(handles[0], 2)
+    joined = ext.concat_rows(handles)
+    try:
+        assert ext.shape(joined) == (sum(rows), k) and ext.lookahead(joined) == 2
+        assert torch.equal(ext.decode_dense(joined), torch.cat([ext.decode_dense(h) for h in handles]))
+        g = torch.Generator(device="cuda").manual_seed(k)
+        for tokens in (1, 40):
+            x = torch.randn(tokens, k, device="cuda", generator=g).to(torch.bfloat16)
+            want = torch.cat([ext.linear(h, x) for h in handles], dim=-1).float()
+            got = ext.linear(joined, x).float()
+            assert got.shape == want.shape
+            assert float((got - want).norm() / want.norm()) < 1e-2, tokens
+    finally:
+        ext.free(joined)
+        for h in handles:
+            ext.free(h)
+
+
+def test_concat_rows_refusals(ext):
+    a = _random_handle(ext, 100, 1024, seed=1)
+    b = _random_handle(ext, 128, 1024, seed=2)
+    c = _random_handle(ext, 128, 2048, seed=3)
+    d = _random_handle(ext, 128, 1024, seed=4, bias=True)
+    try:
+        with pytest.raises(_lib.TexelatorError, match="multiple of 16"):
+            ext.concat_rows([a, b])
+        with pytest.raises(_lib.TexelatorError, match="share K"):
+            ext.concat_rows([b, c])
+        with pytest.raises(_lib.TexelatorError, match="bias"):
+            ext.concat_rows([b, d])
+        joined = ext.concat_rows([b, a])  # ragged rows last is fine
+        ext.free(joined)
+    finally:
+        for h in (a, b, c, d):
+            ext.free(h)
+
+
 def test_linear_add_bias_refuses_a_handle_with_its_own_bias(ext):
     handle = _random_handle(ext, 256, 1024, seed=9, bias=True)
     try:

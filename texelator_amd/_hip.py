@@ -129,6 +129,18 @@ def pack_encoded_device(blocks: torch.Tensor, scales: torch.Tensor, bias: torch.
     return handle
 
 
+def concat_rows(handles: list[int]) -> int:
+    """A new handle with the rows of ``handles`` (one K) in order (``tx_concat_rows``); every handle
+    but the last needs a multiple of 16 rows. The sources stay valid; free the result on its own."""
+    handles = [int(handle) for handle in handles]
+    array = (ctypes.c_uint64 * len(handles))(*handles)
+    out = ctypes.c_uint64(0)
+    check(_lib.load().tx_concat_rows(array, len(handles), ctypes.byref(out)))
+    handle = int(out.value)
+    _SHAPES[handle] = (sum(shape(h)[0] for h in handles), shape(handles[0])[1])
+    return handle
+
+
 def linear(handle: int, x: torch.Tensor) -> torch.Tensor:
     """``y = x W^T (+ bias)`` (``texelator_cuda.cu:1329-1469``); output dtype = input dtype."""
     _require(bool(handle), "null Texelator handle")

@@ -418,6 +418,77 @@ int tx_pack_encoded_device(const uint8_t *blocks, int64_t blocks_bytes, const fl
   return pack_common(blocks, blocks_bytes, scales, rows, bias, bias_dtype, device, true, handle_out);
 }
 
+int tx_concat_rows(const uint64_t *handles, int count, uint64_t *handle_out) {
+  g_last_error.clear();
+  if (!handles || !handle_out || count < 1 || count > 64) return fail(TX_ERR_INVALID, "concat_rows: 1 to 64 handles and an output");
+  std::vector<const Handle *> src(count);
+  int64_t rows = 0;
+  for (int i = 0; i < count; ++i) {
+    src[i] = as_handle(handles[i]);
+    if (!src[i]) return fail(TX_ERR_INVALID, "concat_rows: null Texelator handle");
+    const Handle &a = *src[i], &first = *src[0];
+    if (a.K != first.K || a.device != first.device)
+      return fail(TX_ERR_INVALID, "concat_rows: the handles must share K and the device");
+    if (i + 1 < count && a.M % tx::kTileRows != 0)
+      return fail(TX_ERR_INVALID, "concat_rows: every handle but the last needs a multiple of 16 rows");
+    if ((a.bias != nullptr) != (first.bias != nullptr) || (a.bias && a.bias_dtype != first.bias_dtype))
+      return fail(TX_ERR_INVALID, "concat_rows: all handles or none carry a bias, of one dtype");
+    if (a.lut != first.lut) return fail(TX_ERR_INVALID, "concat_rows: the handles use different palette tables");
+    rows += a.M;
+  }
+  if (rows > (1 << 30)) return fail(TX_ERR_INVALID, "matrix too large");
+  const Handle &first = *src[0];
+  DeviceGuard guard(first.device);
+  Handle *h = new (std::nothrow) Handle;
+  if (!h) return fail(TX_ERR_HIP, "host allocation failed");
+  h->M = (int)rows;
+  h->bpr = first.bpr;
+  h->K = first.K;
+  h->device = first.device;
+  h->RG = (h->M + tx::kTileRows - 1) / tx::kTileRows;
+  h->Mp = h->RG * tx::kTileRows;
+  h->CG = first.CG;
+  h->bp = first.bp;
+  h->cus = first.cus;
+  h->lookahead = first.lookahead;
+  h->prefill_threshold = first.prefill_threshold;
+  h->prefill_tile_rows = first.prefill_tile_rows;
+  h->prefill_backend = first.prefill_backend;
+  h->lut = first.lut;
+  h->gemv_splits = choose_splits(h->RG, h->CG, h->cus);
+  auto cleanup = [&](hipError_t e) {
+    delete h;
+    return fail(TX_ERR_HIP, std::string("HIP: ") + hipGetErrorString(e));
+  };
+  hipError_t e;
+  if ((e = hipMalloc(&h->tiles, (size_t)h->RG * h->CG * tx::kTileBytes)) != hipSuccess) return cleanup(e);
+  if ((e = hipMalloc(&h->scales, (size_t)h->Mp * sizeof(float))) != hipSuccess) return cleanup(e);
+  if (first.bias) {
+    if ((e = hipMalloc(&h->bias, (size_t)h->M * 2)) != hipSuccess) return cleanup(e);
+    h->bias_dtype = first.bias_dtype;
+  }
+  // Tiles are row-group major, so each source's row groups follow the previous source's; every
+  // source but the last fills its row groups, so rows keep their order and the padding stays last.
+  int64_t g = 0, row = 0;
+  for (const Handle *a : src) {
+    const size_t tile_bytes = (size_t)a->RG * a->CG * tx::kTileBytes;
+    if ((e = hipMemcpy(reinterpret_cast<char *>(h->tiles) + (size_t)g * h->CG * tx::kTileBytes, a->tiles, tile_bytes,
+                       hipMemcpyDeviceToDevice)) != hipSuccess)
+      return cleanup(e);
+    if ((e = hipMemcpy(h->scales + row, a->scales, (size_t)a->Mp * sizeof(float), hipMemcpyDeviceToDevice)) != hipSuccess)
+      return cleanup(e);
+    if (a->bias && (e = hipMemcpy(static_cast<char *>(h->bias) + (size_t)row * 2, a->bias, (size_t)a->M * 2,
+                                  hipMemcpyDeviceToDevice)) != hipSuccess)
+      return cleanup(e);
+    g += a->RG;
+    row += a->M;
+  }
+  if ((e = hipMalloc(&h->partials, (size_t)h->gemv_splits * h->Mp * sizeof(float))) != hipSuccess) return cleanup(e);
+  if ((e = hipDeviceSynchronize()) != hipSuccess) return cleanup(e);
+  *handle_out = reinterpret_cast<uint64_t>(h);
+  return TX_OK;
+}
+
 int tx_linear(uint64_t value, const void *x, int x_dtype, int64_t x_numel, int64_t x_last, int device, void *y,
               void *workspace, int64_t workspace_bytes, void *stream) {
   g_last_error.clear();

@@ -277,9 +277,10 @@ def _rope_attention_forward(self, hidden_states: torch.Tensor, position_embeddin
     hf_module = sys.modules[type(self).__module__]
     input_shape = hidden_states.shape[:-1]
     hidden_shape = (*input_shape, -1, self.head_dim)
-    q = self.q_proj(hidden_states).view(hidden_shape)  # [batch, tokens, heads, head_dim]
-    k = self.k_proj(hidden_states).view(hidden_shape)
-    v = self.v_proj(hidden_states).view(hidden_shape).transpose(1, 2)
+    q, k, v = _projections(self, hidden_states)
+    q = q.view(hidden_shape)  # [batch, tokens, heads, head_dim]
+    k = k.view(hidden_shape)
+    v = v.view(hidden_shape).transpose(1, 2)
     cos, sin = position_embeddings  # [batch, tokens, head_dim]
     if q.is_cuda and q.dtype == cos.dtype == torch.bfloat16 and cos.shape[:-1] == q.shape[:-2]:
         q, k = layers.rope_rotate_half(q.contiguous(), k.contiguous(), cos.contiguous(), sin.contiguous())
@@ -293,6 +294,66 @@ def _rope_attention_forward(self, hidden_states: torch.Tensor, position_embeddin
     out, weights = attention(self, q, k, v, attention_mask, dropout=0.0 if not self.training else self.attention_dropout,
                              scaling=self.scaling, sliding_window=self.sliding_window, **kwargs)
     return self.o_proj(out.reshape(*input_shape, -1).contiguous()), weights
+
+
+def _projections(self, hidden_states: torch.Tensor) -> tuple[torch.Tensor, ...]:
+    """q, k and v of an attention module: for one bf16 token of a module :func:`use_texelator_qkv`
+    joined, one GEMV over its q|k|v handle with the three biases in the GEMV's epilogue (views of
+    one output); otherwise the module's three projections."""
+    from . import layers
+
+    joined = self.__dict__.get("_texelator_qkv")
+    x = hidden_states
+    if (joined is not None and x.is_cuda and x.dtype == torch.bfloat16 and x.numel() == x.shape[-1]
+            and x.is_contiguous() and x.data_ptr() % 16 == 0):
+        handle, bias, sizes = joined
+        out = layers.linear_add_bias(handle, x, bias) if bias is not None else extension().linear(handle, x)
+        return out.split(sizes, dim=-1)
+    return self.q_proj(x), self.k_proj(x), self.v_proj(x)
+
+
+def use_texelator_qkv(model: nn.Module) -> list[int]:
+    """Join the q, k and v projections of every Qwen2 attention module whose three projections are
+    single-handle :class:`TexelatorLinear` modules of one K (q and k rows multiples of 16; all with
+    bf16 separate biases or none) into one handle (``concat_rows``), so that a one-token forward runs
+    one GEMV for the three. Takes effect in the forward :func:`use_texelator_rope` installs; the
+    biases are copied now. Returns the new handles; :func:`restore_qkv` drops and frees them."""
+    ext = extension()
+    created = []
+    for module in model.modules():
+        if type(module).__name__ != "Qwen2Attention" or "_texelator_qkv" in module.__dict__:
+            continue
+        projections = [module.q_proj, module.k_proj, module.v_proj]
+        if not all(isinstance(p, TexelatorLinear) and len(p.handles) == 1 for p in projections):
+            continue
+        biases = [p.bias for p in projections]
+        if any(b is None for b in biases):
+            if not all(b is None for b in biases):
+                continue
+            bias = None
+        elif all(b.dtype == torch.bfloat16 and b.is_cuda for b in biases):
+            bias = torch.cat([b.detach().reshape(-1) for b in biases]).contiguous()
+        else:
+            continue
+        try:
+            handle = ext.concat_rows([p.handles[0] for p in projections])
+        except TexelatorError:
+            continue
+        module._texelator_qkv = (handle, bias, [ext.shape(p.handles[0])[0] for p in projections])
+        created.append(handle)
+    return created
+
+
+def restore_qkv(model: nn.Module, created: list[int]) -> None:
+    """Undo :func:`use_texelator_qkv`: the modules run their three projections again and the joined
+    handles are freed."""
+    for module in model.modules():
+        module.__dict__.pop("_texelator_qkv", None)
+    if torch.cuda.is_available():
+        torch.cuda.synchronize()
+    ext = extension()
+    for handle in created:
+        ext.free(handle)
 
 
 def use_texelator_rope(model: nn.Module) -> list[nn.Module]:
