@@ -425,8 +425,8 @@ def hf_section(torch, args) -> dict:
     it (``model.model(input_ids=...)``) and greedy ``model.generate`` of 256 tokens after a 512-token
     prompt, timed on the host clock (``hf.benchmark_generate``); then the same model decoding 256
     tokens through ``hf.GraphedGreedy`` (static cache, the library's attention, norms, fused gate/up
-    SwiGLU GEMV, rotary embedding kernel, joined q|k|v GEMV with its biases in the epilogue, graph
-    replays)."""
+    SwiGLU GEMV, rotary embedding kernel, joined q|k|v GEMV with its biases in the epilogue, the
+    attention's residual add in the post-attention norm, graph replays)."""
     from texelator_amd import hf, modeling, prefill
     from texelator_amd.runtime import free
 
@@ -441,6 +441,7 @@ def hf_section(torch, args) -> dict:
             pre, gate_failed = None, error.correctness
         gen = hf.benchmark_generate(model, prompt_tokens=args.prompt, new_tokens=256, runs=2)
         hf.use_texelator_norms(model)
+        hf.use_texelator_residuals(model)
         hf.use_texelator_mlp(model)
         hf.use_texelator_rope(model)
         handles += hf.use_texelator_qkv(model)
@@ -465,7 +466,8 @@ def hf_section(torch, args) -> dict:
         "graphed_path": "hf.GraphedGreedy: static KV cache, the library's attention and RMSNorm kernels "
                         "(hf.use_texelator_norms), the gate/up SwiGLU GEMV (hf.use_texelator_mlp), the rotary "
                         "embedding kernel (hf.use_texelator_rope), one GEMV over the joined q|k|v handle with the "
-                        "biases in its epilogue (hf.use_texelator_qkv, tx_concat_rows + tx_linear_add_bias), "
+                        "biases in its epilogue (hf.use_texelator_qkv, tx_concat_rows + tx_linear_add_bias), the "
+                        "attention's residual add fused into the post-attention norm (hf.use_texelator_residuals), "
                         "the one-token forward replayed from a HIP graph "
                         "(device clock)",
     }

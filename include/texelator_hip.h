@@ -279,6 +279,15 @@ int tx_lm_head_argmax_workspace(int64_t *bytes);
 int tx_lm_head_argmax(const void *weight, int64_t vocab, int64_t hidden, const void *x, void *logits, void *workspace,
                       int64_t workspace_bytes, int64_t *token, void *stream);
 
+/* RMSNorm over a bf16 residual stream (a Hugging Face decoder layer's: no counterpart in the
+ * reference's own code, whose Hugging Face path leaves the norms and residual adds to torch):
+ * rows x hidden bf16. With delta: sum_out = bf16(residual + delta) (torch's bf16 add) and
+ * out = bf16(weight * bf16(sum * rsqrt(mean(sum^2) + eps))) of that sum, sums of squares in fp32;
+ * without (delta NULL): out = that norm of the residual, sum_out unused. One launch, one block per
+ * row. Pointers 8-byte aligned; hidden a multiple of 4. */
+int tx_add_rmsnorm_bf16(const void *residual, const void *delta, const void *weight, float eps, void *sum_out, void *out,
+                        int64_t rows, int64_t hidden, void *stream);
+
 /* ---- Fused single-token decode (no reference counterpart; same role as the helpers above) ----
  * tx_linear_split runs a handle's one-token decode GEMV (x bf16 [K]) but leaves its output as
  * the fp32 split-K partials in the handle's own buffer; the *_split consumers below read them,

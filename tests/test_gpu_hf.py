@@ -17,7 +17,7 @@ import pytest
 import torch
 from torch.nn.attention import SDPBackend, sdpa_kernel
 
-from texelator_amd import artifacts, encoder, hardware, runtime
+from texelator_amd import artifacts, encoder, hardware, layers, runtime
 
 pytestmark = pytest.mark.gpu
 
@@ -384,6 +384,63 @@ def test_texelator_qkv_joins_the_projections(ext, tiny_bc4):
         for a, biases in zip(attention, saved):
             for p, b in zip((a.q_proj, a.k_proj, a.v_proj), biases):
                 p.bias.data.copy_(b)
+        tiny_bc4.set_attn_implementation("sdpa")
+
+
+@pytest.mark.parametrize("shape", [(1, 1, 2048), (3, 5120), (2, 12288), (5, 36)])
+def test_add_rmsnorm_bf16_matches_torch_and_the_fp32_kernel(ext, shape):
+    """The bf16-residual kernel: its sum is torch's bf16 add bit for bit, and its norm of that sum
+    (or of the residual alone) is bitwise the fp32-residual kernel's on the same values (same
+    reduction order; 12288 columns take the two-pass path); against Hugging Face's RMSNorm at most
+    one bf16 step apart."""
+    from transformers.models.qwen2.modeling_qwen2 import Qwen2RMSNorm
+
+    g = torch.Generator(device="cuda").manual_seed(shape[-1] + len(shape))
+    residual = (torch.randn(shape, device="cuda", generator=g) * 3).to(torch.bfloat16)
+    delta = (torch.randn(shape, device="cuda", generator=g) * 2).to(torch.bfloat16)
+    weight = (1 + 0.1 * torch.randn(shape[-1], device="cuda", generator=g)).to(torch.bfloat16)
+    total, got = layers.add_rmsnorm_bf16(residual, delta, weight, 1e-6)
+    assert torch.equal(total, residual + delta) and got.shape == residual.shape
+    flat = total.reshape(-1, shape[-1]).float()
+    assert torch.equal(got.reshape(flat.shape), layers.add_rmsnorm(flat.clone(), None, weight, 1e-6))
+    none, alone = layers.add_rmsnorm_bf16(residual, None, weight, 1e-6)
+    assert none is None
+    assert torch.equal(alone.reshape(flat.shape), layers.add_rmsnorm(residual.reshape(flat.shape).float(), None, weight, 1e-6))
+    module = Qwen2RMSNorm(shape[-1], eps=1e-6).to(device="cuda", dtype=torch.bfloat16)
+    module.weight.data.copy_(weight)
+    want = module(total)
+    step = torch.maximum(want.float().abs(), got.float().abs()) * 2.0 ** -7
+    assert bool(((got.float() - want.float()).abs() <= step + 1e-30).all())
+
+
+def test_texelator_residuals_are_bitwise_the_norm_modules(tiny_bc4):
+    """``use_texelator_residuals`` after ``use_texelator_norms``: the attention's residual add fused into
+    the post-attention norm gives the same bits as the add followed by the norm module (prompt logits
+    and graphed tokens equal); ``restore_rope`` gives the layers their class's forward back."""
+    from texelator_amd import hf
+
+    ids = torch.randint(0, 512, (1, 30), generator=torch.Generator().manual_seed(28)).cuda()
+    replaced = hf.use_texelator_norms(tiny_bc4)
+    try:
+        tiny_bc4.set_attn_implementation("sdpa")
+        with torch.inference_mode():
+            want = tiny_bc4(ids).logits
+        unchanged = hf.GraphedGreedy(tiny_bc4, max_cache_len=256).generate(ids, 24)
+        changed = hf.use_texelator_residuals(tiny_bc4)
+        try:
+            assert len(changed) == len(tiny_bc4.model.layers)
+            tiny_bc4.set_attn_implementation("sdpa")
+            with torch.inference_mode():
+                assert torch.equal(want, tiny_bc4(ids).logits)
+            runner = hf.GraphedGreedy(tiny_bc4, max_cache_len=256)
+            eager = runner.generate(ids, 24, eager=True)
+            graphed = runner.generate(ids, 24)
+            assert torch.equal(eager, graphed) and torch.equal(graphed, unchanged)
+        finally:
+            hf.restore_rope(changed)
+        assert all("forward" not in layer.__dict__ for layer in tiny_bc4.model.layers)
+    finally:
+        hf.restore_modules(replaced)
         tiny_bc4.set_attn_implementation("sdpa")
 
 

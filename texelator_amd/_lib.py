@@ -47,6 +47,7 @@ SIGNATURES = {
     "tx_set_palette_table": (_I32, [_U64, _P]),
     "tx_handle_info": (_I32, [_U64, ctypes.POINTER(_I64), _I32]),
     "tx_free": (_I32, [_U64]),
+    "tx_add_rmsnorm_bf16": (_I32, [_P, _P, _P, ctypes.c_float, _P, _P, _I64, _I64, _P]),
     "tx_concat_rows": (_I32, [ctypes.POINTER(_U64), _I32, ctypes.POINTER(_U64)]),
     "tx_palette_probe": (_I32, [_P]),
     "tx_decode_dense": (_I32, [_U64, _I32, _P, _P]),

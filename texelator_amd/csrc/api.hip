@@ -808,6 +808,22 @@ int tx_add_rmsnorm(float *residual, const void *delta, const void *weight, float
   return TX_OK;
 }
 
+int tx_add_rmsnorm_bf16(const void *residual, const void *delta, const void *weight, float eps, void *sum_out, void *out,
+                        int64_t rows, int64_t hidden, void *stream) {
+  g_last_error.clear();
+  if (!residual || !weight || !out || (delta && !sum_out) || rows < 0 || rows > 0x7FFFFFFF || hidden <= 0 ||
+      hidden > (1 << 24) || hidden % 4)
+    return fail(TX_ERR_INVALID, "add_rmsnorm_bf16: invalid arguments (hidden must be a positive multiple of 4; "
+                                "a delta needs sum_out)");
+  for (const void *ptr : {residual, delta, weight, static_cast<const void *>(sum_out), static_cast<const void *>(out)})
+    if (reinterpret_cast<uintptr_t>(ptr) % 8) return fail(TX_ERR_INVALID, "add_rmsnorm_bf16: pointers must be 8-byte aligned");
+  if (rows == 0) return TX_OK;
+  TX_HIP(tx::launch_add_rmsnorm_bf16(static_cast<const uint16_t *>(residual), static_cast<const uint16_t *>(delta),
+                                     static_cast<const uint16_t *>(weight), eps, delta ? static_cast<uint16_t *>(sum_out) : nullptr,
+                                     static_cast<uint16_t *>(out), rows, (int)hidden, reinterpret_cast<hipStream_t>(stream)));
+  return TX_OK;
+}
+
 int tx_linear_split(uint64_t value, const void *x, void *stream) {
   g_last_error.clear();
   Handle *h = as_handle(value);

@@ -175,6 +175,81 @@ __global__ __launch_bounds__(kNormThreads) void add_rmsnorm_kernel(float *h, con
   for (int i = threadIdx.x; i < groups; i += kThreads) orow[i] = normalize(hr[i], wr[i]);
 }
 
+// The same normalization over a bf16 residual kept in bf16, as a Hugging Face decoder layer keeps it:
+// v = bf16(residual + delta) (torch's bf16 add: the fp32 sum rounded once) written to sum_out, or
+// v = residual when delta is null (nothing written); out = bf16(weight * bf16(v * rsqrt(mean(v^2) +
+// eps))). Thread t owns the groups of four columns 4 * (t + 1024 * i) and sums their squares in the
+// order add_rmsnorm_kernel does, so for the same v both kernels give the same bits.
+__global__ __launch_bounds__(kNormThreads) void add_rmsnorm_bf16_kernel(const uint16_t *residual, const uint16_t *delta,
+                                                                        const uint16_t *weight, float eps,
+                                                                        uint16_t *sum_out, uint16_t *out, int hidden) {
+  constexpr int kThreads = kNormThreads;
+  constexpr int kUnroll = 2;
+  __shared__ float partial[kThreads / 64];
+  const size_t row = (size_t)blockIdx.x * hidden;
+  const uint2 *rr = reinterpret_cast<const uint2 *>(residual + row);
+  const uint2 *dr = delta ? reinterpret_cast<const uint2 *>(delta + row) : nullptr;
+  uint2 *sr = delta ? reinterpret_cast<uint2 *>(sum_out + row) : nullptr;
+  uint2 *orow = reinterpret_cast<uint2 *>(out + row);
+  const uint2 *wr = reinterpret_cast<const uint2 *>(weight);
+  const int groups = hidden / 4;
+  const bool one_pass = groups <= kThreads * kUnroll;
+  auto value = [&](int i) {
+    const uint2 r = rr[i];
+    float4 v = make_float4(bf((uint16_t)(r.x & 0xFFFFu)), bf((uint16_t)(r.x >> 16)), bf((uint16_t)(r.y & 0xFFFFu)),
+                           bf((uint16_t)(r.y >> 16)));
+    if (dr) {
+      const uint2 d = dr[i];
+      v.x = bf(to_bf(v.x + bf((uint16_t)(d.x & 0xFFFFu))));
+      v.y = bf(to_bf(v.y + bf((uint16_t)(d.x >> 16))));
+      v.z = bf(to_bf(v.z + bf((uint16_t)(d.y & 0xFFFFu))));
+      v.w = bf(to_bf(v.w + bf((uint16_t)(d.y >> 16))));
+    }
+    return v;
+  };
+  float4 v[kUnroll];
+  uint2 wv[kUnroll];
+  float ss = 0.f;
+  for (int base = 0; base < groups; base += kThreads * kUnroll) {
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int i = base + u * kThreads + (int)threadIdx.x;
+      if (i >= groups) continue;
+      v[u] = value(i);
+      if (one_pass) wv[u] = wr[i];
+      if (sr) {
+        sr[i] = make_uint2((uint32_t)to_bf(v[u].x) | ((uint32_t)to_bf(v[u].y) << 16),
+                           (uint32_t)to_bf(v[u].z) | ((uint32_t)to_bf(v[u].w) << 16));
+      }
+      ss += (v[u].x * v[u].x + v[u].y * v[u].y) + (v[u].z * v[u].z + v[u].w * v[u].w);
+    }
+  }
+  ss = wave_sum(ss);
+  if ((threadIdx.x & 63) == 0) partial[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  float total = 0.f;
+#pragma unroll
+  for (int w = 0; w < kThreads / 64; ++w) total += partial[w];
+  const float inv = rsqrtf(total / (float)hidden + eps);
+  auto normalize = [&](const float4 &h4, const uint2 &w) {
+    const float n0 = bf(to_bf(h4.x * inv)), n1 = bf(to_bf(h4.y * inv)), n2 = bf(to_bf(h4.z * inv)), n3 = bf(to_bf(h4.w * inv));
+    const uint32_t lo = (uint32_t)to_bf(bf((uint16_t)(w.x & 0xFFFFu)) * n0) | ((uint32_t)to_bf(bf((uint16_t)(w.x >> 16)) * n1) << 16);
+    const uint32_t hi = (uint32_t)to_bf(bf((uint16_t)(w.y & 0xFFFFu)) * n2) | ((uint32_t)to_bf(bf((uint16_t)(w.y >> 16)) * n3) << 16);
+    return make_uint2(lo, hi);
+  };
+  if (one_pass) {
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int i = u * kThreads + (int)threadIdx.x;
+      if (i < groups) orow[i] = normalize(v[u], wv[u]);
+    }
+    return;
+  }
+  // wider rows: v again from the inputs (the residual and delta are unchanged; sum_out is not read)
+  for (int i = threadIdx.x; i < groups; i += kThreads) orow[i] = normalize(value(i), wr[i]);
+}
+
+
 // One block per (token, head); thread j rotates the pair (j, j + d/2) of rotate-half RoPE.
 // q heads are written to q_out; k heads are rotated into the K cache; v heads are copied.
 // With SPLIT, the [q | k | v] row is the fp32 split-K partials of the qkv decode GEMV.
@@ -930,6 +1005,13 @@ hipError_t launch_add_rmsnorm(float *h, const uint16_t *delta, const uint16_t *w
                               int64_t rows, int hidden, hipStream_t stream) {
   hipLaunchKernelGGL((add_rmsnorm_kernel<false, 0>), dim3((unsigned)rows), dim3(kNormThreads), 0, stream, h, delta, SplitSource{},
                      weight, eps, out, hidden);
+  return hipGetLastError();
+}
+
+hipError_t launch_add_rmsnorm_bf16(const uint16_t *residual, const uint16_t *delta, const uint16_t *weight, float eps,
+                                   uint16_t *sum_out, uint16_t *out, int64_t rows, int hidden, hipStream_t stream) {
+  hipLaunchKernelGGL(add_rmsnorm_bf16_kernel, dim3((unsigned)rows), dim3(kNormThreads), 0, stream, residual, delta, weight,
+                     eps, sum_out, out, hidden);
   return hipGetLastError();
 }
 

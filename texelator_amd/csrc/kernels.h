@@ -164,6 +164,9 @@ hipError_t launch_add_rmsnorm(float *h, const uint16_t *delta, const uint16_t *w
                               int64_t rows, int hidden, hipStream_t stream);
 // The same with delta = the split-K partials of a decode GEMV (summed and rounded as the GEMV's
 // own reduction does).
+// bf16 residual: sum_out = bf16(residual + delta) (delta may be null: nothing written), out its norm.
+hipError_t launch_add_rmsnorm_bf16(const uint16_t *residual, const uint16_t *delta, const uint16_t *weight, float eps,
+                                   uint16_t *sum_out, uint16_t *out, int64_t rows, int hidden, hipStream_t stream);
 hipError_t launch_add_rmsnorm_split(float *h, const SplitSource &delta, const uint16_t *weight, float eps, uint16_t *out,
                                     int64_t rows, int hidden, hipStream_t stream);
 hipError_t launch_rope_cache(const uint16_t *qkv, int64_t stride, int64_t tokens, const int64_t *positions,

@@ -169,10 +169,10 @@ def use_texelator_attention(model: nn.Module) -> None:
 
 class TexelatorRMSNorm(nn.Module):
     """A Hugging Face RMSNorm (Qwen2/Llama form: ``weight * bf16(x * rsqrt(mean(x^2) + eps))``, x in
-    fp32) through the library's add+RMSNorm kernel: two launches (the fp32 copy of x and the
-    kernel) instead of the module's six or seven elementwise ones. The same formula and roundings;
-    the fp32 sum of squares runs in the kernel's order, so a row's result can differ from torch's in
-    the last bit where the two sums round apart. bf16 activations and weight, hidden a multiple of 4."""
+    fp32) through the library's bf16 add+RMSNorm kernel: one launch instead of the module's six or
+    seven elementwise ones. The same formula and roundings; the fp32 sum of squares runs in the
+    kernel's order, so a row's result can differ from torch's in the last bit where the two sums
+    round apart. bf16 activations and weight, hidden a multiple of 4."""
 
     def __init__(self, weight: nn.Parameter, eps: float):
         super().__init__()
@@ -182,6 +182,8 @@ class TexelatorRMSNorm(nn.Module):
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         from . import layers
 
+        if x.dtype == torch.bfloat16 and x.is_cuda and x.is_contiguous() and x.data_ptr() % 8 == 0:
+            return layers.add_rmsnorm_bf16(x, None, self.weight, self.variance_epsilon)[1]
         shape = x.shape
         h = x.reshape(-1, shape[-1]).float()
         return layers.add_rmsnorm(h, None, self.weight, self.variance_epsilon).view(shape)
@@ -354,6 +356,49 @@ def restore_qkv(model: nn.Module, created: list[int]) -> None:
     ext = extension()
     for handle in created:
         ext.free(handle)
+
+
+def _decoder_layer_forward(self, hidden_states: torch.Tensor, attention_mask: torch.Tensor | None = None,
+                           position_ids: torch.Tensor | None = None, past_key_values=None, use_cache: bool | None = False,
+                           position_embeddings: tuple[torch.Tensor, torch.Tensor] | None = None, **kwargs) -> torch.Tensor:
+    """A Qwen2 decoder layer's forward with the attention's residual add and the post-attention
+    RMSNorm in one launch (:func:`~texelator_amd.layers.add_rmsnorm_bf16`: ``bf16(residual +
+    attention)`` as torch adds, then the norm of that sum as :class:`TexelatorRMSNorm` computes it);
+    every other step as the layer does it."""
+    from . import layers
+
+    residual = hidden_states
+    hidden_states = self.input_layernorm(hidden_states)
+    hidden_states, _ = self.self_attn(hidden_states=hidden_states, attention_mask=attention_mask,
+                                      position_ids=position_ids, past_key_values=past_key_values, use_cache=use_cache,
+                                      position_embeddings=position_embeddings, **kwargs)
+    norm = self.post_attention_layernorm
+    if (isinstance(norm, TexelatorRMSNorm) and residual.is_cuda and residual.dtype == hidden_states.dtype == torch.bfloat16
+            and residual.is_contiguous() and hidden_states.is_contiguous() and residual.shape == hidden_states.shape
+            and residual.data_ptr() % 8 == 0 and hidden_states.data_ptr() % 8 == 0):
+        residual, hidden_states = layers.add_rmsnorm_bf16(residual, hidden_states, norm.weight, norm.variance_epsilon)
+    else:
+        hidden_states = residual + hidden_states
+        residual = hidden_states
+        hidden_states = norm(hidden_states)
+    hidden_states = self.mlp(hidden_states)
+    return residual + hidden_states
+
+
+def use_texelator_residuals(model: nn.Module) -> list[nn.Module]:
+    """Give every Qwen2 decoder layer of ``model`` :func:`_decoder_layer_forward` (the attention's
+    residual add fused into the post-attention RMSNorm when :func:`use_texelator_norms` made it a
+    :class:`TexelatorRMSNorm`); returns the layers changed, for :func:`restore_rope`, which gives
+    them their class's forward back the same way."""
+    import types
+
+    changed = []
+    for module in model.modules():
+        if type(module).__name__ != "Qwen2DecoderLayer" or "forward" in module.__dict__:
+            continue
+        module.forward = types.MethodType(_decoder_layer_forward, module)
+        changed.append(module)
+    return changed
 
 
 def use_texelator_rope(model: nn.Module) -> list[nn.Module]:

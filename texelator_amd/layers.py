@@ -47,6 +47,28 @@ def add_rmsnorm(residual: torch.Tensor, delta: torch.Tensor | None, weight: torc
     return out
 
 
+def add_rmsnorm_bf16(residual: torch.Tensor, delta: torch.Tensor | None, weight: torch.Tensor,
+                     eps: float) -> tuple[torch.Tensor | None, torch.Tensor]:
+    """RMSNorm over a bf16 residual ``[..., hidden]`` kept in bf16: with ``delta``, ``(bf16(residual +
+    delta), norm of that sum)`` (torch's bf16 add, then Hugging Face's RMSNorm roundings); without,
+    ``(None, norm of residual)``. One launch; outputs shaped like ``residual``."""
+    _expect(residual.is_cuda and residual.dtype == torch.bfloat16 and residual.is_contiguous()
+            and residual.data_ptr() % 8 == 0, "residual must be a contiguous, 8-byte aligned CUDA bf16 tensor")
+    hidden = residual.shape[-1]
+    rows = residual.numel() // hidden if hidden else 0
+    _expect(weight.is_cuda and weight.dtype == torch.bfloat16 and weight.is_contiguous() and weight.numel() == hidden,
+            "weight must be bf16 [hidden]")
+    total = None
+    if delta is not None:
+        _expect(delta.dtype == torch.bfloat16 and delta.is_contiguous() and delta.shape == residual.shape
+                and delta.device == residual.device, "delta must be a contiguous bf16 tensor shaped like the residual")
+        total = torch.empty_like(residual)
+    out = torch.empty_like(residual)
+    check(_lib.load().tx_add_rmsnorm_bf16(_ptr(residual), _ptr(delta), _ptr(weight), float(eps), _ptr(total), _ptr(out),
+                                          rows, hidden, _stream(residual)))
+    return total, out
+
+
 def rope_kv_cache(qkv: torch.Tensor, positions: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, heads: int,
                   kv_heads: int, head_dim: int, k_cache: torch.Tensor, v_cache: torch.Tensor,
                   q_out: torch.Tensor | None = None) -> torch.Tensor:
