@@ -436,6 +436,32 @@ def test_texelator_rope_forward_replacement_and_restore():
     assert all("forward" not in m.__dict__ for m in changed)
 
 
+def test_texelator_residuals_forward_replacement_and_restore():
+    """``use_texelator_residuals`` gives every Qwen2 decoder layer a forward with the layer's own steps;
+    with Hugging Face's norm modules (here: fp32 on the CPU) it adds and normalizes as the layer does,
+    so the logits are bitwise the unchanged model's (also with ``use_texelator_rope`` on); ``use_texelator_qkv``
+    joins nothing without installed linears; ``restore_rope`` undoes both overrides."""
+    transformers = pytest.importorskip("transformers")
+    from texelator_amd import hf
+
+    config = transformers.Qwen2Config(vocab_size=64, hidden_size=64, intermediate_size=128, num_hidden_layers=2,
+                                      num_attention_heads=4, num_key_value_heads=2, head_dim=16,
+                                      tie_word_embeddings=False)
+    torch.manual_seed(7)
+    model = transformers.Qwen2ForCausalLM(config).eval()
+    ids = torch.randint(0, 64, (1, 9), generator=torch.Generator().manual_seed(8))
+    with torch.no_grad():
+        want = model(ids).logits
+        changed = hf.use_texelator_residuals(model)
+        assert len(changed) == 2 and hf.use_texelator_residuals(model) == []
+        assert torch.equal(want, model(ids).logits)
+        rope = hf.use_texelator_rope(model)
+        assert hf.use_texelator_qkv(model) == []
+        assert torch.equal(want, model(ids).logits)
+    hf.restore_rope(changed + rope)
+    assert all("forward" not in m.__dict__ for m in changed + rope)
+
+
 def test_prefill_benchmark_rejects_plain_models():
     from texelator_amd import prefill
 
