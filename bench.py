@@ -467,7 +467,8 @@ def hf_section(torch, args) -> dict:
                         "(hf.use_texelator_norms), the gate/up SwiGLU GEMV (hf.use_texelator_mlp), the rotary "
                         "embedding kernel (hf.use_texelator_rope), one GEMV over the joined q|k|v handle with the "
                         "biases in its epilogue (hf.use_texelator_qkv, tx_concat_rows + tx_linear_add_bias), the "
-                        "attention's residual add fused into the post-attention norm (hf.use_texelator_residuals), "
+                        "attention's residual add fused into the post-attention norm and the MLP's into the down GEMV "
+                        "(hf.use_texelator_residuals), "
                         "the one-token forward replayed from a HIP graph "
                         "(device clock)",
     }

@@ -414,14 +414,24 @@ def test_add_rmsnorm_bf16_matches_torch_and_the_fp32_kernel(ext, shape):
 
 
 def test_texelator_residuals_are_bitwise_the_norm_modules(tiny_bc4):
-    """``use_texelator_residuals`` after ``use_texelator_norms``: the attention's residual add fused into
-    the post-attention norm gives the same bits as the add followed by the norm module (prompt logits
-    and graphed tokens equal); ``restore_rope`` gives the layers their class's forward back."""
+    """``use_texelator_residuals`` after ``use_texelator_norms`` and ``use_texelator_mlp``: the attention's
+    residual add fused into the post-attention norm and the MLP's residual add fused into the down
+    GEMV give the same bits as the separate adds (one token's MLP output with the residual, prompt
+    logits and graphed tokens equal); ``restore_rope`` gives the layers their class's forward back."""
     from texelator_amd import hf
 
     ids = torch.randint(0, 512, (1, 30), generator=torch.Generator().manual_seed(28)).cuda()
     replaced = hf.use_texelator_norms(tiny_bc4)
+    replaced += hf.use_texelator_mlp(tiny_bc4)
     try:
+        mlp = tiny_bc4.model.layers[0].mlp
+        assert isinstance(mlp, hf.TexelatorMLP)
+        g = torch.Generator(device="cuda").manual_seed(29)
+        hidden = tiny_bc4.config.hidden_size
+        for scale in (1.0, 30.0):
+            x = (torch.randn(1, 1, hidden, device="cuda", generator=g)).to(torch.bfloat16)
+            r = (scale * torch.randn(1, 1, hidden, device="cuda", generator=g)).to(torch.bfloat16)
+            assert torch.equal(mlp.forward_residual(x, r), r + mlp(x))
         tiny_bc4.set_attn_implementation("sdpa")
         with torch.inference_mode():
             want = tiny_bc4(ids).logits

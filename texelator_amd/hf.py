@@ -240,6 +240,32 @@ class TexelatorMLP(nn.Module):
                 return self.original.down_proj(act.view(*x.shape[:-1], act.shape[-1]))
         return self.original(x)
 
+    def forward_residual(self, x: torch.Tensor, residual: torch.Tensor) -> torch.Tensor | None:
+        """``residual + self(x)`` for one bf16 token with the residual added in the down projection's
+        GEMV epilogue (:func:`~texelator_amd.layers.linear_add_bias` with the residual as the vector:
+        the bf16 projection plus the residual rounded again, bit for bit the separate add); ``None``
+        (nothing computed) where that path does not apply."""
+        from . import layers
+        from ._lib import UnsupportedError
+
+        down = self.original.down_proj
+        if not (self.fused and isinstance(down, TexelatorLinear) and len(down.handles) == 1 and down.bias is None
+                and x.dtype == residual.dtype == torch.bfloat16 and x.is_cuda and x.numel() == x.shape[-1]
+                and residual.shape == x.shape and residual.is_contiguous() and residual.data_ptr() % 2 == 0):
+            return None
+        xc = x.contiguous()
+        if xc.data_ptr() % 16:
+            xc = xc.clone()
+        try:
+            act = layers.linear_swiglu_pair(self.gate, self.up, xc.view(-1))
+        except UnsupportedError:
+            self.fused = False
+            return None
+        try:
+            return layers.linear_add_bias(down.handles[0], act, residual.view(-1)).view(residual.shape)
+        except TexelatorError:  # a down handle with its own bias: the separate add
+            return residual + down(act.view(*x.shape[:-1], act.shape[-1]))
+
 
 def use_texelator_mlp(model: nn.Module) -> list[tuple[nn.Module, str, nn.Module]]:
     """Replace every gated SiLU MLP of ``model`` whose gate and up projections are single-handle
@@ -363,8 +389,9 @@ def _decoder_layer_forward(self, hidden_states: torch.Tensor, attention_mask: to
                            position_embeddings: tuple[torch.Tensor, torch.Tensor] | None = None, **kwargs) -> torch.Tensor:
     """A Qwen2 decoder layer's forward with the attention's residual add and the post-attention
     RMSNorm in one launch (:func:`~texelator_amd.layers.add_rmsnorm_bf16`: ``bf16(residual +
-    attention)`` as torch adds, then the norm of that sum as :class:`TexelatorRMSNorm` computes it);
-    every other step as the layer does it."""
+    attention)`` as torch adds, then the norm of that sum as :class:`TexelatorRMSNorm` computes it)
+    and, under :class:`TexelatorMLP`, the MLP's residual add in the down projection's GEMV
+    (:meth:`TexelatorMLP.forward_residual`); every other step as the layer does it."""
     from . import layers
 
     residual = hidden_states
@@ -381,6 +408,10 @@ def _decoder_layer_forward(self, hidden_states: torch.Tensor, attention_mask: to
         hidden_states = residual + hidden_states
         residual = hidden_states
         hidden_states = norm(hidden_states)
+    if isinstance(self.mlp, TexelatorMLP):
+        out = self.mlp.forward_residual(hidden_states, residual)
+        if out is not None:
+            return out
     hidden_states = self.mlp(hidden_states)
     return residual + hidden_states
 
