@@ -468,7 +468,7 @@ def hf_section(torch, args) -> dict:
                         "embedding kernel (hf.use_texelator_rope), one GEMV over the joined q|k|v handle with the "
                         "biases in its epilogue (hf.use_texelator_qkv, tx_concat_rows + tx_linear_add_bias), the "
                         "attention's residual add fused into the post-attention norm and the MLP's into the down GEMV "
-                        "(hf.use_texelator_residuals), "
+                        "(hf.use_texelator_residuals), one token's k/v appended to the static cache in one launch, "
                         "the one-token forward replayed from a HIP graph "
                         "(device clock)",
     }

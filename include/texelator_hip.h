@@ -318,6 +318,14 @@ int tx_linear_swiglu_pair(uint64_t gate, uint64_t up, const void *x, void *out, 
  * overlap). */
 int tx_linear_add_bias(uint64_t handle, const void *x, const void *bias, void *y, void *stream);
 
+/* One token's k and v (bf16 [kv_heads][head_dim] each) into a Hugging Face static KV cache layer:
+ * keys/values bf16 [kv_heads][max_len][head_dim] at row *length (a device int64, the layer's
+ * cumulative length), then *length += 1, in one launch: what its update() does with an index
+ * tensor, two index copies and an in-place add (no counterpart in the reference's own code, whose
+ * Hugging Face path leaves the cache to transformers). A full cache is left unchanged. */
+int tx_kv_cache_append(const void *k, const void *v, int kv_heads, int head_dim, void *keys, void *values,
+                       int64_t max_len, int64_t *length, void *stream);
+
 /* Rotary embedding of q bf16 [tokens][heads][head_dim] and k bf16 [tokens][kv_heads][head_dim] in
  * the "rotate half" form of a Hugging Face Llama/Qwen2 attention module (its
  * apply_rotary_pos_emb, which the reference's Hugging Face path runs as several elementwise

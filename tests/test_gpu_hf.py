@@ -337,6 +337,38 @@ def test_texelator_rope_model_is_bitwise_the_module(tiny_bc4):
         tiny_bc4.set_attn_implementation("sdpa")
 
 
+def test_kv_cache_append_matches_the_static_layer_update(ext):
+    """``_cache_update`` on a Hugging Face static cache: one token's k and v (views, as the attention
+    forward passes them) land where ``StaticLayer.update`` puts them, the length advances the same and
+    the same tensors come back, step after step; a full cache is left as it is; a prompt of several
+    tokens takes the cache's own update."""
+    import transformers
+
+    from texelator_amd import hf
+
+    config = transformers.Qwen2Config(vocab_size=64, hidden_size=256, intermediate_size=512, num_hidden_layers=1,
+                                      num_attention_heads=4, num_key_value_heads=2, head_dim=64)
+    ours = transformers.StaticCache(config=config, max_cache_len=8)
+    theirs = transformers.StaticCache(config=config, max_cache_len=8)
+    g = torch.Generator(device="cuda").manual_seed(30)
+
+    def token_kv(tokens):
+        k = torch.randn(1, tokens, 2, 64, device="cuda", generator=g).to(torch.bfloat16).transpose(1, 2)
+        v = torch.randn(1, tokens, 2, 64, device="cuda", generator=g).to(torch.bfloat16).transpose(1, 2)
+        return k, v
+
+    k, v = token_kv(3)
+    hf._cache_update(ours, 0, k, v)
+    theirs.update(k, v, 0)
+    for step in range(7):
+        k, v = token_kv(1)
+        got = hf._cache_update(ours, 0, k, v)
+        want = theirs.update(k, v, 0) if step < 5 else (theirs.layers[0].keys, theirs.layers[0].values)
+        assert got[0] is ours.layers[0].keys and got[1] is ours.layers[0].values
+        assert torch.equal(got[0], want[0]) and torch.equal(got[1], want[1]), step
+        assert int(ours.layers[0].cumulative_length) == min(4 + step, 8)
+
+
 def test_texelator_qkv_joins_the_projections(ext, tiny_bc4):
     """``use_texelator_qkv`` (with ``use_texelator_rope``'s forward) on the BC4 Qwen2 with non-zero
     biases: one token's q, k and v from the joined handle match the three projections within bf16

@@ -67,6 +67,7 @@ SIGNATURES = {
     "tx_linear_split": (_I32, [_U64, _P, _P]),
     "tx_linear_swiglu": (_I32, [_U64, _P, _P, _P]),
     "tx_linear_swiglu_pair": (_I32, [_U64, _U64, _P, _P, _P]),
+    "tx_kv_cache_append": (_I32, [_P, _P, _I32, _I32, _P, _P, _I64, _P, _P]),
     "tx_rope_rotate_half": (_I32, [_P, _P, _I64, _I32, _I32, _I32, _P, _P, _P, _P, _P]),
     "tx_linear_add_bias": (_I32, [_U64, _P, _P, _P, _P]),
     "tx_linear_swiglu_prefill": (_I32, [_U64, _P, _I64, _P, _P]),

@@ -1314,6 +1314,20 @@ int tx_swiglu(const void *gate_up, int64_t rows, int64_t intermediate, void *out
   return TX_OK;
 }
 
+int tx_kv_cache_append(const void *k, const void *v, int kv_heads, int head_dim, void *keys, void *values,
+                       int64_t max_len, int64_t *length, void *stream) {
+  g_last_error.clear();
+  if (!k || !v || !keys || !values || !length) return fail(TX_ERR_INVALID, "kv_cache_append: null pointer");
+  if (kv_heads <= 0 || head_dim <= 0 || max_len <= 0 || (int64_t)kv_heads * head_dim > (1 << 24) ||
+      (int64_t)kv_heads * max_len * head_dim > (int64_t)1 << 40)
+    return fail(TX_ERR_INVALID, "kv_cache_append: bad shape");
+  if (reinterpret_cast<uintptr_t>(length) % 8) return fail(TX_ERR_INVALID, "kv_cache_append: length must be 8-byte aligned");
+  TX_HIP(tx::launch_kv_append(static_cast<const uint16_t *>(k), static_cast<const uint16_t *>(v), kv_heads, head_dim,
+                              static_cast<uint16_t *>(keys), static_cast<uint16_t *>(values), max_len, length,
+                              reinterpret_cast<hipStream_t>(stream)));
+  return TX_OK;
+}
+
 int tx_rope_rotate_half(const void *q, const void *k, int64_t tokens, int heads, int kv_heads, int head_dim,
                         const void *cos, const void *sin, void *q_out, void *k_out, void *stream) {
   g_last_error.clear();

@@ -999,6 +999,25 @@ __global__ __launch_bounds__(256) void rope_rotate_half_kernel(const uint16_t *q
   o[i + half] = to_bf(hi);
 }
 
+// One token's k and v rows (kv_heads x dim bf16 each) into a Hugging Face static cache [kv_heads][max_len][dim]
+// at row *length, then *length += 1: the index copies and the length update of its update() in one
+// block. Every thread reads the length before thread 0 advances it (the barrier orders the two). A
+// full cache (length >= max_len) is left as it is, length included.
+__global__ __launch_bounds__(256) void kv_append_kernel(const uint16_t *k, const uint16_t *v, int kv_heads, int dim,
+                                                        uint16_t *keys, uint16_t *values, int64_t max_len,
+                                                        int64_t *length) {
+  const int64_t pos = *length;
+  __syncthreads();
+  if (pos < 0 || pos >= max_len) return;
+  for (int i = threadIdx.x; i < kv_heads * dim; i += blockDim.x) {
+    const int h = i / dim, j = i - h * dim;
+    const size_t at = ((size_t)h * max_len + pos) * dim + j;
+    keys[at] = k[i];
+    values[at] = v[i];
+  }
+  if (threadIdx.x == 0) *length = pos + 1;
+}
+
 }  // namespace
 
 hipError_t launch_add_rmsnorm(float *h, const uint16_t *delta, const uint16_t *weight, float eps, uint16_t *out,
@@ -1155,6 +1174,12 @@ hipError_t launch_rope_rotate_half(const uint16_t *q, const uint16_t *k, int64_t
                                    hipStream_t stream) {
   hipLaunchKernelGGL(rope_rotate_half_kernel, dim3((unsigned)tokens, (unsigned)(heads + kv_heads)), dim3(dim / 2), 0,
                      stream, q, k, heads, kv_heads, dim, cos, sin, q_out, k_out);
+  return hipGetLastError();
+}
+
+hipError_t launch_kv_append(const uint16_t *k, const uint16_t *v, int kv_heads, int dim, uint16_t *keys, uint16_t *values,
+                            int64_t max_len, int64_t *length, hipStream_t stream) {
+  hipLaunchKernelGGL(kv_append_kernel, dim3(1), dim3(256), 0, stream, k, v, kv_heads, dim, keys, values, max_len, length);
   return hipGetLastError();
 }
 

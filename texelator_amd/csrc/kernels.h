@@ -205,6 +205,8 @@ hipError_t launch_prefill_attention(const uint16_t *q, int64_t q_stride, const u
 hipError_t launch_swiglu(const uint16_t *gu, int64_t rows, int64_t inter, uint16_t *out, hipStream_t stream);
 // Hugging Face's "rotate half" rotary embedding with its bf16 rounding steps: q [tokens][heads][dim]
 // and k [tokens][kv_heads][dim] with cos/sin [tokens][dim], all bf16 (dim even, <= 512).
+hipError_t launch_kv_append(const uint16_t *k, const uint16_t *v, int kv_heads, int dim, uint16_t *keys, uint16_t *values,
+                            int64_t max_len, int64_t *length, hipStream_t stream);
 hipError_t launch_rope_rotate_half(const uint16_t *q, const uint16_t *k, int64_t tokens, int heads, int kv_heads,
                                    int dim, const uint16_t *cos, const uint16_t *sin, uint16_t *q_out, uint16_t *k_out,
                                    hipStream_t stream);

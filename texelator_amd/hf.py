@@ -316,12 +316,32 @@ def _rope_attention_forward(self, hidden_states: torch.Tensor, position_embeddin
     else:
         q, k = hf_module.apply_rotary_pos_emb(q.transpose(1, 2), k.transpose(1, 2), cos, sin)
     if past_key_values is not None:
-        k, v = past_key_values.update(k, v, self.layer_idx)
+        k, v = _cache_update(past_key_values, self.layer_idx, k, v)
     attention = hf_module.ALL_ATTENTION_FUNCTIONS.get_interface(self.config._attn_implementation,
                                                                  hf_module.eager_attention_forward)
     out, weights = attention(self, q, k, v, attention_mask, dropout=0.0 if not self.training else self.attention_dropout,
                              scaling=self.scaling, sliding_window=self.sliding_window, **kwargs)
     return self.o_proj(out.reshape(*input_shape, -1).contiguous()), weights
+
+
+def _cache_update(cache, index: int, k: torch.Tensor, v: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """``cache.update(k, v, index)``; for one bf16 token into an initialized, not offloaded static
+    layer, its two index copies and length update as one launch
+    (:func:`~texelator_amd.layers.kv_cache_append`), the same cache contents and returned tensors."""
+    from . import layers
+
+    stack = getattr(cache, "layers", None)
+    layer = stack[index] if stack is not None and index < len(stack) else None
+    length = getattr(layer, "cumulative_length", None)
+    if (layer is not None and type(layer).__name__ == "StaticLayer" and getattr(layer, "is_initialized", False)
+            and not getattr(cache, "offloading", False) and k.is_cuda and k.dtype == v.dtype == torch.bfloat16
+            and k.dim() == 4 and k.shape[0] == 1 and k.shape[-2] == 1 and v.shape == k.shape
+            and layer.keys.dtype == torch.bfloat16 and layer.keys.shape[-1] == k.shape[-1]
+            and layer.keys.shape[1] == k.shape[1] and isinstance(length, torch.Tensor) and length.is_cuda
+            and length.dtype == torch.int64 and length.numel() == 1):
+        layers.kv_cache_append(k, v, layer.keys, layer.values, length)
+        return layer.keys, layer.values
+    return cache.update(k, v, index)
 
 
 def _projections(self, hidden_states: torch.Tensor) -> tuple[torch.Tensor, ...]:

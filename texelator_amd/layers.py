@@ -485,6 +485,24 @@ def rope_rotate_half(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, sin: t
     return q_out, k_out
 
 
+def kv_cache_append(k: torch.Tensor, v: torch.Tensor, keys: torch.Tensor, values: torch.Tensor,
+                    length: torch.Tensor) -> None:
+    """One token's ``k`` and ``v`` (``kv_heads x dim`` bf16 each, any view of one token) into a static
+    cache ``keys``/``values`` ``[1, kv_heads, max_len, dim]`` at row ``length`` (a CUDA int64 scalar
+    tensor), then ``length += 1``, in one launch; a full cache is left unchanged."""
+    _expect(keys.is_cuda and keys.dtype == values.dtype == torch.bfloat16 and keys.is_contiguous()
+            and values.is_contiguous() and keys.dim() == 4 and keys.shape[0] == 1 and keys.shape == values.shape,
+            "keys and values must be contiguous CUDA bf16 [1, kv_heads, max_len, dim]")
+    _, kv_heads, max_len, dim = keys.shape
+    _expect(k.dtype == v.dtype == torch.bfloat16 and k.numel() == v.numel() == kv_heads * dim
+            and k.device == v.device == keys.device, "k and v must be one token's bf16 [kv_heads, dim]")
+    _expect(length.is_cuda and length.dtype == torch.int64 and length.numel() == 1 and length.device == keys.device,
+            "length must be a CUDA int64 scalar")
+    k, v = k.reshape(kv_heads, dim).contiguous(), v.reshape(kv_heads, dim).contiguous()
+    check(_lib.load().tx_kv_cache_append(_ptr(k), _ptr(v), kv_heads, dim, _ptr(keys), _ptr(values), max_len,
+                                         _ptr(length), _stream(keys)))
+
+
 def swiglu(gate_up: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
     """``bf16(silu(g) * u)`` for rows ``[g | u]``."""
     _expect(gate_up.dtype == torch.bfloat16 and gate_up.is_contiguous() and gate_up.dim() == 2 and gate_up.shape[1] % 2 == 0,
