@@ -495,6 +495,8 @@ def main() -> int:
                         help="BC4 data of the model-level decoders: encoded random-init weights or uniform bytes")
     parser.add_argument("--no-hf", action="store_true",
                         help="skip the Hugging Face (reference calling path) measurement of BASELINE config 4")
+    parser.add_argument("--hf-only", action="store_true",
+                        help="run only the 3B model through Hugging Face modules (the model_3b_hf section)")
     parser.add_argument("--model-only", action="store_true",
                         help="profiling mode: only the model-level prefill and decode measurement (its JSON)")
     parser.add_argument("--prefill-only", action="store_true",
@@ -531,6 +533,9 @@ def main() -> int:
         return prefill_only(torch, ext, runtime, hardware, device, args)
     if args.fp4_only:
         return fp4_only(torch, ext, runtime, hardware, device, args)
+    if args.hf_only:
+        print(json.dumps({"hf_only": True, "model_3b_hf": hf_section(torch, args)}), flush=True)
+        return 0
     if args.model_only:
         print(json.dumps({"model_only": True, "model": model_section(torch, args)}), flush=True)
         return 0
